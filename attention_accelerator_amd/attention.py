@@ -1,0 +1,230 @@
+"""torch-facing operators over libgqa.so.
+
+The call surface is the golden model's (pyfiles/gen_gqa_wrapper_vectors.py:121-139,
+README.md:41-50): Q rows of one token, a K/V cache in position order,
+`query_position` and `seq_len` in; 32 x 128 BF16 output rows out, in Q-head order.
+Batches of independent sequences are the same call with a leading batch
+dimension and per-sequence lengths.
+
+Every op runs the HIP kernels of libgqa.so on the current torch stream and
+raises if the library is not built; there is no CPU path.
+"""
+from __future__ import annotations
+
+import ctypes
+import math
+from typing import Optional, Sequence, Union
+
+import torch
+
+from . import _lib
+from ._lib import GQA_ROPE_K, GQA_ROPE_Q, GqaKvLayout, GqaParams, check, lib
+
+N_Q_HEADS = 32
+N_KV_HEADS = 8
+GROUP_SIZE = N_Q_HEADS // N_KV_HEADS
+HEAD_DIM = 128
+ROPE_THETA = 500000.0
+DEFAULT_SCALE = 1.0 / math.sqrt(HEAD_DIM)
+
+Lengths = Union[int, Sequence[int], torch.Tensor]
+
+
+def make_params(*, rope_q: bool = True, rope_k: bool = False, theta: float = ROPE_THETA,
+                scale: Optional[float] = None, n_q_heads: int = N_Q_HEADS,
+                n_kv_heads: int = N_KV_HEADS, head_dim: int = HEAD_DIM) -> GqaParams:
+    flags = (GQA_ROPE_Q if rope_q else 0) | (GQA_ROPE_K if rope_k else 0)
+    return GqaParams(n_q_heads, n_kv_heads, head_dim,
+                     DEFAULT_SCALE if scale is None else float(scale), float(theta), flags)
+
+
+def _stream_handle(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def _lengths_to_device(x: Lengths, batch: int, device: torch.device, name: str):
+    """Returns (device int32 tensor, host int32 tensor or None)."""
+    if isinstance(x, torch.Tensor) and x.is_cuda:
+        if x.dtype != torch.int32 or x.numel() != batch:
+            raise ValueError(f"{name} must be an int32 tensor of {batch} elements")
+        return x.contiguous(), None
+    host = torch.as_tensor(x, dtype=torch.int32).reshape(-1)
+    if host.numel() == 1 and batch > 1:
+        host = host.expand(batch)
+    if host.numel() != batch:
+        raise ValueError(f"{name} has {host.numel()} entries for a batch of {batch}")
+    host = host.contiguous()
+    return host.to(device, non_blocking=False), host
+
+
+def decode_workspace_bytes(batch: int, capacity: int, params: Optional[GqaParams] = None) -> int:
+    p = params or make_params()
+    return int(lib().gqa_decode_workspace_bytes(ctypes.byref(p), int(batch), int(capacity)))
+
+
+def gqa_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
+                  query_position: Lengths, seq_len: Lengths, *, rope_q: bool = True,
+                  rope_k: bool = False, theta: float = ROPE_THETA, scale: Optional[float] = None,
+                  out: Optional[torch.Tensor] = None,
+                  workspace: Optional[torch.Tensor] = None,
+                  params: Optional[GqaParams] = None) -> torch.Tensor:
+    """One GQA decode step (32 Q heads over 8 KV heads, head_dim 128, BF16).
+
+    q        [32, 128] or [B, 32, 128] bfloat16 (CUDA/HIP)
+    k_cache  [8, S, 128] or [B, 8, S, 128] bfloat16, positions in order; the last
+             dim must be contiguous (any other strides, multiples of 8)
+    v_cache  same shape and strides as k_cache
+    query_position, seq_len: int, a sequence of B ints, or an int32 tensor.  Host
+             values are validated first (1 <= seq_len <= S, 0 <= qpos < seq_len);
+             device tensors are read by the kernel as they are.
+    rope_q / rope_k: rotate Q at query_position / each K row at its position
+             (the reference core does both; a cache stored post-RoPE sets rope_k=False)
+    Returns out [.., 32, 128] bfloat16.  Key p contributes iff p < seq_len and
+    p <= query_position.  Raises GqaConfigError for what the reference rejects."""
+    single = q.dim() == 2
+    if single:
+        q, k_cache, v_cache = q.unsqueeze(0), k_cache.unsqueeze(0), v_cache.unsqueeze(0)
+    if q.dim() != 3 or k_cache.dim() != 4 or v_cache.dim() != 4:
+        raise ValueError("expected q [B,32,128] and k/v [B,8,S,128]")
+    for name, t in (("q", q), ("k_cache", k_cache), ("v_cache", v_cache)):
+        if t.dtype != torch.bfloat16 or not t.is_cuda:
+            raise ValueError(f"{name} must be a bfloat16 tensor on the GPU")
+    if k_cache.shape != v_cache.shape or k_cache.stride() != v_cache.stride():
+        raise ValueError("k_cache and v_cache must share shape and strides")
+    batch = q.shape[0]
+    if k_cache.shape[0] != batch:
+        raise ValueError("batch mismatch between q and the cache")
+    if k_cache.stride(3) != 1:
+        raise ValueError("cache rows must be contiguous in head_dim")
+    q = q.contiguous()
+    device = q.device
+    capacity = k_cache.shape[2]
+    p = params or make_params(rope_q=rope_q, rope_k=rope_k, theta=theta, scale=scale,
+                              n_q_heads=q.shape[1], n_kv_heads=k_cache.shape[1],
+                              head_dim=q.shape[2])
+    sl_dev, sl_host = _lengths_to_device(seq_len, batch, device, "seq_len")
+    qp_dev, qp_host = _lengths_to_device(query_position, batch, device, "query_position")
+    if sl_host is not None and qp_host is not None:
+        check(lib().gqa_validate_lengths(
+            ctypes.cast(sl_host.data_ptr(), ctypes.POINTER(ctypes.c_int32)),
+            ctypes.cast(qp_host.data_ptr(), ctypes.POINTER(ctypes.c_int32)), batch, capacity),
+            "gqa_validate_lengths")
+    ws_bytes = int(lib().gqa_decode_workspace_bytes(ctypes.byref(p), batch, capacity))
+    if ws_bytes == 0:
+        check(_lib.GQA_ERR_INVALID_CONFIG, "gqa_decode_workspace_bytes")
+    if workspace is None or workspace.numel() * workspace.element_size() < ws_bytes:
+        workspace = torch.empty(ws_bytes, dtype=torch.uint8, device=device)
+    if out is None:
+        out = torch.empty((batch, q.shape[1], q.shape[2]), dtype=torch.bfloat16, device=device)
+    elif out.shape != (batch, q.shape[1], q.shape[2]) or out.dtype != torch.bfloat16 \
+            or not out.is_contiguous():
+        raise ValueError("out must be a contiguous bfloat16 [B,32,128] tensor")
+    layout = GqaKvLayout(k_cache.stride(0), k_cache.stride(1), k_cache.stride(2), capacity)
+    status = lib().gqa_decode_bf16(
+        ctypes.byref(p), q.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(),
+        ctypes.byref(layout), sl_dev.data_ptr(), qp_dev.data_ptr(), batch, out.data_ptr(),
+        workspace.data_ptr(), workspace.numel() * workspace.element_size(),
+        _stream_handle(device))
+    check(status, "gqa_decode_bf16")
+    return out[0] if single else out
+
+
+gqa_decode = gqa_attention
+
+
+def rope_half_split(rows: torch.Tensor, position: Union[int, torch.Tensor] = 0, *,
+                    theta: float = ROPE_THETA, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """rotate_half RoPE of BF16 rows [N, 128] on the GPU (the rope_unit of rope_unit.v).
+
+    position: an int p0 (row r at p0 + r, as tests/tb_rope_unit.sv drives it) or a
+    device int32 tensor of N positions.  Output BF16 = round(f32(round(rope in double)))."""
+    if rows.dtype != torch.bfloat16 or not rows.is_cuda or rows.dim() != 2 \
+            or rows.shape[1] != HEAD_DIM or rows.stride(1) != 1:
+        raise ValueError("rows must be a bfloat16 [N,128] GPU tensor with contiguous rows")
+    if out is None:
+        out = torch.empty_like(rows, memory_format=torch.contiguous_format)
+    if out.shape != rows.shape or out.stride() != rows.stride():
+        rows = rows.contiguous()
+        if out.stride() != rows.stride():
+            raise ValueError("out must match rows' layout")
+    pos_ptr, pos0 = None, 0
+    if isinstance(position, torch.Tensor):
+        if not position.is_cuda or position.dtype != torch.int32 or position.numel() != rows.shape[0]:
+            raise ValueError("position tensor must be int32 on the GPU with one entry per row")
+        position = position.contiguous()
+        pos_ptr = position.data_ptr()
+    else:
+        pos0 = int(position)
+    status = lib().gqa_rope_rows_bf16(rows.data_ptr(), out.data_ptr(), rows.shape[0], rows.stride(0),
+                                      pos_ptr, pos0, float(theta), _stream_handle(rows.device))
+    check(status, "gqa_rope_rows_bf16")
+    return out
+
+
+class PreparedDecode:
+    """A decode call with every argument bound once, for loops that repeat the same
+    step (serving, benchmarking): calling it issues gqa_decode_bf16 on the current
+    stream with no per-call tensor checks, allocation or host validation.
+
+    Lengths must be device int32 tensors (validate them once with
+    validate_lengths); the tensors passed in must stay alive while it is used."""
+
+    def __init__(self, q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
+                 query_position: torch.Tensor, seq_len: torch.Tensor, *, rope_q: bool = True,
+                 rope_k: bool = False, theta: float = ROPE_THETA, scale: Optional[float] = None,
+                 out: Optional[torch.Tensor] = None):
+        if q.dim() != 3 or k_cache.dim() != 4:
+            raise ValueError("expected q [B,32,128] and k/v [B,8,S,128]")
+        if not (query_position.is_cuda and seq_len.is_cuda):
+            raise ValueError("lengths must be device tensors")
+        if k_cache.stride() != v_cache.stride() or k_cache.stride(3) != 1:
+            raise ValueError("k_cache and v_cache must share strides with contiguous rows")
+        self.batch = q.shape[0]
+        self.capacity = k_cache.shape[2]
+        self.params = make_params(rope_q=rope_q, rope_k=rope_k, theta=theta, scale=scale)
+        self.layout = GqaKvLayout(k_cache.stride(0), k_cache.stride(1), k_cache.stride(2),
+                                  self.capacity)
+        ws_bytes = int(lib().gqa_decode_workspace_bytes(ctypes.byref(self.params), self.batch,
+                                                        self.capacity))
+        if ws_bytes == 0:
+            check(_lib.GQA_ERR_INVALID_CONFIG, "gqa_decode_workspace_bytes")
+        self.workspace = torch.empty(ws_bytes, dtype=torch.uint8, device=q.device)
+        self.out = out if out is not None else torch.empty(
+            (self.batch, N_Q_HEADS, HEAD_DIM), dtype=torch.bfloat16, device=q.device)
+        self._keep = (q.contiguous(), k_cache, v_cache, query_position.contiguous(),
+                      seq_len.contiguous())
+        qc, kc, vc, qp, sl = self._keep
+        self._args = (ctypes.byref(self.params), qc.data_ptr(), kc.data_ptr(), vc.data_ptr(),
+                      ctypes.byref(self.layout), sl.data_ptr(), qp.data_ptr(), self.batch,
+                      self.out.data_ptr(), self.workspace.data_ptr(), ws_bytes)
+        self._fn = lib().gqa_decode_bf16
+        self.device = q.device
+
+    def __call__(self) -> torch.Tensor:
+        status = self._fn(*self._args, _stream_handle(self.device))
+        if status:
+            check(status, "gqa_decode_bf16")
+        return self.out
+
+
+def validate_lengths(seq_len, query_position, capacity: int) -> None:
+    """Host check of lengths (raises GqaConfigError), gen_gqa_wrapper_vectors.py:73-78."""
+    sl = torch.as_tensor(seq_len, dtype=torch.int32).reshape(-1).contiguous()
+    qp = torch.as_tensor(query_position, dtype=torch.int32).reshape(-1).contiguous()
+    if sl.numel() != qp.numel():
+        raise ValueError("seq_len and query_position differ in length")
+    check(lib().gqa_validate_lengths(ctypes.cast(sl.data_ptr(), ctypes.POINTER(ctypes.c_int32)),
+                                     ctypes.cast(qp.data_ptr(), ctypes.POINTER(ctypes.c_int32)),
+                                     sl.numel(), int(capacity)), "gqa_validate_lengths")
+
+
+def profile_enable(max_calls: int) -> None:
+    """Start recording kernel times of up to max_calls decode calls (0 stops)."""
+    check(lib().gqa_profile_enable(int(max_calls)), "gqa_profile_enable")
+
+
+def profile_read():
+    """-> (split_ms_total, combine_ms_total, calls) recorded since the last read."""
+    p = _lib.GqaProfile()
+    check(lib().gqa_profile_read(ctypes.byref(p)), "gqa_profile_read")
+    return p.split_ms, p.combine_ms, p.calls

@@ -1,0 +1,239 @@
+// gqa_abi.hip -- the extern "C" surface of libgqa.so (declared in include/gqa.h).
+//
+// Validation mirrors the reference core's start-time rejection
+// (gqa_attention_wrapper.v:230-244): a rejected call launches nothing and writes no
+// output, and the status says why.
+#include <cmath>
+#include <cstdlib>
+#include <cstring>
+#include <mutex>
+#include <vector>
+
+#include "gqa.h"
+#include "gqa_internal.h"
+
+namespace gqa {
+
+void fill_rope_table(double theta, RopeTable* t) {
+    // angle = position * theta ** (-2.0 * i / 128), pyfiles/gen_gqa_wrapper_vectors.py:30.
+    for (int i = 0; i < kPairs; ++i) t->inv_freq[i] = std::pow(theta, (-2.0 * i) / kD);
+}
+
+namespace {
+
+constexpr int64_t kTargetWaves = 8192;
+
+size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
+
+int split_keys_override() {
+    const char* s = std::getenv("GQA_SPLIT_KEYS");
+    if (!s) return 0;
+    const int v = std::atoi(s);
+    return (v >= 64 && v % 64 == 0) ? v : 0;
+}
+
+bool geometry_ok(const gqa_params_t* p) {
+    if (p->n_q_heads != kHq || p->n_kv_heads != kHkv || p->head_dim != kD) return false;
+    if (!(p->scale != 0.f) || !std::isfinite(p->scale)) return false;
+    if ((p->flags & ~(GQA_ROPE_Q | GQA_ROPE_K)) != 0) return false;
+    if ((p->flags & (GQA_ROPE_Q | GQA_ROPE_K)) && !(p->rope_theta > 0.0 && std::isfinite(p->rope_theta)))
+        return false;
+    return true;
+}
+
+bool aligned(const void* p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
+
+// Opt-in kernel timing (gqa_profile_enable / gqa_profile_read).
+struct Profiler {
+    std::mutex mu;
+    std::vector<hipEvent_t> events;   // 3 per recorded call
+    int32_t capacity = 0;
+    int32_t used = 0;
+};
+
+Profiler& profiler() {
+    static Profiler p;
+    return p;
+}
+
+// Returns the next free event triple, or nullptr when profiling is off or full.
+hipEvent_t* profile_slot() {
+    Profiler& p = profiler();
+    std::lock_guard<std::mutex> lock(p.mu);
+    if (p.used >= p.capacity) return nullptr;
+    return &p.events[static_cast<size_t>(p.used++) * 3];
+}
+
+}  // namespace
+
+DecodePlan plan_decode(int32_t batch, int32_t capacity) {
+    DecodePlan plan{};
+    int64_t split = split_keys_override();
+    if (split == 0) {
+        const int64_t total = static_cast<int64_t>(batch) * kHkv * capacity;
+        split = (total + kTargetWaves - 1) / kTargetWaves;
+        split = (split + 63) / 64 * 64;
+        if (split < 64) split = 64;
+        if (split > 4096) split = 4096;
+    }
+    plan.split_keys = static_cast<int32_t>(split);
+    plan.n_splits = static_cast<int32_t>((capacity + split - 1) / split);
+    const size_t units = static_cast<size_t>(batch) * kHkv * plan.n_splits;
+    plan.workspace_bytes = align_up(units * kGroup * kD * sizeof(float), 256) +
+                           align_up(units * kGroup * sizeof(float2), 256);
+    return plan;
+}
+
+}  // namespace gqa
+
+using namespace gqa;
+
+extern "C" {
+
+uint32_t gqa_abi_version(void) { return (1u << 16) | 0u; }
+
+const char* gqa_status_string(int status) {
+    switch (status) {
+        case GQA_OK: return "ok";
+        case GQA_ERR_INVALID_CONFIG: return "invalid configuration";
+        case GQA_ERR_BAD_POINTER: return "null or misaligned pointer or stride";
+        case GQA_ERR_WORKSPACE: return "workspace missing or too small";
+        case GQA_ERR_HIP: return "HIP runtime error";
+        default: return "unknown status";
+    }
+}
+
+int gqa_validate_registers(int32_t n_q_heads, int32_t n_kv_heads, int32_t head_dim,
+                           int32_t tile_dim, int32_t seq_len, int32_t n_kv_tiles,
+                           int32_t kv_block_len, uint16_t scale_bf16) {
+    if (n_q_heads != kHq || n_kv_heads != kHkv || head_dim != kD || tile_dim != 16)
+        return GQA_ERR_INVALID_CONFIG;
+    if (kv_block_len <= 0 || seq_len <= 0) return GQA_ERR_INVALID_CONFIG;
+    const int64_t want_tiles = (static_cast<int64_t>(seq_len) + kv_block_len - 1) / kv_block_len;
+    if (n_kv_tiles != want_tiles) return GQA_ERR_INVALID_CONFIG;
+    if (scale_bf16 == 0) return GQA_ERR_INVALID_CONFIG;
+    return GQA_OK;
+}
+
+int gqa_validate_lengths(const int32_t* seq_len, const int32_t* query_pos, int32_t batch,
+                         int32_t capacity) {
+    if (!seq_len || !query_pos) return GQA_ERR_BAD_POINTER;
+    if (batch <= 0 || capacity <= 0) return GQA_ERR_INVALID_CONFIG;
+    for (int32_t b = 0; b < batch; ++b) {
+        if (seq_len[b] < 1 || seq_len[b] > capacity) return GQA_ERR_INVALID_CONFIG;
+        if (query_pos[b] < 0 || query_pos[b] >= seq_len[b]) return GQA_ERR_INVALID_CONFIG;
+    }
+    return GQA_OK;
+}
+
+size_t gqa_decode_workspace_bytes(const gqa_params_t* params, int32_t batch, int32_t capacity) {
+    if (!params || !geometry_ok(params) || batch <= 0 || capacity <= 0) return 0;
+    return plan_decode(batch, capacity).workspace_bytes;
+}
+
+int gqa_decode_bf16(const gqa_params_t* params, const uint16_t* q, const uint16_t* k,
+                    const uint16_t* v, const gqa_kv_layout_t* kv, const int32_t* seq_len,
+                    const int32_t* query_pos, int32_t batch, uint16_t* out, void* workspace,
+                    size_t workspace_bytes, void* stream) {
+    if (!params || !kv) return GQA_ERR_BAD_POINTER;
+    if (!geometry_ok(params)) return GQA_ERR_INVALID_CONFIG;
+    if (batch <= 0 || kv->capacity <= 0) return GQA_ERR_INVALID_CONFIG;
+    if (kv->pos_stride < kD || kv->head_stride < 0 || kv->batch_stride < 0)
+        return GQA_ERR_INVALID_CONFIG;
+    if (!q || !k || !v || !out || !seq_len || !query_pos) return GQA_ERR_BAD_POINTER;
+    if (!aligned(q, 2) || !aligned(out, 4) || !aligned(k, 16) || !aligned(v, 16) ||
+        !aligned(seq_len, 4) || !aligned(query_pos, 4))
+        return GQA_ERR_BAD_POINTER;
+    if (kv->pos_stride % 8 || kv->head_stride % 8 || kv->batch_stride % 8) return GQA_ERR_BAD_POINTER;
+
+    const DecodePlan plan = plan_decode(batch, kv->capacity);
+    if (!workspace || workspace_bytes < plan.workspace_bytes || !aligned(workspace, 256))
+        return GQA_ERR_WORKSPACE;
+
+    DecodeArgs a{};
+    a.q = q;
+    a.k = k;
+    a.v = v;
+    a.seq_len = seq_len;
+    a.query_pos = query_pos;
+    a.out = out;
+    const size_t units = static_cast<size_t>(batch) * kHkv * plan.n_splits;
+    a.part_o = static_cast<float*>(workspace);
+    a.part_ml = reinterpret_cast<float2*>(static_cast<char*>(workspace) +
+                                          align_up(units * kGroup * kD * sizeof(float), 256));
+    a.kv_batch_stride = kv->batch_stride;
+    a.kv_head_stride = kv->head_stride;
+    a.kv_pos_stride = kv->pos_stride;
+    a.capacity = kv->capacity;
+    a.split_keys = plan.split_keys;
+    a.n_splits = plan.n_splits;
+    a.qk_scale_log2 = static_cast<float>(static_cast<double>(params->scale) * 1.4426950408889634);
+    a.flags = params->flags;
+    fill_rope_table(params->rope_theta, &a.rope);
+    const hipError_t e = launch_decode(a, batch, static_cast<hipStream_t>(stream), profile_slot());
+    return e == hipSuccess ? GQA_OK : GQA_ERR_HIP;
+}
+
+int gqa_profile_enable(int32_t max_calls) {
+    Profiler& p = profiler();
+    std::lock_guard<std::mutex> lock(p.mu);
+    for (hipEvent_t e : p.events)
+        if (e) (void)hipEventDestroy(e);
+    p.events.clear();
+    p.capacity = 0;
+    p.used = 0;
+    if (max_calls <= 0) return GQA_OK;
+    p.events.resize(static_cast<size_t>(max_calls) * 3);
+    for (auto& e : p.events) {
+        if (hipEventCreate(&e) != hipSuccess) {
+            e = nullptr;
+            return GQA_ERR_HIP;
+        }
+    }
+    p.capacity = max_calls;
+    return GQA_OK;
+}
+
+int gqa_profile_read(gqa_profile_t* out) {
+    if (!out) return GQA_ERR_BAD_POINTER;
+    Profiler& p = profiler();
+    std::lock_guard<std::mutex> lock(p.mu);
+    double split = 0.0, combine = 0.0;
+    for (int32_t i = 0; i < p.used; ++i) {
+        hipEvent_t* ev = &p.events[static_cast<size_t>(i) * 3];
+        float a = 0.f, b = 0.f;
+        if (hipEventSynchronize(ev[2]) != hipSuccess) return GQA_ERR_HIP;
+        if (hipEventElapsedTime(&a, ev[0], ev[1]) != hipSuccess) return GQA_ERR_HIP;
+        if (hipEventElapsedTime(&b, ev[1], ev[2]) != hipSuccess) return GQA_ERR_HIP;
+        split += a;
+        combine += b;
+    }
+    out->split_ms = split;
+    out->combine_ms = combine;
+    out->calls = p.used;
+    p.used = 0;
+    return GQA_OK;
+}
+
+int gqa_rope_rows_bf16(const uint16_t* in, uint16_t* out, int64_t n_rows, int64_t row_stride,
+                       const int32_t* positions, int32_t pos0, double theta, void* stream) {
+    if (n_rows < 0 || row_stride < kD || !(theta > 0.0 && std::isfinite(theta)))
+        return GQA_ERR_INVALID_CONFIG;
+    if (n_rows == 0) return GQA_OK;
+    if (!in || !out) return GQA_ERR_BAD_POINTER;
+    if (!aligned(in, 2) || !aligned(out, 2) || (positions && !aligned(positions, 4)))
+        return GQA_ERR_BAD_POINTER;
+    if (n_rows > (int64_t{1} << 31)) return GQA_ERR_INVALID_CONFIG;
+    RopeArgs a{};
+    a.in = in;
+    a.out = out;
+    a.positions = positions;
+    a.n_rows = n_rows;
+    a.row_stride = row_stride;
+    a.pos0 = pos0;
+    fill_rope_table(theta, &a.rope);
+    const hipError_t e = launch_rope_rows(a, static_cast<hipStream_t>(stream));
+    return e == hipSuccess ? GQA_OK : GQA_ERR_HIP;
+}
+
+}  // extern "C"

@@ -1,0 +1,103 @@
+// gqa_device.h -- device helpers shared by the gfx950 kernels (wave64, CDNA4).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace gqa {
+
+constexpr int kHq = 32;       // Q heads
+constexpr int kHkv = 8;       // KV heads
+constexpr int kGroup = 4;     // Q heads per KV head
+constexpr int kD = 128;       // head_dim
+constexpr int kWave = 64;
+constexpr int kPairs = kD / 2;
+
+// theta^(-2i/128) for i < 64, computed on the host in double exactly as the
+// golden computes it (pyfiles/gen_gqa_wrapper_vectors.py:30).
+struct RopeTable {
+    double inv_freq[kPairs];
+};
+
+__device__ __forceinline__ float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float bf16_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+
+__device__ __forceinline__ float bf16_to_f32(uint16_t b) {
+    return __uint_as_float(static_cast<uint32_t>(b) << 16);
+}
+
+// Eight BF16 codes packed in a uint4 -> eight floats (element 0 in the low half
+// of the first dword, i.e. memory order).
+__device__ __forceinline__ void unpack8(const uint4& w, float (&f)[8]) {
+    f[0] = bf16_lo(w.x); f[1] = bf16_hi(w.x);
+    f[2] = bf16_lo(w.y); f[3] = bf16_hi(w.y);
+    f[4] = bf16_lo(w.z); f[5] = bf16_hi(w.z);
+    f[6] = bf16_lo(w.w); f[7] = bf16_hi(w.w);
+}
+
+// float -> BF16 code, round to nearest even (NaN -> quiet NaN).
+__device__ __forceinline__ uint16_t f32_to_bf16_rne(float f) {
+    uint32_t u = __float_as_uint(f);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return 0x7fc0;
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return static_cast<uint16_t>(u >> 16);
+}
+
+// double -> f32 (RNE) -> BF16 (RNE): the reference's f32_to_bf16 path
+// (pyfiles/gqa_reference.py:15-19).
+__device__ __forceinline__ uint16_t f64_to_bf16_via_f32(double d) {
+    return f32_to_bf16_rne(static_cast<float>(d));
+}
+
+// DPP lane moves (row = 16 lanes).  Control codes: quad_perm [1,0,3,2] = 0xB1,
+// quad_perm [2,3,0,1] = 0x4E, row_ror:n = 0x120 + n.
+template <int kCtrl>
+__device__ __forceinline__ float dpp_f(float x) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), kCtrl, 0xf, 0xf, false));
+}
+
+// Sum over the 16 lanes of a DPP row; every lane of the row gets the total.
+__device__ __forceinline__ float row16_sum(float x) {
+    x += dpp_f<0xB1>(x);
+    x += dpp_f<0x4E>(x);
+    x += dpp_f<0x124>(x);
+    x += dpp_f<0x128>(x);
+    return x;
+}
+
+__device__ __forceinline__ float row16_max(float x) {
+    x = fmaxf(x, dpp_f<0xB1>(x));
+    x = fmaxf(x, dpp_f<0x4E>(x));
+    x = fmaxf(x, dpp_f<0x124>(x));
+    x = fmaxf(x, dpp_f<0x128>(x));
+    return x;
+}
+
+// Across the four rows of a wave (lanes l, l^16, l^32, l^48).
+__device__ __forceinline__ float cross_row_sum(float x) {
+    x += __shfl_xor(x, 16);
+    x += __shfl_xor(x, 32);
+    return x;
+}
+
+__device__ __forceinline__ float cross_row_max(float x) {
+    x = fmaxf(x, __shfl_xor(x, 16));
+    x = fmaxf(x, __shfl_xor(x, 32));
+    return x;
+}
+
+__device__ __forceinline__ float wave_sum(float x) { return cross_row_sum(row16_sum(x)); }
+__device__ __forceinline__ float wave_max(float x) { return cross_row_max(row16_max(x)); }
+
+// Rotate one rotate_half pair at `position` for frequency index i, in double
+// (pyfiles/gen_gqa_wrapper_vectors.py:30-34).
+__device__ __forceinline__ void rope_pair(double x, double y, int64_t position, double inv_freq,
+                                          double& xr, double& yr) {
+    double angle = static_cast<double>(position) * inv_freq;
+    double s, c;
+    sincos(angle, &s, &c);
+    xr = x * c - y * s;
+    yr = x * s + y * c;
+}
+
+}  // namespace gqa

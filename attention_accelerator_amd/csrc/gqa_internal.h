@@ -1,0 +1,59 @@
+// gqa_internal.h -- kernel argument blocks and launchers behind the C ABI.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "gqa_device.h"
+
+namespace gqa {
+
+// Everything one decode launch needs, passed by value as the kernel argument.
+struct DecodeArgs {
+    const uint16_t* q;        // [B][32][128]
+    const uint16_t* k;        // rows at b*kv_batch_stride + h*kv_head_stride + p*kv_pos_stride
+    const uint16_t* v;
+    const int32_t* seq_len;   // [B]
+    const int32_t* query_pos; // [B]
+    uint16_t* out;            // [B][32][128]
+    float* part_o;            // [B][8][n_splits][4][128] unnormalised partial outputs
+    float2* part_ml;          // [B][8][n_splits][4] (running max in log2 units, sum)
+    int64_t kv_batch_stride;
+    int64_t kv_head_stride;
+    int64_t kv_pos_stride;
+    int32_t capacity;
+    int32_t split_keys;       // keys per split (multiple of 64)
+    int32_t n_splits;         // splits allotted per (sequence, kv head)
+    float qk_scale_log2;      // scale * log2(e), folded into Q
+    uint32_t flags;           // bit0 RoPE on Q, bit1 RoPE on K
+    RopeTable rope;
+};
+
+// Split plan for a batch of sequences of up to `capacity` positions.
+struct DecodePlan {
+    int32_t split_keys;
+    int32_t n_splits;
+    size_t workspace_bytes;
+};
+
+DecodePlan plan_decode(int32_t batch, int32_t capacity);
+// ev (optional): three events recorded before the split kernel, between the two
+// kernels and after the combine kernel.
+hipError_t launch_decode(const DecodeArgs& a, int batch, hipStream_t stream,
+                         hipEvent_t* ev = nullptr);
+
+struct RopeArgs {
+    const uint16_t* in;
+    uint16_t* out;
+    const int32_t* positions;
+    int64_t n_rows;
+    int64_t row_stride;
+    int32_t pos0;
+    RopeTable rope;
+};
+
+hipError_t launch_rope_rows(const RopeArgs& a, hipStream_t stream);
+
+void fill_rope_table(double theta, RopeTable* t);
+
+}  // namespace gqa

@@ -1,0 +1,190 @@
+#!/usr/bin/env python3
+"""Benchmark: batched ragged GQA decode on one MI355X.
+
+Workload (default): B=64 sequences, KV lengths drawn uniformly from [512, 8192]
+(seed 20260805), cache capacity 8192, 32 Q / 8 KV heads, head_dim 128, BF16
+N(0,1) inputs, K cache stored post-RoPE (RoPE on Q in the kernel), query_position
+= length - 1, unused cache rows NaN.  One step = one gqa_decode_bf16 call (split-KV
+kernel + combine kernel) on inputs already resident in HBM.
+
+Prints one JSON line: value = algorithmic HBM bytes of the step / time per step
+(GB/s), ms_per_step, the roofline of the dominant kernel (split-KV), measured
+with HIP events around each of its launches inside the timed region, and the CPU
+baseline (the compiled oracle on a bounded sample of the same batch, 1 core).
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+METRIC = "GQA decode µs/step + achieved HBM GB/s, B=64 ragged ctx 512–8192"
+HBM_PEAK_GBS = 8000.0
+WORKLOADS = {
+    # name: (batch, capacity, min_len, max_len)
+    "decode_b64_ragged_512_8192": (64, 8192, 512, 8192),
+    "decode_b1_4096": (1, 4096, None, None),
+    "decode_b8_131072": (8, 131072, None, None),
+}
+TRAFFIC_FILE = ROOT / "profiles" / "decode_split_b64_ragged_traffic.txt"
+
+
+def read_traffic(workload: str):
+    """HBM bytes per split-kernel launch measured with rocprofv3 --pmc (FETCH_SIZE +
+    WRITE_SIZE, scaled by the copy-kernel calibration), if committed for this workload."""
+    if workload != "decode_b64_ragged_512_8192" or not TRAFFIC_FILE.exists():
+        return None
+    for line in TRAFFIC_FILE.read_text().splitlines():
+        if line.startswith("traffic_bytes_per_launch="):
+            return float(line.split("=", 1)[1])
+    return None
+
+
+def cpu_baseline(batch, budget_s: float = 12.0):
+    """The compiled oracle (C restatement of the golden loop, double, 1 thread) on the
+    first sequences of the same batch until ~budget_s of CPU work."""
+    import numpy as np
+
+    from attention_accelerator_amd.stimulus import algorithmic_bytes_decode
+    from oracle import oracle as orc
+
+    def codes(t):
+        return t.contiguous().view(__import__("torch").int16).cpu().numpy().view(np.uint16)
+
+    done, t_total, lens = 0, 0.0, []
+    bsz = batch.q.shape[0]
+    while done < bsz and t_total < budget_s:
+        n = int(batch.seq_len[done])
+        q = codes(batch.q[done:done + 1])
+        k = codes(batch.k[done:done + 1, :, :n])
+        v = codes(batch.v[done:done + 1, :, :n])
+        t0 = time.perf_counter()
+        orc.decode(q, k, v, batch.seq_len[done:done + 1].numpy(),
+                   batch.query_pos[done:done + 1].numpy())
+        t_total += time.perf_counter() - t0
+        lens.append(n)
+        done += 1
+    gbs = algorithmic_bytes_decode(lens) / t_total / 1e9
+    return {"value": round(gbs, 4), "unit": "GB/s", "cores": 1, "kind": "port",
+            "sample": (f"sequences 0..{done - 1} of the same batch ({done} of {bsz}, "
+                       f"{sum(lens)} keys, all 32 heads), compiled oracle in double, "
+                       f"{t_total:.2f} s; os.cpu_count()={os.cpu_count()}, "
+                       f"affinity={len(os.sched_getaffinity(0))}")}
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--workload", choices=sorted(WORKLOADS), default="decode_b64_ragged_512_8192")
+    ap.add_argument("--seed", type=int, default=20260805)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-profile", action="store_true",
+                    help="skip the per-kernel HIP events inside the timed region")
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="also run plain 1 GiB device copies (PMC byte-counter calibration)")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported "
+              "(the decode shards by sequence or KV head with no exchange; see DESIGN.md)",
+              file=sys.stderr)
+        return 2
+
+    import torch
+
+    import attention_accelerator_amd as gqa
+    from attention_accelerator_amd import stimulus
+    from attention_accelerator_amd.attention import PreparedDecode, validate_lengths
+
+    dev = torch.device("cuda", 0)
+    bsz, cap, lo, hi = WORKLOADS[args.workload]
+    batch = stimulus.decode_batch(bsz, cap, min_len=lo, max_len=hi, seed=args.seed,
+                                  device=dev, gen_device="cuda")
+    validate_lengths(batch.seq_len, batch.query_pos, cap)
+    lens = [int(x) for x in batch.seq_len]
+    step_bytes = stimulus.algorithmic_bytes_decode(lens)
+    # The split kernel reads K/V rows, Q rows and the lengths; the combine writes O.
+    split_bytes = step_bytes - bsz * stimulus.N_Q_HEADS * stimulus.HEAD_DIM * 2
+    call = PreparedDecode(batch.q, batch.k, batch.v, batch.query_pos.to(dev),
+                          batch.seq_len.to(dev))
+    print(f"[bench] {args.workload}: B={bsz} keys={sum(lens)} bytes/step={step_bytes}",
+          file=sys.stderr, flush=True)
+
+    for _ in range(args.warmup):
+        call()
+    torch.cuda.synchronize()
+
+    if not args.no_profile:
+        gqa.profile_enable(args.steps)
+    torch.cuda.synchronize()
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    ev0.record()
+    for _ in range(args.steps):
+        call()
+    ev1.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms_per_step = ev0.elapsed_time(ev1) / args.steps
+    split_ms = combine_ms = None
+    if not args.no_profile:
+        s_ms, c_ms, n = gqa.profile_read()
+        gqa.profile_enable(0)
+        split_ms, combine_ms = s_ms / n, c_ms / n
+    print(f"[bench] {args.steps} steps: {ms_per_step * 1e3:.2f} us/step (events), "
+          f"wall {wall / args.steps * 1e6:.2f} us/step", file=sys.stderr, flush=True)
+
+    if args.calibrate_copy:
+        src = torch.empty(1 << 30, dtype=torch.uint8, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
+
+    gbs = step_bytes / (ms_per_step * 1e-3) / 1e9
+    roofline = None
+    if split_ms:
+        achieved = split_bytes / (split_ms * 1e-3) / 1e9
+        roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
+                    "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+                    "traffic": read_traffic(args.workload),
+                    "kernel": "decode_split_kernel", "kernel_us": round(split_ms * 1e3, 2),
+                    "combine_us": round(combine_ms * 1e3, 2), "bytes_per_launch": split_bytes}
+    result = {
+        "metric": METRIC,
+        "value": round(gbs, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 5),
+        "us_per_step": round(ms_per_step * 1e3, 2),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": f"synthetic N(0,1) BF16, seed {args.seed}, lengths U[{lo},{hi}]" if lo else
+                f"synthetic N(0,1) BF16, seed {args.seed}",
+        "config": {"workload": args.workload, "batch": bsz, "capacity": cap,
+                   "min_len": lo, "max_len": hi, "total_keys": sum(lens), "q_heads": 32,
+                   "kv_heads": 8, "head_dim": 128, "rope": "q", "accumulate": "fp32",
+                   "bytes_per_step": step_bytes},
+        "roofline": roofline,
+        "cpu_baseline": None if args.no_cpu_baseline else cpu_baseline(
+            stimulus.DecodeBatch(batch.q.cpu(), batch.k, batch.v, batch.seq_len,
+                                 batch.query_pos)),
+    }
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

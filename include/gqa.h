@@ -1,0 +1,147 @@
+/*
+ * gqa.h -- C ABI of libgqa.so: the Llama-3-8B GQA attention step on MI355X (gfx950).
+ *
+ * Geometry is fixed, as in the reference core: 32 Q heads over 8 KV heads (group 4),
+ * head_dim 128, BF16 in and out, RoPE rotate_half with theta 500000, scores scaled
+ * by 1/sqrt(128), masked online softmax, weighted V.
+ *
+ * The ABI replaces the reference core's host contract:
+ *   - AXI-Lite register file          axi_lite_regs.v:5-24 (N_Q_HEADS, N_KV_HEADS,
+ *     HEAD_DIM, TILE_DIM, SEQ_LEN, N_KV_TILES, SCALE, QUERY_POSITION, CTRL.start,
+ *     STATUS.done/error)                        -> gqa_params_t + per-sequence arrays
+ *   - start-time config rejection      gqa_attention_wrapper.v:230-244
+ *                                               -> gqa_validate_registers / status codes
+ *   - AXIS ingress of Q rows and K/V rows in position order (README.md:24-39,
+ *     tests/tb_gqa_attention_wrapper.sv:174-193)  -> device pointers + gqa_kv_layout_t
+ *   - AXIS egress, 32 rows x 128 BF16 in Q-head order (gqa_output_collector.v:32-61)
+ *                                               -> out[B][32][128]
+ *   - rope_unit (rope_unit.v:38-330) in isolation, as tests/tb_rope_unit.sv drives it
+ *                                               -> gqa_rope_rows_bf16
+ *
+ * Conventions: every data pointer is a device pointer; BF16 values are passed as
+ * their 16-bit codes.  Calls are asynchronous on `stream` (a hipStream_t, NULL =
+ * the default stream) and allocate nothing; the caller owns every buffer,
+ * including the workspace.  On any non-zero status nothing was launched and no
+ * output was written (the reference suppresses start and raises its error flag).
+ * Calls are re-entrant from any host thread given distinct workspaces.
+ */
+#ifndef GQA_H
+#define GQA_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Status codes.  GQA_ERR_INVALID_CONFIG is the STATUS.error of
+ * gqa_attention_wrapper.v:288 (bad geometry, zero scale, bad lengths). */
+enum gqa_status {
+    GQA_OK = 0,
+    GQA_ERR_INVALID_CONFIG = 1,
+    GQA_ERR_BAD_POINTER = 2,   /* NULL or misaligned pointer / stride */
+    GQA_ERR_WORKSPACE = 3,     /* workspace missing or smaller than required */
+    GQA_ERR_HIP = 4            /* the HIP runtime refused the launch */
+};
+
+/* Operand rotation flags.  The reference rotates Q at query_position and every
+ * K row at its cache position (gen_gqa_wrapper_vectors.py:124-126,
+ * gqa_attention_wrapper.v:302-308).  A cache stored post-RoPE drops GQA_ROPE_K. */
+#define GQA_ROPE_Q 1u
+#define GQA_ROPE_K 2u
+
+/* Geometry, scale and RoPE: the register subset that shapes the arithmetic.
+ * Only n_q_heads=32, n_kv_heads=8, head_dim=128 are accepted
+ * (gqa_attention_wrapper.v:231-233). */
+typedef struct gqa_params {
+    int32_t n_q_heads;
+    int32_t n_kv_heads;
+    int32_t head_dim;
+    float scale;          /* score scale, normally 1/sqrt(128); 0 is rejected (wrapper.v:237) */
+    double rope_theta;    /* normally 500000; must be > 0 when a RoPE flag is set */
+    uint32_t flags;       /* GQA_ROPE_Q | GQA_ROPE_K */
+} gqa_params_t;
+
+/* Where K/V rows live.  Row (sequence b, KV head h, position p) starts at element
+ * b*batch_stride + h*head_stride + p*pos_stride of the K (and V) base; each row
+ * is 128 contiguous BF16.  Strides are in elements and multiples of 8; pointers
+ * 16-byte aligned.  capacity = positions allocated per sequence. */
+typedef struct gqa_kv_layout {
+    int64_t batch_stride;
+    int64_t head_stride;
+    int64_t pos_stride;
+    int32_t capacity;
+} gqa_kv_layout_t;
+
+/* Host-side check of the reference's register set, as the core does at start
+ * (gqa_attention_wrapper.v:230-237): n_q_heads==32, n_kv_heads==8, head_dim==128,
+ * tile_dim==16, seq_len!=0, n_kv_tiles==ceil(seq_len/kv_block_len), scale_bf16!=0.
+ * kv_block_len is the core's KV_BLOCK_LEN parameter (16, or 4 on PYNQ-Z2).
+ * Returns GQA_OK or GQA_ERR_INVALID_CONFIG. */
+int gqa_validate_registers(int32_t n_q_heads, int32_t n_kv_heads, int32_t head_dim,
+                           int32_t tile_dim, int32_t seq_len, int32_t n_kv_tiles,
+                           int32_t kv_block_len, uint16_t scale_bf16);
+
+/* Host-side check of per-sequence lengths (host arrays): 1 <= seq_len[b] <= capacity
+ * and 0 <= query_pos[b] < seq_len[b] (gen_gqa_wrapper_vectors.py:73-78).  The
+ * decode call reads its length arrays on the device; callers holding host copies
+ * use this to reject bad lengths before launching.  Returns GQA_OK or
+ * GQA_ERR_INVALID_CONFIG. */
+int gqa_validate_lengths(const int32_t* seq_len, const int32_t* query_pos, int32_t batch,
+                         int32_t capacity);
+
+/* Workspace bytes gqa_decode_bf16 needs for `batch` sequences of up to `capacity`
+ * positions.  0 if the configuration is invalid. */
+size_t gqa_decode_workspace_bytes(const gqa_params_t* params, int32_t batch, int32_t capacity);
+
+/* One decode step for a batch of sequences (the reference core computes batch 1):
+ *   q          [batch][32][128]  Q rows of the token at query_pos[b]
+ *   k, v       cache rows per `kv` (positions in order)
+ *   seq_len    [batch] int32, device: valid cache length
+ *   query_pos  [batch] int32, device: position of the query token
+ *   out        [batch][32][128]  output rows in Q-head order
+ * Key p of sequence b contributes iff p < seq_len[b] and p <= query_pos[b]
+ * (gqa_attention_wrapper.v:279); rows outside that range are never read.
+ * Lengths are read on the device: an entry violating the rules of
+ * gqa_validate_lengths yields NaN rows for that sequence (never an out-of-range read).
+ * Replaces CTRL.start of axi_lite_regs.v:147-151 and the stream/egress contract. */
+int gqa_decode_bf16(const gqa_params_t* params, const uint16_t* q, const uint16_t* k,
+                    const uint16_t* v, const gqa_kv_layout_t* kv, const int32_t* seq_len,
+                    const int32_t* query_pos, int32_t batch, uint16_t* out, void* workspace,
+                    size_t workspace_bytes, void* stream);
+
+/* rope_unit in isolation (rope_unit.v:38-330 as tests/tb_rope_unit.sv drives it;
+ * golden pyfiles/gen_rope_test_vectors.py:16-20): out[r] = BF16(rope(in[r], position)),
+ * position = positions[r] if positions != NULL (device int32) else pos0 + r.
+ * Rows are 128 BF16 with row stride `row_stride` elements (in and out). */
+int gqa_rope_rows_bf16(const uint16_t* in, uint16_t* out, int64_t n_rows, int64_t row_stride,
+                       const int32_t* positions, int32_t pos0, double theta, void* stream);
+
+/* Kernel timing for measurement harnesses.  While enabled, each decode call
+ * brackets its split-KV kernel and its combine kernel with HIP events on the
+ * call's stream (up to `max_calls` calls are recorded; later ones are not).
+ * gqa_profile_read waits for the recorded events, returns the summed kernel
+ * times and the number of calls recorded, and clears the record.  Not for the
+ * hot path: enabling creates the events.  No reference counterpart (the
+ * reference's timing is its simulator's cycle count). */
+typedef struct gqa_profile {
+    double split_ms;      /* summed duration of the split-KV kernel launches */
+    double combine_ms;    /* summed duration of the combine kernel launches */
+    int32_t calls;        /* decode calls recorded */
+} gqa_profile_t;
+
+int gqa_profile_enable(int32_t max_calls); /* max_calls <= 0 disables and frees */
+int gqa_profile_read(gqa_profile_t* out);
+
+/* Human-readable name of a status code. */
+const char* gqa_status_string(int status);
+
+/* ABI version: (major << 16) | minor. */
+uint32_t gqa_abi_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* GQA_H */

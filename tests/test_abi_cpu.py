@@ -1,0 +1,132 @@
+"""C-ABI checks that need no GPU: the library loads, exports every function
+include/gqa.h declares, and rejects bad configurations before any launch
+(gqa_attention_wrapper.v:230-244: start suppressed, error flag raised)."""
+from __future__ import annotations
+
+import ctypes
+import math
+import re
+
+import pytest
+
+from attention_accelerator_amd import _lib
+from attention_accelerator_amd._lib import GqaKvLayout, GqaParams
+from conftest import ROOT
+
+OK, BAD_CFG, BAD_PTR, BAD_WS = 0, 1, 2, 3
+
+
+def header_functions():
+    text = (ROOT / "include" / "gqa.h").read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(gqa_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_exports_match_header():
+    declared = header_functions()
+    assert declared == sorted(_lib.EXPORTS)
+    L = _lib.lib()
+    for name in declared:
+        assert hasattr(L, name), name
+
+
+def test_status_strings_and_version():
+    assert _lib.status_string(0) == "ok"
+    assert "invalid" in _lib.status_string(1)
+    assert _lib.lib().gqa_abi_version() >> 16 == 1
+
+
+@pytest.mark.parametrize("regs,ok", [
+    ((32, 8, 128, 16, 30, 2, 16, 0x3DB5), True),
+    ((32, 8, 128, 16, 13, 4, 4, 0x3DB5), True),      # PYNQ-Z2 KV_BLOCK_LEN=4
+    ((31, 8, 128, 16, 30, 2, 16, 0x3DB5), False),    # N_Q_HEADS (tb_gqa_attention_wrapper.sv:323)
+    ((32, 4, 128, 16, 30, 2, 16, 0x3DB5), False),    # N_KV_HEADS
+    ((32, 8, 64, 16, 30, 2, 16, 0x3DB5), False),     # HEAD_DIM
+    ((32, 8, 128, 8, 30, 2, 16, 0x3DB5), False),     # TILE_DIM
+    ((32, 8, 128, 16, 0, 0, 16, 0x3DB5), False),     # SEQ_LEN == 0
+    ((32, 8, 128, 16, 30, 1, 16, 0x3DB5), False),    # N_KV_TILES != ceil(30/16)
+    ((32, 8, 128, 16, 32, 3, 16, 0x3DB5), False),
+    ((32, 8, 128, 16, 30, 2, 16, 0x0000), False),    # SCALE == 0
+])
+def test_validate_registers(regs, ok):
+    st = _lib.lib().gqa_validate_registers(*regs)
+    assert st == (OK if ok else BAD_CFG)
+
+
+def _lens(vals):
+    arr = (ctypes.c_int32 * len(vals))(*vals)
+    return arr
+
+
+@pytest.mark.parametrize("sl,qp,cap,want", [
+    ([30], [29], 32, OK), ([1], [0], 1, OK), ([30, 17], [10, 16], 32, OK),
+    ([30], [30], 32, BAD_CFG), ([30], [-1], 32, BAD_CFG), ([0], [0], 32, BAD_CFG),
+    ([33], [0], 32, BAD_CFG),
+])
+def test_validate_lengths(sl, qp, cap, want):
+    assert _lib.lib().gqa_validate_lengths(_lens(sl), _lens(qp), len(sl), cap) == want
+
+
+def _params(**kw):
+    base = dict(n_q_heads=32, n_kv_heads=8, head_dim=128, scale=1 / math.sqrt(128),
+                rope_theta=500000.0, flags=1)
+    base.update(kw)
+    return GqaParams(**base)
+
+
+def test_workspace_bytes():
+    L = _lib.lib()
+    p = _params()
+    n = L.gqa_decode_workspace_bytes(ctypes.byref(p), 64, 8192)
+    assert n > 0 and n % 256 == 0
+    assert L.gqa_decode_workspace_bytes(ctypes.byref(_params(n_q_heads=31)), 64, 8192) == 0
+    assert L.gqa_decode_workspace_bytes(ctypes.byref(p), 0, 8192) == 0
+
+
+def _decode(p, *, q=256, k=256, v=256, layout=None, sl=256, qp=256, batch=1, out=256,
+            ws=256, ws_bytes=1 << 30):
+    L = _lib.lib()
+    layout = layout or GqaKvLayout(8 * 64 * 128, 64 * 128, 128, 64)
+    return L.gqa_decode_bf16(ctypes.byref(p) if p is not None else None, q, k, v,
+                             ctypes.byref(layout), sl, qp, batch, out, ws, ws_bytes, None)
+
+
+@pytest.mark.parametrize("kw,want", [
+    (dict(p=_params(n_q_heads=31)), BAD_CFG),
+    (dict(p=_params(n_kv_heads=4)), BAD_CFG),
+    (dict(p=_params(head_dim=64)), BAD_CFG),
+    (dict(p=_params(scale=0.0)), BAD_CFG),
+    (dict(p=_params(scale=float("nan"))), BAD_CFG),
+    (dict(p=_params(rope_theta=0.0)), BAD_CFG),
+    (dict(p=_params(flags=8)), BAD_CFG),
+    (dict(p=_params(), batch=0), BAD_CFG),
+    (dict(p=_params(), layout=GqaKvLayout(0, 0, 64, 64)), BAD_CFG),
+    (dict(p=_params(), layout=GqaKvLayout(0, 0, 128, 0)), BAD_CFG),
+    (dict(p=None), BAD_PTR),
+    (dict(p=_params(), q=None), BAD_PTR),
+    (dict(p=_params(), k=None), BAD_PTR),
+    (dict(p=_params(), out=None), BAD_PTR),
+    (dict(p=_params(), sl=None), BAD_PTR),
+    (dict(p=_params(), k=264), BAD_PTR),                        # K not 16-byte aligned
+    (dict(p=_params(), layout=GqaKvLayout(8, 0, 132, 64)), BAD_PTR),   # stride % 8
+    (dict(p=_params(), ws=None), BAD_WS),
+    (dict(p=_params(), ws_bytes=16), BAD_WS),
+])
+def test_decode_rejects_before_launch(kw, want):
+    """Every rejection returns before touching the device (the fake pointers here
+    would fault if anything were launched)."""
+    assert _decode(**kw) == want
+
+
+def test_rope_rejects():
+    L = _lib.lib()
+    assert L.gqa_rope_rows_bf16(256, 256, 4, 64, None, 0, 500000.0, None) == BAD_CFG
+    assert L.gqa_rope_rows_bf16(256, 256, 4, 128, None, 0, -1.0, None) == BAD_CFG
+    assert L.gqa_rope_rows_bf16(None, 256, 4, 128, None, 0, 500000.0, None) == BAD_PTR
+    assert L.gqa_rope_rows_bf16(None, None, 0, 128, None, 0, 500000.0, None) == OK
+
+
+def test_profile_read_empty():
+    p = _lib.GqaProfile()
+    assert _lib.lib().gqa_profile_read(ctypes.byref(p)) == OK
+    assert p.calls == 0

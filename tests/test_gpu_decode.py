@@ -1,0 +1,195 @@
+"""Decode kernel parity against the compiled oracle (oracle/oracle.py) on N(0,1)
+BF16 inputs, the masking rules, and size-independent properties.
+
+Tolerance: 64 BF16 ULP per element with the reference checker's tiny-value
+exemption (pyfiles/check_gqa_output.py:33-34,57-64).  Cache rows that the mask
+excludes hold NaN, so any read of one would poison the output."""
+from __future__ import annotations
+
+import os
+
+import numpy as np
+import pytest
+import torch
+
+import attention_accelerator_amd as gqa
+from attention_accelerator_amd import stimulus
+from oracle import golden_model as gm
+from oracle import oracle as orc
+from _util import assert_within_ulp, to_codes, to_dev
+
+pytestmark = pytest.mark.gpu
+
+
+def _codes(t: torch.Tensor) -> np.ndarray:
+    return to_codes(t)
+
+
+def _oracle(batch: stimulus.DecodeBatch, rope_k=False, kv_heads=None):
+    return orc.decode(_codes(batch.q), _codes(batch.k), _codes(batch.v),
+                      batch.seq_len.numpy(), batch.query_pos.numpy(), rope_k=rope_k,
+                      kv_heads=kv_heads)
+
+
+def _run(batch: stimulus.DecodeBatch, dev, **kw):
+    out = gqa.gqa_attention(batch.q.to(dev), batch.k.to(dev), batch.v.to(dev),
+                            batch.query_pos, batch.seq_len, **kw)
+    torch.cuda.synchronize()
+    return _codes(out)
+
+
+def test_golden_smoke_normal_len30(dev):
+    """The golden smoke case: N(0,1), SEQ_LEN=30, qpos 29, RoPE on Q and K."""
+    q, k, v = gm.stimulus("normal", 30, 20260805)
+    want = np.array(gm.golden_attention(q, k, v, 30, 29), dtype=np.uint16)
+    got = _codes(gqa.gqa_attention(to_dev(q, dev), to_dev(k, dev), to_dev(v, dev), 29, 30,
+                                   rope_q=True, rope_k=True))
+    assert_within_ulp(want, got, 64, "normal L=30")
+
+
+def test_single_sequence_4096(dev):
+    """B=1, L=4096, qpos 4095, K cache post-RoPE (only Q rotated)."""
+    b = stimulus.decode_batch(1, 4096, seed=11)
+    w = assert_within_ulp(_oracle(b), _run(b, dev), 64, "L=4096")
+    print("worst ULP", w)
+
+
+@pytest.mark.parametrize("seed", [1, 2])
+def test_ragged_batch(dev, seed):
+    b = stimulus.decode_batch(12, 1536, min_len=1, max_len=1536, seed=seed)
+    assert_within_ulp(_oracle(b), _run(b, dev), 64, f"ragged seed {seed}")
+
+
+def test_causal_mask_differs_from_padding(dev):
+    """query_position < seq_len - 1: rows qpos+1 .. seq_len-1 are valid cache rows that
+    the causal mask excludes; they hold NaN here and must not be read."""
+    g = torch.Generator().manual_seed(5)
+    lengths = torch.randint(2, 700, (6,), generator=g).to(torch.int32)
+    b = stimulus.decode_batch(6, 704, lengths=lengths, seed=6)
+    qpos = torch.tensor([int(torch.randint(0, int(x) - 1, (1,), generator=g)) for x in lengths],
+                        dtype=torch.int32)
+    k, v = b.k.clone(), b.v.clone()
+    for i in range(6):
+        k[i, :, int(qpos[i]) + 1:] = float("nan")
+        v[i, :, int(qpos[i]) + 1:] = float("nan")
+    b = stimulus.DecodeBatch(b.q, k, v, b.seq_len, qpos)
+    got = _run(b, dev)
+    assert np.isfinite(got.view(np.int16).astype(np.float32)).all()
+    assert_within_ulp(_oracle(b), got, 64, "causal")
+
+
+def test_seq_len_one_is_v0_exactly(dev):
+    """One visible key: weight 1, output = V[0] bit for bit."""
+    b = stimulus.decode_batch(3, 64, lengths=torch.tensor([1, 1, 1]), seed=7)
+    got = _run(b, dev)
+    v0 = _codes(b.v[:, :, 0])                      # [B, 8, 128]
+    want = np.repeat(v0, 4, axis=1)                # Q head h uses KV head h // 4
+    assert np.array_equal(got, want)
+
+
+def test_equal_scores_give_mean_of_v(dev):
+    """Smoke mode of the reference generator: Q = K = 0, every visible score equal,
+    output = BF16(mean of V rows 0..qpos) (pyfiles/gen_gqa_wrapper_vectors.py:4-7)."""
+    q, k, v = gm.stimulus("smoke", 45, 1)
+    got = _codes(gqa.gqa_attention(to_dev(q, dev), to_dev(k, dev), to_dev(v, dev), 40, 45,
+                                   rope_q=True, rope_k=True))
+    vv = (np.array(v, dtype=np.uint32) << 16).view(np.float32).astype(np.float64)
+    mean = vv[:, :41].mean(axis=1)                              # [8, 128]
+    want = np.array([[gm.f32_to_bf16(x) for x in mean[h // 4]] for h in range(32)],
+                    dtype=np.uint16)
+    assert_within_ulp(want, got, 2, "mean of V")
+
+
+def test_deterministic(dev):
+    b = stimulus.decode_batch(8, 2048, min_len=100, max_len=2048, seed=8)
+    assert np.array_equal(_run(b, dev), _run(b, dev))
+
+
+@pytest.mark.parametrize("split", ["64", "320", "2048"])
+def test_split_size_invariance(dev, split, monkeypatch):
+    b = stimulus.decode_batch(4, 3000, min_len=1000, max_len=3000, seed=9)
+    monkeypatch.setenv("GQA_SPLIT_KEYS", split)
+    got = _run(b, dev)
+    assert_within_ulp(_oracle(b), got, 64, f"split {split}")
+
+
+def test_position_major_cache_layout(dev):
+    """Cache stored [B][S][8][128] (position-major) gives the same bits as [B][8][S][128]."""
+    b = stimulus.decode_batch(3, 500, min_len=200, max_len=500, seed=10)
+    ref = _run(b, dev)
+    kp = b.k.permute(0, 2, 1, 3).contiguous().to(dev).permute(0, 2, 1, 3)
+    vp = b.v.permute(0, 2, 1, 3).contiguous().to(dev).permute(0, 2, 1, 3)
+    out = gqa.gqa_attention(b.q.to(dev), kp, vp, b.query_pos, b.seq_len)
+    assert np.array_equal(_codes(out), ref)
+
+
+def test_no_rope(dev):
+    b = stimulus.decode_batch(2, 300, min_len=100, max_len=300, seed=12)
+    want = orc.decode(_codes(b.q), _codes(b.k), _codes(b.v), b.seq_len.numpy(),
+                      b.query_pos.numpy(), rope_q=False, rope_k=False)
+    got = _run(b, dev, rope_q=False, rope_k=False)
+    assert_within_ulp(want, got, 64, "no rope")
+
+
+def test_rope_on_k_long(dev):
+    """RoPE on K inside the kernel (the reference's unrotated cache) at 2K positions."""
+    b = stimulus.decode_batch(2, 2048, min_len=1500, max_len=2048, seed=13)
+    want = _oracle(b, rope_k=True)
+    got = _run(b, dev, rope_q=True, rope_k=True)
+    assert_within_ulp(want, got, 64, "rope_k")
+
+
+def test_device_resident_lengths(dev):
+    b = stimulus.decode_batch(5, 900, min_len=10, max_len=900, seed=14)
+    ref = _run(b, dev)
+    out = gqa.gqa_attention(b.q.to(dev), b.k.to(dev), b.v.to(dev),
+                            b.query_pos.to(dev), b.seq_len.to(dev))
+    assert np.array_equal(_codes(out), ref)
+
+
+def test_invalid_device_lengths_give_nan_rows(dev):
+    b = stimulus.decode_batch(3, 256, lengths=torch.tensor([100, 50, 200]), seed=15)
+    qpos = torch.tensor([99, 50, 199], dtype=torch.int32)      # sequence 1: qpos == seq_len
+    out = _codes(gqa.gqa_attention(b.q.to(dev), b.k.to(dev), b.v.to(dev), qpos.to(dev),
+                                   b.seq_len.to(dev)))
+    assert (out[1] == 0x7FC0).all()
+    good = stimulus.DecodeBatch(b.q[[0, 2]], b.k[[0, 2]], b.v[[0, 2]], b.seq_len[[0, 2]],
+                                qpos[[0, 2]])
+    assert_within_ulp(_oracle(good), out[[0, 2]], 64, "valid rows next to an invalid one")
+
+
+def test_host_validation_rejects(dev):
+    b = stimulus.decode_batch(2, 64, lengths=torch.tensor([10, 20]), seed=16)
+    q, k, v = b.q.to(dev), b.k.to(dev), b.v.to(dev)
+    out = torch.full((2, 32, 128), 7.0, dtype=torch.bfloat16, device=dev)
+    for qpos, sl in (([10, 5], [10, 20]), ([-1, 5], [10, 20]), ([5, 5], [0, 20]),
+                     ([5, 5], [65, 20])):
+        with pytest.raises(gqa.GqaConfigError):
+            gqa.gqa_attention(q, k, v, qpos, sl, out=out)
+    torch.cuda.synchronize()
+    assert (out.float() == 7.0).all()      # a rejected call writes nothing
+
+
+def test_north_star_batch64_ragged(dev):
+    """B=64, lengths U[512, 8192], capacity 8192, NaN in unused rows: every output
+    against the oracle."""
+    b = stimulus.decode_batch(64, 8192, min_len=512, max_len=8192, seed=20260805,
+                              gen_device="cuda", device=dev)
+    got = _codes(gqa.gqa_attention(b.q, b.k, b.v, b.query_pos, b.seq_len))
+    w = assert_within_ulp(_oracle(b), got, 64, "B=64 ragged")
+    print("worst ULP", w)
+
+
+def test_long_context_131072(dev):
+    """B=8, L=131072 (multi-split combine): sequences 0 and 5, KV heads 0 and 7, against
+    the oracle; the whole batch finite and deterministic."""
+    b = stimulus.decode_batch(8, 131072, seed=20260805, gen_device="cuda", device=dev)
+    out1 = _codes(gqa.gqa_attention(b.q, b.k, b.v, b.query_pos, b.seq_len))
+    out2 = _codes(gqa.gqa_attention(b.q, b.k, b.v, b.query_pos, b.seq_len))
+    assert np.array_equal(out1, out2)
+    for s in (0, 5):
+        sub = stimulus.DecodeBatch(b.q[s:s + 1], b.k[s:s + 1], b.v[s:s + 1], b.seq_len[s:s + 1],
+                                   b.query_pos[s:s + 1])
+        want = _oracle(sub, kv_heads=[0, 7])
+        rows = [h for kvh in (0, 7) for h in range(4 * kvh, 4 * kvh + 4)]
+        assert_within_ulp(want[0, rows], out1[s, rows], 64, f"L=131072 seq {s}")
