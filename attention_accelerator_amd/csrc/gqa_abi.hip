@@ -21,15 +21,17 @@ void fill_rope_table(double theta, RopeTable* t) {
 
 namespace {
 
-constexpr int64_t kTargetWaves = 8192;
+// Persistent workgroups of the decode stream kernel: one wave each, eight per CU on
+// the 256 CUs of an MI355X.  GQA_STREAM_WGS overrides it (tuning only).
+constexpr int32_t kStreamWgs = 2048;
 
 size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
 
-int split_keys_override() {
-    const char* s = std::getenv("GQA_SPLIT_KEYS");
-    if (!s) return 0;
+int32_t stream_wgs() {
+    const char* s = std::getenv("GQA_STREAM_WGS");
+    if (!s) return kStreamWgs;
     const int v = std::atoi(s);
-    return (v >= 64 && v % 64 == 0) ? v : 0;
+    return (v >= 1 && v <= 65536) ? v : kStreamWgs;
 }
 
 bool geometry_ok(const gqa_params_t* p) {
@@ -67,20 +69,13 @@ hipEvent_t* profile_slot() {
 }  // namespace
 
 DecodePlan plan_decode(int32_t batch, int32_t capacity) {
+    (void)capacity;
     DecodePlan plan{};
-    int64_t split = split_keys_override();
-    if (split == 0) {
-        const int64_t total = static_cast<int64_t>(batch) * kHkv * capacity;
-        split = (total + kTargetWaves - 1) / kTargetWaves;
-        split = (split + 63) / 64 * 64;
-        if (split < 64) split = 64;
-        if (split > 4096) split = 4096;
-    }
-    plan.split_keys = static_cast<int32_t>(split);
-    plan.n_splits = static_cast<int32_t>((capacity + split - 1) / split);
-    const size_t units = static_cast<size_t>(batch) * kHkv * plan.n_splits;
-    plan.workspace_bytes = align_up(units * kGroup * kD * sizeof(float), 256) +
-                           align_up(units * kGroup * sizeof(float2), 256);
+    plan.n_wgs = stream_wgs();
+    plan.n_slots = static_cast<int64_t>(plan.n_wgs) + static_cast<int64_t>(kHkv) * batch;
+    plan.workspace_bytes =
+        align_up(static_cast<size_t>(plan.n_slots) * kGroup * kD * sizeof(double), 256) +
+        align_up(static_cast<size_t>(plan.n_slots) * kGroup * sizeof(float2), 256);
     return plan;
 }
 
@@ -157,17 +152,17 @@ int gqa_decode_bf16(const gqa_params_t* params, const uint16_t* q, const uint16_
     a.seq_len = seq_len;
     a.query_pos = query_pos;
     a.out = out;
-    const size_t units = static_cast<size_t>(batch) * kHkv * plan.n_splits;
-    a.part_o = static_cast<float*>(workspace);
-    a.part_ml = reinterpret_cast<float2*>(static_cast<char*>(workspace) +
-                                          align_up(units * kGroup * kD * sizeof(float), 256));
+    a.part_o = static_cast<double*>(workspace);
+    a.part_ml = reinterpret_cast<float2*>(
+        static_cast<char*>(workspace) +
+        align_up(static_cast<size_t>(plan.n_slots) * kGroup * kD * sizeof(double), 256));
     a.kv_batch_stride = kv->batch_stride;
     a.kv_head_stride = kv->head_stride;
     a.kv_pos_stride = kv->pos_stride;
     a.capacity = kv->capacity;
-    a.split_keys = plan.split_keys;
-    a.n_splits = plan.n_splits;
-    a.qk_scale_log2 = static_cast<float>(static_cast<double>(params->scale) * 1.4426950408889634);
+    a.batch = batch;
+    a.n_wgs = plan.n_wgs;
+    a.qk_scale_log2 = static_cast<double>(params->scale) * 1.4426950408889634;
     a.flags = params->flags;
     fill_rope_table(params->rope_theta, &a.rope);
     const hipError_t e = launch_decode(a, batch, static_cast<hipStream_t>(stream), profile_slot());

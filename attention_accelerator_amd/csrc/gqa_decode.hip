@@ -1,61 +1,164 @@
-// gqa_decode.hip -- split-KV GQA decode for gfx950.
+// gqa_decode.hip -- GQA decode for gfx950: stream-K split over all keys of the batch,
+// QK^T on MFMA, weighted V on fp64 VALU, exact log-sum-exp combine.
 //
-// One decode step of the reference core (gqa_controller.v:140-277 loop nest,
-// datapath rope_unit -> bf16_dot_product_mac -> scale_unit -> flash_softmax ->
+// One decode step of the reference core (gqa_controller.v:140-277 loop nest, datapath
+// rope_unit -> bf16_dot_product_mac -> scale_unit -> flash_softmax ->
 // output_accumulator) becomes two launches:
 //
-//   1. decode_split_kernel: grid (split, kv_head, sequence), one wave each.  The
-//      wave rotates and scales the 4 Q rows of its group once, then streams its
-//      slice of K/V rows from HBM exactly once, reusing every row for the 4 Q
-//      heads (gqa_kv_broadcast.v:38-59).  Scores, the running max and sum, and the
-//      weighted-V accumulator stay fp32 (flash_softmax.v:233-490,
-//      output_accumulator.v:244-536).  It writes an unnormalised partial
-//      (O[4][128], m, l) per (sequence, kv_head, split).
-//   2. decode_combine_kernel: grid (q_head, sequence); merges the splits with a
-//      log-sum-exp rescale, divides by the sum (output_accumulator.v:540-686) and
-//      rounds to BF16 in Q-head order (gqa_output_collector.v:32-61).
+// 1. decode_stream_kernel, a persistent grid of n_wgs one-wave workgroups.  The keys
+//    of every (sequence, kv_head) segment are laid end to end (segment = b*8 + h,
+//    n_valid(b) keys each) and cut into n_wgs equal ranges, one per workgroup, so
+//    every wave streams the same number of K/V rows whatever the length mix.  The
+//    part of one segment inside one range is a "piece"; each piece leaves an
+//    unnormalised partial (O[4][128] in fp64, running max m, sum l) at slot
+//    wg + segment, which is unique because both increase along the key order.
+//    Inside a piece the wave rotates and scales the 4 Q rows of its group once
+//    and reuses every K/V row for the 4 Q heads (gqa_kv_broadcast.v:38-59).
+// 2. decode_combine_kernel, one wave per (Q head, sequence): merges the pieces of
+//    its segment, divides by the sum (output_accumulator.v:540-686) and rounds to
+//    BF16 in Q-head order (gqa_output_collector.v:32-61).
+//
+// Arithmetic (the golden model is double, pyfiles/gen_gqa_wrapper_vectors.py:121-139):
+//  * Q is rotated in double, scaled by scale*log2(e) in double and split into three
+//    BF16 parts (hi, mid, lo: ~26 significant bits).  K is BF16 already, so the
+//    bf16 x bf16 MFMA products are exact and the scores carry fp32 accumulation
+//    error only.  With RoPE on K (the reference's unrotated cache) the rotated K row
+//    is split the same way.
+//  * The running max m is kept integer-valued (m = ceil(max score)), so every
+//    rescale of the accumulator and every combine weight is an exact power of two.
+//  * p = exp2(s - m) in fp32; the weighted-V accumulation and the combine run in
+//    fp64 (full-rate on CDNA4), so their rounding never reaches the BF16 output.
 //
 // Masking (gqa_attention_wrapper.v:279): key p counts iff p < seq_len and
-// p <= query_position.  Work is bounded to p < n_valid = min(seq_len, qpos+1);
-// rows past it are never loaded, and inside the last tile invalid keys get a
-// score of -inf and a probability of exactly 0 (flash_softmax.v:319-325).
+// p <= query_position.  Only keys p < n_valid = min(seq_len, qpos+1) are ever
+// loaded; inside the last chunk the other lanes load nothing, score -inf and get
+// p = 0 exactly (flash_softmax.v:319-325).
 //
-// Lane layout inside the wave (64 lanes = 4 rows of 16): lane = 16*r + c holds
-// dims [8c, 8c+8) of key (4*it + r) of the current 64-key tile; one 16-byte load
-// per lane covers four whole K (or V) rows, 1 KB per wave instruction.
+// Lane layouts (wave64, l = lane):
+//  * QK, MFMA f32_16x16x32_bf16 with A = K (row = key l%16), B = Q^T (column
+//    n = l%16: n = 4*split + head for n < 12, zero for n >= 12).  Lane group
+//    g = l/16 and element j of MFMA kb cover head dim d = 32*kb + 8*g + j, so a
+//    lane loads 16 contiguous bytes per kb and holds both halves (d, d+64) of its
+//    RoPE pairs (kb and kb+2).  Output lane l holds score(key 4g+i, column n).
+//  * PV: lane (r = l/16, c = l%16) owns dims [8c, 8c+8) of key 4*it + r of the
+//    chunk; one 16-byte load per lane covers four whole V rows (1 KB contiguous).
 #include "gqa_device.h"
 #include "gqa_internal.h"
 
 namespace gqa {
 
-constexpr int kTile = 64;             // keys per softmax tile (one per lane in phase B)
-constexpr int kIters = kTile / 4;     // 4 keys per wave instruction
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+
+constexpr int kChunk = 16;           // keys per MFMA group
+constexpr int kMinRangeKeys = 64;    // smallest per-workgroup key range
+
+__device__ __forceinline__ int seq_valid_keys(const DecodeArgs& a, int b) {
+    const int L = a.seq_len[b];
+    const int qp = a.query_pos[b];
+    if (L < 1 || L > a.capacity || qp < 0 || qp >= L) return 0;
+    return min(L, qp + 1);
+}
+
+__device__ __forceinline__ int64_t wave_sum_i64(int64_t x) {
+#pragma unroll
+    for (int d = 1; d < kWave; d <<= 1) x += __shfl_xor(x, d);
+    return x;
+}
+
+__device__ __forceinline__ int64_t wave_incl_scan_i64(int64_t x, int lane) {
+#pragma unroll
+    for (int d = 1; d < kWave; d <<= 1) {
+        const int64_t y = __shfl_up(x, d);
+        if (lane >= d) x += y;
+    }
+    return x;
+}
+
+// Total keys over all segments (8 per sequence) and the per-workgroup range size.
+__device__ __forceinline__ void stream_totals(const DecodeArgs& a, int lane, int64_t& total,
+                                              int64_t& per_wg) {
+    int64_t t = 0;
+    for (int base = 0; base < a.batch; base += kWave) {
+        const int b = base + lane;
+        t += wave_sum_i64(b < a.batch ? seq_valid_keys(a, b) : 0);
+    }
+    total = t * kHkv;
+    int64_t per = (total + a.n_wgs - 1) / a.n_wgs;
+    per = per < kMinRangeKeys ? kMinRangeKeys : per;
+    per_wg = (per + kChunk - 1) / kChunk * kChunk;
+}
+
+// Sequence whose segments contain global key offset x (0 <= x < total):
+// returns b and off_b = 8 * (valid keys of sequences before b).
+__device__ __forceinline__ int locate_sequence(const DecodeArgs& a, int lane, int64_t x,
+                                               int64_t& off_b) {
+    int64_t carry = 0;
+    for (int base = 0; base < a.batch; base += kWave) {
+        const int b = base + lane;
+        const int64_t nv = b < a.batch ? seq_valid_keys(a, b) : 0;
+        const int64_t incl = wave_incl_scan_i64(nv, lane) + carry;
+        const uint64_t past = __ballot((incl * kHkv) > x);
+        if (past) {
+            const int first = __ffsll(static_cast<unsigned long long>(past)) - 1;
+            off_b = (__shfl(incl, first) - __shfl(nv, first)) * kHkv;
+            return base + first;
+        }
+        carry = __shfl(incl, kWave - 1);
+    }
+    off_b = carry * kHkv;
+    return a.batch;   // unreachable for x < total
+}
+
+// BF16 code of a double, rounding through f32 (any nearby BF16 value serves as the
+// leading part of a split; the residual is formed exactly in double).
+__device__ __forceinline__ uint16_t bf16_of(double d) { return f32_to_bf16_rne(static_cast<float>(d)); }
+
+__device__ __forceinline__ double f64_of_bf16(uint16_t b) { return static_cast<double>(bf16_to_f32(b)); }
+
+// Split v into hi + mid + lo BF16 codes; returns part `which`.
+__device__ __forceinline__ uint16_t split3(double v, int which) {
+    const uint16_t hi = bf16_of(v);
+    const double r1 = v - f64_of_bf16(hi);
+    const uint16_t mid = bf16_of(r1);
+    if (which == 0) return hi;
+    if (which == 1) return mid;
+    return bf16_of(r1 - f64_of_bf16(mid));
+}
+
+__device__ __forceinline__ bf16x8_t pack8(const uint16_t (&h)[8]) {
+    union {
+        uint16_t u[8];
+        bf16x8_t v;
+    } t;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) t.u[j] = h[j];
+    return t.v;
+}
+
+__device__ __forceinline__ bf16x8_t as_bf16x8(const uint4& w) {
+    union {
+        uint4 u;
+        bf16x8_t v;
+    } t;
+    t.u = w;
+    return t.v;
+}
 
 template <bool kRopeQ, bool kRopeK>
-__global__ __launch_bounds__(kWave) void decode_split_kernel(DecodeArgs a) {
-    const int split = blockIdx.x;
-    const int kvh = blockIdx.y;
-    const int b = blockIdx.z;
+__device__ __forceinline__ void process_piece(const DecodeArgs& a, int b, int kvh, int k_a, int k_b,
+                                              int64_t slot, double (*q_s)[kD],
+                                              float (*p_s)[kChunk][kGroup]) {
     const int lane = threadIdx.x;
-    const int r = lane >> 4;
-    const int c = lane & 15;
-
-    const int seq_len = a.seq_len[b];
+    const int n = lane & 15;       // MFMA column / PV dim chunk
+    const int g = lane >> 4;       // MFMA lane group / PV key row
     const int qpos = a.query_pos[b];
-    if (seq_len < 1 || seq_len > a.capacity || qpos < 0 || qpos >= seq_len) return;
-    const int n_valid = min(seq_len, qpos + 1);
-    const int k0 = split * a.split_keys;
-    if (k0 >= n_valid) return;
-    const int k1 = min(k0 + a.split_keys, n_valid);
 
-    __shared__ float q_s[kGroup][kD];
-    __shared__ float4 tile_s[kTile];
-
-    // ---- Q rows of this group: RoPE at qpos in double, scale * log2(e) folded in.
+    // ---- Q rows of the group: rotate at qpos and scale, in double.
+    __syncthreads();
     {
-        const double inv_freq = a.rope.inv_freq[lane];
         double sn = 0.0, cs = 1.0;
-        if (kRopeQ) sincos(static_cast<double>(qpos) * inv_freq, &sn, &cs);
+        if (kRopeQ) sincos(static_cast<double>(qpos) * a.rope.inv_freq[lane], &sn, &cs);
 #pragma unroll
         for (int h = 0; h < kGroup; ++h) {
             const uint16_t* qrow = a.q + (static_cast<int64_t>(b) * kHq + kvh * kGroup + h) * kD;
@@ -66,129 +169,199 @@ __global__ __launch_bounds__(kWave) void decode_split_kernel(DecodeArgs a) {
                 xr = x * cs - y * sn;
                 yr = x * sn + y * cs;
             }
-            q_s[h][lane] = static_cast<float>(xr) * a.qk_scale_log2;
-            q_s[h][lane + kPairs] = static_cast<float>(yr) * a.qk_scale_log2;
+            q_s[h][lane] = xr * a.qk_scale_log2;
+            q_s[h][lane + kPairs] = yr * a.qk_scale_log2;
         }
     }
     __syncthreads();
-    float q[kGroup][8];
+    // MFMA B operand: column n -> split n/4 of head n%4 (zero for n >= 12).
+    bf16x8_t bq[4];
 #pragma unroll
-    for (int h = 0; h < kGroup; ++h)
+    for (int kb = 0; kb < 4; ++kb) {
+        uint16_t h8[8];
 #pragma unroll
-        for (int j = 0; j < 8; ++j) q[h][j] = q_s[h][8 * c + j];
+        for (int j = 0; j < 8; ++j)
+            h8[j] = n < 12 ? split3(q_s[n & 3][32 * kb + 8 * g + j], n >> 2) : uint16_t(0);
+        bq[kb] = pack8(h8);
+    }
 
     const int64_t head_off = static_cast<int64_t>(b) * a.kv_batch_stride +
                              static_cast<int64_t>(kvh) * a.kv_head_stride;
-    const uint16_t* kbase = a.k + head_off + 8 * c;
-    const uint16_t* vbase = a.v + head_off + 8 * c;
     const int64_t ps = a.kv_pos_stride;
+    const uint16_t* kbase = a.k + head_off + 8 * g;        // + key*ps + 32*kb
+    const uint16_t* vbase = a.v + head_off + 8 * n;        // + key*ps
 
-    float acc[kGroup][8];
-    float m[kGroup], lsum[kGroup];
+    double acc[kGroup][8];
 #pragma unroll
-    for (int h = 0; h < kGroup; ++h) {
-        m[h] = -INFINITY;
-        lsum[h] = 0.f;
+    for (int h = 0; h < kGroup; ++h)
 #pragma unroll
-        for (int j = 0; j < 8; ++j) acc[h][j] = 0.f;
-    }
+        for (int j = 0; j < 8; ++j) acc[h][j] = 0.0;
+    float m_run = -INFINITY;   // integer-valued once set; per lane, meaningful for n < 4
+    float l_run = 0.f;         // per lane partial sum of p for head n (n < 4)
 
-    for (int t0 = k0; t0 < k1; t0 += kTile) {
-        // ---- phase A: scores of 64 keys, 4 per iteration.
-#pragma unroll 4
-        for (int it = 0; it < kIters; ++it) {
-            const int key = t0 + 4 * it + r;
-            uint4 kw = make_uint4(0, 0, 0, 0);
-            if (key < k1) kw = *reinterpret_cast<const uint4*>(kbase + key * ps);
-            float kf[8];
-            unpack8(kw, kf);
-            if (kRopeK) {
-                // Pair (i, i+64) sits in lanes c and c^8 of the same row.
-                float other[8];
+    for (int kc = k_a, parity = 0; kc < k_b; kc += kChunk, parity ^= 1) {
+        // ---- loads: K rows for the MFMA layout, V rows for the PV layout.
+        const int kkey = kc + n;
+        uint4 kw[4];
 #pragma unroll
-                for (int j = 0; j < 8; ++j) other[j] = dpp_f<0x128>(kf[j]);
+        for (int kb = 0; kb < 4; ++kb) {
+            kw[kb] = make_uint4(0, 0, 0, 0);
+            if (kkey < k_b) kw[kb] = *reinterpret_cast<const uint4*>(kbase + kkey * ps + 32 * kb);
+        }
+        uint4 vw[4];
+#pragma unroll
+        for (int it = 0; it < 4; ++it) {
+            const int vkey = kc + 4 * it + g;
+            vw[it] = make_uint4(0, 0, 0, 0);
+            if (vkey < k_b) vw[it] = *reinterpret_cast<const uint4*>(vbase + vkey * ps);
+        }
+
+        // ---- scores: D[key][col] = K[key] . Qsplit[col]
+        f32x4_t d = {0.f, 0.f, 0.f, 0.f};
+        if (kRopeK) {
+            // Rotate the K row at its position: pairs (kb, kb+2) of this lane.
+            double kr[4][8];
+#pragma unroll
+            for (int kb = 0; kb < 2; ++kb) {
+                float xf[8], yf[8];
+                unpack8(kw[kb], xf);
+                unpack8(kw[kb + 2], yf);
 #pragma unroll
                 for (int j = 0; j < 8; ++j) {
-                    const int i = 8 * (c & 7) + j;
-                    const double x = (c < 8) ? kf[j] : other[j];
-                    const double y = (c < 8) ? other[j] : kf[j];
                     double xr, yr;
-                    rope_pair(x, y, key, a.rope.inv_freq[i], xr, yr);
-                    kf[j] = static_cast<float>((c < 8) ? xr : yr);
+                    rope_pair(xf[j], yf[j], kkey, a.rope.inv_freq[32 * kb + 8 * g + j], xr, yr);
+                    kr[kb][j] = xr;
+                    kr[kb + 2][j] = yr;
                 }
             }
-            float s[kGroup];
+#pragma unroll
+            for (int part = 0; part < 3; ++part) {
+#pragma unroll
+                for (int kb = 0; kb < 4; ++kb) {
+                    uint16_t h8[8];
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) h8[j] = split3(kr[kb][j], part);
+                    d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pack8(h8), bq[kb], d, 0, 0, 0);
+                }
+            }
+        } else {
+#pragma unroll
+            for (int kb = 0; kb < 4; ++kb)
+                d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(kw[kb]), bq[kb], d, 0, 0, 0);
+        }
+        // Sum the hi/mid/lo columns n, n+4, n+8 into lanes n < 4 (columns 12..15 are zero,
+        // so the three rotations by 4, 8, 12 within the 16-lane row sum exactly those).
+        float s[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const float x = d[i];
+            s[i] = x + dpp_f<0x124>(x) + dpp_f<0x128>(x) + dpp_f<0x12C>(x);
+            if (kc + 4 * g + i >= k_b) s[i] = -INFINITY;
+        }
+
+        // ---- online softmax on the chunk (head n in lanes n < 4; m integer-valued).
+        float cm = fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3]));
+        cm = fmaxf(cm, __shfl_xor(cm, 16));
+        cm = fmaxf(cm, __shfl_xor(cm, 32));
+        const bool grow = (n < kGroup) && (cm > m_run);
+        if (__ballot(grow)) {
+            const float m_new = grow ? ceilf(cm) : m_run;
+            // 2^(m_run - m_new), exact; 0 when nothing has been accumulated yet.
+            const int shift = (m_run == -INFINITY) ? -1100 : static_cast<int>(m_run - m_new);
+            l_run = ldexpf(l_run, max(shift, -200));
+            m_run = m_new;
+            int sh[kGroup];
+#pragma unroll
+            for (int h = 0; h < kGroup; ++h) sh[h] = __shfl(shift, h);
 #pragma unroll
             for (int h = 0; h < kGroup; ++h) {
-                float t = 0.f;
+                if (sh[h] != 0) {
 #pragma unroll
-                for (int j = 0; j < 8; ++j) t = fmaf(q[h][j], kf[j], t);
-                s[h] = row16_sum(t);
+                    for (int j = 0; j < 8; ++j) acc[h][j] = ldexp(acc[h][j], sh[h]);
+                }
             }
-            if (c == 0) tile_s[4 * it + r] = make_float4(s[0], s[1], s[2], s[3]);
+        }
+        float p[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            p[i] = (s[i] == -INFINITY) ? 0.f : exp2f(s[i] - m_run);
+            l_run += p[i];
+        }
+        if (n < kGroup) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) p_s[parity][4 * g + i][n] = p[i];
         }
         __syncthreads();
 
-        // ---- phase B: online softmax, lane = key.
-        const bool valid = (t0 + lane) < k1;
-        const float4 s4 = tile_s[lane];
-        float s[kGroup] = {s4.x, s4.y, s4.z, s4.w};
-        float p[kGroup], alpha[kGroup];
+        // ---- weighted V in fp64.
 #pragma unroll
-        for (int h = 0; h < kGroup; ++h) {
-            const float sv = valid ? s[h] : -INFINITY;
-            const float m_new = fmaxf(m[h], wave_max(sv));
-            alpha[h] = exp2f(m[h] - m_new);     // m = -inf on the first tile -> 0
-            p[h] = valid ? exp2f(sv - m_new) : 0.f;
-            lsum[h] = lsum[h] * alpha[h] + p[h];
-            m[h] = m_new;
-        }
-        __syncthreads();
-        tile_s[lane] = make_float4(p[0], p[1], p[2], p[3]);
-        __syncthreads();
-#pragma unroll
-        for (int h = 0; h < kGroup; ++h)
-#pragma unroll
-            for (int j = 0; j < 8; ++j) acc[h][j] *= alpha[h];
-
-        // ---- phase C: weighted V.
-#pragma unroll 4
-        for (int it = 0; it < kIters; ++it) {
-            const int key = t0 + 4 * it + r;
-            uint4 vw = make_uint4(0, 0, 0, 0);
-            if (key < k1) vw = *reinterpret_cast<const uint4*>(vbase + key * ps);
+        for (int it = 0; it < 4; ++it) {
+            const float4 p4 = *reinterpret_cast<const float4*>(&p_s[parity][4 * it + g][0]);
             float vf[8];
-            unpack8(vw, vf);
-            const float4 p4 = tile_s[4 * it + r];
-            const float pp[kGroup] = {p4.x, p4.y, p4.z, p4.w};
+            unpack8(vw[it], vf);
+            double vd[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) vd[j] = static_cast<double>(vf[j]);
+            const double pd[kGroup] = {p4.x, p4.y, p4.z, p4.w};
 #pragma unroll
             for (int h = 0; h < kGroup; ++h)
 #pragma unroll
-                for (int j = 0; j < 8; ++j) acc[h][j] = fmaf(pp[h], vf[j], acc[h][j]);
+                for (int j = 0; j < 8; ++j) acc[h][j] = fma(pd[h], vd[j], acc[h][j]);
         }
-        __syncthreads();
     }
 
-    // ---- partial (O, m, l) of this split.
+    // ---- partial of this piece: sum the four key rows, then store.
 #pragma unroll
-    for (int h = 0; h < kGroup; ++h) {
-        lsum[h] = wave_sum(lsum[h]);
+    for (int h = 0; h < kGroup; ++h)
 #pragma unroll
-        for (int j = 0; j < 8; ++j) acc[h][j] = cross_row_sum(acc[h][j]);
-    }
-    const int64_t pidx = (static_cast<int64_t>(b) * kHkv + kvh) * a.n_splits + split;
-    if (r == 0) {
+        for (int j = 0; j < 8; ++j) {
+            acc[h][j] += __shfl_xor(acc[h][j], 16);
+            acc[h][j] += __shfl_xor(acc[h][j], 32);
+        }
+    l_run += __shfl_xor(l_run, 16);
+    l_run += __shfl_xor(l_run, 32);
+    if (g == 0) {
 #pragma unroll
         for (int h = 0; h < kGroup; ++h) {
-            float4* dst = reinterpret_cast<float4*>(a.part_o + (pidx * kGroup + h) * kD + 8 * c);
-            dst[0] = make_float4(acc[h][0], acc[h][1], acc[h][2], acc[h][3]);
-            dst[1] = make_float4(acc[h][4], acc[h][5], acc[h][6], acc[h][7]);
+            double2* dst = reinterpret_cast<double2*>(a.part_o + (slot * kGroup + h) * kD + 8 * n);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) dst[j] = make_double2(acc[h][2 * j], acc[h][2 * j + 1]);
         }
     }
-    if (lane < kGroup) {
-        const float mm = lane == 0 ? m[0] : lane == 1 ? m[1] : lane == 2 ? m[2] : m[3];
-        const float ll = lane == 0 ? lsum[0] : lane == 1 ? lsum[1] : lane == 2 ? lsum[2] : lsum[3];
-        a.part_ml[pidx * kGroup + lane] = make_float2(mm, ll);
+    if (lane < kGroup) a.part_ml[slot * kGroup + lane] = make_float2(m_run, l_run);
+}
+
+template <bool kRopeQ, bool kRopeK>
+__global__ __launch_bounds__(kWave) void decode_stream_kernel(DecodeArgs a) {
+    __shared__ double q_s[kGroup][kD];
+    __shared__ float p_s[2][kChunk][kGroup];
+    const int lane = threadIdx.x;
+    const int64_t w = blockIdx.x;
+
+    int64_t total, per_wg;
+    stream_totals(a, lane, total, per_wg);
+    int64_t x = w * per_wg;
+    if (x >= total) return;
+    const int64_t x_end = min(x + per_wg, total);
+
+    int64_t off_b;
+    int b = locate_sequence(a, lane, x, off_b);
+    int nvb = seq_valid_keys(a, b);
+    int kvh = static_cast<int>((x - off_b) / nvb);
+    int key = static_cast<int>((x - off_b) % nvb);
+    while (true) {
+        const int k_b = static_cast<int>(min(static_cast<int64_t>(nvb), key + (x_end - x)));
+        process_piece<kRopeQ, kRopeK>(a, b, kvh, key, k_b, w + static_cast<int64_t>(b) * kHkv + kvh,
+                                      q_s, p_s);
+        x += k_b - key;
+        if (x >= x_end) break;
+        key = 0;
+        if (++kvh == kHkv) {
+            kvh = 0;
+            nvb = 0;
+            while (nvb == 0 && ++b < a.batch) nvb = seq_valid_keys(a, b);
+            if (nvb == 0) break;   // lengths changed under the launch; nothing left to read
+        }
     }
 }
 
@@ -201,45 +374,53 @@ __global__ __launch_bounds__(kWave) void decode_combine_kernel(DecodeArgs a) {
     const int h = qh % kGroup;
     uint32_t* out = reinterpret_cast<uint32_t*>(a.out + (static_cast<int64_t>(b) * kHq + qh) * kD);
 
-    const int seq_len = a.seq_len[b];
-    const int qpos = a.query_pos[b];
-    if (seq_len < 1 || seq_len > a.capacity || qpos < 0 || qpos >= seq_len) {
+    const int nv = seq_valid_keys(a, b);
+    if (nv == 0) {
         out[lane] = 0x7fc07fc0u;   // NaN row marks a rejected sequence
         return;
     }
-    const int n_valid = min(seq_len, qpos + 1);
-    const int ns = (n_valid + a.split_keys - 1) / a.split_keys;
-    const int64_t base = (static_cast<int64_t>(b) * kHkv + kvh) * a.n_splits;
+    int64_t total, per_wg;
+    stream_totals(a, lane, total, per_wg);
+    int64_t carry = 0;
+    for (int base = 0; base < b; base += kWave) {
+        const int bb = base + lane;
+        carry += wave_sum_i64(bb < b ? seq_valid_keys(a, bb) : 0);
+    }
+    const int64_t seg_off = carry * kHkv + static_cast<int64_t>(kvh) * nv;
+    const int64_t w_first = seg_off / per_wg;
+    const int64_t w_last = (seg_off + nv - 1) / per_wg;
+    const int64_t seg = static_cast<int64_t>(b) * kHkv + kvh;
 
     float mx = -INFINITY;
-    for (int s = 0; s < ns; ++s) mx = fmaxf(mx, a.part_ml[(base + s) * kGroup + h].x);
-    float l = 0.f, o0 = 0.f, o1 = 0.f;
-    for (int s = 0; s < ns; ++s) {
-        const float2 ml = a.part_ml[(base + s) * kGroup + h];
-        const float w = exp2f(ml.x - mx);
-        const float2 o = reinterpret_cast<const float2*>(a.part_o + ((base + s) * kGroup + h) * kD)[lane];
-        l = fmaf(ml.y, w, l);
-        o0 = fmaf(o.x, w, o0);
-        o1 = fmaf(o.y, w, o1);
+    for (int64_t w = w_first; w <= w_last; ++w) mx = fmaxf(mx, a.part_ml[(w + seg) * kGroup + h].x);
+    double l = 0.0, o0 = 0.0, o1 = 0.0;
+    for (int64_t w = w_first; w <= w_last; ++w) {
+        const int64_t slot = w + seg;
+        const float2 ml = a.part_ml[slot * kGroup + h];
+        const int e = max(static_cast<int>(ml.x - mx), -1100);
+        const double2 o = reinterpret_cast<const double2*>(a.part_o + (slot * kGroup + h) * kD)[lane];
+        l += ldexp(static_cast<double>(ml.y), e);
+        o0 += ldexp(o.x, e);
+        o1 += ldexp(o.y, e);
     }
-    const uint32_t lo = f32_to_bf16_rne(o0 / l);
-    const uint32_t hi = f32_to_bf16_rne(o1 / l);
+    const uint32_t lo = f32_to_bf16_rne(static_cast<float>(o0 / l));
+    const uint32_t hi = f32_to_bf16_rne(static_cast<float>(o1 / l));
     out[lane] = lo | (hi << 16);
 }
 
 hipError_t launch_decode(const DecodeArgs& a, int batch, hipStream_t stream, hipEvent_t* ev) {
-    const dim3 grid_split(a.n_splits, kHkv, batch);
+    const dim3 grid_stream(a.n_wgs);
     const dim3 grid_combine(kHq, batch);
     const bool rq = (a.flags & 1u) != 0, rk = (a.flags & 2u) != 0;
     if (ev) (void)hipEventRecord(ev[0], stream);
     if (rq && rk)
-        hipLaunchKernelGGL((decode_split_kernel<true, true>), grid_split, dim3(kWave), 0, stream, a);
+        hipLaunchKernelGGL((decode_stream_kernel<true, true>), grid_stream, dim3(kWave), 0, stream, a);
     else if (rq)
-        hipLaunchKernelGGL((decode_split_kernel<true, false>), grid_split, dim3(kWave), 0, stream, a);
+        hipLaunchKernelGGL((decode_stream_kernel<true, false>), grid_stream, dim3(kWave), 0, stream, a);
     else if (rk)
-        hipLaunchKernelGGL((decode_split_kernel<false, true>), grid_split, dim3(kWave), 0, stream, a);
+        hipLaunchKernelGGL((decode_stream_kernel<false, true>), grid_stream, dim3(kWave), 0, stream, a);
     else
-        hipLaunchKernelGGL((decode_split_kernel<false, false>), grid_split, dim3(kWave), 0, stream, a);
+        hipLaunchKernelGGL((decode_stream_kernel<false, false>), grid_stream, dim3(kWave), 0, stream, a);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     if (ev) (void)hipEventRecord(ev[1], stream);

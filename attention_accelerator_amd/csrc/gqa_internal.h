@@ -16,23 +16,23 @@ struct DecodeArgs {
     const int32_t* seq_len;   // [B]
     const int32_t* query_pos; // [B]
     uint16_t* out;            // [B][32][128]
-    float* part_o;            // [B][8][n_splits][4][128] unnormalised partial outputs
-    float2* part_ml;          // [B][8][n_splits][4] (running max in log2 units, sum)
+    double* part_o;           // [n_slots][4][128] unnormalised partial outputs
+    float2* part_ml;          // [n_slots][4] (integer-valued running max in log2 units, sum)
     int64_t kv_batch_stride;
     int64_t kv_head_stride;
     int64_t kv_pos_stride;
     int32_t capacity;
-    int32_t split_keys;       // keys per split (multiple of 64)
-    int32_t n_splits;         // splits allotted per (sequence, kv head)
-    float qk_scale_log2;      // scale * log2(e), folded into Q
+    int32_t batch;
+    int32_t n_wgs;            // persistent workgroups of the stream kernel
+    double qk_scale_log2;     // scale * log2(e), folded into Q
     uint32_t flags;           // bit0 RoPE on Q, bit1 RoPE on K
     RopeTable rope;
 };
 
-// Split plan for a batch of sequences of up to `capacity` positions.
+// Launch plan for a batch: stream-kernel workgroups and partial slots.
 struct DecodePlan {
-    int32_t split_keys;
-    int32_t n_splits;
+    int32_t n_wgs;
+    int64_t n_slots;          // n_wgs + 8 * batch (one per piece, see gqa_decode.hip)
     size_t workspace_bytes;
 };
 

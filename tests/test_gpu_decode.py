@@ -25,10 +25,10 @@ def _codes(t: torch.Tensor) -> np.ndarray:
     return to_codes(t)
 
 
-def _oracle(batch: stimulus.DecodeBatch, rope_k=False, kv_heads=None):
+def _oracle(batch: stimulus.DecodeBatch, rope_k=False, kv_heads=None, want_f64=False):
     return orc.decode(_codes(batch.q), _codes(batch.k), _codes(batch.v),
                       batch.seq_len.numpy(), batch.query_pos.numpy(), rope_k=rope_k,
-                      kv_heads=kv_heads)
+                      kv_heads=kv_heads, want_f64=want_f64)
 
 
 def _run(batch: stimulus.DecodeBatch, dev, **kw):
@@ -50,7 +50,8 @@ def test_golden_smoke_normal_len30(dev):
 def test_single_sequence_4096(dev):
     """B=1, L=4096, qpos 4095, K cache post-RoPE (only Q rotated)."""
     b = stimulus.decode_batch(1, 4096, seed=11)
-    w = assert_within_ulp(_oracle(b), _run(b, dev), 64, "L=4096")
+    want, want64 = _oracle(b, want_f64=True)
+    w = assert_within_ulp(want, _run(b, dev), 64, "L=4096", ref64=want64)
     print("worst ULP", w)
 
 
@@ -105,12 +106,14 @@ def test_deterministic(dev):
     assert np.array_equal(_run(b, dev), _run(b, dev))
 
 
-@pytest.mark.parametrize("split", ["64", "320", "2048"])
-def test_split_size_invariance(dev, split, monkeypatch):
-    b = stimulus.decode_batch(4, 3000, min_len=1000, max_len=3000, seed=9)
-    monkeypatch.setenv("GQA_SPLIT_KEYS", split)
+@pytest.mark.parametrize("wgs", ["1", "7", "333", "2048", "6000"])
+def test_stream_partition_invariance(dev, wgs, monkeypatch):
+    """The key space cut into 1 .. 6000 workgroup ranges (pieces start and end at
+    arbitrary keys, ranges span several sequences and heads): same parity."""
+    b = stimulus.decode_batch(5, 3000, min_len=1, max_len=3000, seed=9)
+    monkeypatch.setenv("GQA_STREAM_WGS", wgs)
     got = _run(b, dev)
-    assert_within_ulp(_oracle(b), got, 64, f"split {split}")
+    assert_within_ulp(_oracle(b), got, 64, f"{wgs} workgroups")
 
 
 def test_position_major_cache_layout(dev):
@@ -176,7 +179,8 @@ def test_north_star_batch64_ragged(dev):
     b = stimulus.decode_batch(64, 8192, min_len=512, max_len=8192, seed=20260805,
                               gen_device="cuda", device=dev)
     got = _codes(gqa.gqa_attention(b.q, b.k, b.v, b.query_pos, b.seq_len))
-    w = assert_within_ulp(_oracle(b), got, 64, "B=64 ragged")
+    want, want64 = _oracle(b, want_f64=True)
+    w = assert_within_ulp(want, got, 64, "B=64 ragged", ref64=want64)
     print("worst ULP", w)
 
 
