@@ -32,7 +32,7 @@ WORKLOADS = {
     "decode_b1_4096": (1, 4096, None, None),
     "decode_b8_131072": (8, 131072, None, None),
 }
-TRAFFIC_FILE = ROOT / "profiles" / "decode_split_b64_ragged_traffic.txt"
+TRAFFIC_FILE = ROOT / "profiles" / "decode_stream_b64_ragged_traffic.txt"
 
 
 def read_traffic(workload: str):
@@ -156,7 +156,7 @@ def main() -> int:
         roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                     "traffic": read_traffic(args.workload),
-                    "kernel": "decode_split_kernel", "kernel_us": round(split_ms * 1e3, 2),
+                    "kernel": "decode_stream_kernel", "kernel_us": round(split_ms * 1e3, 2),
                     "combine_us": round(combine_ms * 1e3, 2), "bytes_per_launch": split_bytes}
     result = {
         "metric": METRIC,
@@ -175,7 +175,7 @@ def main() -> int:
                 f"synthetic N(0,1) BF16, seed {args.seed}",
         "config": {"workload": args.workload, "batch": bsz, "capacity": cap,
                    "min_len": lo, "max_len": hi, "total_keys": sum(lens), "q_heads": 32,
-                   "kv_heads": 8, "head_dim": 128, "rope": "q", "accumulate": "fp32",
+                   "kv_heads": 8, "head_dim": 128, "rope": "q", "accumulate": "fp32 scores, fp64 weighted V",
                    "bytes_per_step": step_bytes},
         "roofline": roofline,
         "cpu_baseline": None if args.no_cpu_baseline else cpu_baseline(
