@@ -9,8 +9,8 @@ memfmt (.mem codec), stimulus (synthetic inputs), build (hipcc in-tree build).
 """
 from .attention import (DEFAULT_SCALE, GROUP_SIZE, HEAD_DIM, N_KV_HEADS, N_Q_HEADS,  # noqa: F401
                         ROPE_THETA, PreparedDecode, decode_workspace_bytes, gqa_attention,
-                        gqa_decode, make_params, profile_enable, profile_read, rope_half_split,
-                        validate_lengths)
+                        gqa_decode, make_params, new_workspace, profile_enable, profile_read,
+                        rope_half_split, validate_lengths)
 from ._lib import GqaConfigError, GqaError  # noqa: F401
 
 __version__ = "0.1.0"

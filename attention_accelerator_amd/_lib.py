@@ -30,6 +30,7 @@ EXPORTS = (
     "gqa_validate_registers",
     "gqa_validate_lengths",
     "gqa_decode_workspace_bytes",
+    "gqa_decode_workspace_init",
     "gqa_decode_bf16",
     "gqa_rope_rows_bf16",
     "gqa_profile_enable",
@@ -98,6 +99,9 @@ def lib() -> ctypes.CDLL:
     L.gqa_decode_workspace_bytes.argtypes = [ctypes.POINTER(GqaParams), ctypes.c_int32,
                                              ctypes.c_int32]
     L.gqa_decode_workspace_bytes.restype = ctypes.c_size_t
+    L.gqa_decode_workspace_init.argtypes = [ctypes.POINTER(GqaParams), ctypes.c_int32,
+                                            ctypes.c_int32, vp, ctypes.c_size_t, vp]
+    L.gqa_decode_workspace_init.restype = ctypes.c_int
     L.gqa_decode_bf16.argtypes = [ctypes.POINTER(GqaParams), vp, vp, vp,
                                   ctypes.POINTER(GqaKvLayout), vp, vp, ctypes.c_int32, vp, vp,
                                   ctypes.c_size_t, vp]

@@ -62,6 +62,22 @@ def decode_workspace_bytes(batch: int, capacity: int, params: Optional[GqaParams
     return int(lib().gqa_decode_workspace_bytes(ctypes.byref(p), int(batch), int(capacity)))
 
 
+def new_workspace(batch: int, capacity: int, device, params: Optional[GqaParams] = None
+                  ) -> torch.Tensor:
+    """A decode workspace for `batch` sequences of up to `capacity` positions, prepared
+    with gqa_decode_workspace_init.  Reuse it across calls with the same batch size on
+    one stream; calls sharing it must not overlap."""
+    p = params or make_params()
+    nbytes = int(lib().gqa_decode_workspace_bytes(ctypes.byref(p), int(batch), int(capacity)))
+    if nbytes == 0:
+        check(_lib.GQA_ERR_INVALID_CONFIG, "gqa_decode_workspace_bytes")
+    ws = torch.empty(nbytes, dtype=torch.uint8, device=device)
+    check(lib().gqa_decode_workspace_init(ctypes.byref(p), int(batch), int(capacity), ws.data_ptr(),
+                                          nbytes, _stream_handle(torch.device(device))),
+          "gqa_decode_workspace_init")
+    return ws
+
+
 def gqa_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
                   query_position: Lengths, seq_len: Lengths, *, rope_q: bool = True,
                   rope_k: bool = False, theta: float = ROPE_THETA, scale: Optional[float] = None,
@@ -79,6 +95,8 @@ def gqa_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
              device tensors are read by the kernel as they are.
     rope_q / rope_k: rotate Q at query_position / each K row at its position
              (the reference core does both; a cache stored post-RoPE sets rope_k=False)
+    workspace: from new_workspace(B, S, device) to reuse across calls (else one is
+             allocated and prepared per call)
     Returns out [.., 32, 128] bfloat16.  Key p contributes iff p < seq_len and
     p <= query_position.  Raises GqaConfigError for what the reference rejects."""
     single = q.dim() == 2
@@ -112,8 +130,11 @@ def gqa_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
     ws_bytes = int(lib().gqa_decode_workspace_bytes(ctypes.byref(p), batch, capacity))
     if ws_bytes == 0:
         check(_lib.GQA_ERR_INVALID_CONFIG, "gqa_decode_workspace_bytes")
-    if workspace is None or workspace.numel() * workspace.element_size() < ws_bytes:
-        workspace = torch.empty(ws_bytes, dtype=torch.uint8, device=device)
+    if workspace is None:
+        workspace = new_workspace(batch, capacity, device, p)
+    elif workspace.numel() * workspace.element_size() < ws_bytes:
+        raise ValueError(f"workspace holds {workspace.numel() * workspace.element_size()} bytes; "
+                         f"{ws_bytes} needed")
     if out is None:
         out = torch.empty((batch, q.shape[1], q.shape[2]), dtype=torch.bfloat16, device=device)
     elif out.shape != (batch, q.shape[1], q.shape[2]) or out.dtype != torch.bfloat16 \
@@ -184,11 +205,8 @@ class PreparedDecode:
         self.params = make_params(rope_q=rope_q, rope_k=rope_k, theta=theta, scale=scale)
         self.layout = GqaKvLayout(k_cache.stride(0), k_cache.stride(1), k_cache.stride(2),
                                   self.capacity)
-        ws_bytes = int(lib().gqa_decode_workspace_bytes(ctypes.byref(self.params), self.batch,
-                                                        self.capacity))
-        if ws_bytes == 0:
-            check(_lib.GQA_ERR_INVALID_CONFIG, "gqa_decode_workspace_bytes")
-        self.workspace = torch.empty(ws_bytes, dtype=torch.uint8, device=q.device)
+        self.workspace = new_workspace(self.batch, self.capacity, q.device, self.params)
+        ws_bytes = self.workspace.numel()
         self.out = out if out is not None else torch.empty(
             (self.batch, N_Q_HEADS, HEAD_DIM), dtype=torch.bfloat16, device=q.device)
         self._keep = (q.contiguous(), k_cache, v_cache, query_position.contiguous(),

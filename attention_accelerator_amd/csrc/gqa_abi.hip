@@ -73,9 +73,10 @@ DecodePlan plan_decode(int32_t batch, int32_t capacity) {
     DecodePlan plan{};
     plan.n_wgs = stream_wgs();
     plan.n_slots = static_cast<int64_t>(plan.n_wgs) + static_cast<int64_t>(kHkv) * batch;
-    plan.workspace_bytes =
-        align_up(static_cast<size_t>(plan.n_slots) * kGroup * kD * sizeof(double), 256) +
-        align_up(static_cast<size_t>(plan.n_slots) * kGroup * sizeof(float2), 256);
+    plan.counter_bytes = align_up(static_cast<size_t>(kHkv) * batch * sizeof(int32_t), 256);
+    plan.part_o_bytes = align_up(static_cast<size_t>(plan.n_slots) * kGroup * kD * sizeof(double), 256);
+    plan.workspace_bytes = plan.counter_bytes + plan.part_o_bytes +
+                           align_up(static_cast<size_t>(plan.n_slots) * kGroup * sizeof(float2), 256);
     return plan;
 }
 
@@ -152,10 +153,10 @@ int gqa_decode_bf16(const gqa_params_t* params, const uint16_t* q, const uint16_
     a.seq_len = seq_len;
     a.query_pos = query_pos;
     a.out = out;
-    a.part_o = static_cast<double*>(workspace);
-    a.part_ml = reinterpret_cast<float2*>(
-        static_cast<char*>(workspace) +
-        align_up(static_cast<size_t>(plan.n_slots) * kGroup * kD * sizeof(double), 256));
+    char* ws = static_cast<char*>(workspace);
+    a.counters = reinterpret_cast<int32_t*>(ws);
+    a.part_o = reinterpret_cast<double*>(ws + plan.counter_bytes);
+    a.part_ml = reinterpret_cast<float2*>(ws + plan.counter_bytes + plan.part_o_bytes);
     a.kv_batch_stride = kv->batch_stride;
     a.kv_head_stride = kv->head_stride;
     a.kv_pos_stride = kv->pos_stride;
@@ -208,6 +209,19 @@ int gqa_profile_read(gqa_profile_t* out) {
     out->calls = p.used;
     p.used = 0;
     return GQA_OK;
+}
+
+int gqa_decode_workspace_init(const gqa_params_t* params, int32_t batch, int32_t capacity,
+                              void* workspace, size_t workspace_bytes, void* stream) {
+    if (!params) return GQA_ERR_BAD_POINTER;
+    if (!geometry_ok(params) || batch <= 0 || capacity <= 0) return GQA_ERR_INVALID_CONFIG;
+    const DecodePlan plan = plan_decode(batch, capacity);
+    if (!workspace || workspace_bytes < plan.workspace_bytes || !aligned(workspace, 256))
+        return GQA_ERR_WORKSPACE;
+    const hipError_t e = launch_zero_words(static_cast<uint32_t*>(workspace),
+                                           static_cast<int64_t>(plan.counter_bytes / 4),
+                                           static_cast<hipStream_t>(stream));
+    return e == hipSuccess ? GQA_OK : GQA_ERR_HIP;
 }
 
 int gqa_rope_rows_bf16(const uint16_t* in, uint16_t* out, int64_t n_rows, int64_t row_stride,

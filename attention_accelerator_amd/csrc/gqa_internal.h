@@ -16,6 +16,7 @@ struct DecodeArgs {
     const int32_t* seq_len;   // [B]
     const int32_t* query_pos; // [B]
     uint16_t* out;            // [B][32][128]
+    int32_t* counters;        // [8B] finished pieces per segment; zero between calls
     double* part_o;           // [n_slots][4][128] unnormalised partial outputs
     float2* part_ml;          // [n_slots][4] (integer-valued running max in log2 units, sum)
     int64_t kv_batch_stride;
@@ -33,7 +34,9 @@ struct DecodeArgs {
 struct DecodePlan {
     int32_t n_wgs;
     int64_t n_slots;          // n_wgs + 8 * batch (one per piece, see gqa_decode.hip)
-    size_t workspace_bytes;
+    size_t counter_bytes;     // [8B] int32 segment counters at offset 0, 256-aligned
+    size_t part_o_bytes;      // then the fp64 partial outputs
+    size_t workspace_bytes;   // then the (m, l) pairs
 };
 
 DecodePlan plan_decode(int32_t batch, int32_t capacity);
@@ -41,6 +44,7 @@ DecodePlan plan_decode(int32_t batch, int32_t capacity);
 // kernels and after the combine kernel.
 hipError_t launch_decode(const DecodeArgs& a, int batch, hipStream_t stream,
                          hipEvent_t* ev = nullptr);
+hipError_t launch_zero_words(uint32_t* p, int64_t n, hipStream_t stream);
 
 struct RopeArgs {
     const uint16_t* in;

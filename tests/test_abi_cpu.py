@@ -130,3 +130,15 @@ def test_profile_read_empty():
     p = _lib.GqaProfile()
     assert _lib.lib().gqa_profile_read(ctypes.byref(p)) == OK
     assert p.calls == 0
+
+
+def test_workspace_init_rejects():
+    L = _lib.lib()
+    p = _params()
+    n = L.gqa_decode_workspace_bytes(ctypes.byref(p), 4, 1000)
+    assert L.gqa_decode_workspace_init(ctypes.byref(_params(n_q_heads=31)), 4, 1000, 256, n, None) == BAD_CFG
+    assert L.gqa_decode_workspace_init(ctypes.byref(p), 0, 1000, 256, n, None) == BAD_CFG
+    assert L.gqa_decode_workspace_init(ctypes.byref(p), 4, 1000, None, n, None) == BAD_WS
+    assert L.gqa_decode_workspace_init(ctypes.byref(p), 4, 1000, 256, n - 1, None) == BAD_WS
+    assert L.gqa_decode_workspace_init(ctypes.byref(p), 4, 1000, 260, n, None) == BAD_WS
+    assert L.gqa_decode_workspace_init(None, 4, 1000, 256, n, None) == BAD_PTR

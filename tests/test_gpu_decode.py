@@ -116,6 +116,27 @@ def test_stream_partition_invariance(dev, wgs, monkeypatch):
     assert_within_ulp(_oracle(b), got, 64, f"{wgs} workgroups")
 
 
+def test_workspace_reuse_across_calls(dev):
+    """A prepared call reuses one workspace: the per-segment counters must come back
+    to zero after every call, and repeated calls give identical bits."""
+    from attention_accelerator_amd.attention import PreparedDecode
+    b = stimulus.decode_batch(6, 2500, min_len=1, max_len=2500, seed=17)
+    ref = _run(b, dev)
+    call = PreparedDecode(b.q.to(dev), b.k.to(dev), b.v.to(dev), b.query_pos.to(dev),
+                          b.seq_len.to(dev))
+    for _ in range(3):
+        out = call()
+        torch.cuda.synchronize()
+        assert np.array_equal(_codes(out), ref)
+    counters = call.workspace[:6 * 8 * 4].view(torch.int32)
+    assert int(counters.abs().sum()) == 0
+    # same workspace, other contents
+    b2 = stimulus.decode_batch(6, 2500, min_len=1, max_len=2500, seed=18)
+    out2 = gqa.gqa_attention(b2.q.to(dev), b2.k.to(dev), b2.v.to(dev), b2.query_pos, b2.seq_len,
+                             workspace=call.workspace)
+    assert_within_ulp(_oracle(b2), _codes(out2), 64, "reused workspace")
+
+
 def test_position_major_cache_layout(dev):
     """Cache stored [B][S][8][128] (position-major) gives the same bits as [B][8][S][128]."""
     b = stimulus.decode_batch(3, 500, min_len=200, max_len=500, seed=10)
