@@ -73,10 +73,12 @@ DecodePlan plan_decode(int32_t batch, int32_t capacity) {
     DecodePlan plan{};
     plan.n_wgs = stream_wgs();
     plan.n_slots = static_cast<int64_t>(plan.n_wgs) + static_cast<int64_t>(kHkv) * batch;
-    plan.counter_bytes = align_up(static_cast<size_t>(kHkv) * batch * sizeof(int32_t), 256);
     plan.part_o_bytes = align_up(static_cast<size_t>(plan.n_slots) * kGroup * kD * sizeof(double), 256);
-    plan.workspace_bytes = plan.counter_bytes + plan.part_o_bytes +
-                           align_up(static_cast<size_t>(plan.n_slots) * kGroup * sizeof(float2), 256);
+    plan.part_ml_bytes = align_up(static_cast<size_t>(plan.n_slots) * kGroup * sizeof(float2), 256);
+    plan.q_op_bytes = static_cast<size_t>(batch) * kHkv * 4 * kWave * sizeof(uint4);
+    plan.plan_bytes = 256 + align_up(static_cast<size_t>(batch) * sizeof(int64_t), 256) +
+                      align_up(static_cast<size_t>(plan.n_wgs) * sizeof(int4), 256);
+    plan.workspace_bytes = plan.part_o_bytes + plan.part_ml_bytes + plan.q_op_bytes + plan.plan_bytes;
     return plan;
 }
 
@@ -141,6 +143,10 @@ int gqa_decode_bf16(const gqa_params_t* params, const uint16_t* q, const uint16_
         !aligned(seq_len, 4) || !aligned(query_pos, 4))
         return GQA_ERR_BAD_POINTER;
     if (kv->pos_stride % 8 || kv->head_stride % 8 || kv->batch_stride % 8) return GQA_ERR_BAD_POINTER;
+    // Rows of one (sequence, KV head) are addressed with 32-bit byte offsets.
+    if (static_cast<uint64_t>(kv->capacity) * static_cast<uint64_t>(kv->pos_stride) * 2u >
+        0xFFFFFF00ull)
+        return GQA_ERR_INVALID_CONFIG;
 
     const DecodePlan plan = plan_decode(batch, kv->capacity);
     if (!workspace || workspace_bytes < plan.workspace_bytes || !aligned(workspace, 256))
@@ -154,9 +160,13 @@ int gqa_decode_bf16(const gqa_params_t* params, const uint16_t* q, const uint16_
     a.query_pos = query_pos;
     a.out = out;
     char* ws = static_cast<char*>(workspace);
-    a.counters = reinterpret_cast<int32_t*>(ws);
-    a.part_o = reinterpret_cast<double*>(ws + plan.counter_bytes);
-    a.part_ml = reinterpret_cast<float2*>(ws + plan.counter_bytes + plan.part_o_bytes);
+    a.part_o = reinterpret_cast<double*>(ws);
+    a.part_ml = reinterpret_cast<float2*>(ws + plan.part_o_bytes);
+    a.q_op = reinterpret_cast<uint4*>(ws + plan.part_o_bytes + plan.part_ml_bytes);
+    char* pl = ws + plan.part_o_bytes + plan.part_ml_bytes + plan.q_op_bytes;
+    a.plan_hdr = reinterpret_cast<int64_t*>(pl);
+    a.seq_off = reinterpret_cast<int64_t*>(pl + 256);
+    a.wg_start = reinterpret_cast<int4*>(pl + 256 + align_up(static_cast<size_t>(batch) * sizeof(int64_t), 256));
     a.kv_batch_stride = kv->batch_stride;
     a.kv_head_stride = kv->head_stride;
     a.kv_pos_stride = kv->pos_stride;
@@ -219,7 +229,7 @@ int gqa_decode_workspace_init(const gqa_params_t* params, int32_t batch, int32_t
     if (!workspace || workspace_bytes < plan.workspace_bytes || !aligned(workspace, 256))
         return GQA_ERR_WORKSPACE;
     const hipError_t e = launch_zero_words(static_cast<uint32_t*>(workspace),
-                                           static_cast<int64_t>(plan.counter_bytes / 4),
+                                           static_cast<int64_t>(plan.workspace_bytes / 4),
                                            static_cast<hipStream_t>(stream));
     return e == hipSuccess ? GQA_OK : GQA_ERR_HIP;
 }

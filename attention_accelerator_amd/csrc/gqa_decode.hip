@@ -1,10 +1,10 @@
-// gqa_decode.hip -- GQA decode for gfx950: one persistent launch, stream-K split over
-// all keys of the batch, QK^T on MFMA, weighted V on fp64 VALU, exact merge of pieces.
+// gqa_decode.hip -- GQA decode for gfx950: a persistent stream-K split over all keys
+// of the batch, QK^T on MFMA, weighted V on fp64 VALU, exact merge of pieces.
 //
 // One decode step of the reference core (gqa_controller.v:140-277 loop nest, datapath
 // rope_unit -> bf16_dot_product_mac -> scale_unit -> flash_softmax ->
 // output_accumulator -> gqa_output_collector) is decode_stream_kernel, a persistent
-// grid of n_wgs one-wave workgroups:
+// grid of n_wgs one-wave workgroups, followed by decode_merge_kernel:
 //
 //  * The keys of every (sequence, kv_head) segment are laid end to end (segment =
 //    b*8 + h, n_valid(b) keys each) and cut into n_wgs equal ranges, one per
@@ -17,8 +17,10 @@
 //    (output_accumulator.v:540-686, BF16 in Q-head order, gqa_output_collector.v:32-61).
 //    Otherwise it leaves an unnormalised partial (O[4][128] fp64, running max m,
 //    sum l) at slot wg + segment -- unique because both increase along the key
-//    order -- and bumps the segment's counter; the piece that finishes last merges
-//    all partials of the segment and resets the counter for the next call.
+//    order -- and decode_merge_kernel, launched next on the same stream, merges the
+//    pieces of each such segment.  The kernel boundary orders the partials; an
+//    in-kernel "last piece merges" scheme would need a device-scope release per
+//    piece, which on gfx950 writes back the XCD's L2 and measured 1.65x slower.
 //
 // Arithmetic (the golden model is double, pyfiles/gen_gqa_wrapper_vectors.py:121-139):
 //  * Q is rotated in double, scaled by scale*log2(e) in double and split into three
@@ -42,8 +44,9 @@
 //    g = l/16 and element j of MFMA kb cover head dim d = 32*kb + 8*g + j, so a
 //    lane loads 16 contiguous bytes per kb and holds both halves (d, d+64) of its
 //    RoPE pairs (kb and kb+2).  Output lane l holds score(key 4g+i, column n).
-//  * PV: lane (r = l/16, c = l%16) owns dims [8c, 8c+8) of key 4*it + r of the
-//    chunk; one 16-byte load per lane covers four whole V rows (1 KB contiguous).
+//  * PV: lane (g, n) owns dims [8n, 8n+8) of keys 4g+i of the chunk -- the keys whose
+//    scores row g holds -- so each 16-lane row runs its own online softmax and the
+//    rows merge once per piece.  V load i covers whole rows i, 4+i, 8+i, 12+i.
 #include "gqa_device.h"
 #include "gqa_internal.h"
 
@@ -91,27 +94,6 @@ __device__ __forceinline__ void stream_totals(const DecodeArgs& a, int lane, int
     per_wg = (per + kChunk - 1) / kChunk * kChunk;
 }
 
-// Sequence whose segments contain global key offset x (0 <= x < total):
-// returns b and off_b = 8 * (valid keys of sequences before b).
-__device__ __forceinline__ int locate_sequence(const DecodeArgs& a, int lane, int64_t x,
-                                               int64_t& off_b) {
-    int64_t carry = 0;
-    for (int base = 0; base < a.batch; base += kWave) {
-        const int b = base + lane;
-        const int64_t nv = b < a.batch ? seq_valid_keys(a, b) : 0;
-        const int64_t incl = wave_incl_scan_i64(nv, lane) + carry;
-        const uint64_t past = __ballot((incl * kHkv) > x);
-        if (past) {
-            const int first = __ffsll(static_cast<unsigned long long>(past)) - 1;
-            off_b = (__shfl(incl, first) - __shfl(nv, first)) * kHkv;
-            return base + first;
-        }
-        carry = __shfl(incl, kWave - 1);
-    }
-    off_b = carry * kHkv;
-    return a.batch;   // unreachable for x < total
-}
-
 // BF16 code of a double, rounding through f32 (any nearby BF16 value serves as the
 // leading part of a split; the residual is formed exactly in double).
 __device__ __forceinline__ uint16_t bf16_of(double d) { return f32_to_bf16_rne(static_cast<float>(d)); }
@@ -153,35 +135,52 @@ struct Chunk {
     uint4 vw[4];
 };
 
-// Running state of one piece: fp64 weighted-V accumulator (4 heads x this lane's 8 dims),
-// integer-valued running max and partial sum (head n in lanes n < 4).
+// Running state of one piece in lane (g, n): fp64 weighted-V accumulator of row g
+// (4 heads x dims [8n, 8n+8)), and row g's integer-valued running max and sum of p
+// for head n%4.
 struct PieceState {
     double acc[kGroup][8];
     float m_run;
     float l_run;
 };
 
-__device__ __forceinline__ void load_chunk(const uint16_t* kbase, const uint16_t* vbase,
-                                           int64_t ps, int kc, int k_b, int n, int g, Chunk& c) {
-    const int kkey = kc + n;
+// Byte offsets (from the segment's first K / V row) of this lane's rows in the current
+// chunk.  Loads are unconditional so that the compiler counts them exactly (a load
+// under a branch makes it wait for every outstanding load at the join, prefetches
+// included); rows past the piece are clamped to its last row and masked afterwards.
+struct ChunkRows {
+    uint32_t k;       // key kc + n, + 16*g bytes into the row
+    uint32_t v[4];    // keys kc + 4*g + i, + 16*n bytes into the row
+};
+
+__device__ __forceinline__ void load_chunk(const char* kseg, const char* vseg, const ChunkRows& r,
+                                           uint32_t k_last, uint32_t v_last, Chunk& c) {
+    const char* kp = kseg + min(r.k, k_last);
 #pragma unroll
-    for (int kb = 0; kb < 4; ++kb) {
-        c.kw[kb] = make_uint4(0, 0, 0, 0);
-        if (kkey < k_b) c.kw[kb] = *reinterpret_cast<const uint4*>(kbase + kkey * ps + 32 * kb);
-    }
+    for (int kb = 0; kb < 4; ++kb) c.kw[kb] = *reinterpret_cast<const uint4*>(kp + 64 * kb);
 #pragma unroll
-    for (int it = 0; it < 4; ++it) {
-        const int vkey = kc + 4 * it + g;
-        c.vw[it] = make_uint4(0, 0, 0, 0);
-        if (vkey < k_b) c.vw[it] = *reinterpret_cast<const uint4*>(vbase + vkey * ps);
-    }
+    for (int it = 0; it < 4; ++it)
+        c.vw[it] = *reinterpret_cast<const uint4*>(vseg + min(r.v[it], v_last));
+}
+
+__device__ __forceinline__ void advance(ChunkRows& r, uint32_t step) {
+    r.k += step;
+#pragma unroll
+    for (int it = 0; it < 4; ++it) r.v[it] += step;
 }
 
 // Scores, online softmax and weighted V of one chunk [kc, kc+16) (keys >= k_b masked).
+//
+// Lane (g = l/16, n = l%16): MFMA output rows are keys kc+4g+i (i = 0..3) and
+// columns n, so after summing the split columns every lane holds the scores of
+// keys kc+4g+i for head n%4.  The same row g then weights V rows kc+4g+i (dims
+// [8n, 8n+8)), so each 16-lane row is an independent flash-decoding stream with
+// its own running max and sum per head: no cross-row step until the piece ends,
+// and p moves to the weighted-V lanes by quad_perm DPP, not through LDS.
 template <bool kRopeK>
 __device__ __forceinline__ void compute_chunk(const DecodeArgs& a, int kc, int k_b, int n, int g,
                                               const Chunk& c, const bf16x8_t (&bq)[4],
-                                              PieceState& st, float (*p_tile)[kGroup]) {
+                                              PieceState& st) {
     f32x4_t d = {0.f, 0.f, 0.f, 0.f};
     if (kRopeK) {
         // Rotate the K row at its position: pairs (kb, kb+2) of this lane.
@@ -215,8 +214,8 @@ __device__ __forceinline__ void compute_chunk(const DecodeArgs& a, int kc, int k
         for (int kb = 0; kb < 4; ++kb)
             d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(c.kw[kb]), bq[kb], d, 0, 0, 0);
     }
-    // Sum the hi/mid/lo columns n, n+4, n+8 into every lane of the same n%4 (columns
-    // 12..15 are zero, so the rotations by 4, 8 and 12 within the 16-lane row add exactly those).
+    // Sum the hi/mid/lo columns (n, n+4, n+8; 12..15 are zero): the rotations by 4, 8
+    // and 12 within the 16-lane row leave every lane with the total of its n%4 class.
     float s[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -225,11 +224,10 @@ __device__ __forceinline__ void compute_chunk(const DecodeArgs& a, int kc, int k
         if (kc + 4 * g + i >= k_b) s[i] = -INFINITY;
     }
 
-    // Online softmax (head n in lanes n < 4; m integer-valued so rescales are exact).
-    float cm = fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3]));
-    cm = fmaxf(cm, __shfl_xor(cm, 16));
-    cm = fmaxf(cm, __shfl_xor(cm, 32));
-    const bool grow = (n < kGroup) && (cm > st.m_run);
+    // Online softmax of this row's 4 keys for head n%4 (m integer-valued, so every
+    // rescale is an exact power of two).
+    const float cm = fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3]));
+    const bool grow = cm > st.m_run;
     if (__ballot(grow)) {
         const float m_new = grow ? ceilf(cm) : st.m_run;
         // 2^(m_run - m_new), exact; 0 when nothing has been accumulated yet.
@@ -237,15 +235,14 @@ __device__ __forceinline__ void compute_chunk(const DecodeArgs& a, int kc, int k
         st.l_run = ldexpf(st.l_run, max(shift, -200));
         st.m_run = m_new;
         int sh[kGroup];
+        sh[0] = dpp_i<0x00>(shift);
+        sh[1] = dpp_i<0x55>(shift);
+        sh[2] = dpp_i<0xAA>(shift);
+        sh[3] = dpp_i<0xFF>(shift);
 #pragma unroll
-        for (int h = 0; h < kGroup; ++h) sh[h] = __shfl(shift, h);
+        for (int h = 0; h < kGroup; ++h)
 #pragma unroll
-        for (int h = 0; h < kGroup; ++h) {
-            if (sh[h] != 0) {
-#pragma unroll
-                for (int j = 0; j < 8; ++j) st.acc[h][j] = ldexp(st.acc[h][j], sh[h]);
-            }
-        }
+            for (int j = 0; j < 8; ++j) st.acc[h][j] = ldexp(st.acc[h][j], sh[h]);
     }
     float p[4];
 #pragma unroll
@@ -253,22 +250,24 @@ __device__ __forceinline__ void compute_chunk(const DecodeArgs& a, int kc, int k
         p[i] = (s[i] == -INFINITY) ? 0.f : exp2f(s[i] - st.m_run);
         st.l_run += p[i];
     }
-    if (n < kGroup) {
-#pragma unroll
-        for (int i = 0; i < 4; ++i) p_tile[4 * g + i][n] = p[i];
-    }
-    __syncthreads();
 
-    // Weighted V in fp64.
+    // Weighted V in fp64.  In a partial chunk the clamped rows carry p = 0; their V is
+    // zeroed too so that no value of another row can reach the sum.
+    const bool partial = kc + kChunk > k_b;
 #pragma unroll
-    for (int it = 0; it < 4; ++it) {
-        const float4 p4 = *reinterpret_cast<const float4*>(&p_tile[4 * it + g][0]);
+    for (int i = 0; i < 4; ++i) {
+        // p of key kc+4g+i for heads 0..3, from lanes 4*(n/4) + h of this quad.
+        const double pd[kGroup] = {static_cast<double>(dpp_f<0x00>(p[i])),
+                                   static_cast<double>(dpp_f<0x55>(p[i])),
+                                   static_cast<double>(dpp_f<0xAA>(p[i])),
+                                   static_cast<double>(dpp_f<0xFF>(p[i]))};
+        uint4 vw = c.vw[i];
+        if (partial && kc + 4 * g + i >= k_b) vw = make_uint4(0, 0, 0, 0);
         float vf[8];
-        unpack8(c.vw[it], vf);
+        unpack8(vw, vf);
         double vd[8];
 #pragma unroll
         for (int j = 0; j < 8; ++j) vd[j] = static_cast<double>(vf[j]);
-        const double pd[kGroup] = {p4.x, p4.y, p4.z, p4.w};
 #pragma unroll
         for (int h = 0; h < kGroup; ++h)
 #pragma unroll
@@ -276,88 +275,149 @@ __device__ __forceinline__ void compute_chunk(const DecodeArgs& a, int kc, int k
     }
 }
 
-// Merge the pieces of segment (b, kvh) -- slots w + seg for w in [w_first, w_last] --
-// with exact power-of-two weights in fp64; write the 4 output rows.  Lane: 2 dims.
-__device__ __forceinline__ void combine_segment(const DecodeArgs& a, int b, int kvh, int64_t seg,
-                                                int64_t w_first, int64_t w_last) {
-    const int lane = threadIdx.x;
-#pragma unroll 1
-    for (int h = 0; h < kGroup; ++h) {
-        float mx = -INFINITY;
-        for (int64_t w = w_first; w <= w_last; ++w)
-            mx = fmaxf(mx, a.part_ml[(w + seg) * kGroup + h].x);
-        double l = 0.0, o0 = 0.0, o1 = 0.0;
-        for (int64_t w = w_first; w <= w_last; ++w) {
-            const int64_t slot = w + seg;
-            const float2 ml = a.part_ml[slot * kGroup + h];
-            const int e = max(static_cast<int>(ml.x - mx), -1100);
-            const double2 o = reinterpret_cast<const double2*>(a.part_o + (slot * kGroup + h) * kD)[lane];
-            l += ldexp(static_cast<double>(ml.y), e);
-            o0 += ldexp(o.x, e);
-            o1 += ldexp(o.y, e);
+// Q operands of every (sequence, KV head), written once per call by
+// decode_prepare_kernel and read by each piece: the 4 Q rows of the group rotated at
+// query_position and scaled by scale*log2(e) in double, split into hi/mid/lo BF16,
+// in the MFMA B-operand layout (lane l, MFMA kb: column n = l%16 -> split n/4 of
+// head n%4, dims 32kb + 8(l/16) + j).  One wave per (kv_head, sequence).  It also
+// writes the NaN rows of sequences whose lengths break the rules, and (an extra row of
+// the grid) the stream-K plan.
+// Start of stream workgroup w, whose range begins inside sequence b (segments from
+// global key offset off, nv keys each): KV head by comparison, no division.
+__device__ __forceinline__ void write_wg_start(const DecodeArgs& a, int64_t w, int64_t per_wg,
+                                               int64_t off, int nv, int b) {
+    const int64_t rel = w * per_wg - off;       // in [0, 8 * nv)
+    int kvh = 0;
+#pragma unroll
+    for (int k = 1; k < kHkv; ++k) kvh += rel >= static_cast<int64_t>(k) * nv;
+    a.wg_start[w] = make_int4(b, kvh, static_cast<int>(rel - static_cast<int64_t>(kvh) * nv), nv);
+}
+
+// The stream-K plan (row B of the prepare grid, one wave): per-sequence key offsets,
+// the total and the range size, and where every stream workgroup starts.  For each
+// sequence in turn the lanes share the workgroups whose ranges begin inside its
+// segments.
+__device__ __forceinline__ void build_plan(const DecodeArgs& a, int lane) {
+    int64_t total, per_wg;
+    stream_totals(a, lane, total, per_wg);
+    if (lane == 0) {
+        a.plan_hdr[0] = total;
+        a.plan_hdr[1] = per_wg;
+    }
+    int64_t carry = 0;
+    for (int base = 0; base < a.batch; base += kWave) {
+        const int b = base + lane;
+        const int nv = b < a.batch ? seq_valid_keys(a, b) : 0;
+        const int64_t incl = wave_incl_scan_i64(nv, lane) + carry;
+        const int64_t off = (incl - nv) * kHkv;
+        if (b < a.batch) a.seq_off[b] = off;
+        // Workgroups whose ranges start inside sequence b's segments: [w0, w1).
+        const int64_t w0 = (off + per_wg - 1) / per_wg;
+        const int64_t w1 = (off + static_cast<int64_t>(kHkv) * nv + per_wg - 1) / per_wg;
+        // Few workgroups per sequence (the common case): each lane writes its own.
+        // Many (a long sequence): the lanes share them, one such sequence at a time.
+        const bool own = b < a.batch && nv > 0 && w1 - w0 <= kWave;
+        if (own) {
+            for (int64_t w = w0; w < w1; ++w) write_wg_start(a, w, per_wg, off, nv, b);
         }
-        uint32_t* out = reinterpret_cast<uint32_t*>(
-            a.out + (static_cast<int64_t>(b) * kHq + kvh * kGroup + h) * kD);
-        const uint32_t lo = f32_to_bf16_rne(static_cast<float>(o0 / l));
-        const uint32_t hi = f32_to_bf16_rne(static_cast<float>(o1 / l));
-        out[lane] = lo | (hi << 16);
+        uint64_t big = __ballot(b < a.batch && nv > 0 && !own);
+        while (big) {
+            const int j = __ffsll(static_cast<unsigned long long>(big)) - 1;
+            big &= big - 1;
+            const int nv_j = __shfl(nv, j);
+            const int64_t off_j = __shfl(off, j);
+            const int64_t w1_j = __shfl(w1, j);
+            for (int64_t w = __shfl(w0, j) + lane; w < w1_j; w += kWave)
+                write_wg_start(a, w, per_wg, off_j, nv_j, base + j);
+        }
+        carry = __shfl(incl, kWave - 1);
     }
 }
 
-// One piece: keys [k_a, k_b) of segment (b, kvh), which starts at global key offset
-// seg_off.  Writes the output rows itself when the piece is the whole segment;
-// otherwise leaves a partial, and the last piece of the segment to finish merges all.
-template <bool kRopeQ, bool kRopeK>
-__device__ __forceinline__ void process_piece(const DecodeArgs& a, int b, int kvh, int nv, int k_a,
-                                              int k_b, int64_t seg_off, int64_t per_wg,
-                                              int64_t wg, double (*q_s)[kD],
-                                              float (*p_s)[kChunk][kGroup]) {
+template <bool kRopeQ>
+__global__ __launch_bounds__(kWave) void decode_prepare_kernel(DecodeArgs a) {
+    __shared__ double q_s[kGroup][kD];
+    const int kvh = blockIdx.x;
+    const int b = blockIdx.y;
     const int lane = threadIdx.x;
-    const int n = lane & 15;       // MFMA column / PV dim chunk
-    const int g = lane >> 4;       // MFMA lane group / PV key row
-    const int qpos = a.query_pos[b];
-
-    const int64_t head_off = static_cast<int64_t>(b) * a.kv_batch_stride +
-                             static_cast<int64_t>(kvh) * a.kv_head_stride;
-    const int64_t ps = a.kv_pos_stride;
-    const uint16_t* kbase = a.k + head_off + 8 * g;        // + key*ps + 32*kb
-    const uint16_t* vbase = a.v + head_off + 8 * n;        // + key*ps
-
-    // First chunk's rows are requested before the Q prologue so that their latency
-    // overlaps it.
-    Chunk c0, c1;
-    load_chunk(kbase, vbase, ps, k_a, k_b, n, g, c0);
-
-    // ---- Q rows of the group: rotate at qpos and scale, in double.
-    __syncthreads();
-    {
-        double sn = 0.0, cs = 1.0;
-        if (kRopeQ) sincos(static_cast<double>(qpos) * a.rope.inv_freq[lane], &sn, &cs);
-#pragma unroll
-        for (int h = 0; h < kGroup; ++h) {
-            const uint16_t* qrow = a.q + (static_cast<int64_t>(b) * kHq + kvh * kGroup + h) * kD;
-            const double x = bf16_to_f32(qrow[lane]);
-            const double y = bf16_to_f32(qrow[lane + kPairs]);
-            double xr = x, yr = y;
-            if (kRopeQ) {
-                xr = x * cs - y * sn;
-                yr = x * sn + y * cs;
-            }
-            q_s[h][lane] = xr * a.qk_scale_log2;
-            q_s[h][lane + kPairs] = yr * a.qk_scale_log2;
+    const int n = lane & 15;
+    const int g = lane >> 4;
+    if (b == a.batch) {
+        if (kvh == 0) build_plan(a, lane);
+        return;
+    }
+    const int nv = seq_valid_keys(a, b);
+    if (nv == 0) {
+        if (kvh == 0) {
+            uint4* out = reinterpret_cast<uint4*>(a.out + static_cast<int64_t>(b) * kHq * kD);
+            for (int i = lane; i < kHq * kD / 8; i += kWave)
+                out[i] = make_uint4(0x7fc07fc0u, 0x7fc07fc0u, 0x7fc07fc0u, 0x7fc07fc0u);
         }
+        return;
+    }
+    const int qpos = a.query_pos[b];
+    double sn = 0.0, cs = 1.0;
+    if (kRopeQ) rope_sincos(qpos, a.rope.inv_freq[lane], sn, cs);
+#pragma unroll
+    for (int h = 0; h < kGroup; ++h) {
+        const uint16_t* qrow = a.q + (static_cast<int64_t>(b) * kHq + kvh * kGroup + h) * kD;
+        const double x = bf16_to_f32(qrow[lane]);
+        const double y = bf16_to_f32(qrow[lane + kPairs]);
+        double xr = x, yr = y;
+        if (kRopeQ) {
+            xr = x * cs - y * sn;
+            yr = x * sn + y * cs;
+        }
+        q_s[h][lane] = xr * a.qk_scale_log2;
+        q_s[h][lane + kPairs] = yr * a.qk_scale_log2;
     }
     __syncthreads();
-    // MFMA B operand: column n -> split n/4 of head n%4 (zero for n >= 12).
-    bf16x8_t bq[4];
+    uint4* dst = a.q_op + ((static_cast<int64_t>(b) * kHkv + kvh) * 4) * kWave;
 #pragma unroll
     for (int kb = 0; kb < 4; ++kb) {
         uint16_t h8[8];
 #pragma unroll
         for (int j = 0; j < 8; ++j)
             h8[j] = n < 12 ? split3(q_s[n & 3][32 * kb + 8 * g + j], n >> 2) : uint16_t(0);
-        bq[kb] = pack8(h8);
+        uint4 w;
+        w.x = h8[0] | (static_cast<uint32_t>(h8[1]) << 16);
+        w.y = h8[2] | (static_cast<uint32_t>(h8[3]) << 16);
+        w.z = h8[4] | (static_cast<uint32_t>(h8[5]) << 16);
+        w.w = h8[6] | (static_cast<uint32_t>(h8[7]) << 16);
+        dst[kb * kWave + lane] = w;
     }
+}
+
+// One piece: keys [k_a, k_b) of segment (b, kvh).  Writes the output rows itself when
+// the piece is the whole segment; otherwise leaves a partial for the merge kernel.
+template <bool kRopeK>
+__device__ __forceinline__ void process_piece(const DecodeArgs& a, int b, int kvh, int nv, int k_a,
+                                              int k_b, int64_t wg) {
+    const int lane = threadIdx.x;
+    const int n = lane & 15;       // MFMA column / PV dim chunk
+    const int g = lane >> 4;       // MFMA lane group / PV key row
+    const int64_t head_off = static_cast<int64_t>(b) * a.kv_batch_stride +
+                             static_cast<int64_t>(kvh) * a.kv_head_stride;
+    const char* kseg = reinterpret_cast<const char*>(a.k + head_off);
+    const char* vseg = reinterpret_cast<const char*>(a.v + head_off);
+    const uint32_t row = static_cast<uint32_t>(a.kv_pos_stride) * 2u;   // bytes per position
+    ChunkRows rows;
+    rows.k = static_cast<uint32_t>(k_a + n) * row + 16u * g;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) rows.v[i] = static_cast<uint32_t>(k_a + 4 * g + i) * row + 16u * n;
+    const uint32_t k_last = static_cast<uint32_t>(k_b - 1) * row + 16u * g;
+    const uint32_t v_last = static_cast<uint32_t>(k_b - 1) * row + 16u * n;
+    const uint32_t step = kChunk * row;
+
+    // First chunk's rows are requested together with the Q operands.
+    Chunk c0, c1;
+    load_chunk(kseg, vseg, rows, k_last, v_last, c0);
+
+    // Q operands prepared by decode_prepare_kernel for this (sequence, KV head).
+    const uint4* qop = a.q_op + ((static_cast<int64_t>(b) * kHkv + kvh) * 4) * kWave + lane;
+    bf16x8_t bq[4];
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb) bq[kb] = as_bf16x8(qop[kb * kWave]);
 
     PieceState st;
 #pragma unroll
@@ -367,41 +427,63 @@ __device__ __forceinline__ void process_piece(const DecodeArgs& a, int b, int kv
     st.m_run = -INFINITY;
     st.l_run = 0.f;
 
-    // Two register sets: chunk j+1 is in flight while chunk j is computed.
-    for (int kc = k_a;; kc += 2 * kChunk) {
-        const bool more1 = kc + kChunk < k_b;
-        if (more1) load_chunk(kbase, vbase, ps, kc + kChunk, k_b, n, g, c1);
-        compute_chunk<kRopeK>(a, kc, k_b, n, g, c0, bq, st, p_s[0]);
-        if (!more1) break;
-        const bool more2 = kc + 2 * kChunk < k_b;
-        if (more2) load_chunk(kbase, vbase, ps, kc + 2 * kChunk, k_b, n, g, c0);
-        compute_chunk<kRopeK>(a, kc + kChunk, k_b, n, g, c1, bq, st, p_s[1]);
-        if (!more2) break;
+    // Two register sets: chunk j+1 is in flight while chunk j is computed.  The
+    // prefetch is issued even past the last chunk (clamped to the piece's last row,
+    // so it reads that one row again) to keep the loop body free of load branches.
+    const int n_chunks = (k_b - k_a + kChunk - 1) / kChunk;
+    for (int i = 0;; i += 2) {
+        advance(rows, step);
+        load_chunk(kseg, vseg, rows, k_last, v_last, c1);
+        compute_chunk<kRopeK>(a, k_a + i * kChunk, k_b, n, g, c0, bq, st);
+        if (i + 1 >= n_chunks) break;
+        advance(rows, step);
+        load_chunk(kseg, vseg, rows, k_last, v_last, c0);
+        compute_chunk<kRopeK>(a, k_a + (i + 1) * kChunk, k_b, n, g, c1, bq, st);
+        if (i + 2 >= n_chunks) break;
     }
 
-    // ---- sum the four key rows; every lane then holds the totals.
+    // ---- merge the four rows: common max per head, exact power-of-two weights.
+    float mh[kGroup];
+    mh[0] = dpp_f<0x00>(st.m_run);
+    mh[1] = dpp_f<0x55>(st.m_run);
+    mh[2] = dpp_f<0xAA>(st.m_run);
+    mh[3] = dpp_f<0xFF>(st.m_run);
+    float lh[kGroup];
+    lh[0] = dpp_f<0x00>(st.l_run);
+    lh[1] = dpp_f<0x55>(st.l_run);
+    lh[2] = dpp_f<0xAA>(st.l_run);
+    lh[3] = dpp_f<0xFF>(st.l_run);
+    float m_tot[kGroup];
+    double l_tot[kGroup];
 #pragma unroll
-    for (int h = 0; h < kGroup; ++h)
+    for (int h = 0; h < kGroup; ++h) {
+        float mx = fmaxf(mh[h], __shfl_xor(mh[h], 16));
+        mx = fmaxf(mx, __shfl_xor(mx, 32));
+        m_tot[h] = mx;
+        // a row that saw no key of this piece has m = -inf and contributes nothing
+        const int e = (mh[h] == -INFINITY) ? -1100 : static_cast<int>(mh[h] - mx);
+        double lr = ldexp(static_cast<double>(lh[h]), e);
+        lr += __shfl_xor(lr, 16);
+        lr += __shfl_xor(lr, 32);
+        l_tot[h] = lr;
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
-            st.acc[h][j] += __shfl_xor(st.acc[h][j], 16);
-            st.acc[h][j] += __shfl_xor(st.acc[h][j], 32);
+            double v = ldexp(st.acc[h][j], e);
+            v += __shfl_xor(v, 16);
+            v += __shfl_xor(v, 32);
+            st.acc[h][j] = v;
         }
-    st.l_run += __shfl_xor(st.l_run, 16);
-    st.l_run += __shfl_xor(st.l_run, 32);
+    }
 
     const int64_t seg = static_cast<int64_t>(b) * kHkv + kvh;
     if (k_a == 0 && k_b == nv) {
         // The whole segment: normalise in fp64, round double -> f32 -> BF16.
-        double lh[kGroup];
-#pragma unroll
-        for (int h = 0; h < kGroup; ++h) lh[h] = static_cast<double>(__shfl(st.l_run, h));
         if (g == 0) {
 #pragma unroll
             for (int h = 0; h < kGroup; ++h) {
                 uint16_t o8[8];
 #pragma unroll
-                for (int j = 0; j < 8; ++j) o8[j] = f32_to_bf16_rne(static_cast<float>(st.acc[h][j] / lh[h]));
+                for (int j = 0; j < 8; ++j) o8[j] = f32_to_bf16_rne(static_cast<float>(st.acc[h][j] / l_tot[h]));
                 uint4 pk;
                 pk.x = o8[0] | (static_cast<uint32_t>(o8[1]) << 16);
                 pk.y = o8[2] | (static_cast<uint32_t>(o8[3]) << 16);
@@ -423,55 +505,38 @@ __device__ __forceinline__ void process_piece(const DecodeArgs& a, int b, int kv
             for (int j = 0; j < 4; ++j) dst[j] = make_double2(st.acc[h][2 * j], st.acc[h][2 * j + 1]);
         }
     }
-    if (lane < kGroup) a.part_ml[slot * kGroup + lane] = make_float2(st.m_run, st.l_run);
-
-    // Count finished pieces; the last one merges.  Release the partial before the
-    // count, acquire the others' after it (device scope: the pieces ran on other CUs
-    // and XCDs).
-    __threadfence();
-    int done = 0;
-    if (lane == 0) done = atomicAdd(&a.counters[seg], 1);
-    done = __shfl(done, 0);
-    const int64_t w_first = seg_off / per_wg;
-    const int64_t w_last = (seg_off + nv - 1) / per_wg;
-    if (done == static_cast<int>(w_last - w_first)) {
-        __threadfence();
-        combine_segment(a, b, kvh, seg, w_first, w_last);
-        if (lane == 0) atomicExch(&a.counters[seg], 0);   // ready for the next call
+    if (lane < kGroup) {
+        const float mm = lane == 0 ? m_tot[0] : lane == 1 ? m_tot[1] : lane == 2 ? m_tot[2] : m_tot[3];
+        const double ll = lane == 0 ? l_tot[0] : lane == 1 ? l_tot[1] : lane == 2 ? l_tot[2] : l_tot[3];
+        a.part_ml[slot * kGroup + lane] = make_float2(mm, static_cast<float>(ll));
     }
+
 }
 
-template <bool kRopeQ, bool kRopeK>
+template <bool kRopeK>
 __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(2))) void decode_stream_kernel(DecodeArgs a) {
-    __shared__ double q_s[kGroup][kD];
-    __shared__ float p_s[2][kChunk][kGroup];
-    const int lane = threadIdx.x;
     const int64_t w = blockIdx.x;
-
-    // Sequences whose lengths break the rules get NaN rows (and no reads):
-    // workgroup w checks sequences w, w + n_wgs, ...
-    for (int64_t bb = w; bb < a.batch; bb += a.n_wgs) {
-        if (seq_valid_keys(a, static_cast<int>(bb)) == 0) {
-            uint4* out = reinterpret_cast<uint4*>(a.out + bb * kHq * kD);
-            for (int i = lane; i < kHq * kD / 8; i += kWave)
-                out[i] = make_uint4(0x7fc07fc0u, 0x7fc07fc0u, 0x7fc07fc0u, 0x7fc07fc0u);
-        }
-    }
-
-    int64_t total, per_wg;
-    stream_totals(a, lane, total, per_wg);
+    const int64_t total = a.plan_hdr[0];
+    const int64_t per_wg = a.plan_hdr[1];
+    const int4 start = a.wg_start[w];
     int64_t x = w * per_wg;
     if (x >= total) return;
     const int64_t x_end = min(x + per_wg, total);
 
-    int64_t off_b;
-    int b = locate_sequence(a, lane, x, off_b);
-    int nvb = seq_valid_keys(a, b);
-    int kvh = static_cast<int>((x - off_b) / nvb);
-    int key = static_cast<int>((x - off_b) % nvb);
+    int b = start.x;
+    int kvh = start.y;
+    int key = start.z;
+    int nvb = start.w;
     while (true) {
-        const int k_b = static_cast<int>(min(static_cast<int64_t>(nvb), key + (x_end - x)));
-        process_piece<kRopeQ, kRopeK>(a, b, kvh, nvb, key, k_b, x - key, per_wg, w, q_s, p_s);
+        // Everything that shapes the piece is wave-uniform; say so, so that the loop
+        // control and the segment bases live in scalar registers.
+        b = __builtin_amdgcn_readfirstlane(b);
+        kvh = __builtin_amdgcn_readfirstlane(kvh);
+        key = __builtin_amdgcn_readfirstlane(key);
+        nvb = __builtin_amdgcn_readfirstlane(nvb);
+        const int k_b = __builtin_amdgcn_readfirstlane(
+            static_cast<int>(min(static_cast<int64_t>(nvb), key + (x_end - x))));
+        process_piece<kRopeK>(a, b, kvh, nvb, key, k_b, w);
         x += k_b - key;
         if (x >= x_end) break;
         key = 0;
@@ -482,6 +547,78 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(2))) void
             if (nvb == 0) break;   // lengths changed under the launch; nothing left to read
         }
     }
+}
+
+// Merge the pieces of multi-piece segments: one 4-wave workgroup per (KV head,
+// sequence), wave h for Q head 4*kvh + h.  Slots w + seg for w in [w_first, w_last]
+// hold the pieces of segment seg; their (m, l) are read one per lane, the weights
+// 2^(m - max) are exact, O is summed in fp64 two dims per lane, and the row is
+// rounded double -> f32 -> BF16.  Segments held by one workgroup were written by the
+// stream kernel and are skipped.
+__global__ __launch_bounds__(kGroup * kWave) void decode_merge_kernel(DecodeArgs a) {
+    const int kvh = blockIdx.x;
+    const int b = blockIdx.y;
+    const int lane = threadIdx.x & (kWave - 1);
+    const int h = threadIdx.x / kWave;
+    const int nv = seq_valid_keys(a, b);
+    if (nv == 0) return;
+    const int64_t per_wg = a.plan_hdr[1];
+    const int64_t seg_off = a.seq_off[b] + static_cast<int64_t>(kvh) * nv;
+    const int64_t w_first = seg_off / per_wg;
+    const int n_pieces = static_cast<int>((seg_off + nv - 1) / per_wg - w_first) + 1;
+    if (n_pieces == 1) return;
+    const int64_t slot0 = w_first + static_cast<int64_t>(b) * kHkv + kvh;
+
+    // (m, l) of up to 64 pieces per pass, one per lane.
+    float mx = -INFINITY;
+    for (int p0 = 0; p0 < n_pieces; p0 += kWave) {
+        const int p = p0 + lane;
+        const float m = p < n_pieces ? a.part_ml[(slot0 + p) * kGroup + h].x : -INFINITY;
+        mx = fmaxf(mx, m);
+    }
+    mx = wave_max(mx);
+    double l = 0.0, o0 = 0.0, o1 = 0.0;
+    for (int p0 = 0; p0 < n_pieces; p0 += kWave) {
+        const int p = p0 + lane;
+        int e = -1100;
+        if (p < n_pieces) {
+            const float2 ml = a.part_ml[(slot0 + p) * kGroup + h];
+            e = static_cast<int>(ml.x - mx);
+            l += ldexp(static_cast<double>(ml.y), e);
+        }
+        // O of this pass's pieces, eight at a time, every load issued before the sums
+        // (indices clamped to the last piece, whose extra copies get weight 0).
+        const int cnt = min(kWave, n_pieces - p0);
+        for (int q = 0; q < cnt; q += 8) {
+            double2 o[8];
+            int ee[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                const int qq = min(q + u, cnt - 1);
+                o[u] = reinterpret_cast<const double2*>(
+                    a.part_o + ((slot0 + p0 + qq) * kGroup + h) * kD)[lane];
+                ee[u] = __shfl(e, qq);
+            }
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                if (q + u < cnt) {
+                    o0 += ldexp(o[u].x, ee[u]);
+                    o1 += ldexp(o[u].y, ee[u]);
+                }
+            }
+        }
+    }
+    l += __shfl_xor(l, 1);
+    l += __shfl_xor(l, 2);
+    l += __shfl_xor(l, 4);
+    l += __shfl_xor(l, 8);
+    l += __shfl_xor(l, 16);
+    l += __shfl_xor(l, 32);
+    uint32_t* out = reinterpret_cast<uint32_t*>(
+        a.out + (static_cast<int64_t>(b) * kHq + kvh * kGroup + h) * kD);
+    const uint32_t lo = f32_to_bf16_rne(static_cast<float>(o0 / l));
+    const uint32_t hi = f32_to_bf16_rne(static_cast<float>(o1 / l));
+    out[lane] = lo | (hi << 16);
 }
 
 __global__ __launch_bounds__(256) void zero_words_kernel(uint32_t* p, int64_t n) {
@@ -497,24 +634,24 @@ hipError_t launch_zero_words(uint32_t* p, int64_t n, hipStream_t stream) {
 }
 
 hipError_t launch_decode(const DecodeArgs& a, int batch, hipStream_t stream, hipEvent_t* ev) {
-    const dim3 grid_stream(a.n_wgs);
     const bool rq = (a.flags & 1u) != 0, rk = (a.flags & 2u) != 0;
-    if (ev) (void)hipEventRecord(ev[0], stream);
-    if (rq && rk)
-        hipLaunchKernelGGL((decode_stream_kernel<true, true>), grid_stream, dim3(kWave), 0, stream, a);
-    else if (rq)
-        hipLaunchKernelGGL((decode_stream_kernel<true, false>), grid_stream, dim3(kWave), 0, stream, a);
-    else if (rk)
-        hipLaunchKernelGGL((decode_stream_kernel<false, true>), grid_stream, dim3(kWave), 0, stream, a);
+    if (rq)
+        hipLaunchKernelGGL((decode_prepare_kernel<true>), dim3(kHkv, batch + 1), dim3(kWave), 0, stream, a);
     else
-        hipLaunchKernelGGL((decode_stream_kernel<false, false>), grid_stream, dim3(kWave), 0, stream, a);
+        hipLaunchKernelGGL((decode_prepare_kernel<false>), dim3(kHkv, batch + 1), dim3(kWave), 0, stream, a);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    if (ev) {
-        (void)hipEventRecord(ev[1], stream);
-        (void)hipEventRecord(ev[2], stream);
-    }
-    (void)batch;
+    if (ev) (void)hipEventRecord(ev[0], stream);
+    if (rk)
+        hipLaunchKernelGGL((decode_stream_kernel<true>), dim3(a.n_wgs), dim3(kWave), 0, stream, a);
+    else
+        hipLaunchKernelGGL((decode_stream_kernel<false>), dim3(a.n_wgs), dim3(kWave), 0, stream, a);
+    e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    if (ev) (void)hipEventRecord(ev[1], stream);
+    hipLaunchKernelGGL(decode_merge_kernel, dim3(kHkv, batch), dim3(kGroup * kWave), 0, stream, a);
+    e = hipGetLastError();
+    if (ev) (void)hipEventRecord(ev[2], stream);
     return e;
 }
 

@@ -50,10 +50,16 @@ __device__ __forceinline__ uint16_t f64_to_bf16_via_f32(double d) {
 }
 
 // DPP lane moves (row = 16 lanes).  Control codes: quad_perm [1,0,3,2] = 0xB1,
-// quad_perm [2,3,0,1] = 0x4E, row_ror:n = 0x120 + n.
+// quad_perm [2,3,0,1] = 0x4E, quad_perm [h,h,h,h] = 0x55*h (broadcast lane h of each
+// quad), row_ror:n = 0x120 + n.
 template <int kCtrl>
 __device__ __forceinline__ float dpp_f(float x) {
     return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), kCtrl, 0xf, 0xf, false));
+}
+
+template <int kCtrl>
+__device__ __forceinline__ int dpp_i(int x) {
+    return __builtin_amdgcn_update_dpp(0, x, kCtrl, 0xf, 0xf, false);
 }
 
 // Sum over the 16 lanes of a DPP row; every lane of the row gets the total.
@@ -89,13 +95,26 @@ __device__ __forceinline__ float cross_row_max(float x) {
 __device__ __forceinline__ float wave_sum(float x) { return cross_row_sum(row16_sum(x)); }
 __device__ __forceinline__ float wave_max(float x) { return cross_row_max(row16_max(x)); }
 
+// sin and cos of angle = position * inv_freq, in double.  The angle (up to ~2^31 rad)
+// is first reduced modulo 2*pi with a two-part Cody-Waite constant and fused
+// multiply-adds (error ~1e-16 rad), so that sincos only ever sees |r| <= pi and
+// never takes its slow large-argument path.
+__device__ __forceinline__ void rope_sincos(int64_t position, double inv_freq, double& s, double& c) {
+    const double angle = static_cast<double>(position) * inv_freq;
+    const double two_pi_hi = 6.283185307179586232;        // 2*pi rounded to double
+    const double two_pi_lo = 2.4492935982947064e-16;      // 2*pi - two_pi_hi
+    const double k = rint(angle * 0.15915494309189535);   // 1/(2*pi)
+    double r = fma(-k, two_pi_hi, angle);
+    r = fma(-k, two_pi_lo, r);
+    sincos(r, &s, &c);
+}
+
 // Rotate one rotate_half pair at `position` for frequency index i, in double
 // (pyfiles/gen_gqa_wrapper_vectors.py:30-34).
 __device__ __forceinline__ void rope_pair(double x, double y, int64_t position, double inv_freq,
                                           double& xr, double& yr) {
-    double angle = static_cast<double>(position) * inv_freq;
     double s, c;
-    sincos(angle, &s, &c);
+    rope_sincos(position, inv_freq, s, c);
     xr = x * c - y * s;
     yr = x * s + y * c;
 }

@@ -16,7 +16,10 @@ struct DecodeArgs {
     const int32_t* seq_len;   // [B]
     const int32_t* query_pos; // [B]
     uint16_t* out;            // [B][32][128]
-    int32_t* counters;        // [8B] finished pieces per segment; zero between calls
+    uint4* q_op;              // [B][8][4][64] prepared Q operands (MFMA B layout)
+    int64_t* plan_hdr;        // {total keys, keys per stream workgroup}
+    int64_t* seq_off;         // [B] first global key offset of sequence b's segments
+    int4* wg_start;           // [n_wgs] {b, kv_head, key, n_valid(b)} where workgroup w starts
     double* part_o;           // [n_slots][4][128] unnormalised partial outputs
     float2* part_ml;          // [n_slots][4] (integer-valued running max in log2 units, sum)
     int64_t kv_batch_stride;
@@ -34,9 +37,11 @@ struct DecodeArgs {
 struct DecodePlan {
     int32_t n_wgs;
     int64_t n_slots;          // n_wgs + 8 * batch (one per piece, see gqa_decode.hip)
-    size_t counter_bytes;     // [8B] int32 segment counters at offset 0, 256-aligned
-    size_t part_o_bytes;      // then the fp64 partial outputs
-    size_t workspace_bytes;   // then the (m, l) pairs
+    size_t part_o_bytes;      // fp64 partial outputs at offset 0
+    size_t part_ml_bytes;     // then the (m, l) pairs
+    size_t q_op_bytes;        // then the prepared Q operands
+    size_t plan_bytes;        // then the plan: header, seq_off[B], wg_start[n_wgs]
+    size_t workspace_bytes;
 };
 
 DecodePlan plan_decode(int32_t batch, int32_t capacity);

@@ -66,7 +66,8 @@ typedef struct gqa_params {
 /* Where K/V rows live.  Row (sequence b, KV head h, position p) starts at element
  * b*batch_stride + h*head_stride + p*pos_stride of the K (and V) base; each row
  * is 128 contiguous BF16.  Strides are in elements and multiples of 8; pointers
- * 16-byte aligned.  capacity = positions allocated per sequence. */
+ * 16-byte aligned.  capacity = positions allocated per sequence; the rows of one
+ * (sequence, KV head) must span less than 4 GiB (capacity * pos_stride * 2 bytes). */
 typedef struct gqa_kv_layout {
     int64_t batch_stride;
     int64_t head_stride;
@@ -95,11 +96,10 @@ int gqa_validate_lengths(const int32_t* seq_len, const int32_t* query_pos, int32
  * positions.  0 if the configuration is invalid. */
 size_t gqa_decode_workspace_bytes(const gqa_params_t* params, int32_t batch, int32_t capacity);
 
-/* Prepare a workspace for decode calls with this `batch`: zero-fills its segment
- * counters (a fill kernel on `stream`, no memset).  Required once before the first
- * gqa_decode_bf16 with a workspace, and again after using it with another batch
- * size; every completed decode call leaves the counters zero for the next.  No
- * reference counterpart (the core keeps no state between starts). */
+/* Zero-fill a decode workspace with a fill kernel on `stream` (no memset, so the call
+ * may sit inside a captured graph).  Optional: decode calls need no particular
+ * workspace contents; provided for callers that want defined memory.  No reference
+ * counterpart. */
 int gqa_decode_workspace_init(const gqa_params_t* params, int32_t batch, int32_t capacity,
                               void* workspace, size_t workspace_bytes, void* stream);
 
@@ -109,8 +109,8 @@ int gqa_decode_workspace_init(const gqa_params_t* params, int32_t batch, int32_t
  *   seq_len    [batch] int32, device: valid cache length
  *   query_pos  [batch] int32, device: position of the query token
  *   out        [batch][32][128]  output rows in Q-head order
- *   workspace  gqa_decode_workspace_bytes bytes, prepared by gqa_decode_workspace_init;
- *              calls sharing a workspace must be ordered (same stream)
+ *   workspace  gqa_decode_workspace_bytes bytes (any contents); calls sharing a
+ *              workspace must be ordered (same stream)
  * Key p of sequence b contributes iff p < seq_len[b] and p <= query_pos[b]
  * (gqa_attention_wrapper.v:279); rows outside that range are never read.
  * Lengths are read on the device: an entry violating the rules of
@@ -129,15 +129,15 @@ int gqa_rope_rows_bf16(const uint16_t* in, uint16_t* out, int64_t n_rows, int64_
                        const int32_t* positions, int32_t pos0, double theta, void* stream);
 
 /* Kernel timing for measurement harnesses.  While enabled, each decode call
- * brackets its decode kernel with HIP events on the call's stream (combine_ms is
- * kept for layout compatibility and reads 0: the merge runs inside that kernel) (up to `max_calls` calls are recorded; later ones are not).
+ * brackets its stream kernel and its merge kernel with HIP events on the call's
+ * stream (up to `max_calls` calls are recorded; later ones are not).
  * gqa_profile_read waits for the recorded events, returns the summed kernel
  * times and the number of calls recorded, and clears the record.  Not for the
  * hot path: enabling creates the events.  No reference counterpart (the
  * reference's timing is its simulator's cycle count). */
 typedef struct gqa_profile {
-    double split_ms;      /* summed duration of the decode kernel launches */
-    double combine_ms;    /* 0: the merge of pieces runs inside the decode kernel */
+    double split_ms;      /* summed duration of the stream (split-KV) kernel launches */
+    double combine_ms;    /* summed duration of the merge kernel launches */
     int32_t calls;        /* decode calls recorded */
 } gqa_profile_t;
 
