@@ -21,17 +21,33 @@ void fill_rope_table(double theta, RopeTable* t) {
 
 namespace {
 
-// Persistent workgroups of the decode stream kernel: one wave each, eight per CU on
-// the 256 CUs of an MI355X.  GQA_STREAM_WGS overrides it (tuning only).
-constexpr int32_t kStreamWgs = 2048;
+// Persistent workgroups of the decode stream kernel: one wave each, one per SIMD (four
+// per CU) of the current device -- 1024 on the 256 CUs of an MI355X.  Measured on
+// MI355X, one wave per SIMD streams faster than two (fewer concurrent DRAM streams; the
+// kernel's ~250 registers leave room for one wave per SIMD anyway).  1024 when no
+// device answers.  GQA_STREAM_WGS overrides it (tuning only).
+constexpr int32_t kStreamWgsDefault = 1024;
+constexpr int32_t kWavesPerCu = 4;
 
 size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
 
+int32_t device_stream_wgs() {
+    int dev = 0, cus = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) {
+        (void)hipGetLastError();   // leave no error behind for the caller's next HIP call
+        return kStreamWgsDefault;
+    }
+    return cus * kWavesPerCu;
+}
+
 int32_t stream_wgs() {
     const char* s = std::getenv("GQA_STREAM_WGS");
-    if (!s) return kStreamWgs;
-    const int v = std::atoi(s);
-    return (v >= 1 && v <= 65536) ? v : kStreamWgs;
+    if (s) {
+        const int v = std::atoi(s);
+        if (v >= 1 && v <= 65536) return v;
+    }
+    return device_stream_wgs();
 }
 
 bool geometry_ok(const gqa_params_t* p) {
@@ -143,8 +159,9 @@ int gqa_decode_bf16(const gqa_params_t* params, const uint16_t* q, const uint16_
         !aligned(seq_len, 4) || !aligned(query_pos, 4))
         return GQA_ERR_BAD_POINTER;
     if (kv->pos_stride % 8 || kv->head_stride % 8 || kv->batch_stride % 8) return GQA_ERR_BAD_POINTER;
-    // Rows of one (sequence, KV head) are addressed with 32-bit byte offsets.
-    if (static_cast<uint64_t>(kv->capacity) * static_cast<uint64_t>(kv->pos_stride) * 2u >
+    // Rows of one (sequence, KV head) are addressed with 32-bit byte offsets, which run
+    // up to 64 rows past the last valid one (prefetch offsets, clamped before use).
+    if ((static_cast<uint64_t>(kv->capacity) + 64u) * static_cast<uint64_t>(kv->pos_stride) * 2u >
         0xFFFFFF00ull)
         return GQA_ERR_INVALID_CONFIG;
 

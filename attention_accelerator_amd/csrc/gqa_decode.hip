@@ -129,6 +129,16 @@ __device__ __forceinline__ bf16x8_t as_bf16x8(const uint4& w) {
     return t.v;
 }
 
+// 16-byte load with the nontemporal hint (global_load_dwordx4 ... nt).  Every K/V row
+// is read exactly once per step, so the rows should not displace anything in L2 or
+// the Infinity Cache; on MI355X the hint raised the stream kernel from 5.5 to 6.1 TB/s
+// on the B=64 ragged batch.
+typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ uint4 load_stream16(const char* p) {
+    const u32x4_t v = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(p));
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
+
 // K and V rows of one 16-key chunk, in the MFMA (K) and PV (V) lane layouts.
 struct Chunk {
     uint4 kw[4];
@@ -157,10 +167,10 @@ __device__ __forceinline__ void load_chunk(const char* kseg, const char* vseg, c
                                            uint32_t k_last, uint32_t v_last, Chunk& c) {
     const char* kp = kseg + min(r.k, k_last);
 #pragma unroll
-    for (int kb = 0; kb < 4; ++kb) c.kw[kb] = *reinterpret_cast<const uint4*>(kp + 64 * kb);
+    for (int kb = 0; kb < 4; ++kb) c.kw[kb] = load_stream16(kp + 64 * kb);
 #pragma unroll
     for (int it = 0; it < 4; ++it)
-        c.vw[it] = *reinterpret_cast<const uint4*>(vseg + min(r.v[it], v_last));
+        c.vw[it] = load_stream16(vseg + min(r.v[it], v_last));
 }
 
 __device__ __forceinline__ void advance(ChunkRows& r, uint32_t step) {
@@ -282,54 +292,25 @@ __device__ __forceinline__ void compute_chunk(const DecodeArgs& a, int kc, int k
 // head n%4, dims 32kb + 8(l/16) + j).  One wave per (kv_head, sequence).  It also
 // writes the NaN rows of sequences whose lengths break the rules, and (an extra row of
 // the grid) the stream-K plan.
-// Start of stream workgroup w, whose range begins inside sequence b (segments from
-// global key offset off, nv keys each): KV head by comparison, no division.
-__device__ __forceinline__ void write_wg_start(const DecodeArgs& a, int64_t w, int64_t per_wg,
-                                               int64_t off, int nv, int b) {
-    const int64_t rel = w * per_wg - off;       // in [0, 8 * nv)
-    int kvh = 0;
-#pragma unroll
-    for (int k = 1; k < kHkv; ++k) kvh += rel >= static_cast<int64_t>(k) * nv;
-    a.wg_start[w] = make_int4(b, kvh, static_cast<int>(rel - static_cast<int64_t>(kvh) * nv), nv);
-}
-
-// The stream-K plan (row B of the prepare grid, one wave): per-sequence key offsets,
-// the total and the range size, and where every stream workgroup starts.  For each
-// sequence in turn the lanes share the workgroups whose ranges begin inside its
-// segments.
+//
+// The stream-K plan (row B of the prepare grid, one wave): seq_off[b] = global key
+// offset of sequence b's first segment (an exclusive scan of 8 * n_valid), seq_off[B]
+// = total keys, and the header {total, keys per stream workgroup}.  Every stream
+// workgroup finds where its range starts from these with one ballot.
 __device__ __forceinline__ void build_plan(const DecodeArgs& a, int lane) {
     int64_t total, per_wg;
     stream_totals(a, lane, total, per_wg);
     if (lane == 0) {
         a.plan_hdr[0] = total;
         a.plan_hdr[1] = per_wg;
+        a.seq_off[a.batch] = total;
     }
     int64_t carry = 0;
     for (int base = 0; base < a.batch; base += kWave) {
         const int b = base + lane;
         const int nv = b < a.batch ? seq_valid_keys(a, b) : 0;
         const int64_t incl = wave_incl_scan_i64(nv, lane) + carry;
-        const int64_t off = (incl - nv) * kHkv;
-        if (b < a.batch) a.seq_off[b] = off;
-        // Workgroups whose ranges start inside sequence b's segments: [w0, w1).
-        const int64_t w0 = (off + per_wg - 1) / per_wg;
-        const int64_t w1 = (off + static_cast<int64_t>(kHkv) * nv + per_wg - 1) / per_wg;
-        // Few workgroups per sequence (the common case): each lane writes its own.
-        // Many (a long sequence): the lanes share them, one such sequence at a time.
-        const bool own = b < a.batch && nv > 0 && w1 - w0 <= kWave;
-        if (own) {
-            for (int64_t w = w0; w < w1; ++w) write_wg_start(a, w, per_wg, off, nv, b);
-        }
-        uint64_t big = __ballot(b < a.batch && nv > 0 && !own);
-        while (big) {
-            const int j = __ffsll(static_cast<unsigned long long>(big)) - 1;
-            big &= big - 1;
-            const int nv_j = __shfl(nv, j);
-            const int64_t off_j = __shfl(off, j);
-            const int64_t w1_j = __shfl(w1, j);
-            for (int64_t w = __shfl(w0, j) + lane; w < w1_j; w += kWave)
-                write_wg_start(a, w, per_wg, off_j, nv_j, base + j);
-        }
+        if (b < a.batch) a.seq_off[b] = (incl - nv) * kHkv;
         carry = __shfl(incl, kWave - 1);
     }
 }
@@ -388,36 +369,76 @@ __global__ __launch_bounds__(kWave) void decode_prepare_kernel(DecodeArgs a) {
     }
 }
 
-// One piece: keys [k_a, k_b) of segment (b, kvh).  Writes the output rows itself when
-// the piece is the whole segment; otherwise leaves a partial for the merge kernel.
+// Where the rows of one piece live: segment base pointers and this lane's offsets of
+// the chunk to load next (clamped to the piece's last row).
+struct PieceRows {
+    const char* kseg;
+    const char* vseg;
+    ChunkRows rows;
+    uint32_t k_last;
+    uint32_t v_last;
+};
+
+__device__ __forceinline__ void piece_rows(const DecodeArgs& a, int b, int kvh, int k_a, int k_b,
+                                           PieceRows& r) {
+    const int lane = threadIdx.x;
+    const int n = lane & 15;
+    const int g = lane >> 4;
+    const int64_t head_off = static_cast<int64_t>(b) * a.kv_batch_stride +
+                             static_cast<int64_t>(kvh) * a.kv_head_stride;
+    r.kseg = reinterpret_cast<const char*>(a.k + head_off);
+    r.vseg = reinterpret_cast<const char*>(a.v + head_off);
+    const uint32_t row = static_cast<uint32_t>(a.kv_pos_stride) * 2u;   // bytes per position
+    r.rows.k = static_cast<uint32_t>(k_a + n) * row + 16u * g;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) r.rows.v[i] = static_cast<uint32_t>(k_a + 4 * g + i) * row + 16u * n;
+    r.k_last = static_cast<uint32_t>(k_b - 1) * row + 16u * g;
+    r.v_last = static_cast<uint32_t>(k_b - 1) * row + 16u * n;
+}
+
+__device__ __forceinline__ void load_next(PieceRows& r, uint32_t step, Chunk& c) {
+    load_chunk(r.kseg, r.vseg, r.rows, r.k_last, r.v_last, c);
+    advance(r.rows, step);
+}
+
+// Chunk `c` from the current piece when `in_cur`, else the first chunk of the next piece
+// (the condition is wave-uniform; both addresses are formed and one is selected, so
+// the load itself is unconditional).  Either way rows past the piece are clamped to its
+// last row.
+__device__ __forceinline__ void load_cur_or_next(bool in_cur, PieceRows& cur, const PieceRows& nxt,
+                                                 uint32_t step, Chunk& c) {
+    const char* kp = in_cur ? cur.kseg + min(cur.rows.k, cur.k_last) : nxt.kseg + min(nxt.rows.k, nxt.k_last);
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb) c.kw[kb] = load_stream16(kp + 64 * kb);
+#pragma unroll
+    for (int it = 0; it < 4; ++it) {
+        const char* vp = in_cur ? cur.vseg + min(cur.rows.v[it], cur.v_last)
+                                : nxt.vseg + min(nxt.rows.v[it], nxt.v_last);
+        c.vw[it] = load_stream16(vp);
+    }
+    advance(cur.rows, step);
+}
+
+__device__ __forceinline__ void load_q_operands(const DecodeArgs& a, int b, int kvh, bf16x8_t (&bq)[4]) {
+    const uint4* qop = a.q_op + ((static_cast<int64_t>(b) * kHkv + kvh) * 4) * kWave + threadIdx.x;
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb) bq[kb] = as_bf16x8(qop[kb * kWave]);
+}
+
+// One piece: keys [k_a, k_b) of segment (b, kvh), whose first chunk is already in c0
+// and whose Q operands are in bq.  While the piece's last chunk is computed, the first
+// chunk of the next piece (rows `nxt`) is requested into c0, so the wave never waits
+// at a piece boundary.  Writes the output rows itself when the piece is the whole
+// segment; otherwise leaves a partial for the merge kernel.
 template <bool kRopeK>
 __device__ __forceinline__ void process_piece(const DecodeArgs& a, int b, int kvh, int nv, int k_a,
-                                              int k_b, int64_t wg) {
+                                              int k_b, int64_t wg, PieceRows& cur,
+                                              const PieceRows& nxt, Chunk& c0, Chunk& c1,
+                                              const bf16x8_t (&bq)[4]) {
     const int lane = threadIdx.x;
     const int n = lane & 15;       // MFMA column / PV dim chunk
     const int g = lane >> 4;       // MFMA lane group / PV key row
-    const int64_t head_off = static_cast<int64_t>(b) * a.kv_batch_stride +
-                             static_cast<int64_t>(kvh) * a.kv_head_stride;
-    const char* kseg = reinterpret_cast<const char*>(a.k + head_off);
-    const char* vseg = reinterpret_cast<const char*>(a.v + head_off);
-    const uint32_t row = static_cast<uint32_t>(a.kv_pos_stride) * 2u;   // bytes per position
-    ChunkRows rows;
-    rows.k = static_cast<uint32_t>(k_a + n) * row + 16u * g;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) rows.v[i] = static_cast<uint32_t>(k_a + 4 * g + i) * row + 16u * n;
-    const uint32_t k_last = static_cast<uint32_t>(k_b - 1) * row + 16u * g;
-    const uint32_t v_last = static_cast<uint32_t>(k_b - 1) * row + 16u * n;
-    const uint32_t step = kChunk * row;
-
-    // First chunk's rows are requested together with the Q operands.
-    Chunk c0, c1;
-    load_chunk(kseg, vseg, rows, k_last, v_last, c0);
-
-    // Q operands prepared by decode_prepare_kernel for this (sequence, KV head).
-    const uint4* qop = a.q_op + ((static_cast<int64_t>(b) * kHkv + kvh) * 4) * kWave + lane;
-    bf16x8_t bq[4];
-#pragma unroll
-    for (int kb = 0; kb < 4; ++kb) bq[kb] = as_bf16x8(qop[kb * kWave]);
+    const uint32_t step = kChunk * static_cast<uint32_t>(a.kv_pos_stride) * 2u;
 
     PieceState st;
 #pragma unroll
@@ -427,18 +448,16 @@ __device__ __forceinline__ void process_piece(const DecodeArgs& a, int b, int kv
     st.m_run = -INFINITY;
     st.l_run = 0.f;
 
-    // Two register sets: chunk j+1 is in flight while chunk j is computed.  The
-    // prefetch is issued even past the last chunk (clamped to the piece's last row,
-    // so it reads that one row again) to keep the loop body free of load branches.
+    // Two register sets: chunk j+1 is in flight while chunk j is computed.  Chunk i+1
+    // of an odd-length piece does not exist; its slot re-reads the piece's last row (a
+    // clamped, unconditional load) and its computation is skipped, so that the next
+    // piece's first chunk always lands in c0.
     const int n_chunks = (k_b - k_a + kChunk - 1) / kChunk;
     for (int i = 0;; i += 2) {
-        advance(rows, step);
-        load_chunk(kseg, vseg, rows, k_last, v_last, c1);
+        load_cur_or_next(true, cur, nxt, step, c1);
         compute_chunk<kRopeK>(a, k_a + i * kChunk, k_b, n, g, c0, bq, st);
-        if (i + 1 >= n_chunks) break;
-        advance(rows, step);
-        load_chunk(kseg, vseg, rows, k_last, v_last, c0);
-        compute_chunk<kRopeK>(a, k_a + (i + 1) * kChunk, k_b, n, g, c1, bq, st);
+        load_cur_or_next(i + 2 < n_chunks, cur, nxt, step, c0);
+        if (i + 1 < n_chunks) compute_chunk<kRopeK>(a, k_a + (i + 1) * kChunk, k_b, n, g, c1, bq, st);
         if (i + 2 >= n_chunks) break;
     }
 
@@ -510,42 +529,133 @@ __device__ __forceinline__ void process_piece(const DecodeArgs& a, int b, int kv
         const double ll = lane == 0 ? l_tot[0] : lane == 1 ? l_tot[1] : lane == 2 ? l_tot[2] : l_tot[3];
         a.part_ml[slot * kGroup + lane] = make_float2(mm, static_cast<float>(ll));
     }
+}
 
+// Per-sequence key offsets for 64 sequences at a time, one per lane: o = seq_off[base +
+// lane], o1 = seq_off[base + lane + 1] (the segments of sequence b hold keys [o, o1)).
+struct SeqWindow {
+    int base;
+    int64_t o;
+    int64_t o1;
+};
+
+__device__ __forceinline__ void load_seq_window(const DecodeArgs& a, int base, SeqWindow& sw) {
+    const int bb = base + static_cast<int>(threadIdx.x);
+    sw.base = base;
+    sw.o = bb < a.batch ? a.seq_off[bb] : INT64_MAX;
+    sw.o1 = bb < a.batch ? a.seq_off[bb + 1] : INT64_MAX;
+}
+
+// The segment after (b, kvh) that has keys: the next KV head of b, or KV head 0 of the
+// next sequence with keys.  Returns false when there is none (possible only if the
+// lengths changed while the kernel ran).
+__device__ __forceinline__ bool next_segment(const DecodeArgs& a, SeqWindow& sw, int& b, int& kvh,
+                                             int& nv) {
+    if (kvh + 1 < kHkv) {
+        ++kvh;
+        return true;
+    }
+    kvh = 0;
+    while (true) {
+        const int bb = sw.base + static_cast<int>(threadIdx.x);
+        const uint64_t m = __ballot(bb < a.batch && bb > b && sw.o1 > sw.o);
+        if (m) {
+            const int j = __ffsll(static_cast<unsigned long long>(m)) - 1;
+            b = sw.base + j;
+            nv = static_cast<int>((__shfl(sw.o1, j) - __shfl(sw.o, j)) / kHkv);
+            return true;
+        }
+        if (sw.base + kWave >= a.batch) return false;
+        load_seq_window(a, sw.base + kWave, sw);
+    }
 }
 
 template <bool kRopeK>
-__global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(2))) void decode_stream_kernel(DecodeArgs a) {
+__global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(1))) void decode_stream_kernel(DecodeArgs a) {
     const int64_t w = blockIdx.x;
     const int64_t total = a.plan_hdr[0];
     const int64_t per_wg = a.plan_hdr[1];
-    const int4 start = a.wg_start[w];
     int64_t x = w * per_wg;
     if (x >= total) return;
     const int64_t x_end = min(x + per_wg, total);
 
-    int b = start.x;
-    int kvh = start.y;
-    int key = start.z;
-    int nvb = start.w;
-    while (true) {
-        // Everything that shapes the piece is wave-uniform; say so, so that the loop
-        // control and the segment bases live in scalar registers.
-        b = __builtin_amdgcn_readfirstlane(b);
-        kvh = __builtin_amdgcn_readfirstlane(kvh);
-        key = __builtin_amdgcn_readfirstlane(key);
-        nvb = __builtin_amdgcn_readfirstlane(nvb);
-        const int k_b = __builtin_amdgcn_readfirstlane(
-            static_cast<int>(min(static_cast<int64_t>(nvb), key + (x_end - x))));
-        process_piece<kRopeK>(a, b, kvh, nvb, key, k_b, w);
-        x += k_b - key;
-        if (x >= x_end) break;
-        key = 0;
-        if (++kvh == kHkv) {
-            kvh = 0;
-            nvb = 0;
-            while (nvb == 0 && ++b < a.batch) nvb = seq_valid_keys(a, b);
-            if (nvb == 0) break;   // lengths changed under the launch; nothing left to read
+    // Start sequence b = the last b with seq_off[b] <= x (it has keys, since x < total).
+    SeqWindow sw;
+    int b = 0;
+    int64_t off = 0, next = 0;
+    for (int base = 0; base < a.batch; base += kWave) {
+        SeqWindow t;
+        load_seq_window(a, base, t);
+        const uint64_t le = __ballot(t.o <= x);
+        if (le) {
+            const int j = 63 - __clzll(static_cast<long long>(le));
+            b = base + j;
+            off = __shfl(t.o, j);
+            next = __shfl(t.o1, j);
+            sw = t;
         }
+    }
+    int nvb = static_cast<int>((next - off) / kHkv);
+    const int64_t rel = x - off;                  // in [0, 8 * nvb)
+    int kvh = 0;
+#pragma unroll
+    for (int k = 1; k < kHkv; ++k) kvh += rel >= static_cast<int64_t>(k) * nvb;
+    int key = static_cast<int>(rel - static_cast<int64_t>(kvh) * nvb);
+    b = __builtin_amdgcn_readfirstlane(b);
+    kvh = __builtin_amdgcn_readfirstlane(kvh);
+    key = __builtin_amdgcn_readfirstlane(key);
+    nvb = __builtin_amdgcn_readfirstlane(nvb);
+    int k_b = __builtin_amdgcn_readfirstlane(
+        static_cast<int>(min(static_cast<int64_t>(nvb), key + (x_end - x))));
+
+    const uint32_t step = kChunk * static_cast<uint32_t>(a.kv_pos_stride) * 2u;
+    PieceRows cur;
+    piece_rows(a, b, kvh, key, k_b, cur);
+    Chunk c0, c1;
+    load_next(cur, step, c0);
+    bf16x8_t bq[4];
+    load_q_operands(a, b, kvh, bq);
+
+    while (true) {
+        // The next piece of this range (or, after the last one, a re-read of this piece's
+        // last row), whose first chunk and Q operands are requested during this piece.
+        const int64_t x_next = x + (k_b - key);
+        int b2 = b, kvh2 = kvh, nv2 = nvb, key2 = k_b - 1, k_b2 = k_b;
+        bool more = x_next < x_end;
+        if (more) {
+            more = next_segment(a, sw, b2, kvh2, nv2);
+            b2 = __builtin_amdgcn_readfirstlane(b2);
+            kvh2 = __builtin_amdgcn_readfirstlane(kvh2);
+            nv2 = __builtin_amdgcn_readfirstlane(nv2);
+            key2 = 0;
+            k_b2 = __builtin_amdgcn_readfirstlane(
+                static_cast<int>(min(static_cast<int64_t>(nv2), x_end - x_next)));
+        }
+        if (!more) {
+            b2 = b;
+            kvh2 = kvh;
+            nv2 = nvb;
+            key2 = k_b - 1;
+            k_b2 = k_b;
+        }
+        PieceRows nxt;
+        piece_rows(a, b2, kvh2, key2, k_b2, nxt);
+        bf16x8_t bq2[4];
+        load_q_operands(a, b2, kvh2, bq2);
+
+        process_piece<kRopeK>(a, b, kvh, nvb, key, k_b, w, cur, nxt, c0, c1, bq);
+        if (!more) break;
+
+        x = x_next;
+        b = b2;
+        kvh = kvh2;
+        nvb = nv2;
+        key = key2;
+        k_b = k_b2;
+        cur = nxt;
+        advance(cur.rows, step);     // its first chunk is in c0 already
+#pragma unroll
+        for (int kb = 0; kb < 4; ++kb) bq[kb] = bq2[kb];
     }
 }
 
@@ -560,50 +670,53 @@ __global__ __launch_bounds__(kGroup * kWave) void decode_merge_kernel(DecodeArgs
     const int b = blockIdx.y;
     const int lane = threadIdx.x & (kWave - 1);
     const int h = threadIdx.x / kWave;
-    const int nv = seq_valid_keys(a, b);
-    if (nv == 0) return;
     const int64_t per_wg = a.plan_hdr[1];
-    const int64_t seg_off = a.seq_off[b] + static_cast<int64_t>(kvh) * nv;
+    const int64_t off = a.seq_off[b];
+    const int nv = static_cast<int>((a.seq_off[b + 1] - off) / kHkv);
+    if (nv == 0) return;
+    const int64_t seg_off = off + static_cast<int64_t>(kvh) * nv;
     const int64_t w_first = seg_off / per_wg;
     const int n_pieces = static_cast<int>((seg_off + nv - 1) / per_wg - w_first) + 1;
     if (n_pieces == 1) return;
     const int64_t slot0 = w_first + static_cast<int64_t>(b) * kHkv + kvh;
 
-    // (m, l) of up to 64 pieces per pass, one per lane.
+    // Pieces in passes of 64, one (m, l) per lane; the O rows of a pass are requested
+    // together with its (m, l) (indices clamped to the last piece, whose extra copies get
+    // weight 0) and weighted by 2^(m - running max) once the pass's max is known.
     float mx = -INFINITY;
-    for (int p0 = 0; p0 < n_pieces; p0 += kWave) {
-        const int p = p0 + lane;
-        const float m = p < n_pieces ? a.part_ml[(slot0 + p) * kGroup + h].x : -INFINITY;
-        mx = fmaxf(mx, m);
-    }
-    mx = wave_max(mx);
     double l = 0.0, o0 = 0.0, o1 = 0.0;
     for (int p0 = 0; p0 < n_pieces; p0 += kWave) {
-        const int p = p0 + lane;
-        int e = -1100;
-        if (p < n_pieces) {
-            const float2 ml = a.part_ml[(slot0 + p) * kGroup + h];
-            e = static_cast<int>(ml.x - mx);
-            l += ldexp(static_cast<double>(ml.y), e);
-        }
-        // O of this pass's pieces, eight at a time, every load issued before the sums
-        // (indices clamped to the last piece, whose extra copies get weight 0).
         const int cnt = min(kWave, n_pieces - p0);
+        const int p = p0 + min(lane, cnt - 1);
+        const float2 ml = a.part_ml[(slot0 + p) * kGroup + h];
         for (int q = 0; q < cnt; q += 8) {
             double2 o[8];
-            int ee[8];
 #pragma unroll
             for (int u = 0; u < 8; ++u) {
                 const int qq = min(q + u, cnt - 1);
                 o[u] = reinterpret_cast<const double2*>(
                     a.part_o + ((slot0 + p0 + qq) * kGroup + h) * kD)[lane];
-                ee[u] = __shfl(e, qq);
             }
+            if (q == 0) {
+                // New running max over this pass; rescale what earlier passes summed.
+                const float m_pass = wave_max(lane < cnt ? ml.x : -INFINITY);
+                const float m_new = fmaxf(mx, m_pass);
+                if (mx != -INFINITY && m_new != mx) {
+                    const int e = static_cast<int>(mx - m_new);
+                    l = ldexp(l, e);
+                    o0 = ldexp(o0, e);
+                    o1 = ldexp(o1, e);
+                }
+                mx = m_new;
+                if (lane < cnt) l += ldexp(static_cast<double>(ml.y), static_cast<int>(ml.x - mx));
+            }
+            const int e_lane = lane < cnt ? static_cast<int>(ml.x - mx) : -1100;
 #pragma unroll
             for (int u = 0; u < 8; ++u) {
+                const int ee = __shfl(e_lane, min(q + u, kWave - 1));
                 if (q + u < cnt) {
-                    o0 += ldexp(o[u].x, ee[u]);
-                    o1 += ldexp(o[u].y, ee[u]);
+                    o0 += ldexp(o[u].x, ee);
+                    o1 += ldexp(o[u].y, ee);
                 }
             }
         }

@@ -67,7 +67,8 @@ typedef struct gqa_params {
  * b*batch_stride + h*head_stride + p*pos_stride of the K (and V) base; each row
  * is 128 contiguous BF16.  Strides are in elements and multiples of 8; pointers
  * 16-byte aligned.  capacity = positions allocated per sequence; the rows of one
- * (sequence, KV head) must span less than 4 GiB (capacity * pos_stride * 2 bytes). */
+ * (sequence, KV head) must span less than 4 GiB ((capacity + 64) * pos_stride * 2
+ * bytes). */
 typedef struct gqa_kv_layout {
     int64_t batch_stride;
     int64_t head_stride;
