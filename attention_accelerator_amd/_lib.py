@@ -32,6 +32,9 @@ EXPORTS = (
     "gqa_decode_workspace_bytes",
     "gqa_decode_workspace_init",
     "gqa_decode_bf16",
+    "gqa_prefill_workspace_bytes",
+    "gqa_prefill_bf16",
+    "gqa_kv_append_bf16",
     "gqa_rope_rows_bf16",
     "gqa_profile_enable",
     "gqa_profile_read",
@@ -62,8 +65,7 @@ class GqaKvLayout(ctypes.Structure):
 
 class GqaProfile(ctypes.Structure):
     _fields_ = [
-        ("split_ms", ctypes.c_double),
-        ("combine_ms", ctypes.c_double),
+        ("kernel_ms", ctypes.c_double * 2),
         ("calls", ctypes.c_int32),
     ]
 
@@ -106,6 +108,17 @@ def lib() -> ctypes.CDLL:
                                   ctypes.POINTER(GqaKvLayout), vp, vp, ctypes.c_int32, vp, vp,
                                   ctypes.c_size_t, vp]
     L.gqa_decode_bf16.restype = ctypes.c_int
+    L.gqa_prefill_workspace_bytes.argtypes = [ctypes.POINTER(GqaParams), ctypes.c_int32,
+                                              ctypes.c_int32]
+    L.gqa_prefill_workspace_bytes.restype = ctypes.c_size_t
+    L.gqa_prefill_bf16.argtypes = [ctypes.POINTER(GqaParams), vp, vp, vp, vp, vp,
+                                   ctypes.POINTER(GqaKvLayout), vp, ctypes.c_int32, ctypes.c_int32,
+                                   vp, vp, ctypes.c_size_t, vp]
+    L.gqa_prefill_bf16.restype = ctypes.c_int
+    L.gqa_kv_append_bf16.argtypes = [ctypes.POINTER(GqaParams), vp, vp, vp, vp,
+                                     ctypes.POINTER(GqaKvLayout), vp, ctypes.c_int32, ctypes.c_int32,
+                                     vp]
+    L.gqa_kv_append_bf16.restype = ctypes.c_int
     L.gqa_rope_rows_bf16.argtypes = [vp, vp, ctypes.c_int64, ctypes.c_int64, vp, ctypes.c_int32,
                                      ctypes.c_double, vp]
     L.gqa_rope_rows_bf16.restype = ctypes.c_int

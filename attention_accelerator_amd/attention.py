@@ -225,6 +225,109 @@ class PreparedDecode:
         return self.out
 
 
+def _cache_layout(k_cache: torch.Tensor, v_cache: torch.Tensor) -> GqaKvLayout:
+    if k_cache.dim() != 4 or k_cache.shape != v_cache.shape or k_cache.stride() != v_cache.stride():
+        raise ValueError("k_cache and v_cache must be [B,8,S,128] with the same shape and strides")
+    for name, t in (("k_cache", k_cache), ("v_cache", v_cache)):
+        if t.dtype != torch.bfloat16 or not t.is_cuda:
+            raise ValueError(f"{name} must be a bfloat16 tensor on the GPU")
+    if k_cache.stride(3) != 1:
+        raise ValueError("cache rows must be contiguous in head_dim")
+    return GqaKvLayout(k_cache.stride(0), k_cache.stride(1), k_cache.stride(2), k_cache.shape[2])
+
+
+def _start_tensor(start: Lengths, batch: int, capacity: int, n_new: int, device):
+    """Device int32 start positions; host values are checked first
+    (0 <= start <= capacity - n_new)."""
+    if isinstance(start, torch.Tensor) and start.is_cuda:
+        if start.dtype != torch.int32 or start.numel() != batch:
+            raise ValueError(f"start must be an int32 tensor of {batch} elements")
+        return start.contiguous()
+    host = torch.as_tensor(start, dtype=torch.int32).reshape(-1)
+    if host.numel() == 1 and batch > 1:
+        host = host.expand(batch)
+    if host.numel() != batch:
+        raise ValueError(f"start has {host.numel()} entries for a batch of {batch}")
+    if int(host.min()) < 0 or int(host.max()) > capacity - n_new:
+        check(_lib.GQA_ERR_INVALID_CONFIG, "start positions")
+    return host.contiguous().to(device)
+
+
+def prefill_workspace_bytes(batch: int, n_new: int, params: Optional[GqaParams] = None) -> int:
+    p = params or make_params()
+    return int(lib().gqa_prefill_workspace_bytes(ctypes.byref(p), int(batch), int(n_new)))
+
+
+def gqa_prefill(q: torch.Tensor, k_new: torch.Tensor, v_new: torch.Tensor, k_cache: torch.Tensor,
+                v_cache: torch.Tensor, start: Lengths, *, rope_q: bool = True, rope_k: bool = True,
+                theta: float = ROPE_THETA, scale: Optional[float] = None,
+                out: Optional[torch.Tensor] = None, workspace: Optional[torch.Tensor] = None,
+                params: Optional[GqaParams] = None) -> torch.Tensor:
+    """Chunked prefill: T new tokens per sequence after start[b] cached positions.
+
+    q            [B, T, 32, 128] bfloat16 (rotated at positions start+t when rope_q)
+    k_new, v_new [B, T, 8, 128] bfloat16 (K rotated at start+t when rope_k)
+    k_cache, v_cache [B, 8, S, 128] bfloat16, rows < start post-RoPE; the chunk's rows are
+             written at start+t (K rotated, rounded to BF16) before the attention
+    start    int, B ints, or a device int32 tensor (host values checked:
+             0 <= start <= S - T)
+    Returns out [B, T, 32, 128]: token t attends to keys p <= start + t."""
+    if q.dim() != 4 or k_new.dim() != 4 or v_new.shape != k_new.shape:
+        raise ValueError("expected q [B,T,32,128] and k_new/v_new [B,T,8,128]")
+    for name, t in (("q", q), ("k_new", k_new), ("v_new", v_new)):
+        if t.dtype != torch.bfloat16 or not t.is_cuda:
+            raise ValueError(f"{name} must be a bfloat16 tensor on the GPU")
+    batch, n_new = q.shape[0], q.shape[1]
+    if k_new.shape[:2] != (batch, n_new) or k_cache.shape[0] != batch:
+        raise ValueError("batch / token count mismatch")
+    layout = _cache_layout(k_cache, v_cache)
+    p = params or make_params(rope_q=rope_q, rope_k=rope_k, theta=theta, scale=scale,
+                              n_q_heads=q.shape[2], n_kv_heads=k_new.shape[2], head_dim=q.shape[3])
+    device = q.device
+    st = _start_tensor(start, batch, k_cache.shape[2], n_new, device)
+    q, k_new, v_new = q.contiguous(), k_new.contiguous(), v_new.contiguous()
+    ws_bytes = int(lib().gqa_prefill_workspace_bytes(ctypes.byref(p), batch, n_new))
+    if ws_bytes == 0:
+        check(_lib.GQA_ERR_INVALID_CONFIG, "gqa_prefill_workspace_bytes")
+    if workspace is None:
+        workspace = torch.empty(ws_bytes, dtype=torch.uint8, device=device)
+    elif workspace.numel() * workspace.element_size() < ws_bytes:
+        raise ValueError(f"workspace holds {workspace.numel() * workspace.element_size()} bytes; "
+                         f"{ws_bytes} needed")
+    if out is None:
+        out = torch.empty(q.shape, dtype=torch.bfloat16, device=device)
+    elif out.shape != q.shape or out.dtype != torch.bfloat16 or not out.is_contiguous():
+        raise ValueError("out must be a contiguous bfloat16 tensor shaped like q")
+    status = lib().gqa_prefill_bf16(
+        ctypes.byref(p), q.data_ptr(), k_new.data_ptr(), v_new.data_ptr(), k_cache.data_ptr(),
+        v_cache.data_ptr(), ctypes.byref(layout), st.data_ptr(), batch, n_new, out.data_ptr(),
+        workspace.data_ptr(), workspace.numel() * workspace.element_size(), _stream_handle(device))
+    check(status, "gqa_prefill_bf16")
+    return out
+
+
+def kv_append(k_new: torch.Tensor, v_new: torch.Tensor, k_cache: torch.Tensor,
+              v_cache: torch.Tensor, start: Lengths, *, rope_k: bool = True,
+              theta: float = ROPE_THETA) -> None:
+    """Write k_new / v_new [B, T, 8, 128] into the cache at positions start+t, K rotated
+    at its position (rope_k) and rounded to BF16: the cache stays post-RoPE."""
+    if k_new.dim() != 4 or v_new.shape != k_new.shape:
+        raise ValueError("expected k_new/v_new [B,T,8,128]")
+    for name, t in (("k_new", k_new), ("v_new", v_new)):
+        if t.dtype != torch.bfloat16 or not t.is_cuda:
+            raise ValueError(f"{name} must be a bfloat16 tensor on the GPU")
+    batch, n_new = k_new.shape[0], k_new.shape[1]
+    layout = _cache_layout(k_cache, v_cache)
+    p = make_params(rope_q=False, rope_k=rope_k, theta=theta, n_kv_heads=k_new.shape[2],
+                    head_dim=k_new.shape[3])
+    st = _start_tensor(start, batch, k_cache.shape[2], n_new, k_new.device)
+    k_new, v_new = k_new.contiguous(), v_new.contiguous()
+    status = lib().gqa_kv_append_bf16(ctypes.byref(p), k_new.data_ptr(), v_new.data_ptr(),
+                                      k_cache.data_ptr(), v_cache.data_ptr(), ctypes.byref(layout),
+                                      st.data_ptr(), batch, n_new, _stream_handle(k_new.device))
+    check(status, "gqa_kv_append_bf16")
+
+
 def validate_lengths(seq_len, query_position, capacity: int) -> None:
     """Host check of lengths (raises GqaConfigError), gen_gqa_wrapper_vectors.py:73-78."""
     sl = torch.as_tensor(seq_len, dtype=torch.int32).reshape(-1).contiguous()
@@ -237,12 +340,13 @@ def validate_lengths(seq_len, query_position, capacity: int) -> None:
 
 
 def profile_enable(max_calls: int) -> None:
-    """Start recording kernel times of up to max_calls decode calls (0 stops)."""
+    """Start recording kernel times of up to max_calls decode or prefill calls (0 stops)."""
     check(lib().gqa_profile_enable(int(max_calls)), "gqa_profile_enable")
 
 
 def profile_read():
-    """-> (split_ms_total, combine_ms_total, calls) recorded since the last read."""
+    """-> (first_kernel_ms_total, second_kernel_ms_total, calls) recorded since the last
+    read: decode calls {stream, merge}, prefill calls {KV append, attention}."""
     p = _lib.GqaProfile()
     check(lib().gqa_profile_read(ctypes.byref(p)), "gqa_profile_read")
-    return p.split_ms, p.combine_ms, p.calls
+    return p.kernel_ms[0], p.kernel_ms[1], p.calls

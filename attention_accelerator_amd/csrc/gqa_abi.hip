@@ -231,8 +231,8 @@ int gqa_profile_read(gqa_profile_t* out) {
         split += a;
         combine += b;
     }
-    out->split_ms = split;
-    out->combine_ms = combine;
+    out->kernel_ms[0] = split;
+    out->kernel_ms[1] = combine;
     out->calls = p.used;
     p.used = 0;
     return GQA_OK;
@@ -269,6 +269,86 @@ int gqa_rope_rows_bf16(const uint16_t* in, uint16_t* out, int64_t n_rows, int64_
     a.pos0 = pos0;
     fill_rope_table(theta, &a.rope);
     const hipError_t e = launch_rope_rows(a, static_cast<hipStream_t>(stream));
+    return e == hipSuccess ? GQA_OK : GQA_ERR_HIP;
+}
+
+}  // extern "C"
+
+namespace {
+
+// Checks shared by the prefill and append entry points; fills the argument block.
+int prefill_args(const gqa_params_t* params, const uint16_t* k_new, const uint16_t* v_new,
+                 uint16_t* k_cache, uint16_t* v_cache, const gqa_kv_layout_t* kv, const int32_t* start,
+                 int32_t batch, int32_t n_new, PrefillArgs& a) {
+    if (!params || !kv) return GQA_ERR_BAD_POINTER;
+    if (!geometry_ok(params)) return GQA_ERR_INVALID_CONFIG;
+    if (batch <= 0 || n_new <= 0 || kv->capacity < n_new) return GQA_ERR_INVALID_CONFIG;
+    if (kv->pos_stride < kD || kv->head_stride < 0 || kv->batch_stride < 0) return GQA_ERR_INVALID_CONFIG;
+    if (!k_new || !v_new || !k_cache || !v_cache || !start) return GQA_ERR_BAD_POINTER;
+    if (!aligned(k_new, 2) || !aligned(v_new, 2) || !aligned(k_cache, 16) || !aligned(v_cache, 16) ||
+        !aligned(start, 4))
+        return GQA_ERR_BAD_POINTER;
+    if (kv->pos_stride % 8 || kv->head_stride % 8 || kv->batch_stride % 8) return GQA_ERR_BAD_POINTER;
+    a = PrefillArgs{};
+    a.k_new = k_new;
+    a.v_new = v_new;
+    a.k = k_cache;
+    a.v = v_cache;
+    a.start = start;
+    a.kv_batch_stride = kv->batch_stride;
+    a.kv_head_stride = kv->head_stride;
+    a.kv_pos_stride = kv->pos_stride;
+    a.capacity = kv->capacity;
+    a.batch = batch;
+    a.n_new = n_new;
+    a.n_qblk = (n_new + 31) / 32;
+    a.qk_scale_log2 = static_cast<double>(params->scale) * 1.4426950408889634;
+    a.flags = params->flags;
+    fill_rope_table(params->rope_theta, &a.rope);
+    return GQA_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+size_t gqa_prefill_workspace_bytes(const gqa_params_t* params, int32_t batch, int32_t n_new) {
+    if (!params || !geometry_ok(params) || batch <= 0 || n_new <= 0) return 0;
+    return align_up(prefill_split_bytes(batch, n_new), 256);
+}
+
+int gqa_kv_append_bf16(const gqa_params_t* params, const uint16_t* k_new, const uint16_t* v_new,
+                       uint16_t* k_cache, uint16_t* v_cache, const gqa_kv_layout_t* kv,
+                       const int32_t* start, int32_t batch, int32_t n_new, void* stream) {
+    PrefillArgs a;
+    const int st = prefill_args(params, k_new, v_new, k_cache, v_cache, kv, start, batch, n_new, a);
+    if (st != GQA_OK) return st;
+    a.k_split = nullptr;
+    const hipError_t e = launch_kv_append(a, static_cast<hipStream_t>(stream));
+    return e == hipSuccess ? GQA_OK : GQA_ERR_HIP;
+}
+
+int gqa_prefill_bf16(const gqa_params_t* params, const uint16_t* q, const uint16_t* k_new,
+                     const uint16_t* v_new, uint16_t* k_cache, uint16_t* v_cache,
+                     const gqa_kv_layout_t* kv, const int32_t* start, int32_t batch, int32_t n_new,
+                     uint16_t* out, void* workspace, size_t workspace_bytes, void* stream) {
+    PrefillArgs a;
+    const int st = prefill_args(params, k_new, v_new, k_cache, v_cache, kv, start, batch, n_new, a);
+    if (st != GQA_OK) return st;
+    if (!q || !out) return GQA_ERR_BAD_POINTER;
+    if (!aligned(q, 2) || !aligned(out, 8)) return GQA_ERR_BAD_POINTER;
+    const size_t need = gqa_prefill_workspace_bytes(params, batch, n_new);
+    if (!workspace || workspace_bytes < need || !aligned(workspace, 256)) return GQA_ERR_WORKSPACE;
+    a.q = q;
+    a.out = out;
+    a.k_split = static_cast<uint16_t*>(workspace);
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    hipEvent_t* ev = profile_slot();
+    if (ev) (void)hipEventRecord(ev[0], s);
+    hipError_t e = launch_kv_append(a, s);
+    if (ev) (void)hipEventRecord(ev[1], s);
+    if (e == hipSuccess) e = launch_prefill_attention(a, s);
+    if (ev) (void)hipEventRecord(ev[2], s);
     return e == hipSuccess ? GQA_OK : GQA_ERR_HIP;
 }
 

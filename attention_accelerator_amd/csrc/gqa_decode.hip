@@ -52,9 +52,6 @@
 
 namespace gqa {
 
-typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
-typedef float f32x4_t __attribute__((ext_vector_type(4)));
-
 constexpr int kChunk = 16;           // keys per MFMA group
 constexpr int kMinRangeKeys = 64;    // smallest per-workgroup key range
 
@@ -92,51 +89,6 @@ __device__ __forceinline__ void stream_totals(const DecodeArgs& a, int lane, int
     int64_t per = (total + a.n_wgs - 1) / a.n_wgs;
     per = per < kMinRangeKeys ? kMinRangeKeys : per;
     per_wg = (per + kChunk - 1) / kChunk * kChunk;
-}
-
-// BF16 code of a double, rounding through f32 (any nearby BF16 value serves as the
-// leading part of a split; the residual is formed exactly in double).
-__device__ __forceinline__ uint16_t bf16_of(double d) { return f32_to_bf16_rne(static_cast<float>(d)); }
-
-__device__ __forceinline__ double f64_of_bf16(uint16_t b) { return static_cast<double>(bf16_to_f32(b)); }
-
-// Split v into hi + mid + lo BF16 codes; returns part `which`.
-__device__ __forceinline__ uint16_t split3(double v, int which) {
-    const uint16_t hi = bf16_of(v);
-    const double r1 = v - f64_of_bf16(hi);
-    const uint16_t mid = bf16_of(r1);
-    if (which == 0) return hi;
-    if (which == 1) return mid;
-    return bf16_of(r1 - f64_of_bf16(mid));
-}
-
-__device__ __forceinline__ bf16x8_t pack8(const uint16_t (&h)[8]) {
-    union {
-        uint16_t u[8];
-        bf16x8_t v;
-    } t;
-#pragma unroll
-    for (int j = 0; j < 8; ++j) t.u[j] = h[j];
-    return t.v;
-}
-
-__device__ __forceinline__ bf16x8_t as_bf16x8(const uint4& w) {
-    union {
-        uint4 u;
-        bf16x8_t v;
-    } t;
-    t.u = w;
-    return t.v;
-}
-
-// 16-byte load with the nontemporal hint (global_load_dwordx4 ... nt).  Every K/V row
-// is read exactly once per step, so the rows should not displace anything in L2 or
-// the Infinity Cache; on MI355X the hint raised the stream kernel from 5.5 to 6.1 TB/s
-// on the B=64 ragged batch.
-typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
-__device__ __forceinline__ uint4 load_stream16(const char* p) {
-    const u32x4_t v = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(p));
-    return make_uint4(v.x, v.y, v.z, v.w);
 }
 
 // K and V rows of one 16-key chunk, in the MFMA (K) and PV (V) lane layouts.

@@ -65,4 +65,33 @@ hipError_t launch_rope_rows(const RopeArgs& a, hipStream_t stream);
 
 void fill_rope_table(double theta, RopeTable* t);
 
+// Chunked prefill: n_new query tokens per sequence appended after start[b] cached
+// positions (gqa_prefill.hip).
+struct PrefillArgs {
+    const uint16_t* q;        // [B][T][32][128]
+    const uint16_t* k_new;    // [B][T][8][128] new K rows as given (unrotated when RoPE on K)
+    const uint16_t* v_new;    // [B][T][8][128]
+    uint16_t* k;              // cache, rows at b*kv_batch_stride + h*kv_head_stride + p*kv_pos_stride
+    uint16_t* v;
+    const int32_t* start;     // [B] cached positions before the chunk (device)
+    uint16_t* out;            // [B][T][32][128]
+    uint16_t* k_split;        // [2][B][T][8][128] second and third BF16 parts of the rotated new K
+                              // (nullptr: append only, no split planes)
+    int64_t kv_batch_stride;
+    int64_t kv_head_stride;
+    int64_t kv_pos_stride;
+    int32_t capacity;
+    int32_t batch;
+    int32_t n_new;            // T
+    int32_t n_qblk;           // query blocks of 32 positions per sequence
+    double qk_scale_log2;     // scale * log2(e), folded into Q
+    uint32_t flags;           // bit0 RoPE on Q, bit1 RoPE on the new K rows
+    RopeTable rope;
+};
+
+size_t prefill_split_bytes(int32_t batch, int32_t n_new);
+hipError_t launch_kv_append(const PrefillArgs& a, hipStream_t stream);
+hipError_t launch_prefill_attention(const PrefillArgs& a, hipStream_t stream);
+
+
 }  // namespace gqa

@@ -1,0 +1,428 @@
+// gqa_prefill.hip -- chunked prefill (multi-query GQA) on MFMA for gfx950, and the KV
+// append with RoPE on insert.
+//
+// The reference core computes one query token per start (gqa_controller.v:140-277;
+// golden pyfiles/gen_gqa_wrapper_vectors.py:121-139).  A prefill chunk is that step for
+// T consecutive tokens of a sequence: token t sits at position start+t and attends to
+// keys p <= start+t (the causal half of gqa_attention_wrapper.v:279), where keys
+// p < start are cache rows as stored (post-RoPE) and keys start..start+T-1 are the
+// chunk's own K/V rows, rotated at their positions in double and not re-rounded, as
+// the golden rotates K (gen_gqa_wrapper_vectors.py:124-126).
+//
+// kv_append_kernel writes the chunk's K rows (rotated, rounded double -> f32 -> BF16,
+// pyfiles/gqa_reference.py:15-19) and V rows into the cache, and the second and third
+// BF16 parts of each rotated K row into the workspace, so that the cache row plus
+// those two parts carry the rotated value to ~24 bits.
+//
+// prefill_attn_kernel: one workgroup of 8 waves per (sequence, KV head, 32 query
+// positions); wave w computes Q head 4*kv_head + (w & 3) for 16 positions.  The K/V
+// rows of each 64-key block are loaded once per workgroup into LDS and used by all 4
+// heads of the group and all 32 positions (gqa_kv_broadcast.v:38-59 at block scale).
+//
+//  * Scores S^T = K Q^T with v_mfma_f32_16x16x32_bf16: A = 16 keys x 32 dims of K from
+//    LDS (row = key), B = Q^T (column = query) held in registers.  Q is rotated and
+//    scaled by scale*log2(e) in double and split into three BF16 parts, so the exact
+//    bf16 x bf16 products carry ~24 bits of Q; for blocks with chunk keys the second and
+//    third parts of K add the (k2,q1), (k2,q2), (k3,q1) products.  Lane (g, n) ends with
+//    the scores of keys 4g+i (i = 0..3) of each 16-key tile for query n.
+//  * Online softmax per query with an integer-valued running max (every rescale is an
+//    exact power of two), p = exp2(s - m) in fp32, masked keys p = 0 exactly.
+//  * O^T += V^T P^T with the same MFMA: A = 16 dims x 32 keys of V^T from LDS, B = P^T.
+//    The lane already holds P for keys {4g+i} of tiles 2w and 2w+1, which is its B
+//    operand for the 32-key window w if V^T stores each window's keys in that order
+//    (slot 8g+4h+i <-> key 16h+4g+i).  P is split into three BF16 parts (~24 bits).
+//    Each block's fp32 product is added to an fp64 accumulator, so accumulation over
+//    thousands of keys adds no fp32 rounding.
+//  * O / l, rounded double -> f32 -> BF16, written in Q-head order.
+#include "gqa_device.h"
+#include "gqa_internal.h"
+
+namespace gqa {
+
+namespace {
+
+constexpr int kPfPos = 32;                 // query positions per workgroup
+constexpr int kPfWaves = 8;                // 4 Q heads x 2 tiles of 16 positions
+constexpr int kPfThreads = kPfWaves * kWave;
+constexpr int kPfBlk = 64;                 // keys per K/V block
+constexpr int kKRow = 136;                 // LDS K row stride in BF16 (256 B + 16 B pad)
+constexpr int kVRow = 72;                  // LDS V^T row stride in BF16 (128 B + 16 B pad)
+constexpr int kKPlane = kPfBlk * kKRow;    // BF16 elements per LDS K plane
+
+constexpr uint32_t kPermLo = 0x05040100u;  // v_perm_b32: low halves of (b, a) -> a.lo | b.lo << 16
+constexpr uint32_t kPermHi = 0x07060302u;  // high halves
+
+}  // namespace
+
+size_t prefill_split_bytes(int32_t batch, int32_t n_new) {
+    return 2ull * static_cast<size_t>(batch) * static_cast<size_t>(n_new) * kHkv * kD * sizeof(uint16_t);
+}
+
+__device__ __forceinline__ bool prefill_start_ok(const PrefillArgs& a, int st) {
+    return st >= 0 && st <= a.capacity - a.n_new;
+}
+
+__device__ __forceinline__ int64_t cache_elem(const PrefillArgs& a, int b, int h, int64_t p) {
+    return static_cast<int64_t>(b) * a.kv_batch_stride + static_cast<int64_t>(h) * a.kv_head_stride +
+           p * a.kv_pos_stride;
+}
+
+// ---------------------------------------------------------------------------------
+// KV append: one wave per new (sequence, token, KV head) row; lane i rotates the pair
+// (i, i+64) at position start+t in double (pyfiles/gen_gqa_wrapper_vectors.py:25-35).
+__global__ __launch_bounds__(256) void kv_append_kernel(PrefillArgs a) {
+    const int64_t row = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & (kWave - 1);
+    const int64_t n_rows = static_cast<int64_t>(a.batch) * a.n_new * kHkv;
+    if (row >= n_rows) return;
+    const int kvh = static_cast<int>(row % kHkv);
+    const int64_t bt = row / kHkv;
+    const int t = static_cast<int>(bt % a.n_new);
+    const int b = static_cast<int>(bt / a.n_new);
+    const int st = a.start[b];
+    if (!prefill_start_ok(a, st)) return;
+    const int64_t pos = static_cast<int64_t>(st) + t;
+    const uint16_t* ksrc = a.k_new + row * kD;
+    const uint16_t* vsrc = a.v_new + row * kD;
+    const double x = bf16_to_f32(ksrc[lane]);
+    const double y = bf16_to_f32(ksrc[lane + kPairs]);
+    double xr = x, yr = y;
+    if (a.flags & 2u) rope_pair(x, y, pos, a.rope.inv_freq[lane], xr, yr);
+    const uint16_t hx = bf16_of(xr), hy = bf16_of(yr);
+    uint16_t* kdst = a.k + cache_elem(a, b, kvh, pos);
+    uint16_t* vdst = a.v + cache_elem(a, b, kvh, pos);
+    kdst[lane] = hx;
+    kdst[lane + kPairs] = hy;
+    vdst[lane] = vsrc[lane];
+    vdst[lane + kPairs] = vsrc[lane + kPairs];
+    if (a.k_split) {
+        const double rx = xr - f64_of_bf16(hx), ry = yr - f64_of_bf16(hy);
+        const uint16_t mx = bf16_of(rx), my = bf16_of(ry);
+        uint16_t* mid = a.k_split + row * kD;
+        uint16_t* lo = a.k_split + (n_rows + row) * kD;
+        mid[lane] = mx;
+        mid[lane + kPairs] = my;
+        lo[lane] = bf16_of(rx - f64_of_bf16(mx));
+        lo[lane + kPairs] = bf16_of(ry - f64_of_bf16(my));
+    }
+}
+
+hipError_t launch_kv_append(const PrefillArgs& a, hipStream_t stream) {
+    const int64_t n_rows = static_cast<int64_t>(a.batch) * a.n_new * kHkv;
+    if (n_rows == 0) return hipSuccess;
+    hipLaunchKernelGGL(kv_append_kernel, dim3(static_cast<unsigned>((n_rows + 3) / 4)), dim3(256), 0,
+                       stream, a);
+    return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------------
+// Attention.
+
+// Registers staging one K/V block on its way to LDS.  Threads 0..255 hold a quad of
+// V rows (keys 4q..4q+3, dims 8c..8c+7); threads 256..511 a 64-byte segment of a K
+// row (plane 0, the cache row).  `s` holds a 64-byte segment of a K row of plane 1
+// (threads 0..255) or plane 2 (256..511): the second or third BF16 part of a chunk
+// key, zero for cached keys.
+struct PfStage {
+    uint4 a[4];
+    uint4 s[4];
+    bool s_zero;
+};
+
+__device__ __forceinline__ void pf_load_block(const PrefillArgs& a, int b, int kvh, int st, int blk,
+                                              int n_keys, PfStage& sg) {
+    const int tid = threadIdx.x;
+    const int half = tid >> 8;
+    const int t = tid & 255;
+    const int key0 = blk * kPfBlk;
+    const int key_last = n_keys - 1;
+    const int64_t head_elem = static_cast<int64_t>(b) * a.kv_batch_stride +
+                              static_cast<int64_t>(kvh) * a.kv_head_stride;
+    // Plane 0 / V: addresses formed for both roles, one selected (no branch).
+    const int r = t >> 2, seg = t & 3;        // K row segment
+    const int qd = t >> 4, c = t & 15;        // V quad, dim chunk
+    const char* kbase = reinterpret_cast<const char*>(a.k + head_elem);
+    const char* vbase = reinterpret_cast<const char*>(a.v + head_elem);
+    const int64_t row_bytes = a.kv_pos_stride * 2;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int kk = half ? key0 + r : key0 + 4 * qd + i;
+        const int64_t off = static_cast<int64_t>(min(kk, key_last)) * row_bytes + (half ? 64 * seg + 16 * i : 16 * c);
+        sg.a[i] = *reinterpret_cast<const uint4*>((half ? kbase : vbase) + off);
+    }
+    // Planes 1 and 2 of chunk keys (u = key - start in [0, T)).
+    const int u = key0 + r - st;
+    sg.s_zero = u < 0;
+    const int uc = min(max(u, 0), a.n_new - 1);
+    const int64_t n_rows = static_cast<int64_t>(a.batch) * a.n_new * kHkv;
+    const char* pbase = reinterpret_cast<const char*>(
+        a.k_split + (static_cast<int64_t>(half) * n_rows + (static_cast<int64_t>(b) * a.n_new + uc) * kHkv + kvh) * kD);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) sg.s[i] = *reinterpret_cast<const uint4*>(pbase + 64 * seg + 16 * i);
+}
+
+__device__ __forceinline__ void pf_store_block(uint16_t* k_lds, uint16_t* v_lds, const PfStage& sg) {
+    const int tid = threadIdx.x;
+    const int half = tid >> 8;
+    const int t = tid & 255;
+    const int r = t >> 2, seg = t & 3;
+    if (half) {
+        uint4* dst = reinterpret_cast<uint4*>(k_lds + r * kKRow + 32 * seg);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) dst[i] = sg.a[i];
+    } else {
+        // V quad -> V^T: keys 4q..4q+3 share (window w, h, g), slots 32w + 8g + 4h + i.
+        const int qd = t >> 4, c = t & 15;
+        const int slot = 32 * (qd >> 3) + 8 * (qd & 3) + 4 * ((qd >> 2) & 1);
+        const uint32_t* k0 = reinterpret_cast<const uint32_t*>(&sg.a[0]);
+        const uint32_t* k1 = reinterpret_cast<const uint32_t*>(&sg.a[1]);
+        const uint32_t* k2 = reinterpret_cast<const uint32_t*>(&sg.a[2]);
+        const uint32_t* k3 = reinterpret_cast<const uint32_t*>(&sg.a[3]);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const uint32_t sel = (e & 1) ? kPermHi : kPermLo;
+            uint2 w;
+            w.x = __builtin_amdgcn_perm(k1[e >> 1], k0[e >> 1], sel);
+            w.y = __builtin_amdgcn_perm(k3[e >> 1], k2[e >> 1], sel);
+            *reinterpret_cast<uint2*>(v_lds + (8 * c + e) * kVRow + slot) = w;
+        }
+    }
+    uint4* pdst = reinterpret_cast<uint4*>(k_lds + (1 + half) * kKPlane + r * kKRow + 32 * seg);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) pdst[i] = sg.s_zero ? make_uint4(0, 0, 0, 0) : sg.s[i];
+}
+
+// Upper 16 bits of two floats packed as BF16 codes (truncation; used for exact splits).
+__device__ __forceinline__ uint32_t pack_hi16(float lo, float hi) {
+    return __builtin_amdgcn_perm(__float_as_uint(hi), __float_as_uint(lo), kPermHi);
+}
+
+__global__ __launch_bounds__(kPfThreads) void prefill_attn_kernel(PrefillArgs a) {
+    __shared__ __attribute__((aligned(16))) uint16_t k_lds[3 * kKPlane];
+    __shared__ __attribute__((aligned(16))) uint16_t v_lds[kD * kVRow];
+
+    // Workgroup -> (sequence, KV head, query block).  Workgroups are dealt to the 8 XCDs
+    // round-robin; when the (sequence, KV head) pairs divide evenly, all query blocks of
+    // a pair go to one XCD so that its K/V blocks are shared in that XCD's L2.
+    const int n_pairs = a.batch * kHkv;
+    const int id = blockIdx.x;
+    int pair, qb;
+    if (n_pairs % 8 == 0) {
+        const int k = id >> 3;
+        qb = k % a.n_qblk;
+        pair = (k / a.n_qblk) * 8 + (id & 7);
+    } else {
+        pair = id / a.n_qblk;
+        qb = id % a.n_qblk;
+    }
+    const int b = pair / kHkv;
+    const int kvh = pair % kHkv;
+    const int tid = threadIdx.x;
+    const int wave = tid >> 6;
+    const int lane = tid & (kWave - 1);
+    const int n = lane & 15;
+    const int g = lane >> 4;
+    const int hq = kvh * kGroup + (wave & 3);
+    const int pt = wave >> 2;
+    const int T = a.n_new;
+    const int t_wave0 = qb * kPfPos + pt * 16;
+    const int tq = t_wave0 + n;
+    const bool q_ok = tq < T;
+    const int st = a.start[b];
+
+    if (!prefill_start_ok(a, st)) {
+        if (q_ok && g == 0) {
+            uint4* o = reinterpret_cast<uint4*>(a.out + ((static_cast<int64_t>(b) * T + tq) * kHq + hq) * kD);
+            for (int i = 0; i < kD / 8; ++i) o[i] = make_uint4(0x7fc07fc0u, 0x7fc07fc0u, 0x7fc07fc0u, 0x7fc07fc0u);
+        }
+        return;
+    }
+
+    const int tq_c = min(tq, T - 1);
+    const int pos_n = st + tq_c;            // this lane's query position
+    const bool wave_has_q = t_wave0 < T;
+    const int n_keys = st + min(T, qb * kPfPos + kPfPos);
+    const int n_keys_wave = st + min(T, t_wave0 + 16);
+    const int n_blk = (n_keys + kPfBlk - 1) / kPfBlk;
+
+    // First block's rows are requested before the Q operands are formed.
+    PfStage sg;
+    pf_load_block(a, b, kvh, st, 0, n_keys, sg);
+
+    // Q operands: query n = this lane's column, dims 32kb + 8g + j, three BF16 parts.
+    bf16x8_t qop[3][4];
+    {
+        const uint16_t* qrow = a.q + ((static_cast<int64_t>(b) * T + tq_c) * kHq + hq) * kD;
+        double qv[4][8];
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb) {
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const int d = 32 * kb + 8 * g + j;
+                const double x = bf16_to_f32(qrow[d]);
+                const double y = bf16_to_f32(qrow[d + kPairs]);
+                double xr = x, yr = y;
+                if (a.flags & 1u) rope_pair(x, y, pos_n, a.rope.inv_freq[d], xr, yr);
+                qv[kb][j] = xr * a.qk_scale_log2;
+                qv[kb + 2][j] = yr * a.qk_scale_log2;
+            }
+        }
+#pragma unroll
+        for (int s = 0; s < 3; ++s)
+#pragma unroll
+            for (int kb = 0; kb < 4; ++kb) {
+                uint16_t h8[8];
+#pragma unroll
+                for (int j = 0; j < 8; ++j) h8[j] = split3(qv[kb][j], s);
+                qop[s][kb] = pack8(h8);
+            }
+    }
+
+    double o64[8][4];
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) o64[dt][i] = 0.0;
+    double l64 = 0.0;
+    float m_run = -INFINITY;
+
+    for (int blk = 0; blk < n_blk; ++blk) {
+        __syncthreads();                       // every wave is done with the previous block
+        pf_store_block(k_lds, v_lds, sg);
+        __syncthreads();
+        // Next block's rows (the last block is requested again at the end: the load stays
+        // unconditional, so the compiler never waits for it before the math below).
+        pf_load_block(a, b, kvh, st, min(blk + 1, n_blk - 1), n_keys, sg);
+
+        const int key0 = blk * kPfBlk;
+        if (!wave_has_q || key0 >= n_keys_wave) continue;
+        const bool has_new = key0 + kPfBlk - 1 >= st;
+
+        // ---- scores S^T[key][query] for the 4 key tiles of the block.
+        f32x4_t sacc[4];
+#pragma unroll
+        for (int kt = 0; kt < 4; ++kt) sacc[kt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int kb = 0; kb < 4; ++kb) {
+            bf16x8_t ak[4];
+#pragma unroll
+            for (int kt = 0; kt < 4; ++kt)
+                ak[kt] = *reinterpret_cast<const bf16x8_t*>(k_lds + (16 * kt + n) * kKRow + 32 * kb + 8 * g);
+#pragma unroll
+            for (int s = 0; s < 3; ++s)
+#pragma unroll
+                for (int kt = 0; kt < 4; ++kt)
+                    sacc[kt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ak[kt], qop[s][kb], sacc[kt], 0, 0, 0);
+            if (has_new) {
+#pragma unroll
+                for (int kt = 0; kt < 4; ++kt)
+                    ak[kt] = *reinterpret_cast<const bf16x8_t*>(k_lds + kKPlane + (16 * kt + n) * kKRow + 32 * kb + 8 * g);
+#pragma unroll
+                for (int s = 0; s < 2; ++s)
+#pragma unroll
+                    for (int kt = 0; kt < 4; ++kt)
+                        sacc[kt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ak[kt], qop[s][kb], sacc[kt], 0, 0, 0);
+#pragma unroll
+                for (int kt = 0; kt < 4; ++kt)
+                    ak[kt] = *reinterpret_cast<const bf16x8_t*>(k_lds + 2 * kKPlane + (16 * kt + n) * kKRow + 32 * kb + 8 * g);
+#pragma unroll
+                for (int kt = 0; kt < 4; ++kt)
+                    sacc[kt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ak[kt], qop[0][kb], sacc[kt], 0, 0, 0);
+            }
+        }
+
+        // ---- online softmax for query n over keys key0 + 16kt + 4g + i.
+        float sv[4][4];
+        float bmax = -INFINITY;
+        const bool need_mask = key0 + kPfBlk - 1 > st + t_wave0;
+#pragma unroll
+        for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                float x = sacc[kt][i];
+                if (need_mask && key0 + 16 * kt + 4 * g + i > pos_n) x = -INFINITY;
+                sv[kt][i] = x;
+                bmax = fmaxf(bmax, x);
+            }
+        bmax = fmaxf(bmax, __shfl_xor(bmax, 16));
+        bmax = fmaxf(bmax, __shfl_xor(bmax, 32));
+        const bool grow = bmax > m_run;
+        if (__ballot(grow)) {
+            const float m_new = grow ? ceilf(bmax) : m_run;
+            const int shift = (m_run == -INFINITY) ? 0 : static_cast<int>(m_run - m_new);
+#pragma unroll
+            for (int dt = 0; dt < 8; ++dt)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) o64[dt][i] = ldexp(o64[dt][i], shift);
+            l64 = ldexp(l64, shift);
+            m_run = m_new;
+        }
+        float lsum = 0.f;
+        uint32_t ph[3][2][4];   // [part][window][dword]: BF16 pairs of P^T, B-operand order
+#pragma unroll
+        for (int kt = 0; kt < 4; ++kt) {
+            float p[4], r1[4], r2[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                p[i] = exp2f(sv[kt][i] - m_run);
+                lsum += p[i];
+                r1[i] = p[i] - __uint_as_float(__float_as_uint(p[i]) & 0xffff0000u);
+                r2[i] = r1[i] - __uint_as_float(__float_as_uint(r1[i]) & 0xffff0000u);
+            }
+            const int w = kt >> 1, d0 = (kt & 1) * 2;
+            ph[0][w][d0] = pack_hi16(p[0], p[1]);
+            ph[0][w][d0 + 1] = pack_hi16(p[2], p[3]);
+            ph[1][w][d0] = pack_hi16(r1[0], r1[1]);
+            ph[1][w][d0 + 1] = pack_hi16(r1[2], r1[3]);
+            ph[2][w][d0] = pack_hi16(r2[0], r2[1]);
+            ph[2][w][d0 + 1] = pack_hi16(r2[2], r2[3]);
+        }
+        l64 += static_cast<double>(lsum);
+
+        // ---- O^T[dim][query] += V^T P^T, fp32 per block, then into fp64.
+        f32x4_t oacc[8];
+#pragma unroll
+        for (int dt = 0; dt < 8; ++dt) oacc[dt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int w = 0; w < 2; ++w) {
+            bf16x8_t pb[3];
+#pragma unroll
+            for (int s = 0; s < 3; ++s)
+                pb[s] = as_bf16x8(make_uint4(ph[s][w][0], ph[s][w][1], ph[s][w][2], ph[s][w][3]));
+#pragma unroll
+            for (int dt = 0; dt < 8; ++dt) {
+                const bf16x8_t av = *reinterpret_cast<const bf16x8_t*>(v_lds + (16 * dt + n) * kVRow + 32 * w + 8 * g);
+#pragma unroll
+                for (int s = 0; s < 3; ++s)
+                    oacc[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, pb[s], oacc[dt], 0, 0, 0);
+            }
+        }
+#pragma unroll
+        for (int dt = 0; dt < 8; ++dt)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) o64[dt][i] += static_cast<double>(oacc[dt][i]);
+    }
+
+    if (!q_ok) return;
+    double l = l64 + __shfl_xor(l64, 16);
+    l += __shfl_xor(l, 32);
+    uint16_t* orow = a.out + ((static_cast<int64_t>(b) * T + tq) * kHq + hq) * kD;
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt) {
+        uint2 pk;
+        pk.x = f32_to_bf16_rne(static_cast<float>(o64[dt][0] / l)) |
+               (static_cast<uint32_t>(f32_to_bf16_rne(static_cast<float>(o64[dt][1] / l))) << 16);
+        pk.y = f32_to_bf16_rne(static_cast<float>(o64[dt][2] / l)) |
+               (static_cast<uint32_t>(f32_to_bf16_rne(static_cast<float>(o64[dt][3] / l))) << 16);
+        *reinterpret_cast<uint2*>(orow + 16 * dt + 4 * g) = pk;
+    }
+}
+
+hipError_t launch_prefill_attention(const PrefillArgs& a, hipStream_t stream) {
+    const int64_t n_wg = static_cast<int64_t>(a.batch) * kHkv * a.n_qblk;
+    if (n_wg == 0) return hipSuccess;
+    hipLaunchKernelGGL(prefill_attn_kernel, dim3(static_cast<unsigned>(n_wg)), dim3(kPfThreads), 0, stream, a);
+    return hipGetLastError();
+}
+
+}  // namespace gqa

@@ -12,6 +12,12 @@ Prints one JSON line: value = algorithmic HBM bytes of the step / time per step
 (the stream kernel), timed with HIP events around each of its launches in a second
 region of K steps, and the CPU baseline (the compiled oracle on a bounded sample of
 the same batch, 1 core).
+
+--workload prefill_b4_512_over_8192 times the chunked prefill instead: B=4, 512 new
+tokens per sequence after an 8192-token post-RoPE cache, RoPE on Q and the new K
+(one step = one gqa_prefill_bf16 call: KV append + attention), with a 512 MiB write
+between steps so that no step finds the 142 MB of K/V in the Infinity Cache.  value =
+algorithmic flops / time per step (TFLOP/s) and the roofline is MFMA (BF16 dense peak).
 """
 from __future__ import annotations
 
@@ -33,6 +39,11 @@ WORKLOADS = {
     "decode_b1_4096": (1, 4096, None, None),
     "decode_b8_131072": (8, 131072, None, None),
 }
+PREFILL_WORKLOADS = {
+    # name: (batch, new tokens, cached positions)
+    "prefill_b4_512_over_8192": (4, 512, 8192),
+}
+MFMA_BF16_PEAK_TFLOPS = 2500.0
 TRAFFIC_FILE = ROOT / "profiles" / "decode_stream_b64_ragged_traffic.txt"
 
 
@@ -78,13 +89,129 @@ def cpu_baseline(batch, budget_s: float = 12.0):
                        f"{t_total:.2f} s; os.cpu_count()={os.cpu_count()}, "
                        f"affinity={len(os.sched_getaffinity(0))}")}
 
+def prefill_flops(batch: int, n_new: int, start: int) -> int:
+    """QK^T and PV multiply-adds of a chunk, 2 flops each: token t sees start+t+1 keys."""
+    keys = n_new * start + n_new * (n_new + 1) // 2
+    return batch * 32 * keys * 128 * 4
+
+
+def prefill_cpu_baseline(q, kn, vn, k, v, starts, budget_s: float = 12.0):
+    """The compiled oracle (double, 1 thread) on the first rows of sequence 0."""
+    import numpy as np
+
+    from oracle import oracle as orc
+
+    def codes(t):
+        return t.contiguous().view(__import__("torch").int16).cpu().numpy().view(np.uint16)
+
+    s0 = int(starts[0])
+    qc, knc, vnc = codes(q[:1]), codes(kn[:1]), codes(vn[:1])
+    kc, vc = codes(k[:1, :, :s0]), codes(v[:1, :, :s0])
+    rows, t_total, step = [], 0.0, 8
+    while t_total < budget_s and len(rows) < q.shape[1]:
+        batch_rows = list(range(len(rows), min(len(rows) + step, q.shape[1])))
+        t0 = time.perf_counter()
+        orc.prefill(qc, kc, vc, knc, vnc, np.asarray([s0]), rows=batch_rows)
+        t_total += time.perf_counter() - t0
+        rows += batch_rows
+    flops = sum(32 * (s0 + t + 1) * 128 * 4 for t in rows)
+    return {"value": round(flops / t_total / 1e12, 6), "unit": "TFLOP/s", "cores": 1, "kind": "port",
+            "sample": (f"tokens 0..{rows[-1]} of sequence 0 ({len(rows)} of {q.shape[1]} tokens, all "
+                       f"32 heads, {s0} cached keys), compiled oracle in double, {t_total:.2f} s; "
+                       f"os.cpu_count()={os.cpu_count()}, affinity={len(os.sched_getaffinity(0))}")}
+
+
+def bench_prefill(args, torch, gqa, dev) -> int:
+    bsz, n_new, start = PREFILL_WORKLOADS[args.workload]
+    cap = start + n_new
+    g = torch.Generator("cuda").manual_seed(args.seed)
+    q = torch.randn((bsz, n_new, 32, 128), generator=g, device=dev).to(torch.bfloat16)
+    kn = torch.randn((bsz, n_new, 8, 128), generator=g, device=dev).to(torch.bfloat16)
+    vn = torch.randn((bsz, n_new, 8, 128), generator=g, device=dev).to(torch.bfloat16)
+    k = torch.full((bsz, 8, cap, 128), float("nan"), dtype=torch.bfloat16, device=dev)
+    v = torch.full_like(k, float("nan"))
+    k[:, :, :start] = torch.randn((bsz, 8, start, 128), generator=g, device=dev).to(torch.bfloat16)
+    v[:, :, :start] = torch.randn((bsz, 8, start, 128), generator=g, device=dev).to(torch.bfloat16)
+    k_host, v_host = (k.cpu(), v.cpu()) if not args.no_cpu_baseline else (None, None)
+    starts = torch.full((bsz,), start, dtype=torch.int32, device=dev)
+    ws = torch.empty(gqa.prefill_workspace_bytes(bsz, n_new), dtype=torch.uint8, device=dev)
+    out = torch.empty_like(q)
+    flush = torch.empty(512 << 20, dtype=torch.uint8, device=dev)
+    flops = prefill_flops(bsz, n_new, start)
+    print(f"[bench] {args.workload}: B={bsz} new={n_new} start={start} flops/step={flops}",
+          file=sys.stderr, flush=True)
+
+    def call():
+        gqa.gqa_prefill(q, kn, vn, k, v, starts, out=out, workspace=ws)
+
+    for _ in range(args.warmup):
+        call()
+    torch.cuda.synchronize()
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+           for _ in range(args.steps)]
+    for i in range(args.steps):
+        flush.fill_(i & 0xFF)                      # outside the timed pair of events
+        evs[i][0].record()
+        call()
+        evs[i][1].record()
+    torch.cuda.synchronize()
+    ms_per_step = sum(a.elapsed_time(b) for a, b in evs) / args.steps
+
+    attn_ms = append_ms = None
+    if not args.no_profile:
+        gqa.profile_enable(args.steps)
+        for i in range(args.steps):
+            flush.fill_(i & 0xFF)
+            call()
+        torch.cuda.synchronize()
+        ap_ms, at_ms, n = gqa.profile_read()
+        gqa.profile_enable(0)
+        append_ms, attn_ms = ap_ms / n, at_ms / n
+    print(f"[bench] {args.steps} steps: {ms_per_step * 1e3:.2f} us/step", file=sys.stderr, flush=True)
+
+    tflops = flops / (ms_per_step * 1e-3) / 1e12
+    roofline = None
+    if attn_ms:
+        achieved = flops / (attn_ms * 1e-3) / 1e12
+        roofline = {"bound": "mfma", "achieved": round(achieved, 2), "peak": MFMA_BF16_PEAK_TFLOPS,
+                    "unit": "TFLOP/s", "frac": round(achieved / MFMA_BF16_PEAK_TFLOPS, 4),
+                    "traffic": None, "kernel": "prefill_attn_kernel",
+                    "kernel_us": round(attn_ms * 1e3, 2), "append_us": round(append_ms * 1e3, 2),
+                    "flops_per_launch": flops}
+    result = {
+        "metric": "GQA chunked prefill µs/step + MFMA TFLOP/s, B=4 512 new over 8192 cached",
+        "value": round(tflops, 2),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 5),
+        "us_per_step": round(ms_per_step * 1e3, 2),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": f"synthetic N(0,1) BF16, seed {args.seed}",
+        "config": {"workload": args.workload, "batch": bsz, "new_tokens": n_new,
+                   "cached": start, "q_heads": 32, "kv_heads": 8, "head_dim": 128,
+                   "rope": "q and new k", "precision": "Q, new K and P in three BF16 parts, "
+                   "fp32 MFMA accumulation per 64-key block, fp64 across blocks",
+                   "flops_per_step": flops},
+        "roofline": roofline,
+        "cpu_baseline": None if args.no_cpu_baseline else prefill_cpu_baseline(
+            q, kn, vn, k_host, v_host, [start] * bsz),
+    }
+    print(json.dumps(result), flush=True)
+    return 0
+
 
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--workload", choices=sorted(WORKLOADS), default="decode_b64_ragged_512_8192")
+    ap.add_argument("--workload", choices=sorted(WORKLOADS) + sorted(PREFILL_WORKLOADS),
+                    default="decode_b64_ragged_512_8192")
     ap.add_argument("--seed", type=int, default=20260805)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-profile", action="store_true",
@@ -105,6 +232,8 @@ def main() -> int:
     from attention_accelerator_amd.attention import PreparedDecode, validate_lengths
 
     dev = torch.device("cuda", 0)
+    if args.workload in PREFILL_WORKLOADS:
+        return bench_prefill(args, torch, gqa, dev)
     bsz, cap, lo, hi = WORKLOADS[args.workload]
     batch = stimulus.decode_batch(bsz, cap, min_len=lo, max_len=hi, seed=args.seed,
                                   device=dev, gen_device="cuda")

@@ -122,6 +122,41 @@ int gqa_decode_bf16(const gqa_params_t* params, const uint16_t* q, const uint16_
                     const int32_t* query_pos, int32_t batch, uint16_t* out, void* workspace,
                     size_t workspace_bytes, void* stream);
 
+/* Chunked prefill: n_new query tokens per sequence, appended after start[b] cached
+ * positions (the reference core computes one token per start; a chunk is that step for
+ * tokens at positions start[b] .. start[b]+n_new-1 of one sequence,
+ * gen_gqa_wrapper_vectors.py:121-139 per token):
+ *   q          [batch][n_new][32][128]  Q rows of the chunk's tokens (unrotated; rotated at
+ *              their positions when GQA_ROPE_Q)
+ *   k_new, v_new [batch][n_new][8][128]  the chunk's K and V rows (K rotated at its
+ *              position when GQA_ROPE_K)
+ *   k_cache, v_cache  cache per `kv`; rows at positions < start[b] are read as stored
+ *              (post-RoPE); the call writes the chunk's rows at start[b] + t (K rotated
+ *              and rounded double -> f32 -> BF16, V as given) before it attends
+ *   start      [batch] int32, device; 0 <= start[b] <= capacity - n_new, else that
+ *              sequence's output rows are NaN and its cache is not written
+ *   out        [batch][n_new][32][128]
+ *   workspace  gqa_prefill_workspace_bytes bytes (any contents)
+ * Token t attends to keys p <= start[b] + t (gqa_attention_wrapper.v:279 per token), the
+ * chunk's own keys carried to ~24 bits (their rotated value is not re-rounded, as in the
+ * golden).  Replaces the reference's per-token start loop for a run of tokens. */
+size_t gqa_prefill_workspace_bytes(const gqa_params_t* params, int32_t batch, int32_t n_new);
+
+int gqa_prefill_bf16(const gqa_params_t* params, const uint16_t* q, const uint16_t* k_new,
+                     const uint16_t* v_new, uint16_t* k_cache, uint16_t* v_cache,
+                     const gqa_kv_layout_t* kv, const int32_t* start, int32_t batch, int32_t n_new,
+                     uint16_t* out, void* workspace, size_t workspace_bytes, void* stream);
+
+/* KV append with RoPE on insert: writes k_new / v_new ([batch][n_new][8][128]) into the
+ * cache at positions start[b] + t, K rotated at its position when GQA_ROPE_K and rounded
+ * double -> f32 -> BF16 (the rope_unit's role in gqa_attention_wrapper.v:302-308 for a
+ * cache kept post-RoPE; rounding pyfiles/gqa_reference.py:15-19).  Sequences with
+ * start[b] outside [0, capacity - n_new] are skipped.  The step before a decode call on a
+ * post-RoPE cache. */
+int gqa_kv_append_bf16(const gqa_params_t* params, const uint16_t* k_new, const uint16_t* v_new,
+                       uint16_t* k_cache, uint16_t* v_cache, const gqa_kv_layout_t* kv,
+                       const int32_t* start, int32_t batch, int32_t n_new, void* stream);
+
 /* rope_unit in isolation (rope_unit.v:38-330 as tests/tb_rope_unit.sv drives it;
  * golden pyfiles/gen_rope_test_vectors.py:16-20): out[r] = BF16(rope(in[r], position)),
  * position = positions[r] if positions != NULL (device int32) else pos0 + r.
@@ -129,17 +164,17 @@ int gqa_decode_bf16(const gqa_params_t* params, const uint16_t* q, const uint16_
 int gqa_rope_rows_bf16(const uint16_t* in, uint16_t* out, int64_t n_rows, int64_t row_stride,
                        const int32_t* positions, int32_t pos0, double theta, void* stream);
 
-/* Kernel timing for measurement harnesses.  While enabled, each decode call
- * brackets its stream kernel and its merge kernel with HIP events on the call's
- * stream (up to `max_calls` calls are recorded; later ones are not).
- * gqa_profile_read waits for the recorded events, returns the summed kernel
- * times and the number of calls recorded, and clears the record.  Not for the
- * hot path: enabling creates the events.  No reference counterpart (the
- * reference's timing is its simulator's cycle count). */
+/* Kernel timing for measurement harnesses.  While enabled, each decode or prefill
+ * call brackets its two kernels with HIP events on the call's stream (up to
+ * `max_calls` calls are recorded; later ones are not): decode {stream kernel, merge
+ * kernel}, prefill {KV append kernel, attention kernel}.  The Q-operand preparation
+ * kernel of a decode call runs before the first event.  gqa_profile_read waits for the
+ * recorded events, returns the summed kernel times and the number of calls recorded,
+ * and clears the record.  Not for the hot path: enabling creates the events.  No
+ * reference counterpart (the reference's timing is its simulator's cycle count). */
 typedef struct gqa_profile {
-    double split_ms;      /* summed duration of the stream (split-KV) kernel launches */
-    double combine_ms;    /* summed duration of the merge kernel launches */
-    int32_t calls;        /* decode calls recorded */
+    double kernel_ms[2];  /* summed durations of the call's first and second kernel */
+    int32_t calls;        /* calls recorded */
 } gqa_profile_t;
 
 int gqa_profile_enable(int32_t max_calls); /* max_calls <= 0 disables and frees */

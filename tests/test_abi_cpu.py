@@ -142,3 +142,53 @@ def test_workspace_init_rejects():
     assert L.gqa_decode_workspace_init(ctypes.byref(p), 4, 1000, 256, n - 1, None) == BAD_WS
     assert L.gqa_decode_workspace_init(ctypes.byref(p), 4, 1000, 260, n, None) == BAD_WS
     assert L.gqa_decode_workspace_init(None, 4, 1000, 256, n, None) == BAD_PTR
+
+
+def test_prefill_workspace_bytes():
+    L = _lib.lib()
+    p = _params(flags=3)
+    n = L.gqa_prefill_workspace_bytes(ctypes.byref(p), 4, 512)
+    assert n >= 2 * 4 * 512 * 8 * 128 * 2 and n % 256 == 0
+    assert L.gqa_prefill_workspace_bytes(ctypes.byref(_params(head_dim=64)), 4, 512) == 0
+    assert L.gqa_prefill_workspace_bytes(ctypes.byref(p), 4, 0) == 0
+
+
+def _prefill(p, *, q=256, kn=256, vn=256, k=256, v=256, layout=None, start=256, batch=1,
+             n_new=8, out=256, ws=256, ws_bytes=1 << 30):
+    L = _lib.lib()
+    layout = layout or GqaKvLayout(8 * 64 * 128, 64 * 128, 128, 64)
+    return L.gqa_prefill_bf16(ctypes.byref(p) if p is not None else None, q, kn, vn, k, v,
+                              ctypes.byref(layout), start, batch, n_new, out, ws, ws_bytes, None)
+
+
+@pytest.mark.parametrize("kw,want", [
+    (dict(p=_params(n_q_heads=31)), BAD_CFG),
+    (dict(p=_params(scale=0.0)), BAD_CFG),
+    (dict(p=_params(flags=3, rope_theta=-5.0)), BAD_CFG),
+    (dict(p=_params(), batch=0), BAD_CFG),
+    (dict(p=_params(), n_new=0), BAD_CFG),
+    (dict(p=_params(), n_new=65), BAD_CFG),                      # chunk longer than the cache
+    (dict(p=_params(), layout=GqaKvLayout(0, 0, 64, 64)), BAD_CFG),
+    (dict(p=None), BAD_PTR),
+    (dict(p=_params(), q=None), BAD_PTR),
+    (dict(p=_params(), kn=None), BAD_PTR),
+    (dict(p=_params(), start=None), BAD_PTR),
+    (dict(p=_params(), out=None), BAD_PTR),
+    (dict(p=_params(), k=264), BAD_PTR),
+    (dict(p=_params(), out=260), BAD_PTR),
+    (dict(p=_params(), ws=None), BAD_WS),
+    (dict(p=_params(), ws_bytes=16), BAD_WS),
+])
+def test_prefill_rejects_before_launch(kw, want):
+    assert _prefill(**kw) == want
+
+
+def test_kv_append_rejects_before_launch():
+    L = _lib.lib()
+    lay = GqaKvLayout(8 * 64 * 128, 64 * 128, 128, 64)
+    p = _params(flags=2)
+    assert L.gqa_kv_append_bf16(None, 256, 256, 256, 256, ctypes.byref(lay), 256, 1, 1, None) == BAD_PTR
+    assert L.gqa_kv_append_bf16(ctypes.byref(p), 256, 256, 256, 256, ctypes.byref(lay), 256, 0, 1, None) == BAD_CFG
+    assert L.gqa_kv_append_bf16(ctypes.byref(p), 256, 256, 256, 256, ctypes.byref(lay), 256, 1, 65, None) == BAD_CFG
+    assert L.gqa_kv_append_bf16(ctypes.byref(p), 256, None, 256, 256, ctypes.byref(lay), 256, 1, 1, None) == BAD_PTR
+    assert L.gqa_kv_append_bf16(ctypes.byref(p), 256, 256, 264, 256, ctypes.byref(lay), 256, 1, 1, None) == BAD_PTR

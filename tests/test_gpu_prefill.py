@@ -1,0 +1,179 @@
+"""Chunked prefill (MFMA path) and KV append parity against the compiled oracle
+(oracle/oracle.py prefill: the one-token golden of pyfiles/gen_gqa_wrapper_vectors.py:
+121-139 per new token, new K rotated at its position and not re-rounded).
+
+Tolerance: 64 BF16 ULP per element with the reference checker's tiny-value exemption
+(pyfiles/check_gqa_output.py:33-34,57-64).  Cache rows past the chunk hold NaN, so any
+read of one would poison the output."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import attention_accelerator_amd as gqa
+from oracle import oracle as orc
+from _util import assert_within_ulp, to_codes, to_dev
+
+pytestmark = pytest.mark.gpu
+
+
+def _bf16_rne(x64: np.ndarray) -> np.ndarray:
+    """double -> f32 (RNE) -> BF16 code (RNE): pyfiles/gqa_reference.py:15-19."""
+    u = np.asarray(x64, dtype=np.float64).astype(np.float32).view(np.uint32).astype(np.uint64)
+    return (((u + 0x7FFF + ((u >> 16) & 1)) >> 16) & 0xFFFF).astype(np.uint16)
+
+
+def _chunk(batch, n_new, capacity, start, seed, device="cpu"):
+    """N(0,1) BF16 inputs; cache rows < start random, rows >= start NaN."""
+    g = torch.Generator("cpu").manual_seed(seed)
+    q = torch.randn((batch, n_new, 32, 128), generator=g).to(torch.bfloat16)
+    k_new = torch.randn((batch, n_new, 8, 128), generator=g).to(torch.bfloat16)
+    v_new = torch.randn((batch, n_new, 8, 128), generator=g).to(torch.bfloat16)
+    k = torch.full((batch, 8, capacity, 128), float("nan"), dtype=torch.bfloat16)
+    v = torch.full((batch, 8, capacity, 128), float("nan"), dtype=torch.bfloat16)
+    for b in range(batch):
+        s = int(start[b])
+        k[b, :, :s] = torch.randn((8, s, 128), generator=g).to(torch.bfloat16)
+        v[b, :, :s] = torch.randn((8, s, 128), generator=g).to(torch.bfloat16)
+    return q, k_new, v_new, k, v
+
+
+def _oracle(q, k_new, v_new, k, v, start, rows=None, rope_q=True, rope_k=True):
+    return orc.prefill(to_codes(q), to_codes(k), to_codes(v), to_codes(k_new), to_codes(v_new),
+                       np.asarray(start), rope_q=rope_q, rope_k_new=rope_k, rows=rows)
+
+
+def _run(q, k_new, v_new, k, v, start, dev, **kw):
+    kd, vd = k.to(dev), v.to(dev)
+    out = gqa.gqa_prefill(q.to(dev), k_new.to(dev), v_new.to(dev), kd, vd, start, **kw)
+    torch.cuda.synchronize()
+    return to_codes(out), kd, vd
+
+
+@pytest.mark.parametrize("batch,n_new,starts,seed", [
+    (2, 40, [100, 37], 1),        # ragged query block (40 = 32 + 8), chunk straddling a K block
+    (1, 64, [0], 2),              # no cache: the chunk attends only to itself
+    (3, 17, [5, 64, 190], 3),     # short chunk, starts at and off block boundaries
+    (1, 1, [300], 4),             # one token: a decode step whose newest key is unrounded
+])
+def test_prefill_small_all_rows(dev, batch, n_new, starts, seed):
+    cap = max(starts) + n_new + 9
+    q, kn, vn, k, v = _chunk(batch, n_new, cap, starts, seed)
+    want = _oracle(q, kn, vn, k, v, starts)
+    got, kd, vd = _run(q, kn, vn, k, v, starts, dev)
+    assert_within_ulp(want.reshape(-1, 128), got.reshape(-1, 128), 64, f"prefill {batch}x{n_new}")
+    # the chunk's rows landed in the cache: K rotated and rounded, V as given
+    kc, vc = to_codes(kd), to_codes(vd)
+    for b, s in enumerate(starts):
+        for h in range(8):
+            rot = orc.prepare_rows(to_codes(kn[b, :, h]), True, s)
+            assert np.array_equal(kc[b, h, s:s + n_new], _bf16_rne(rot))
+            assert np.array_equal(vc[b, h, s:s + n_new], to_codes(vn[b, :, h]))
+        # rows past the chunk untouched (still NaN)
+        assert (kc[b, :, s + n_new:] == to_codes(k[b, :, s + n_new:])).all()
+
+
+def test_prefill_no_rope(dev):
+    starts = [70, 150]
+    q, kn, vn, k, v = _chunk(2, 33, 200, starts, 5)
+    want = _oracle(q, kn, vn, k, v, starts, rope_q=False, rope_k=False)
+    got, kd, _ = _run(q, kn, vn, k, v, starts, dev, rope_q=False, rope_k=False)
+    assert_within_ulp(want.reshape(-1, 128), got.reshape(-1, 128), 64, "prefill no rope")
+    assert np.array_equal(to_codes(kd)[0, 3, 70:103], to_codes(kn[0, :, 3]))
+
+
+def test_prefill_causal_independence(dev):
+    """Token t's output does not depend on chunk rows after t (masked keys contribute
+    exactly zero): perturbing rows t+1.. leaves rows 0..t bit-identical."""
+    starts = [200]
+    q, kn, vn, k, v = _chunk(1, 96, 300, starts, 6)
+    ref, _, _ = _run(q, kn, vn, k, v, starts, dev)
+    t = 45
+    kn2, vn2, q2 = kn.clone(), vn.clone(), q.clone()
+    kn2[:, t + 1:] = torch.randn(kn2[:, t + 1:].shape).to(torch.bfloat16) * 4
+    vn2[:, t + 1:] = torch.randn(vn2[:, t + 1:].shape).to(torch.bfloat16) * 4
+    q2[:, t + 1:] = 0
+    got, _, _ = _run(q2, kn2, vn2, k, v, starts, dev)
+    assert np.array_equal(got[:, :t + 1], ref[:, :t + 1])
+
+
+def test_prefill_deterministic_and_workspace_reuse(dev):
+    starts = [128, 0, 77]
+    q, kn, vn, k, v = _chunk(3, 50, 180, starts, 7)
+    a, _, _ = _run(q, kn, vn, k, v, starts, dev)
+    ws = torch.empty(gqa.prefill_workspace_bytes(3, 50), dtype=torch.uint8, device=dev)
+    ws.fill_(0xFF)
+    b, _, _ = _run(q, kn, vn, k, v, starts, dev, workspace=ws)
+    assert np.array_equal(a, b)
+
+
+def test_prefill_invalid_device_start_gives_nan_rows(dev):
+    starts = torch.tensor([40, 500], dtype=torch.int32)     # sequence 1: 500 + 20 > capacity
+    q, kn, vn, k, v = _chunk(2, 20, 100, [40, 0], 8)
+    kd, vd = k.to(dev), v.to(dev)
+    out = gqa.gqa_prefill(q.to(dev), kn.to(dev), vn.to(dev), kd, vd, starts.to(dev))
+    torch.cuda.synchronize()
+    got = to_codes(out)
+    assert (got[1] == 0x7FC0).all()
+    assert np.array_equal(to_codes(kd)[1], to_codes(k)[1])   # cache of sequence 1 untouched
+    want = _oracle(q[:1], kn[:1], vn[:1], k[:1], v[:1], [40])
+    assert_within_ulp(want.reshape(-1, 128), got[:1].reshape(-1, 128), 64, "valid next to invalid")
+
+
+def test_prefill_host_validation_rejects(dev):
+    q, kn, vn, k, v = _chunk(1, 10, 50, [0], 9)
+    kd, vd = k.to(dev), v.to(dev)
+    for st in ([-1], [41]):
+        with pytest.raises(gqa.GqaConfigError):
+            gqa.gqa_prefill(q.to(dev), kn.to(dev), vn.to(dev), kd, vd, st)
+
+
+def test_prefill_config5_sampled_rows(dev):
+    """B=4, 512 new tokens after an 8192-token post-RoPE cache (8704 keys for the last
+    token): rows 0, 1, 31, 32, 255, 256, 480 and 511 of every sequence against the oracle;
+    every output finite; a second call bit-identical."""
+    starts = [8192] * 4
+    g = torch.Generator("cuda").manual_seed(20260805)
+    shape_q, shape_n = (4, 512, 32, 128), (4, 512, 8, 128)
+    q = torch.randn(shape_q, generator=g, device=dev).to(torch.bfloat16)
+    kn = torch.randn(shape_n, generator=g, device=dev).to(torch.bfloat16)
+    vn = torch.randn(shape_n, generator=g, device=dev).to(torch.bfloat16)
+    k = torch.full((4, 8, 8704, 128), float("nan"), dtype=torch.bfloat16, device=dev)
+    v = torch.full_like(k, float("nan"))
+    k[:, :, :8192] = torch.randn((4, 8, 8192, 128), generator=g, device=dev).to(torch.bfloat16)
+    v[:, :, :8192] = torch.randn((4, 8, 8192, 128), generator=g, device=dev).to(torch.bfloat16)
+    k_host, v_host = k.cpu(), v.cpu()
+    out = gqa.gqa_prefill(q, kn, vn, k, v, starts)
+    out2 = gqa.gqa_prefill(q, kn, vn, k, v, starts)
+    got = to_codes(out)
+    assert np.array_equal(got, to_codes(out2))
+    assert np.isfinite(out.float().cpu().numpy()).all()
+    rows = [0, 1, 31, 32, 255, 256, 480, 511]
+    want = orc.prefill(to_codes(q), to_codes(k_host), to_codes(v_host), to_codes(kn), to_codes(vn),
+                       np.asarray(starts), rows=rows)
+    w = assert_within_ulp(want.reshape(-1, 128), got[:, rows].reshape(-1, 128), 64,
+                          "config 5 sampled rows")
+    print("worst ULP", w)
+
+
+def test_kv_append_then_decode(dev):
+    """Append one token per sequence with RoPE on insert, then decode over the grown
+    cache: equals the oracle on the cache the append wrote (a post-RoPE cache)."""
+    starts = [31, 500, 257]
+    cap = 520
+    q, kn, vn, k, v = _chunk(3, 1, cap, starts, 10)
+    kd, vd = k.to(dev), v.to(dev)
+    gqa.kv_append(kn.to(dev), vn.to(dev), kd, vd, starts)
+    torch.cuda.synchronize()
+    kc, vc = to_codes(kd), to_codes(vd)
+    for b, s in enumerate(starts):
+        for h in range(8):
+            rot = orc.prepare_rows(to_codes(kn[b, :, h]), True, s)
+            assert np.array_equal(kc[b, h, s:s + 1], _bf16_rne(rot))
+            assert np.array_equal(vc[b, h, s:s + 1], to_codes(vn[b, :, h]))
+    seq_len = [s + 1 for s in starts]
+    qd = q[:, 0].to(dev)
+    got = to_codes(gqa.gqa_attention(qd, kd, vd, starts, seq_len))
+    want = orc.decode(to_codes(q[:, 0]), kc, vc, np.asarray(seq_len), np.asarray(starts))
+    assert_within_ulp(want, got, 64, "append then decode")
