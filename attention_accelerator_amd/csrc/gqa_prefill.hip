@@ -119,10 +119,10 @@ hipError_t launch_kv_append(const PrefillArgs& a, hipStream_t stream) {
 // Attention.
 
 // Registers staging one K/V block on its way to LDS.  Threads 0..255 hold a quad of
-// V rows (keys 4q..4q+3, dims 8c..8c+7); threads 256..511 a 64-byte segment of a K
-// row (plane 0, the cache row).  `s` holds a 64-byte segment of a K row of plane 1
-// (threads 0..255) or plane 2 (256..511): the second or third BF16 part of a chunk
-// key, zero for cached keys.
+// V rows (keys 4q..4q+3, dims 8c..8c+7, c = t/16, q = t%16); threads 256..511 a
+// 64-byte segment of a K row (plane 0, the cache row).  `s` holds a 64-byte segment of
+// a K row of plane 1 (threads 0..255) or plane 2 (256..511): the second or third BF16
+// part of a chunk key, zero for cached keys.
 struct PfStage {
     uint4 a[4];
     uint4 s[4];
@@ -140,7 +140,7 @@ __device__ __forceinline__ void pf_load_block(const PrefillArgs& a, int b, int k
                               static_cast<int64_t>(kvh) * a.kv_head_stride;
     // Plane 0 / V: addresses formed for both roles, one selected (no branch).
     const int r = t >> 2, seg = t & 3;        // K row segment
-    const int qd = t >> 4, c = t & 15;        // V quad, dim chunk
+    const int c = t >> 4, qd = t & 15;        // V dim chunk, quad
     const char* kbase = reinterpret_cast<const char*>(a.k + head_elem);
     const char* vbase = reinterpret_cast<const char*>(a.v + head_elem);
     const int64_t row_bytes = a.kv_pos_stride * 2;
@@ -172,7 +172,9 @@ __device__ __forceinline__ void pf_store_block(uint16_t* k_lds, uint16_t* v_lds,
         for (int i = 0; i < 4; ++i) dst[i] = sg.a[i];
     } else {
         // V quad -> V^T: keys 4q..4q+3 share (window w, h, g), slots 32w + 8g + 4h + i.
-        const int qd = t >> 4, c = t & 15;
+        // The 16 lanes of one dim chunk hold all 16 quads, so each store instruction
+        // writes whole 128-byte V^T rows (no LDS bank conflicts).
+        const int c = t >> 4, qd = t & 15;
         const int slot = 32 * (qd >> 3) + 8 * (qd & 3) + 4 * ((qd >> 2) & 1);
         const uint32_t* k0 = reinterpret_cast<const uint32_t*>(&sg.a[0]);
         const uint32_t* k1 = reinterpret_cast<const uint32_t*>(&sg.a[1]);
@@ -274,7 +276,15 @@ __global__ __launch_bounds__(kPfThreads) void prefill_attn_kernel(PrefillArgs a)
                 uint16_t h8[8];
 #pragma unroll
                 for (int j = 0; j < 8; ++j) h8[j] = split3(qv[kb][j], s);
-                qop[s][kb] = pack8(h8);
+                // Pin the operand: without this the compiler re-derives it from the double
+                // rows inside the block loop (~600 extra VALU per block) to save registers.
+                union {
+                    bf16x8_t v;
+                    uint32_t w[4];
+                } u;
+                u.v = pack8(h8);
+                asm volatile("" : "+v"(u.w[0]), "+v"(u.w[1]), "+v"(u.w[2]), "+v"(u.w[3]));
+                qop[s][kb] = u.v;
             }
     }
 
@@ -333,17 +343,22 @@ __global__ __launch_bounds__(kPfThreads) void prefill_attn_kernel(PrefillArgs a)
 
         // ---- online softmax for query n over keys key0 + 16kt + 4g + i.
         float sv[4][4];
-        float bmax = -INFINITY;
-        const bool need_mask = key0 + kPfBlk - 1 > st + t_wave0;
 #pragma unroll
         for (int kt = 0; kt < 4; ++kt)
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                float x = sacc[kt][i];
-                if (need_mask && key0 + 16 * kt + 4 * g + i > pos_n) x = -INFINITY;
-                sv[kt][i] = x;
-                bmax = fmaxf(bmax, x);
-            }
+            for (int i = 0; i < 4; ++i) sv[kt][i] = sacc[kt][i];
+        if (key0 + kPfBlk - 1 > st + t_wave0) {     // the block reaches past some query
+#pragma unroll
+            for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                    if (key0 + 16 * kt + 4 * g + i > pos_n) sv[kt][i] = -INFINITY;
+        }
+        float bmax = -INFINITY;
+#pragma unroll
+        for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) bmax = fmaxf(bmax, sv[kt][i]);
         bmax = fmaxf(bmax, __shfl_xor(bmax, 16));
         bmax = fmaxf(bmax, __shfl_xor(bmax, 32));
         const bool grow = bmax > m_run;
@@ -364,7 +379,9 @@ __global__ __launch_bounds__(kPfThreads) void prefill_attn_kernel(PrefillArgs a)
             float p[4], r1[4], r2[4];
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                p[i] = exp2f(sv[kt][i] - m_run);
+                // v_exp_f32: 2^x, 0 for -inf (masked keys); results below 2^-126 flush
+                // to 0, far below anything the BF16 output can see.
+                p[i] = __builtin_amdgcn_exp2f(sv[kt][i] - m_run);
                 lsum += p[i];
                 r1[i] = p[i] - __uint_as_float(__float_as_uint(p[i]) & 0xffff0000u);
                 r2[i] = r1[i] - __uint_as_float(__float_as_uint(r1[i]) & 0xffff0000u);
