@@ -29,6 +29,19 @@ namespace {
 constexpr int32_t kStreamWgsDefault = 1024;
 constexpr int32_t kWavesPerCu = 4;
 
+// Batches whose caches hold at most this many keys in all (B * 8 * capacity; 128 MB of
+// K/V) run as one launch (decode_single_kernel): for them the three dependent launches of
+// the stream path cost more than the HBM traffic.  GQA_SINGLE_LAUNCH_MAX_KEYS overrides
+// it (tuning and tests; 0 disables the single-launch path).
+int64_t single_launch_max_keys() {
+    const char* s = std::getenv("GQA_SINGLE_LAUNCH_MAX_KEYS");
+    if (s) {
+        const long long v = std::atoll(s);
+        if (v >= 0) return v;
+    }
+    return int64_t{1} << 18;
+}
+
 size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
 
 int32_t device_stream_wgs() {
@@ -85,16 +98,29 @@ hipEvent_t* profile_slot() {
 }  // namespace
 
 DecodePlan plan_decode(int32_t batch, int32_t capacity) {
-    (void)capacity;
     DecodePlan plan{};
     plan.n_wgs = stream_wgs();
-    plan.n_slots = static_cast<int64_t>(plan.n_wgs) + static_cast<int64_t>(kHkv) * batch;
+    const int64_t keys_cap = static_cast<int64_t>(batch) * kHkv * capacity;
+    if (keys_cap <= single_launch_max_keys()) {
+        // Single launch: about one 4-wave workgroup per CU (n_wgs / 4), pieces of at least
+        // 128 keys (32 per wave) in multiples of 64, sized from the capacity (the lengths
+        // live on the device); pieces past a sequence's length exit at once.
+        const int64_t n_pieces = plan.n_wgs / 4 > 0 ? plan.n_wgs / 4 : 1;
+        int64_t pk = (keys_cap + n_pieces - 1) / n_pieces;
+        pk = pk < 128 ? 128 : (pk + 63) / 64 * 64;
+        plan.piece_keys = static_cast<int32_t>(pk);
+        plan.pieces_cap = static_cast<int32_t>((capacity + pk - 1) / pk);
+        plan.n_slots = static_cast<int64_t>(batch) * kHkv * plan.pieces_cap;
+    } else {
+        plan.n_slots = static_cast<int64_t>(plan.n_wgs) + static_cast<int64_t>(kHkv) * batch;
+        plan.q_op_bytes = static_cast<size_t>(batch) * kHkv * 4 * kWave * sizeof(uint4);
+        plan.plan_bytes = 256 + align_up((static_cast<size_t>(batch) + 1) * sizeof(int64_t), 256);
+    }
     plan.part_o_bytes = align_up(static_cast<size_t>(plan.n_slots) * kGroup * kD * sizeof(double), 256);
     plan.part_ml_bytes = align_up(static_cast<size_t>(plan.n_slots) * kGroup * sizeof(float2), 256);
-    plan.q_op_bytes = static_cast<size_t>(batch) * kHkv * 4 * kWave * sizeof(uint4);
-    plan.plan_bytes = 256 + align_up(static_cast<size_t>(batch) * sizeof(int64_t), 256) +
-                      align_up(static_cast<size_t>(plan.n_wgs) * sizeof(int4), 256);
-    plan.workspace_bytes = plan.part_o_bytes + plan.part_ml_bytes + plan.q_op_bytes + plan.plan_bytes;
+    plan.count_bytes = align_up(static_cast<size_t>(batch) * kHkv * sizeof(unsigned long long), 256);
+    plan.workspace_bytes =
+        plan.part_o_bytes + plan.part_ml_bytes + plan.q_op_bytes + plan.plan_bytes + plan.count_bytes;
     return plan;
 }
 
@@ -183,7 +209,9 @@ int gqa_decode_bf16(const gqa_params_t* params, const uint16_t* q, const uint16_
     char* pl = ws + plan.part_o_bytes + plan.part_ml_bytes + plan.q_op_bytes;
     a.plan_hdr = reinterpret_cast<int64_t*>(pl);
     a.seq_off = reinterpret_cast<int64_t*>(pl + 256);
-    a.wg_start = reinterpret_cast<int4*>(pl + 256 + align_up(static_cast<size_t>(batch) * sizeof(int64_t), 256));
+    a.seg_count = reinterpret_cast<unsigned long long*>(pl + plan.plan_bytes);
+    a.pieces_cap = plan.pieces_cap;
+    a.piece_keys = plan.piece_keys;
     a.kv_batch_stride = kv->batch_stride;
     a.kv_head_stride = kv->head_stride;
     a.kv_pos_stride = kv->pos_stride;

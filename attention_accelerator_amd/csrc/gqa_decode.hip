@@ -237,6 +237,124 @@ __device__ __forceinline__ void compute_chunk(const DecodeArgs& a, int kc, int k
     }
 }
 
+// ---- end of a piece.
+
+// Merge the four 16-lane rows of a piece (each ran its own online softmax): common max per
+// head, exact power-of-two weights, sums in fp64.  Afterwards every row holds the totals:
+// lane (g, n) has O[h][8n .. 8n+8) for the 4 heads in st.acc, and m_tot / l_tot per head.
+__device__ __forceinline__ void merge_rows(PieceState& st, float (&m_tot)[kGroup], double (&l_tot)[kGroup]) {
+    float mh[kGroup];
+    mh[0] = dpp_f<0x00>(st.m_run);
+    mh[1] = dpp_f<0x55>(st.m_run);
+    mh[2] = dpp_f<0xAA>(st.m_run);
+    mh[3] = dpp_f<0xFF>(st.m_run);
+    float lh[kGroup];
+    lh[0] = dpp_f<0x00>(st.l_run);
+    lh[1] = dpp_f<0x55>(st.l_run);
+    lh[2] = dpp_f<0xAA>(st.l_run);
+    lh[3] = dpp_f<0xFF>(st.l_run);
+#pragma unroll
+    for (int h = 0; h < kGroup; ++h) {
+        float mx = fmaxf(mh[h], __shfl_xor(mh[h], 16));
+        mx = fmaxf(mx, __shfl_xor(mx, 32));
+        m_tot[h] = mx;
+        // a row that saw no key of this piece has m = -inf and contributes nothing
+        const int e = (mh[h] == -INFINITY) ? -1100 : static_cast<int>(mh[h] - mx);
+        double lr = ldexp(static_cast<double>(lh[h]), e);
+        lr += __shfl_xor(lr, 16);
+        lr += __shfl_xor(lr, 32);
+        l_tot[h] = lr;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            double v = ldexp(st.acc[h][j], e);
+            v += __shfl_xor(v, 16);
+            v += __shfl_xor(v, 32);
+            st.acc[h][j] = v;
+        }
+    }
+}
+
+// Normalise in fp64 and round double -> f32 -> BF16 (the 4 output rows of the group, in
+// Q-head order, output_accumulator.v:540-686, gqa_output_collector.v:32-61).
+__device__ __forceinline__ void write_rows(const DecodeArgs& a, int b, int kvh, const PieceState& st,
+                                           const double (&l_tot)[kGroup]) {
+    const int lane = threadIdx.x & (kWave - 1);
+    if (lane >= 16) return;
+    const int n = lane;
+#pragma unroll
+    for (int h = 0; h < kGroup; ++h) {
+        uint16_t o8[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) o8[j] = f32_to_bf16_rne(static_cast<float>(st.acc[h][j] / l_tot[h]));
+        uint4 pk;
+        pk.x = o8[0] | (static_cast<uint32_t>(o8[1]) << 16);
+        pk.y = o8[2] | (static_cast<uint32_t>(o8[3]) << 16);
+        pk.z = o8[4] | (static_cast<uint32_t>(o8[5]) << 16);
+        pk.w = o8[6] | (static_cast<uint32_t>(o8[7]) << 16);
+        *reinterpret_cast<uint4*>(a.out + (static_cast<int64_t>(b) * kHq + kvh * kGroup + h) * kD + 8 * n) = pk;
+    }
+}
+
+// Unnormalised partial of a piece: O (fp64) and (m, l) per head at `slot`.
+__device__ __forceinline__ void write_partial(const DecodeArgs& a, int64_t slot, const PieceState& st,
+                                              const float (&m_tot)[kGroup], const double (&l_tot)[kGroup]) {
+    const int lane = threadIdx.x & (kWave - 1);
+    const int n = lane & 15;
+    if (lane < 16) {
+#pragma unroll
+        for (int h = 0; h < kGroup; ++h) {
+            double2* dst = reinterpret_cast<double2*>(a.part_o + (slot * kGroup + h) * kD + 8 * n);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) dst[j] = make_double2(st.acc[h][2 * j], st.acc[h][2 * j + 1]);
+        }
+    }
+    if (lane < kGroup) {
+        const float mm = lane == 0 ? m_tot[0] : lane == 1 ? m_tot[1] : lane == 2 ? m_tot[2] : m_tot[3];
+        const double ll = lane == 0 ? l_tot[0] : lane == 1 ? l_tot[1] : lane == 2 ? l_tot[2] : l_tot[3];
+        a.part_ml[slot * kGroup + lane] = make_float2(mm, static_cast<float>(ll));
+    }
+}
+
+// This lane's Q operands for (sequence b, KV head kvh): the group's 4 Q rows rotated at
+// query_position and scaled by scale*log2(e) in double, each value split into three BF16
+// parts, in the MFMA B-operand layout (MFMA kb: column n = l%16 -> part n/4 of head n%4,
+// dims 32kb + 8(l/16) + j; columns 12..15 zero).  q_s: 4 KB of LDS for the wave.
+template <bool kRopeQ>
+__device__ __forceinline__ void make_q_operands(const DecodeArgs& a, int b, int kvh, double (*q_s)[kD],
+                                                uint4 (&w)[4]) {
+    const int lane = threadIdx.x & (kWave - 1);
+    const int n = lane & 15;
+    const int g = lane >> 4;
+    const int qpos = a.query_pos[b];
+    double sn = 0.0, cs = 1.0;
+    if (kRopeQ) rope_sincos(qpos, a.rope.inv_freq[lane], sn, cs);
+#pragma unroll
+    for (int h = 0; h < kGroup; ++h) {
+        const uint16_t* qrow = a.q + (static_cast<int64_t>(b) * kHq + kvh * kGroup + h) * kD;
+        const double x = bf16_to_f32(qrow[lane]);
+        const double y = bf16_to_f32(qrow[lane + kPairs]);
+        double xr = x, yr = y;
+        if (kRopeQ) {
+            xr = x * cs - y * sn;
+            yr = x * sn + y * cs;
+        }
+        q_s[h][lane] = xr * a.qk_scale_log2;
+        q_s[h][lane + kPairs] = yr * a.qk_scale_log2;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb) {
+        uint16_t h8[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+            h8[j] = n < 12 ? split3(q_s[n & 3][32 * kb + 8 * g + j], n >> 2) : uint16_t(0);
+        w[kb].x = h8[0] | (static_cast<uint32_t>(h8[1]) << 16);
+        w[kb].y = h8[2] | (static_cast<uint32_t>(h8[3]) << 16);
+        w[kb].z = h8[4] | (static_cast<uint32_t>(h8[5]) << 16);
+        w[kb].w = h8[6] | (static_cast<uint32_t>(h8[7]) << 16);
+    }
+}
+
 // Q operands of every (sequence, KV head), written once per call by
 // decode_prepare_kernel and read by each piece: the 4 Q rows of the group rotated at
 // query_position and scaled by scale*log2(e) in double, split into hi/mid/lo BF16,
@@ -273,8 +391,6 @@ __global__ __launch_bounds__(kWave) void decode_prepare_kernel(DecodeArgs a) {
     const int kvh = blockIdx.x;
     const int b = blockIdx.y;
     const int lane = threadIdx.x;
-    const int n = lane & 15;
-    const int g = lane >> 4;
     if (b == a.batch) {
         if (kvh == 0) build_plan(a, lane);
         return;
@@ -288,37 +404,11 @@ __global__ __launch_bounds__(kWave) void decode_prepare_kernel(DecodeArgs a) {
         }
         return;
     }
-    const int qpos = a.query_pos[b];
-    double sn = 0.0, cs = 1.0;
-    if (kRopeQ) rope_sincos(qpos, a.rope.inv_freq[lane], sn, cs);
-#pragma unroll
-    for (int h = 0; h < kGroup; ++h) {
-        const uint16_t* qrow = a.q + (static_cast<int64_t>(b) * kHq + kvh * kGroup + h) * kD;
-        const double x = bf16_to_f32(qrow[lane]);
-        const double y = bf16_to_f32(qrow[lane + kPairs]);
-        double xr = x, yr = y;
-        if (kRopeQ) {
-            xr = x * cs - y * sn;
-            yr = x * sn + y * cs;
-        }
-        q_s[h][lane] = xr * a.qk_scale_log2;
-        q_s[h][lane + kPairs] = yr * a.qk_scale_log2;
-    }
-    __syncthreads();
+    uint4 w[4];
+    make_q_operands<kRopeQ>(a, b, kvh, q_s, w);
     uint4* dst = a.q_op + ((static_cast<int64_t>(b) * kHkv + kvh) * 4) * kWave;
 #pragma unroll
-    for (int kb = 0; kb < 4; ++kb) {
-        uint16_t h8[8];
-#pragma unroll
-        for (int j = 0; j < 8; ++j)
-            h8[j] = n < 12 ? split3(q_s[n & 3][32 * kb + 8 * g + j], n >> 2) : uint16_t(0);
-        uint4 w;
-        w.x = h8[0] | (static_cast<uint32_t>(h8[1]) << 16);
-        w.y = h8[2] | (static_cast<uint32_t>(h8[3]) << 16);
-        w.z = h8[4] | (static_cast<uint32_t>(h8[5]) << 16);
-        w.w = h8[6] | (static_cast<uint32_t>(h8[7]) << 16);
-        dst[kb * kWave + lane] = w;
-    }
+    for (int kb = 0; kb < 4; ++kb) dst[kb * kWave + lane] = w[kb];
 }
 
 // Where the rows of one piece live: segment base pointers and this lane's offsets of
@@ -333,7 +423,7 @@ struct PieceRows {
 
 __device__ __forceinline__ void piece_rows(const DecodeArgs& a, int b, int kvh, int k_a, int k_b,
                                            PieceRows& r) {
-    const int lane = threadIdx.x;
+    const int lane = threadIdx.x & (kWave - 1);
     const int n = lane & 15;
     const int g = lane >> 4;
     const int64_t head_off = static_cast<int64_t>(b) * a.kv_batch_stride +
@@ -372,7 +462,7 @@ __device__ __forceinline__ void load_cur_or_next(bool in_cur, PieceRows& cur, co
 }
 
 __device__ __forceinline__ void load_q_operands(const DecodeArgs& a, int b, int kvh, bf16x8_t (&bq)[4]) {
-    const uint4* qop = a.q_op + ((static_cast<int64_t>(b) * kHkv + kvh) * 4) * kWave + threadIdx.x;
+    const uint4* qop = a.q_op + ((static_cast<int64_t>(b) * kHkv + kvh) * 4) * kWave + (threadIdx.x & (kWave - 1));
 #pragma unroll
     for (int kb = 0; kb < 4; ++kb) bq[kb] = as_bf16x8(qop[kb * kWave]);
 }
@@ -387,7 +477,7 @@ __device__ __forceinline__ void process_piece(const DecodeArgs& a, int b, int kv
                                               int k_b, int64_t wg, PieceRows& cur,
                                               const PieceRows& nxt, Chunk& c0, Chunk& c1,
                                               const bf16x8_t (&bq)[4]) {
-    const int lane = threadIdx.x;
+    const int lane = threadIdx.x & (kWave - 1);
     const int n = lane & 15;       // MFMA column / PV dim chunk
     const int g = lane >> 4;       // MFMA lane group / PV key row
     const uint32_t step = kChunk * static_cast<uint32_t>(a.kv_pos_stride) * 2u;
@@ -413,74 +503,14 @@ __device__ __forceinline__ void process_piece(const DecodeArgs& a, int b, int kv
         if (i + 2 >= n_chunks) break;
     }
 
-    // ---- merge the four rows: common max per head, exact power-of-two weights.
-    float mh[kGroup];
-    mh[0] = dpp_f<0x00>(st.m_run);
-    mh[1] = dpp_f<0x55>(st.m_run);
-    mh[2] = dpp_f<0xAA>(st.m_run);
-    mh[3] = dpp_f<0xFF>(st.m_run);
-    float lh[kGroup];
-    lh[0] = dpp_f<0x00>(st.l_run);
-    lh[1] = dpp_f<0x55>(st.l_run);
-    lh[2] = dpp_f<0xAA>(st.l_run);
-    lh[3] = dpp_f<0xFF>(st.l_run);
     float m_tot[kGroup];
     double l_tot[kGroup];
-#pragma unroll
-    for (int h = 0; h < kGroup; ++h) {
-        float mx = fmaxf(mh[h], __shfl_xor(mh[h], 16));
-        mx = fmaxf(mx, __shfl_xor(mx, 32));
-        m_tot[h] = mx;
-        // a row that saw no key of this piece has m = -inf and contributes nothing
-        const int e = (mh[h] == -INFINITY) ? -1100 : static_cast<int>(mh[h] - mx);
-        double lr = ldexp(static_cast<double>(lh[h]), e);
-        lr += __shfl_xor(lr, 16);
-        lr += __shfl_xor(lr, 32);
-        l_tot[h] = lr;
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            double v = ldexp(st.acc[h][j], e);
-            v += __shfl_xor(v, 16);
-            v += __shfl_xor(v, 32);
-            st.acc[h][j] = v;
-        }
-    }
-
-    const int64_t seg = static_cast<int64_t>(b) * kHkv + kvh;
+    merge_rows(st, m_tot, l_tot);
     if (k_a == 0 && k_b == nv) {
-        // The whole segment: normalise in fp64, round double -> f32 -> BF16.
-        if (g == 0) {
-#pragma unroll
-            for (int h = 0; h < kGroup; ++h) {
-                uint16_t o8[8];
-#pragma unroll
-                for (int j = 0; j < 8; ++j) o8[j] = f32_to_bf16_rne(static_cast<float>(st.acc[h][j] / l_tot[h]));
-                uint4 pk;
-                pk.x = o8[0] | (static_cast<uint32_t>(o8[1]) << 16);
-                pk.y = o8[2] | (static_cast<uint32_t>(o8[3]) << 16);
-                pk.z = o8[4] | (static_cast<uint32_t>(o8[5]) << 16);
-                pk.w = o8[6] | (static_cast<uint32_t>(o8[7]) << 16);
-                *reinterpret_cast<uint4*>(a.out + (static_cast<int64_t>(b) * kHq + kvh * kGroup + h) * kD +
-                                          8 * n) = pk;
-            }
-        }
+        write_rows(a, b, kvh, st, l_tot);      // the whole segment
         return;
     }
-
-    const int64_t slot = wg + seg;
-    if (g == 0) {
-#pragma unroll
-        for (int h = 0; h < kGroup; ++h) {
-            double2* dst = reinterpret_cast<double2*>(a.part_o + (slot * kGroup + h) * kD + 8 * n);
-#pragma unroll
-            for (int j = 0; j < 4; ++j) dst[j] = make_double2(st.acc[h][2 * j], st.acc[h][2 * j + 1]);
-        }
-    }
-    if (lane < kGroup) {
-        const float mm = lane == 0 ? m_tot[0] : lane == 1 ? m_tot[1] : lane == 2 ? m_tot[2] : m_tot[3];
-        const double ll = lane == 0 ? l_tot[0] : lane == 1 ? l_tot[1] : lane == 2 ? l_tot[2] : l_tot[3];
-        a.part_ml[slot * kGroup + lane] = make_float2(mm, static_cast<float>(ll));
-    }
+    write_partial(a, wg + static_cast<int64_t>(b) * kHkv + kvh, st, m_tot, l_tot);
 }
 
 // Per-sequence key offsets for 64 sequences at a time, one per lane: o = seq_off[base +
@@ -492,7 +522,7 @@ struct SeqWindow {
 };
 
 __device__ __forceinline__ void load_seq_window(const DecodeArgs& a, int base, SeqWindow& sw) {
-    const int bb = base + static_cast<int>(threadIdx.x);
+    const int bb = base + static_cast<int>(threadIdx.x & (kWave - 1));
     sw.base = base;
     sw.o = bb < a.batch ? a.seq_off[bb] : INT64_MAX;
     sw.o1 = bb < a.batch ? a.seq_off[bb + 1] : INT64_MAX;
@@ -509,7 +539,7 @@ __device__ __forceinline__ bool next_segment(const DecodeArgs& a, SeqWindow& sw,
     }
     kvh = 0;
     while (true) {
-        const int bb = sw.base + static_cast<int>(threadIdx.x);
+        const int bb = sw.base + static_cast<int>(threadIdx.x & (kWave - 1));
         const uint64_t m = __ballot(bb < a.batch && bb > b && sw.o1 > sw.o);
         if (m) {
             const int j = __ffsll(static_cast<unsigned long long>(m)) - 1;
@@ -686,6 +716,224 @@ __global__ __launch_bounds__(kGroup * kWave) void decode_merge_kernel(DecodeArgs
     out[lane] = lo | (hi << 16);
 }
 
+
+// ---------------------------------------------------------------------------------
+// Single-launch decode for small batches (few keys in all, where three dependent launches
+// would cost more than the HBM traffic).  One 4-wave workgroup per (piece, segment);
+// a piece is a.piece_keys keys, a quarter per wave.  The workgroup prepares the group's
+// Q operands once (wave h rotates head h), each wave streams its quarter like a
+// stream-kernel piece, the four wave states are combined in LDS, and the piece either
+// writes the output rows (a one-piece segment) or leaves its partial; the last piece of
+// a segment to finish merges them, one wave per head.  Partials are written and read
+// with agent-scope (sc1) accesses, which go through to memory past the XCD-local L2s,
+// and the per-segment counter is a device-scope atomic incremented only after the
+// partial's stores have completed.  The merging piece resets the counter, so a
+// workspace needs zeroing (gqa_decode_workspace_init) before its first use only.
+
+// Agent-scope (sc1) 8-byte stores and loads: coherent across the XCDs without a cache
+// write-back or invalidate (used to hand partials between workgroups inside a launch).
+__device__ __forceinline__ void store_agent(unsigned long long* p, double v) {
+    __hip_atomic_store(p, static_cast<unsigned long long>(__double_as_longlong(v)), __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__device__ __forceinline__ void store_agent(unsigned long long* p, float2 v) {
+    unsigned long long u;
+    __builtin_memcpy(&u, &v, 8);
+    __hip_atomic_store(p, u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__device__ __forceinline__ float2 load_agent_f2(const float2* p) {
+    const unsigned long long u =
+        __hip_atomic_load(reinterpret_cast<const unsigned long long*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    float2 v;
+    __builtin_memcpy(&v, &u, 8);
+    return v;
+}
+
+__device__ __forceinline__ double2 load_agent_d2(const double* p) {
+    const unsigned long long* q = reinterpret_cast<const unsigned long long*>(p);
+    return make_double2(__longlong_as_double(__hip_atomic_load(q, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)),
+                        __longlong_as_double(__hip_atomic_load(q + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)));
+}
+
+constexpr int kSingleWaves = 4;
+
+template <bool kRopeQ, bool kRopeK>
+__global__ __launch_bounds__(kSingleWaves * kWave) void decode_single_kernel(DecodeArgs a) {
+    __shared__ double q_s[kGroup][kD];
+    __shared__ double o_s[kSingleWaves][kGroup][kD];     // each wave's O (row-merged)
+    __shared__ float m_s[kSingleWaves][kGroup];
+    __shared__ double l_s[kSingleWaves][kGroup];
+    __shared__ int last_s;
+    const int piece = blockIdx.x;
+    const int seg = blockIdx.y;
+    const int b = seg / kHkv;
+    const int kvh = seg % kHkv;
+    const int wave = threadIdx.x / kWave;
+    const int lane = threadIdx.x % kWave;
+    const int n = lane & 15;
+    const int g = lane >> 4;
+    const int nv = seq_valid_keys(a, b);
+    if (nv == 0) {
+        if (kvh == 0 && piece == 0) {
+            uint4* out = reinterpret_cast<uint4*>(a.out + static_cast<int64_t>(b) * kHq * kD);
+            for (int i = threadIdx.x; i < kHq * kD / 8; i += kSingleWaves * kWave)
+                out[i] = make_uint4(0x7fc07fc0u, 0x7fc07fc0u, 0x7fc07fc0u, 0x7fc07fc0u);
+        }
+        return;
+    }
+    const int n_pieces = (nv + a.piece_keys - 1) / a.piece_keys;
+    if (piece >= n_pieces) return;                       // uniform over the workgroup
+    const int quarter = a.piece_keys / kSingleWaves;
+    const int k_a = min(nv, piece * a.piece_keys + wave * quarter);
+    const int k_b = min(nv, k_a + quarter);
+    const bool busy = k_a < k_b;                         // uniform over the wave
+
+    // First chunk of this wave's quarter, requested before the Q operands are formed.
+    PieceRows cur;
+    piece_rows(a, b, kvh, busy ? k_a : nv - 1, busy ? k_b : nv, cur);
+    const uint32_t step = kChunk * static_cast<uint32_t>(a.kv_pos_stride) * 2u;
+    Chunk c0, c1;
+    load_next(cur, step, c0);
+
+    // Q operands: wave h rotates and scales Q head 4*kvh + h into q_s.
+    {
+        const int qpos = a.query_pos[b];
+        double sn = 0.0, cs = 1.0;
+        if (kRopeQ) rope_sincos(qpos, a.rope.inv_freq[lane], sn, cs);
+        const uint16_t* qrow = a.q + (static_cast<int64_t>(b) * kHq + kvh * kGroup + wave) * kD;
+        const double x = bf16_to_f32(qrow[lane]);
+        const double y = bf16_to_f32(qrow[lane + kPairs]);
+        double xr = x, yr = y;
+        if (kRopeQ) {
+            xr = x * cs - y * sn;
+            yr = x * sn + y * cs;
+        }
+        q_s[wave][lane] = xr * a.qk_scale_log2;
+        q_s[wave][lane + kPairs] = yr * a.qk_scale_log2;
+    }
+    __syncthreads();
+    bf16x8_t bq[4];
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb) {
+        uint16_t h8[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+            h8[j] = n < 12 ? split3(q_s[n & 3][32 * kb + 8 * g + j], n >> 2) : uint16_t(0);
+        bq[kb] = pack8(h8);
+    }
+
+    PieceState st;
+#pragma unroll
+    for (int h = 0; h < kGroup; ++h)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) st.acc[h][j] = 0.0;
+    st.m_run = -INFINITY;
+    st.l_run = 0.f;
+    if (busy) {
+        const int n_chunks = (k_b - k_a + kChunk - 1) / kChunk;
+        for (int i = 0;; i += 2) {
+            load_next(cur, step, c1);
+            compute_chunk<kRopeK>(a, k_a + i * kChunk, k_b, n, g, c0, bq, st);
+            if (i + 1 >= n_chunks) break;
+            load_next(cur, step, c0);
+            compute_chunk<kRopeK>(a, k_a + (i + 1) * kChunk, k_b, n, g, c1, bq, st);
+            if (i + 2 >= n_chunks) break;
+        }
+    }
+    float m_tot[kGroup];
+    double l_tot[kGroup];
+    merge_rows(st, m_tot, l_tot);
+    if (lane < 16) {
+#pragma unroll
+        for (int h = 0; h < kGroup; ++h)
+#pragma unroll
+            for (int j = 0; j < 8; ++j) o_s[wave][h][8 * n + j] = st.acc[h][j];
+    }
+    if (lane < kGroup) {
+        m_s[wave][lane] = lane == 0 ? m_tot[0] : lane == 1 ? m_tot[1] : lane == 2 ? m_tot[2] : m_tot[3];
+        l_s[wave][lane] = lane == 0 ? l_tot[0] : lane == 1 ? l_tot[1] : lane == 2 ? l_tot[2] : l_tot[3];
+    }
+    __syncthreads();
+
+    // Wave h combines head h over the four quarters: lane owns dims 2*lane, 2*lane + 1.
+    const int h = wave;
+    float mx = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < kSingleWaves; ++w) mx = fmaxf(mx, m_s[w][h]);
+    double l = 0.0, o0 = 0.0, o1 = 0.0;
+#pragma unroll
+    for (int w = 0; w < kSingleWaves; ++w) {
+        const float m = m_s[w][h];
+        if (m == -INFINITY) continue;                    // an idle quarter
+        const int e = static_cast<int>(m - mx);
+        l += ldexp(l_s[w][h], e);
+        o0 += ldexp(o_s[w][h][2 * lane], e);
+        o1 += ldexp(o_s[w][h][2 * lane + 1], e);
+    }
+    uint32_t* orow = reinterpret_cast<uint32_t*>(a.out + (static_cast<int64_t>(b) * kHq + kvh * kGroup + h) * kD);
+    if (n_pieces == 1) {
+        orow[lane] = f32_to_bf16_rne(static_cast<float>(o0 / l)) |
+                     (static_cast<uint32_t>(f32_to_bf16_rne(static_cast<float>(o1 / l))) << 16);
+        return;
+    }
+    const int64_t slot0 = static_cast<int64_t>(seg) * a.pieces_cap;
+    // Publish the partial with agent-scope stores (written through the XCD's L2, which is
+    // not coherent with the other XCDs'), and wait until they have completed before the
+    // counter is touched: a __threadfence here would write back the whole L2 instead.
+    {
+        unsigned long long* po =
+            reinterpret_cast<unsigned long long*>(a.part_o + ((slot0 + piece) * kGroup + h) * kD) + 2 * lane;
+        store_agent(po, o0);
+        store_agent(po + 1, o1);
+        if (lane == 0)
+            store_agent(reinterpret_cast<unsigned long long*>(a.part_ml + (slot0 + piece) * kGroup + h),
+                        make_float2(mx, static_cast<float>(l)));
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");   // s_waitcnt: stores done
+    }
+    __syncthreads();
+    // Count finished pieces (device-scope atomic); the last piece merges and resets the
+    // counter for the next call on this workspace.
+    if (threadIdx.x == 0) last_s = atomicAdd(&a.seg_count[seg], 1ull) == static_cast<unsigned long long>(n_pieces - 1);
+    __syncthreads();
+    if (!last_s) return;
+    if (threadIdx.x == 0) a.seg_count[seg] = 0;
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+
+    // Merge the segment's pieces, wave h for head h: (m, l) of 64 pieces per pass, one per
+    // lane, then their O rows (lane owns dims 2*lane, 2*lane + 1), 16 requested at a time.
+    float m_all = -INFINITY;
+    for (int p0 = 0; p0 < n_pieces; p0 += kWave) {
+        const int p = p0 + lane;
+        m_all = fmaxf(m_all, p < n_pieces ? load_agent_f2(a.part_ml + (slot0 + p) * kGroup + h).x : -INFINITY);
+    }
+    m_all = wave_max(m_all);
+    l = 0.0;
+    o0 = 0.0;
+    o1 = 0.0;
+    for (int p0 = 0; p0 < n_pieces; p0 += 16) {
+        double2 ov[16];
+        float2 ml[16];
+#pragma unroll
+        for (int u = 0; u < 16; ++u) {
+            const int p = min(p0 + u, n_pieces - 1);
+            ov[u] = load_agent_d2(a.part_o + ((slot0 + p) * kGroup + h) * kD + 2 * lane);
+            ml[u] = load_agent_f2(a.part_ml + (slot0 + p) * kGroup + h);
+        }
+#pragma unroll
+        for (int u = 0; u < 16; ++u) {
+            // copies of the last piece (indices clamped above) get weight 0
+            const int e = p0 + u < n_pieces ? static_cast<int>(ml[u].x - m_all) : -1100;
+            l += ldexp(static_cast<double>(ml[u].y), e);
+            o0 += ldexp(ov[u].x, e);
+            o1 += ldexp(ov[u].y, e);
+        }
+    }
+    orow[lane] = f32_to_bf16_rne(static_cast<float>(o0 / l)) |
+                 (static_cast<uint32_t>(f32_to_bf16_rne(static_cast<float>(o1 / l))) << 16);
+}
+
 __global__ __launch_bounds__(256) void zero_words_kernel(uint32_t* p, int64_t n) {
     const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
     if (i < n) p[i] = 0u;
@@ -700,6 +948,25 @@ hipError_t launch_zero_words(uint32_t* p, int64_t n, hipStream_t stream) {
 
 hipError_t launch_decode(const DecodeArgs& a, int batch, hipStream_t stream, hipEvent_t* ev) {
     const bool rq = (a.flags & 1u) != 0, rk = (a.flags & 2u) != 0;
+    if (a.pieces_cap > 0) {
+        // Single launch (small batches).
+        if (ev) (void)hipEventRecord(ev[0], stream);
+        const dim3 grid(a.pieces_cap, batch * kHkv);
+        if (rq && rk)
+            hipLaunchKernelGGL((decode_single_kernel<true, true>), grid, dim3(kSingleWaves * kWave), 0, stream, a);
+        else if (rq)
+            hipLaunchKernelGGL((decode_single_kernel<true, false>), grid, dim3(kSingleWaves * kWave), 0, stream, a);
+        else if (rk)
+            hipLaunchKernelGGL((decode_single_kernel<false, true>), grid, dim3(kSingleWaves * kWave), 0, stream, a);
+        else
+            hipLaunchKernelGGL((decode_single_kernel<false, false>), grid, dim3(kSingleWaves * kWave), 0, stream, a);
+        const hipError_t e = hipGetLastError();
+        if (ev) {
+            (void)hipEventRecord(ev[1], stream);
+            (void)hipEventRecord(ev[2], stream);
+        }
+        return e;
+    }
     if (rq)
         hipLaunchKernelGGL((decode_prepare_kernel<true>), dim3(kHkv, batch + 1), dim3(kWave), 0, stream, a);
     else

@@ -18,29 +18,35 @@ struct DecodeArgs {
     uint16_t* out;            // [B][32][128]
     uint4* q_op;              // [B][8][4][64] prepared Q operands (MFMA B layout)
     int64_t* plan_hdr;        // {total keys, keys per stream workgroup}
-    int64_t* seq_off;         // [B] first global key offset of sequence b's segments
-    int4* wg_start;           // [n_wgs] {b, kv_head, key, n_valid(b)} where workgroup w starts
+    int64_t* seq_off;         // [B+1] first global key offset of sequence b's segments
     double* part_o;           // [n_slots][4][128] unnormalised partial outputs
     float2* part_ml;          // [n_slots][4] (integer-valued running max in log2 units, sum)
+    unsigned long long* seg_count;  // [B*8] pieces finished per segment, single-launch path (zero between calls)
     int64_t kv_batch_stride;
     int64_t kv_head_stride;
     int64_t kv_pos_stride;
     int32_t capacity;
     int32_t batch;
     int32_t n_wgs;            // persistent workgroups of the stream kernel
+    int32_t pieces_cap;       // > 0: single-launch path, pieces per segment (grid x)
+    int32_t piece_keys;       // single-launch path: keys per piece
     double qk_scale_log2;     // scale * log2(e), folded into Q
     uint32_t flags;           // bit0 RoPE on Q, bit1 RoPE on K
     RopeTable rope;
 };
 
-// Launch plan for a batch: stream-kernel workgroups and partial slots.
+// Launch plan for a batch: stream-kernel workgroups and partial slots, or (small batches)
+// the single-launch piece size.
 struct DecodePlan {
     int32_t n_wgs;
-    int64_t n_slots;          // n_wgs + 8 * batch (one per piece, see gqa_decode.hip)
+    int32_t pieces_cap;       // > 0 selects the single-launch path
+    int32_t piece_keys;
+    int64_t n_slots;          // stream path: n_wgs + 8 * batch; single path: 8 * batch * pieces_cap
     size_t part_o_bytes;      // fp64 partial outputs at offset 0
     size_t part_ml_bytes;     // then the (m, l) pairs
     size_t q_op_bytes;        // then the prepared Q operands
-    size_t plan_bytes;        // then the plan: header, seq_off[B], wg_start[n_wgs]
+    size_t plan_bytes;        // then the plan: header, seq_off[B+1]
+    size_t count_bytes;       // then the per-segment counters of the single-launch path
     size_t workspace_bytes;
 };
 

@@ -68,49 +68,58 @@ __device__ __forceinline__ int64_t cache_elem(const PrefillArgs& a, int b, int h
 }
 
 // ---------------------------------------------------------------------------------
-// KV append: one wave per new (sequence, token, KV head) row; lane i rotates the pair
-// (i, i+64) at position start+t in double (pyfiles/gen_gqa_wrapper_vectors.py:25-35).
+// KV append: one wave per new (sequence, token); lane i computes the angle of frequency i
+// at position start+t once (pyfiles/gen_gqa_wrapper_vectors.py:30-31) and rotates the
+// pair (i, i+64) of all 8 KV heads' rows in double (:25-35).
 __global__ __launch_bounds__(256) void kv_append_kernel(PrefillArgs a) {
-    const int64_t row = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+    const int64_t bt = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);   // b * T + t
     const int lane = threadIdx.x & (kWave - 1);
-    const int64_t n_rows = static_cast<int64_t>(a.batch) * a.n_new * kHkv;
-    if (row >= n_rows) return;
-    const int kvh = static_cast<int>(row % kHkv);
-    const int64_t bt = row / kHkv;
+    if (bt >= static_cast<int64_t>(a.batch) * a.n_new) return;
     const int t = static_cast<int>(bt % a.n_new);
     const int b = static_cast<int>(bt / a.n_new);
     const int st = a.start[b];
     if (!prefill_start_ok(a, st)) return;
     const int64_t pos = static_cast<int64_t>(st) + t;
-    const uint16_t* ksrc = a.k_new + row * kD;
-    const uint16_t* vsrc = a.v_new + row * kD;
-    const double x = bf16_to_f32(ksrc[lane]);
-    const double y = bf16_to_f32(ksrc[lane + kPairs]);
-    double xr = x, yr = y;
-    if (a.flags & 2u) rope_pair(x, y, pos, a.rope.inv_freq[lane], xr, yr);
-    const uint16_t hx = bf16_of(xr), hy = bf16_of(yr);
-    uint16_t* kdst = a.k + cache_elem(a, b, kvh, pos);
-    uint16_t* vdst = a.v + cache_elem(a, b, kvh, pos);
-    kdst[lane] = hx;
-    kdst[lane + kPairs] = hy;
-    vdst[lane] = vsrc[lane];
-    vdst[lane + kPairs] = vsrc[lane + kPairs];
-    if (a.k_split) {
-        const double rx = xr - f64_of_bf16(hx), ry = yr - f64_of_bf16(hy);
-        const uint16_t mx = bf16_of(rx), my = bf16_of(ry);
-        uint16_t* mid = a.k_split + row * kD;
-        uint16_t* lo = a.k_split + (n_rows + row) * kD;
-        mid[lane] = mx;
-        mid[lane + kPairs] = my;
-        lo[lane] = bf16_of(rx - f64_of_bf16(mx));
-        lo[lane + kPairs] = bf16_of(ry - f64_of_bf16(my));
+    const int64_t n_rows = static_cast<int64_t>(a.batch) * a.n_new * kHkv;
+    const bool rope = (a.flags & 2u) != 0;
+    double sn = 0.0, cs = 1.0;
+    if (rope) rope_sincos(pos, a.rope.inv_freq[lane], sn, cs);
+#pragma unroll 2
+    for (int kvh = 0; kvh < kHkv; ++kvh) {
+        const int64_t row = bt * kHkv + kvh;
+        const uint16_t* ksrc = a.k_new + row * kD;
+        const uint16_t* vsrc = a.v_new + row * kD;
+        const double x = bf16_to_f32(ksrc[lane]);
+        const double y = bf16_to_f32(ksrc[lane + kPairs]);
+        double xr = x, yr = y;
+        if (rope) {
+            xr = x * cs - y * sn;
+            yr = x * sn + y * cs;
+        }
+        const uint16_t hx = bf16_of(xr), hy = bf16_of(yr);
+        uint16_t* kdst = a.k + cache_elem(a, b, kvh, pos);
+        uint16_t* vdst = a.v + cache_elem(a, b, kvh, pos);
+        kdst[lane] = hx;
+        kdst[lane + kPairs] = hy;
+        vdst[lane] = vsrc[lane];
+        vdst[lane + kPairs] = vsrc[lane + kPairs];
+        if (a.k_split) {
+            const double rx = xr - f64_of_bf16(hx), ry = yr - f64_of_bf16(hy);
+            const uint16_t mx = bf16_of(rx), my = bf16_of(ry);
+            uint16_t* mid = a.k_split + row * kD;
+            uint16_t* lo = a.k_split + (n_rows + row) * kD;
+            mid[lane] = mx;
+            mid[lane + kPairs] = my;
+            lo[lane] = bf16_of(rx - f64_of_bf16(mx));
+            lo[lane + kPairs] = bf16_of(ry - f64_of_bf16(my));
+        }
     }
 }
 
 hipError_t launch_kv_append(const PrefillArgs& a, hipStream_t stream) {
-    const int64_t n_rows = static_cast<int64_t>(a.batch) * a.n_new * kHkv;
-    if (n_rows == 0) return hipSuccess;
-    hipLaunchKernelGGL(kv_append_kernel, dim3(static_cast<unsigned>((n_rows + 3) / 4)), dim3(256), 0,
+    const int64_t n_tok = static_cast<int64_t>(a.batch) * a.n_new;
+    if (n_tok == 0) return hipSuccess;
+    hipLaunchKernelGGL(kv_append_kernel, dim3(static_cast<unsigned>((n_tok + 3) / 4)), dim3(256), 0,
                        stream, a);
     return hipGetLastError();
 }

@@ -98,9 +98,10 @@ int gqa_validate_lengths(const int32_t* seq_len, const int32_t* query_pos, int32
 size_t gqa_decode_workspace_bytes(const gqa_params_t* params, int32_t batch, int32_t capacity);
 
 /* Zero-fill a decode workspace with a fill kernel on `stream` (no memset, so the call
- * may sit inside a captured graph).  Optional: decode calls need no particular
- * workspace contents; provided for callers that want defined memory.  No reference
- * counterpart. */
+ * may sit inside a captured graph).  Required once before a workspace's first decode
+ * call: small batches finish in one launch and count finished pieces in it (each call
+ * leaves the counters at zero again).  A workspace prepared for (batch, capacity) serves
+ * later calls with the same batch and capacity.  No reference counterpart. */
 int gqa_decode_workspace_init(const gqa_params_t* params, int32_t batch, int32_t capacity,
                               void* workspace, size_t workspace_bytes, void* stream);
 
@@ -110,8 +111,12 @@ int gqa_decode_workspace_init(const gqa_params_t* params, int32_t batch, int32_t
  *   seq_len    [batch] int32, device: valid cache length
  *   query_pos  [batch] int32, device: position of the query token
  *   out        [batch][32][128]  output rows in Q-head order
- *   workspace  gqa_decode_workspace_bytes bytes (any contents); calls sharing a
+ *   workspace  gqa_decode_workspace_bytes bytes, prepared once by
+ *              gqa_decode_workspace_init for this batch and capacity; calls sharing a
  *              workspace must be ordered (same stream)
+ * Batches whose caches hold at most 2^18 keys in all (batch * 8 * capacity) run as one
+ * launch whose pieces merge in-kernel; larger ones as a prepare, a stream-K and a merge
+ * launch.
  * Key p of sequence b contributes iff p < seq_len[b] and p <= query_pos[b]
  * (gqa_attention_wrapper.v:279); rows outside that range are never read.
  * Lengths are read on the device: an entry violating the rules of

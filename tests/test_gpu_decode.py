@@ -112,8 +112,56 @@ def test_stream_partition_invariance(dev, wgs, monkeypatch):
     arbitrary keys, ranges span several sequences and heads): same parity."""
     b = stimulus.decode_batch(5, 3000, min_len=1, max_len=3000, seed=9)
     monkeypatch.setenv("GQA_STREAM_WGS", wgs)
+    monkeypatch.setenv("GQA_SINGLE_LAUNCH_MAX_KEYS", "0")       # the stream-K path
     got = _run(b, dev)
     assert_within_ulp(_oracle(b), got, 64, f"{wgs} workgroups")
+
+
+@pytest.mark.parametrize("wgs", ["16", "200", "1024", "5000"])
+def test_single_launch_pieces(dev, wgs, monkeypatch):
+    """Small batches run as one launch whose pieces (64 keys and up, here 64 .. 2304)
+    merge in-kernel: parity for every piece size, and the stream-K path agrees.
+
+    V is N(0,1) + 2 here so that no output lies within a few 1e-9 of zero: this test is
+    about how pieces split and merge, and near-zero outputs sit on the fp32-score error
+    floor (about 3e-9 absolute, which exceeds 64 BF16 ULP of an output below ~1e-8; see
+    test_north_star_batch64_ragged and DESIGN.md for that floor)."""
+    b = stimulus.decode_batch(4, 2300, min_len=1, max_len=2300, seed=19)
+    b = stimulus.DecodeBatch(b.q, b.k, (b.v.float() + 2.0).to(torch.bfloat16), b.seq_len,
+                             b.query_pos)
+    monkeypatch.setenv("GQA_STREAM_WGS", wgs)
+    single = _run(b, dev)
+    want = _oracle(b)
+    assert_within_ulp(want, single, 64, f"single launch, {wgs}")
+    monkeypatch.setenv("GQA_SINGLE_LAUNCH_MAX_KEYS", "0")
+    stream = _run(b, dev)
+    assert_within_ulp(stream, single, 2, "single launch vs stream-K")
+
+
+def test_single_launch_workspace_init_and_reuse(dev):
+    """The single-launch path counts finished pieces in the workspace: after
+    gqa_decode_workspace_init (here over garbage) one workspace serves many calls in a row,
+    each leaving the counters at zero (same bits every time)."""
+    import ctypes
+    from attention_accelerator_amd._lib import lib
+    b = stimulus.decode_batch(2, 4096, seed=20)
+    b = stimulus.DecodeBatch(b.q, b.k, (b.v.float() + 2.0).to(torch.bfloat16), b.seq_len,
+                             b.query_pos)
+    want = _oracle(b)
+    nbytes = gqa.decode_workspace_bytes(2, 4096)
+    ref = None
+    for fill in (0xFF, 0x5A):
+        ws = torch.full((nbytes,), fill, dtype=torch.uint8, device=dev)
+        p = gqa.make_params()
+        assert lib().gqa_decode_workspace_init(ctypes.byref(p), 2, 4096, ws.data_ptr(), nbytes,
+                                               torch.cuda.current_stream().cuda_stream) == 0
+        for _ in range(4):
+            got = _codes(gqa.gqa_attention(b.q.to(dev), b.k.to(dev), b.v.to(dev), b.query_pos,
+                                           b.seq_len, workspace=ws))
+            if ref is None:
+                assert_within_ulp(want, got, 64, "single launch")
+                ref = got
+            assert np.array_equal(got, ref)
 
 
 def test_workspace_reuse_across_calls(dev):
