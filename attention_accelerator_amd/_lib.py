@@ -32,6 +32,9 @@ EXPORTS = (
     "gqa_decode_workspace_bytes",
     "gqa_decode_workspace_init",
     "gqa_decode_bf16",
+    "gqa_decode_paged_workspace_bytes",
+    "gqa_decode_paged_bf16",
+    "gqa_kv_append_paged_bf16",
     "gqa_prefill_workspace_bytes",
     "gqa_prefill_bf16",
     "gqa_kv_append_bf16",
@@ -60,6 +63,17 @@ class GqaKvLayout(ctypes.Structure):
         ("head_stride", ctypes.c_int64),
         ("pos_stride", ctypes.c_int64),
         ("capacity", ctypes.c_int32),
+    ]
+
+
+class GqaPagedKv(ctypes.Structure):
+    _fields_ = [
+        ("block_stride", ctypes.c_int64),
+        ("head_stride", ctypes.c_int64),
+        ("pos_stride", ctypes.c_int64),
+        ("block_size", ctypes.c_int32),
+        ("max_blocks", ctypes.c_int32),
+        ("n_blocks", ctypes.c_int32),
     ]
 
 
@@ -108,6 +122,17 @@ def lib() -> ctypes.CDLL:
                                   ctypes.POINTER(GqaKvLayout), vp, vp, ctypes.c_int32, vp, vp,
                                   ctypes.c_size_t, vp]
     L.gqa_decode_bf16.restype = ctypes.c_int
+    L.gqa_decode_paged_workspace_bytes.argtypes = [ctypes.POINTER(GqaParams), ctypes.c_int32,
+                                                   ctypes.c_int32]
+    L.gqa_decode_paged_workspace_bytes.restype = ctypes.c_size_t
+    L.gqa_decode_paged_bf16.argtypes = [ctypes.POINTER(GqaParams), vp, vp, vp,
+                                        ctypes.POINTER(GqaPagedKv), vp, vp, vp, ctypes.c_int32, vp,
+                                        vp, ctypes.c_size_t, vp]
+    L.gqa_decode_paged_bf16.restype = ctypes.c_int
+    L.gqa_kv_append_paged_bf16.argtypes = [ctypes.POINTER(GqaParams), vp, vp, vp, vp,
+                                           ctypes.POINTER(GqaPagedKv), vp, vp, ctypes.c_int32,
+                                           ctypes.c_int32, vp]
+    L.gqa_kv_append_paged_bf16.restype = ctypes.c_int
     L.gqa_prefill_workspace_bytes.argtypes = [ctypes.POINTER(GqaParams), ctypes.c_int32,
                                               ctypes.c_int32]
     L.gqa_prefill_workspace_bytes.restype = ctypes.c_size_t

@@ -18,7 +18,7 @@ from typing import Optional, Sequence, Union
 import torch
 
 from . import _lib
-from ._lib import GQA_ROPE_K, GQA_ROPE_Q, GqaKvLayout, GqaParams, check, lib
+from ._lib import GQA_ROPE_K, GQA_ROPE_Q, GqaKvLayout, GqaPagedKv, GqaParams, check, lib
 
 N_Q_HEADS = 32
 N_KV_HEADS = 8
@@ -326,6 +326,95 @@ def kv_append(k_new: torch.Tensor, v_new: torch.Tensor, k_cache: torch.Tensor,
                                       k_cache.data_ptr(), v_cache.data_ptr(), ctypes.byref(layout),
                                       st.data_ptr(), batch, n_new, _stream_handle(k_new.device))
     check(status, "gqa_kv_append_bf16")
+
+
+BLOCK_SIZE = 16   # positions per block of a paged cache (the core's KV_BLOCK_LEN)
+
+
+def _paged_layout(k_pool: torch.Tensor, v_pool: torch.Tensor, block_table: torch.Tensor
+                  ) -> GqaPagedKv:
+    """Pools [n_blocks, 8, 16, 128] bfloat16 (any strides with contiguous rows), block
+    table [B, max_blocks] int32 on the device."""
+    if k_pool.dim() != 4 or k_pool.shape != v_pool.shape or k_pool.stride() != v_pool.stride():
+        raise ValueError("k_pool and v_pool must be [n_blocks,8,16,128] with the same strides")
+    if k_pool.shape[2] != BLOCK_SIZE:
+        raise ValueError(f"blocks hold {BLOCK_SIZE} positions")
+    for name, t in (("k_pool", k_pool), ("v_pool", v_pool)):
+        if t.dtype != torch.bfloat16 or not t.is_cuda:
+            raise ValueError(f"{name} must be a bfloat16 tensor on the GPU")
+    if k_pool.stride(3) != 1:
+        raise ValueError("pool rows must be contiguous in head_dim")
+    if block_table.dim() != 2 or block_table.dtype != torch.int32 or not block_table.is_cuda:
+        raise ValueError("block_table must be an int32 [B, max_blocks] tensor on the GPU")
+    return GqaPagedKv(k_pool.stride(0), k_pool.stride(1), k_pool.stride(2), BLOCK_SIZE,
+                      block_table.shape[1], k_pool.shape[0])
+
+
+def gqa_decode_paged(q: torch.Tensor, k_pool: torch.Tensor, v_pool: torch.Tensor,
+                     block_table: torch.Tensor, query_position: Lengths, seq_len: Lengths, *,
+                     rope_q: bool = True, rope_k: bool = False, theta: float = ROPE_THETA,
+                     scale: Optional[float] = None, out: Optional[torch.Tensor] = None,
+                     workspace: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """gqa_attention over a paged cache: q [B, 32, 128]; k_pool, v_pool [n_blocks, 8, 16,
+    128]; block_table [B, max_blocks] int32 (block j of sequence b holds positions
+    16j .. 16j+15).  Host lengths are checked against capacity = 16 * max_blocks."""
+    if q.dim() != 3 or q.dtype != torch.bfloat16 or not q.is_cuda:
+        raise ValueError("q must be a bfloat16 [B,32,128] tensor on the GPU")
+    layout = _paged_layout(k_pool, v_pool, block_table)
+    batch = q.shape[0]
+    if block_table.shape[0] != batch:
+        raise ValueError("block_table has one row per sequence")
+    capacity = BLOCK_SIZE * block_table.shape[1]
+    device = q.device
+    p = make_params(rope_q=rope_q, rope_k=rope_k, theta=theta, scale=scale)
+    sl_dev, sl_host = _lengths_to_device(seq_len, batch, device, "seq_len")
+    qp_dev, qp_host = _lengths_to_device(query_position, batch, device, "query_position")
+    if sl_host is not None and qp_host is not None:
+        check(lib().gqa_validate_lengths(
+            ctypes.cast(sl_host.data_ptr(), ctypes.POINTER(ctypes.c_int32)),
+            ctypes.cast(qp_host.data_ptr(), ctypes.POINTER(ctypes.c_int32)), batch, capacity),
+            "gqa_validate_lengths")
+    ws_bytes = int(lib().gqa_decode_paged_workspace_bytes(ctypes.byref(p), batch,
+                                                          block_table.shape[1]))
+    if ws_bytes == 0:
+        check(_lib.GQA_ERR_INVALID_CONFIG, "gqa_decode_paged_workspace_bytes")
+    if workspace is None:
+        workspace = torch.empty(ws_bytes, dtype=torch.uint8, device=device)
+    elif workspace.numel() * workspace.element_size() < ws_bytes:
+        raise ValueError(f"workspace holds {workspace.numel() * workspace.element_size()} bytes; "
+                         f"{ws_bytes} needed")
+    if out is None:
+        out = torch.empty((batch, N_Q_HEADS, HEAD_DIM), dtype=torch.bfloat16, device=device)
+    q = q.contiguous()
+    bt = block_table.contiguous()
+    status = lib().gqa_decode_paged_bf16(
+        ctypes.byref(p), q.data_ptr(), k_pool.data_ptr(), v_pool.data_ptr(), ctypes.byref(layout),
+        bt.data_ptr(), sl_dev.data_ptr(), qp_dev.data_ptr(), batch, out.data_ptr(),
+        workspace.data_ptr(), workspace.numel() * workspace.element_size(), _stream_handle(device))
+    check(status, "gqa_decode_paged_bf16")
+    return out
+
+
+def kv_append_paged(k_new: torch.Tensor, v_new: torch.Tensor, k_pool: torch.Tensor,
+                    v_pool: torch.Tensor, block_table: torch.Tensor, start: Lengths, *,
+                    rope_k: bool = True, theta: float = ROPE_THETA) -> None:
+    """kv_append into a paged cache (rows to block block_table[b][(start+t)//16])."""
+    if k_new.dim() != 4 or v_new.shape != k_new.shape:
+        raise ValueError("expected k_new/v_new [B,T,8,128]")
+    for name, t in (("k_new", k_new), ("v_new", v_new)):
+        if t.dtype != torch.bfloat16 or not t.is_cuda:
+            raise ValueError(f"{name} must be a bfloat16 tensor on the GPU")
+    layout = _paged_layout(k_pool, v_pool, block_table)
+    batch, n_new = k_new.shape[0], k_new.shape[1]
+    p = make_params(rope_q=False, rope_k=rope_k, theta=theta)
+    st = _start_tensor(start, batch, BLOCK_SIZE * block_table.shape[1], n_new, k_new.device)
+    k_new, v_new = k_new.contiguous(), v_new.contiguous()
+    bt = block_table.contiguous()
+    status = lib().gqa_kv_append_paged_bf16(ctypes.byref(p), k_new.data_ptr(), v_new.data_ptr(),
+                                            k_pool.data_ptr(), v_pool.data_ptr(), ctypes.byref(layout),
+                                            bt.data_ptr(), st.data_ptr(), batch, n_new,
+                                            _stream_handle(k_new.device))
+    check(status, "gqa_kv_append_paged_bf16")
 
 
 def validate_lengths(seq_len, query_position, capacity: int) -> None:

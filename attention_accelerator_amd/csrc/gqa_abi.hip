@@ -97,11 +97,11 @@ hipEvent_t* profile_slot() {
 
 }  // namespace
 
-DecodePlan plan_decode(int32_t batch, int32_t capacity) {
+DecodePlan plan_decode(int32_t batch, int32_t capacity, bool paged) {
     DecodePlan plan{};
     plan.n_wgs = stream_wgs();
     const int64_t keys_cap = static_cast<int64_t>(batch) * kHkv * capacity;
-    if (keys_cap <= single_launch_max_keys()) {
+    if (!paged && keys_cap <= single_launch_max_keys()) {
         // Single launch: about one 4-wave workgroup per CU (n_wgs / 4), pieces of at least
         // 128 keys (32 per wave) in multiples of 64, sized from the capacity (the lengths
         // live on the device); pieces past a sequence's length exit at once.
@@ -171,27 +171,16 @@ size_t gqa_decode_workspace_bytes(const gqa_params_t* params, int32_t batch, int
     return plan_decode(batch, capacity).workspace_bytes;
 }
 
-int gqa_decode_bf16(const gqa_params_t* params, const uint16_t* q, const uint16_t* k,
-                    const uint16_t* v, const gqa_kv_layout_t* kv, const int32_t* seq_len,
-                    const int32_t* query_pos, int32_t batch, uint16_t* out, void* workspace,
-                    size_t workspace_bytes, void* stream) {
-    if (!params || !kv) return GQA_ERR_BAD_POINTER;
-    if (!geometry_ok(params)) return GQA_ERR_INVALID_CONFIG;
-    if (batch <= 0 || kv->capacity <= 0) return GQA_ERR_INVALID_CONFIG;
-    if (kv->pos_stride < kD || kv->head_stride < 0 || kv->batch_stride < 0)
-        return GQA_ERR_INVALID_CONFIG;
-    if (!q || !k || !v || !out || !seq_len || !query_pos) return GQA_ERR_BAD_POINTER;
-    if (!aligned(q, 2) || !aligned(out, 4) || !aligned(k, 16) || !aligned(v, 16) ||
-        !aligned(seq_len, 4) || !aligned(query_pos, 4))
-        return GQA_ERR_BAD_POINTER;
-    if (kv->pos_stride % 8 || kv->head_stride % 8 || kv->batch_stride % 8) return GQA_ERR_BAD_POINTER;
-    // Rows of one (sequence, KV head) are addressed with 32-bit byte offsets, which run
-    // up to 64 rows past the last valid one (prefetch offsets, clamped before use).
-    if ((static_cast<uint64_t>(kv->capacity) + 64u) * static_cast<uint64_t>(kv->pos_stride) * 2u >
-        0xFFFFFF00ull)
-        return GQA_ERR_INVALID_CONFIG;
+}  // extern "C"
 
-    const DecodePlan plan = plan_decode(batch, kv->capacity);
+namespace {
+
+// Common tail of the contiguous and paged decode entry points: workspace carve-up and launch.
+int decode_launch(const gqa_params_t* params, const uint16_t* q, const uint16_t* k, const uint16_t* v,
+                  int64_t s0, int64_t s1, int64_t s2, int32_t capacity, const int32_t* block_table,
+                  int32_t max_blocks, int32_t n_blocks, const int32_t* seq_len, const int32_t* query_pos,
+                  int32_t batch, uint16_t* out, void* workspace, size_t workspace_bytes, void* stream) {
+    const DecodePlan plan = plan_decode(batch, capacity, block_table != nullptr);
     if (!workspace || workspace_bytes < plan.workspace_bytes || !aligned(workspace, 256))
         return GQA_ERR_WORKSPACE;
 
@@ -212,10 +201,13 @@ int gqa_decode_bf16(const gqa_params_t* params, const uint16_t* q, const uint16_
     a.seg_count = reinterpret_cast<unsigned long long*>(pl + plan.plan_bytes);
     a.pieces_cap = plan.pieces_cap;
     a.piece_keys = plan.piece_keys;
-    a.kv_batch_stride = kv->batch_stride;
-    a.kv_head_stride = kv->head_stride;
-    a.kv_pos_stride = kv->pos_stride;
-    a.capacity = kv->capacity;
+    a.block_table = block_table;
+    a.max_blocks = max_blocks;
+    a.n_blocks = n_blocks;
+    a.kv_batch_stride = s0;
+    a.kv_head_stride = s1;
+    a.kv_pos_stride = s2;
+    a.capacity = capacity;
     a.batch = batch;
     a.n_wgs = plan.n_wgs;
     a.qk_scale_log2 = static_cast<double>(params->scale) * 1.4426950408889634;
@@ -223,6 +215,62 @@ int gqa_decode_bf16(const gqa_params_t* params, const uint16_t* q, const uint16_
     fill_rope_table(params->rope_theta, &a.rope);
     const hipError_t e = launch_decode(a, batch, static_cast<hipStream_t>(stream), profile_slot());
     return e == hipSuccess ? GQA_OK : GQA_ERR_HIP;
+}
+
+bool paged_layout_ok(const gqa_paged_kv_t* kv) {
+    return kv->block_size == 16 && kv->max_blocks > 0 && kv->n_blocks > 0 && kv->pos_stride >= kD &&
+           kv->head_stride >= 0 && kv->block_stride >= 0 &&
+           static_cast<int64_t>(kv->max_blocks) * 16 <= 0x7FFFFFFF;
+}
+
+}  // namespace
+
+extern "C" {
+
+int gqa_decode_bf16(const gqa_params_t* params, const uint16_t* q, const uint16_t* k,
+                    const uint16_t* v, const gqa_kv_layout_t* kv, const int32_t* seq_len,
+                    const int32_t* query_pos, int32_t batch, uint16_t* out, void* workspace,
+                    size_t workspace_bytes, void* stream) {
+    if (!params || !kv) return GQA_ERR_BAD_POINTER;
+    if (!geometry_ok(params)) return GQA_ERR_INVALID_CONFIG;
+    if (batch <= 0 || kv->capacity <= 0) return GQA_ERR_INVALID_CONFIG;
+    if (kv->pos_stride < kD || kv->head_stride < 0 || kv->batch_stride < 0)
+        return GQA_ERR_INVALID_CONFIG;
+    if (!q || !k || !v || !out || !seq_len || !query_pos) return GQA_ERR_BAD_POINTER;
+    if (!aligned(q, 2) || !aligned(out, 4) || !aligned(k, 16) || !aligned(v, 16) ||
+        !aligned(seq_len, 4) || !aligned(query_pos, 4))
+        return GQA_ERR_BAD_POINTER;
+    if (kv->pos_stride % 8 || kv->head_stride % 8 || kv->batch_stride % 8) return GQA_ERR_BAD_POINTER;
+    // Rows of one (sequence, KV head) are addressed with 32-bit byte offsets, which run
+    // up to 64 rows past the last valid one (prefetch offsets, clamped before use).
+    if ((static_cast<uint64_t>(kv->capacity) + 64u) * static_cast<uint64_t>(kv->pos_stride) * 2u >
+        0xFFFFFF00ull)
+        return GQA_ERR_INVALID_CONFIG;
+    return decode_launch(params, q, k, v, kv->batch_stride, kv->head_stride, kv->pos_stride, kv->capacity,
+                         nullptr, 0, 0, seq_len, query_pos, batch, out, workspace, workspace_bytes, stream);
+}
+
+size_t gqa_decode_paged_workspace_bytes(const gqa_params_t* params, int32_t batch, int32_t max_blocks) {
+    if (!params || !geometry_ok(params) || batch <= 0 || max_blocks <= 0 ||
+        static_cast<int64_t>(max_blocks) * 16 > 0x7FFFFFFF)
+        return 0;
+    return plan_decode(batch, max_blocks * 16, true).workspace_bytes;
+}
+
+int gqa_decode_paged_bf16(const gqa_params_t* params, const uint16_t* q, const uint16_t* k_pool,
+                          const uint16_t* v_pool, const gqa_paged_kv_t* kv, const int32_t* block_table,
+                          const int32_t* seq_len, const int32_t* query_pos, int32_t batch, uint16_t* out,
+                          void* workspace, size_t workspace_bytes, void* stream) {
+    if (!params || !kv) return GQA_ERR_BAD_POINTER;
+    if (!geometry_ok(params) || batch <= 0 || !paged_layout_ok(kv)) return GQA_ERR_INVALID_CONFIG;
+    if (!q || !k_pool || !v_pool || !out || !seq_len || !query_pos || !block_table) return GQA_ERR_BAD_POINTER;
+    if (!aligned(q, 2) || !aligned(out, 4) || !aligned(k_pool, 16) || !aligned(v_pool, 16) ||
+        !aligned(seq_len, 4) || !aligned(query_pos, 4) || !aligned(block_table, 4))
+        return GQA_ERR_BAD_POINTER;
+    if (kv->pos_stride % 8 || kv->head_stride % 8 || kv->block_stride % 8) return GQA_ERR_BAD_POINTER;
+    return decode_launch(params, q, k_pool, v_pool, kv->block_stride, kv->head_stride, kv->pos_stride,
+                         kv->max_blocks * 16, block_table, kv->max_blocks, kv->n_blocks, seq_len, query_pos,
+                         batch, out, workspace, workspace_bytes, stream);
 }
 
 int gqa_profile_enable(int32_t max_calls) {
@@ -352,6 +400,26 @@ int gqa_kv_append_bf16(const gqa_params_t* params, const uint16_t* k_new, const 
     const int st = prefill_args(params, k_new, v_new, k_cache, v_cache, kv, start, batch, n_new, a);
     if (st != GQA_OK) return st;
     a.k_split = nullptr;
+    const hipError_t e = launch_kv_append(a, static_cast<hipStream_t>(stream));
+    return e == hipSuccess ? GQA_OK : GQA_ERR_HIP;
+}
+
+int gqa_kv_append_paged_bf16(const gqa_params_t* params, const uint16_t* k_new, const uint16_t* v_new,
+                             uint16_t* k_pool, uint16_t* v_pool, const gqa_paged_kv_t* kv,
+                             const int32_t* block_table, const int32_t* start, int32_t batch, int32_t n_new,
+                             void* stream) {
+    if (!kv) return GQA_ERR_BAD_POINTER;
+    if (!paged_layout_ok(kv)) return GQA_ERR_INVALID_CONFIG;
+    if (!block_table) return GQA_ERR_BAD_POINTER;
+    if (!aligned(block_table, 4)) return GQA_ERR_BAD_POINTER;
+    gqa_kv_layout_t lay{kv->block_stride, kv->head_stride, kv->pos_stride, kv->max_blocks * 16};
+    PrefillArgs a;
+    const int st = prefill_args(params, k_new, v_new, k_pool, v_pool, &lay, start, batch, n_new, a);
+    if (st != GQA_OK) return st;
+    a.k_split = nullptr;
+    a.block_table = block_table;
+    a.max_blocks = kv->max_blocks;
+    a.n_blocks = kv->n_blocks;
     const hipError_t e = launch_kv_append(a, static_cast<hipStream_t>(stream));
     return e == hipSuccess ? GQA_OK : GQA_ERR_HIP;
 }

@@ -77,13 +77,20 @@ __device__ __forceinline__ int64_t wave_incl_scan_i64(int64_t x, int lane) {
     return x;
 }
 
+// Keys of sequence b's segments in the stream-K key space: n_valid, rounded up to the
+// 16-position block for a paged cache so that every piece starts on a block.
+__device__ __forceinline__ int plan_keys(const DecodeArgs& a, int b) {
+    const int nv = seq_valid_keys(a, b);
+    return a.block_table ? (nv + kChunk - 1) / kChunk * kChunk : nv;
+}
+
 // Total keys over all segments (8 per sequence) and the per-workgroup range size.
 __device__ __forceinline__ void stream_totals(const DecodeArgs& a, int lane, int64_t& total,
                                               int64_t& per_wg) {
     int64_t t = 0;
     for (int base = 0; base < a.batch; base += kWave) {
         const int b = base + lane;
-        t += wave_sum_i64(b < a.batch ? seq_valid_keys(a, b) : 0);
+        t += wave_sum_i64(b < a.batch ? plan_keys(a, b) : 0);
     }
     total = t * kHkv;
     int64_t per = (total + a.n_wgs - 1) / a.n_wgs;
@@ -378,7 +385,7 @@ __device__ __forceinline__ void build_plan(const DecodeArgs& a, int lane) {
     int64_t carry = 0;
     for (int base = 0; base < a.batch; base += kWave) {
         const int b = base + lane;
-        const int nv = b < a.batch ? seq_valid_keys(a, b) : 0;
+        const int nv = b < a.batch ? plan_keys(a, b) : 0;
         const int64_t incl = wave_incl_scan_i64(nv, lane) + carry;
         if (b < a.batch) a.seq_off[b] = (incl - nv) * kHkv;
         carry = __shfl(incl, kWave - 1);
@@ -641,6 +648,170 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(1))) void
     }
 }
 
+
+// ---------------------------------------------------------------------------------
+// Paged cache (block tables).  The pool holds blocks of 16 positions -- the reference
+// core's KV_BLOCK_LEN (gqa_controller.v:20) -- and block j of sequence b is pool block
+// block_table[b][j]; block id, KV head and position address a row as
+// id*block_stride + h*head_stride + p*pos_stride.  The stream-K key space pads every
+// segment to whole blocks, so each piece starts on a block and each 16-key chunk is one
+// (block, KV head): 4 KB of K and 4 KB of V at one place.  Block ids are requested two
+// chunks ahead of the chunk that needs them.  An id outside [0, n_blocks) reads block 0
+// instead and turns that sequence's rows into NaN (never an out-of-range read).
+
+// Block id of block j of sequence b, as a (lane-uniform) vector load: its value is made
+// scalar only where it is used, so that waiting for it never waits for loads issued
+// after it.
+__device__ __forceinline__ int load_block_id(const DecodeArgs& a, int b, int j) {
+    return a.block_table[static_cast<int64_t>(b) * a.max_blocks + j];
+}
+
+// Pool element offset of (block id, KV head kvh); ids outside the pool read block 0 and
+// clear `ok`.
+__device__ __forceinline__ int64_t page_elem(const DecodeArgs& a, int id_vgpr, int kvh, bool& ok) {
+    const int pid = __builtin_amdgcn_readfirstlane(id_vgpr);
+    ok = pid >= 0 && pid < a.n_blocks;
+    return static_cast<int64_t>(ok ? pid : 0) * a.kv_batch_stride + static_cast<int64_t>(kvh) * a.kv_head_stride;
+}
+
+// K and V rows of one block-chunk: lane rows clamped to the chunk's last valid row.
+__device__ __forceinline__ void load_page_chunk(const DecodeArgs& a, int64_t elem, int rows_valid, int n,
+                                                int g, Chunk& c) {
+    const char* kp = reinterpret_cast<const char*>(a.k + elem);
+    const char* vp = reinterpret_cast<const char*>(a.v + elem);
+    const uint32_t row = static_cast<uint32_t>(a.kv_pos_stride) * 2u;
+    const int r_last = rows_valid - 1;
+    const char* krow = kp + static_cast<uint32_t>(min(n, r_last)) * row + 16u * g;
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb) c.kw[kb] = load_stream16(krow + 64 * kb);
+#pragma unroll
+    for (int it = 0; it < 4; ++it)
+        c.vw[it] = load_stream16(vp + static_cast<uint32_t>(min(4 * g + it, r_last)) * row + 16u * n);
+}
+
+template <bool kRopeK>
+__device__ __forceinline__ void process_page_piece(const DecodeArgs& a, int b, int kvh, int nvp, int nreal,
+                                                   int k_a, int k_b, int64_t wg) {
+    const int lane = threadIdx.x & (kWave - 1);
+    const int n = lane & 15;
+    const int g = lane >> 4;
+    const int kend = min(k_b, nreal);          // keys past n_valid are block padding
+    PieceState st;
+#pragma unroll
+    for (int h = 0; h < kGroup; ++h)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) st.acc[h][j] = 0.0;
+    st.m_run = -INFINITY;
+    st.l_run = 0.f;
+    bool all_ok = true;
+    if (k_a < kend) {
+        const int j0 = k_a / kChunk;
+        const int jn = (kend - 1) / kChunk;    // last block holding a key of this piece
+        const int n_chunks = jn - j0 + 1;
+        bool ok;
+        Chunk c0, c1;
+        // Block ids are requested two chunks ahead of the chunk whose loads need them, each
+        // before that iteration's data loads: waiting for one never waits for data that
+        // is still meant to be in flight.
+        const int id_first = load_block_id(a, b, j0);
+        int id_next = load_block_id(a, b, min(j0 + 1, jn));
+        load_page_chunk(a, page_elem(a, id_first, kvh, ok), min(kChunk, kend - j0 * kChunk), n, g, c0);
+        all_ok = all_ok && ok;
+        bf16x8_t bq[4];
+        load_q_operands(a, b, kvh, bq);
+        // One exit, at the end: chunks past the piece's last re-read its last block
+        // (clamped, unconditional loads) and are not computed, so that every path into
+        // the loop head has the same loads in flight.
+        for (int i = 0;; i += 2) {
+            {
+                const int j = min(j0 + i + 1, jn);
+                const int id_after = load_block_id(a, b, min(j + 1, jn));
+                load_page_chunk(a, page_elem(a, id_next, kvh, ok), min(kChunk, kend - j * kChunk), n, g, c1);
+                all_ok = all_ok && ok;
+                id_next = id_after;
+            }
+            compute_chunk<kRopeK>(a, k_a + i * kChunk, kend, n, g, c0, bq, st);
+            {
+                const int j = min(j0 + i + 2, jn);
+                const int id_after = load_block_id(a, b, min(j + 1, jn));
+                load_page_chunk(a, page_elem(a, id_next, kvh, ok), min(kChunk, kend - j * kChunk), n, g, c0);
+                all_ok = all_ok && ok;
+                id_next = id_after;
+            }
+            if (i + 1 < n_chunks) compute_chunk<kRopeK>(a, k_a + (i + 1) * kChunk, kend, n, g, c1, bq, st);
+            if (i + 2 >= n_chunks) break;
+        }
+    }
+    float m_tot[kGroup];
+    double l_tot[kGroup];
+    merge_rows(st, m_tot, l_tot);
+    if (!all_ok) {
+        // an invalid block id: poison the sequence's rows of this segment
+#pragma unroll
+        for (int h = 0; h < kGroup; ++h) {
+            m_tot[h] = 0.f;
+            l_tot[h] = __longlong_as_double(0x7ff8000000000000ll);
+        }
+    }
+    if (k_a == 0 && k_b == nvp) {
+        write_rows(a, b, kvh, st, l_tot);      // the whole segment
+        return;
+    }
+    write_partial(a, wg + static_cast<int64_t>(b) * kHkv + kvh, st, m_tot, l_tot);
+}
+
+template <bool kRopeK>
+__global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(1))) void decode_paged_stream_kernel(DecodeArgs a) {
+    const int64_t w = blockIdx.x;
+    const int lane = threadIdx.x;
+    const int64_t total = a.plan_hdr[0];
+    const int64_t per_wg = a.plan_hdr[1];
+    int64_t x = w * per_wg;
+    if (x >= total) return;
+    const int64_t x_end = min(x + per_wg, total);
+
+    // Start sequence: the last b with seq_off[b] <= x (it has keys, since x < total).
+    int b = 0;
+    int64_t off = 0, next = 0;
+    for (int base = 0; base < a.batch; base += kWave) {
+        const int bb = base + lane;
+        const int64_t o = bb < a.batch ? a.seq_off[bb] : INT64_MAX;
+        const int64_t o1 = bb < a.batch ? a.seq_off[bb + 1] : INT64_MAX;
+        const uint64_t le = __ballot(o <= x);
+        if (le) {
+            const int j = 63 - __clzll(static_cast<long long>(le));
+            b = base + j;
+            off = __shfl(o, j);
+            next = __shfl(o1, j);
+        }
+    }
+    int nvp = static_cast<int>((next - off) / kHkv);
+    const int64_t rel = x - off;
+    int kvh = 0;
+#pragma unroll
+    for (int k = 1; k < kHkv; ++k) kvh += rel >= static_cast<int64_t>(k) * nvp;
+    int key = static_cast<int>(rel - static_cast<int64_t>(kvh) * nvp);
+    while (true) {
+        b = __builtin_amdgcn_readfirstlane(b);
+        kvh = __builtin_amdgcn_readfirstlane(kvh);
+        key = __builtin_amdgcn_readfirstlane(key);
+        nvp = __builtin_amdgcn_readfirstlane(nvp);
+        const int k_b = __builtin_amdgcn_readfirstlane(
+            static_cast<int>(min(static_cast<int64_t>(nvp), key + (x_end - x))));
+        const int nreal = __builtin_amdgcn_readfirstlane(seq_valid_keys(a, b));
+        process_page_piece<kRopeK>(a, b, kvh, nvp, nreal, key, k_b, w);
+        x += k_b - key;
+        if (x >= x_end) break;
+        key = 0;
+        if (++kvh == kHkv) {
+            kvh = 0;
+            nvp = 0;
+            while (nvp == 0 && ++b < a.batch) nvp = plan_keys(a, b);
+            if (nvp == 0) break;   // lengths changed under the launch; nothing left to read
+        }
+    }
+}
+
 // Merge the pieces of multi-piece segments: one 4-wave workgroup per (KV head,
 // sequence), wave h for Q head 4*kvh + h.  Slots w + seg for w in [w_first, w_last]
 // hold the pieces of segment seg; their (m, l) are read one per lane, the weights
@@ -690,9 +861,10 @@ __global__ __launch_bounds__(kGroup * kWave) void decode_merge_kernel(DecodeArgs
                     o1 = ldexp(o1, e);
                 }
                 mx = m_new;
-                if (lane < cnt) l += ldexp(static_cast<double>(ml.y), static_cast<int>(ml.x - mx));
+                if (lane < cnt && ml.x != -INFINITY) l += ldexp(static_cast<double>(ml.y), static_cast<int>(ml.x - mx));
             }
-            const int e_lane = lane < cnt ? static_cast<int>(ml.x - mx) : -1100;
+            // a piece holding no key (padding of a paged segment) has m = -inf: weight 0
+            const int e_lane = lane < cnt && ml.x != -INFINITY ? static_cast<int>(ml.x - mx) : -1100;
 #pragma unroll
             for (int u = 0; u < 8; ++u) {
                 const int ee = __shfl(e_lane, min(q + u, kWave - 1));
@@ -948,8 +1120,8 @@ hipError_t launch_zero_words(uint32_t* p, int64_t n, hipStream_t stream) {
 
 hipError_t launch_decode(const DecodeArgs& a, int batch, hipStream_t stream, hipEvent_t* ev) {
     const bool rq = (a.flags & 1u) != 0, rk = (a.flags & 2u) != 0;
-    if (a.pieces_cap > 0) {
-        // Single launch (small batches).
+    if (a.pieces_cap > 0 && !a.block_table) {
+        // Single launch (small batches, contiguous cache).
         if (ev) (void)hipEventRecord(ev[0], stream);
         const dim3 grid(a.pieces_cap, batch * kHkv);
         if (rq && rk)
@@ -974,10 +1146,16 @@ hipError_t launch_decode(const DecodeArgs& a, int batch, hipStream_t stream, hip
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     if (ev) (void)hipEventRecord(ev[0], stream);
-    if (rk)
+    if (a.block_table) {
+        if (rk)
+            hipLaunchKernelGGL((decode_paged_stream_kernel<true>), dim3(a.n_wgs), dim3(kWave), 0, stream, a);
+        else
+            hipLaunchKernelGGL((decode_paged_stream_kernel<false>), dim3(a.n_wgs), dim3(kWave), 0, stream, a);
+    } else if (rk) {
         hipLaunchKernelGGL((decode_stream_kernel<true>), dim3(a.n_wgs), dim3(kWave), 0, stream, a);
-    else
+    } else {
         hipLaunchKernelGGL((decode_stream_kernel<false>), dim3(a.n_wgs), dim3(kWave), 0, stream, a);
+    }
     e = hipGetLastError();
     if (e != hipSuccess) return e;
     if (ev) (void)hipEventRecord(ev[1], stream);

@@ -22,10 +22,13 @@ struct DecodeArgs {
     double* part_o;           // [n_slots][4][128] unnormalised partial outputs
     float2* part_ml;          // [n_slots][4] (integer-valued running max in log2 units, sum)
     unsigned long long* seg_count;  // [B*8] pieces finished per segment, single-launch path (zero between calls)
-    int64_t kv_batch_stride;
+    const int32_t* block_table;  // paged cache: [B][max_blocks] block ids (nullptr: contiguous cache)
+    int64_t kv_batch_stride;  // contiguous: elements per sequence; paged: per block of the pool
     int64_t kv_head_stride;
     int64_t kv_pos_stride;
-    int32_t capacity;
+    int32_t capacity;         // positions per sequence (paged: max_blocks * 16)
+    int32_t max_blocks;       // paged: block-table entries per sequence
+    int32_t n_blocks;         // paged: blocks in the pool (ids outside [0, n_blocks) poison the row)
     int32_t batch;
     int32_t n_wgs;            // persistent workgroups of the stream kernel
     int32_t pieces_cap;       // > 0: single-launch path, pieces per segment (grid x)
@@ -50,7 +53,7 @@ struct DecodePlan {
     size_t workspace_bytes;
 };
 
-DecodePlan plan_decode(int32_t batch, int32_t capacity);
+DecodePlan plan_decode(int32_t batch, int32_t capacity, bool paged = false);
 // ev (optional): three events recorded before the split kernel, between the two
 // kernels and after the combine kernel.
 hipError_t launch_decode(const DecodeArgs& a, int batch, hipStream_t stream,
@@ -78,7 +81,11 @@ struct PrefillArgs {
     const uint16_t* k_new;    // [B][T][8][128] new K rows as given (unrotated when RoPE on K)
     const uint16_t* v_new;    // [B][T][8][128]
     uint16_t* k;              // cache, rows at b*kv_batch_stride + h*kv_head_stride + p*kv_pos_stride
-    uint16_t* v;
+    uint16_t* v;              // (paged: block_table[b][p/16]*kv_batch_stride + h*kv_head_stride
+                              //  + (p%16)*kv_pos_stride)
+    const int32_t* block_table;  // paged cache: [B][max_blocks] (nullptr: contiguous)
+    int32_t max_blocks;
+    int32_t n_blocks;
     const int32_t* start;     // [B] cached positions before the chunk (device)
     uint16_t* out;            // [B][T][32][128]
     uint16_t* k_split;        // [2][B][T][8][128] second and third BF16 parts of the rotated new K

@@ -62,7 +62,15 @@ __device__ __forceinline__ bool prefill_start_ok(const PrefillArgs& a, int st) {
     return st >= 0 && st <= a.capacity - a.n_new;
 }
 
+// Element offset of cache row (b, h, p); -1 for a paged cache whose block id for p is
+// outside the pool.
 __device__ __forceinline__ int64_t cache_elem(const PrefillArgs& a, int b, int h, int64_t p) {
+    if (a.block_table) {
+        const int pid = a.block_table[static_cast<int64_t>(b) * a.max_blocks + p / 16];
+        if (pid < 0 || pid >= a.n_blocks) return -1;
+        return static_cast<int64_t>(pid) * a.kv_batch_stride + static_cast<int64_t>(h) * a.kv_head_stride +
+               (p % 16) * a.kv_pos_stride;
+    }
     return static_cast<int64_t>(b) * a.kv_batch_stride + static_cast<int64_t>(h) * a.kv_head_stride +
            p * a.kv_pos_stride;
 }
@@ -97,12 +105,15 @@ __global__ __launch_bounds__(256) void kv_append_kernel(PrefillArgs a) {
             yr = x * sn + y * cs;
         }
         const uint16_t hx = bf16_of(xr), hy = bf16_of(yr);
-        uint16_t* kdst = a.k + cache_elem(a, b, kvh, pos);
-        uint16_t* vdst = a.v + cache_elem(a, b, kvh, pos);
-        kdst[lane] = hx;
-        kdst[lane + kPairs] = hy;
-        vdst[lane] = vsrc[lane];
-        vdst[lane + kPairs] = vsrc[lane + kPairs];
+        const int64_t ce = cache_elem(a, b, kvh, pos);
+        if (ce >= 0) {
+            uint16_t* kdst = a.k + ce;
+            uint16_t* vdst = a.v + ce;
+            kdst[lane] = hx;
+            kdst[lane + kPairs] = hy;
+            vdst[lane] = vsrc[lane];
+            vdst[lane + kPairs] = vsrc[lane + kPairs];
+        }
         if (a.k_split) {
             const double rx = xr - f64_of_bf16(hx), ry = yr - f64_of_bf16(hy);
             const uint16_t mx = bf16_of(rx), my = bf16_of(ry);

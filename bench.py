@@ -38,6 +38,8 @@ WORKLOADS = {
     "decode_b64_ragged_512_8192": (64, 8192, 512, 8192),
     "decode_b1_4096": (1, 4096, None, None),
     "decode_b8_131072": (8, 131072, None, None),
+    # the north-star batch through a paged cache (blocks of 16 positions, shuffled pool)
+    "decode_paged_b64_ragged_512_8192": (64, 8192, 512, 8192),
 }
 PREFILL_WORKLOADS = {
     # name: (batch, new tokens, cached positions)
@@ -242,8 +244,29 @@ def main() -> int:
     step_bytes = stimulus.algorithmic_bytes_decode(lens)
     # The split kernel reads K/V rows, Q rows and the lengths; the combine writes O.
     split_bytes = step_bytes - bsz * stimulus.N_Q_HEADS * stimulus.HEAD_DIM * 2
-    call = PreparedDecode(batch.q, batch.k, batch.v, batch.query_pos.to(dev),
-                          batch.seq_len.to(dev))
+    if args.workload.startswith("decode_paged"):
+        # Scatter every (sequence, 16-position block) to a random pool block.
+        nb = cap // 16
+        kp = batch.k.view(bsz, 8, nb, 16, 128).permute(0, 2, 1, 3, 4).reshape(bsz * nb, 8, 16, 128)
+        vp = batch.v.view(bsz, 8, nb, 16, 128).permute(0, 2, 1, 3, 4).reshape(bsz * nb, 8, 16, 128)
+        perm = torch.randperm(bsz * nb, generator=torch.Generator().manual_seed(args.seed)).to(dev)
+        k_pool = torch.empty_like(kp)
+        v_pool = torch.empty_like(vp)
+        k_pool[perm] = kp
+        v_pool[perm] = vp
+        table = perm.view(bsz, nb).to(torch.int32).contiguous()
+        del kp, vp
+        qp_dev, sl_dev = batch.query_pos.to(dev), batch.seq_len.to(dev)
+        ws = torch.empty(gqa.attention.decode_workspace_bytes(bsz, cap), dtype=torch.uint8,
+                         device=dev)
+        out = torch.empty((bsz, 32, 128), dtype=torch.bfloat16, device=dev)
+
+        def call():
+            gqa.gqa_decode_paged(batch.q, k_pool, v_pool, table, qp_dev, sl_dev, out=out,
+                                 workspace=ws)
+    else:
+        call = PreparedDecode(batch.q, batch.k, batch.v, batch.query_pos.to(dev),
+                              batch.seq_len.to(dev))
     print(f"[bench] {args.workload}: B={bsz} keys={sum(lens)} bytes/step={step_bytes}",
           file=sys.stderr, flush=True)
 

@@ -127,6 +127,41 @@ int gqa_decode_bf16(const gqa_params_t* params, const uint16_t* q, const uint16_
                     const int32_t* query_pos, int32_t batch, uint16_t* out, void* workspace,
                     size_t workspace_bytes, void* stream);
 
+/* Paged cache: a pool of blocks of 16 positions (the core's KV_BLOCK_LEN,
+ * gqa_controller.v:20); block j of sequence b is pool block block_table[b*max_blocks + j],
+ * and row (block id, KV head h, position-in-block r) starts at element
+ * id*block_stride + h*head_stride + r*pos_stride (each row 128 contiguous BF16, strides
+ * multiples of 8, pools 16-byte aligned).  [n_blocks][8][16][128] is the natural pool. */
+typedef struct gqa_paged_kv {
+    int64_t block_stride;
+    int64_t head_stride;
+    int64_t pos_stride;
+    int32_t block_size;   /* must be 16 */
+    int32_t max_blocks;   /* block-table entries per sequence; capacity = 16 * max_blocks */
+    int32_t n_blocks;     /* blocks in the pool */
+} gqa_paged_kv_t;
+
+/* Workspace bytes gqa_decode_paged_bf16 needs.  0 if the configuration is invalid. */
+size_t gqa_decode_paged_workspace_bytes(const gqa_params_t* params, int32_t batch, int32_t max_blocks);
+
+/* gqa_decode_bf16 over a paged cache: same arguments, results and rules, with the K/V
+ * pools and the block table (device, int32 [batch][max_blocks]) in place of the
+ * contiguous cache.  A block id outside [0, n_blocks) for a row the sequence needs gives
+ * NaN rows for that sequence (never an out-of-range read).  The workspace needs no
+ * particular contents.  Replaces the same start of axi_lite_regs.v:147-151, with the
+ * K/V stream fed block by block as the core's KV_BLOCK_LEN tiles. */
+int gqa_decode_paged_bf16(const gqa_params_t* params, const uint16_t* q, const uint16_t* k_pool,
+                          const uint16_t* v_pool, const gqa_paged_kv_t* kv, const int32_t* block_table,
+                          const int32_t* seq_len, const int32_t* query_pos, int32_t batch, uint16_t* out,
+                          void* workspace, size_t workspace_bytes, void* stream);
+
+/* gqa_kv_append_bf16 into a paged cache: rows go to block block_table[b][(start+t)/16],
+ * row (start+t)%16; rows whose block id is outside [0, n_blocks) are not written. */
+int gqa_kv_append_paged_bf16(const gqa_params_t* params, const uint16_t* k_new, const uint16_t* v_new,
+                             uint16_t* k_pool, uint16_t* v_pool, const gqa_paged_kv_t* kv,
+                             const int32_t* block_table, const int32_t* start, int32_t batch, int32_t n_new,
+                             void* stream);
+
 /* Chunked prefill: n_new query tokens per sequence, appended after start[b] cached
  * positions (the reference core computes one token per start; a chunk is that step for
  * tokens at positions start[b] .. start[b]+n_new-1 of one sequence,

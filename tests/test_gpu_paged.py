@@ -1,0 +1,142 @@
+"""Paged-cache decode and append against the oracle.
+
+The pools are built from contiguous caches by scattering every 16-position block of every
+(sequence, KV head) to a random pool block; the oracle reads the contiguous cache, so a
+wrong block, row or head lookup shows up as a parity failure.  Unused pool blocks hold
+NaN.  Tolerance: 64 BF16 ULP (pyfiles/check_gqa_output.py:33-34,57-64)."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import attention_accelerator_amd as gqa
+from attention_accelerator_amd import stimulus
+from oracle import oracle as orc
+from _util import assert_within_ulp, to_codes
+
+pytestmark = pytest.mark.gpu
+
+
+def _paginate(k, v, seq_len, seed, spare=7):
+    """k, v [B, 8, S, 128] -> pools [n_blocks, 8, 16, 128] and block table [B, S/16]
+    (entries past a sequence's blocks are -1)."""
+    bsz, _, cap, _ = k.shape
+    mb = (cap + 15) // 16
+    need = [(int(x) + 15) // 16 for x in seq_len]
+    n_blocks = sum(need) + spare
+    g = torch.Generator().manual_seed(seed)
+    ids = torch.randperm(n_blocks, generator=g)
+    kp = torch.full((n_blocks, 8, 16, 128), float("nan"), dtype=torch.bfloat16)
+    vp = torch.full_like(kp, float("nan"))
+    table = torch.full((bsz, mb), -1, dtype=torch.int32)
+    nxt = 0
+    for b in range(bsz):
+        for j in range(need[b]):
+            pid = int(ids[nxt])
+            nxt += 1
+            table[b, j] = pid
+            rows = slice(16 * j, min(16 * j + 16, cap))
+            n = rows.stop - rows.start
+            kp[pid, :, :n] = k[b, :, rows]
+            vp[pid, :, :n] = v[b, :, rows]
+    return kp, vp, table
+
+
+def _oracle(b: stimulus.DecodeBatch, **kw):
+    return orc.decode(to_codes(b.q), to_codes(b.k), to_codes(b.v), b.seq_len.numpy(),
+                      b.query_pos.numpy(), **kw)
+
+
+@pytest.mark.parametrize("bsz,cap,lo,seed", [(6, 3000, 1, 1), (3, 500, 15, 2), (2, 64, 16, 3)])
+def test_paged_matches_oracle_and_contiguous(dev, bsz, cap, lo, seed):
+    b = stimulus.decode_batch(bsz, cap, min_len=lo, max_len=cap, seed=seed)
+    kp, vp, table = _paginate(b.k, b.v, b.seq_len, seed)
+    got = to_codes(gqa.gqa_decode_paged(b.q.to(dev), kp.to(dev), vp.to(dev), table.to(dev),
+                                        b.query_pos, b.seq_len))
+    want = _oracle(b)
+    assert_within_ulp(want, got, 64, f"paged {bsz}x{cap}")
+    contiguous = to_codes(gqa.gqa_attention(b.q.to(dev), b.k.to(dev), b.v.to(dev), b.query_pos,
+                                            b.seq_len))
+    assert_within_ulp(contiguous, got, 2, "paged vs contiguous")
+
+
+def test_paged_causal_and_partial_blocks(dev):
+    """query_position < seq_len - 1: rows past the query are in the pool (NaN here) but
+    masked, including inside the query's own block."""
+    b = stimulus.decode_batch(4, 400, lengths=torch.tensor([400, 37, 129, 16]), seed=4)
+    qpos = torch.tensor([250, 20, 128, 3], dtype=torch.int32)
+    k, v = b.k.clone(), b.v.clone()
+    for i in range(4):
+        k[i, :, int(qpos[i]) + 1:] = float("nan")
+        v[i, :, int(qpos[i]) + 1:] = float("nan")
+    b = stimulus.DecodeBatch(b.q, k, v, b.seq_len, qpos)
+    kp, vp, table = _paginate(k, v, b.seq_len, 4)
+    got = to_codes(gqa.gqa_decode_paged(b.q.to(dev), kp.to(dev), vp.to(dev), table.to(dev),
+                                        qpos, b.seq_len))
+    assert np.isfinite(got.view(np.int16).astype(np.float32)).all()
+    assert_within_ulp(_oracle(b), got, 64, "paged causal")
+
+
+def test_paged_rope_on_k(dev):
+    b = stimulus.decode_batch(2, 700, min_len=300, max_len=700, seed=5)
+    kp, vp, table = _paginate(b.k, b.v, b.seq_len, 5)
+    got = to_codes(gqa.gqa_decode_paged(b.q.to(dev), kp.to(dev), vp.to(dev), table.to(dev),
+                                        b.query_pos, b.seq_len, rope_k=True))
+    assert_within_ulp(_oracle(b, rope_k=True), got, 64, "paged rope_k")
+
+
+def test_paged_invalid_block_id_gives_nan_rows(dev):
+    b = stimulus.decode_batch(3, 320, lengths=torch.tensor([300, 200, 100]), seed=6)
+    kp, vp, table = _paginate(b.k, b.v, b.seq_len, 6)
+    table[1, 5] = kp.shape[0] + 3                      # needed block of sequence 1: out of range
+    got = to_codes(gqa.gqa_decode_paged(b.q.to(dev), kp.to(dev), vp.to(dev), table.to(dev),
+                                        b.query_pos, b.seq_len))
+    bits = got[1].astype(np.uint32)
+    assert (((bits & 0x7F80) == 0x7F80) & ((bits & 0x7F) != 0)).all()   # every row NaN
+    keep = [0, 2]
+    sub = stimulus.DecodeBatch(b.q[keep], b.k[keep], b.v[keep], b.seq_len[keep], b.query_pos[keep])
+    assert_within_ulp(_oracle(sub), got[keep], 64, "valid rows next to a bad block id")
+
+
+def test_paged_append_then_decode(dev):
+    """Append a token per sequence into the pool (RoPE on insert), mid-block and into a
+    fresh block, then decode: the appended rows sit where the table says, and the decode
+    equals the oracle on the grown (post-RoPE) cache."""
+    b = stimulus.decode_batch(3, 96, lengths=torch.tensor([40, 64, 17]), seed=7)
+    k, v = b.k.clone(), b.v.clone()
+    kp, vp, table = _paginate(k, v, torch.tensor([41, 65, 18]), 7, spare=3)
+    g = torch.Generator().manual_seed(8)
+    kn = torch.randn((3, 1, 8, 128), generator=g).to(torch.bfloat16)
+    vn = torch.randn((3, 1, 8, 128), generator=g).to(torch.bfloat16)
+    kpd, vpd, td = kp.to(dev), vp.to(dev), table.to(dev)
+    starts = [40, 64, 17]
+    gqa.kv_append_paged(kn.to(dev), vn.to(dev), kpd, vpd, td, starts)
+    torch.cuda.synchronize()
+    kc, vc = to_codes(kpd), to_codes(vpd)
+    for i, s in enumerate(starts):
+        pid, r = int(table[i, s // 16]), s % 16
+        for h in range(8):
+            rot = orc.prepare_rows(to_codes(kn[i, :, h]), True, s)
+            u = rot.astype(np.float32).view(np.uint32).astype(np.uint64)
+            want_k = (((u + 0x7FFF + ((u >> 16) & 1)) >> 16) & 0xFFFF).astype(np.uint16)
+            assert np.array_equal(kc[pid, h, r:r + 1], want_k)
+            assert np.array_equal(vc[pid, h, r:r + 1], to_codes(vn[i, :, h]))
+            k[i, h, s] = torch.from_numpy(want_k.view(np.int16)).view(torch.bfloat16)[0]
+            v[i, h, s] = vn[i, 0, h]
+    seq_len = torch.tensor([s + 1 for s in starts], dtype=torch.int32)
+    grown = stimulus.DecodeBatch(b.q, k, v, seq_len, torch.tensor(starts, dtype=torch.int32))
+    got = to_codes(gqa.gqa_decode_paged(b.q.to(dev), kpd, vpd, td, grown.query_pos, seq_len))
+    assert_within_ulp(_oracle(grown), got, 64, "paged append then decode")
+
+
+def test_paged_north_star_batch64_ragged(dev):
+    """B=64, lengths U[512, 8192] through a paged pool: every output against the oracle."""
+    b = stimulus.decode_batch(64, 8192, min_len=512, max_len=8192, seed=20260805,
+                              gen_device="cuda", device=dev)
+    bc = stimulus.DecodeBatch(b.q.cpu(), b.k.cpu(), b.v.cpu(), b.seq_len, b.query_pos)
+    kp, vp, table = _paginate(bc.k, bc.v, bc.seq_len, 9)
+    got = to_codes(gqa.gqa_decode_paged(b.q, kp.to(dev), vp.to(dev), table.to(dev),
+                                        b.query_pos, b.seq_len))
+    w = assert_within_ulp(_oracle(bc), got, 64, "paged B=64 ragged")
+    print("worst ULP", w)
