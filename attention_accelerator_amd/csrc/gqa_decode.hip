@@ -53,6 +53,7 @@
 namespace gqa {
 
 constexpr int kChunk = 16;           // keys per MFMA group
+constexpr int kFusedWindows = kFusedMaxBatch / kWave;
 constexpr int kMinRangeKeys = 64;    // smallest per-workgroup key range
 
 __device__ __forceinline__ int seq_valid_keys(const DecodeArgs& a, int b) {
@@ -60,6 +61,14 @@ __device__ __forceinline__ int seq_valid_keys(const DecodeArgs& a, int b) {
     const int qp = a.query_pos[b];
     if (L < 1 || L > a.capacity || qp < 0 || qp >= L) return 0;
     return min(L, qp + 1);
+}
+
+// A wave-uniform 64-bit value made scalar (shuffle results are per-lane values to the
+// compiler even when every lane holds the same one).
+__device__ __forceinline__ int64_t uniform_i64(int64_t v) {
+    const uint32_t lo = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(v));
+    const uint32_t hi = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(static_cast<uint64_t>(v) >> 32));
+    return static_cast<int64_t>((static_cast<uint64_t>(hi) << 32) | lo);
 }
 
 __device__ __forceinline__ int64_t wave_sum_i64(int64_t x) {
@@ -322,44 +331,176 @@ __device__ __forceinline__ void write_partial(const DecodeArgs& a, int64_t slot,
     }
 }
 
-// This lane's Q operands for (sequence b, KV head kvh): the group's 4 Q rows rotated at
-// query_position and scaled by scale*log2(e) in double, each value split into three BF16
-// parts, in the MFMA B-operand layout (MFMA kb: column n = l%16 -> part n/4 of head n%4,
-// dims 32kb + 8(l/16) + j; columns 12..15 zero).  q_s: 4 KB of LDS for the wave.
-template <bool kRopeQ>
-__device__ __forceinline__ void make_q_operands(const DecodeArgs& a, int b, int kvh, double (*q_s)[kD],
-                                                uint4 (&w)[4]) {
+// Agent-scope (sc1) 8-byte stores and loads: coherent across the XCDs without a cache
+// write-back or invalidate (used to hand partials between workgroups inside a launch).
+__device__ __forceinline__ void store_agent(unsigned long long* p, double v) {
+    __hip_atomic_store(p, static_cast<unsigned long long>(__double_as_longlong(v)), __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__device__ __forceinline__ void store_agent(unsigned long long* p, float2 v) {
+    unsigned long long u;
+    __builtin_memcpy(&u, &v, 8);
+    __hip_atomic_store(p, u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__device__ __forceinline__ float2 load_agent_f2(const float2* p) {
+    const unsigned long long u =
+        __hip_atomic_load(reinterpret_cast<const unsigned long long*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    float2 v;
+    __builtin_memcpy(&v, &u, 8);
+    return v;
+}
+
+__device__ __forceinline__ double2 load_agent_d2(const double* p) {
+    const unsigned long long* q = reinterpret_cast<const unsigned long long*>(p);
+    return make_double2(__longlong_as_double(__hip_atomic_load(q, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)),
+                        __longlong_as_double(__hip_atomic_load(q + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)));
+}
+
+// write_partial with agent-scope stores, for a partial merged inside the same launch.
+__device__ __forceinline__ void publish_partial(const DecodeArgs& a, int64_t slot, const PieceState& st,
+                                                const float (&m_tot)[kGroup], const double (&l_tot)[kGroup]) {
     const int lane = threadIdx.x & (kWave - 1);
     const int n = lane & 15;
-    const int g = lane >> 4;
-    const int qpos = a.query_pos[b];
-    double sn = 0.0, cs = 1.0;
-    if (kRopeQ) rope_sincos(qpos, a.rope.inv_freq[lane], sn, cs);
+    if (lane < 16) {
+#pragma unroll
+        for (int h = 0; h < kGroup; ++h) {
+            unsigned long long* dst =
+                reinterpret_cast<unsigned long long*>(a.part_o + (slot * kGroup + h) * kD + 8 * n);
+#pragma unroll
+            for (int j = 0; j < 8; ++j) store_agent(dst + j, st.acc[h][j]);
+        }
+    }
+    if (lane < kGroup) {
+        const float mm = lane == 0 ? m_tot[0] : lane == 1 ? m_tot[1] : lane == 2 ? m_tot[2] : m_tot[3];
+        const double ll = lane == 0 ? l_tot[0] : lane == 1 ? l_tot[1] : lane == 2 ? l_tot[2] : l_tot[3];
+        store_agent(reinterpret_cast<unsigned long long*>(a.part_ml + slot * kGroup + lane),
+                    make_float2(mm, static_cast<float>(ll)));
+    }
+}
+
+// A partial held in LDS until the end of the workgroup's range (fused kernel).
+struct PartialStage {
+    double o[kGroup][kD];
+    float2 ml[kGroup];
+};
+
+__device__ __forceinline__ void stage_partial(PartialStage& s, const PieceState& st, const float (&m_tot)[kGroup],
+                                              const double (&l_tot)[kGroup]) {
+    const int lane = threadIdx.x & (kWave - 1);
+    const int n = lane & 15;
+    if (lane < 16) {
+#pragma unroll
+        for (int h = 0; h < kGroup; ++h)
+#pragma unroll
+            for (int j = 0; j < 8; ++j) s.o[h][8 * n + j] = st.acc[h][j];
+    }
+    if (lane < kGroup) {
+        const float mm = lane == 0 ? m_tot[0] : lane == 1 ? m_tot[1] : lane == 2 ? m_tot[2] : m_tot[3];
+        const double ll = lane == 0 ? l_tot[0] : lane == 1 ? l_tot[1] : lane == 2 ? l_tot[2] : l_tot[3];
+        s.ml[lane] = make_float2(mm, static_cast<float>(ll));
+    }
+}
+
+// publish_partial of a staged partial: lane l writes dims [8(l%16), 8(l%16) + 8) of head l/16.
+__device__ __forceinline__ void publish_staged(const DecodeArgs& a, int64_t slot, const PartialStage& s) {
+    const int lane = threadIdx.x & (kWave - 1);
+    const int hh = lane >> 4;
+    const int c = lane & 15;
+    unsigned long long* dst = reinterpret_cast<unsigned long long*>(a.part_o + (slot * kGroup + hh) * kD + 8 * c);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) store_agent(dst + j, s.o[hh][8 * c + j]);
+    if (lane < kGroup) store_agent(reinterpret_cast<unsigned long long*>(a.part_ml + slot * kGroup + lane), s.ml[lane]);
+}
+
+// Wait until every memory access this wave has issued has completed (s_waitcnt vmcnt(0)).
+// A workgroup-scope release fence does not wait for global stores on gfx950, so a
+// partial's stores are waited for explicitly before the counter that announces them.
+__device__ __forceinline__ void wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0F70); }
+
+// This lane's Q operands for (sequence b, KV head kvh): the group's 4 Q rows rotated at
+// query_position and scaled by scale*log2(e) in double, each value split into three BF16
+// parts, in the MFMA B-operand layout.  Two steps, so that the loads can be issued long
+// before the values are needed: load_q_raw reads the 4 Q rows (lane l: dims l and l + 64
+// of each head) and the query position; build_q_operands rotates and scales them (q),
+// splits each value once into hi/mid/lo codes (lane l splits dims [8(l%16), 8(l%16) + 8)
+// of head l/16) and reads the codes back in the B layout (lane (g, n), MFMA kb: 8 codes
+// of part n/4 of head n%4, dims 32kb + 8g ..; columns 12..15 zero).  sin/cos are kept
+// while the query position stays the same (the 8 KV heads of a sequence).
+struct QStage {
+    double q[kGroup][kD];
+    uint16_t codes[3][kGroup][kD];
+};
+
+struct QRaw {
+    uint32_t xy[kGroup];    // head h: dim lane (low half), dim lane + 64 (high half)
+    int qpos;
+};
+
+struct QRope {
+    int qpos;               // position sn, cs were formed for (-1: none yet)
+    double inv_freq;        // frequency of this lane's rotation pair
+    double sn, cs;
+};
+
+__device__ __forceinline__ void load_q_raw(const DecodeArgs& a, int b, int kvh, QRaw& r) {
+    const int lane = threadIdx.x & (kWave - 1);
+    r.qpos = a.query_pos[b];
 #pragma unroll
     for (int h = 0; h < kGroup; ++h) {
         const uint16_t* qrow = a.q + (static_cast<int64_t>(b) * kHq + kvh * kGroup + h) * kD;
-        const double x = bf16_to_f32(qrow[lane]);
-        const double y = bf16_to_f32(qrow[lane + kPairs]);
+        r.xy[h] = qrow[lane] | (static_cast<uint32_t>(qrow[lane + kPairs]) << 16);
+    }
+}
+
+template <bool kRopeQ>
+__device__ __forceinline__ void build_q_operands(const DecodeArgs& a, const QRaw& r, QRope& rope, QStage& s,
+                                                 bf16x8_t (&bq)[4]) {
+    const int lane = threadIdx.x & (kWave - 1);
+    if (kRopeQ && r.qpos != rope.qpos) {       // (uniform)
+        rope_sincos(r.qpos, rope.inv_freq, rope.sn, rope.cs);
+        rope.qpos = r.qpos;
+    }
+#pragma unroll
+    for (int h = 0; h < kGroup; ++h) {
+        const double x = bf16_to_f32(static_cast<uint16_t>(r.xy[h] & 0xFFFFu));
+        const double y = bf16_to_f32(static_cast<uint16_t>(r.xy[h] >> 16));
         double xr = x, yr = y;
         if (kRopeQ) {
-            xr = x * cs - y * sn;
-            yr = x * sn + y * cs;
+            xr = x * rope.cs - y * rope.sn;
+            yr = x * rope.sn + y * rope.cs;
         }
-        q_s[h][lane] = xr * a.qk_scale_log2;
-        q_s[h][lane + kPairs] = yr * a.qk_scale_log2;
+        s.q[h][lane] = xr * a.qk_scale_log2;
+        s.q[h][lane + kPairs] = yr * a.qk_scale_log2;
     }
     __syncthreads();
+    {
+        const int hh = lane >> 4;
+        const int c = lane & 15;
+        uint16_t p0[8], p1[8], p2[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const double v = s.q[hh][8 * c + j];
+            p0[j] = bf16_of(v);
+            const double r1 = v - f64_of_bf16(p0[j]);
+            p1[j] = bf16_of(r1);
+            p2[j] = bf16_of(r1 - f64_of_bf16(p1[j]));
+        }
+        *reinterpret_cast<bf16x8_t*>(&s.codes[0][hh][8 * c]) = pack8(p0);
+        *reinterpret_cast<bf16x8_t*>(&s.codes[1][hh][8 * c]) = pack8(p1);
+        *reinterpret_cast<bf16x8_t*>(&s.codes[2][hh][8 * c]) = pack8(p2);
+    }
+    __syncthreads();
+    const int n = lane & 15;
+    const int g = lane >> 4;
+    const int part = n < 12 ? n >> 2 : 0;
 #pragma unroll
     for (int kb = 0; kb < 4; ++kb) {
-        uint16_t h8[8];
-#pragma unroll
-        for (int j = 0; j < 8; ++j)
-            h8[j] = n < 12 ? split3(q_s[n & 3][32 * kb + 8 * g + j], n >> 2) : uint16_t(0);
-        w[kb].x = h8[0] | (static_cast<uint32_t>(h8[1]) << 16);
-        w[kb].y = h8[2] | (static_cast<uint32_t>(h8[3]) << 16);
-        w[kb].z = h8[4] | (static_cast<uint32_t>(h8[5]) << 16);
-        w[kb].w = h8[6] | (static_cast<uint32_t>(h8[7]) << 16);
+        const bf16x8_t v = *reinterpret_cast<const bf16x8_t*>(&s.codes[part][n & 3][32 * kb + 8 * g]);
+        bq[kb] = n < 12 ? v : bf16x8_t{};
     }
+    // (one wave: its LDS accesses run in order, so the next piece's writes need no barrier)
 }
 
 // Q operands of every (sequence, KV head), written once per call by
@@ -394,7 +535,7 @@ __device__ __forceinline__ void build_plan(const DecodeArgs& a, int lane) {
 
 template <bool kRopeQ>
 __global__ __launch_bounds__(kWave) void decode_prepare_kernel(DecodeArgs a) {
-    __shared__ double q_s[kGroup][kD];
+    __shared__ QStage qs;
     const int kvh = blockIdx.x;
     const int b = blockIdx.y;
     const int lane = threadIdx.x;
@@ -402,8 +543,15 @@ __global__ __launch_bounds__(kWave) void decode_prepare_kernel(DecodeArgs a) {
         if (kvh == 0) build_plan(a, lane);
         return;
     }
-    const int nv = seq_valid_keys(a, b);
-    if (nv == 0) {
+    // The Q rows are requested together with the lengths (they exist whatever the lengths).
+    QRaw raw;
+    load_q_raw(a, b, kvh, raw);
+    QRope rope;
+    rope.qpos = -1;
+    rope.inv_freq = kRopeQ ? a.rope.inv_freq[lane] : 0.0;
+    rope.sn = 0.0;
+    rope.cs = 1.0;
+    if (seq_valid_keys(a, b) == 0) {
         if (kvh == 0) {
             uint4* out = reinterpret_cast<uint4*>(a.out + static_cast<int64_t>(b) * kHq * kD);
             for (int i = lane; i < kHq * kD / 8; i += kWave)
@@ -411,11 +559,11 @@ __global__ __launch_bounds__(kWave) void decode_prepare_kernel(DecodeArgs a) {
         }
         return;
     }
-    uint4 w[4];
-    make_q_operands<kRopeQ>(a, b, kvh, q_s, w);
-    uint4* dst = a.q_op + ((static_cast<int64_t>(b) * kHkv + kvh) * 4) * kWave;
+    bf16x8_t bq[4];
+    build_q_operands<kRopeQ>(a, raw, rope, qs, bq);
+    bf16x8_t* dst = reinterpret_cast<bf16x8_t*>(a.q_op) + ((static_cast<int64_t>(b) * kHkv + kvh) * 4) * kWave;
 #pragma unroll
-    for (int kb = 0; kb < 4; ++kb) dst[kb * kWave + lane] = w[kb];
+    for (int kb = 0; kb < 4; ++kb) dst[kb * kWave + lane] = bq[kb];
 }
 
 // Where the rows of one piece live: segment base pointers and this lane's offsets of
@@ -479,11 +627,11 @@ __device__ __forceinline__ void load_q_operands(const DecodeArgs& a, int b, int 
 // chunk of the next piece (rows `nxt`) is requested into c0, so the wave never waits
 // at a piece boundary.  Writes the output rows itself when the piece is the whole
 // segment; otherwise leaves a partial for the merge kernel.
-template <bool kRopeK>
-__device__ __forceinline__ void process_piece(const DecodeArgs& a, int b, int kvh, int nv, int k_a,
+template <bool kRopeK, bool kFused = false>
+__device__ __forceinline__ bool process_piece(const DecodeArgs& a, int b, int kvh, int nv, int k_a,
                                               int k_b, int64_t wg, PieceRows& cur,
                                               const PieceRows& nxt, Chunk& c0, Chunk& c1,
-                                              const bf16x8_t (&bq)[4]) {
+                                              const bf16x8_t (&bq)[4], PartialStage* stage = nullptr) {
     const int lane = threadIdx.x & (kWave - 1);
     const int n = lane & 15;       // MFMA column / PV dim chunk
     const int g = lane >> 4;       // MFMA lane group / PV key row
@@ -515,9 +663,21 @@ __device__ __forceinline__ void process_piece(const DecodeArgs& a, int b, int kv
     merge_rows(st, m_tot, l_tot);
     if (k_a == 0 && k_b == nv) {
         write_rows(a, b, kvh, st, l_tot);      // the whole segment
-        return;
+        return false;
+    }
+    if (kFused) {
+        // A split piece of the fused kernel: kept in LDS while more pieces follow (agent-scope
+        // stores issued now would hold up every later load of the wave: the memory counter
+        // retires in order, and these stores complete only once written through to memory),
+        // else published at once (nothing follows).
+        if (stage)
+            stage_partial(*stage, st, m_tot, l_tot);
+        else
+            publish_partial(a, wg + static_cast<int64_t>(b) * kHkv + kvh, st, m_tot, l_tot);
+        return true;
     }
     write_partial(a, wg + static_cast<int64_t>(b) * kHkv + kvh, st, m_tot, l_tot);
+    return false;
 }
 
 // Per-sequence key offsets for 64 sequences at a time, one per lane: o = seq_off[base +
@@ -526,6 +686,7 @@ struct SeqWindow {
     int base;
     int64_t o;
     int64_t o1;
+    int64_t carry;    // scanned windows: keys (per segment) of the sequences before base + 64
 };
 
 __device__ __forceinline__ void load_seq_window(const DecodeArgs& a, int base, SeqWindow& sw) {
@@ -535,9 +696,32 @@ __device__ __forceinline__ void load_seq_window(const DecodeArgs& a, int base, S
     sw.o1 = bb < a.batch ? a.seq_off[bb + 1] : INT64_MAX;
 }
 
+// The same window computed from the lengths (the fused kernel has no plan in memory):
+// an inclusive scan of the window's per-segment keys on top of `carry`, the keys of the
+// sequences before `base`.
+__device__ __forceinline__ void scan_seq_window(const DecodeArgs& a, int base, int64_t carry, SeqWindow& sw) {
+    const int lane = static_cast<int>(threadIdx.x & (kWave - 1));
+    const int bb = base + lane;
+    const int nv = bb < a.batch ? plan_keys(a, bb) : 0;
+    const int64_t incl = wave_incl_scan_i64(nv, lane) + carry;
+    sw.base = base;
+    sw.o = bb < a.batch ? (incl - nv) * kHkv : INT64_MAX;
+    sw.o1 = bb < a.batch ? incl * kHkv : INT64_MAX;
+    sw.carry = __shfl(incl, kWave - 1);
+}
+
+template <bool kScan>
+__device__ __forceinline__ void seq_window(const DecodeArgs& a, int base, int64_t carry, SeqWindow& sw) {
+    if (kScan)
+        scan_seq_window(a, base, carry, sw);
+    else
+        load_seq_window(a, base, sw);
+}
+
 // The segment after (b, kvh) that has keys: the next KV head of b, or KV head 0 of the
 // next sequence with keys.  Returns false when there is none (possible only if the
 // lengths changed while the kernel ran).
+template <bool kScan = false>
 __device__ __forceinline__ bool next_segment(const DecodeArgs& a, SeqWindow& sw, int& b, int& kvh,
                                              int& nv) {
     if (kvh + 1 < kHkv) {
@@ -555,7 +739,7 @@ __device__ __forceinline__ bool next_segment(const DecodeArgs& a, SeqWindow& sw,
             return true;
         }
         if (sw.base + kWave >= a.batch) return false;
-        load_seq_window(a, sw.base + kWave, sw);
+        seq_window<kScan>(a, sw.base + kWave, sw.carry, sw);
     }
 }
 
@@ -646,6 +830,321 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(1))) void
 #pragma unroll
         for (int kb = 0; kb < 4; ++kb) bq[kb] = bq2[kb];
     }
+}
+
+
+// ---------------------------------------------------------------------------------
+// Fused decode: the stream kernel with its plan, Q operands and merge done in-kernel, so a
+// call is one launch.  Each workgroup scans the lengths itself (a batch of at most
+// kFusedMaxBatch sequences is a few windows of 64), forms the Q operands of each piece
+// while that piece's first chunk is in flight, and the pieces of a split segment meet
+// through agent-scope partials and a per-segment counter: the last piece to finish
+// merges them in piece order and resets the counter.
+
+// Merge the n_pieces partials of segment (b, kvh) at slots slot0.. in piece order: lane
+// (head l/16, dims [8(l%16), 8(l%16) + 8)), exact power-of-two weights, fp64 sums, the
+// row rounded double -> f32 -> BF16.  A piece that saw no key (m = -inf) weighs 0.
+__device__ __forceinline__ void merge_segment(const DecodeArgs& a, int b, int kvh, int64_t slot0, int n_pieces) {
+    const int lane = threadIdx.x & (kWave - 1);
+    const int hh = lane >> 4;
+    const int c = lane & 15;
+    float m_all = -INFINITY;
+    for (int p0 = 0; p0 < n_pieces; p0 += 16) {
+        const int p = min(p0 + c, n_pieces - 1);
+        m_all = fmaxf(m_all, load_agent_f2(a.part_ml + (slot0 + p) * kGroup + hh).x);
+    }
+    m_all = fmaxf(m_all, __shfl_xor(m_all, 1));
+    m_all = fmaxf(m_all, __shfl_xor(m_all, 2));
+    m_all = fmaxf(m_all, __shfl_xor(m_all, 4));
+    m_all = fmaxf(m_all, __shfl_xor(m_all, 8));
+    double l = 0.0;
+    double o[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) o[j] = 0.0;
+    for (int p0 = 0; p0 < n_pieces; p0 += 4) {
+        float2 ml[4];
+        double2 ov[4][4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int64_t slot = slot0 + min(p0 + u, n_pieces - 1);
+            ml[u] = load_agent_f2(a.part_ml + slot * kGroup + hh);
+#pragma unroll
+            for (int q = 0; q < 4; ++q) ov[u][q] = load_agent_d2(a.part_o + (slot * kGroup + hh) * kD + 8 * c + 2 * q);
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            if (p0 + u < n_pieces) {     // (uniform) copies of the last piece are skipped
+                const int e = ml[u].x == -INFINITY ? -1100 : static_cast<int>(ml[u].x - m_all);
+                l += ldexp(static_cast<double>(ml[u].y), e);
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    o[2 * q] += ldexp(ov[u][q].x, e);
+                    o[2 * q + 1] += ldexp(ov[u][q].y, e);
+                }
+            }
+        }
+    }
+    uint16_t o8[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) o8[j] = f32_to_bf16_rne(static_cast<float>(o[j] / l));
+    *reinterpret_cast<bf16x8_t*>(a.out + (static_cast<int64_t>(b) * kHq + kvh * kGroup + hh) * kD + 8 * c) =
+        pack8(o8);
+}
+
+// A split segment's piece whose partial is published: count it in (device-scope atomic on
+// the segment's counter; the partial's stores have completed before), and the last of
+// the segment's pieces merges and resets the counter.  A workgroup has at most two split
+// pieces, its first and its last; both are counted at its end, with one wait for the
+// stores and the two atomics in flight together, and when the segments it merges hold
+// at most kMergeBatch pieces in all, every partial is requested at once.
+struct SplitPiece {
+    int b, kvh, nv;
+    int64_t seg_off;        // < 0: none
+};
+
+constexpr int kMergeBatch = 8;
+
+__device__ __forceinline__ int count_pieces(int64_t seg_off, int nv, int64_t per_wg, int64_t& w_first) {
+    w_first = seg_off / per_wg;
+    return static_cast<int>((seg_off + nv - 1) / per_wg - w_first) + 1;
+}
+
+// Lane (head l/16, dims [8(l%16), 8(l%16) + 8)) of the merged row of a segment whose
+// partials, in piece order, are ml[u0 .. u0 + n) / ov[u0 .. u0 + n).
+__device__ __forceinline__ void store_merged(const DecodeArgs& a, int b, int kvh, const float2 (&ml)[kMergeBatch],
+                                             const double2 (&ov)[kMergeBatch][4], int u0, int n) {
+    const int lane = threadIdx.x & (kWave - 1);
+    const int hh = lane >> 4;
+    const int c = lane & 15;
+    float m_all = -INFINITY;
+#pragma unroll
+    for (int u = 0; u < kMergeBatch; ++u)
+        if (u >= u0 && u < u0 + n) m_all = fmaxf(m_all, ml[u].x);
+    double l = 0.0;
+    double o[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) o[j] = 0.0;
+#pragma unroll
+    for (int u = 0; u < kMergeBatch; ++u) {
+        if (u >= u0 && u < u0 + n) {         // (uniform)
+            const int e = ml[u].x == -INFINITY ? -1100 : static_cast<int>(ml[u].x - m_all);
+            l += ldexp(static_cast<double>(ml[u].y), e);
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                o[2 * q] += ldexp(ov[u][q].x, e);
+                o[2 * q + 1] += ldexp(ov[u][q].y, e);
+            }
+        }
+    }
+    uint16_t o8[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) o8[j] = f32_to_bf16_rne(static_cast<float>(o[j] / l));
+    *reinterpret_cast<bf16x8_t*>(a.out + (static_cast<int64_t>(b) * kHq + kvh * kGroup + hh) * kD + 8 * c) =
+        pack8(o8);
+}
+
+__device__ __forceinline__ void finish_split_pieces(const DecodeArgs& a, const SplitPiece& p1, const SplitPiece& p2,
+                                                    int64_t per_wg) {
+    wait_vmem();                                   // the partials' stores have completed
+    const int lane = threadIdx.x & (kWave - 1);
+    int d1 = -1, d2 = -1;
+    if (lane == 0) {
+        if (p1.seg_off >= 0) d1 = static_cast<int>(atomicAdd(&a.seg_count[p1.b * kHkv + p1.kvh], 1ull));
+        if (p2.seg_off >= 0) d2 = static_cast<int>(atomicAdd(&a.seg_count[p2.b * kHkv + p2.kvh], 1ull));
+    }
+    d1 = __builtin_amdgcn_readfirstlane(d1);
+    d2 = __builtin_amdgcn_readfirstlane(d2);
+    int64_t w1 = 0, w2 = 0;
+    const int n1 = p1.seg_off >= 0 ? count_pieces(p1.seg_off, p1.nv, per_wg, w1) : 0;
+    const int n2 = p2.seg_off >= 0 ? count_pieces(p2.seg_off, p2.nv, per_wg, w2) : 0;
+    const bool m1 = p1.seg_off >= 0 && d1 == n1 - 1;
+    const bool m2 = p2.seg_off >= 0 && d2 == n2 - 1;
+    if (!m1 && !m2) return;
+    const int seg1 = p1.b * kHkv + p1.kvh;
+    const int seg2 = p2.b * kHkv + p2.kvh;
+    if (lane == 0) {
+        if (m1) __hip_atomic_store(&a.seg_count[seg1], 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (m2) __hip_atomic_store(&a.seg_count[seg2], 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    const int k1 = m1 ? n1 : 0;
+    const int k2 = m2 ? n2 : 0;
+    if (k1 + k2 > kMergeBatch) {
+        if (m1) merge_segment(a, p1.b, p1.kvh, w1 + seg1, n1);
+        if (m2) merge_segment(a, p2.b, p2.kvh, w2 + seg2, n2);
+        return;
+    }
+    // One batch: slots of segment 1's pieces, then segment 2's (unused entries repeat a
+    // slot of the batch and are not read back).
+    const int hh = lane >> 4;
+    const int c = lane & 15;
+    float2 ml[kMergeBatch];
+    double2 ov[kMergeBatch][4];
+#pragma unroll
+    for (int u = 0; u < kMergeBatch; ++u) {
+        const int64_t slot = u < k1   ? w1 + seg1 + u
+                             : k2 > 0 ? w2 + seg2 + min(u - k1, k2 - 1)
+                                      : w1 + seg1 + (k1 - 1);
+        ml[u] = load_agent_f2(a.part_ml + slot * kGroup + hh);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) ov[u][q] = load_agent_d2(a.part_o + (slot * kGroup + hh) * kD + 8 * c + 2 * q);
+    }
+    if (m1) store_merged(a, p1.b, p1.kvh, ml, ov, 0, k1);
+    if (m2) store_merged(a, p2.b, p2.kvh, ml, ov, k1, k2);
+}
+
+__device__ __forceinline__ void write_nan_rows(const DecodeArgs& a, int b) {
+    uint4* out = reinterpret_cast<uint4*>(a.out + static_cast<int64_t>(b) * kHq * kD);
+    for (int i = threadIdx.x & (kWave - 1); i < kHq * kD / 8; i += kWave)
+        out[i] = make_uint4(0x7fc07fc0u, 0x7fc07fc0u, 0x7fc07fc0u, 0x7fc07fc0u);
+}
+
+// Rows of sequences whose lengths break the rules: NaN, sequence b by workgroup b mod n_wgs
+// (nvw: per-segment keys of the batch, 64 sequences per window, 0 for such a sequence).
+__device__ __forceinline__ void write_nan_rows_of(const DecodeArgs& a, const int (&nvw)[kFusedWindows], int64_t w) {
+    const int lane = threadIdx.x & (kWave - 1);
+#pragma unroll
+    for (int k = 0; k < kFusedWindows; ++k) {
+        const int bb = kWave * k + lane;
+        uint64_t m = __ballot(bb < a.batch && nvw[k] == 0 && bb % a.n_wgs == w);
+        while (m) {
+            const int j = __ffsll(static_cast<unsigned long long>(m)) - 1;
+            m &= m - 1;
+            write_nan_rows(a, kWave * k + j);
+        }
+    }
+}
+
+template <bool kRopeQ, bool kRopeK>
+__global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(1))) void decode_fused_kernel(DecodeArgs a) {
+    __shared__ QStage qs;
+    __shared__ PartialStage first_part;
+    const int64_t w = blockIdx.x;
+    const int lane = threadIdx.x & (kWave - 1);
+
+    // The plan from the lengths, all requested at once (a batch of at most kFusedMaxBatch
+    // sequences: kFusedWindows windows of 64).
+    int nvw[kFusedWindows];
+#pragma unroll
+    for (int k = 0; k < kFusedWindows; ++k) {
+        const int bb = kWave * k + lane;
+        nvw[k] = bb < a.batch ? plan_keys(a, bb) : 0;
+    }
+    int64_t total = 0;
+#pragma unroll
+    for (int k = 0; k < kFusedWindows; ++k) total += wave_sum_i64(nvw[k]);
+    total = uniform_i64(total * kHkv);
+    int64_t per_wg = (total + a.n_wgs - 1) / a.n_wgs;
+    per_wg = per_wg < kMinRangeKeys ? kMinRangeKeys : per_wg;
+    per_wg = (per_wg + kChunk - 1) / kChunk * kChunk;
+    int64_t x = w * per_wg;
+    if (x >= total) {
+        write_nan_rows_of(a, nvw, w);
+        return;
+    }
+    const int64_t x_end = min(x + per_wg, total);
+
+    // Start sequence b = the last b whose first segment starts at or before x.
+    SeqWindow sw;
+    int b = 0;
+    int64_t off = 0, next = 0, carry = 0;
+#pragma unroll
+    for (int k = 0; k < kFusedWindows; ++k) {
+        const int bb = kWave * k + lane;
+        const int64_t incl = wave_incl_scan_i64(nvw[k], lane) + carry;
+        SeqWindow t;
+        t.base = kWave * k;
+        t.o = bb < a.batch ? (incl - nvw[k]) * kHkv : INT64_MAX;
+        t.o1 = bb < a.batch ? incl * kHkv : INT64_MAX;
+        t.carry = __shfl(incl, kWave - 1);
+        carry = t.carry;
+        const uint64_t le = __ballot(t.o <= x);
+        if (le) {
+            const int j = 63 - __clzll(static_cast<long long>(le));
+            b = kWave * k + j;
+            off = __shfl(t.o, j);
+            next = __shfl(t.o1, j);
+            sw = t;
+        }
+    }
+    int nvb = static_cast<int>((next - off) / kHkv);
+    const int64_t rel = x - off;
+    int kvh = 0;
+#pragma unroll
+    for (int kk = 1; kk < kHkv; ++kk) kvh += rel >= static_cast<int64_t>(kk) * nvb;
+    int key = static_cast<int>(rel - static_cast<int64_t>(kvh) * nvb);
+    b = __builtin_amdgcn_readfirstlane(b);
+    kvh = __builtin_amdgcn_readfirstlane(kvh);
+    key = __builtin_amdgcn_readfirstlane(key);
+    nvb = __builtin_amdgcn_readfirstlane(nvb);
+    int k_b = __builtin_amdgcn_readfirstlane(
+        static_cast<int>(min(static_cast<int64_t>(nvb), key + (x_end - x))));
+
+    const uint32_t step = kChunk * static_cast<uint32_t>(a.kv_pos_stride) * 2u;
+    PieceRows cur;
+    piece_rows(a, b, kvh, key, k_b, cur);
+    Chunk c0, c1;
+    load_next(cur, step, c0);
+    QRope rope;
+    rope.qpos = -1;
+    rope.inv_freq = kRopeQ ? a.rope.inv_freq[lane] : 0.0;
+    rope.sn = 0.0;
+    rope.cs = 1.0;
+    QRaw raw;
+    load_q_raw(a, b, kvh, raw);
+    bf16x8_t bq[4];
+    build_q_operands<kRopeQ>(a, raw, rope, qs, bq);
+
+    SplitPiece first = {0, 0, 0, -1};
+    SplitPiece last = {0, 0, 0, -1};
+    while (true) {
+        const int64_t x_next = x + (k_b - key);
+        int b2 = b, kvh2 = kvh, nv2 = nvb, key2 = k_b - 1, k_b2 = k_b;
+        bool more = x_next < x_end;
+        if (more) {
+            more = next_segment<true>(a, sw, b2, kvh2, nv2);
+            b2 = __builtin_amdgcn_readfirstlane(b2);
+            kvh2 = __builtin_amdgcn_readfirstlane(kvh2);
+            nv2 = __builtin_amdgcn_readfirstlane(nv2);
+            key2 = 0;
+            k_b2 = __builtin_amdgcn_readfirstlane(
+                static_cast<int>(min(static_cast<int64_t>(nv2), x_end - x_next)));
+        }
+        if (!more) {
+            b2 = b;
+            kvh2 = kvh;
+            nv2 = nvb;
+            key2 = k_b - 1;
+            k_b2 = k_b;
+        }
+        PieceRows nxt;
+        piece_rows(a, b2, kvh2, key2, k_b2, nxt);
+        load_q_raw(a, b2, kvh2, raw);              // the next piece's Q rows
+
+        if (process_piece<kRopeK, true>(a, b, kvh, nvb, key, k_b, w, cur, nxt, c0, c1, bq,
+                                        more ? &first_part : nullptr)) {
+            // a split piece: the range's first (more pieces follow) or its last
+            SplitPiece& sp = more ? first : last;
+            sp.b = b;
+            sp.kvh = kvh;
+            sp.nv = nvb;
+            sp.seg_off = x - key;
+        }
+        if (!more) break;
+        build_q_operands<kRopeQ>(a, raw, rope, qs, bq);   // while the next piece's first chunk is in flight
+
+        x = x_next;
+        b = b2;
+        kvh = kvh2;
+        nvb = nv2;
+        key = key2;
+        k_b = k_b2;
+        cur = nxt;
+        advance(cur.rows, step);     // its first chunk is in c0 already
+    }
+    if (first.seg_off >= 0)
+        publish_staged(a, w + static_cast<int64_t>(first.b) * kHkv + first.kvh, first_part);
+    finish_split_pieces(a, first, last, per_wg);
+    write_nan_rows_of(a, nvw, w);
 }
 
 
@@ -902,33 +1401,6 @@ __global__ __launch_bounds__(kGroup * kWave) void decode_merge_kernel(DecodeArgs
 // partial's stores have completed.  The merging piece resets the counter, so a
 // workspace needs zeroing (gqa_decode_workspace_init) before its first use only.
 
-// Agent-scope (sc1) 8-byte stores and loads: coherent across the XCDs without a cache
-// write-back or invalidate (used to hand partials between workgroups inside a launch).
-__device__ __forceinline__ void store_agent(unsigned long long* p, double v) {
-    __hip_atomic_store(p, static_cast<unsigned long long>(__double_as_longlong(v)), __ATOMIC_RELAXED,
-                       __HIP_MEMORY_SCOPE_AGENT);
-}
-
-__device__ __forceinline__ void store_agent(unsigned long long* p, float2 v) {
-    unsigned long long u;
-    __builtin_memcpy(&u, &v, 8);
-    __hip_atomic_store(p, u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
-__device__ __forceinline__ float2 load_agent_f2(const float2* p) {
-    const unsigned long long u =
-        __hip_atomic_load(reinterpret_cast<const unsigned long long*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    float2 v;
-    __builtin_memcpy(&v, &u, 8);
-    return v;
-}
-
-__device__ __forceinline__ double2 load_agent_d2(const double* p) {
-    const unsigned long long* q = reinterpret_cast<const unsigned long long*>(p);
-    return make_double2(__longlong_as_double(__hip_atomic_load(q, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)),
-                        __longlong_as_double(__hip_atomic_load(q + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)));
-}
-
 constexpr int kSingleWaves = 4;
 
 template <bool kRopeQ, bool kRopeK>
@@ -1054,6 +1526,8 @@ __global__ __launch_bounds__(kSingleWaves * kWave) void decode_single_kernel(Dec
     // Publish the partial with agent-scope stores (written through the XCD's L2, which is
     // not coherent with the other XCDs'), and wait until they have completed before the
     // counter is touched: a __threadfence here would write back the whole L2 instead.
+    // The counter's atomic returns only after it is performed, and the merge's agent-scope
+    // loads are issued after that.
     {
         unsigned long long* po =
             reinterpret_cast<unsigned long long*>(a.part_o + ((slot0 + piece) * kGroup + h) * kD) + 2 * lane;
@@ -1062,7 +1536,7 @@ __global__ __launch_bounds__(kSingleWaves * kWave) void decode_single_kernel(Dec
         if (lane == 0)
             store_agent(reinterpret_cast<unsigned long long*>(a.part_ml + (slot0 + piece) * kGroup + h),
                         make_float2(mx, static_cast<float>(l)));
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");   // s_waitcnt: stores done
+        wait_vmem();
     }
     __syncthreads();
     // Count finished pieces (device-scope atomic); the last piece merges and resets the
@@ -1070,8 +1544,7 @@ __global__ __launch_bounds__(kSingleWaves * kWave) void decode_single_kernel(Dec
     if (threadIdx.x == 0) last_s = atomicAdd(&a.seg_count[seg], 1ull) == static_cast<unsigned long long>(n_pieces - 1);
     __syncthreads();
     if (!last_s) return;
-    if (threadIdx.x == 0) a.seg_count[seg] = 0;
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+    if (threadIdx.x == 0) __hip_atomic_store(&a.seg_count[seg], 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 
     // Merge the segment's pieces, wave h for head h: (m, l) of 64 pieces per pass, one per
     // lane, then their O rows (lane owns dims 2*lane, 2*lane + 1), 16 requested at a time.
@@ -1132,6 +1605,25 @@ hipError_t launch_decode(const DecodeArgs& a, int batch, hipStream_t stream, hip
             hipLaunchKernelGGL((decode_single_kernel<false, true>), grid, dim3(kSingleWaves * kWave), 0, stream, a);
         else
             hipLaunchKernelGGL((decode_single_kernel<false, false>), grid, dim3(kSingleWaves * kWave), 0, stream, a);
+        const hipError_t e = hipGetLastError();
+        if (ev) {
+            (void)hipEventRecord(ev[1], stream);
+            (void)hipEventRecord(ev[2], stream);
+        }
+        return e;
+    }
+    if (a.fused && !a.block_table) {
+        // One launch: plan, Q operands and merge inside the stream kernel.
+        if (ev) (void)hipEventRecord(ev[0], stream);
+        const dim3 grid(a.n_wgs);
+        if (rq && rk)
+            hipLaunchKernelGGL((decode_fused_kernel<true, true>), grid, dim3(kWave), 0, stream, a);
+        else if (rq)
+            hipLaunchKernelGGL((decode_fused_kernel<true, false>), grid, dim3(kWave), 0, stream, a);
+        else if (rk)
+            hipLaunchKernelGGL((decode_fused_kernel<false, true>), grid, dim3(kWave), 0, stream, a);
+        else
+            hipLaunchKernelGGL((decode_fused_kernel<false, false>), grid, dim3(kWave), 0, stream, a);
         const hipError_t e = hipGetLastError();
         if (ev) {
             (void)hipEventRecord(ev[1], stream);
