@@ -45,17 +45,16 @@ constexpr int kPfPos = 32;                 // query positions per workgroup
 constexpr int kPfWaves = 8;                // 4 Q heads x 2 tiles of 16 positions
 constexpr int kPfThreads = kPfWaves * kWave;
 constexpr int kPfBlk = 64;                 // keys per K/V block
-constexpr int kKRow = 136;                 // LDS K row stride in BF16 (256 B + 16 B pad)
-constexpr int kVRow = 72;                  // LDS V^T row stride in BF16 (128 B + 16 B pad)
-constexpr int kKPlane = kPfBlk * kKRow;    // BF16 elements per LDS K plane
 
 constexpr uint32_t kPermLo = 0x05040100u;  // v_perm_b32: low halves of (b, a) -> a.lo | b.lo << 16
 constexpr uint32_t kPermHi = 0x07060302u;  // high halves
 
 }  // namespace
 
+// The second and third BF16 parts of every rotated new K row, then one zero row (the parts
+// of a cached key, which the attention kernel copies for keys before the chunk).
 size_t prefill_split_bytes(int32_t batch, int32_t n_new) {
-    return 2ull * static_cast<size_t>(batch) * static_cast<size_t>(n_new) * kHkv * kD * sizeof(uint16_t);
+    return (2ull * static_cast<size_t>(batch) * static_cast<size_t>(n_new) * kHkv + 1) * kD * sizeof(uint16_t);
 }
 
 __device__ __forceinline__ bool prefill_start_ok(const PrefillArgs& a, int st) {
@@ -82,6 +81,11 @@ __device__ __forceinline__ int64_t cache_elem(const PrefillArgs& a, int b, int h
 __global__ __launch_bounds__(256) void kv_append_kernel(PrefillArgs a) {
     const int64_t bt = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);   // b * T + t
     const int lane = threadIdx.x & (kWave - 1);
+    if (a.k_split && blockIdx.x == 0 && threadIdx.x < kD / 2) {
+        uint32_t* zero_row = reinterpret_cast<uint32_t*>(
+            a.k_split + 2 * static_cast<int64_t>(a.batch) * a.n_new * kHkv * kD);
+        zero_row[threadIdx.x] = 0u;
+    }
     if (bt >= static_cast<int64_t>(a.batch) * a.n_new) return;
     const int t = static_cast<int>(bt % a.n_new);
     const int b = static_cast<int>(bt / a.n_new);
@@ -138,80 +142,85 @@ hipError_t launch_kv_append(const PrefillArgs& a, hipStream_t stream) {
 // ---------------------------------------------------------------------------------
 // Attention.
 
-// Registers staging one K/V block on its way to LDS.  Threads 0..255 hold a quad of
-// V rows (keys 4q..4q+3, dims 8c..8c+7, c = t/16, q = t%16); threads 256..511 a
-// 64-byte segment of a K row (plane 0, the cache row).  `s` holds a 64-byte segment of
-// a K row of plane 1 (threads 0..255) or plane 2 (256..511): the second or third BF16
-// part of a chunk key, zero for cached keys.
-struct PfStage {
-    uint4 a[4];
-    uint4 s[4];
-    bool s_zero;
-};
+// LDS holds two blocks (double buffer), each: K (the cache row, plane 0), the second and
+// third BF16 parts of chunk keys (planes 1, 2) and V, 64 rows of 256 B per plane (128 KB in
+// all).  Rows are copied from HBM straight into LDS (global_load_lds_dwordx4: lane l of an
+// instruction writes bytes [16l, 16l + 16) of a 1 KB stretch = 4 rows), so a row's 16
+// 16-byte chunks are placed by choosing which chunk each lane fetches: chunk c of row r
+// sits at position c ^ pf_swz(r).  With that swizzle the K operand reads (16 rows, one
+// chunk) and the V^T transpose reads (16 rows, two chunks) hit 64 distinct banks per
+// half-wave.
+constexpr int kRowB = 256;                  // LDS bytes per row
+constexpr int kPlaneB = kPfBlk * kRowB;     // 16 KB per plane
+constexpr int kBufB = 4 * kPlaneB;          // K, K part 2, K part 3, V
+constexpr int kVOff = 3 * kPlaneB;
 
-__device__ __forceinline__ void pf_load_block(const PrefillArgs& a, int b, int kvh, int st, int blk,
-                                              int n_keys, PfStage& sg) {
-    const int tid = threadIdx.x;
-    const int half = tid >> 8;
-    const int t = tid & 255;
+__device__ __forceinline__ int pf_swz(int row) { return (2 * row + (row >> 3)) & 15; }
+
+typedef short short4_t __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) void lds_void_t;
+typedef __attribute__((address_space(3))) short4_t lds_short4_t;
+
+// Request block blk into the LDS buffer at `dst`.  Wave w fetches rows
+// 8w .. 8w+7 (two 4-row instructions per plane).  Rows past the keys this workgroup needs
+// repeat its last key; planes 1 and 2 are fetched only for a block holding chunk keys, and a
+// cached key's parts come from the zero row.
+__device__ __forceinline__ void pf_issue_block(const PrefillArgs& a, const char* kbase, const char* vbase,
+                                               int b, int kvh, int st, int blk, int n_keys, bool has_new,
+                                               uint8_t* dst, int wave, int lane) {
     const int key0 = blk * kPfBlk;
-    const int key_last = n_keys - 1;
-    const int64_t head_elem = static_cast<int64_t>(b) * a.kv_batch_stride +
-                              static_cast<int64_t>(kvh) * a.kv_head_stride;
-    // Plane 0 / V: addresses formed for both roles, one selected (no branch).
-    const int r = t >> 2, seg = t & 3;        // K row segment
-    const int c = t >> 4, qd = t & 15;        // V dim chunk, quad
-    const char* kbase = reinterpret_cast<const char*>(a.k + head_elem);
-    const char* vbase = reinterpret_cast<const char*>(a.v + head_elem);
     const int64_t row_bytes = a.kv_pos_stride * 2;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const int kk = half ? key0 + r : key0 + 4 * qd + i;
-        const int64_t off = static_cast<int64_t>(min(kk, key_last)) * row_bytes + (half ? 64 * seg + 16 * i : 16 * c);
-        sg.a[i] = *reinterpret_cast<const uint4*>((half ? kbase : vbase) + off);
-    }
-    // Planes 1 and 2 of chunk keys (u = key - start in [0, T)).
-    const int u = key0 + r - st;
-    sg.s_zero = u < 0;
-    const int uc = min(max(u, 0), a.n_new - 1);
     const int64_t n_rows = static_cast<int64_t>(a.batch) * a.n_new * kHkv;
-    const char* pbase = reinterpret_cast<const char*>(
-        a.k_split + (static_cast<int64_t>(half) * n_rows + (static_cast<int64_t>(b) * a.n_new + uc) * kHkv + kvh) * kD);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) sg.s[i] = *reinterpret_cast<const uint4*>(pbase + 64 * seg + 16 * i);
-}
-
-__device__ __forceinline__ void pf_store_block(uint16_t* k_lds, uint16_t* v_lds, const PfStage& sg) {
-    const int tid = threadIdx.x;
-    const int half = tid >> 8;
-    const int t = tid & 255;
-    const int r = t >> 2, seg = t & 3;
-    if (half) {
-        uint4* dst = reinterpret_cast<uint4*>(k_lds + r * kKRow + 32 * seg);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) dst[i] = sg.a[i];
-    } else {
-        // V quad -> V^T: keys 4q..4q+3 share (window w, h, g), slots 32w + 8g + 4h + i.
-        // The 16 lanes of one dim chunk hold all 16 quads, so each store instruction
-        // writes whole 128-byte V^T rows (no LDS bank conflicts).
-        const int c = t >> 4, qd = t & 15;
-        const int slot = 32 * (qd >> 3) + 8 * (qd & 3) + 4 * ((qd >> 2) & 1);
-        const uint32_t* k0 = reinterpret_cast<const uint32_t*>(&sg.a[0]);
-        const uint32_t* k1 = reinterpret_cast<const uint32_t*>(&sg.a[1]);
-        const uint32_t* k2 = reinterpret_cast<const uint32_t*>(&sg.a[2]);
-        const uint32_t* k3 = reinterpret_cast<const uint32_t*>(&sg.a[3]);
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-            const uint32_t sel = (e & 1) ? kPermHi : kPermLo;
-            uint2 w;
-            w.x = __builtin_amdgcn_perm(k1[e >> 1], k0[e >> 1], sel);
-            w.y = __builtin_amdgcn_perm(k3[e >> 1], k2[e >> 1], sel);
-            *reinterpret_cast<uint2*>(v_lds + (8 * c + e) * kVRow + slot) = w;
+    for (int ii = 0; ii < 2; ++ii) {
+        const int r = 4 * (2 * wave + ii) + (lane >> 4);
+        const int c = (lane & 15) ^ pf_swz(r);
+        const int key = min(key0 + r, n_keys - 1);
+        const int stretch = (2 * wave + ii) * 1024;
+        const int64_t off = static_cast<int64_t>(key) * row_bytes + 16 * c;
+        __builtin_amdgcn_global_load_lds(kbase + off, (lds_void_t*)(dst + stretch), 16, 0, 0);
+        __builtin_amdgcn_global_load_lds(vbase + off, (lds_void_t*)(dst + kVOff + stretch), 16, 0, 0);
+        if (has_new) {
+            const int u = key - st;          // chunk row of this key (< 0: a cached key)
+            const int64_t prow = u < 0 ? 2 * n_rows : (static_cast<int64_t>(b) * a.n_new + u) * kHkv + kvh;
+            const int64_t lrow = u < 0 ? 2 * n_rows : n_rows + prow;
+            const char* p1 = reinterpret_cast<const char*>(a.k_split + prow * kD) + 16 * c;
+            const char* p2 = reinterpret_cast<const char*>(a.k_split + lrow * kD) + 16 * c;
+            __builtin_amdgcn_global_load_lds(p1, (lds_void_t*)(dst + kPlaneB + stretch), 16, 0, 0);
+            __builtin_amdgcn_global_load_lds(p2, (lds_void_t*)(dst + 2 * kPlaneB + stretch), 16, 0, 0);
         }
     }
-    uint4* pdst = reinterpret_cast<uint4*>(k_lds + (1 + half) * kKPlane + r * kKRow + 32 * seg);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) pdst[i] = sg.s_zero ? make_uint4(0, 0, 0, 0) : sg.s[i];
+}
+
+// 8 K values of row `row`, bytes [16 chunk, 16 chunk + 16) of the plane at `plane`.
+__device__ __forceinline__ bf16x8_t pf_k_chunk(const uint8_t* plane, int row, int chunk) {
+    return *reinterpret_cast<const bf16x8_t*>(plane + row * kRowB + 16 * (chunk ^ pf_swz(row)));
+}
+
+// V^T operand of the 32-key window w, dims 16dt .. 16dt+15: lane (g, m) gets keys
+// 32w + 4g + i (slots 0..3) and 32w + 16 + 4g + i (slots 4..7) of dim 16dt + m, through two
+// transpose reads (ds_read_b64_tr_b16: lane i of a 16-lane group receives element i%4 of
+// the 8 bytes addressed by lane 4j + i/4, j = 0..3).  Supplying lane a addresses row
+// 32w + 4g + a/4 (+16), dims 16dt + 4(a%4) .. +3.
+__device__ __forceinline__ bf16x8_t pf_vt_operand(const uint8_t* vplane, int w, int dt, int lane) {
+    const int g = lane >> 4;
+    const int a = lane & 15;
+    const int row = 32 * w + 4 * g + (a >> 2);
+    const int chunk = 2 * dt + ((a & 3) >> 1);
+    const int half = (a & 1) * 8;
+    const uint8_t* p0 = vplane + row * kRowB + 16 * (chunk ^ pf_swz(row)) + half;
+    const uint8_t* p1 = vplane + (row + 16) * kRowB + 16 * (chunk ^ pf_swz(row + 16)) + half;
+    const short4_t r0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+        (lds_short4_t*)(p0));
+    const short4_t r1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+        (lds_short4_t*)(p1));
+    union {
+        short4_t h[2];
+        bf16x8_t v;
+    } u;
+    u.h[0] = r0;
+    u.h[1] = r1;
+    return u.v;
 }
 
 // Upper 16 bits of two floats packed as BF16 codes (truncation; used for exact splits).
@@ -219,9 +228,137 @@ __device__ __forceinline__ uint32_t pack_hi16(float lo, float hi) {
     return __builtin_amdgcn_perm(__float_as_uint(hi), __float_as_uint(lo), kPermHi);
 }
 
+// Scores S^T[key][query] of one 16-query tile over the block's 4 key tiles: the 3 BF16 parts
+// of Q against the cache row, and for chunk keys the (k2,q1), (k2,q2), (k3,q1) products.
+template <bool kNew>
+__device__ __forceinline__ void pf_scores(const uint8_t* kp, const bf16x8_t (&qop)[3][4], int n, int g,
+                                          f32x4_t (&sacc)[4]) {
+#pragma unroll
+    for (int kt = 0; kt < 4; ++kt) sacc[kt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb) {
+        bf16x8_t ak[4];
+#pragma unroll
+        for (int kt = 0; kt < 4; ++kt) ak[kt] = pf_k_chunk(kp, 16 * kt + n, 4 * kb + g);
+#pragma unroll
+        for (int s = 0; s < 3; ++s)
+#pragma unroll
+            for (int kt = 0; kt < 4; ++kt)
+                sacc[kt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ak[kt], qop[s][kb], sacc[kt], 0, 0, 0);
+        if (kNew) {
+#pragma unroll
+            for (int kt = 0; kt < 4; ++kt) ak[kt] = pf_k_chunk(kp + kPlaneB, 16 * kt + n, 4 * kb + g);
+#pragma unroll
+            for (int s = 0; s < 2; ++s)
+#pragma unroll
+                for (int kt = 0; kt < 4; ++kt)
+                    sacc[kt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ak[kt], qop[s][kb], sacc[kt], 0, 0, 0);
+#pragma unroll
+            for (int kt = 0; kt < 4; ++kt) ak[kt] = pf_k_chunk(kp + 2 * kPlaneB, 16 * kt + n, 4 * kb + g);
+#pragma unroll
+            for (int kt = 0; kt < 4; ++kt)
+                sacc[kt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ak[kt], qop[0][kb], sacc[kt], 0, 0, 0);
+        }
+    }
+}
+
+// Per-tile softmax state: the running max (integer-valued, log2 units), sum and O (fp64,
+// lane (g, n): O^T[16dt + 4g + i][query n]).
+struct PfTile {
+    double o64[8][4];
+    double l64;
+    float m_run;
+};
+
+// Block max of a tile's scores (masking keys past each query on diagonal blocks); grows the
+// running max to ceil(block max) and rescales O and l by the exact power of two.
+__device__ __forceinline__ void pf_block_max(f32x4_t (&sacc)[4], bool diag, int key0, int g, int pos_n, PfTile& t) {
+    if (diag) {
+#pragma unroll
+        for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                if (key0 + 16 * kt + 4 * g + i > pos_n) sacc[kt][i] = -INFINITY;
+    }
+    float bmax = -INFINITY;
+#pragma unroll
+    for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) bmax = fmaxf(bmax, sacc[kt][i]);
+    bmax = fmaxf(bmax, __shfl_xor(bmax, 16));
+    bmax = fmaxf(bmax, __shfl_xor(bmax, 32));
+    const bool grow = bmax > t.m_run;
+    if (__ballot(grow)) {
+        const float m_new = grow ? ceilf(bmax) : t.m_run;
+        const int shift = (t.m_run == -INFINITY) ? 0 : static_cast<int>(t.m_run - m_new);
+#pragma unroll
+        for (int dt = 0; dt < 8; ++dt)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) t.o64[dt][i] = ldexp(t.o64[dt][i], shift);
+        t.l64 = ldexp(t.l64, shift);
+        t.m_run = m_new;
+    }
+}
+
+// p = 2^(s - m) (0 for masked keys), summed into l, split by truncation into three BF16
+// parts packed as the P^T B operand: ph[part][window][dword].
+__device__ __forceinline__ void pf_probs(const f32x4_t (&sacc)[4], PfTile& t, uint32_t (&ph)[3][2][4]) {
+    float lsum = 0.f;
+#pragma unroll
+    for (int kt = 0; kt < 4; ++kt) {
+        float p[4], r1[4], r2[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            // v_exp_f32: 2^x, 0 for -inf (masked keys); results below 2^-126 flush to 0,
+            // far below anything the BF16 output can see.
+            p[i] = __builtin_amdgcn_exp2f(sacc[kt][i] - t.m_run);
+            lsum += p[i];
+            r1[i] = p[i] - __uint_as_float(__float_as_uint(p[i]) & 0xffff0000u);
+            r2[i] = r1[i] - __uint_as_float(__float_as_uint(r1[i]) & 0xffff0000u);
+        }
+        const int w = kt >> 1, d0 = (kt & 1) * 2;
+        ph[0][w][d0] = pack_hi16(p[0], p[1]);
+        ph[0][w][d0 + 1] = pack_hi16(p[2], p[3]);
+        ph[1][w][d0] = pack_hi16(r1[0], r1[1]);
+        ph[1][w][d0 + 1] = pack_hi16(r1[2], r1[3]);
+        ph[2][w][d0] = pack_hi16(r2[0], r2[1]);
+        ph[2][w][d0 + 1] = pack_hi16(r2[2], r2[3]);
+    }
+    t.l64 += static_cast<double>(lsum);
+}
+
+// O^T[dim][query] += the block's V^T P^T: per 16-dim tile, V^T (transpose reads) against the
+// three P parts of both 32-key windows in fp32, then added into the fp64 O; two tiles at a
+// time, so that few accumulators are live.
+__device__ __forceinline__ void pf_pv(const uint8_t* vp, const uint32_t (&ph)[3][2][4], int lane, PfTile& t) {
+    bf16x8_t pb[2][3];
+#pragma unroll
+    for (int w = 0; w < 2; ++w)
+#pragma unroll
+        for (int s = 0; s < 3; ++s) pb[w][s] = as_bf16x8(make_uint4(ph[s][w][0], ph[s][w][1], ph[s][w][2], ph[s][w][3]));
+#pragma unroll
+    for (int d0 = 0; d0 < 8; d0 += 2) {
+        f32x4_t oacc[2];
+#pragma unroll
+        for (int e = 0; e < 2; ++e) oacc[e] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int w = 0; w < 2; ++w)
+#pragma unroll
+            for (int e = 0; e < 2; ++e) {
+                const bf16x8_t av = pf_vt_operand(vp, w, d0 + e, lane);
+#pragma unroll
+                for (int s = 0; s < 3; ++s)
+                    oacc[e] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, pb[w][s], oacc[e], 0, 0, 0);
+            }
+#pragma unroll
+        for (int e = 0; e < 2; ++e)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) t.o64[d0 + e][i] += static_cast<double>(oacc[e][i]);
+    }
+}
+
 __global__ __launch_bounds__(kPfThreads) void prefill_attn_kernel(PrefillArgs a) {
-    __shared__ __attribute__((aligned(16))) uint16_t k_lds[3 * kKPlane];
-    __shared__ __attribute__((aligned(16))) uint16_t v_lds[kD * kVRow];
+    __shared__ __attribute__((aligned(1024))) uint8_t lds[2 * kBufB];
 
     // Workgroup -> (sequence, KV head, query block).  Workgroups are dealt to the 8 XCDs
     // round-robin; when the (sequence, KV head) pairs divide evenly, all query blocks of
@@ -240,7 +377,7 @@ __global__ __launch_bounds__(kPfThreads) void prefill_attn_kernel(PrefillArgs a)
     const int b = pair / kHkv;
     const int kvh = pair % kHkv;
     const int tid = threadIdx.x;
-    const int wave = tid >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int lane = tid & (kWave - 1);
     const int n = lane & 15;
     const int g = lane >> 4;
@@ -266,10 +403,13 @@ __global__ __launch_bounds__(kPfThreads) void prefill_attn_kernel(PrefillArgs a)
     const int n_keys = st + min(T, qb * kPfPos + kPfPos);
     const int n_keys_wave = st + min(T, t_wave0 + 16);
     const int n_blk = (n_keys + kPfBlk - 1) / kPfBlk;
+    const int64_t head_elem = static_cast<int64_t>(b) * a.kv_batch_stride +
+                              static_cast<int64_t>(kvh) * a.kv_head_stride;
+    const char* kbase = reinterpret_cast<const char*>(a.k + head_elem);
+    const char* vbase = reinterpret_cast<const char*>(a.v + head_elem);
 
-    // First block's rows are requested before the Q operands are formed.
-    PfStage sg;
-    pf_load_block(a, b, kvh, st, 0, n_keys, sg);
+    // Block 0 is requested before the Q operands are formed.
+    pf_issue_block(a, kbase, vbase, b, kvh, st, 0, n_keys, kPfBlk - 1 >= st, lds, wave, lane);
 
     // Q operands: query n = this lane's column, dims 32kb + 8g + j, three BF16 parts.
     bf16x8_t qop[3][4];
@@ -308,149 +448,49 @@ __global__ __launch_bounds__(kPfThreads) void prefill_attn_kernel(PrefillArgs a)
             }
     }
 
-    double o64[8][4];
+    PfTile tl;
 #pragma unroll
     for (int dt = 0; dt < 8; ++dt)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) o64[dt][i] = 0.0;
-    double l64 = 0.0;
-    float m_run = -INFINITY;
+        for (int i = 0; i < 4; ++i) tl.o64[dt][i] = 0.0;
+    tl.l64 = 0.0;
+    tl.m_run = -INFINITY;
 
     for (int blk = 0; blk < n_blk; ++blk) {
-        __syncthreads();                       // every wave is done with the previous block
-        pf_store_block(k_lds, v_lds, sg);
+        // This wave's copies into LDS are complete; after the barrier every wave's are, and
+        // every wave is done with the buffer the next block goes to.
+        __builtin_amdgcn_s_waitcnt(0x0F70);    // vmcnt(0)
         __syncthreads();
-        // Next block's rows (the last block is requested again at the end: the load stays
-        // unconditional, so the compiler never waits for it before the math below).
-        pf_load_block(a, b, kvh, st, min(blk + 1, n_blk - 1), n_keys, sg);
-
+        if (blk + 1 < n_blk) {
+            const int nb = blk + 1;
+            pf_issue_block(a, kbase, vbase, b, kvh, st, nb, n_keys, nb * kPfBlk + kPfBlk - 1 >= st,
+                           lds + (nb & 1) * kBufB, wave, lane);
+        }
         const int key0 = blk * kPfBlk;
         if (!wave_has_q || key0 >= n_keys_wave) continue;
-        const bool has_new = key0 + kPfBlk - 1 >= st;
-
-        // ---- scores S^T[key][query] for the 4 key tiles of the block.
+        const uint8_t* kp = lds + (blk & 1) * kBufB;
         f32x4_t sacc[4];
-#pragma unroll
-        for (int kt = 0; kt < 4; ++kt) sacc[kt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int kb = 0; kb < 4; ++kb) {
-            bf16x8_t ak[4];
-#pragma unroll
-            for (int kt = 0; kt < 4; ++kt)
-                ak[kt] = *reinterpret_cast<const bf16x8_t*>(k_lds + (16 * kt + n) * kKRow + 32 * kb + 8 * g);
-#pragma unroll
-            for (int s = 0; s < 3; ++s)
-#pragma unroll
-                for (int kt = 0; kt < 4; ++kt)
-                    sacc[kt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ak[kt], qop[s][kb], sacc[kt], 0, 0, 0);
-            if (has_new) {
-#pragma unroll
-                for (int kt = 0; kt < 4; ++kt)
-                    ak[kt] = *reinterpret_cast<const bf16x8_t*>(k_lds + kKPlane + (16 * kt + n) * kKRow + 32 * kb + 8 * g);
-#pragma unroll
-                for (int s = 0; s < 2; ++s)
-#pragma unroll
-                    for (int kt = 0; kt < 4; ++kt)
-                        sacc[kt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ak[kt], qop[s][kb], sacc[kt], 0, 0, 0);
-#pragma unroll
-                for (int kt = 0; kt < 4; ++kt)
-                    ak[kt] = *reinterpret_cast<const bf16x8_t*>(k_lds + 2 * kKPlane + (16 * kt + n) * kKRow + 32 * kb + 8 * g);
-#pragma unroll
-                for (int kt = 0; kt < 4; ++kt)
-                    sacc[kt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ak[kt], qop[0][kb], sacc[kt], 0, 0, 0);
-            }
-        }
-
-        // ---- online softmax for query n over keys key0 + 16kt + 4g + i.
-        float sv[4][4];
-#pragma unroll
-        for (int kt = 0; kt < 4; ++kt)
-#pragma unroll
-            for (int i = 0; i < 4; ++i) sv[kt][i] = sacc[kt][i];
-        if (key0 + kPfBlk - 1 > st + t_wave0) {     // the block reaches past some query
-#pragma unroll
-            for (int kt = 0; kt < 4; ++kt)
-#pragma unroll
-                for (int i = 0; i < 4; ++i)
-                    if (key0 + 16 * kt + 4 * g + i > pos_n) sv[kt][i] = -INFINITY;
-        }
-        float bmax = -INFINITY;
-#pragma unroll
-        for (int kt = 0; kt < 4; ++kt)
-#pragma unroll
-            for (int i = 0; i < 4; ++i) bmax = fmaxf(bmax, sv[kt][i]);
-        bmax = fmaxf(bmax, __shfl_xor(bmax, 16));
-        bmax = fmaxf(bmax, __shfl_xor(bmax, 32));
-        const bool grow = bmax > m_run;
-        if (__ballot(grow)) {
-            const float m_new = grow ? ceilf(bmax) : m_run;
-            const int shift = (m_run == -INFINITY) ? 0 : static_cast<int>(m_run - m_new);
-#pragma unroll
-            for (int dt = 0; dt < 8; ++dt)
-#pragma unroll
-                for (int i = 0; i < 4; ++i) o64[dt][i] = ldexp(o64[dt][i], shift);
-            l64 = ldexp(l64, shift);
-            m_run = m_new;
-        }
-        float lsum = 0.f;
-        uint32_t ph[3][2][4];   // [part][window][dword]: BF16 pairs of P^T, B-operand order
-#pragma unroll
-        for (int kt = 0; kt < 4; ++kt) {
-            float p[4], r1[4], r2[4];
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                // v_exp_f32: 2^x, 0 for -inf (masked keys); results below 2^-126 flush
-                // to 0, far below anything the BF16 output can see.
-                p[i] = __builtin_amdgcn_exp2f(sv[kt][i] - m_run);
-                lsum += p[i];
-                r1[i] = p[i] - __uint_as_float(__float_as_uint(p[i]) & 0xffff0000u);
-                r2[i] = r1[i] - __uint_as_float(__float_as_uint(r1[i]) & 0xffff0000u);
-            }
-            const int w = kt >> 1, d0 = (kt & 1) * 2;
-            ph[0][w][d0] = pack_hi16(p[0], p[1]);
-            ph[0][w][d0 + 1] = pack_hi16(p[2], p[3]);
-            ph[1][w][d0] = pack_hi16(r1[0], r1[1]);
-            ph[1][w][d0 + 1] = pack_hi16(r1[2], r1[3]);
-            ph[2][w][d0] = pack_hi16(r2[0], r2[1]);
-            ph[2][w][d0 + 1] = pack_hi16(r2[2], r2[3]);
-        }
-        l64 += static_cast<double>(lsum);
-
-        // ---- O^T[dim][query] += V^T P^T, fp32 per block, then into fp64.
-        f32x4_t oacc[8];
-#pragma unroll
-        for (int dt = 0; dt < 8; ++dt) oacc[dt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int w = 0; w < 2; ++w) {
-            bf16x8_t pb[3];
-#pragma unroll
-            for (int s = 0; s < 3; ++s)
-                pb[s] = as_bf16x8(make_uint4(ph[s][w][0], ph[s][w][1], ph[s][w][2], ph[s][w][3]));
-#pragma unroll
-            for (int dt = 0; dt < 8; ++dt) {
-                const bf16x8_t av = *reinterpret_cast<const bf16x8_t*>(v_lds + (16 * dt + n) * kVRow + 32 * w + 8 * g);
-#pragma unroll
-                for (int s = 0; s < 3; ++s)
-                    oacc[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, pb[s], oacc[dt], 0, 0, 0);
-            }
-        }
-#pragma unroll
-        for (int dt = 0; dt < 8; ++dt)
-#pragma unroll
-            for (int i = 0; i < 4; ++i) o64[dt][i] += static_cast<double>(oacc[dt][i]);
+        if (key0 + kPfBlk - 1 >= st)
+            pf_scores<true>(kp, qop, n, g, sacc);
+        else
+            pf_scores<false>(kp, qop, n, g, sacc);
+        pf_block_max(sacc, key0 + kPfBlk - 1 > st + t_wave0, key0, g, pos_n, tl);
+        uint32_t ph[3][2][4];
+        pf_probs(sacc, tl, ph);
+        pf_pv(kp + kVOff, ph, lane, tl);
     }
 
     if (!q_ok) return;
-    double l = l64 + __shfl_xor(l64, 16);
+    double l = tl.l64 + __shfl_xor(tl.l64, 16);
     l += __shfl_xor(l, 32);
     uint16_t* orow = a.out + ((static_cast<int64_t>(b) * T + tq) * kHq + hq) * kD;
 #pragma unroll
     for (int dt = 0; dt < 8; ++dt) {
         uint2 pk;
-        pk.x = f32_to_bf16_rne(static_cast<float>(o64[dt][0] / l)) |
-               (static_cast<uint32_t>(f32_to_bf16_rne(static_cast<float>(o64[dt][1] / l))) << 16);
-        pk.y = f32_to_bf16_rne(static_cast<float>(o64[dt][2] / l)) |
-               (static_cast<uint32_t>(f32_to_bf16_rne(static_cast<float>(o64[dt][3] / l))) << 16);
+        pk.x = f32_to_bf16_rne(static_cast<float>(tl.o64[dt][0] / l)) |
+               (static_cast<uint32_t>(f32_to_bf16_rne(static_cast<float>(tl.o64[dt][1] / l))) << 16);
+        pk.y = f32_to_bf16_rne(static_cast<float>(tl.o64[dt][2] / l)) |
+               (static_cast<uint32_t>(f32_to_bf16_rne(static_cast<float>(tl.o64[dt][3] / l))) << 16);
         *reinterpret_cast<uint2*>(orow + 16 * dt + 4 * g) = pk;
     }
 }
