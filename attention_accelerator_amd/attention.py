@@ -306,6 +306,47 @@ def gqa_prefill(q: torch.Tensor, k_new: torch.Tensor, v_new: torch.Tensor, k_cac
     return out
 
 
+class PreparedPrefill:
+    """A chunked-prefill call with every argument bound once (the prefill counterpart of
+    PreparedDecode): calling it issues gqa_prefill_bf16 on the current stream with no
+    per-call checks or allocation.  start must be a device int32 tensor whose values
+    satisfy 0 <= start <= S - T (checked on the device: a bad entry gives NaN rows); the
+    tensors passed in must stay alive while it is used."""
+
+    def __init__(self, q: torch.Tensor, k_new: torch.Tensor, v_new: torch.Tensor, k_cache: torch.Tensor,
+                 v_cache: torch.Tensor, start: torch.Tensor, *, rope_q: bool = True, rope_k: bool = True,
+                 theta: float = ROPE_THETA, scale: Optional[float] = None,
+                 out: Optional[torch.Tensor] = None):
+        if q.dim() != 4 or k_new.dim() != 4 or v_new.shape != k_new.shape:
+            raise ValueError("expected q [B,T,32,128] and k_new/v_new [B,T,8,128]")
+        if not (isinstance(start, torch.Tensor) and start.is_cuda and start.dtype == torch.int32):
+            raise ValueError("start must be a device int32 tensor")
+        self.batch, self.n_new = q.shape[0], q.shape[1]
+        if k_new.shape[:2] != (self.batch, self.n_new) or start.numel() != self.batch:
+            raise ValueError("batch / token count mismatch")
+        self.layout = _cache_layout(k_cache, v_cache)
+        self.params = make_params(rope_q=rope_q, rope_k=rope_k, theta=theta, scale=scale)
+        ws_bytes = int(lib().gqa_prefill_workspace_bytes(ctypes.byref(self.params), self.batch, self.n_new))
+        if ws_bytes == 0:
+            check(_lib.GQA_ERR_INVALID_CONFIG, "gqa_prefill_workspace_bytes")
+        self.workspace = torch.empty(ws_bytes, dtype=torch.uint8, device=q.device)
+        self.out = out if out is not None else torch.empty(q.shape, dtype=torch.bfloat16, device=q.device)
+        self._keep = (q.contiguous(), k_new.contiguous(), v_new.contiguous(), k_cache, v_cache,
+                      start.contiguous())
+        qc, kn, vn, kc, vc, st = self._keep
+        self._args = (ctypes.byref(self.params), qc.data_ptr(), kn.data_ptr(), vn.data_ptr(), kc.data_ptr(),
+                      vc.data_ptr(), ctypes.byref(self.layout), st.data_ptr(), self.batch, self.n_new,
+                      self.out.data_ptr(), self.workspace.data_ptr(), ws_bytes)
+        self._fn = lib().gqa_prefill_bf16
+        self.device = q.device
+
+    def __call__(self) -> torch.Tensor:
+        status = self._fn(*self._args, _stream_handle(self.device))
+        if status:
+            check(status, "gqa_prefill_bf16")
+        return self.out
+
+
 def kv_append(k_new: torch.Tensor, v_new: torch.Tensor, k_cache: torch.Tensor,
               v_cache: torch.Tensor, start: Lengths, *, rope_k: bool = True,
               theta: float = ROPE_THETA) -> None:

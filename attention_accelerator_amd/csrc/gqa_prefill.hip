@@ -77,7 +77,8 @@ __device__ __forceinline__ int64_t cache_elem(const PrefillArgs& a, int b, int h
 // ---------------------------------------------------------------------------------
 // KV append: one wave per new (sequence, token); lane i computes the angle of frequency i
 // at position start+t once (pyfiles/gen_gqa_wrapper_vectors.py:30-31) and rotates the
-// pair (i, i+64) of all 8 KV heads' rows in double (:25-35).
+// pair (i, i+64) of all 8 KV heads' rows in double (:25-35).  All 8 heads' rows are
+// requested before any is written, so a wave waits for memory once.
 __global__ __launch_bounds__(256) void kv_append_kernel(PrefillArgs a) {
     const int64_t bt = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);   // b * T + t
     const int lane = threadIdx.x & (kWave - 1);
@@ -94,29 +95,37 @@ __global__ __launch_bounds__(256) void kv_append_kernel(PrefillArgs a) {
     const int64_t pos = static_cast<int64_t>(st) + t;
     const int64_t n_rows = static_cast<int64_t>(a.batch) * a.n_new * kHkv;
     const bool rope = (a.flags & 2u) != 0;
-    double sn = 0.0, cs = 1.0;
-    if (rope) rope_sincos(pos, a.rope.inv_freq[lane], sn, cs);
-#pragma unroll 2
+    uint16_t kx[kHkv], ky[kHkv], vx[kHkv], vy[kHkv];
+    int64_t ce[kHkv];
+#pragma unroll
     for (int kvh = 0; kvh < kHkv; ++kvh) {
         const int64_t row = bt * kHkv + kvh;
-        const uint16_t* ksrc = a.k_new + row * kD;
-        const uint16_t* vsrc = a.v_new + row * kD;
-        const double x = bf16_to_f32(ksrc[lane]);
-        const double y = bf16_to_f32(ksrc[lane + kPairs]);
+        kx[kvh] = a.k_new[row * kD + lane];
+        ky[kvh] = a.k_new[row * kD + lane + kPairs];
+        vx[kvh] = a.v_new[row * kD + lane];
+        vy[kvh] = a.v_new[row * kD + lane + kPairs];
+        ce[kvh] = cache_elem(a, b, kvh, pos);
+    }
+    double sn = 0.0, cs = 1.0;
+    if (rope) rope_sincos(pos, a.rope.inv_freq[lane], sn, cs);
+#pragma unroll
+    for (int kvh = 0; kvh < kHkv; ++kvh) {
+        const int64_t row = bt * kHkv + kvh;
+        const double x = bf16_to_f32(kx[kvh]);
+        const double y = bf16_to_f32(ky[kvh]);
         double xr = x, yr = y;
         if (rope) {
             xr = x * cs - y * sn;
             yr = x * sn + y * cs;
         }
         const uint16_t hx = bf16_of(xr), hy = bf16_of(yr);
-        const int64_t ce = cache_elem(a, b, kvh, pos);
-        if (ce >= 0) {
-            uint16_t* kdst = a.k + ce;
-            uint16_t* vdst = a.v + ce;
+        if (ce[kvh] >= 0) {
+            uint16_t* kdst = a.k + ce[kvh];
+            uint16_t* vdst = a.v + ce[kvh];
             kdst[lane] = hx;
             kdst[lane + kPairs] = hy;
-            vdst[lane] = vsrc[lane];
-            vdst[lane + kPairs] = vsrc[lane + kPairs];
+            vdst[lane] = vx[kvh];
+            vdst[lane + kPairs] = vy[kvh];
         }
         if (a.k_split) {
             const double rx = xr - f64_of_bf16(hx), ry = yr - f64_of_bf16(hy);

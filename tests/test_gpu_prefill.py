@@ -108,6 +108,21 @@ def test_prefill_deterministic_and_workspace_reuse(dev):
     assert np.array_equal(a, b)
 
 
+def test_prepared_prefill_matches_and_repeats(dev):
+    """PreparedPrefill (arguments bound once) gives the bits of gqa_prefill, call after call
+    on the same cache (each call rewrites the chunk's rows with the same values)."""
+    starts = [96, 3]
+    q, kn, vn, k, v = _chunk(2, 40, 160, starts, 11)
+    want, _, _ = _run(q, kn, vn, k, v, starts, dev)
+    kd, vd = k.to(dev), v.to(dev)
+    call = gqa.PreparedPrefill(q.to(dev), kn.to(dev), vn.to(dev), kd, vd,
+                               torch.tensor(starts, dtype=torch.int32, device=dev))
+    for _ in range(3):
+        got = to_codes(call())
+        torch.cuda.synchronize()
+        assert np.array_equal(got, want)
+
+
 def test_prefill_invalid_device_start_gives_nan_rows(dev):
     starts = torch.tensor([40, 500], dtype=torch.int32)     # sequence 1: 500 + 20 > capacity
     q, kn, vn, k, v = _chunk(2, 20, 100, [40, 0], 8)
