@@ -263,6 +263,28 @@ def test_north_star_batch64_ragged(dev):
     print("worst ULP", w)
 
 
+@pytest.mark.parametrize("bsz,hi,seed", [(300, 600, 31), (1000, 48, 32)])
+def test_many_sequences(dev, bsz, hi, seed, monkeypatch):
+    """Batches spanning many 64-sequence windows of the plan (300 sequences up to 600 keys;
+    1000 sequences of 1..48 keys, many segments per workgroup range): every output against
+    the oracle, with and without the fused launch (which takes at most 256 sequences, so
+    B=300 and B=1000 stay on three launches either way).
+
+    V is N(0,1) + 2 so that no output lies near zero: with a few dozen keys the outputs are
+    sums of a few large terms, and the fp32 score error (~1e-7 relative in p) leaves about
+    5e-8 absolute on each output, more than 64 BF16 ULP of an output below ~2e-7 (one of
+    4M N(0,1) outputs here).  That floor is the same on every path."""
+    b = stimulus.decode_batch(bsz, hi, min_len=1, max_len=hi, seed=seed)
+    b = stimulus.DecodeBatch(b.q, b.k, (b.v.float() + 2.0).to(torch.bfloat16), b.seq_len,
+                             b.query_pos)
+    want = _oracle(b)
+    monkeypatch.setenv("GQA_SINGLE_LAUNCH_MAX_KEYS", "0")
+    got = _run(b, dev)
+    assert_within_ulp(want, got, 64, f"B={bsz}")
+    monkeypatch.setenv("GQA_DECODE_FUSED", "1")
+    assert np.array_equal(_run(b, dev), got)
+
+
 def test_fused_launch_matches_three_kernels(dev, monkeypatch):
     """B=64 ragged: the fused launch (plan, Q operands and merge in-kernel) and the
     prepare/stream/merge kernels cut the keys into the same pieces and compute them

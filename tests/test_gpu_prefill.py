@@ -83,6 +83,20 @@ def test_prefill_no_rope(dev):
     assert np.array_equal(to_codes(kd)[0, 3, 70:103], to_codes(kn[0, :, 3]))
 
 
+def test_prefill_position_major_cache(dev):
+    """Cache stored [B][S][8][128] (position-major): same bits as head-major, and the chunk's
+    rows land at the right (position, head)."""
+    starts = [45, 130]
+    q, kn, vn, k, v = _chunk(2, 24, 180, starts, 12)
+    want, kd_ref, _ = _run(q, kn, vn, k, v, starts, dev)
+    kp = k.permute(0, 2, 1, 3).contiguous().to(dev).permute(0, 2, 1, 3)
+    vp = v.permute(0, 2, 1, 3).contiguous().to(dev).permute(0, 2, 1, 3)
+    got = to_codes(gqa.gqa_prefill(q.to(dev), kn.to(dev), vn.to(dev), kp, vp, starts))
+    torch.cuda.synchronize()
+    assert np.array_equal(got, want)
+    assert np.array_equal(to_codes(kp), to_codes(kd_ref))
+
+
 def test_prefill_causal_independence(dev):
     """Token t's output does not depend on chunk rows after t (masked keys contribute
     exactly zero): perturbing rows t+1.. leaves rows 0..t bit-identical."""
