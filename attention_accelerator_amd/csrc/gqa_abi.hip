@@ -126,7 +126,8 @@ DecodePlan plan_decode(int32_t batch, int32_t capacity, bool paged) {
         plan.fused = !paged && use_fused(batch);
         plan.n_slots = static_cast<int64_t>(plan.n_wgs) + static_cast<int64_t>(kHkv) * batch;
         plan.q_op_bytes = static_cast<size_t>(batch) * kHkv * 4 * kWave * sizeof(uint4);
-        plan.plan_bytes = 256 + align_up((static_cast<size_t>(batch) + 1) * sizeof(int64_t), 256);
+        plan.plan_bytes = 256 + align_up((static_cast<size_t>(batch) + 1) * sizeof(int64_t), 256) +
+                          align_up(static_cast<size_t>(batch) * sizeof(int32_t), 256);
     }
     plan.part_o_bytes = align_up(static_cast<size_t>(plan.n_slots) * kGroup * kD * sizeof(double), 256);
     plan.part_ml_bytes = align_up(static_cast<size_t>(plan.n_slots) * kGroup * sizeof(float2), 256);
@@ -210,6 +211,7 @@ int decode_launch(const gqa_params_t* params, const uint16_t* q, const uint16_t*
     char* pl = ws + plan.part_o_bytes + plan.part_ml_bytes + plan.q_op_bytes;
     a.plan_hdr = reinterpret_cast<int64_t*>(pl);
     a.seq_off = reinterpret_cast<int64_t*>(pl + 256);
+    a.seq_nreal = reinterpret_cast<int32_t*>(pl + 256 + align_up((static_cast<size_t>(batch) + 1) * sizeof(int64_t), 256));
     a.seg_count = reinterpret_cast<unsigned long long*>(pl + plan.plan_bytes);
     a.pieces_cap = plan.pieces_cap;
     a.fused = plan.fused;

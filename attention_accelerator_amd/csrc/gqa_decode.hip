@@ -528,7 +528,10 @@ __device__ __forceinline__ void build_plan(const DecodeArgs& a, int lane) {
         const int b = base + lane;
         const int nv = b < a.batch ? plan_keys(a, b) : 0;
         const int64_t incl = wave_incl_scan_i64(nv, lane) + carry;
-        if (b < a.batch) a.seq_off[b] = (incl - nv) * kHkv;
+        if (b < a.batch) {
+            a.seq_off[b] = (incl - nv) * kHkv;
+            a.seq_nreal[b] = seq_valid_keys(a, b);
+        }
         carry = __shfl(incl, kWave - 1);
     }
 }
@@ -687,6 +690,7 @@ struct SeqWindow {
     int64_t o;
     int64_t o1;
     int64_t carry;    // scanned windows: keys (per segment) of the sequences before base + 64
+    int nreal;        // planned windows: keys that count (less than o1 - o for a paged cache)
 };
 
 __device__ __forceinline__ void load_seq_window(const DecodeArgs& a, int base, SeqWindow& sw) {
@@ -694,6 +698,7 @@ __device__ __forceinline__ void load_seq_window(const DecodeArgs& a, int base, S
     sw.base = base;
     sw.o = bb < a.batch ? a.seq_off[bb] : INT64_MAX;
     sw.o1 = bb < a.batch ? a.seq_off[bb + 1] : INT64_MAX;
+    sw.nreal = bb < a.batch ? a.seq_nreal[bb] : 0;
 }
 
 // The same window computed from the lengths (the fused kernel has no plan in memory):
@@ -708,6 +713,7 @@ __device__ __forceinline__ void scan_seq_window(const DecodeArgs& a, int base, i
     sw.o = bb < a.batch ? (incl - nv) * kHkv : INT64_MAX;
     sw.o1 = bb < a.batch ? incl * kHkv : INT64_MAX;
     sw.carry = __shfl(incl, kWave - 1);
+    sw.nreal = nv;
 }
 
 template <bool kScan>
@@ -1188,13 +1194,37 @@ __device__ __forceinline__ void load_page_chunk(const DecodeArgs& a, int64_t ele
         c.vw[it] = load_stream16(vp + static_cast<uint32_t>(min(4 * g + it, r_last)) * row + 16u * n);
 }
 
+// A piece of the paged stream: segment (b, kvh), keys [k_a, k_b) of nvp block-padded keys
+// (kend = the piece's last real key + 1).  Its first chunk is loaded before it starts (by
+// the previous piece, or the kernel's prologue), with the id of its second block.
+struct PagePiece {
+    int b, kvh, nvp, k_a, k_b, kend;
+    int id1;          // block id (vector register) of the piece's second block (clamped)
+    bool ok;          // the first chunk's block id was valid
+};
+
+// The first chunk of piece `p` (block k_a/16 of sequence p.b, id `id0`) into c; returns
+// whether the id was valid.
+__device__ __forceinline__ bool load_first_page_chunk(const DecodeArgs& a, const PagePiece& p, int id0, Chunk& c) {
+    const int lane = threadIdx.x & (kWave - 1);
+    bool ok;
+    const int j0 = p.k_a / kChunk;
+    load_page_chunk(a, page_elem(a, id0, p.kvh, ok), max(1, min(kChunk, p.kend - j0 * kChunk)), lane & 15,
+                    lane >> 4, c);
+    return ok;
+}
+
+// One piece whose first chunk is in c0.  The last iteration's second load fetches the first
+// chunk of `nx` (when has_next; its first block id nx_id0) into c0 -- so that the next
+// piece never waits for its first data -- and sets nx.ok.
 template <bool kRopeK>
-__device__ __forceinline__ void process_page_piece(const DecodeArgs& a, int b, int kvh, int nvp, int nreal,
-                                                   int k_a, int k_b, int64_t wg) {
+__device__ __forceinline__ void process_page_piece(const DecodeArgs& a, const PagePiece& p, int64_t wg, Chunk& c0,
+                                                   Chunk& c1, const bf16x8_t (&bq)[4], bool has_next, PagePiece& nx,
+                                                   int nx_id0) {
     const int lane = threadIdx.x & (kWave - 1);
     const int n = lane & 15;
     const int g = lane >> 4;
-    const int kend = min(k_b, nreal);          // keys past n_valid are block padding
+    const int b = p.b, kvh = p.kvh, k_a = p.k_a, kend = p.kend;
     PieceState st;
 #pragma unroll
     for (int h = 0; h < kGroup; ++h)
@@ -1202,25 +1232,19 @@ __device__ __forceinline__ void process_page_piece(const DecodeArgs& a, int b, i
         for (int j = 0; j < 8; ++j) st.acc[h][j] = 0.0;
     st.m_run = -INFINITY;
     st.l_run = 0.f;
-    bool all_ok = true;
+    bool all_ok = p.ok;
     if (k_a < kend) {
         const int j0 = k_a / kChunk;
         const int jn = (kend - 1) / kChunk;    // last block holding a key of this piece
         const int n_chunks = jn - j0 + 1;
         bool ok;
-        Chunk c0, c1;
         // Block ids are requested two chunks ahead of the chunk whose loads need them, each
         // before that iteration's data loads: waiting for one never waits for data that
         // is still meant to be in flight.
-        const int id_first = load_block_id(a, b, j0);
-        int id_next = load_block_id(a, b, min(j0 + 1, jn));
-        load_page_chunk(a, page_elem(a, id_first, kvh, ok), min(kChunk, kend - j0 * kChunk), n, g, c0);
-        all_ok = all_ok && ok;
-        bf16x8_t bq[4];
-        load_q_operands(a, b, kvh, bq);
-        // One exit, at the end: chunks past the piece's last re-read its last block
-        // (clamped, unconditional loads) and are not computed, so that every path into
-        // the loop head has the same loads in flight.
+        int id_next = p.id1;
+        // One exit, at the end: chunks past the piece's last re-read its last block (or,
+        // for the last one, fetch the next piece's first chunk) and are not computed, so
+        // that every path into the loop head has the same loads in flight.
         for (int i = 0;; i += 2) {
             {
                 const int j = min(j0 + i + 1, jn);
@@ -1231,15 +1255,25 @@ __device__ __forceinline__ void process_page_piece(const DecodeArgs& a, int b, i
             }
             compute_chunk<kRopeK>(a, k_a + i * kChunk, kend, n, g, c0, bq, st);
             {
+                const bool last = i + 2 >= n_chunks;
+                const bool to_next = last && has_next;
                 const int j = min(j0 + i + 2, jn);
                 const int id_after = load_block_id(a, b, min(j + 1, jn));
-                load_page_chunk(a, page_elem(a, id_next, kvh, ok), min(kChunk, kend - j * kChunk), n, g, c0);
-                all_ok = all_ok && ok;
+                const int nj0 = nx.k_a / kChunk;
+                load_page_chunk(a, page_elem(a, to_next ? nx_id0 : id_next, to_next ? nx.kvh : kvh, ok),
+                                to_next ? max(1, min(kChunk, nx.kend - nj0 * kChunk)) : min(kChunk, kend - j * kChunk),
+                                n, g, c0);
+                if (to_next)
+                    nx.ok = ok;
+                else
+                    all_ok = all_ok && ok;
                 id_next = id_after;
             }
             if (i + 1 < n_chunks) compute_chunk<kRopeK>(a, k_a + (i + 1) * kChunk, kend, n, g, c1, bq, st);
             if (i + 2 >= n_chunks) break;
         }
+    } else if (has_next) {
+        nx.ok = load_first_page_chunk(a, nx, nx_id0, c0);   // a piece of padding only
     }
     float m_tot[kGroup];
     double l_tot[kGroup];
@@ -1252,7 +1286,7 @@ __device__ __forceinline__ void process_page_piece(const DecodeArgs& a, int b, i
             l_tot[h] = __longlong_as_double(0x7ff8000000000000ll);
         }
     }
-    if (k_a == 0 && k_b == nvp) {
+    if (k_a == 0 && p.k_b == p.nvp) {
         write_rows(a, b, kvh, st, l_tot);      // the whole segment
         return;
     }
@@ -1262,7 +1296,6 @@ __device__ __forceinline__ void process_page_piece(const DecodeArgs& a, int b, i
 template <bool kRopeK>
 __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(1))) void decode_paged_stream_kernel(DecodeArgs a) {
     const int64_t w = blockIdx.x;
-    const int lane = threadIdx.x;
     const int64_t total = a.plan_hdr[0];
     const int64_t per_wg = a.plan_hdr[1];
     int64_t x = w * per_wg;
@@ -1270,44 +1303,73 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(1))) void
     const int64_t x_end = min(x + per_wg, total);
 
     // Start sequence: the last b with seq_off[b] <= x (it has keys, since x < total).
+    SeqWindow sw;
     int b = 0;
     int64_t off = 0, next = 0;
     for (int base = 0; base < a.batch; base += kWave) {
-        const int bb = base + lane;
-        const int64_t o = bb < a.batch ? a.seq_off[bb] : INT64_MAX;
-        const int64_t o1 = bb < a.batch ? a.seq_off[bb + 1] : INT64_MAX;
-        const uint64_t le = __ballot(o <= x);
+        SeqWindow t;
+        load_seq_window(a, base, t);
+        const uint64_t le = __ballot(t.o <= x);
         if (le) {
             const int j = 63 - __clzll(static_cast<long long>(le));
             b = base + j;
-            off = __shfl(o, j);
-            next = __shfl(o1, j);
+            off = __shfl(t.o, j);
+            next = __shfl(t.o1, j);
+            sw = t;
         }
     }
-    int nvp = static_cast<int>((next - off) / kHkv);
+    PagePiece cur;
+    cur.b = __builtin_amdgcn_readfirstlane(b);
+    cur.nvp = __builtin_amdgcn_readfirstlane(static_cast<int>((next - off) / kHkv));
     const int64_t rel = x - off;
     int kvh = 0;
 #pragma unroll
-    for (int k = 1; k < kHkv; ++k) kvh += rel >= static_cast<int64_t>(k) * nvp;
-    int key = static_cast<int>(rel - static_cast<int64_t>(kvh) * nvp);
+    for (int k = 1; k < kHkv; ++k) kvh += rel >= static_cast<int64_t>(k) * cur.nvp;
+    cur.kvh = __builtin_amdgcn_readfirstlane(kvh);
+    cur.k_a = __builtin_amdgcn_readfirstlane(static_cast<int>(rel - static_cast<int64_t>(cur.kvh) * cur.nvp));
+    cur.k_b = __builtin_amdgcn_readfirstlane(
+        static_cast<int>(min(static_cast<int64_t>(cur.nvp), cur.k_a + (x_end - x))));
+    cur.kend = min(cur.k_b, __builtin_amdgcn_readfirstlane(__shfl(sw.nreal, cur.b - sw.base)));
+    {
+        const int j0 = cur.k_a / kChunk;
+        const int jn = max(j0, (cur.kend - 1) / kChunk);
+        cur.id1 = load_block_id(a, cur.b, min(j0 + 1, jn));
+        cur.ok = true;
+    }
+    Chunk c0, c1;
+    if (cur.k_a < cur.kend) cur.ok = load_first_page_chunk(a, cur, load_block_id(a, cur.b, cur.k_a / kChunk), c0);
+    bf16x8_t bq[4];
+    load_q_operands(a, cur.b, cur.kvh, bq);
+
     while (true) {
-        b = __builtin_amdgcn_readfirstlane(b);
-        kvh = __builtin_amdgcn_readfirstlane(kvh);
-        key = __builtin_amdgcn_readfirstlane(key);
-        nvp = __builtin_amdgcn_readfirstlane(nvp);
-        const int k_b = __builtin_amdgcn_readfirstlane(
-            static_cast<int>(min(static_cast<int64_t>(nvp), key + (x_end - x))));
-        const int nreal = __builtin_amdgcn_readfirstlane(seq_valid_keys(a, b));
-        process_page_piece<kRopeK>(a, b, kvh, nvp, nreal, key, k_b, w);
-        x += k_b - key;
-        if (x >= x_end) break;
-        key = 0;
-        if (++kvh == kHkv) {
-            kvh = 0;
-            nvp = 0;
-            while (nvp == 0 && ++b < a.batch) nvp = plan_keys(a, b);
-            if (nvp == 0) break;   // lengths changed under the launch; nothing left to read
+        // The next piece of this range, and everything it needs before its first chunk
+        // (its length, first two block ids, Q operands), requested during this piece.
+        const int64_t x_next = x + (cur.k_b - cur.k_a);
+        PagePiece nx = cur;
+        int b2 = cur.b, kvh2 = cur.kvh, nv2 = cur.nvp;
+        bool more = x_next < x_end;
+        if (more) more = next_segment(a, sw, b2, kvh2, nv2);
+        int nx_id0 = cur.id1;
+        bf16x8_t bq2[4];
+        if (more) {
+            nx.b = __builtin_amdgcn_readfirstlane(b2);
+            nx.kvh = __builtin_amdgcn_readfirstlane(kvh2);
+            nx.nvp = __builtin_amdgcn_readfirstlane(nv2);
+            nx.k_a = 0;
+            nx.k_b = __builtin_amdgcn_readfirstlane(static_cast<int>(min(static_cast<int64_t>(nx.nvp), x_end - x_next)));
+            nx.kend = min(nx.k_b, __builtin_amdgcn_readfirstlane(__shfl(sw.nreal, nx.b - sw.base)));
+            const int jn2 = max(0, (nx.kend - 1) / kChunk);
+            nx_id0 = load_block_id(a, nx.b, 0);
+            nx.id1 = load_block_id(a, nx.b, min(1, jn2));
+            nx.ok = true;
+            load_q_operands(a, nx.b, nx.kvh, bq2);
         }
+        process_page_piece<kRopeK>(a, cur, w, c0, c1, bq, more, nx, nx_id0);
+        if (!more) break;
+        x = x_next;
+        cur = nx;
+#pragma unroll
+        for (int kb = 0; kb < 4; ++kb) bq[kb] = bq2[kb];
     }
 }
 

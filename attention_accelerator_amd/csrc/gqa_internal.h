@@ -22,6 +22,7 @@ struct DecodeArgs {
     uint4* q_op;              // [B][8][4][64] prepared Q operands (MFMA B layout)
     int64_t* plan_hdr;        // {total keys, keys per stream workgroup}
     int64_t* seq_off;         // [B+1] first global key offset of sequence b's segments
+    int32_t* seq_nreal;       // [B] keys of sequence b that count (n_valid; the plan pads to blocks)
     double* part_o;           // [n_slots][4][128] unnormalised partial outputs
     float2* part_ml;          // [n_slots][4] (integer-valued running max in log2 units, sum)
     unsigned long long* seg_count;  // [B*8] pieces finished per segment, single-launch path (zero between calls)
@@ -53,7 +54,7 @@ struct DecodePlan {
     size_t part_o_bytes;      // fp64 partial outputs at offset 0
     size_t part_ml_bytes;     // then the (m, l) pairs
     size_t q_op_bytes;        // then the prepared Q operands
-    size_t plan_bytes;        // then the plan: header, seq_off[B+1]
+    size_t plan_bytes;        // then the plan: header, seq_off[B+1], seq_nreal[B]
     size_t count_bytes;       // then the per-segment counters of the single-launch path
     size_t workspace_bytes;
 };

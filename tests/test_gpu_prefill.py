@@ -83,6 +83,19 @@ def test_prefill_no_rope(dev):
     assert np.array_equal(to_codes(kd)[0, 3, 70:103], to_codes(kn[0, :, 3]))
 
 
+def test_multi_token_decode_ragged_batch(dev):
+    """Multi-token decode (T=4 new tokens per sequence, e.g. speculative drafts) over a
+    ragged batch of 8 sequences with 100..3000 cached positions, through gqa_prefill:
+    every output row against the oracle's per-token reference step."""
+    g = torch.Generator("cpu").manual_seed(13)
+    starts = [int(x) for x in torch.randint(100, 3001, (8,), generator=g)]
+    q, kn, vn, k, v = _chunk(8, 4, 3004, starts, 13)
+    want = _oracle(q, kn, vn, k, v, starts)
+    got, _, _ = _run(q, kn, vn, k, v, starts, dev)
+    w = assert_within_ulp(want.reshape(-1, 128), got.reshape(-1, 128), 64, "multi-token decode")
+    print("worst ULP", w)
+
+
 def test_prefill_position_major_cache(dev):
     """Cache stored [B][S][8][128] (position-major): same bits as head-major, and the chunk's
     rows land at the right (position, head)."""
