@@ -1468,6 +1468,7 @@ constexpr int kSingleWaves = 4;
 template <bool kRopeQ, bool kRopeK>
 __global__ __launch_bounds__(kSingleWaves * kWave) void decode_single_kernel(DecodeArgs a) {
     __shared__ double q_s[kGroup][kD];
+    __shared__ uint16_t codes_s[3][kGroup][kD];          // hi/mid/lo BF16 parts of q_s
     __shared__ double o_s[kSingleWaves][kGroup][kD];     // each wave's O (row-merged)
     __shared__ float m_s[kSingleWaves][kGroup];
     __shared__ double l_s[kSingleWaves][kGroup];
@@ -1520,14 +1521,31 @@ __global__ __launch_bounds__(kSingleWaves * kWave) void decode_single_kernel(Dec
         q_s[wave][lane + kPairs] = yr * a.qk_scale_log2;
     }
     __syncthreads();
+    // Each value split once (two per thread), then read back in the MFMA B-operand layout
+    // (lane (g, n), MFMA kb: 8 codes of part n/4 of head n%4, dims 32kb + 8g ..).
+    {
+        const int hh = threadIdx.x >> 6;
+        const int d = 2 * lane;
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+            const double v = q_s[hh][d + e];
+            const uint16_t hi = bf16_of(v);
+            const double r1 = v - f64_of_bf16(hi);
+            const uint16_t mid = bf16_of(r1);
+            codes_s[0][hh][d + e] = hi;
+            codes_s[1][hh][d + e] = mid;
+            codes_s[2][hh][d + e] = bf16_of(r1 - f64_of_bf16(mid));
+        }
+    }
+    __syncthreads();
     bf16x8_t bq[4];
+    {
+        const int part = n < 12 ? n >> 2 : 0;
 #pragma unroll
-    for (int kb = 0; kb < 4; ++kb) {
-        uint16_t h8[8];
-#pragma unroll
-        for (int j = 0; j < 8; ++j)
-            h8[j] = n < 12 ? split3(q_s[n & 3][32 * kb + 8 * g + j], n >> 2) : uint16_t(0);
-        bq[kb] = pack8(h8);
+        for (int kb = 0; kb < 4; ++kb) {
+            const bf16x8_t v = *reinterpret_cast<const bf16x8_t*>(&codes_s[part][n & 3][32 * kb + 8 * g]);
+            bq[kb] = n < 12 ? v : bf16x8_t{};
+        }
     }
 
     PieceState st;
@@ -1608,33 +1626,55 @@ __global__ __launch_bounds__(kSingleWaves * kWave) void decode_single_kernel(Dec
     if (!last_s) return;
     if (threadIdx.x == 0) __hip_atomic_store(&a.seg_count[seg], 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 
-    // Merge the segment's pieces, wave h for head h: (m, l) of 64 pieces per pass, one per
-    // lane, then their O rows (lane owns dims 2*lane, 2*lane + 1), 16 requested at a time.
-    float m_all = -INFINITY;
-    for (int p0 = 0; p0 < n_pieces; p0 += kWave) {
-        const int p = p0 + lane;
-        m_all = fmaxf(m_all, p < n_pieces ? load_agent_f2(a.part_ml + (slot0 + p) * kGroup + h).x : -INFINITY);
-    }
-    m_all = wave_max(m_all);
+    // Merge the segment's pieces, wave h for head h (lane owns dims 2*lane, 2*lane + 1), in
+    // piece order.  Up to 16 pieces: every (m, l) and O row requested at once.  More: the
+    // (m, l) of 64 pieces per pass, one per lane, first, then the O rows 16 at a time.
     l = 0.0;
     o0 = 0.0;
     o1 = 0.0;
-    for (int p0 = 0; p0 < n_pieces; p0 += 16) {
+    if (n_pieces <= 16) {
         double2 ov[16];
         float2 ml[16];
 #pragma unroll
         for (int u = 0; u < 16; ++u) {
-            const int p = min(p0 + u, n_pieces - 1);
+            const int p = min(u, n_pieces - 1);
             ov[u] = load_agent_d2(a.part_o + ((slot0 + p) * kGroup + h) * kD + 2 * lane);
             ml[u] = load_agent_f2(a.part_ml + (slot0 + p) * kGroup + h);
         }
+        float m_all = -INFINITY;
+#pragma unroll
+        for (int u = 0; u < 16; ++u) m_all = fmaxf(m_all, ml[u].x);     // copies of the last piece add nothing
 #pragma unroll
         for (int u = 0; u < 16; ++u) {
-            // copies of the last piece (indices clamped above) get weight 0
-            const int e = p0 + u < n_pieces ? static_cast<int>(ml[u].x - m_all) : -1100;
+            const int e = u < n_pieces ? static_cast<int>(ml[u].x - m_all) : -1100;
             l += ldexp(static_cast<double>(ml[u].y), e);
             o0 += ldexp(ov[u].x, e);
             o1 += ldexp(ov[u].y, e);
+        }
+    } else {
+        float m_all = -INFINITY;
+        for (int p0 = 0; p0 < n_pieces; p0 += kWave) {
+            const int p = p0 + lane;
+            m_all = fmaxf(m_all, p < n_pieces ? load_agent_f2(a.part_ml + (slot0 + p) * kGroup + h).x : -INFINITY);
+        }
+        m_all = wave_max(m_all);
+        for (int p0 = 0; p0 < n_pieces; p0 += 16) {
+            double2 ov[16];
+            float2 ml[16];
+#pragma unroll
+            for (int u = 0; u < 16; ++u) {
+                const int p = min(p0 + u, n_pieces - 1);
+                ov[u] = load_agent_d2(a.part_o + ((slot0 + p) * kGroup + h) * kD + 2 * lane);
+                ml[u] = load_agent_f2(a.part_ml + (slot0 + p) * kGroup + h);
+            }
+#pragma unroll
+            for (int u = 0; u < 16; ++u) {
+                // copies of the last piece (indices clamped above) get weight 0
+                const int e = p0 + u < n_pieces ? static_cast<int>(ml[u].x - m_all) : -1100;
+                l += ldexp(static_cast<double>(ml[u].y), e);
+                o0 += ldexp(ov[u].x, e);
+                o1 += ldexp(ov[u].y, e);
+            }
         }
     }
     orow[lane] = f32_to_bf16_rne(static_cast<float>(o0 / l)) |

@@ -236,7 +236,7 @@ def main() -> int:
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported "
-              "(the decode shards by sequence or KV head with no exchange; see DESIGN.md)",
+              "(the decode shards by sequence or KV head with no exchange between GPUs)",
               file=sys.stderr)
         return 2
 

@@ -130,7 +130,7 @@ def test_paged_append_then_decode(dev):
     assert_within_ulp(_oracle(grown), got, 64, "paged append then decode")
 
 
-def test_paged_north_star_batch64_ragged(dev):
+def test_paged_batch64_ragged_512_8192(dev):
     """B=64, lengths U[512, 8192] through a paged pool: every output against the oracle."""
     b = stimulus.decode_batch(64, 8192, min_len=512, max_len=8192, seed=20260805,
                               gen_device="cuda", device=dev)
