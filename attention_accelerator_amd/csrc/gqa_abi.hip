@@ -382,6 +382,11 @@ int prefill_args(const gqa_params_t* params, const uint16_t* k_new, const uint16
         !aligned(start, 4))
         return GQA_ERR_BAD_POINTER;
     if (kv->pos_stride % 8 || kv->head_stride % 8 || kv->batch_stride % 8) return GQA_ERR_BAD_POINTER;
+    // The attention kernel addresses the rows of a 64-key block with 32-bit byte offsets
+    // from the block's first row; the layout's 4 GiB bound per (sequence, KV head) covers it.
+    if ((static_cast<uint64_t>(kv->capacity) + 64u) * static_cast<uint64_t>(kv->pos_stride) * 2u >
+        0xFFFFFF00ull)
+        return GQA_ERR_INVALID_CONFIG;
     a = PrefillArgs{};
     a.k_new = k_new;
     a.v_new = v_new;

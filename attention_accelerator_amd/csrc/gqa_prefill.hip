@@ -16,8 +16,10 @@
 //
 // prefill_attn_kernel: one workgroup of 8 waves per (sequence, KV head, 32 query
 // positions); wave w computes Q head 4*kv_head + (w & 3) for 16 positions.  The K/V
-// rows of each 64-key block are loaded once per workgroup into LDS and used by all 4
+// rows of each 64-key block are copied once per workgroup into LDS and used by all 4
 // heads of the group and all 32 positions (gqa_kv_broadcast.v:38-59 at block scale).
+// K runs one block ahead of V, so that each wave forms block j's probabilities while its
+// MFMAs form block j+1's scores, then accumulates block j's V^T P^T.
 //
 //  * Scores S^T = K Q^T with v_mfma_f32_16x16x32_bf16: A = 16 keys x 32 dims of K from
 //    LDS (row = key), B = Q^T (column = query) held in registers.  Q is rotated and
@@ -46,7 +48,6 @@ constexpr int kPfWaves = 8;                // 4 Q heads x 2 tiles of 16 position
 constexpr int kPfThreads = kPfWaves * kWave;
 constexpr int kPfBlk = 64;                 // keys per K/V block
 
-constexpr uint32_t kPermLo = 0x05040100u;  // v_perm_b32: low halves of (b, a) -> a.lo | b.lo << 16
 constexpr uint32_t kPermHi = 0x07060302u;  // high halves
 
 }  // namespace
@@ -151,53 +152,94 @@ hipError_t launch_kv_append(const PrefillArgs& a, hipStream_t stream) {
 // ---------------------------------------------------------------------------------
 // Attention.
 
-// LDS holds two blocks (double buffer), each: K (the cache row, plane 0), the second and
-// third BF16 parts of chunk keys (planes 1, 2) and V, 64 rows of 256 B per plane (128 KB in
-// all).  Rows are copied from HBM straight into LDS (global_load_lds_dwordx4: lane l of an
-// instruction writes bytes [16l, 16l + 16) of a 1 KB stretch = 4 rows), so a row's 16
-// 16-byte chunks are placed by choosing which chunk each lane fetches: chunk c of row r
-// sits at position c ^ pf_swz(r).  With that swizzle the K operand reads (16 rows, one
-// chunk) and the V^T transpose reads (16 rows, two chunks) hit 64 distinct banks per
-// half-wave.
+// LDS: eight 16 KB planes of 64 rows x 256 B -- K of buffers 0 and 1, V of buffers 0 and 1,
+// then the second and third BF16 parts of chunk keys for buffers 0 and 1 (128 KB in all).
+// K runs one block ahead of V: while block j's probabilities are formed and its V^T P^T
+// accumulated, block j+1's scores are formed from the other K buffer.  Rows are copied from
+// HBM straight into LDS (global_load_lds_dwordx4: lane l of an instruction writes bytes
+// [16l, 16l + 16) of a 1 KB stretch = 4 rows), so a row's 16 16-byte chunks are placed by
+// choosing which chunk each lane fetches: chunk c of row r sits at position c ^ pf_swz(r & 15).
+// With that swizzle the K operand reads (16 rows, one chunk) and the V^T transpose reads
+// (16 rows, two chunks) hit 64 distinct banks per pass, and because it depends on r & 15 only,
+// the rows 16 apart that one lane reads differ by a constant offset.
 constexpr int kRowB = 256;                  // LDS bytes per row
 constexpr int kPlaneB = kPfBlk * kRowB;     // 16 KB per plane
-constexpr int kBufB = 4 * kPlaneB;          // K, K part 2, K part 3, V
-constexpr int kVOff = 3 * kPlaneB;
+constexpr int kOffK = 0;                    // + buffer * kPlaneB
+constexpr int kOffV = 2 * kPlaneB;
+constexpr int kOffK2 = 4 * kPlaneB;
+constexpr int kOffK3 = 6 * kPlaneB;
+constexpr int kLdsB = 8 * kPlaneB;
 
-__device__ __forceinline__ int pf_swz(int row) { return (2 * row + (row >> 3)) & 15; }
+__device__ __forceinline__ int pf_swz(int row) {
+    const int r = row & 15;
+    return (2 * r + (r >> 3)) & 15;
+}
 
 typedef short short4_t __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) void lds_void_t;
-typedef __attribute__((address_space(3))) short4_t lds_short4_t;
 
-// Request block blk into the LDS buffer at `dst`.  Wave w fetches rows
-// 8w .. 8w+7 (two 4-row instructions per plane).  Rows past the keys this workgroup needs
-// repeat its last key; planes 1 and 2 are fetched only for a block holding chunk keys, and a
-// cached key's parts come from the zero row.
-__device__ __forceinline__ void pf_issue_block(const PrefillArgs& a, const char* kbase, const char* vbase,
-                                               int b, int kvh, int st, int blk, int n_keys, bool has_new,
-                                               uint8_t* dst, int wave, int lane) {
-    const int key0 = blk * kPfBlk;
+// Wave w of the workgroup copies rows 8w .. 8w+7 of a plane (two 4-row instructions).
+// Rows past the keys this workgroup needs repeat its last key.
+__device__ __forceinline__ int pf_copy_row(int wave, int ii, int lane) { return 4 * (2 * wave + ii) + (lane >> 4); }
+
+// Request the K rows of block blk into K buffer `buf`, and for a block holding chunk keys the
+// second and third parts of its rows (a cached key's parts come from the zero row).  For a
+// block whose 64 keys all exist the addresses are the block's first row (uniform) plus the
+// lane's 32-bit offset `loff` (pf_copy_offsets).
+__device__ __forceinline__ void pf_issue_k(const PrefillArgs& a, const char* kbase, int b, int kvh, int st,
+                                           int blk, int n_keys, bool has_new, const uint32_t (&loff)[2],
+                                           uint8_t* lds, int buf, int wave, int lane) {
     const int64_t row_bytes = a.kv_pos_stride * 2;
     const int64_t n_rows = static_cast<int64_t>(a.batch) * a.n_new * kHkv;
+    const int key0 = blk * kPfBlk;
+    const bool full = key0 + kPfBlk <= n_keys;
+    const char* brow = kbase + static_cast<int64_t>(key0) * row_bytes;
 #pragma unroll
     for (int ii = 0; ii < 2; ++ii) {
-        const int r = 4 * (2 * wave + ii) + (lane >> 4);
+        const int r = pf_copy_row(wave, ii, lane);
         const int c = (lane & 15) ^ pf_swz(r);
         const int key = min(key0 + r, n_keys - 1);
-        const int stretch = (2 * wave + ii) * 1024;
-        const int64_t off = static_cast<int64_t>(key) * row_bytes + 16 * c;
-        __builtin_amdgcn_global_load_lds(kbase + off, (lds_void_t*)(dst + stretch), 16, 0, 0);
-        __builtin_amdgcn_global_load_lds(vbase + off, (lds_void_t*)(dst + kVOff + stretch), 16, 0, 0);
+        const int stretch = buf * kPlaneB + (2 * wave + ii) * 1024;
+        const char* src = full ? brow + loff[ii] : kbase + static_cast<int64_t>(key) * row_bytes + 16 * c;
+        __builtin_amdgcn_global_load_lds(src, (lds_void_t*)(lds + kOffK + stretch), 16, 0, 0);
         if (has_new) {
             const int u = key - st;          // chunk row of this key (< 0: a cached key)
             const int64_t prow = u < 0 ? 2 * n_rows : (static_cast<int64_t>(b) * a.n_new + u) * kHkv + kvh;
             const int64_t lrow = u < 0 ? 2 * n_rows : n_rows + prow;
             const char* p1 = reinterpret_cast<const char*>(a.k_split + prow * kD) + 16 * c;
             const char* p2 = reinterpret_cast<const char*>(a.k_split + lrow * kD) + 16 * c;
-            __builtin_amdgcn_global_load_lds(p1, (lds_void_t*)(dst + kPlaneB + stretch), 16, 0, 0);
-            __builtin_amdgcn_global_load_lds(p2, (lds_void_t*)(dst + 2 * kPlaneB + stretch), 16, 0, 0);
+            __builtin_amdgcn_global_load_lds(p1, (lds_void_t*)(lds + kOffK2 + stretch), 16, 0, 0);
+            __builtin_amdgcn_global_load_lds(p2, (lds_void_t*)(lds + kOffK3 + stretch), 16, 0, 0);
         }
+    }
+}
+
+// Request the V rows of block blk into V buffer `buf` (addresses as in pf_issue_k).
+__device__ __forceinline__ void pf_issue_v(const PrefillArgs& a, const char* vbase, int blk, int n_keys,
+                                           const uint32_t (&loff)[2], uint8_t* lds, int buf, int wave, int lane) {
+    const int64_t row_bytes = a.kv_pos_stride * 2;
+    const int key0 = blk * kPfBlk;
+    const bool full = key0 + kPfBlk <= n_keys;
+    const char* brow = vbase + static_cast<int64_t>(key0) * row_bytes;
+#pragma unroll
+    for (int ii = 0; ii < 2; ++ii) {
+        const int r = pf_copy_row(wave, ii, lane);
+        const int c = (lane & 15) ^ pf_swz(r);
+        const int key = min(key0 + r, n_keys - 1);
+        const int stretch = buf * kPlaneB + (2 * wave + ii) * 1024;
+        const char* src = full ? brow + loff[ii] : vbase + static_cast<int64_t>(key) * row_bytes + 16 * c;
+        __builtin_amdgcn_global_load_lds(src, (lds_void_t*)(lds + kOffV + stretch), 16, 0, 0);
+    }
+}
+
+// The lane's byte offset from a block's first row for its two copy instructions (below 2^32:
+// the ABI keeps (capacity + 64) rows of a (sequence, KV head) under 4 GiB).
+__device__ __forceinline__ void pf_copy_offsets(const PrefillArgs& a, int wave, int lane, uint32_t (&loff)[2]) {
+    const uint32_t row_bytes = static_cast<uint32_t>(a.kv_pos_stride * 2);
+#pragma unroll
+    for (int ii = 0; ii < 2; ++ii) {
+        const int r = pf_copy_row(wave, ii, lane);
+        loff[ii] = static_cast<uint32_t>(r) * row_bytes + 16u * static_cast<uint32_t>((lane & 15) ^ pf_swz(r));
     }
 }
 
@@ -206,68 +248,38 @@ __device__ __forceinline__ bf16x8_t pf_k_chunk(const uint8_t* plane, int row, in
     return *reinterpret_cast<const bf16x8_t*>(plane + row * kRowB + 16 * (chunk ^ pf_swz(row)));
 }
 
-// V^T operand of the 32-key window w, dims 16dt .. 16dt+15: lane (g, m) gets keys
-// 32w + 4g + i (slots 0..3) and 32w + 16 + 4g + i (slots 4..7) of dim 16dt + m, through two
-// transpose reads (ds_read_b64_tr_b16: lane i of a 16-lane group receives element i%4 of
-// the 8 bytes addressed by lane 4j + i/4, j = 0..3).  Supplying lane a addresses row
-// 32w + 4g + a/4 (+16), dims 16dt + 4(a%4) .. +3.
-__device__ __forceinline__ bf16x8_t pf_vt_operand(const uint8_t* vplane, int w, int dt, int lane) {
-    const int g = lane >> 4;
-    const int a = lane & 15;
-    const int row = 32 * w + 4 * g + (a >> 2);
-    const int chunk = 2 * dt + ((a & 3) >> 1);
-    const int half = (a & 1) * 8;
-    const uint8_t* p0 = vplane + row * kRowB + 16 * (chunk ^ pf_swz(row)) + half;
-    const uint8_t* p1 = vplane + (row + 16) * kRowB + 16 * (chunk ^ pf_swz(row + 16)) + half;
-    const short4_t r0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-        (lds_short4_t*)(p0));
-    const short4_t r1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-        (lds_short4_t*)(p1));
-    union {
-        short4_t h[2];
-        bf16x8_t v;
-    } u;
-    u.h[0] = r0;
-    u.h[1] = r1;
-    return u.v;
-}
-
 // Upper 16 bits of two floats packed as BF16 codes (truncation; used for exact splits).
 __device__ __forceinline__ uint32_t pack_hi16(float lo, float hi) {
     return __builtin_amdgcn_perm(__float_as_uint(hi), __float_as_uint(lo), kPermHi);
 }
 
-// Scores S^T[key][query] of one 16-query tile over the block's 4 key tiles: the 3 BF16 parts
-// of Q against the cache row, and for chunk keys the (k2,q1), (k2,q2), (k3,q1) products.
+// One 32-dim slice (dims 32q .. 32q+31) of the scores S^T[key][query] of one 16-query tile
+// over the block's 4 key tiles: the 3 BF16 parts of Q against the cache row, and for chunk
+// keys the (k2,q1), (k2,q2), (k3,q1) products.
 template <bool kNew>
-__device__ __forceinline__ void pf_scores(const uint8_t* kp, const bf16x8_t (&qop)[3][4], int n, int g,
-                                          f32x4_t (&sacc)[4]) {
+__device__ __forceinline__ void pf_qk_slice(const uint8_t* kplane, const bf16x8_t (&qop)[3][4], int q, int n,
+                                            int g, f32x4_t (&sacc)[4]) {
+    bf16x8_t ak[4];
 #pragma unroll
-    for (int kt = 0; kt < 4; ++kt) sacc[kt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    for (int kt = 0; kt < 4; ++kt) ak[kt] = pf_k_chunk(kplane, 16 * kt + n, 4 * q + g);
 #pragma unroll
-    for (int kb = 0; kb < 4; ++kb) {
-        bf16x8_t ak[4];
+    for (int s = 0; s < 3; ++s)
 #pragma unroll
-        for (int kt = 0; kt < 4; ++kt) ak[kt] = pf_k_chunk(kp, 16 * kt + n, 4 * kb + g);
+        for (int kt = 0; kt < 4; ++kt)
+            sacc[kt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ak[kt], qop[s][q], sacc[kt], 0, 0, 0);
+    if (kNew) {
 #pragma unroll
-        for (int s = 0; s < 3; ++s)
+        for (int kt = 0; kt < 4; ++kt) ak[kt] = pf_k_chunk(kplane + (kOffK2 - kOffK), 16 * kt + n, 4 * q + g);
 #pragma unroll
-            for (int kt = 0; kt < 4; ++kt)
-                sacc[kt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ak[kt], qop[s][kb], sacc[kt], 0, 0, 0);
-        if (kNew) {
-#pragma unroll
-            for (int kt = 0; kt < 4; ++kt) ak[kt] = pf_k_chunk(kp + kPlaneB, 16 * kt + n, 4 * kb + g);
-#pragma unroll
-            for (int s = 0; s < 2; ++s)
-#pragma unroll
-                for (int kt = 0; kt < 4; ++kt)
-                    sacc[kt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ak[kt], qop[s][kb], sacc[kt], 0, 0, 0);
-#pragma unroll
-            for (int kt = 0; kt < 4; ++kt) ak[kt] = pf_k_chunk(kp + 2 * kPlaneB, 16 * kt + n, 4 * kb + g);
+        for (int s = 0; s < 2; ++s)
 #pragma unroll
             for (int kt = 0; kt < 4; ++kt)
-                sacc[kt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ak[kt], qop[0][kb], sacc[kt], 0, 0, 0);
-        }
+                sacc[kt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ak[kt], qop[s][q], sacc[kt], 0, 0, 0);
+#pragma unroll
+        for (int kt = 0; kt < 4; ++kt) ak[kt] = pf_k_chunk(kplane + (kOffK3 - kOffK), 16 * kt + n, 4 * q + g);
+#pragma unroll
+        for (int kt = 0; kt < 4; ++kt)
+            sacc[kt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ak[kt], qop[0][q], sacc[kt], 0, 0, 0);
     }
 }
 
@@ -279,9 +291,11 @@ struct PfTile {
     float m_run;
 };
 
-// Block max of a tile's scores (masking keys past each query on diagonal blocks); grows the
-// running max to ceil(block max) and rescales O and l by the exact power of two.
-__device__ __forceinline__ void pf_block_max(f32x4_t (&sacc)[4], bool diag, int key0, int g, int pos_n, PfTile& t) {
+// Running max after a block: masks keys past each query on diagonal blocks, then returns
+// ceil(block max) where that exceeds the running max m (integer-valued, so every rescale is an
+// exact power of two), else m.  The two cross-row steps are gfx950 lane swaps (rows 16 and 32
+// lanes apart), not LDS permutes.
+__device__ __forceinline__ float pf_next_max(f32x4_t (&sacc)[4], bool diag, int key0, int g, int pos_n, float m) {
     if (diag) {
 #pragma unroll
         for (int kt = 0; kt < 4; ++kt)
@@ -294,11 +308,16 @@ __device__ __forceinline__ void pf_block_max(f32x4_t (&sacc)[4], bool diag, int 
     for (int kt = 0; kt < 4; ++kt)
 #pragma unroll
         for (int i = 0; i < 4; ++i) bmax = fmaxf(bmax, sacc[kt][i]);
-    bmax = fmaxf(bmax, __shfl_xor(bmax, 16));
-    bmax = fmaxf(bmax, __shfl_xor(bmax, 32));
-    const bool grow = bmax > t.m_run;
-    if (__ballot(grow)) {
-        const float m_new = grow ? ceilf(bmax) : t.m_run;
+    const auto x16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(bmax), __float_as_uint(bmax), false, false);
+    bmax = fmaxf(__uint_as_float(x16[0]), __uint_as_float(x16[1]));
+    const auto x32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(bmax), __float_as_uint(bmax), false, false);
+    bmax = fmaxf(__uint_as_float(x32[0]), __uint_as_float(x32[1]));
+    return bmax > m ? ceilf(bmax) : m;
+}
+
+// Moves O and l to the running max m_new (exact power-of-two scaling).
+__device__ __forceinline__ void pf_rescale(PfTile& t, float m_new) {
+    if (__ballot(m_new != t.m_run)) {
         const int shift = (t.m_run == -INFINITY) ? 0 : static_cast<int>(t.m_run - m_new);
 #pragma unroll
         for (int dt = 0; dt < 8; ++dt)
@@ -309,44 +328,101 @@ __device__ __forceinline__ void pf_block_max(f32x4_t (&sacc)[4], bool diag, int 
     }
 }
 
-// p = 2^(s - m) (0 for masked keys), summed into l, split by truncation into three BF16
-// parts packed as the P^T B operand: ph[part][window][dword].
-__device__ __forceinline__ void pf_probs(const f32x4_t (&sacc)[4], PfTile& t, uint32_t (&ph)[3][2][4]) {
-    float lsum = 0.f;
+// p = 2^(s - m) of key tile kt (0 for masked keys), summed into lsum, split by truncation
+// into three BF16 parts packed as the P^T B operand: ph[part][window][dword].
+__device__ __forceinline__ void pf_probs_tile(const f32x4_t& s, float m, float& lsum, uint32_t (&ph)[3][2][4],
+                                              int kt) {
+    float p[4], r1[4], r2[4];
 #pragma unroll
-    for (int kt = 0; kt < 4; ++kt) {
-        float p[4], r1[4], r2[4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            // v_exp_f32: 2^x, 0 for -inf (masked keys); results below 2^-126 flush to 0,
-            // far below anything the BF16 output can see.
-            p[i] = __builtin_amdgcn_exp2f(sacc[kt][i] - t.m_run);
-            lsum += p[i];
-            r1[i] = p[i] - __uint_as_float(__float_as_uint(p[i]) & 0xffff0000u);
-            r2[i] = r1[i] - __uint_as_float(__float_as_uint(r1[i]) & 0xffff0000u);
-        }
-        const int w = kt >> 1, d0 = (kt & 1) * 2;
-        ph[0][w][d0] = pack_hi16(p[0], p[1]);
-        ph[0][w][d0 + 1] = pack_hi16(p[2], p[3]);
-        ph[1][w][d0] = pack_hi16(r1[0], r1[1]);
-        ph[1][w][d0 + 1] = pack_hi16(r1[2], r1[3]);
-        ph[2][w][d0] = pack_hi16(r2[0], r2[1]);
-        ph[2][w][d0 + 1] = pack_hi16(r2[2], r2[3]);
+    for (int i = 0; i < 4; ++i) {
+        // v_exp_f32: 2^x, 0 for -inf (masked keys); results below 2^-126 flush to 0, far
+        // below anything the BF16 output can see.
+        p[i] = __builtin_amdgcn_exp2f(s[i] - m);
+        lsum += p[i];
+        r1[i] = p[i] - __uint_as_float(__float_as_uint(p[i]) & 0xffff0000u);
+        r2[i] = r1[i] - __uint_as_float(__float_as_uint(r1[i]) & 0xffff0000u);
     }
-    t.l64 += static_cast<double>(lsum);
+    const int w = kt >> 1, d0 = (kt & 1) * 2;
+    ph[0][w][d0] = pack_hi16(p[0], p[1]);
+    ph[0][w][d0 + 1] = pack_hi16(p[2], p[3]);
+    ph[1][w][d0] = pack_hi16(r1[0], r1[1]);
+    ph[1][w][d0 + 1] = pack_hi16(r1[2], r1[3]);
+    ph[2][w][d0] = pack_hi16(r2[0], r2[1]);
+    ph[2][w][d0 + 1] = pack_hi16(r2[2], r2[3]);
+}
+
+// V^T operands of one 16-dim tile dt for both 32-key windows: lane (g, m) gets keys
+// 32w + 4g + i (slots 0..3) and 32w + 16 + 4g + i (slots 4..7) of dim 16dt + m, through
+// transpose reads (ds_read_b64_tr_b16: lane i of a 16-lane group receives element i%4 of the
+// 8 bytes addressed by lane 4j + i/4, j = 0..3).  Supplying lane a addresses row
+// 32w + 4g + a/4 (+16), dims 16dt + 4(a%4) .. +3; `addr` is that address for w = 0 without
+// the +16, and the other three rows are 16, 32 and 48 rows further.
+//
+// The reads are issued from inline assembly and waited for by pf_vt_wait: the compiler
+// treats every transpose read as possibly reading LDS that an outstanding copy writes and
+// would wait for all of them (the next block's copies included) before the first one.  The
+// copies that fill the buffer read here completed before the barrier that opened this block.
+struct VtPair {
+    short4_t r[2][2];   // [window][half]
+};
+
+__device__ __forceinline__ VtPair pf_vt_issue(uint32_t addr) {
+    VtPair v;
+    asm volatile("ds_read_b64_tr_b16 %0, %1" : "=v"(v.r[0][0]) : "v"(addr));
+    asm volatile("ds_read_b64_tr_b16 %0, %1 offset:4096" : "=v"(v.r[0][1]) : "v"(addr));
+    asm volatile("ds_read_b64_tr_b16 %0, %1 offset:8192" : "=v"(v.r[1][0]) : "v"(addr));
+    asm volatile("ds_read_b64_tr_b16 %0, %1 offset:12288" : "=v"(v.r[1][1]) : "v"(addr));
+    return v;
+}
+
+// Waits for every outstanding LDS read (lgkmcnt(0)); tied to the operands so that their uses
+// stay behind it.
+__device__ __forceinline__ void pf_vt_wait(VtPair& v0, VtPair& v1) {
+    asm volatile("s_waitcnt lgkmcnt(0)"
+                 : "+v"(v0.r[0][0]), "+v"(v0.r[0][1]), "+v"(v0.r[1][0]), "+v"(v0.r[1][1]), "+v"(v1.r[0][0]),
+                   "+v"(v1.r[0][1]), "+v"(v1.r[1][0]), "+v"(v1.r[1][1]));
+}
+
+__device__ __forceinline__ bf16x8_t pf_vt_operand(const VtPair& v, int w) {
+    union {
+        short4_t h[2];
+        bf16x8_t v;
+    } u;
+    u.h[0] = v.r[w][0];
+    u.h[1] = v.r[w][1];
+    return u.v;
+}
+
+// Per-lane LDS address of the transpose reads of dim tile dt (V buffer 0, window 0).
+__device__ __forceinline__ uint32_t pf_vt_addr(uint32_t lds_base, int dt, int lane) {
+    const int g = lane >> 4;
+    const int a = lane & 15;
+    const int row = 4 * g + (a >> 2);
+    const int chunk = 2 * dt + ((a & 3) >> 1);
+    return lds_base + kOffV + row * kRowB + 16 * (chunk ^ pf_swz(row)) + (a & 1) * 8;
 }
 
 // O^T[dim][query] += the block's V^T P^T: per 16-dim tile, V^T (transpose reads) against the
 // three P parts of both 32-key windows in fp32, then added into the fp64 O; two tiles at a
-// time, so that few accumulators are live.
-__device__ __forceinline__ void pf_pv(const uint8_t* vp, const uint32_t (&ph)[3][2][4], int lane, PfTile& t) {
+// time, the next two tiles' operands requested before the current two's products.
+__device__ __forceinline__ void pf_pv(const uint32_t (&vaddr)[8], uint32_t voff, const uint32_t (&ph)[3][2][4],
+                                      PfTile& t) {
     bf16x8_t pb[2][3];
 #pragma unroll
     for (int w = 0; w < 2; ++w)
 #pragma unroll
         for (int s = 0; s < 3; ++s) pb[w][s] = as_bf16x8(make_uint4(ph[s][w][0], ph[s][w][1], ph[s][w][2], ph[s][w][3]));
+    VtPair cur[2];
+    cur[0] = pf_vt_issue(vaddr[0] + voff);
+    cur[1] = pf_vt_issue(vaddr[1] + voff);
 #pragma unroll
     for (int d0 = 0; d0 < 8; d0 += 2) {
+        pf_vt_wait(cur[0], cur[1]);
+        VtPair nxt[2];
+        if (d0 + 2 < 8) {
+            nxt[0] = pf_vt_issue(vaddr[d0 + 2] + voff);
+            nxt[1] = pf_vt_issue(vaddr[d0 + 3] + voff);
+        }
         f32x4_t oacc[2];
 #pragma unroll
         for (int e = 0; e < 2; ++e) oacc[e] = f32x4_t{0.f, 0.f, 0.f, 0.f};
@@ -354,7 +430,7 @@ __device__ __forceinline__ void pf_pv(const uint8_t* vp, const uint32_t (&ph)[3]
         for (int w = 0; w < 2; ++w)
 #pragma unroll
             for (int e = 0; e < 2; ++e) {
-                const bf16x8_t av = pf_vt_operand(vp, w, d0 + e, lane);
+                const bf16x8_t av = pf_vt_operand(cur[e], w);
 #pragma unroll
                 for (int s = 0; s < 3; ++s)
                     oacc[e] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, pb[w][s], oacc[e], 0, 0, 0);
@@ -363,11 +439,33 @@ __device__ __forceinline__ void pf_pv(const uint8_t* vp, const uint32_t (&ph)[3]
         for (int e = 0; e < 2; ++e)
 #pragma unroll
             for (int i = 0; i < 4; ++i) t.o64[d0 + e][i] += static_cast<double>(oacc[e][i]);
+        if (d0 + 2 < 8) {
+            cur[0] = nxt[0];
+            cur[1] = nxt[1];
+        }
     }
 }
 
+// Probabilities of the current block (scores `scur`, running max already grown) interleaved
+// with the scores of the next block from K buffer `kplane` (kNext: there is one; kNew: it
+// holds chunk keys).
+template <bool kNext, bool kNew>
+__device__ __forceinline__ void pf_probs_and_next(const f32x4_t (&scur)[4], const uint8_t* kplane,
+                                                  const bf16x8_t (&qop)[3][4], int n, int g, PfTile& t,
+                                                  uint32_t (&ph)[3][2][4], f32x4_t (&snext)[4]) {
+#pragma unroll
+    for (int kt = 0; kt < 4; ++kt) snext[kt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    float lsum = 0.f;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        if (kNext) pf_qk_slice<kNew>(kplane, qop, q, n, g, snext);
+        pf_probs_tile(scur[q], t.m_run, lsum, ph, q);
+    }
+    t.l64 += static_cast<double>(lsum);
+}
+
 __global__ __launch_bounds__(kPfThreads) void prefill_attn_kernel(PrefillArgs a) {
-    __shared__ __attribute__((aligned(1024))) uint8_t lds[2 * kBufB];
+    __shared__ __attribute__((aligned(1024))) uint8_t lds[kLdsB];
 
     // Workgroup -> (sequence, KV head, query block).  Workgroups are dealt to the 8 XCDs
     // round-robin; when the (sequence, KV head) pairs divide evenly, all query blocks of
@@ -406,19 +504,27 @@ __global__ __launch_bounds__(kPfThreads) void prefill_attn_kernel(PrefillArgs a)
         return;
     }
 
+    // Every wave runs every block of the workgroup; a block past the keys of this wave's
+    // queries is masked for all of them (block 0 always holds a valid key, so the running
+    // max is finite from the first block on).  Waves past the last query compute the last
+    // query and write nothing.
     const int tq_c = min(tq, T - 1);
     const int pos_n = st + tq_c;            // this lane's query position
-    const bool wave_has_q = t_wave0 < T;
     const int n_keys = st + min(T, qb * kPfPos + kPfPos);
-    const int n_keys_wave = st + min(T, t_wave0 + 16);
     const int n_blk = (n_keys + kPfBlk - 1) / kPfBlk;
     const int64_t head_elem = static_cast<int64_t>(b) * a.kv_batch_stride +
                               static_cast<int64_t>(kvh) * a.kv_head_stride;
     const char* kbase = reinterpret_cast<const char*>(a.k + head_elem);
     const char* vbase = reinterpret_cast<const char*>(a.v + head_elem);
+    auto blk_new = [&](int blk) { return blk * kPfBlk + kPfBlk - 1 >= st; };
+    auto blk_diag = [&](int blk) { return blk * kPfBlk + kPfBlk - 1 > st + t_wave0; };
 
-    // Block 0 is requested before the Q operands are formed.
-    pf_issue_block(a, kbase, vbase, b, kvh, st, 0, n_keys, kPfBlk - 1 >= st, lds, wave, lane);
+    // K of blocks 0 and 1 and V of block 0 are requested before the Q operands are formed.
+    uint32_t loff[2];
+    pf_copy_offsets(a, wave, lane, loff);
+    pf_issue_k(a, kbase, b, kvh, st, 0, n_keys, blk_new(0), loff, lds, 0, wave, lane);
+    pf_issue_v(a, vbase, 0, n_keys, loff, lds, 0, wave, lane);
+    if (n_blk > 1) pf_issue_k(a, kbase, b, kvh, st, 1, n_keys, blk_new(1), loff, lds, 1, wave, lane);
 
     // Q operands: query n = this lane's column, dims 32kb + 8g + j, three BF16 parts.
     bf16x8_t qop[3][4];
@@ -457,6 +563,11 @@ __global__ __launch_bounds__(kPfThreads) void prefill_attn_kernel(PrefillArgs a)
             }
     }
 
+    const uint32_t lds_base = static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_void_t*)(lds)));
+    uint32_t vaddr[8];
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt) vaddr[dt] = pf_vt_addr(lds_base, dt, lane);
+
     PfTile tl;
 #pragma unroll
     for (int dt = 0; dt < 8; ++dt)
@@ -465,28 +576,58 @@ __global__ __launch_bounds__(kPfThreads) void prefill_attn_kernel(PrefillArgs a)
     tl.l64 = 0.0;
     tl.m_run = -INFINITY;
 
+    // Block 0's scores.  The barrier after them frees K buffer 0 for block 2.
+    __builtin_amdgcn_s_waitcnt(0x0F70);    // vmcnt(0)
+    __syncthreads();
+    f32x4_t scur[4];
+#pragma unroll
+    for (int kt = 0; kt < 4; ++kt) scur[kt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    if (blk_new(0)) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) pf_qk_slice<true>(lds + kOffK, qop, q, n, g, scur);
+    } else {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) pf_qk_slice<false>(lds + kOffK, qop, q, n, g, scur);
+    }
+    pf_rescale(tl, pf_next_max(scur, blk_diag(0), 0, g, pos_n, tl.m_run));
+    __syncthreads();
+
     for (int blk = 0; blk < n_blk; ++blk) {
+        // Resident: K of block blk+1 (K buffer (blk+1)&1) and V of block blk (V buffer blk&1).
+        // Free: K buffer blk&1 (block blk, scored in the previous step) and V buffer
+        // (blk+1)&1 (block blk-1).
+        if (blk + 2 < n_blk)
+            pf_issue_k(a, kbase, b, kvh, st, blk + 2, n_keys, blk_new(blk + 2), loff, lds, blk & 1, wave, lane);
+        if (blk + 1 < n_blk) pf_issue_v(a, vbase, blk + 1, n_keys, loff, lds, (blk + 1) & 1, wave, lane);
+
+        uint32_t ph[3][2][4];
+        f32x4_t snext[4];
+        const uint8_t* knext = lds + kOffK + ((blk + 1) & 1) * kPlaneB;
+        // The two waves of a SIMD run the same steps; the one in this MFMA + VALU mix gets
+        // issue priority over the other's V^T P^T (5 % faster than equal priorities).
+        __builtin_amdgcn_s_setprio(1);
+        if (blk + 1 >= n_blk)
+            pf_probs_and_next<false, false>(scur, knext, qop, n, g, tl, ph, snext);
+        else if (blk_new(blk + 1))
+            pf_probs_and_next<true, true>(scur, knext, qop, n, g, tl, ph, snext);
+        else
+            pf_probs_and_next<true, false>(scur, knext, qop, n, g, tl, ph, snext);
+        __builtin_amdgcn_s_setprio(0);
+
+        // The next block's running max is found before this block's V^T P^T (which still
+        // accumulates at the current max); O and l move to it afterwards.
+        float m_next = tl.m_run;
+        if (blk + 1 < n_blk) m_next = pf_next_max(snext, blk_diag(blk + 1), (blk + 1) * kPfBlk, g, pos_n, tl.m_run);
+
+        pf_pv(vaddr, (blk & 1) * kPlaneB, ph, tl);
+
+        pf_rescale(tl, m_next);
+#pragma unroll
+        for (int kt = 0; kt < 4; ++kt) scur[kt] = snext[kt];
         // This wave's copies into LDS are complete; after the barrier every wave's are, and
-        // every wave is done with the buffer the next block goes to.
+        // every wave is done with the buffers the next step's copies go to.
         __builtin_amdgcn_s_waitcnt(0x0F70);    // vmcnt(0)
         __syncthreads();
-        if (blk + 1 < n_blk) {
-            const int nb = blk + 1;
-            pf_issue_block(a, kbase, vbase, b, kvh, st, nb, n_keys, nb * kPfBlk + kPfBlk - 1 >= st,
-                           lds + (nb & 1) * kBufB, wave, lane);
-        }
-        const int key0 = blk * kPfBlk;
-        if (!wave_has_q || key0 >= n_keys_wave) continue;
-        const uint8_t* kp = lds + (blk & 1) * kBufB;
-        f32x4_t sacc[4];
-        if (key0 + kPfBlk - 1 >= st)
-            pf_scores<true>(kp, qop, n, g, sacc);
-        else
-            pf_scores<false>(kp, qop, n, g, sacc);
-        pf_block_max(sacc, key0 + kPfBlk - 1 > st + t_wave0, key0, g, pos_n, tl);
-        uint32_t ph[3][2][4];
-        pf_probs(sacc, tl, ph);
-        pf_pv(kp + kVOff, ph, lane, tl);
     }
 
     if (!q_ok) return;

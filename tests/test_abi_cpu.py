@@ -169,6 +169,7 @@ def _prefill(p, *, q=256, kn=256, vn=256, k=256, v=256, layout=None, start=256, 
     (dict(p=_params(), n_new=0), BAD_CFG),
     (dict(p=_params(), n_new=65), BAD_CFG),                      # chunk longer than the cache
     (dict(p=_params(), layout=GqaKvLayout(0, 0, 64, 64)), BAD_CFG),
+    (dict(p=_params(), layout=GqaKvLayout(0, 0, 1 << 25, 64)), BAD_CFG),   # rows span >= 4 GiB
     (dict(p=None), BAD_PTR),
     (dict(p=_params(), q=None), BAD_PTR),
     (dict(p=_params(), kn=None), BAD_PTR),
