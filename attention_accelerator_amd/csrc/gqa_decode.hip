@@ -3,24 +3,32 @@
 //
 // One decode step of the reference core (gqa_controller.v:140-277 loop nest, datapath
 // rope_unit -> bf16_dot_product_mac -> scale_unit -> flash_softmax ->
-// output_accumulator -> gqa_output_collector) is decode_stream_kernel, a persistent
-// grid of n_wgs one-wave workgroups, followed by decode_merge_kernel:
+// output_accumulator -> gqa_output_collector) is, by default, three launches on one
+// stream: decode_prepare_kernel (the plan of pieces below, and every segment's 4 Q rows
+// rotated, scaled and split into MFMA operands once), decode_stream_kernel (a persistent
+// grid of n_wgs one-wave workgroups) and decode_merge_kernel:
 //
 //  * The keys of every (sequence, kv_head) segment are laid end to end (segment =
 //    b*8 + h, n_valid(b) keys each) and cut into n_wgs equal ranges, one per
 //    workgroup, so every wave streams the same number of K/V rows whatever the
 //    length mix.  The part of one segment inside one range is a "piece".
-//  * Inside a piece the wave rotates and scales the 4 Q rows of its group once and
-//    reuses every K/V row for the 4 Q heads (gqa_kv_broadcast.v:38-59), keeping the
-//    next 16-key chunk in flight while it computes the current one.
+//  * Inside a piece the wave reuses every K/V row for the 4 Q heads of its group
+//    (gqa_kv_broadcast.v:38-59), keeping the next 16-key chunk in flight while it
+//    computes the current one; the next piece's first chunk is requested before the
+//    current piece ends.
 //  * A piece that is a whole segment normalises and writes its 4 output rows
 //    (output_accumulator.v:540-686, BF16 in Q-head order, gqa_output_collector.v:32-61).
 //    Otherwise it leaves an unnormalised partial (O[4][128] fp64, running max m,
 //    sum l) at slot wg + segment -- unique because both increase along the key
 //    order -- and decode_merge_kernel, launched next on the same stream, merges the
-//    pieces of each such segment.  The kernel boundary orders the partials; an
-//    in-kernel "last piece merges" scheme would need a device-scope release per
-//    piece, which on gfx950 writes back the XCD's L2 and measured 1.65x slower.
+//    pieces of each such segment; the kernel boundary orders the partials.
+//
+// Other launch shapes of the same step: decode_single_kernel (small batches: one launch,
+// one 4-wave workgroup per piece of a segment, the last piece of a segment to finish
+// merges it after an agent-scope counter), decode_fused_kernel (opt-in, batches up to kFusedMaxBatch: the
+// stream kernel planning its own range and forming its own Q operands, split segments
+// merged in-kernel the same way) and decode_paged_stream_kernel (the stream kernel over
+// a block-table cache).
 //
 // Arithmetic (the golden model is double, pyfiles/gen_gqa_wrapper_vectors.py:121-139):
 //  * Q is rotated in double, scaled by scale*log2(e) in double and split into three
