@@ -9,9 +9,11 @@
 // grid of n_wgs one-wave workgroups) and decode_merge_kernel:
 //
 //  * The keys of every (sequence, kv_head) segment are laid end to end (segment =
-//    b*8 + h, n_valid(b) keys each) and cut into n_wgs equal ranges, one per
-//    workgroup, so every wave streams the same number of K/V rows whatever the
-//    length mix.  The part of one segment inside one range is a "piece".
+//    b*8 + h, n_valid(b) keys each; in a batch of segments shorter than a few ranges,
+//    each preceded by a lead of positions that stands for a piece's fixed cost) and cut
+//    into n_wgs equal ranges, one per workgroup, so every wave takes about as long
+//    whatever the length mix.  The part of one segment's keys inside one range is a
+//    "piece".
 //  * Inside a piece the wave reuses every K/V row for the 4 Q heads of its group
 //    (gqa_kv_broadcast.v:38-59), keeping the next 16-key chunk in flight while it
 //    computes the current one; the next piece's first chunk is requested before the
@@ -85,6 +87,12 @@ __device__ __forceinline__ int64_t wave_sum_i64(int64_t x) {
     return x;
 }
 
+__device__ __forceinline__ int64_t wave_max_i64(int64_t x) {
+#pragma unroll
+    for (int d = 1; d < kWave; d <<= 1) x = max(x, static_cast<int64_t>(__shfl_xor(x, d)));
+    return x;
+}
+
 __device__ __forceinline__ int64_t wave_incl_scan_i64(int64_t x, int lane) {
 #pragma unroll
     for (int d = 1; d < kWave; d <<= 1) {
@@ -101,18 +109,70 @@ __device__ __forceinline__ int plan_keys(const DecodeArgs& a, int b) {
     return a.block_table ? (nv + kChunk - 1) / kChunk * kChunk : nv;
 }
 
-// Total keys over all segments (8 per sequence) and the per-workgroup range size.
-__device__ __forceinline__ void stream_totals(const DecodeArgs& a, int lane, int64_t& total,
-                                              int64_t& per_wg) {
-    int64_t t = 0;
+// Each segment's span in the stream-K key space: `lead` positions that hold no key, then
+// its plan_keys keys (0 for a sequence with no key).  A range pays for the lead of every
+// segment it starts a piece of -- about what a piece's fixed cost (row merge, output or
+// partial, first requests) takes in streaming time -- so that a range crossing many
+// segment starts gets fewer keys and every range takes about as long.  The lead is
+// kSegLead when every segment is shorter than kLeadRanges ranges, else 0: a batch of
+// segments many ranges long gains little from it and its ranges would no longer line up
+// with the segments (one piece each when the lengths divide evenly).
+constexpr int kSegLead = 32;
+constexpr int kLeadRanges = 4;
+
+__device__ __forceinline__ int plan_span(const DecodeArgs& a, int b, int lead) {
+    const int k = plan_keys(a, b);
+    return k > 0 ? k + lead : 0;
+}
+
+// The first piece of a range that starts at stream position x inside sequence b's
+// segments, which span [off, next): its KV head, first key (0 when x falls in a segment's
+// lead), the segment's keys, and x moved to the stream position of that first key.
+__device__ __forceinline__ void locate_first_piece(int64_t off, int64_t next, int lead, int64_t& x, int& kvh,
+                                                   int& key, int& nv) {
+    const int span = static_cast<int>((next - off) / kHkv);
+    const int64_t rel = x - off;
+    int k = 0;
+#pragma unroll
+    for (int i = 1; i < kHkv; ++i) k += rel >= static_cast<int64_t>(i) * span;
+    const int u = static_cast<int>(rel - static_cast<int64_t>(k) * span);
+    kvh = k;
+    nv = span - lead;
+    key = max(u - lead, 0);
+    x = off + static_cast<int64_t>(k) * span + lead + key;
+}
+
+// Range size for `total` stream positions over n_wgs workgroups.
+__device__ __forceinline__ int64_t range_size(int64_t total, int n_wgs) {
+    int64_t per = (total + n_wgs - 1) / n_wgs;
+    per = per < kMinRangeKeys ? kMinRangeKeys : per;
+    return (per + kChunk - 1) / kChunk * kChunk;
+}
+
+// The lead and the stream totals from the batch's plan_keys: their sum, maximum and the
+// number of sequences with keys.
+__device__ __forceinline__ void plan_lead_totals(int64_t sum, int max_keys, int n_seq, int n_wgs, int& lead,
+                                                 int64_t& total, int64_t& per_wg) {
+    const int64_t per0 = range_size(sum * kHkv, n_wgs);
+    lead = static_cast<int64_t>(max_keys) < kLeadRanges * per0 ? kSegLead : 0;
+    total = (sum + static_cast<int64_t>(n_seq) * lead) * kHkv;
+    per_wg = range_size(total, n_wgs);
+}
+
+// Stream positions over all segments (8 per sequence), the per-workgroup range size and
+// the segment lead.
+__device__ __forceinline__ void stream_totals(const DecodeArgs& a, int lane, int64_t& total, int64_t& per_wg,
+                                              int& lead) {
+    int64_t sum = 0;
+    int max_keys = 0, n_seq = 0;
     for (int base = 0; base < a.batch; base += kWave) {
         const int b = base + lane;
-        t += wave_sum_i64(b < a.batch ? plan_keys(a, b) : 0);
+        const int k = b < a.batch ? plan_keys(a, b) : 0;
+        sum += wave_sum_i64(k);
+        max_keys = max(max_keys, static_cast<int>(wave_max_i64(k)));
+        n_seq += static_cast<int>(wave_sum_i64(k > 0 ? 1 : 0));
     }
-    total = t * kHkv;
-    int64_t per = (total + a.n_wgs - 1) / a.n_wgs;
-    per = per < kMinRangeKeys ? kMinRangeKeys : per;
-    per_wg = (per + kChunk - 1) / kChunk * kChunk;
+    plan_lead_totals(sum, max_keys, n_seq, a.n_wgs, lead, total, per_wg);
 }
 
 // K and V rows of one 16-key chunk, in the MFMA (K) and PV (V) lane layouts.
@@ -277,24 +337,17 @@ __device__ __forceinline__ void merge_rows(PieceState& st, float (&m_tot)[kGroup
     lh[1] = dpp_f<0x55>(st.l_run);
     lh[2] = dpp_f<0xAA>(st.l_run);
     lh[3] = dpp_f<0xFF>(st.l_run);
+    // Rows 16 lanes apart combine through lane swaps (no LDS round trips).
 #pragma unroll
     for (int h = 0; h < kGroup; ++h) {
-        float mx = fmaxf(mh[h], __shfl_xor(mh[h], 16));
-        mx = fmaxf(mx, __shfl_xor(mx, 32));
+        const float mx = swap32_max(swap16_max(mh[h]));
         m_tot[h] = mx;
         // a row that saw no key of this piece has m = -inf and contributes nothing
         const int e = (mh[h] == -INFINITY) ? -1100 : static_cast<int>(mh[h] - mx);
-        double lr = ldexp(static_cast<double>(lh[h]), e);
-        lr += __shfl_xor(lr, 16);
-        lr += __shfl_xor(lr, 32);
-        l_tot[h] = lr;
+        l_tot[h] = swap_add_f64<true>(swap_add_f64<false>(ldexp(static_cast<double>(lh[h]), e)));
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            double v = ldexp(st.acc[h][j], e);
-            v += __shfl_xor(v, 16);
-            v += __shfl_xor(v, 32);
-            st.acc[h][j] = v;
-        }
+        for (int j = 0; j < 8; ++j)
+            st.acc[h][j] = swap_add_f64<true>(swap_add_f64<false>(ldexp(st.acc[h][j], e)));
     }
 }
 
@@ -519,22 +572,24 @@ __device__ __forceinline__ void build_q_operands(const DecodeArgs& a, const QRaw
 // writes the NaN rows of sequences whose lengths break the rules, and (an extra row of
 // the grid) the stream-K plan.
 //
-// The stream-K plan (row B of the prepare grid, one wave): seq_off[b] = global key
-// offset of sequence b's first segment (an exclusive scan of 8 * n_valid), seq_off[B]
-// = total keys, and the header {total, keys per stream workgroup}.  Every stream
-// workgroup finds where its range starts from these with one ballot.
+// The stream-K plan (row B of the prepare grid, one wave): seq_off[b] = stream position
+// of sequence b's first segment (an exclusive scan of 8 * plan_span), seq_off[B] = total
+// positions, and the header {total, positions per stream workgroup, segment lead}.  Every
+// stream workgroup finds where its range starts from these with one ballot.
 __device__ __forceinline__ void build_plan(const DecodeArgs& a, int lane) {
     int64_t total, per_wg;
-    stream_totals(a, lane, total, per_wg);
+    int lead;
+    stream_totals(a, lane, total, per_wg, lead);
     if (lane == 0) {
         a.plan_hdr[0] = total;
         a.plan_hdr[1] = per_wg;
+        a.plan_hdr[2] = lead;
         a.seq_off[a.batch] = total;
     }
     int64_t carry = 0;
     for (int base = 0; base < a.batch; base += kWave) {
         const int b = base + lane;
-        const int nv = b < a.batch ? plan_keys(a, b) : 0;
+        const int nv = b < a.batch ? plan_span(a, b, lead) : 0;
         const int64_t incl = wave_incl_scan_i64(nv, lane) + carry;
         if (b < a.batch) {
             a.seq_off[b] = (incl - nv) * kHkv;
@@ -637,7 +692,8 @@ __device__ __forceinline__ void load_q_operands(const DecodeArgs& a, int b, int 
 // and whose Q operands are in bq.  While the piece's last chunk is computed, the first
 // chunk of the next piece (rows `nxt`) is requested into c0, so the wave never waits
 // at a piece boundary.  Writes the output rows itself when the piece is the whole
-// segment; otherwise leaves a partial for the merge kernel.
+// segment; otherwise leaves a partial for the merge kernel.  (Requesting the next piece's
+// second chunk too, before this piece's end work, measured 1 % slower on long segments.)
 template <bool kRopeK, bool kFused = false>
 __device__ __forceinline__ bool process_piece(const DecodeArgs& a, int b, int kvh, int nv, int k_a,
                                               int k_b, int64_t wg, PieceRows& cur,
@@ -699,6 +755,7 @@ struct SeqWindow {
     int64_t o1;
     int64_t carry;    // scanned windows: keys (per segment) of the sequences before base + 64
     int nreal;        // planned windows: keys that count (less than o1 - o for a paged cache)
+    int lead;         // stream positions before each segment's first key (uniform)
 };
 
 __device__ __forceinline__ void load_seq_window(const DecodeArgs& a, int base, SeqWindow& sw) {
@@ -710,18 +767,18 @@ __device__ __forceinline__ void load_seq_window(const DecodeArgs& a, int base, S
 }
 
 // The same window computed from the lengths (the fused kernel has no plan in memory):
-// an inclusive scan of the window's per-segment keys on top of `carry`, the keys of the
+// an inclusive scan of the window's segment spans on top of `carry`, the span of the
 // sequences before `base`.
 __device__ __forceinline__ void scan_seq_window(const DecodeArgs& a, int base, int64_t carry, SeqWindow& sw) {
     const int lane = static_cast<int>(threadIdx.x & (kWave - 1));
     const int bb = base + lane;
-    const int nv = bb < a.batch ? plan_keys(a, bb) : 0;
-    const int64_t incl = wave_incl_scan_i64(nv, lane) + carry;
+    const int span = bb < a.batch ? plan_span(a, bb, sw.lead) : 0;
+    const int64_t incl = wave_incl_scan_i64(span, lane) + carry;
     sw.base = base;
-    sw.o = bb < a.batch ? (incl - nv) * kHkv : INT64_MAX;
+    sw.o = bb < a.batch ? (incl - span) * kHkv : INT64_MAX;
     sw.o1 = bb < a.batch ? incl * kHkv : INT64_MAX;
     sw.carry = __shfl(incl, kWave - 1);
-    sw.nreal = nv;
+    sw.nreal = bb < a.batch ? plan_keys(a, bb) : 0;
 }
 
 template <bool kScan>
@@ -749,7 +806,7 @@ __device__ __forceinline__ bool next_segment(const DecodeArgs& a, SeqWindow& sw,
         if (m) {
             const int j = __ffsll(static_cast<unsigned long long>(m)) - 1;
             b = sw.base + j;
-            nv = static_cast<int>((__shfl(sw.o1, j) - __shfl(sw.o, j)) / kHkv);
+            nv = static_cast<int>((__shfl(sw.o1, j) - __shfl(sw.o, j)) / kHkv) - sw.lead;
             return true;
         }
         if (sw.base + kWave >= a.batch) return false;
@@ -759,9 +816,14 @@ __device__ __forceinline__ bool next_segment(const DecodeArgs& a, SeqWindow& sw,
 
 template <bool kRopeK>
 __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(1))) void decode_stream_kernel(DecodeArgs a) {
+    // The first window of sequence offsets does not depend on the plan header: both are
+    // requested at once.
+    SeqWindow w0;
+    load_seq_window(a, 0, w0);
     const int64_t w = blockIdx.x;
     const int64_t total = a.plan_hdr[0];
     const int64_t per_wg = a.plan_hdr[1];
+    const int lead = static_cast<int>(a.plan_hdr[2]);
     int64_t x = w * per_wg;
     if (x >= total) return;
     const int64_t x_end = min(x + per_wg, total);
@@ -771,8 +833,8 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(1))) void
     int b = 0;
     int64_t off = 0, next = 0;
     for (int base = 0; base < a.batch; base += kWave) {
-        SeqWindow t;
-        load_seq_window(a, base, t);
+        SeqWindow t = w0;
+        if (base > 0) load_seq_window(a, base, t);
         const uint64_t le = __ballot(t.o <= x);
         if (le) {
             const int j = 63 - __clzll(static_cast<long long>(le));
@@ -782,12 +844,10 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(1))) void
             sw = t;
         }
     }
-    int nvb = static_cast<int>((next - off) / kHkv);
-    const int64_t rel = x - off;                  // in [0, 8 * nvb)
-    int kvh = 0;
-#pragma unroll
-    for (int k = 1; k < kHkv; ++k) kvh += rel >= static_cast<int64_t>(k) * nvb;
-    int key = static_cast<int>(rel - static_cast<int64_t>(kvh) * nvb);
+    sw.lead = lead;
+    int kvh, key, nvb;
+    locate_first_piece(off, next, lead, x, kvh, key, nvb);
+    x = uniform_i64(x);
     b = __builtin_amdgcn_readfirstlane(b);
     kvh = __builtin_amdgcn_readfirstlane(kvh);
     key = __builtin_amdgcn_readfirstlane(key);
@@ -806,9 +866,11 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(1))) void
     while (true) {
         // The next piece of this range (or, after the last one, a re-read of this piece's
         // last row), whose first chunk and Q operands are requested during this piece.
+        // x_next is the end of this segment's span when the piece reaches it; the range has
+        // a piece of the next segment if it reaches that segment's first key.
         const int64_t x_next = x + (k_b - key);
         int b2 = b, kvh2 = kvh, nv2 = nvb, key2 = k_b - 1, k_b2 = k_b;
-        bool more = x_next < x_end;
+        bool more = x_next + lead < x_end;
         if (more) {
             more = next_segment(a, sw, b2, kvh2, nv2);
             b2 = __builtin_amdgcn_readfirstlane(b2);
@@ -816,7 +878,7 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(1))) void
             nv2 = __builtin_amdgcn_readfirstlane(nv2);
             key2 = 0;
             k_b2 = __builtin_amdgcn_readfirstlane(
-                static_cast<int>(min(static_cast<int64_t>(nv2), x_end - x_next)));
+                static_cast<int>(min(static_cast<int64_t>(nv2), x_end - x_next - lead)));
         }
         if (!more) {
             b2 = b;
@@ -833,7 +895,7 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(1))) void
         process_piece<kRopeK>(a, b, kvh, nvb, key, k_b, w, cur, nxt, c0, c1, bq);
         if (!more) break;
 
-        x = x_next;
+        x = x_next + lead;
         b = b2;
         kvh = kvh2;
         nvb = nv2;
@@ -1043,13 +1105,20 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(1))) void
         const int bb = kWave * k + lane;
         nvw[k] = bb < a.batch ? plan_keys(a, bb) : 0;
     }
-    int64_t total = 0;
+    int64_t sum = 0;
+    int max_keys = 0, n_seq = 0;
 #pragma unroll
-    for (int k = 0; k < kFusedWindows; ++k) total += wave_sum_i64(nvw[k]);
-    total = uniform_i64(total * kHkv);
-    int64_t per_wg = (total + a.n_wgs - 1) / a.n_wgs;
-    per_wg = per_wg < kMinRangeKeys ? kMinRangeKeys : per_wg;
-    per_wg = (per_wg + kChunk - 1) / kChunk * kChunk;
+    for (int k = 0; k < kFusedWindows; ++k) {
+        sum += wave_sum_i64(nvw[k]);
+        max_keys = max(max_keys, static_cast<int>(wave_max_i64(nvw[k])));
+        n_seq += static_cast<int>(wave_sum_i64(nvw[k] > 0 ? 1 : 0));
+    }
+    int lead;
+    int64_t total, per_wg;
+    plan_lead_totals(uniform_i64(sum), __builtin_amdgcn_readfirstlane(max_keys),
+                     __builtin_amdgcn_readfirstlane(n_seq), a.n_wgs, lead, total, per_wg);
+#pragma unroll
+    for (int k = 0; k < kFusedWindows; ++k) nvw[k] = nvw[k] > 0 ? nvw[k] + lead : 0;   // spans
     int64_t x = w * per_wg;
     if (x >= total) {
         write_nan_rows_of(a, nvw, w);
@@ -1080,12 +1149,10 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(1))) void
             sw = t;
         }
     }
-    int nvb = static_cast<int>((next - off) / kHkv);
-    const int64_t rel = x - off;
-    int kvh = 0;
-#pragma unroll
-    for (int kk = 1; kk < kHkv; ++kk) kvh += rel >= static_cast<int64_t>(kk) * nvb;
-    int key = static_cast<int>(rel - static_cast<int64_t>(kvh) * nvb);
+    sw.lead = lead;
+    int kvh, key, nvb;
+    locate_first_piece(off, next, lead, x, kvh, key, nvb);
+    x = uniform_i64(x);
     b = __builtin_amdgcn_readfirstlane(b);
     kvh = __builtin_amdgcn_readfirstlane(kvh);
     key = __builtin_amdgcn_readfirstlane(key);
@@ -1111,9 +1178,9 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(1))) void
     SplitPiece first = {0, 0, 0, -1};
     SplitPiece last = {0, 0, 0, -1};
     while (true) {
-        const int64_t x_next = x + (k_b - key);
+        const int64_t x_next = x + (k_b - key);      // as in decode_stream_kernel
         int b2 = b, kvh2 = kvh, nv2 = nvb, key2 = k_b - 1, k_b2 = k_b;
-        bool more = x_next < x_end;
+        bool more = x_next + lead < x_end;
         if (more) {
             more = next_segment<true>(a, sw, b2, kvh2, nv2);
             b2 = __builtin_amdgcn_readfirstlane(b2);
@@ -1121,7 +1188,7 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(1))) void
             nv2 = __builtin_amdgcn_readfirstlane(nv2);
             key2 = 0;
             k_b2 = __builtin_amdgcn_readfirstlane(
-                static_cast<int>(min(static_cast<int64_t>(nv2), x_end - x_next)));
+                static_cast<int>(min(static_cast<int64_t>(nv2), x_end - x_next - lead)));
         }
         if (!more) {
             b2 = b;
@@ -1146,7 +1213,7 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(1))) void
         if (!more) break;
         build_q_operands<kRopeQ>(a, raw, rope, qs, bq);   // while the next piece's first chunk is in flight
 
-        x = x_next;
+        x = x_next + lead;
         b = b2;
         kvh = kvh2;
         nvb = nv2;
@@ -1306,6 +1373,7 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(1))) void
     const int64_t w = blockIdx.x;
     const int64_t total = a.plan_hdr[0];
     const int64_t per_wg = a.plan_hdr[1];
+    const int lead = static_cast<int>(a.plan_hdr[2]);
     int64_t x = w * per_wg;
     if (x >= total) return;
     const int64_t x_end = min(x + per_wg, total);
@@ -1327,14 +1395,16 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(1))) void
         }
     }
     PagePiece cur;
-    cur.b = __builtin_amdgcn_readfirstlane(b);
-    cur.nvp = __builtin_amdgcn_readfirstlane(static_cast<int>((next - off) / kHkv));
-    const int64_t rel = x - off;
-    int kvh = 0;
-#pragma unroll
-    for (int k = 1; k < kHkv; ++k) kvh += rel >= static_cast<int64_t>(k) * cur.nvp;
-    cur.kvh = __builtin_amdgcn_readfirstlane(kvh);
-    cur.k_a = __builtin_amdgcn_readfirstlane(static_cast<int>(rel - static_cast<int64_t>(cur.kvh) * cur.nvp));
+    {
+        sw.lead = lead;
+        int kvh, key, nvp;
+        locate_first_piece(off, next, lead, x, kvh, key, nvp);
+        x = uniform_i64(x);
+        cur.b = __builtin_amdgcn_readfirstlane(b);
+        cur.nvp = __builtin_amdgcn_readfirstlane(nvp);
+        cur.kvh = __builtin_amdgcn_readfirstlane(kvh);
+        cur.k_a = __builtin_amdgcn_readfirstlane(key);
+    }
     cur.k_b = __builtin_amdgcn_readfirstlane(
         static_cast<int>(min(static_cast<int64_t>(cur.nvp), cur.k_a + (x_end - x))));
     cur.kend = min(cur.k_b, __builtin_amdgcn_readfirstlane(__shfl(sw.nreal, cur.b - sw.base)));
@@ -1352,10 +1422,10 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(1))) void
     while (true) {
         // The next piece of this range, and everything it needs before its first chunk
         // (its length, first two block ids, Q operands), requested during this piece.
-        const int64_t x_next = x + (cur.k_b - cur.k_a);
+        const int64_t x_next = x + (cur.k_b - cur.k_a);   // as in decode_stream_kernel
         PagePiece nx = cur;
         int b2 = cur.b, kvh2 = cur.kvh, nv2 = cur.nvp;
-        bool more = x_next < x_end;
+        bool more = x_next + lead < x_end;
         if (more) more = next_segment(a, sw, b2, kvh2, nv2);
         int nx_id0 = cur.id1;
         bf16x8_t bq2[4];
@@ -1364,7 +1434,8 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(1))) void
             nx.kvh = __builtin_amdgcn_readfirstlane(kvh2);
             nx.nvp = __builtin_amdgcn_readfirstlane(nv2);
             nx.k_a = 0;
-            nx.k_b = __builtin_amdgcn_readfirstlane(static_cast<int>(min(static_cast<int64_t>(nx.nvp), x_end - x_next)));
+            nx.k_b = __builtin_amdgcn_readfirstlane(
+                static_cast<int>(min(static_cast<int64_t>(nx.nvp), x_end - x_next - lead)));
             nx.kend = min(nx.k_b, __builtin_amdgcn_readfirstlane(__shfl(sw.nreal, nx.b - sw.base)));
             const int jn2 = max(0, (nx.kend - 1) / kChunk);
             nx_id0 = load_block_id(a, nx.b, 0);
@@ -1374,7 +1445,7 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(1))) void
         }
         process_page_piece<kRopeK>(a, cur, w, c0, c1, bq, more, nx, nx_id0);
         if (!more) break;
-        x = x_next;
+        x = x_next + lead;
         cur = nx;
 #pragma unroll
         for (int kb = 0; kb < 4; ++kb) bq[kb] = bq2[kb];
@@ -1394,9 +1465,11 @@ __global__ __launch_bounds__(kGroup * kWave) void decode_merge_kernel(DecodeArgs
     const int h = threadIdx.x / kWave;
     const int64_t per_wg = a.plan_hdr[1];
     const int64_t off = a.seq_off[b];
-    const int nv = static_cast<int>((a.seq_off[b + 1] - off) / kHkv);
-    if (nv == 0) return;
-    const int64_t seg_off = off + static_cast<int64_t>(kvh) * nv;
+    const int span = static_cast<int>((a.seq_off[b + 1] - off) / kHkv);
+    if (span == 0) return;
+    const int lead = static_cast<int>(a.plan_hdr[2]);
+    const int nv = span - lead;
+    const int64_t seg_off = off + static_cast<int64_t>(kvh) * span + lead;   // stream position of key 0
     const int64_t w_first = seg_off / per_wg;
     const int n_pieces = static_cast<int>((seg_off + nv - 1) / per_wg - w_first) + 1;
     if (n_pieces == 1) return;

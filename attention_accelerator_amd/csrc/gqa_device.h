@@ -92,6 +92,34 @@ __device__ __forceinline__ float cross_row_max(float x) {
     return x;
 }
 
+// x of lane l combined with x of lane l ^ 16 (row pairs 0-1, 2-3) or l ^ 32 (halves) through
+// gfx950's lane swaps v_permlane16_swap_b32 / v_permlane32_swap_b32 (VALU, no LDS round
+// trip).  A swap returns {own, partner} in an order fixed by the lane, and the two are
+// combined commutatively, so both lanes of a pair get the same value, bit for bit the value
+// that x + __shfl_xor(x, 16) (or 32) gives.  All 64 lanes must be active.
+__device__ __forceinline__ float swap16_max(float x) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+
+__device__ __forceinline__ float swap32_max(float x) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+
+template <bool k32>
+__device__ __forceinline__ double swap_add_f64(double x) {
+    const unsigned long long u = static_cast<unsigned long long>(__double_as_longlong(x));
+    const unsigned lo = static_cast<unsigned>(u), hi = static_cast<unsigned>(u >> 32);
+    const auto rl = k32 ? __builtin_amdgcn_permlane32_swap(lo, lo, false, false)
+                        : __builtin_amdgcn_permlane16_swap(lo, lo, false, false);
+    const auto rh = k32 ? __builtin_amdgcn_permlane32_swap(hi, hi, false, false)
+                        : __builtin_amdgcn_permlane16_swap(hi, hi, false, false);
+    const double a = __longlong_as_double(static_cast<long long>((static_cast<unsigned long long>(rh[0]) << 32) | rl[0]));
+    const double b = __longlong_as_double(static_cast<long long>((static_cast<unsigned long long>(rh[1]) << 32) | rl[1]));
+    return a + b;
+}
+
 __device__ __forceinline__ float wave_sum(float x) { return cross_row_sum(row16_sum(x)); }
 __device__ __forceinline__ float wave_max(float x) { return cross_row_max(row16_max(x)); }
 
