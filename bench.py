@@ -18,6 +18,12 @@ tokens per sequence after an 8192-token post-RoPE cache, RoPE on Q and the new K
 (one step = one gqa_prefill_bf16 call: KV append + attention), with a 512 MiB write
 between steps so that no step finds the 142 MB of K/V in the Infinity Cache.  value =
 algorithmic flops / time per step (TFLOP/s) and the roofline is MFMA (BF16 dense peak).
+
+--workload multitoken_b64_ragged_512_8192_t4 times multi-token decode (e.g. verifying 4
+drafted tokens): the default batch's lengths, the last 4 positions of each sequence being
+new tokens that one gqa_prefill_bf16 call appends (K rotated) and attends causally.  value =
+the attention's algorithmic HBM bytes (every K/V row the last token sees, Q in, O out) /
+time per step (GB/s); the roofline is HBM.
 """
 from __future__ import annotations
 
@@ -44,6 +50,11 @@ WORKLOADS = {
 PREFILL_WORKLOADS = {
     # name: (batch, new tokens, cached positions)
     "prefill_b4_512_over_8192": (4, 512, 8192),
+}
+MULTI_WORKLOADS = {
+    # name: (batch, capacity, min_len, max_len, new tokens): the decode batch's lengths, whose
+    # last `new` positions are the new tokens (appended with RoPE, then attended causally)
+    "multitoken_b64_ragged_512_8192_t4": (64, 8192, 512, 8192, 4),
 }
 MFMA_BF16_PEAK_TFLOPS = 2500.0
 TRAFFIC_FILE = ROOT / "profiles" / "decode_stream_b64_ragged_traffic.txt"
@@ -218,6 +229,109 @@ def bench_prefill(args, torch, gqa, dev) -> int:
     return 0
 
 
+def multitoken_bytes(lengths, n_new: int) -> int:
+    """HBM bytes of the attention: every K and V row each sequence's last token sees, once,
+    the Q rows in and the output rows out (the append's own traffic is not counted)."""
+    kv = sum(2 * 8 * 128 * 2 * int(x) for x in lengths)
+    return kv + 2 * len(lengths) * n_new * 32 * 128 * 2
+
+
+def multitoken_cpu_baseline(q, kn, vn, k, v, starts, n_new: int, budget_s: float = 12.0):
+    """The compiled oracle (double, 1 thread) on whole sequences (all new tokens) from 0 on."""
+    import numpy as np
+
+    from oracle import oracle as orc
+
+    def codes(t):
+        return t.contiguous().view(__import__("torch").int16).cpu().numpy().view(np.uint16)
+
+    done, t_total, byts = 0, 0.0, 0
+    while t_total < budget_s and done < q.shape[0]:
+        b, s0 = done, int(starts[done])
+        qc, knc, vnc = codes(q[b:b + 1]), codes(kn[b:b + 1]), codes(vn[b:b + 1])
+        kc, vc = codes(k[b:b + 1, :, :s0]), codes(v[b:b + 1, :, :s0])
+        t0 = time.perf_counter()
+        orc.prefill(qc, kc, vc, knc, vnc, np.asarray([s0]), rows=list(range(n_new)))
+        t_total += time.perf_counter() - t0
+        byts += multitoken_bytes([s0 + n_new], n_new)
+        done += 1
+    return {"value": round(byts / t_total / 1e9, 4), "unit": "GB/s", "cores": 1, "kind": "port",
+            "sample": (f"sequences 0..{done - 1} ({done} of {q.shape[0]}, all {n_new} new tokens, all 32 "
+                       f"heads), compiled oracle in double, {t_total:.2f} s; "
+                       f"os.cpu_count()={os.cpu_count()}, affinity={len(os.sched_getaffinity(0))}")}
+
+
+def bench_multitoken(args, torch, gqa, dev, stimulus) -> int:
+    bsz, cap, lo, hi, n_new = MULTI_WORKLOADS[args.workload]
+    batch = stimulus.decode_batch(bsz, cap, min_len=lo, max_len=hi, seed=args.seed, device=dev,
+                                  gen_device="cuda")
+    lens = [int(x) for x in batch.seq_len]
+    g = torch.Generator("cuda").manual_seed(args.seed + 1)
+    q = torch.randn((bsz, n_new, 32, 128), generator=g, device=dev).to(torch.bfloat16)
+    kn = torch.randn((bsz, n_new, 8, 128), generator=g, device=dev).to(torch.bfloat16)
+    vn = torch.randn((bsz, n_new, 8, 128), generator=g, device=dev).to(torch.bfloat16)
+    starts_l = [x - n_new for x in lens]
+    starts = torch.tensor(starts_l, dtype=torch.int32, device=dev)
+    k_host, v_host = (batch.k.cpu(), batch.v.cpu()) if not args.no_cpu_baseline else (None, None)
+    out = torch.empty_like(q)
+    step_bytes = multitoken_bytes(lens, n_new)
+    print(f"[bench] {args.workload}: B={bsz} new={n_new} keys={sum(lens)} bytes/step={step_bytes}",
+          file=sys.stderr, flush=True)
+    call = gqa.PreparedPrefill(q, kn, vn, batch.k, batch.v, starts, out=out)
+
+    spin_up(call, torch, args.spinup_s)
+    for _ in range(args.warmup):
+        call()
+    torch.cuda.synchronize()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        call()
+    torch.cuda.synchronize()
+    ms_per_step = (time.perf_counter() - t0) * 1e3 / args.steps
+
+    attn_ms = append_ms = None
+    if not args.no_profile:
+        gqa.profile_enable(args.steps)
+        for _ in range(args.steps):
+            call()
+        torch.cuda.synchronize()
+        ap_ms, at_ms, n = gqa.profile_read()
+        gqa.profile_enable(0)
+        append_ms, attn_ms = ap_ms / n, at_ms / n
+    print(f"[bench] {args.steps} steps: {ms_per_step * 1e3:.2f} us/step", file=sys.stderr, flush=True)
+    roofline = None
+    if attn_ms:
+        achieved = step_bytes / (attn_ms * 1e-3) / 1e9
+        roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                    "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                    "kernel": "prefill_attn_kernel", "kernel_us": round(attn_ms * 1e3, 2),
+                    "append_us": round(append_ms * 1e3, 2), "bytes_per_launch": step_bytes}
+    result = {
+        "metric": "GQA multi-token decode µs/step + achieved HBM GB/s, B=64 ragged ctx 512–8192, 4 new tokens",
+        "value": round(step_bytes / (ms_per_step * 1e-3) / 1e9, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 5),
+        "us_per_step": round(ms_per_step * 1e3, 2),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": f"synthetic N(0,1) BF16, seed {args.seed}",
+        "config": {"workload": args.workload, "batch": bsz, "new_tokens": n_new, "keys": sum(lens),
+                   "q_heads": 32, "kv_heads": 8, "head_dim": 128, "rope": "q and new k",
+                   "bytes_per_step": step_bytes, "spinup_s": args.spinup_s},
+        "roofline": roofline,
+        "cpu_baseline": None if args.no_cpu_baseline else multitoken_cpu_baseline(
+            q, kn, vn, k_host, v_host, starts_l, n_new),
+    }
+    print(json.dumps(result), flush=True)
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -225,7 +339,7 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--spinup-s", type=float, default=0.3,
                     help="seconds of untimed steps before the warm-up (engine clock ramp)")
-    ap.add_argument("--workload", choices=sorted(WORKLOADS) + sorted(PREFILL_WORKLOADS),
+    ap.add_argument("--workload", choices=sorted(WORKLOADS) + sorted(PREFILL_WORKLOADS) + sorted(MULTI_WORKLOADS),
                     default="decode_b64_ragged_512_8192")
     ap.add_argument("--seed", type=int, default=20260805)
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -249,6 +363,8 @@ def main() -> int:
     dev = torch.device("cuda", 0)
     if args.workload in PREFILL_WORKLOADS:
         return bench_prefill(args, torch, gqa, dev)
+    if args.workload in MULTI_WORKLOADS:
+        return bench_multitoken(args, torch, gqa, dev, stimulus)
     bsz, cap, lo, hi = WORKLOADS[args.workload]
     batch = stimulus.decode_batch(bsz, cap, min_len=lo, max_len=hi, seed=args.seed,
                                   device=dev, gen_device="cuda")
