@@ -65,13 +65,22 @@ int32_t stream_wgs() {
 
 // Fused stream launch (contiguous cache, past the single-launch size, at most
 // kFusedMaxBatch sequences), chosen with GQA_DECODE_FUSED=1: one launch per call instead
-// of three.  It is not the default: on B=64 ragged 512..8192 its call takes about 3 %
+// of three.  It is not the default: on B=64 ragged 512..8192 its call takes about 6 %
 // longer than the three launches (the in-kernel plan, Q operands and end-of-range merge
 // cost more than the two launches they remove).
 bool use_fused(int32_t batch) {
     if (batch > kFusedMaxBatch) return false;
     const char* s = std::getenv("GQA_DECODE_FUSED");
     return s && s[0] == '1';
+}
+
+// Chunks of at most kMultiMaxNew new tokens take the multi-token path (stream-K over the
+// keys, prefill arithmetic); GQA_PREFILL_MULTI=0 in the environment sends them through the
+// prefill attention kernel instead.
+bool use_multi(int32_t n_new) {
+    if (n_new > kMultiMaxNew) return false;
+    const char* s = std::getenv("GQA_PREFILL_MULTI");
+    return !(s && s[0] == '0');
 }
 
 bool geometry_ok(const gqa_params_t* p) {
@@ -412,7 +421,9 @@ extern "C" {
 
 size_t gqa_prefill_workspace_bytes(const gqa_params_t* params, int32_t batch, int32_t n_new) {
     if (!params || !geometry_ok(params) || batch <= 0 || n_new <= 0) return 0;
-    return align_up(prefill_split_bytes(batch, n_new), 256);
+    size_t bytes = align_up(prefill_split_bytes(batch, n_new), 256);
+    if (use_multi(n_new)) bytes += prefill_multi_bytes(batch, stream_wgs());
+    return bytes;
 }
 
 int gqa_kv_append_bf16(const gqa_params_t* params, const uint16_t* k_new, const uint16_t* v_new,
@@ -460,10 +471,18 @@ int gqa_prefill_bf16(const gqa_params_t* params, const uint16_t* q, const uint16
     a.q = q;
     a.out = out;
     a.k_split = static_cast<uint16_t*>(workspace);
+    const bool multi = use_multi(n_new);
+    if (multi)
+        prefill_multi_layout(a, static_cast<char*>(workspace) + align_up(prefill_split_bytes(batch, n_new), 256),
+                             stream_wgs());
     hipStream_t s = static_cast<hipStream_t>(stream);
     hipEvent_t* ev = profile_slot();
     if (ev) (void)hipEventRecord(ev[0], s);
     hipError_t e = launch_kv_append(a, s);
+    if (multi) {
+        if (e == hipSuccess) e = launch_prefill_multi(a, s, ev);
+        return e == hipSuccess ? GQA_OK : GQA_ERR_HIP;
+    }
     if (ev) (void)hipEventRecord(ev[1], s);
     if (e == hipSuccess) e = launch_prefill_attention(a, s);
     if (ev) (void)hipEventRecord(ev[2], s);

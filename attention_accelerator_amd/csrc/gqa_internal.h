@@ -106,11 +106,27 @@ struct PrefillArgs {
     double qk_scale_log2;     // scale * log2(e), folded into Q
     uint32_t flags;           // bit0 RoPE on Q, bit1 RoPE on the new K rows
     RopeTable rope;
+    // Multi-token path (n_new <= kMultiMaxNew): the stream-K split of the decode path.
+    uint4* q_op;              // [B][8][3][4][64] Q operands (3 BF16 parts, MFMA B layout)
+    int64_t* plan_hdr;        // {total stream positions, positions per workgroup, segment lead}
+    int64_t* seq_off;         // [B+1] stream position of sequence b's first segment
+    double* part_o;           // [n_slots][16][128] unnormalised partial outputs (column 4t + h)
+    float2* part_ml;          // [n_slots][16] (integer-valued running max in log2 units, sum)
+    int32_t n_wgs;            // persistent workgroups of the multi-token stream kernel
 };
 
+// Chunks of at most this many new tokens per sequence take the multi-token path.
+constexpr int32_t kMultiMaxNew = 4;
+
 size_t prefill_split_bytes(int32_t batch, int32_t n_new);
+// Workspace of the multi-token path after the split planes: Q operands, plan, partials.
+size_t prefill_multi_bytes(int32_t batch, int32_t n_wgs);
+void prefill_multi_layout(PrefillArgs& a, void* base, int32_t n_wgs);
 hipError_t launch_kv_append(const PrefillArgs& a, hipStream_t stream);
 hipError_t launch_prefill_attention(const PrefillArgs& a, hipStream_t stream);
+// The multi-token path's three kernels; ev (optional): events recorded before its stream
+// kernel and after it (the merge follows).
+hipError_t launch_prefill_multi(const PrefillArgs& a, hipStream_t stream, hipEvent_t* ev = nullptr);
 
 
 }  // namespace gqa

@@ -38,6 +38,7 @@
 //  * O / l, rounded double -> f32 -> BF16, written in Q-head order.
 #include "gqa_device.h"
 #include "gqa_internal.h"
+#include "gqa_streamk.h"
 
 namespace gqa {
 
@@ -649,6 +650,569 @@ hipError_t launch_prefill_attention(const PrefillArgs& a, hipStream_t stream) {
     const int64_t n_wg = static_cast<int64_t>(a.batch) * kHkv * a.n_qblk;
     if (n_wg == 0) return hipSuccess;
     hipLaunchKernelGGL(prefill_attn_kernel, dim3(static_cast<unsigned>(n_wg)), dim3(kPfThreads), 0, stream, a);
+    return hipGetLastError();
+}
+
+
+// ---------------------------------------------------------------------------------
+// Multi-token decode: chunks of at most kMultiMaxNew (4) new tokens per sequence -- drafted
+// tokens being verified, or decode steps that append their own K/V.  The attention kernel
+// above gives each (sequence, KV head, 32 positions) one workgroup over all of that
+// sequence's keys, which for a short chunk leaves most of its MFMA columns empty and a
+// ragged batch waiting for its longest sequence.  Here the 16 query rows of a KV head's
+// group -- 4 heads x up to 4 tokens, column n = 4t + h -- form one MFMA B operand, and the
+// keys are split stream-K over n_wgs one-wave workgroups as in the decode path: every
+// segment (sequence, KV head) holds start + T keys, a range's part of a segment is a
+// piece, a split segment's pieces leave partials that mt_merge_kernel combines.  The
+// arithmetic is the attention kernel's: three BF16 parts of Q, the chunk's own keys
+// carried to ~24 bits, P in three parts, fp64 accumulation, integer-valued running max.
+//
+// Per 32-key window a wave copies the window's K and V rows into its own LDS (double-
+// buffered, the next window's copies in flight while the current one is computed; no
+// barrier, the workgroup is one wave), forms the scores of both 16-key tiles, and adds
+// V^T P^T with the transposed V reads of the attention kernel.
+
+constexpr int kMtWin = 32;                    // keys per window
+constexpr int kMtPlaneB = kMtWin * kRowB;     // 8 KB: 32 rows of 256 B
+constexpr int kMtBufB = 2 * kMtPlaneB;        // K plane, then V plane
+constexpr int kMtLdsB = 2 * kMtBufB;          // two buffers: 32 KB per workgroup
+constexpr int kMtCols = 16;                   // query rows per segment: 4 heads x 4 tokens
+constexpr int kMtCopies = 16;                 // copy instructions per window per lane (8 K + 8 V)
+
+// s_waitcnt immediate for vmcnt(n) alone (gfx9: vmcnt bits 3:0 and 15:14, expcnt and
+// lgkmcnt at their maxima).
+constexpr int vmcnt_imm(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
+static_assert(vmcnt_imm(0) == 0x0F70 && vmcnt_imm(16) == 0x4F70, "vmcnt encoding");
+
+// Keys of sequence b's segments: every key its last new token sees (0 for a start outside
+// [0, capacity - T]).
+__device__ __forceinline__ int mt_keys(const PrefillArgs& a, int b) {
+    const int st = a.start[b];
+    return prefill_start_ok(a, st) ? st + a.n_new : 0;
+}
+
+size_t prefill_multi_bytes(int32_t batch, int32_t n_wgs) {
+    const size_t n_slots = static_cast<size_t>(n_wgs) + static_cast<size_t>(kHkv) * batch;
+    auto al = [](size_t x) { return (x + 255) / 256 * 256; };
+    return al(static_cast<size_t>(batch) * kHkv * 12 * kWave * sizeof(uint4)) + 256 +
+           al((static_cast<size_t>(batch) + 1) * sizeof(int64_t)) + al(n_slots * kMtCols * kD * sizeof(double)) +
+           al(n_slots * kMtCols * sizeof(float2));
+}
+
+void prefill_multi_layout(PrefillArgs& a, void* base, int32_t n_wgs) {
+    const size_t n_slots = static_cast<size_t>(n_wgs) + static_cast<size_t>(kHkv) * a.batch;
+    auto al = [](size_t x) { return (x + 255) / 256 * 256; };
+    char* p = static_cast<char*>(base);
+    a.q_op = reinterpret_cast<uint4*>(p);
+    p += al(static_cast<size_t>(a.batch) * kHkv * 12 * kWave * sizeof(uint4));
+    a.plan_hdr = reinterpret_cast<int64_t*>(p);
+    p += 256;
+    a.seq_off = reinterpret_cast<int64_t*>(p);
+    p += al((static_cast<size_t>(a.batch) + 1) * sizeof(int64_t));
+    a.part_o = reinterpret_cast<double*>(p);
+    p += al(n_slots * kMtCols * kD * sizeof(double));
+    a.part_ml = reinterpret_cast<float2*>(p);
+    a.n_wgs = n_wgs;
+}
+
+// The stream-K plan (one wave): seq_off[b] = stream position of sequence b's first segment,
+// seq_off[B] = total, header {total, positions per workgroup, lead} (gqa_streamk.h).
+__device__ __forceinline__ void mt_build_plan(const PrefillArgs& a, int lane) {
+    int64_t sum = 0;
+    int max_keys = 0, n_seq = 0;
+    for (int base = 0; base < a.batch; base += kWave) {
+        const int b = base + lane;
+        const int k = b < a.batch ? mt_keys(a, b) : 0;
+        sum += wave_sum_i64(k);
+        max_keys = max(max_keys, static_cast<int>(wave_max_i64(k)));
+        n_seq += static_cast<int>(wave_sum_i64(k > 0 ? 1 : 0));
+    }
+    int lead;
+    int64_t total, per_wg;
+    plan_lead_totals(sum, max_keys, n_seq, a.n_wgs, lead, total, per_wg);
+    if (lane == 0) {
+        a.plan_hdr[0] = total;
+        a.plan_hdr[1] = per_wg;
+        a.plan_hdr[2] = lead;
+        a.seq_off[a.batch] = total;
+    }
+    int64_t carry = 0;
+    for (int base = 0; base < a.batch; base += kWave) {
+        const int b = base + lane;
+        const int k = b < a.batch ? mt_keys(a, b) : 0;
+        const int span = k > 0 ? k + lead : 0;
+        const int64_t incl = wave_incl_scan_i64(span, lane) + carry;
+        if (b < a.batch) a.seq_off[b] = (incl - span) * kHkv;
+        carry = __shfl(incl, kWave - 1);
+    }
+}
+
+// Q operands of segment (b, kvh): lane (g, n) holds column n = 4t + h (token t, Q head
+// 4*kvh + h) at dims 32kb + 8g + j, rotated at position start + t and scaled by
+// scale*log2(e) in double, in three BF16 parts; columns of tokens t >= T are zero.  Row B
+// of the grid builds the plan; a sequence whose start is out of range gets NaN rows.
+__global__ __launch_bounds__(kWave) void mt_prepare_kernel(PrefillArgs a) {
+    const int kvh = blockIdx.x;
+    const int b = blockIdx.y;
+    const int lane = threadIdx.x;
+    if (b == a.batch) {
+        if (kvh == 0) mt_build_plan(a, lane);
+        return;
+    }
+    const int T = a.n_new;
+    const int st = a.start[b];
+    if (!prefill_start_ok(a, st)) {
+        for (int i = lane; i < T * kGroup * (kD / 8); i += kWave) {
+            const int t = i / (kGroup * (kD / 8));
+            const int r = i % (kGroup * (kD / 8));
+            uint4* o = reinterpret_cast<uint4*>(a.out + ((static_cast<int64_t>(b) * T + t) * kHq + kvh * kGroup) * kD);
+            o[r] = make_uint4(0x7fc07fc0u, 0x7fc07fc0u, 0x7fc07fc0u, 0x7fc07fc0u);
+        }
+        return;
+    }
+    const int g = lane >> 4;
+    const int n = lane & 15;
+    const int t = n >> 2;
+    const bool col = t < T;
+    const int tc = col ? t : T - 1;
+    const uint16_t* qrow = a.q + ((static_cast<int64_t>(b) * T + tc) * kHq + kvh * kGroup + (n & 3)) * kD;
+    // sin and cos of (start + t) * inv_freq[i], once per token and frequency (lane i).
+    __shared__ double sn_s[kMultiMaxNew][kPairs], cs_s[kMultiMaxNew][kPairs];
+    const bool rope = (a.flags & 1u) != 0;
+    if (rope) {
+        for (int tt = 0; tt < T; ++tt)
+            rope_sincos(static_cast<int64_t>(st) + tt, a.rope.inv_freq[lane], sn_s[tt][lane], cs_s[tt][lane]);
+        __syncthreads();
+    }
+    double qv[4][8];
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const int d = 32 * kb + 8 * g + j;
+            const double x = bf16_to_f32(qrow[d]);
+            const double y = bf16_to_f32(qrow[d + kPairs]);
+            double xr = x, yr = y;
+            if (rope) {
+                const double sn = sn_s[tc][d], cs = cs_s[tc][d];
+                xr = x * cs - y * sn;
+                yr = x * sn + y * cs;
+            }
+            qv[kb][j] = col ? xr * a.qk_scale_log2 : 0.0;
+            qv[kb + 2][j] = col ? yr * a.qk_scale_log2 : 0.0;
+        }
+    uint4* dst = a.q_op + (static_cast<int64_t>(b) * kHkv + kvh) * 12 * kWave + lane;
+#pragma unroll
+    for (int s = 0; s < 3; ++s)
+#pragma unroll
+        for (int kb = 0; kb < 4; ++kb) {
+            uint16_t h8[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) h8[j] = split3(qv[kb][j], s);
+            union {
+                bf16x8_t v;
+                uint4 u;
+            } cv;
+            cv.v = pack8(h8);
+            dst[(s * 4 + kb) * kWave] = cv.u;
+        }
+}
+
+// Copies of the window of keys [key0, key0 + 32) of a segment (rows past k_last repeat
+// row k_last) into buffer `buf`, nontemporal (each row is read once): lane l of copy ii
+// writes row 4ii + l/16, chunk position l%16, the chunk it fetches swizzled as in the
+// attention kernel.  The 8 K copies are issued before the 8 V copies, so that the scores
+// can start once K has landed.
+__device__ __forceinline__ void mt_issue_window(const char* kseg, const char* vseg, int64_t row_bytes, int key0,
+                                                int k_last, uint8_t* lds, int buf, int lane) {
+    constexpr int kNt = 2;     // cache policy: nontemporal
+    int64_t off[kMtWin / 4];
+#pragma unroll
+    for (int ii = 0; ii < kMtWin / 4; ++ii) {
+        const int r = 4 * ii + (lane >> 4);
+        const int c = (lane & 15) ^ pf_swz(r);
+        off[ii] = static_cast<int64_t>(min(key0 + r, k_last)) * row_bytes + 16 * c;
+    }
+    uint8_t* d = lds + buf * kMtBufB;
+#pragma unroll
+    for (int ii = 0; ii < kMtWin / 4; ++ii)
+        __builtin_amdgcn_global_load_lds(kseg + off[ii], (lds_void_t*)(d + ii * 1024), 16, 0, kNt);
+#pragma unroll
+    for (int ii = 0; ii < kMtWin / 4; ++ii)
+        __builtin_amdgcn_global_load_lds(vseg + off[ii], (lds_void_t*)(d + kMtPlaneB + ii * 1024), 16, 0, kNt);
+}
+
+// Running state of a piece in lane (g, n): O^T[16dt + 4g + i][column n] in fp64, the
+// lane's share of the column's sum, and the column's running max (log2 units, integer-
+// valued; -inf until the piece has seen a key the column may attend to).
+struct MtState {
+    double o64[8][4];
+    double l64;
+    float m_run;
+};
+
+// One 32-key window [key0, key0 + 32) of a piece ending at k_b: scores, online softmax,
+// V^T P^T.  `lim` = the last key this lane's column may attend to (start + t).  Chunk keys
+// (>= st) add the products of their second and third K parts, read from the workspace.
+template <bool kChunkKeys, bool kNextIssued>
+__device__ __forceinline__ void mt_window(const PrefillArgs& a, const uint8_t* kplane, uint32_t vbase,
+                                          const bf16x8_t (&qop)[3][4], int b, int kvh, int st, int key0, int k_b,
+                                          int lim, int lane, MtState& t) {
+    // This window's K copies have landed (the 8 V copies and, when issued, the next window's
+    // 16 are younger); V is waited for before V^T P^T.
+    __builtin_amdgcn_s_waitcnt(vmcnt_imm(kNextIssued ? kMtCopies + kMtCopies / 2 : kMtCopies / 2));
+    const int n = lane & 15;
+    const int g = lane >> 4;
+    f32x4_t sacc[2] = {f32x4_t{0.f, 0.f, 0.f, 0.f}, f32x4_t{0.f, 0.f, 0.f, 0.f}};
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb) {
+        bf16x8_t ak[2];
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt) ak[kt] = pf_k_chunk(kplane, 16 * kt + n, 4 * kb + g);
+#pragma unroll
+        for (int s = 0; s < 3; ++s)
+#pragma unroll
+            for (int kt = 0; kt < 2; ++kt)
+                sacc[kt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ak[kt], qop[s][kb], sacc[kt], 0, 0, 0);
+    }
+    if (kChunkKeys) {
+        const int64_t n_rows = static_cast<int64_t>(a.batch) * a.n_new * kHkv;
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt) {
+            const int u = key0 + 16 * kt + n - st;     // chunk row of this lane's key
+            const int64_t prow = (u >= 0 && u < a.n_new) ? (static_cast<int64_t>(b) * a.n_new + u) * kHkv + kvh
+                                                          : 2 * n_rows;
+            const int64_t lrow = prow == 2 * n_rows ? prow : n_rows + prow;
+            const uint4* p2 = reinterpret_cast<const uint4*>(a.k_split + prow * kD) + g;
+            const uint4* p3 = reinterpret_cast<const uint4*>(a.k_split + lrow * kD) + g;
+#pragma unroll
+            for (int kb = 0; kb < 4; ++kb) {
+                const bf16x8_t k2 = as_bf16x8(p2[4 * kb]);
+                const bf16x8_t k3 = as_bf16x8(p3[4 * kb]);
+                sacc[kt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(k2, qop[0][kb], sacc[kt], 0, 0, 0);
+                sacc[kt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(k2, qop[1][kb], sacc[kt], 0, 0, 0);
+                sacc[kt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(k3, qop[0][kb], sacc[kt], 0, 0, 0);
+            }
+        }
+    }
+    // Mask (keys past the piece or past the column's token), window max per column.
+    float bmax = -INFINITY;
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int key = key0 + 16 * kt + 4 * g + i;
+            if (key >= k_b || key > lim) sacc[kt][i] = -INFINITY;
+            bmax = fmaxf(bmax, sacc[kt][i]);
+        }
+    bmax = swap32_max(swap16_max(bmax));
+    const float m_new = bmax > t.m_run ? ceilf(bmax) : t.m_run;
+    if (__ballot(m_new != t.m_run)) {
+        const int shift = (t.m_run == -INFINITY) ? 0 : static_cast<int>(t.m_run - m_new);
+#pragma unroll
+        for (int dt = 0; dt < 8; ++dt)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) t.o64[dt][i] = ldexp(t.o64[dt][i], shift);
+        t.l64 = ldexp(t.l64, shift);
+        t.m_run = m_new;
+    }
+    // A column that has seen no key yet keeps m = -inf and p = 0 (every score -inf).
+    const float m_eff = t.m_run == -INFINITY ? 0.f : t.m_run;
+    uint32_t ph[3][2][4];
+    float lsum = 0.f;
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt) pf_probs_tile(sacc[kt], m_eff, lsum, ph, kt);
+    t.l64 += static_cast<double>(lsum);
+
+    __builtin_amdgcn_s_waitcnt(vmcnt_imm(kNextIssued ? kMtCopies : 0));
+    // V^T P^T: dim tile dt from two transposed reads (rows 4g + a/4 and 16 rows on).
+    bf16x8_t pb[3];
+#pragma unroll
+    for (int s = 0; s < 3; ++s) pb[s] = as_bf16x8(make_uint4(ph[s][0][0], ph[s][0][1], ph[s][0][2], ph[s][0][3]));
+#pragma unroll
+    for (int d0 = 0; d0 < 8; d0 += 2) {
+        short4_t r[2][2];
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+            const uint32_t ad = vbase + pf_vt_addr(0u, d0 + e, lane) - kOffV;
+            asm volatile("ds_read_b64_tr_b16 %0, %1" : "=v"(r[e][0]) : "v"(ad));
+            asm volatile("ds_read_b64_tr_b16 %0, %1 offset:4096" : "=v"(r[e][1]) : "v"(ad));
+        }
+        asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(r[0][0]), "+v"(r[0][1]), "+v"(r[1][0]), "+v"(r[1][1]));
+        f32x4_t oacc[2];
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+            union {
+                short4_t h[2];
+                bf16x8_t v;
+            } u;
+            u.h[0] = r[e][0];
+            u.h[1] = r[e][1];
+            oacc[e] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int s = 0; s < 3; ++s) oacc[e] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(u.v, pb[s], oacc[e], 0, 0, 0);
+        }
+#pragma unroll
+        for (int e = 0; e < 2; ++e)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) t.o64[d0 + e][i] += static_cast<double>(oacc[e][i]);
+    }
+}
+
+// End of a piece: the column sums over the four rows; a whole segment writes its output
+// rows (tokens < T), a split one its partial at slot wg + segment.
+__device__ __forceinline__ void mt_piece_end(const PrefillArgs& a, int b, int kvh, bool whole, int64_t slot,
+                                             int lane, MtState& t) {
+    const int n = lane & 15;
+    const int g = lane >> 4;
+    const double l = swap_add_f64<true>(swap_add_f64<false>(t.l64));
+    if (whole) {
+        const int tok = n >> 2;
+        if (tok >= a.n_new) return;
+        uint16_t* orow = a.out + ((static_cast<int64_t>(b) * a.n_new + tok) * kHq + kvh * kGroup + (n & 3)) * kD;
+#pragma unroll
+        for (int dt = 0; dt < 8; ++dt) {
+            uint2 pk;
+            pk.x = f32_to_bf16_rne(static_cast<float>(t.o64[dt][0] / l)) |
+                   (static_cast<uint32_t>(f32_to_bf16_rne(static_cast<float>(t.o64[dt][1] / l))) << 16);
+            pk.y = f32_to_bf16_rne(static_cast<float>(t.o64[dt][2] / l)) |
+                   (static_cast<uint32_t>(f32_to_bf16_rne(static_cast<float>(t.o64[dt][3] / l))) << 16);
+            *reinterpret_cast<uint2*>(orow + 16 * dt + 4 * g) = pk;
+        }
+        return;
+    }
+    double* po = a.part_o + (slot * kMtCols + n) * kD;
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt) {
+        double2* d = reinterpret_cast<double2*>(po + 16 * dt + 4 * g);
+        d[0] = make_double2(t.o64[dt][0], t.o64[dt][1]);
+        d[1] = make_double2(t.o64[dt][2], t.o64[dt][3]);
+    }
+    if (g == 0) a.part_ml[slot * kMtCols + n] = make_float2(t.m_run, static_cast<float>(l));
+}
+
+// Sequence windows of the plan: o = seq_off[base + lane], o1 = seq_off[base + lane + 1].
+struct MtWindow {
+    int base;
+    int64_t o, o1;
+};
+
+__device__ __forceinline__ void mt_load_window(const PrefillArgs& a, int base, MtWindow& w) {
+    const int bb = base + static_cast<int>(threadIdx.x & (kWave - 1));
+    w.base = base;
+    w.o = bb < a.batch ? a.seq_off[bb] : INT64_MAX;
+    w.o1 = bb < a.batch ? a.seq_off[bb + 1] : INT64_MAX;
+}
+
+// The segment after (b, kvh) that has keys; false when there is none.
+__device__ __forceinline__ bool mt_next_segment(const PrefillArgs& a, MtWindow& w, int lead, int& b, int& kvh,
+                                                int& nk) {
+    if (kvh + 1 < kHkv) {
+        ++kvh;
+        return true;
+    }
+    kvh = 0;
+    while (true) {
+        const int bb = w.base + static_cast<int>(threadIdx.x & (kWave - 1));
+        const uint64_t m = __ballot(bb < a.batch && bb > b && w.o1 > w.o);
+        if (m) {
+            const int j = __ffsll(static_cast<unsigned long long>(m)) - 1;
+            b = w.base + j;
+            nk = static_cast<int>((__shfl(w.o1, j) - __shfl(w.o, j)) / kHkv) - lead;
+            return true;
+        }
+        if (w.base + kWave >= a.batch) return false;
+        mt_load_window(a, w.base + kWave, w);
+    }
+}
+
+__global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(1))) void mt_stream_kernel(PrefillArgs a) {
+    __shared__ __attribute__((aligned(1024))) uint8_t lds[kMtLdsB];
+    MtWindow w0;
+    mt_load_window(a, 0, w0);
+    const int64_t wg = blockIdx.x;
+    const int64_t total = a.plan_hdr[0];
+    const int64_t per_wg = a.plan_hdr[1];
+    const int lead = static_cast<int>(a.plan_hdr[2]);
+    int64_t x = wg * per_wg;
+    if (x >= total) return;
+    const int64_t x_end = min(x + per_wg, total);
+    const int lane = threadIdx.x & (kWave - 1);
+    const int n = lane & 15;
+    const int64_t row_bytes = a.kv_pos_stride * 2;
+    const uint32_t lds_base = static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_void_t*)(lds)));
+
+    // First piece: the last sequence b with seq_off[b] <= x.
+    MtWindow sw;
+    int b = 0;
+    int64_t off = 0, next = 0;
+    for (int base = 0; base < a.batch; base += kWave) {
+        MtWindow t = w0;
+        if (base > 0) mt_load_window(a, base, t);
+        const uint64_t le = __ballot(t.o <= x);
+        if (le) {
+            const int j = 63 - __clzll(static_cast<long long>(le));
+            b = base + j;
+            off = __shfl(t.o, j);
+            next = __shfl(t.o1, j);
+            sw = t;
+        }
+    }
+    int kvh, key, nk;
+    locate_first_piece(off, next, lead, x, kvh, key, nk);
+    x = uniform_i64(x);
+    b = __builtin_amdgcn_readfirstlane(b);
+    kvh = __builtin_amdgcn_readfirstlane(kvh);
+    key = __builtin_amdgcn_readfirstlane(key);
+    nk = __builtin_amdgcn_readfirstlane(nk);
+    int k_b = __builtin_amdgcn_readfirstlane(static_cast<int>(min(static_cast<int64_t>(nk), key + (x_end - x))));
+
+    auto seg_base = [&](const uint16_t* base, int bb, int hh) {
+        return reinterpret_cast<const char*>(base + static_cast<int64_t>(bb) * a.kv_batch_stride +
+                                             static_cast<int64_t>(hh) * a.kv_head_stride);
+    };
+    // The current window (piece b/kvh, keys [kw, kw + 32) of [key, k_b)) is in buffer
+    // `buf`; its copies were requested before it.
+    int buf = 0;
+    int kw = key;
+    mt_issue_window(seg_base(a.k, b, kvh), seg_base(a.v, b, kvh), row_bytes, kw, k_b - 1, lds, 0, lane);
+
+    while (true) {
+        // This piece: Q operands, start, window loop.
+        const int st = a.start[b];
+        bf16x8_t qop[3][4];
+        {
+            const uint4* src = a.q_op + (static_cast<int64_t>(b) * kHkv + kvh) * 12 * kWave + lane;
+#pragma unroll
+            for (int s = 0; s < 3; ++s)
+#pragma unroll
+                for (int kb = 0; kb < 4; ++kb) qop[s][kb] = as_bf16x8(src[(s * 4 + kb) * kWave]);
+        }
+        const int lim = st + min(n >> 2, a.n_new - 1);
+        MtState t;
+#pragma unroll
+        for (int dt = 0; dt < 8; ++dt)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) t.o64[dt][i] = 0.0;
+        t.l64 = 0.0;
+        t.m_run = -INFINITY;
+
+        // The next piece (its first window's copies are requested during this piece's last).
+        const int64_t x_next = x + (k_b - key);
+        int b2 = b, kvh2 = kvh, nk2 = nk;
+        bool more = x_next + lead < x_end;
+        if (more) {
+            more = mt_next_segment(a, sw, lead, b2, kvh2, nk2);
+            b2 = __builtin_amdgcn_readfirstlane(b2);
+            kvh2 = __builtin_amdgcn_readfirstlane(kvh2);
+            nk2 = __builtin_amdgcn_readfirstlane(nk2);
+        }
+        const int k_b2 = more ? __builtin_amdgcn_readfirstlane(
+                                    static_cast<int>(min(static_cast<int64_t>(nk2), x_end - x_next - lead)))
+                              : 0;
+
+        const char* kseg = seg_base(a.k, b, kvh);
+        const char* vseg = seg_base(a.v, b, kvh);
+        for (;;) {
+            // Request the next window (this piece's, else the next piece's first), then wait
+            // for this one's copies.
+            const bool in_piece = kw + kMtWin < k_b;
+            int issued = 0;
+            if (in_piece) {
+                mt_issue_window(kseg, vseg, row_bytes, kw + kMtWin, k_b - 1, lds, buf ^ 1, lane);
+                issued = kMtCopies;
+            } else if (more) {
+                mt_issue_window(seg_base(a.k, b2, kvh2), seg_base(a.v, b2, kvh2), row_bytes, 0, k_b2 - 1, lds,
+                                buf ^ 1, lane);
+                issued = kMtCopies;
+            }
+            // mt_window waits for this window's copies (the counter retires in issue order, so
+            // older requests -- the piece's Q operands, earlier stores -- are waited for too).
+            const uint8_t* kplane = lds + buf * kMtBufB;
+            const uint32_t vbase = lds_base + buf * kMtBufB + kMtPlaneB;
+            const bool chunk_keys = kw + kMtWin > st;
+            if (issued) {
+                if (chunk_keys)
+                    mt_window<true, true>(a, kplane, vbase, qop, b, kvh, st, kw, k_b, lim, lane, t);
+                else
+                    mt_window<false, true>(a, kplane, vbase, qop, b, kvh, st, kw, k_b, lim, lane, t);
+            } else {
+                if (chunk_keys)
+                    mt_window<true, false>(a, kplane, vbase, qop, b, kvh, st, kw, k_b, lim, lane, t);
+                else
+                    mt_window<false, false>(a, kplane, vbase, qop, b, kvh, st, kw, k_b, lim, lane, t);
+            }
+            buf ^= 1;
+            if (!in_piece) break;
+            kw += kMtWin;
+        }
+        mt_piece_end(a, b, kvh, key == 0 && k_b == nk, wg + static_cast<int64_t>(b) * kHkv + kvh, lane, t);
+        if (!more) break;
+        x = x_next + lead;
+        b = b2;
+        kvh = kvh2;
+        nk = nk2;
+        key = 0;
+        k_b = k_b2;
+        kw = 0;
+    }
+}
+
+// Merge the pieces of split segments: one 256-thread workgroup per (KV head, sequence);
+// thread i handles column i/16 (token, head), dims 8(i%16) .. +8.  Weights 2^(m - max) are
+// exact; a piece that saw no key the column may attend to has m = -inf and weight 0.
+__global__ __launch_bounds__(256) void mt_merge_kernel(PrefillArgs a) {
+    const int kvh = blockIdx.x;
+    const int b = blockIdx.y;
+    const int64_t per_wg = a.plan_hdr[1];
+    const int lead = static_cast<int>(a.plan_hdr[2]);
+    const int64_t off = a.seq_off[b];
+    const int span = static_cast<int>((a.seq_off[b + 1] - off) / kHkv);
+    if (span == 0) return;
+    const int nk = span - lead;
+    const int64_t seg_off = off + static_cast<int64_t>(kvh) * span + lead;
+    const int64_t w_first = seg_off / per_wg;
+    const int n_pieces = static_cast<int>((seg_off + nk - 1) / per_wg - w_first) + 1;
+    if (n_pieces == 1) return;
+    const int64_t slot0 = w_first + static_cast<int64_t>(b) * kHkv + kvh;
+    const int col = threadIdx.x >> 4;
+    const int d0 = 8 * (threadIdx.x & 15);
+    const int tok = col >> 2;
+    if (tok >= a.n_new) return;
+    float mx = -INFINITY;
+    for (int p = 0; p < n_pieces; ++p) mx = fmaxf(mx, a.part_ml[(slot0 + p) * kMtCols + col].x);
+    double l = 0.0, o[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    for (int p = 0; p < n_pieces; ++p) {
+        const float2 ml = a.part_ml[(slot0 + p) * kMtCols + col];
+        if (ml.x == -INFINITY) continue;
+        const int e = static_cast<int>(ml.x - mx);
+        l += ldexp(static_cast<double>(ml.y), e);
+        const double* po = a.part_o + ((slot0 + p) * kMtCols + col) * kD + d0;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) o[j] += ldexp(po[j], e);
+    }
+    uint16_t h8[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) h8[j] = f32_to_bf16_rne(static_cast<float>(o[j] / l));
+    uint4 pk;
+    pk.x = h8[0] | (static_cast<uint32_t>(h8[1]) << 16);
+    pk.y = h8[2] | (static_cast<uint32_t>(h8[3]) << 16);
+    pk.z = h8[4] | (static_cast<uint32_t>(h8[5]) << 16);
+    pk.w = h8[6] | (static_cast<uint32_t>(h8[7]) << 16);
+    *reinterpret_cast<uint4*>(a.out + ((static_cast<int64_t>(b) * a.n_new + tok) * kHq + kvh * kGroup + (col & 3)) * kD +
+                              d0) = pk;
+}
+
+hipError_t launch_prefill_multi(const PrefillArgs& a, hipStream_t stream, hipEvent_t* ev) {
+    hipLaunchKernelGGL(mt_prepare_kernel, dim3(kHkv, static_cast<unsigned>(a.batch) + 1), dim3(kWave), 0, stream, a);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    if (ev) (void)hipEventRecord(ev[1], stream);
+    hipLaunchKernelGGL(mt_stream_kernel, dim3(static_cast<unsigned>(a.n_wgs)), dim3(kWave), 0, stream, a);
+    e = hipGetLastError();
+    if (ev) (void)hipEventRecord(ev[2], stream);
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(mt_merge_kernel, dim3(kHkv, static_cast<unsigned>(a.batch)), dim3(256), 0, stream, a);
     return hipGetLastError();
 }
 

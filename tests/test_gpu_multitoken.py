@@ -1,0 +1,172 @@
+"""Multi-token decode (chunks of 1..4 new tokens per sequence: speculative drafts, a few
+steps of one sequence at once) through gqa_prefill, which sends such chunks down the
+stream-K path (key ranges split over all CUs, per-range partials merged) instead of the
+prefill attention kernel.  Every output row is checked against the compiled oracle's
+per-token reference step (the one-token golden of pyfiles/gen_gqa_wrapper_vectors.py:
+121-139 per new token, new K rotated at its position, not re-rounded), within 64 BF16 ULP
+with the reference checker's tiny-value exemption (pyfiles/check_gqa_output.py:33-34,57-64).
+Cache rows past the chunk hold NaN, so a read of one would poison the output."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import attention_accelerator_amd as gqa
+from oracle import oracle as orc
+from _util import assert_within_ulp, to_codes
+
+pytestmark = pytest.mark.gpu
+
+
+def _chunk(starts, n_new, capacity, seed):
+    """N(0,1) BF16 inputs; cache rows < start random, rows >= start NaN."""
+    g = torch.Generator("cpu").manual_seed(seed)
+    batch = len(starts)
+    q = torch.randn((batch, n_new, 32, 128), generator=g).to(torch.bfloat16)
+    kn = torch.randn((batch, n_new, 8, 128), generator=g).to(torch.bfloat16)
+    vn = torch.randn((batch, n_new, 8, 128), generator=g).to(torch.bfloat16)
+    k = torch.full((batch, 8, capacity, 128), float("nan"), dtype=torch.bfloat16)
+    v = torch.full((batch, 8, capacity, 128), float("nan"), dtype=torch.bfloat16)
+    for b, s in enumerate(starts):
+        k[b, :, :s] = torch.randn((8, s, 128), generator=g).to(torch.bfloat16)
+        v[b, :, :s] = torch.randn((8, s, 128), generator=g).to(torch.bfloat16)
+    return q, kn, vn, k, v
+
+
+def _oracle(q, kn, vn, k, v, starts, rope_q=True, rope_k=True):
+    return orc.prefill(to_codes(q), to_codes(k), to_codes(v), to_codes(kn), to_codes(vn),
+                       np.asarray(starts), rope_q=rope_q, rope_k_new=rope_k)
+
+
+def _run(q, kn, vn, k, v, starts, dev, **kw):
+    kd, vd = k.to(dev), v.to(dev)
+    out = gqa.gqa_prefill(q.to(dev), kn.to(dev), vn.to(dev), kd, vd, starts, **kw)
+    torch.cuda.synchronize()
+    return to_codes(out), kd, vd
+
+
+# Starts at 0 (the chunk sees only itself), inside the first 16-key range, on and off
+# range boundaries, and long enough to span several workgroups' ranges.
+_STARTS = [0, 1, 15, 16, 33, 700, 2047, 4100]
+
+
+@pytest.mark.parametrize("n_new", [1, 2, 3, 4])
+def test_multi_all_rows_against_oracle(dev, n_new):
+    starts = _STARTS
+    q, kn, vn, k, v = _chunk(starts, n_new, max(starts) + n_new + 5, 30 + n_new)
+    want = _oracle(q, kn, vn, k, v, starts)
+    got, kd, vd = _run(q, kn, vn, k, v, starts, dev)
+    w = assert_within_ulp(want.reshape(-1, 128), got.reshape(-1, 128), 64, f"multi T={n_new}")
+    print(f"T={n_new}: worst {w} ULP")
+    kc, vc = to_codes(kd), to_codes(vd)
+    for b, s in enumerate(starts):
+        assert np.array_equal(vc[b, :, s:s + n_new], to_codes(vn[b]).transpose(1, 0, 2))
+        assert (kc[b, :, s + n_new:] == to_codes(k[b, :, s + n_new:])).all()
+
+
+def test_multi_no_rope(dev):
+    starts = [3, 260, 1500]
+    q, kn, vn, k, v = _chunk(starts, 3, 1510, 40)
+    want = _oracle(q, kn, vn, k, v, starts, rope_q=False, rope_k=False)
+    got, kd, _ = _run(q, kn, vn, k, v, starts, dev, rope_q=False, rope_k=False)
+    assert_within_ulp(want.reshape(-1, 128), got.reshape(-1, 128), 64, "multi no rope")
+    assert np.array_equal(to_codes(kd)[1, 5, 260:263], to_codes(kn[1, :, 5]))
+
+
+def test_multi_long_sequences(dev):
+    """8192 cached positions (the longest of the decode workloads) beside short ones."""
+    starts = [8188, 3001, 9]
+    q, kn, vn, k, v = _chunk(starts, 4, 8192, 41)
+    want = _oracle(q, kn, vn, k, v, starts)
+    got, _, _ = _run(q, kn, vn, k, v, starts, dev)
+    assert_within_ulp(want.reshape(-1, 128), got.reshape(-1, 128), 64, "multi long")
+
+
+@pytest.mark.parametrize("n_wgs", ["1", "7", "64", "333", "4096"])
+def test_multi_partition_counts(dev, monkeypatch, n_wgs):
+    """The split of the keys over workgroups (GQA_STREAM_WGS workgroups) changes the order
+    of the partial sums only: every split stays within the tolerance of the oracle."""
+    monkeypatch.setenv("GQA_STREAM_WGS", n_wgs)
+    starts = [5, 1200, 64, 2999, 0, 17]
+    q, kn, vn, k, v = _chunk(starts, 4, 3010, 42)
+    want = _oracle(q, kn, vn, k, v, starts)
+    got, _, _ = _run(q, kn, vn, k, v, starts, dev)
+    assert_within_ulp(want.reshape(-1, 128), got.reshape(-1, 128), 64, f"multi wgs={n_wgs}")
+
+
+def test_multi_and_prefill_kernel_agree(dev, monkeypatch):
+    """The same chunk through the stream-K path and through the prefill attention kernel
+    (GQA_PREFILL_MULTI=0): both within the tolerance of the oracle, caches bit-identical."""
+    starts = [77, 1024, 300]
+    q, kn, vn, k, v = _chunk(starts, 4, 1100, 43)
+    want = _oracle(q, kn, vn, k, v, starts)
+    a, ka, va = _run(q, kn, vn, k, v, starts, dev)
+    monkeypatch.setenv("GQA_PREFILL_MULTI", "0")
+    b, kb, vb = _run(q, kn, vn, k, v, starts, dev)
+    assert_within_ulp(want.reshape(-1, 128), a.reshape(-1, 128), 64, "stream-K path")
+    assert_within_ulp(want.reshape(-1, 128), b.reshape(-1, 128), 64, "prefill kernel path")
+    assert np.array_equal(to_codes(ka), to_codes(kb)) and np.array_equal(to_codes(va), to_codes(vb))
+
+
+def test_multi_causal_independence(dev):
+    """Token t's row does not depend on the chunk's later tokens: perturbing token 3's Q,
+    K and V leaves rows 0..2 bit-identical."""
+    starts = [400, 31]
+    q, kn, vn, k, v = _chunk(starts, 4, 420, 44)
+    ref, _, _ = _run(q, kn, vn, k, v, starts, dev)
+    q2, kn2, vn2 = q.clone(), kn.clone(), vn.clone()
+    q2[:, 3] = torch.randn(q2[:, 3].shape).to(torch.bfloat16) * 3
+    kn2[:, 3] = torch.randn(kn2[:, 3].shape).to(torch.bfloat16) * 4
+    vn2[:, 3] = torch.randn(vn2[:, 3].shape).to(torch.bfloat16) * 4
+    got, _, _ = _run(q2, kn2, vn2, k, v, starts, dev)
+    assert np.array_equal(got[:, :3], ref[:, :3])
+    assert not np.array_equal(got[:, 3], ref[:, 3])
+
+
+def test_multi_position_major_cache(dev):
+    """Cache stored [B][S][8][128]: the same bits as head-major."""
+    starts = [45, 130, 0]
+    q, kn, vn, k, v = _chunk(starts, 2, 140, 45)
+    want, kd_ref, _ = _run(q, kn, vn, k, v, starts, dev)
+    kp = k.permute(0, 2, 1, 3).contiguous().to(dev).permute(0, 2, 1, 3)
+    vp = v.permute(0, 2, 1, 3).contiguous().to(dev).permute(0, 2, 1, 3)
+    got = to_codes(gqa.gqa_prefill(q.to(dev), kn.to(dev), vn.to(dev), kp, vp, starts))
+    torch.cuda.synchronize()
+    assert np.array_equal(got, want)
+    assert np.array_equal(to_codes(kp), to_codes(kd_ref))
+
+
+def test_multi_invalid_device_start_gives_nan_rows(dev):
+    """A device start past capacity - T: NaN rows for that sequence, its cache untouched,
+    the other sequences unaffected."""
+    starts = torch.tensor([40, 98, 7], dtype=torch.int32)   # sequence 1: 98 + 3 > 100
+    q, kn, vn, k, v = _chunk([40, 0, 7], 3, 100, 46)
+    kd, vd = k.to(dev), v.to(dev)
+    out = gqa.gqa_prefill(q.to(dev), kn.to(dev), vn.to(dev), kd, vd, starts.to(dev))
+    torch.cuda.synchronize()
+    got = to_codes(out)
+    assert (got[1] == 0x7FC0).all()
+    assert np.array_equal(to_codes(kd)[1], to_codes(k)[1])
+    idx = [0, 2]
+    want = _oracle(q[idx], kn[idx], vn[idx], k[idx], v[idx], [40, 7])
+    assert_within_ulp(want.reshape(-1, 128), got[idx].reshape(-1, 128), 64, "valid beside invalid")
+
+
+def test_multi_workspace_garbage_and_repeat(dev):
+    """A workspace full of 0xFF gives the same bits (the plan, partials and Q operands are
+    all written before they are read), and a PreparedPrefill repeats them call after call."""
+    starts = [128, 0, 777, 5]
+    q, kn, vn, k, v = _chunk(starts, 4, 790, 47)
+    a, _, _ = _run(q, kn, vn, k, v, starts, dev)
+    ws = torch.empty(gqa.prefill_workspace_bytes(4, 4), dtype=torch.uint8, device=dev)
+    ws.fill_(0xFF)
+    b, _, _ = _run(q, kn, vn, k, v, starts, dev, workspace=ws)
+    assert np.array_equal(a, b)
+    kd, vd = k.to(dev), v.to(dev)
+    call = gqa.PreparedPrefill(q.to(dev), kn.to(dev), vn.to(dev), kd, vd,
+                               torch.tensor(starts, dtype=torch.int32, device=dev))
+    for _ in range(3):
+        got = to_codes(call())
+        torch.cuda.synchronize()
+        assert np.array_equal(got, a)
