@@ -83,6 +83,18 @@ bool use_multi(int32_t n_new) {
     return !(s && s[0] == '0');
 }
 
+// XCD weighting of the stream-K ranges, per mille of a range moved from each workgroup on
+// an odd XCD to its even neighbour (GQA_XCD_SKEW overrides; 0 gives equal ranges).  At
+// most 250: an odd range keeps at least 3/4 of the range size, more than a segment lead.
+int32_t xcd_skew_pm() {
+    const char* s = std::getenv("GQA_XCD_SKEW");
+    if (s) {
+        const int v = std::atoi(s);
+        if (v >= 0 && v <= 250) return v;
+    }
+    return 40;
+}
+
 bool geometry_ok(const gqa_params_t* p) {
     if (p->n_q_heads != kHq || p->n_kv_heads != kHkv || p->head_dim != kD) return false;
     if (!(p->scale != 0.f) || !std::isfinite(p->scale)) return false;
@@ -421,9 +433,10 @@ extern "C" {
 
 size_t gqa_prefill_workspace_bytes(const gqa_params_t* params, int32_t batch, int32_t n_new) {
     if (!params || !geometry_ok(params) || batch <= 0 || n_new <= 0) return 0;
-    size_t bytes = align_up(prefill_split_bytes(batch, n_new), 256);
-    if (use_multi(n_new)) bytes += prefill_multi_bytes(batch, stream_wgs());
-    return bytes;
+    // The multi-token path needs no split planes: the chunk's unrounded keys enter through
+    // the scores its preparation kernel forms.
+    if (use_multi(n_new)) return prefill_multi_bytes(batch, stream_wgs());
+    return align_up(prefill_split_bytes(batch, n_new), 256);
 }
 
 int gqa_kv_append_bf16(const gqa_params_t* params, const uint16_t* k_new, const uint16_t* v_new,
@@ -470,19 +483,23 @@ int gqa_prefill_bf16(const gqa_params_t* params, const uint16_t* q, const uint16
     if (!workspace || workspace_bytes < need || !aligned(workspace, 256)) return GQA_ERR_WORKSPACE;
     a.q = q;
     a.out = out;
-    a.k_split = static_cast<uint16_t*>(workspace);
     const bool multi = use_multi(n_new);
-    if (multi)
-        prefill_multi_layout(a, static_cast<char*>(workspace) + align_up(prefill_split_bytes(batch, n_new), 256),
-                             stream_wgs());
+    if (multi) {
+        a.k_split = nullptr;
+        prefill_multi_layout(a, workspace, stream_wgs());
+        a.skew_pm = xcd_skew_pm();
+    } else {
+        a.k_split = static_cast<uint16_t*>(workspace);
+    }
     hipStream_t s = static_cast<hipStream_t>(stream);
     hipEvent_t* ev = profile_slot();
     if (ev) (void)hipEventRecord(ev[0], s);
-    hipError_t e = launch_kv_append(a, s);
     if (multi) {
-        if (e == hipSuccess) e = launch_prefill_multi(a, s, ev);
+        // The preparation kernel of the multi-token path appends the chunk's rows itself.
+        const hipError_t e = launch_prefill_multi(a, s, ev);
         return e == hipSuccess ? GQA_OK : GQA_ERR_HIP;
     }
+    hipError_t e = launch_kv_append(a, s);
     if (ev) (void)hipEventRecord(ev[1], s);
     if (e == hipSuccess) e = launch_prefill_attention(a, s);
     if (ev) (void)hipEventRecord(ev[2], s);

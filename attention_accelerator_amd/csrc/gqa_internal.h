@@ -108,11 +108,14 @@ struct PrefillArgs {
     RopeTable rope;
     // Multi-token path (n_new <= kMultiMaxNew): the stream-K split of the decode path.
     uint4* q_op;              // [B][8][3][4][64] Q operands (3 BF16 parts, MFMA B layout)
-    int64_t* plan_hdr;        // {total stream positions, positions per workgroup, segment lead}
+    int64_t* plan_hdr;        // {total stream positions, positions per workgroup, segment lead,
+                              //  positions moved from odd to even ranges}
     int64_t* seq_off;         // [B+1] stream position of sequence b's first segment
     double* part_o;           // [n_slots][16][128] unnormalised partial outputs (column 4t + h)
     float2* part_ml;          // [n_slots][16] (integer-valued running max in log2 units, sum)
+    float4* chunk_s;          // [B][8][16] scores of the chunk's keys u = 0..3 per column (log2 units)
     int32_t n_wgs;            // persistent workgroups of the multi-token stream kernel
+    int32_t skew_pm;          // XCD weighting of the ranges (per mille of a range)
 };
 
 // Chunks of at most this many new tokens per sequence take the multi-token path.

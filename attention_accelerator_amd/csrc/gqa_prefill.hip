@@ -667,17 +667,21 @@ hipError_t launch_prefill_attention(const PrefillArgs& a, hipStream_t stream) {
 // arithmetic is the attention kernel's: three BF16 parts of Q, the chunk's own keys
 // carried to ~24 bits, P in three parts, fp64 accumulation, integer-valued running max.
 //
-// Per 32-key window a wave copies the window's K and V rows into its own LDS (double-
-// buffered, the next window's copies in flight while the current one is computed; no
-// barrier, the workgroup is one wave), forms the scores of both 16-key tiles, and adds
-// V^T P^T with the transposed V reads of the attention kernel.
+// Per 32-key window a wave copies the window's K rows and V rows (a plane of 8 KB each)
+// into its own LDS, forms the scores of both 16-key tiles, and adds V^T P^T with the
+// transposed V reads of the attention kernel.  The planes form a ring of five slots in the
+// order K0 V0 K1 V1 K2 ...: while window i is computed, K of windows i+1 and i+2 and V of
+// window i+1 are in flight (24 KB per wave; the HBM latency under full load is about two
+// and a half window periods, so two windows in flight leave the wave waiting).  No
+// barrier: the workgroup is one wave.  Five slots are 40 KB: the four workgroups of a CU
+// fill its 160 KB of LDS.
 
 constexpr int kMtWin = 32;                    // keys per window
 constexpr int kMtPlaneB = kMtWin * kRowB;     // 8 KB: 32 rows of 256 B
-constexpr int kMtBufB = 2 * kMtPlaneB;        // K plane, then V plane
-constexpr int kMtLdsB = 2 * kMtBufB;          // two buffers: 32 KB per workgroup
+constexpr int kMtSlots = 5;                   // ring slots, one plane each
+constexpr int kMtLdsB = kMtSlots * kMtPlaneB; // 40 KB per workgroup
 constexpr int kMtCols = 16;                   // query rows per segment: 4 heads x 4 tokens
-constexpr int kMtCopies = 16;                 // copy instructions per window per lane (8 K + 8 V)
+constexpr int kMtHalf = kMtWin / 4;           // copy instructions per plane per lane (1 KB each)
 
 // s_waitcnt immediate for vmcnt(n) alone (gfx9: vmcnt bits 3:0 and 15:14, expcnt and
 // lgkmcnt at their maxima).
@@ -696,7 +700,7 @@ size_t prefill_multi_bytes(int32_t batch, int32_t n_wgs) {
     auto al = [](size_t x) { return (x + 255) / 256 * 256; };
     return al(static_cast<size_t>(batch) * kHkv * 12 * kWave * sizeof(uint4)) + 256 +
            al((static_cast<size_t>(batch) + 1) * sizeof(int64_t)) + al(n_slots * kMtCols * kD * sizeof(double)) +
-           al(n_slots * kMtCols * sizeof(float2));
+           al(n_slots * kMtCols * sizeof(float2)) + al(static_cast<size_t>(batch) * kHkv * kMtCols * sizeof(float4));
 }
 
 void prefill_multi_layout(PrefillArgs& a, void* base, int32_t n_wgs) {
@@ -712,6 +716,8 @@ void prefill_multi_layout(PrefillArgs& a, void* base, int32_t n_wgs) {
     a.part_o = reinterpret_cast<double*>(p);
     p += al(n_slots * kMtCols * kD * sizeof(double));
     a.part_ml = reinterpret_cast<float2*>(p);
+    p += al(n_slots * kMtCols * sizeof(float2));
+    a.chunk_s = reinterpret_cast<float4*>(p);
     a.n_wgs = n_wgs;
 }
 
@@ -734,6 +740,7 @@ __device__ __forceinline__ void mt_build_plan(const PrefillArgs& a, int lane) {
         a.plan_hdr[0] = total;
         a.plan_hdr[1] = per_wg;
         a.plan_hdr[2] = lead;
+        a.plan_hdr[3] = range_extra(per_wg, a.skew_pm);
         a.seq_off[a.batch] = total;
     }
     int64_t carry = 0;
@@ -747,99 +754,202 @@ __device__ __forceinline__ void mt_build_plan(const PrefillArgs& a, int lane) {
     }
 }
 
-// Q operands of segment (b, kvh): lane (g, n) holds column n = 4t + h (token t, Q head
-// 4*kvh + h) at dims 32kb + 8g + j, rotated at position start + t and scaled by
-// scale*log2(e) in double, in three BF16 parts; columns of tokens t >= T are zero.  Row B
-// of the grid builds the plan; a sequence whose start is out of range gets NaN rows.
-__global__ __launch_bounds__(kWave) void mt_prepare_kernel(PrefillArgs a) {
+// Four consecutive BF16 values from p: one 8-byte load when the tensor is 16-byte aligned
+// (kVec; p is then a multiple of 4 elements past an aligned row start), else four 2-byte
+// loads.
+template <bool kVec>
+__device__ __forceinline__ void load4(const uint16_t* p, uint16_t (&h)[4]) {
+    if (kVec) {
+        const uint2 v = *reinterpret_cast<const uint2*>(p);
+        h[0] = static_cast<uint16_t>(v.x & 0xFFFFu);
+        h[1] = static_cast<uint16_t>(v.x >> 16);
+        h[2] = static_cast<uint16_t>(v.y & 0xFFFFu);
+        h[3] = static_cast<uint16_t>(v.y >> 16);
+    } else {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) h[i] = p[i];
+    }
+}
+
+// Per (sequence b, KV head kvh), four waves; wave w:
+//  - the KV append of new row u = w of this head (what kv_append_kernel does for all
+//    heads): lane i rotates the pair (i, i + 64) at position start + w in double and
+//    writes it rounded to BF16, and copies the V row;
+//  - a quarter of the Q operands: lane (g, n) holds column n = 4t + h (token t, Q head
+//    4*kvh + h) at dims 32kb + 8g + j; wave w takes kb = w & 1 and its pair kb + 2, j in
+//    [4(w >> 1), +4), rotated at position start + t and scaled by scale*log2(e) in
+//    double, split into three BF16 parts; columns of tokens t >= T are zero;
+//  - the same dims' share of the scores of the chunk's own keys (key start + u, u < T:
+//    the new K row rotated at its position and not rounded, as the reference rotates K)
+//    against every column, in double.  Wave 0 adds the four shares in a fixed order and
+//    rounds once to f32: the stream kernel takes these scores in place of the ones it
+//    would form from the cache's rounded copy of those rows.
+// Row B of the grid builds the plan.  A sequence whose start is out of range gets NaN
+// rows and no cache write.
+template <bool kVec>
+__global__ __launch_bounds__(256) void mt_prepare_kernel(PrefillArgs a) {
     const int kvh = blockIdx.x;
     const int b = blockIdx.y;
-    const int lane = threadIdx.x;
+    const int w = threadIdx.x >> 6;
+    const int lane = threadIdx.x & (kWave - 1);
     if (b == a.batch) {
-        if (kvh == 0) mt_build_plan(a, lane);
+        if (kvh == 0 && w == 0) mt_build_plan(a, lane);
         return;
     }
     const int T = a.n_new;
     const int st = a.start[b];
-    if (!prefill_start_ok(a, st)) {
-        for (int i = lane; i < T * kGroup * (kD / 8); i += kWave) {
-            const int t = i / (kGroup * (kD / 8));
-            const int r = i % (kGroup * (kD / 8));
-            uint4* o = reinterpret_cast<uint4*>(a.out + ((static_cast<int64_t>(b) * T + t) * kHq + kvh * kGroup) * kD);
-            o[r] = make_uint4(0x7fc07fc0u, 0x7fc07fc0u, 0x7fc07fc0u, 0x7fc07fc0u);
-        }
-        return;
-    }
+    // Every load first (the stores below may alias them as far as the compiler knows, so a
+    // load placed after a store would wait for it).
     const int g = lane >> 4;
     const int n = lane & 15;
     const int t = n >> 2;
     const bool col = t < T;
     const int tc = col ? t : T - 1;
-    const uint16_t* qrow = a.q + ((static_cast<int64_t>(b) * T + tc) * kHq + kvh * kGroup + (n & 3)) * kD;
-    // sin and cos of (start + t) * inv_freq[i], once per token and frequency (lane i).
-    __shared__ double sn_s[kMultiMaxNew][kPairs], cs_s[kMultiMaxNew][kPairs];
-    const bool rope = (a.flags & 1u) != 0;
-    if (rope) {
-        for (int tt = 0; tt < T; ++tt)
-            rope_sincos(static_cast<int64_t>(st) + tt, a.rope.inv_freq[lane], sn_s[tt][lane], cs_s[tt][lane]);
-        __syncthreads();
+    const int kbp = w & 1;
+    const int d0 = 32 * kbp + 8 * g + 4 * (w >> 1);
+    uint16_t akx = 0, aky = 0, avx = 0, avy = 0;
+    if (w < T) {
+        const int64_t row = ((static_cast<int64_t>(b) * T + w) * kHkv + kvh) * kD;
+        akx = a.k_new[row + lane];
+        aky = a.k_new[row + lane + kPairs];
+        avx = a.v_new[row + lane];
+        avy = a.v_new[row + lane + kPairs];
     }
-    double qv[4][8];
+    const uint16_t* qrow = a.q + ((static_cast<int64_t>(b) * T + tc) * kHq + kvh * kGroup + (n & 3)) * kD;
+    uint16_t qx[4], qy[4];
+    load4<kVec>(qrow + d0, qx);
+    load4<kVec>(qrow + d0 + kPairs, qy);
+    uint16_t kx[kMultiMaxNew][4], ky[kMultiMaxNew][4];
 #pragma unroll
-    for (int kb = 0; kb < 2; ++kb)
+    for (int u = 0; u < kMultiMaxNew; ++u) {
+        if (u < T) {
+            const uint16_t* krow = a.k_new + ((static_cast<int64_t>(b) * T + u) * kHkv + kvh) * kD;
+            load4<kVec>(krow + d0, kx[u]);
+            load4<kVec>(krow + d0 + kPairs, ky[u]);
+        }
+    }
+    if (!prefill_start_ok(a, st)) {
+        for (int i = threadIdx.x; i < T * kGroup * (kD / 4); i += blockDim.x) {
+            const int tt = i / (kGroup * (kD / 4));
+            const int r = i % (kGroup * (kD / 4));
+            uint2* o = reinterpret_cast<uint2*>(a.out + ((static_cast<int64_t>(b) * T + tt) * kHq + kvh * kGroup) * kD);
+            o[r] = make_uint2(0x7fc07fc0u, 0x7fc07fc0u);
+        }
+        return;
+    }
+    // sin and cos of (start + u) * inv_freq[i]: wave u, lane i.
+    __shared__ double sn_s[kMultiMaxNew][kPairs], cs_s[kMultiMaxNew][kPairs];
+    __shared__ double part_s[4][kMultiMaxNew][kMtCols];
+    const bool rope_q = (a.flags & 1u) != 0;
+    const bool rope_k = (a.flags & 2u) != 0;
+    if ((rope_q || rope_k) && w < T)
+        rope_sincos(static_cast<int64_t>(st) + w, a.rope.inv_freq[lane], sn_s[w][lane], cs_s[w][lane]);
+    __syncthreads();
+
+    double qvx[4], qvy[4];
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            const int d = 32 * kb + 8 * g + j;
-            const double x = bf16_to_f32(qrow[d]);
-            const double y = bf16_to_f32(qrow[d + kPairs]);
-            double xr = x, yr = y;
-            if (rope) {
-                const double sn = sn_s[tc][d], cs = cs_s[tc][d];
-                xr = x * cs - y * sn;
-                yr = x * sn + y * cs;
+    for (int jj = 0; jj < 4; ++jj) {
+        const int d = d0 + jj;
+        const double x = bf16_to_f32(qx[jj]);
+        const double y = bf16_to_f32(qy[jj]);
+        double xr = x, yr = y;
+        if (rope_q) {
+            const double sn = sn_s[tc][d], cs = cs_s[tc][d];
+            xr = x * cs - y * sn;
+            yr = x * sn + y * cs;
+        }
+        qvx[jj] = col ? xr * a.qk_scale_log2 : 0.0;
+        qvy[jj] = col ? yr * a.qk_scale_log2 : 0.0;
+    }
+    // This wave's share of the chunk-key scores, summed over the four lanes of column n.
+#pragma unroll
+    for (int u = 0; u < kMultiMaxNew; ++u) {
+        double acc = 0.0;
+        if (u < T) {
+#pragma unroll
+            for (int jj = 0; jj < 4; ++jj) {
+                const int d = d0 + jj;
+                const double x = bf16_to_f32(kx[u][jj]);
+                const double y = bf16_to_f32(ky[u][jj]);
+                double xr = x, yr = y;
+                if (rope_k) {
+                    const double sn = sn_s[u][d], cs = cs_s[u][d];
+                    xr = x * cs - y * sn;
+                    yr = x * sn + y * cs;
+                }
+                acc = fma(qvx[jj], xr, acc);
+                acc = fma(qvy[jj], yr, acc);
             }
-            qv[kb][j] = col ? xr * a.qk_scale_log2 : 0.0;
-            qv[kb + 2][j] = col ? yr * a.qk_scale_log2 : 0.0;
         }
-    uint4* dst = a.q_op + (static_cast<int64_t>(b) * kHkv + kvh) * 12 * kWave + lane;
-#pragma unroll
-    for (int s = 0; s < 3; ++s)
-#pragma unroll
-        for (int kb = 0; kb < 4; ++kb) {
-            uint16_t h8[8];
-#pragma unroll
-            for (int j = 0; j < 8; ++j) h8[j] = split3(qv[kb][j], s);
-            union {
-                bf16x8_t v;
-                uint4 u;
-            } cv;
-            cv.v = pack8(h8);
-            dst[(s * 4 + kb) * kWave] = cv.u;
+        acc += __shfl_xor(acc, 16);
+        acc += __shfl_xor(acc, 32);
+        if (g == 0) part_s[w][u][n] = acc;
+    }
+
+    // Stores: the appended cache row, this wave's Q operand quarter.
+    if (w < T) {
+        const int64_t ce = cache_elem(a, b, kvh, static_cast<int64_t>(st) + w);
+        double xr = bf16_to_f32(akx), yr = bf16_to_f32(aky);
+        if (rope_k) {
+            const double x = xr, y = yr;
+            xr = x * cs_s[w][lane] - y * sn_s[w][lane];
+            yr = x * sn_s[w][lane] + y * cs_s[w][lane];
         }
+        if (ce >= 0) {
+            a.k[ce + lane] = bf16_of(xr);
+            a.k[ce + lane + kPairs] = bf16_of(yr);
+            a.v[ce + lane] = avx;
+            a.v[ce + lane + kPairs] = avy;
+        }
+    }
+    uint16_t px[3][4], py[3][4];
+#pragma unroll
+    for (int jj = 0; jj < 4; ++jj) {
+#pragma unroll
+        for (int s = 0; s < 3; ++s) {
+            px[s][jj] = split3(qvx[jj], s);
+            py[s][jj] = split3(qvy[jj], s);
+        }
+    }
+    uint4* base = a.q_op + (static_cast<int64_t>(b) * kHkv + kvh) * 12 * kWave + lane;
+#pragma unroll
+    for (int s = 0; s < 3; ++s) {
+        uint2* dx = reinterpret_cast<uint2*>(base + (s * 4 + kbp) * kWave) + (w >> 1);
+        uint2* dy = reinterpret_cast<uint2*>(base + (s * 4 + kbp + 2) * kWave) + (w >> 1);
+        *dx = make_uint2(px[s][0] | (static_cast<uint32_t>(px[s][1]) << 16),
+                         px[s][2] | (static_cast<uint32_t>(px[s][3]) << 16));
+        *dy = make_uint2(py[s][0] | (static_cast<uint32_t>(py[s][1]) << 16),
+                         py[s][2] | (static_cast<uint32_t>(py[s][3]) << 16));
+    }
+    __syncthreads();
+    if (w == 0 && g == 0) {
+        double sc[kMultiMaxNew];
+#pragma unroll
+        for (int u = 0; u < kMultiMaxNew; ++u)
+            sc[u] = ((part_s[0][u][n] + part_s[1][u][n]) + part_s[2][u][n]) + part_s[3][u][n];
+        a.chunk_s[(static_cast<int64_t>(b) * kHkv + kvh) * kMtCols + n] =
+            make_float4(static_cast<float>(sc[0]), static_cast<float>(sc[1]), static_cast<float>(sc[2]),
+                        static_cast<float>(sc[3]));
+    }
 }
 
-// Copies of the window of keys [key0, key0 + 32) of a segment (rows past k_last repeat
-// row k_last) into buffer `buf`, nontemporal (each row is read once): lane l of copy ii
-// writes row 4ii + l/16, chunk position l%16, the chunk it fetches swizzled as in the
-// attention kernel.  The 8 K copies are issued before the 8 V copies, so that the scores
-// can start once K has landed.
-__device__ __forceinline__ void mt_issue_window(const char* kseg, const char* vseg, int64_t row_bytes, int key0,
-                                                int k_last, uint8_t* lds, int buf, int lane) {
+// Copies of one plane (K or V rows of the window of keys [key0, key0 + 32) of a segment;
+// rows past k_last repeat row k_last) into the ring slot at `dst`, nontemporal (each row is
+// read once): lane l of copy ii writes row 4ii + l/16, chunk position l%16, the chunk it
+// fetches swizzled as in the attention kernel.
+__device__ __forceinline__ void mt_issue_plane(const char* seg, int64_t row_bytes, int key0, int k_last,
+                                               uint8_t* dst, int lane) {
     constexpr int kNt = 2;     // cache policy: nontemporal
-    int64_t off[kMtWin / 4];
+    int64_t off[kMtHalf];
 #pragma unroll
-    for (int ii = 0; ii < kMtWin / 4; ++ii) {
+    for (int ii = 0; ii < kMtHalf; ++ii) {
         const int r = 4 * ii + (lane >> 4);
         const int c = (lane & 15) ^ pf_swz(r);
         off[ii] = static_cast<int64_t>(min(key0 + r, k_last)) * row_bytes + 16 * c;
     }
-    uint8_t* d = lds + buf * kMtBufB;
 #pragma unroll
-    for (int ii = 0; ii < kMtWin / 4; ++ii)
-        __builtin_amdgcn_global_load_lds(kseg + off[ii], (lds_void_t*)(d + ii * 1024), 16, 0, kNt);
-#pragma unroll
-    for (int ii = 0; ii < kMtWin / 4; ++ii)
-        __builtin_amdgcn_global_load_lds(vseg + off[ii], (lds_void_t*)(d + kMtPlaneB + ii * 1024), 16, 0, kNt);
+    for (int ii = 0; ii < kMtHalf; ++ii)
+        __builtin_amdgcn_global_load_lds(seg + off[ii], (lds_void_t*)(dst + ii * 1024), 16, 0, kNt);
 }
 
 // Running state of a piece in lane (g, n): O^T[16dt + 4g + i][column n] in fp64, the
@@ -853,14 +963,18 @@ struct MtState {
 
 // One 32-key window [key0, key0 + 32) of a piece ending at k_b: scores, online softmax,
 // V^T P^T.  `lim` = the last key this lane's column may attend to (start + t).  Chunk keys
-// (>= st) add the products of their second and third K parts, read from the workspace.
-template <bool kChunkKeys, bool kNextIssued>
+// (>= st) take the scores the preparation formed from their unrounded rows (`cs`: this
+// lane's column against chunk keys u = 0..3).
+// kAhead = windows after this one whose copies are in flight (0..2): with two, the planes
+// requested after this window's K are its V, K and V of the next window and K of the one
+// after (32 copies), after its V three planes (24); with one, 24 and 16; with none, 8 and 0.
+template <bool kChunkKeys, int kAhead>
 __device__ __forceinline__ void mt_window(const PrefillArgs& a, const uint8_t* kplane, uint32_t vbase,
-                                          const bf16x8_t (&qop)[3][4], int b, int kvh, int st, int key0, int k_b,
+                                          const bf16x8_t (&qop)[3][4], float4 cs, int st, int key0, int k_b,
                                           int lim, int lane, MtState& t) {
-    // This window's K copies have landed (the 8 V copies and, when issued, the next window's
-    // 16 are younger); V is waited for before V^T P^T.
-    __builtin_amdgcn_s_waitcnt(vmcnt_imm(kNextIssued ? kMtCopies + kMtCopies / 2 : kMtCopies / 2));
+    // This window's K copies have landed (the counter retires in issue order; requests of
+    // other kinds issued since -- Q operands, stores -- only make the wait longer).
+    __builtin_amdgcn_s_waitcnt(vmcnt_imm(kMtHalf * (kAhead == 2 ? 4 : kAhead == 1 ? 3 : 1)));
     const int n = lane & 15;
     const int g = lane >> 4;
     f32x4_t sacc[2] = {f32x4_t{0.f, 0.f, 0.f, 0.f}, f32x4_t{0.f, 0.f, 0.f, 0.f}};
@@ -876,24 +990,13 @@ __device__ __forceinline__ void mt_window(const PrefillArgs& a, const uint8_t* k
                 sacc[kt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ak[kt], qop[s][kb], sacc[kt], 0, 0, 0);
     }
     if (kChunkKeys) {
-        const int64_t n_rows = static_cast<int64_t>(a.batch) * a.n_new * kHkv;
 #pragma unroll
-        for (int kt = 0; kt < 2; ++kt) {
-            const int u = key0 + 16 * kt + n - st;     // chunk row of this lane's key
-            const int64_t prow = (u >= 0 && u < a.n_new) ? (static_cast<int64_t>(b) * a.n_new + u) * kHkv + kvh
-                                                          : 2 * n_rows;
-            const int64_t lrow = prow == 2 * n_rows ? prow : n_rows + prow;
-            const uint4* p2 = reinterpret_cast<const uint4*>(a.k_split + prow * kD) + g;
-            const uint4* p3 = reinterpret_cast<const uint4*>(a.k_split + lrow * kD) + g;
+        for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
-            for (int kb = 0; kb < 4; ++kb) {
-                const bf16x8_t k2 = as_bf16x8(p2[4 * kb]);
-                const bf16x8_t k3 = as_bf16x8(p3[4 * kb]);
-                sacc[kt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(k2, qop[0][kb], sacc[kt], 0, 0, 0);
-                sacc[kt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(k2, qop[1][kb], sacc[kt], 0, 0, 0);
-                sacc[kt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(k3, qop[0][kb], sacc[kt], 0, 0, 0);
+            for (int i = 0; i < 4; ++i) {
+                const int u = key0 + 16 * kt + 4 * g + i - st;
+                if (u >= 0 && u < a.n_new) sacc[kt][i] = u == 0 ? cs.x : u == 1 ? cs.y : u == 2 ? cs.z : cs.w;
             }
-        }
     }
     // Mask (keys past the piece or past the column's token), window max per column.
     float bmax = -INFINITY;
@@ -924,7 +1027,7 @@ __device__ __forceinline__ void mt_window(const PrefillArgs& a, const uint8_t* k
     for (int kt = 0; kt < 2; ++kt) pf_probs_tile(sacc[kt], m_eff, lsum, ph, kt);
     t.l64 += static_cast<double>(lsum);
 
-    __builtin_amdgcn_s_waitcnt(vmcnt_imm(kNextIssued ? kMtCopies : 0));
+    __builtin_amdgcn_s_waitcnt(vmcnt_imm(kMtHalf * (kAhead == 2 ? 3 : kAhead == 1 ? 2 : 0)));
     // V^T P^T: dim tile dt from two transposed reads (rows 4g + a/4 and 16 rows on).
     bf16x8_t pb[3];
 #pragma unroll
@@ -1026,6 +1129,39 @@ __device__ __forceinline__ bool mt_next_segment(const PrefillArgs& a, MtWindow& 
     }
 }
 
+// A position in a workgroup's window stream: piece keys [pk, k_b) of segment (b, kvh)
+// (nk keys), current window at key kw, x = stream position of key pk; `sw` is the plan's
+// sequence window around b.  mt_advance moves to the next window of the piece, else to the
+// first window of the next piece, else marks the cursor invalid.
+struct MtCursor {
+    int b, kvh, nk, pk, k_b, kw;
+    int64_t x;
+    bool valid;
+    MtWindow sw;
+};
+
+__device__ __forceinline__ void mt_advance(const PrefillArgs& a, MtCursor& c, int64_t x_end, int lead) {
+    if (c.kw + kMtWin < c.k_b) {
+        c.kw += kMtWin;
+        return;
+    }
+    const int64_t x_next = c.x + (c.k_b - c.pk);
+    int b = c.b, kvh = c.kvh, nk = c.nk;
+    bool more = x_next + lead < x_end;
+    if (more) more = mt_next_segment(a, c.sw, lead, b, kvh, nk);
+    if (!more) {
+        c.valid = false;
+        return;
+    }
+    c.b = __builtin_amdgcn_readfirstlane(b);
+    c.kvh = __builtin_amdgcn_readfirstlane(kvh);
+    c.nk = __builtin_amdgcn_readfirstlane(nk);
+    c.x = uniform_i64(x_next + lead);
+    c.pk = 0;
+    c.kw = 0;
+    c.k_b = __builtin_amdgcn_readfirstlane(static_cast<int>(min(static_cast<int64_t>(c.nk), x_end - c.x)));
+}
+
 __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(1))) void mt_stream_kernel(PrefillArgs a) {
     __shared__ __attribute__((aligned(1024))) uint8_t lds[kMtLdsB];
     MtWindow w0;
@@ -1034,60 +1170,68 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(1))) void
     const int64_t total = a.plan_hdr[0];
     const int64_t per_wg = a.plan_hdr[1];
     const int lead = static_cast<int>(a.plan_hdr[2]);
-    int64_t x = wg * per_wg;
+    const int64_t extra = a.plan_hdr[3];
+    int64_t x = range_start(per_wg, extra, wg);
     if (x >= total) return;
-    const int64_t x_end = min(x + per_wg, total);
+    const int64_t x_end = min(range_start(per_wg, extra, wg + 1), total);
     const int lane = threadIdx.x & (kWave - 1);
     const int n = lane & 15;
     const int64_t row_bytes = a.kv_pos_stride * 2;
     const uint32_t lds_base = static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_void_t*)(lds)));
 
     // First piece: the last sequence b with seq_off[b] <= x.
-    MtWindow sw;
-    int b = 0;
+    MtCursor c;
     int64_t off = 0, next = 0;
+    c.b = 0;
     for (int base = 0; base < a.batch; base += kWave) {
         MtWindow t = w0;
         if (base > 0) mt_load_window(a, base, t);
         const uint64_t le = __ballot(t.o <= x);
         if (le) {
             const int j = 63 - __clzll(static_cast<long long>(le));
-            b = base + j;
+            c.b = base + j;
             off = __shfl(t.o, j);
             next = __shfl(t.o1, j);
-            sw = t;
+            c.sw = t;
         }
     }
     int kvh, key, nk;
     locate_first_piece(off, next, lead, x, kvh, key, nk);
-    x = uniform_i64(x);
-    b = __builtin_amdgcn_readfirstlane(b);
-    kvh = __builtin_amdgcn_readfirstlane(kvh);
-    key = __builtin_amdgcn_readfirstlane(key);
-    nk = __builtin_amdgcn_readfirstlane(nk);
-    int k_b = __builtin_amdgcn_readfirstlane(static_cast<int>(min(static_cast<int64_t>(nk), key + (x_end - x))));
+    c.x = uniform_i64(x);
+    c.b = __builtin_amdgcn_readfirstlane(c.b);
+    c.kvh = __builtin_amdgcn_readfirstlane(kvh);
+    c.pk = __builtin_amdgcn_readfirstlane(key);
+    c.kw = c.pk;
+    c.nk = __builtin_amdgcn_readfirstlane(nk);
+    c.k_b = __builtin_amdgcn_readfirstlane(static_cast<int>(min(static_cast<int64_t>(c.nk), c.pk + (x_end - c.x))));
+    c.valid = true;
 
     auto seg_base = [&](const uint16_t* base, int bb, int hh) {
         return reinterpret_cast<const char*>(base + static_cast<int64_t>(bb) * a.kv_batch_stride +
                                              static_cast<int64_t>(hh) * a.kv_head_stride);
     };
-    // The current window (piece b/kvh, keys [kw, kw + 32) of [key, k_b)) is in buffer
-    // `buf`; its copies were requested before it.
-    int buf = 0;
-    int kw = key;
-    mt_issue_window(seg_base(a.k, b, kvh), seg_base(a.v, b, kvh), row_bytes, kw, k_b - 1, lds, 0, lane);
+    auto slot_ptr = [&](int sl) { return lds + sl * kMtPlaneB; };
+    // The producer p is the last window whose K copies were requested; the consumer c's
+    // window has its K plane in slot `slot` and its V plane in the next one.
+    MtCursor p = c;
+    int slot = 0;
+    mt_issue_plane(seg_base(a.k, p.b, p.kvh), row_bytes, p.kw, p.k_b - 1, slot_ptr(0), lane);
+    mt_issue_plane(seg_base(a.v, p.b, p.kvh), row_bytes, p.kw, p.k_b - 1, slot_ptr(1), lane);
+    mt_advance(a, p, x_end, lead);
+    if (p.valid) mt_issue_plane(seg_base(a.k, p.b, p.kvh), row_bytes, p.kw, p.k_b - 1, slot_ptr(2), lane);
 
     while (true) {
         // This piece: Q operands, start, window loop.
-        const int st = a.start[b];
+        const int st = a.start[c.b];
         bf16x8_t qop[3][4];
         {
-            const uint4* src = a.q_op + (static_cast<int64_t>(b) * kHkv + kvh) * 12 * kWave + lane;
+            const uint4* src = a.q_op + (static_cast<int64_t>(c.b) * kHkv + c.kvh) * 12 * kWave + lane;
 #pragma unroll
             for (int s = 0; s < 3; ++s)
 #pragma unroll
                 for (int kb = 0; kb < 4; ++kb) qop[s][kb] = as_bf16x8(src[(s * 4 + kb) * kWave]);
         }
+        const float4 cs = a.chunk_s[(static_cast<int64_t>(c.b) * kHkv + c.kvh) * kMtCols + n];
         const int lim = st + min(n >> 2, a.n_new - 1);
         MtState t;
 #pragma unroll
@@ -1097,64 +1241,42 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(1))) void
         t.l64 = 0.0;
         t.m_run = -INFINITY;
 
-        // The next piece (its first window's copies are requested during this piece's last).
-        const int64_t x_next = x + (k_b - key);
-        int b2 = b, kvh2 = kvh, nk2 = nk;
-        bool more = x_next + lead < x_end;
-        if (more) {
-            more = mt_next_segment(a, sw, lead, b2, kvh2, nk2);
-            b2 = __builtin_amdgcn_readfirstlane(b2);
-            kvh2 = __builtin_amdgcn_readfirstlane(kvh2);
-            nk2 = __builtin_amdgcn_readfirstlane(nk2);
-        }
-        const int k_b2 = more ? __builtin_amdgcn_readfirstlane(
-                                    static_cast<int>(min(static_cast<int64_t>(nk2), x_end - x_next - lead)))
-                              : 0;
-
-        const char* kseg = seg_base(a.k, b, kvh);
-        const char* vseg = seg_base(a.v, b, kvh);
         for (;;) {
-            // Request the next window (this piece's, else the next piece's first), then wait
-            // for this one's copies.
-            const bool in_piece = kw + kMtWin < k_b;
-            int issued = 0;
-            if (in_piece) {
-                mt_issue_window(kseg, vseg, row_bytes, kw + kMtWin, k_b - 1, lds, buf ^ 1, lane);
-                issued = kMtCopies;
-            } else if (more) {
-                mt_issue_window(seg_base(a.k, b2, kvh2), seg_base(a.v, b2, kvh2), row_bytes, 0, k_b2 - 1, lds,
-                                buf ^ 1, lane);
-                issued = kMtCopies;
+            // Request V of the producer's window (the consumer's next) and K of the window
+            // after it, then compute this one.
+            int ahead = 0;
+            if (p.valid) {
+                const int sv = slot + 3 >= kMtSlots ? slot + 3 - kMtSlots : slot + 3;
+                mt_issue_plane(seg_base(a.v, p.b, p.kvh), row_bytes, p.kw, p.k_b - 1, slot_ptr(sv), lane);
+                ahead = 1;
+                mt_advance(a, p, x_end, lead);
+                if (p.valid) {
+                    const int sk = slot + 4 >= kMtSlots ? slot + 4 - kMtSlots : slot + 4;
+                    mt_issue_plane(seg_base(a.k, p.b, p.kvh), row_bytes, p.kw, p.k_b - 1, slot_ptr(sk), lane);
+                    ahead = 2;
+                }
             }
-            // mt_window waits for this window's copies (the counter retires in issue order, so
-            // older requests -- the piece's Q operands, earlier stores -- are waited for too).
-            const uint8_t* kplane = lds + buf * kMtBufB;
-            const uint32_t vbase = lds_base + buf * kMtBufB + kMtPlaneB;
-            const bool chunk_keys = kw + kMtWin > st;
-            if (issued) {
-                if (chunk_keys)
-                    mt_window<true, true>(a, kplane, vbase, qop, b, kvh, st, kw, k_b, lim, lane, t);
-                else
-                    mt_window<false, true>(a, kplane, vbase, qop, b, kvh, st, kw, k_b, lim, lane, t);
+            const int slot_v = slot + 1 >= kMtSlots ? 0 : slot + 1;
+            const uint8_t* kplane = slot_ptr(slot);
+            const uint32_t vbase = lds_base + slot_v * kMtPlaneB;
+            const bool chunk_keys = c.kw + kMtWin > st;
+#define MT_WINDOW(ck, ah) mt_window<ck, ah>(a, kplane, vbase, qop, cs, st, c.kw, c.k_b, lim, lane, t)
+            if (ahead == 2) {
+                if (chunk_keys) MT_WINDOW(true, 2); else MT_WINDOW(false, 2);
+            } else if (ahead == 1) {
+                if (chunk_keys) MT_WINDOW(true, 1); else MT_WINDOW(false, 1);
             } else {
-                if (chunk_keys)
-                    mt_window<true, false>(a, kplane, vbase, qop, b, kvh, st, kw, k_b, lim, lane, t);
-                else
-                    mt_window<false, false>(a, kplane, vbase, qop, b, kvh, st, kw, k_b, lim, lane, t);
+                if (chunk_keys) MT_WINDOW(true, 0); else MT_WINDOW(false, 0);
             }
-            buf ^= 1;
-            if (!in_piece) break;
-            kw += kMtWin;
+#undef MT_WINDOW
+            slot = slot + 2 >= kMtSlots ? slot + 2 - kMtSlots : slot + 2;
+            if (c.kw + kMtWin >= c.k_b) break;
+            c.kw += kMtWin;
         }
-        mt_piece_end(a, b, kvh, key == 0 && k_b == nk, wg + static_cast<int64_t>(b) * kHkv + kvh, lane, t);
-        if (!more) break;
-        x = x_next + lead;
-        b = b2;
-        kvh = kvh2;
-        nk = nk2;
-        key = 0;
-        k_b = k_b2;
-        kw = 0;
+        mt_piece_end(a, c.b, c.kvh, c.pk == 0 && c.k_b == c.nk, wg + static_cast<int64_t>(c.b) * kHkv + c.kvh, lane,
+                     t);
+        mt_advance(a, c, x_end, lead);
+        if (!c.valid) break;
     }
 }
 
@@ -1166,13 +1288,14 @@ __global__ __launch_bounds__(256) void mt_merge_kernel(PrefillArgs a) {
     const int b = blockIdx.y;
     const int64_t per_wg = a.plan_hdr[1];
     const int lead = static_cast<int>(a.plan_hdr[2]);
+    const int64_t extra = a.plan_hdr[3];
     const int64_t off = a.seq_off[b];
     const int span = static_cast<int>((a.seq_off[b + 1] - off) / kHkv);
     if (span == 0) return;
     const int nk = span - lead;
     const int64_t seg_off = off + static_cast<int64_t>(kvh) * span + lead;
-    const int64_t w_first = seg_off / per_wg;
-    const int n_pieces = static_cast<int>((seg_off + nk - 1) / per_wg - w_first) + 1;
+    const int64_t w_first = range_of(per_wg, extra, seg_off);
+    const int n_pieces = static_cast<int>(range_of(per_wg, extra, seg_off + nk - 1) - w_first) + 1;
     if (n_pieces == 1) return;
     const int64_t slot0 = w_first + static_cast<int64_t>(b) * kHkv + kvh;
     const int col = threadIdx.x >> 4;
@@ -1194,17 +1317,19 @@ __global__ __launch_bounds__(256) void mt_merge_kernel(PrefillArgs a) {
     uint16_t h8[8];
 #pragma unroll
     for (int j = 0; j < 8; ++j) h8[j] = f32_to_bf16_rne(static_cast<float>(o[j] / l));
-    uint4 pk;
-    pk.x = h8[0] | (static_cast<uint32_t>(h8[1]) << 16);
-    pk.y = h8[2] | (static_cast<uint32_t>(h8[3]) << 16);
-    pk.z = h8[4] | (static_cast<uint32_t>(h8[5]) << 16);
-    pk.w = h8[6] | (static_cast<uint32_t>(h8[7]) << 16);
-    *reinterpret_cast<uint4*>(a.out + ((static_cast<int64_t>(b) * a.n_new + tok) * kHq + kvh * kGroup + (col & 3)) * kD +
-                              d0) = pk;
+    uint2* dst = reinterpret_cast<uint2*>(a.out + ((static_cast<int64_t>(b) * a.n_new + tok) * kHq + kvh * kGroup +
+                                                   (col & 3)) * kD + d0);   // out is 8-byte aligned
+    dst[0] = make_uint2(h8[0] | (static_cast<uint32_t>(h8[1]) << 16), h8[2] | (static_cast<uint32_t>(h8[3]) << 16));
+    dst[1] = make_uint2(h8[4] | (static_cast<uint32_t>(h8[5]) << 16), h8[6] | (static_cast<uint32_t>(h8[7]) << 16));
 }
 
 hipError_t launch_prefill_multi(const PrefillArgs& a, hipStream_t stream, hipEvent_t* ev) {
-    hipLaunchKernelGGL(mt_prepare_kernel, dim3(kHkv, static_cast<unsigned>(a.batch) + 1), dim3(kWave), 0, stream, a);
+    const bool vec = (reinterpret_cast<uintptr_t>(a.q) % 16) == 0 && (reinterpret_cast<uintptr_t>(a.k_new) % 16) == 0;
+    const dim3 grid(kHkv, static_cast<unsigned>(a.batch) + 1);
+    if (vec)
+        hipLaunchKernelGGL(mt_prepare_kernel<true>, grid, dim3(4 * kWave), 0, stream, a);
+    else
+        hipLaunchKernelGGL(mt_prepare_kernel<false>, grid, dim3(4 * kWave), 0, stream, a);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     if (ev) (void)hipEventRecord(ev[1], stream);

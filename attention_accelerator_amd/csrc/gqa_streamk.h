@@ -70,6 +70,27 @@ __device__ __forceinline__ void locate_first_piece(int64_t off, int64_t next, in
     x = off + static_cast<int64_t>(k) * span + lead + key;
 }
 
+// XCD-weighted ranges.  Workgroups are dealt round-robin over the 8 XCDs (block w runs
+// on XCD w % 8), and on MI355X a streaming wave on an odd XCD reads about 7 % slower than
+// one on an even XCD (the same ranges swapped between neighbours: the slowness stays with
+// the XCD).  Each pair of blocks (2j, 2j+1) covers 2 * per positions, the even block
+// per + extra of them, the odd one per - extra.
+__device__ __forceinline__ int64_t range_start(int64_t per, int64_t extra, int64_t w) {
+    return (w >> 1) * 2 * per + ((w & 1) ? per + extra : 0);
+}
+
+// The range holding stream position x.
+__device__ __forceinline__ int64_t range_of(int64_t per, int64_t extra, int64_t x) {
+    const int64_t j = x / (2 * per);
+    return 2 * j + (x - 2 * j * per >= per + extra ? 1 : 0);
+}
+
+// Positions moved from each odd range to its even neighbour: skew_pm per mille of a
+// range, whole 16-key chunks.
+__device__ __forceinline__ int64_t range_extra(int64_t per, int skew_pm) {
+    return per * skew_pm / 1000 / kRangeAlign * kRangeAlign;
+}
+
 // Range size for `total` stream positions over n_wgs workgroups.
 __device__ __forceinline__ int64_t range_size(int64_t total, int n_wgs) {
     int64_t per = (total + n_wgs - 1) / n_wgs;

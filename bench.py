@@ -305,8 +305,8 @@ def bench_multitoken(args, torch, gqa, dev, stimulus) -> int:
         achieved = step_bytes / (attn_ms * 1e-3) / 1e9
         roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
-                    "kernel": "prefill_attn_kernel", "kernel_us": round(attn_ms * 1e3, 2),
-                    "append_us": round(append_ms * 1e3, 2), "bytes_per_launch": step_bytes}
+                    "kernel": "mt_stream_kernel", "kernel_us": round(attn_ms * 1e3, 2),
+                    "append_prepare_us": round(append_ms * 1e3, 2), "bytes_per_launch": step_bytes}
     result = {
         "metric": "GQA multi-token decode µs/step + achieved HBM GB/s, B=64 ragged ctx 512–8192, 4 new tokens",
         "value": round(step_bytes / (ms_per_step * 1e-3) / 1e9, 1),

@@ -170,3 +170,37 @@ def test_multi_workspace_garbage_and_repeat(dev):
         got = to_codes(call())
         torch.cuda.synchronize()
         assert np.array_equal(got, a)
+
+
+def test_multi_two_byte_aligned_inputs(dev):
+    """Q and the new K/V rows at 2-byte (not 16-byte) aligned addresses take the preparation
+    kernel's element-wise loads: the same bits as aligned inputs."""
+    starts = [300, 9]
+    q, kn, vn, k, v = _chunk(starts, 3, 320, 48)
+    want, _, _ = _run(q, kn, vn, k, v, starts, dev)
+
+    def shifted(x):
+        flat = torch.empty(x.numel() + 1, dtype=x.dtype, device=dev)
+        view = flat[1:].view(x.shape)
+        view.copy_(x.to(dev))
+        return view
+
+    qs, kns, vns = shifted(q), shifted(kn), shifted(vn)
+    assert qs.data_ptr() % 16 != 0 and kns.data_ptr() % 16 != 0
+    kd, vd = k.to(dev), v.to(dev)
+    got = to_codes(gqa.gqa_prefill(qs, kns, vns, kd, vd, starts))
+    torch.cuda.synchronize()
+    assert np.array_equal(got, want)
+
+
+@pytest.mark.parametrize("skew", ["0", "250"])
+def test_multi_xcd_skew_bounds(dev, monkeypatch, skew):
+    """Equal ranges (skew 0) and the largest XCD weighting (odd ranges 3/4 of the size, even
+    ones 5/4) over a short and a long batch: every row within the tolerance of the oracle."""
+    monkeypatch.setenv("GQA_XCD_SKEW", skew)
+    monkeypatch.setenv("GQA_STREAM_WGS", "96")
+    starts = [5, 1200, 64, 2999, 0, 17, 640]
+    q, kn, vn, k, v = _chunk(starts, 4, 3010, 49)
+    want = _oracle(q, kn, vn, k, v, starts)
+    got, _, _ = _run(q, kn, vn, k, v, starts, dev)
+    assert_within_ulp(want.reshape(-1, 128), got.reshape(-1, 128), 64, f"multi skew={skew}")
