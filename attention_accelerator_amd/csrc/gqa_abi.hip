@@ -95,6 +95,13 @@ int32_t xcd_skew_pm() {
     return 40;
 }
 
+// Workgroups of the multi-token stream kernel: one wave per SIMD, multi_waves(n_new) waves
+// per workgroup.
+int32_t multi_wgs(int32_t n_new) {
+    const int32_t w = stream_wgs() / multi_waves(n_new);
+    return w > 0 ? w : 1;
+}
+
 bool geometry_ok(const gqa_params_t* p) {
     if (p->n_q_heads != kHq || p->n_kv_heads != kHkv || p->head_dim != kD) return false;
     if (!(p->scale != 0.f) || !std::isfinite(p->scale)) return false;
@@ -435,7 +442,7 @@ size_t gqa_prefill_workspace_bytes(const gqa_params_t* params, int32_t batch, in
     if (!params || !geometry_ok(params) || batch <= 0 || n_new <= 0) return 0;
     // The multi-token path needs no split planes: the chunk's unrounded keys enter through
     // the scores its preparation kernel forms.
-    if (use_multi(n_new)) return prefill_multi_bytes(batch, stream_wgs());
+    if (use_multi(n_new)) return prefill_multi_bytes(batch, n_new, multi_wgs(n_new));
     return align_up(prefill_split_bytes(batch, n_new), 256);
 }
 
@@ -486,7 +493,7 @@ int gqa_prefill_bf16(const gqa_params_t* params, const uint16_t* q, const uint16
     const bool multi = use_multi(n_new);
     if (multi) {
         a.k_split = nullptr;
-        prefill_multi_layout(a, workspace, stream_wgs());
+        prefill_multi_layout(a, workspace, multi_wgs(n_new));
         a.skew_pm = xcd_skew_pm();
     } else {
         a.k_split = static_cast<uint16_t*>(workspace);

@@ -106,24 +106,27 @@ struct PrefillArgs {
     double qk_scale_log2;     // scale * log2(e), folded into Q
     uint32_t flags;           // bit0 RoPE on Q, bit1 RoPE on the new K rows
     RopeTable rope;
-    // Multi-token path (n_new <= kMultiMaxNew): the stream-K split of the decode path.
-    uint4* q_op;              // [B][8][3][4][64] Q operands (3 BF16 parts, MFMA B layout)
+    // Multi-token path (n_new <= kMultiMaxNew): the stream-K split of the decode path, W =
+    // multi_waves(n_new) column tiles of 16 (4 heads x 4 tokens) per segment.
+    uint4* q_op;              // [B][8][W][3][4][64] Q operands (3 BF16 parts, MFMA B layout)
     int64_t* plan_hdr;        // {total stream positions, positions per workgroup, segment lead,
                               //  positions moved from odd to even ranges}
     int64_t* seq_off;         // [B+1] stream position of sequence b's first segment
-    double* part_o;           // [n_slots][16][128] unnormalised partial outputs (column 4t + h)
-    float2* part_ml;          // [n_slots][16] (integer-valued running max in log2 units, sum)
-    float4* chunk_s;          // [B][8][16] scores of the chunk's keys u = 0..3 per column (log2 units)
+    double* part_o;           // [n_slots][16W][128] unnormalised partial outputs (column 16w + 4t + h)
+    float2* part_ml;          // [n_slots][16W] (integer-valued running max in log2 units, sum)
+    float* chunk_s;           // [B][8][16W][4W] scores of the chunk's keys u per column (log2 units)
     int32_t n_wgs;            // persistent workgroups of the multi-token stream kernel
     int32_t skew_pm;          // XCD weighting of the ranges (per mille of a range)
 };
 
 // Chunks of at most this many new tokens per sequence take the multi-token path.
-constexpr int32_t kMultiMaxNew = 4;
+constexpr int32_t kMultiMaxNew = 8;
+// Waves per workgroup (16-column tiles) of the multi-token path for T new tokens: 1 or 2.
+int32_t multi_waves(int32_t n_new);
 
 size_t prefill_split_bytes(int32_t batch, int32_t n_new);
-// Workspace of the multi-token path after the split planes: Q operands, plan, partials.
-size_t prefill_multi_bytes(int32_t batch, int32_t n_wgs);
+// Workspace of the multi-token path: Q operands, plan, partials, chunk-key scores.
+size_t prefill_multi_bytes(int32_t batch, int32_t n_new, int32_t n_wgs);
 void prefill_multi_layout(PrefillArgs& a, void* base, int32_t n_wgs);
 hipError_t launch_kv_append(const PrefillArgs& a, hipStream_t stream);
 hipError_t launch_prefill_attention(const PrefillArgs& a, hipStream_t stream);

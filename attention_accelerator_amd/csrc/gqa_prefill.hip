@@ -655,38 +655,67 @@ hipError_t launch_prefill_attention(const PrefillArgs& a, hipStream_t stream) {
 
 
 // ---------------------------------------------------------------------------------
-// Multi-token decode: chunks of at most kMultiMaxNew (4) new tokens per sequence -- drafted
-// tokens being verified, or decode steps that append their own K/V.  The attention kernel
-// above gives each (sequence, KV head, 32 positions) one workgroup over all of that
+// Multi-token decode: chunks of at most kMultiMaxNew (8) new tokens per sequence --
+// drafted tokens being verified, or decode steps that append their own K/V.  The attention
+// kernel above gives each (sequence, KV head, 32 positions) one workgroup over all of that
 // sequence's keys, which for a short chunk leaves most of its MFMA columns empty and a
-// ragged batch waiting for its longest sequence.  Here the 16 query rows of a KV head's
-// group -- 4 heads x up to 4 tokens, column n = 4t + h -- form one MFMA B operand, and the
-// keys are split stream-K over n_wgs one-wave workgroups as in the decode path: every
-// segment (sequence, KV head) holds start + T keys, a range's part of a segment is a
-// piece, a split segment's pieces leave partials that mt_merge_kernel combines.  The
-// arithmetic is the attention kernel's: three BF16 parts of Q, the chunk's own keys
-// carried to ~24 bits, P in three parts, fp64 accumulation, integer-valued running max.
+// ragged batch waiting for its longest sequence.  Here the query rows of a KV head's group
+// form MFMA B operands of 16 columns -- tile w holds tokens 4w .. 4w+3 of the 4 heads,
+// column 16w + n for token 4w + n/4 and head n%4 -- and the keys are split stream-K as in
+// the decode path: every segment (sequence, KV head) holds start + T keys, a range's part
+// of a segment is a piece, a split segment's pieces leave partials that mt_merge_kernel
+// combines.  The arithmetic is the attention kernel's: three BF16 parts of Q, the chunk's
+// own keys at full precision, P in three parts, fp64 accumulation within a piece,
+// integer-valued running max.
 //
-// Per 32-key window a wave copies the window's K rows and V rows (a plane of 8 KB each)
-// into its own LDS, forms the scores of both 16-key tiles, and adds V^T P^T with the
-// transposed V reads of the attention kernel.  The planes form a ring of five slots in the
-// order K0 V0 K1 V1 K2 ...: while window i is computed, K of windows i+1 and i+2 and V of
-// window i+1 are in flight (24 KB per wave; the HBM latency under full load is about two
-// and a half window periods, so two windows in flight leave the wave waiting).  No
-// barrier: the workgroup is one wave.  Five slots are 40 KB: the four workgroups of a CU
-// fill its 160 KB of LDS.
+// A workgroup has one wave per column tile (W = 1 or 2 waves for T <= 4 or 8) and there
+// are 4 * CUs / W of them: one wave per SIMD.  Per 32-key window the workgroup copies
+// the window's K rows and V rows (a plane of 8 KB each) from HBM into LDS once -- each wave
+// issues 8/W of the plane's 1 KB copies -- and every wave forms its tile's scores and
+// V^T P^T from them.  The planes form a ring in the order K0 V0 K1 V1 ...: while window i
+// is computed, K of windows i+1 .. i+A+1 and V of windows i+1 .. i+A are in flight.  A = 1
+// for W = 1 and 3 for W = 2 keeps 12 to 14 planes in flight per CU (2A + 3 slots: 40 or 72 KB
+// per workgroup).  Longer chunks are compute-bound here -- every window costs each wave
+// about 2,000 cycles of MFMA and fp64 work for its 16 columns, and T = 16 on four waves
+// measured slower than the prefill attention kernel -- so they take that kernel.  Each wave waits for its own copies, then a fence-free
+// barrier makes the whole plane visible: once after K lands (which also tells every wave
+// that V of the previous window has been read, so its slot may be refilled) and once after
+// V lands.
 
 constexpr int kMtWin = 32;                    // keys per window
 constexpr int kMtPlaneB = kMtWin * kRowB;     // 8 KB: 32 rows of 256 B
-constexpr int kMtSlots = 5;                   // ring slots, one plane each
-constexpr int kMtLdsB = kMtSlots * kMtPlaneB; // 40 KB per workgroup
-constexpr int kMtCols = 16;                   // query rows per segment: 4 heads x 4 tokens
-constexpr int kMtHalf = kMtWin / 4;           // copy instructions per plane per lane (1 KB each)
+constexpr int kMtTile = 16;                   // query rows per wave: 4 heads x 4 tokens
+constexpr int kMtCopies = kMtWin / 4;         // 1 KB copies per plane (each writes 4 rows)
+
+__host__ __device__ constexpr int mt_ahead(int w) { return w == 1 ? 1 : 3; }
+__host__ __device__ constexpr int mt_slots(int w) { return 2 * mt_ahead(w) + 3; }
 
 // s_waitcnt immediate for vmcnt(n) alone (gfx9: vmcnt bits 3:0 and 15:14, expcnt and
 // lgkmcnt at their maxima).
 constexpr int vmcnt_imm(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
 static_assert(vmcnt_imm(0) == 0x0F70 && vmcnt_imm(16) == 0x4F70, "vmcnt encoding");
+
+// Wait until at most `planes` planes of this wave's copies (kC instructions each) are in
+// flight: the counter retires in issue order, so everything older has landed.  Requests
+// of other kinds issued since (Q operands, stores) only make the wait longer.
+template <int kC>
+__device__ __forceinline__ void mt_wait_planes(int planes) {
+    switch (planes) {
+#define MT_CASE(k) \
+    case k: __builtin_amdgcn_s_waitcnt(vmcnt_imm(k * kC < 63 ? k * kC : 63)); break;
+        MT_CASE(1) MT_CASE(2) MT_CASE(3) MT_CASE(4) MT_CASE(5) MT_CASE(6) MT_CASE(7) MT_CASE(8) MT_CASE(9)
+        MT_CASE(10) MT_CASE(11)
+#undef MT_CASE
+        default: __builtin_amdgcn_s_waitcnt(vmcnt_imm(0)); break;
+    }
+}
+static_assert(7 * (kMtCopies / 2) <= 63 && 3 * kMtCopies <= 63, "vmcnt range");
+
+// Barrier without the memory fence __syncthreads adds (which would wait for every copy in
+// flight).
+__device__ __forceinline__ void mt_barrier() { asm volatile("s_barrier" ::: "memory"); }
+
+int32_t multi_waves(int32_t n_new) { return n_new <= 4 ? 1 : 2; }
 
 // Keys of sequence b's segments: every key its last new token sees (0 for a start outside
 // [0, capacity - T]).
@@ -695,34 +724,47 @@ __device__ __forceinline__ int mt_keys(const PrefillArgs& a, int b) {
     return prefill_start_ok(a, st) ? st + a.n_new : 0;
 }
 
-size_t prefill_multi_bytes(int32_t batch, int32_t n_wgs) {
+namespace {
+struct MtLayout {
+    size_t q_op, plan, seq_off, part_o, part_ml, chunk_s, total;
+};
+
+MtLayout mt_layout(int32_t batch, int32_t n_new, int32_t n_wgs) {
+    const size_t w = static_cast<size_t>(multi_waves(n_new));
+    const size_t cols = kMtTile * w;
     const size_t n_slots = static_cast<size_t>(n_wgs) + static_cast<size_t>(kHkv) * batch;
     auto al = [](size_t x) { return (x + 255) / 256 * 256; };
-    return al(static_cast<size_t>(batch) * kHkv * 12 * kWave * sizeof(uint4)) + 256 +
-           al((static_cast<size_t>(batch) + 1) * sizeof(int64_t)) + al(n_slots * kMtCols * kD * sizeof(double)) +
-           al(n_slots * kMtCols * sizeof(float2)) + al(static_cast<size_t>(batch) * kHkv * kMtCols * sizeof(float4));
+    MtLayout l{};
+    l.q_op = 0;
+    l.plan = l.q_op + al(static_cast<size_t>(batch) * kHkv * w * 12 * kWave * sizeof(uint4));
+    l.seq_off = l.plan + 256;
+    l.part_o = l.seq_off + al((static_cast<size_t>(batch) + 1) * sizeof(int64_t));
+    l.part_ml = l.part_o + al(n_slots * cols * kD * sizeof(double));
+    l.chunk_s = l.part_ml + al(n_slots * cols * sizeof(float2));
+    l.total = l.chunk_s + al(static_cast<size_t>(batch) * kHkv * cols * 4 * w * sizeof(float));
+    return l;
+}
+}  // namespace
+
+size_t prefill_multi_bytes(int32_t batch, int32_t n_new, int32_t n_wgs) {
+    return mt_layout(batch, n_new, n_wgs).total;
 }
 
 void prefill_multi_layout(PrefillArgs& a, void* base, int32_t n_wgs) {
-    const size_t n_slots = static_cast<size_t>(n_wgs) + static_cast<size_t>(kHkv) * a.batch;
-    auto al = [](size_t x) { return (x + 255) / 256 * 256; };
+    const MtLayout l = mt_layout(a.batch, a.n_new, n_wgs);
     char* p = static_cast<char*>(base);
-    a.q_op = reinterpret_cast<uint4*>(p);
-    p += al(static_cast<size_t>(a.batch) * kHkv * 12 * kWave * sizeof(uint4));
-    a.plan_hdr = reinterpret_cast<int64_t*>(p);
-    p += 256;
-    a.seq_off = reinterpret_cast<int64_t*>(p);
-    p += al((static_cast<size_t>(a.batch) + 1) * sizeof(int64_t));
-    a.part_o = reinterpret_cast<double*>(p);
-    p += al(n_slots * kMtCols * kD * sizeof(double));
-    a.part_ml = reinterpret_cast<float2*>(p);
-    p += al(n_slots * kMtCols * sizeof(float2));
-    a.chunk_s = reinterpret_cast<float4*>(p);
+    a.q_op = reinterpret_cast<uint4*>(p + l.q_op);
+    a.plan_hdr = reinterpret_cast<int64_t*>(p + l.plan);
+    a.seq_off = reinterpret_cast<int64_t*>(p + l.seq_off);
+    a.part_o = reinterpret_cast<double*>(p + l.part_o);
+    a.part_ml = reinterpret_cast<float2*>(p + l.part_ml);
+    a.chunk_s = reinterpret_cast<float*>(p + l.chunk_s);
     a.n_wgs = n_wgs;
 }
 
 // The stream-K plan (one wave): seq_off[b] = stream position of sequence b's first segment,
-// seq_off[B] = total, header {total, positions per workgroup, lead} (gqa_streamk.h).
+// seq_off[B] = total, header {total, positions per workgroup, lead, XCD extra}
+// (gqa_streamk.h).
 __device__ __forceinline__ void mt_build_plan(const PrefillArgs& a, int lane) {
     int64_t sum = 0;
     int max_keys = 0, n_seq = 0;
@@ -772,22 +814,25 @@ __device__ __forceinline__ void load4(const uint16_t* p, uint16_t (&h)[4]) {
 }
 
 // Per (sequence b, KV head kvh), four waves; wave w:
-//  - the KV append of new row u = w of this head (what kv_append_kernel does for all
-//    heads): lane i rotates the pair (i, i + 64) at position start + w in double and
-//    writes it rounded to BF16, and copies the V row;
-//  - a quarter of the Q operands: lane (g, n) holds column n = 4t + h (token t, Q head
-//    4*kvh + h) at dims 32kb + 8g + j; wave w takes kb = w & 1 and its pair kb + 2, j in
-//    [4(w >> 1), +4), rotated at position start + t and scaled by scale*log2(e) in
-//    double, split into three BF16 parts; columns of tokens t >= T are zero;
+//  - the KV append of this head's new rows u = w, w + 4, ... (what kv_append_kernel does
+//    for all heads): lane i rotates the pair (i, i + 64) at position start + u in double
+//    and writes it rounded to BF16, and copies the V row;
+//  - a quarter of the Q operands of every column tile: lane (g, n) of tile tau holds
+//    column 16 tau + n (token 4 tau + n/4, Q head 4*kvh + n%4) at dims 32kb + 8g + j; wave
+//    w takes kb = w & 1 and its pair kb + 2, j in [4(w >> 1), +4), rotated at the token's
+//    position and scaled by scale*log2(e) in double, split into three BF16 parts; columns
+//    of tokens t >= T are zero;
 //  - the same dims' share of the scores of the chunk's own keys (key start + u, u < T:
 //    the new K row rotated at its position and not rounded, as the reference rotates K)
-//    against every column, in double.  Wave 0 adds the four shares in a fixed order and
-//    rounds once to f32: the stream kernel takes these scores in place of the ones it
+//    against every column, in double.  The four shares are added in a fixed order and
+//    rounded once to f32: the stream kernel takes these scores in place of the ones it
 //    would form from the cache's rounded copy of those rows.
 // Row B of the grid builds the plan.  A sequence whose start is out of range gets NaN
 // rows and no cache write.
-template <bool kVec>
+template <bool kVec, int kW>
 __global__ __launch_bounds__(256) void mt_prepare_kernel(PrefillArgs a) {
+    constexpr int kCols = kMtTile * kW;
+    constexpr int kU = 4 * kW;                // chunk keys per column held (>= T)
     const int kvh = blockIdx.x;
     const int b = blockIdx.y;
     const int w = threadIdx.x >> 6;
@@ -798,35 +843,32 @@ __global__ __launch_bounds__(256) void mt_prepare_kernel(PrefillArgs a) {
     }
     const int T = a.n_new;
     const int st = a.start[b];
-    // Every load first (the stores below may alias them as far as the compiler knows, so a
-    // load placed after a store would wait for it).
+    // Loads of the append rows and of Q before any store (a store may alias them as far as
+    // the compiler knows, and a load placed after it would wait for it).
     const int g = lane >> 4;
     const int n = lane & 15;
-    const int t = n >> 2;
-    const bool col = t < T;
-    const int tc = col ? t : T - 1;
     const int kbp = w & 1;
     const int d0 = 32 * kbp + 8 * g + 4 * (w >> 1);
-    uint16_t akx = 0, aky = 0, avx = 0, avy = 0;
-    if (w < T) {
-        const int64_t row = ((static_cast<int64_t>(b) * T + w) * kHkv + kvh) * kD;
-        akx = a.k_new[row + lane];
-        aky = a.k_new[row + lane + kPairs];
-        avx = a.v_new[row + lane];
-        avy = a.v_new[row + lane + kPairs];
-    }
-    const uint16_t* qrow = a.q + ((static_cast<int64_t>(b) * T + tc) * kHq + kvh * kGroup + (n & 3)) * kD;
-    uint16_t qx[4], qy[4];
-    load4<kVec>(qrow + d0, qx);
-    load4<kVec>(qrow + d0 + kPairs, qy);
-    uint16_t kx[kMultiMaxNew][4], ky[kMultiMaxNew][4];
+    uint16_t akx[kW], aky[kW], avx[kW], avy[kW];
 #pragma unroll
-    for (int u = 0; u < kMultiMaxNew; ++u) {
+    for (int r = 0; r < kW; ++r) {
+        const int u = w + 4 * r;
+        akx[r] = aky[r] = avx[r] = avy[r] = 0;
         if (u < T) {
-            const uint16_t* krow = a.k_new + ((static_cast<int64_t>(b) * T + u) * kHkv + kvh) * kD;
-            load4<kVec>(krow + d0, kx[u]);
-            load4<kVec>(krow + d0 + kPairs, ky[u]);
+            const int64_t row = ((static_cast<int64_t>(b) * T + u) * kHkv + kvh) * kD;
+            akx[r] = a.k_new[row + lane];
+            aky[r] = a.k_new[row + lane + kPairs];
+            avx[r] = a.v_new[row + lane];
+            avy[r] = a.v_new[row + lane + kPairs];
         }
+    }
+    uint16_t qx[kW][4], qy[kW][4];
+#pragma unroll
+    for (int tau = 0; tau < kW; ++tau) {
+        const int tc = min(4 * tau + (n >> 2), T - 1);
+        const uint16_t* qrow = a.q + ((static_cast<int64_t>(b) * T + tc) * kHq + kvh * kGroup + (n & 3)) * kD;
+        load4<kVec>(qrow + d0, qx[tau]);
+        load4<kVec>(qrow + d0 + kPairs, qy[tau]);
     }
     if (!prefill_start_ok(a, st)) {
         for (int i = threadIdx.x; i < T * kGroup * (kD / 4); i += blockDim.x) {
@@ -837,119 +879,137 @@ __global__ __launch_bounds__(256) void mt_prepare_kernel(PrefillArgs a) {
         }
         return;
     }
-    // sin and cos of (start + u) * inv_freq[i]: wave u, lane i.
-    __shared__ double sn_s[kMultiMaxNew][kPairs], cs_s[kMultiMaxNew][kPairs];
-    __shared__ double part_s[4][kMultiMaxNew][kMtCols];
+    // sin and cos of (start + u) * inv_freq[i]: wave u % 4, lane i.
+    __shared__ double sn_s[kU][kPairs], cs_s[kU][kPairs];
+    __shared__ double part_s[4][kU][kCols];
     const bool rope_q = (a.flags & 1u) != 0;
     const bool rope_k = (a.flags & 2u) != 0;
-    if ((rope_q || rope_k) && w < T)
-        rope_sincos(static_cast<int64_t>(st) + w, a.rope.inv_freq[lane], sn_s[w][lane], cs_s[w][lane]);
+    if (rope_q || rope_k)
+        for (int u = w; u < T; u += 4)
+            rope_sincos(static_cast<int64_t>(st) + u, a.rope.inv_freq[lane], sn_s[u][lane], cs_s[u][lane]);
     __syncthreads();
 
-    double qvx[4], qvy[4];
+    double qvx[kW][4], qvy[kW][4];
 #pragma unroll
-    for (int jj = 0; jj < 4; ++jj) {
-        const int d = d0 + jj;
-        const double x = bf16_to_f32(qx[jj]);
-        const double y = bf16_to_f32(qy[jj]);
-        double xr = x, yr = y;
-        if (rope_q) {
-            const double sn = sn_s[tc][d], cs = cs_s[tc][d];
-            xr = x * cs - y * sn;
-            yr = x * sn + y * cs;
+    for (int tau = 0; tau < kW; ++tau) {
+        const int t = 4 * tau + (n >> 2);
+        const bool col = t < T;
+        const int tc = col ? t : T - 1;
+#pragma unroll
+        for (int jj = 0; jj < 4; ++jj) {
+            const int d = d0 + jj;
+            const double x = bf16_to_f32(qx[tau][jj]);
+            const double y = bf16_to_f32(qy[tau][jj]);
+            double xr = x, yr = y;
+            if (rope_q) {
+                const double sn = sn_s[tc][d], cs = cs_s[tc][d];
+                xr = x * cs - y * sn;
+                yr = x * sn + y * cs;
+            }
+            qvx[tau][jj] = col ? xr * a.qk_scale_log2 : 0.0;
+            qvy[tau][jj] = col ? yr * a.qk_scale_log2 : 0.0;
         }
-        qvx[jj] = col ? xr * a.qk_scale_log2 : 0.0;
-        qvy[jj] = col ? yr * a.qk_scale_log2 : 0.0;
     }
-    // This wave's share of the chunk-key scores, summed over the four lanes of column n.
-#pragma unroll
-    for (int u = 0; u < kMultiMaxNew; ++u) {
-        double acc = 0.0;
+    // This wave's share of the chunk-key scores, summed over the four lanes of each column.
+    for (int u = 0; u < kU; ++u) {
+        double kxr[4] = {0.0, 0.0, 0.0, 0.0}, kyr[4] = {0.0, 0.0, 0.0, 0.0};
         if (u < T) {
+            const uint16_t* krow = a.k_new + ((static_cast<int64_t>(b) * T + u) * kHkv + kvh) * kD;
+            uint16_t hx[4], hy[4];
+            load4<kVec>(krow + d0, hx);
+            load4<kVec>(krow + d0 + kPairs, hy);
 #pragma unroll
             for (int jj = 0; jj < 4; ++jj) {
-                const int d = d0 + jj;
-                const double x = bf16_to_f32(kx[u][jj]);
-                const double y = bf16_to_f32(ky[u][jj]);
-                double xr = x, yr = y;
+                const double x = bf16_to_f32(hx[jj]);
+                const double y = bf16_to_f32(hy[jj]);
+                kxr[jj] = x;
+                kyr[jj] = y;
                 if (rope_k) {
-                    const double sn = sn_s[u][d], cs = cs_s[u][d];
-                    xr = x * cs - y * sn;
-                    yr = x * sn + y * cs;
+                    const double sn = sn_s[u][d0 + jj], cs = cs_s[u][d0 + jj];
+                    kxr[jj] = x * cs - y * sn;
+                    kyr[jj] = x * sn + y * cs;
                 }
-                acc = fma(qvx[jj], xr, acc);
-                acc = fma(qvy[jj], yr, acc);
             }
         }
-        acc += __shfl_xor(acc, 16);
-        acc += __shfl_xor(acc, 32);
-        if (g == 0) part_s[w][u][n] = acc;
+#pragma unroll
+        for (int tau = 0; tau < kW; ++tau) {
+            double acc = 0.0;
+#pragma unroll
+            for (int jj = 0; jj < 4; ++jj) {
+                acc = fma(qvx[tau][jj], kxr[jj], acc);
+                acc = fma(qvy[tau][jj], kyr[jj], acc);
+            }
+            acc += __shfl_xor(acc, 16);
+            acc += __shfl_xor(acc, 32);
+            if (g == 0) part_s[w][u][kMtTile * tau + n] = acc;
+        }
     }
 
-    // Stores: the appended cache row, this wave's Q operand quarter.
-    if (w < T) {
-        const int64_t ce = cache_elem(a, b, kvh, static_cast<int64_t>(st) + w);
-        double xr = bf16_to_f32(akx), yr = bf16_to_f32(aky);
-        if (rope_k) {
-            const double x = xr, y = yr;
-            xr = x * cs_s[w][lane] - y * sn_s[w][lane];
-            yr = x * sn_s[w][lane] + y * cs_s[w][lane];
-        }
-        if (ce >= 0) {
-            a.k[ce + lane] = bf16_of(xr);
-            a.k[ce + lane + kPairs] = bf16_of(yr);
-            a.v[ce + lane] = avx;
-            a.v[ce + lane + kPairs] = avy;
+    // Stores: the appended cache rows, this wave's quarter of the Q operands.
+#pragma unroll
+    for (int r = 0; r < kW; ++r) {
+        const int u = w + 4 * r;
+        if (u < T) {
+            const int64_t ce = cache_elem(a, b, kvh, static_cast<int64_t>(st) + u);
+            double xr = bf16_to_f32(akx[r]), yr = bf16_to_f32(aky[r]);
+            if (rope_k) {
+                const double x = xr, y = yr;
+                xr = x * cs_s[u][lane] - y * sn_s[u][lane];
+                yr = x * sn_s[u][lane] + y * cs_s[u][lane];
+            }
+            if (ce >= 0) {
+                a.k[ce + lane] = bf16_of(xr);
+                a.k[ce + lane + kPairs] = bf16_of(yr);
+                a.v[ce + lane] = avx[r];
+                a.v[ce + lane + kPairs] = avy[r];
+            }
         }
     }
-    uint16_t px[3][4], py[3][4];
 #pragma unroll
-    for (int jj = 0; jj < 4; ++jj) {
+    for (int tau = 0; tau < kW; ++tau) {
+        uint4* base = a.q_op + ((static_cast<int64_t>(b) * kHkv + kvh) * kW + tau) * 12 * kWave + lane;
 #pragma unroll
         for (int s = 0; s < 3; ++s) {
-            px[s][jj] = split3(qvx[jj], s);
-            py[s][jj] = split3(qvy[jj], s);
+            uint16_t px[4], py[4];
+#pragma unroll
+            for (int jj = 0; jj < 4; ++jj) {
+                px[jj] = split3(qvx[tau][jj], s);
+                py[jj] = split3(qvy[tau][jj], s);
+            }
+            uint2* dx = reinterpret_cast<uint2*>(base + (s * 4 + kbp) * kWave) + (w >> 1);
+            uint2* dy = reinterpret_cast<uint2*>(base + (s * 4 + kbp + 2) * kWave) + (w >> 1);
+            *dx = make_uint2(px[0] | (static_cast<uint32_t>(px[1]) << 16), px[2] | (static_cast<uint32_t>(px[3]) << 16));
+            *dy = make_uint2(py[0] | (static_cast<uint32_t>(py[1]) << 16), py[2] | (static_cast<uint32_t>(py[3]) << 16));
         }
     }
-    uint4* base = a.q_op + (static_cast<int64_t>(b) * kHkv + kvh) * 12 * kWave + lane;
-#pragma unroll
-    for (int s = 0; s < 3; ++s) {
-        uint2* dx = reinterpret_cast<uint2*>(base + (s * 4 + kbp) * kWave) + (w >> 1);
-        uint2* dy = reinterpret_cast<uint2*>(base + (s * 4 + kbp + 2) * kWave) + (w >> 1);
-        *dx = make_uint2(px[s][0] | (static_cast<uint32_t>(px[s][1]) << 16),
-                         px[s][2] | (static_cast<uint32_t>(px[s][3]) << 16));
-        *dy = make_uint2(py[s][0] | (static_cast<uint32_t>(py[s][1]) << 16),
-                         py[s][2] | (static_cast<uint32_t>(py[s][3]) << 16));
-    }
     __syncthreads();
-    if (w == 0 && g == 0) {
-        double sc[kMultiMaxNew];
-#pragma unroll
-        for (int u = 0; u < kMultiMaxNew; ++u)
-            sc[u] = ((part_s[0][u][n] + part_s[1][u][n]) + part_s[2][u][n]) + part_s[3][u][n];
-        a.chunk_s[(static_cast<int64_t>(b) * kHkv + kvh) * kMtCols + n] =
-            make_float4(static_cast<float>(sc[0]), static_cast<float>(sc[1]), static_cast<float>(sc[2]),
-                        static_cast<float>(sc[3]));
+    float* cs_out = a.chunk_s + (static_cast<int64_t>(b) * kHkv + kvh) * kCols * kU;
+    for (int i = threadIdx.x; i < kCols * kU; i += blockDim.x) {
+        const int c = i / kU;
+        const int u = i % kU;
+        cs_out[i] = static_cast<float>(((part_s[0][u][c] + part_s[1][u][c]) + part_s[2][u][c]) + part_s[3][u][c]);
     }
 }
 
-// Copies of one plane (K or V rows of the window of keys [key0, key0 + 32) of a segment;
-// rows past k_last repeat row k_last) into the ring slot at `dst`, nontemporal (each row is
-// read once): lane l of copy ii writes row 4ii + l/16, chunk position l%16, the chunk it
-// fetches swizzled as in the attention kernel.
+// This wave's share (copies [wv * kC, (wv + 1) * kC)) of one plane: K or V rows of the
+// window of keys [key0, key0 + 32) of a segment (rows past k_last repeat row k_last), into
+// the ring slot at `dst`, nontemporal (each row is read once): lane l of copy ii writes row
+// 4ii + l/16, chunk position l%16, the chunk it fetches swizzled as in the attention
+// kernel.
+template <int kC>
 __device__ __forceinline__ void mt_issue_plane(const char* seg, int64_t row_bytes, int key0, int k_last,
-                                               uint8_t* dst, int lane) {
+                                               uint8_t* dst, int wv, int lane) {
     constexpr int kNt = 2;     // cache policy: nontemporal
-    int64_t off[kMtHalf];
+    int64_t off[kC];
 #pragma unroll
-    for (int ii = 0; ii < kMtHalf; ++ii) {
-        const int r = 4 * ii + (lane >> 4);
+    for (int q = 0; q < kC; ++q) {
+        const int r = 4 * (wv * kC + q) + (lane >> 4);
         const int c = (lane & 15) ^ pf_swz(r);
-        off[ii] = static_cast<int64_t>(min(key0 + r, k_last)) * row_bytes + 16 * c;
+        off[q] = static_cast<int64_t>(min(key0 + r, k_last)) * row_bytes + 16 * c;
     }
 #pragma unroll
-    for (int ii = 0; ii < kMtHalf; ++ii)
-        __builtin_amdgcn_global_load_lds(seg + off[ii], (lds_void_t*)(dst + ii * 1024), 16, 0, kNt);
+    for (int q = 0; q < kC; ++q)
+        __builtin_amdgcn_global_load_lds(seg + off[q], (lds_void_t*)(dst + (wv * kC + q) * 1024), 16, 0, kNt);
 }
 
 // Running state of a piece in lane (g, n): O^T[16dt + 4g + i][column n] in fp64, the
@@ -962,19 +1022,14 @@ struct MtState {
 };
 
 // One 32-key window [key0, key0 + 32) of a piece ending at k_b: scores, online softmax,
-// V^T P^T.  `lim` = the last key this lane's column may attend to (start + t).  Chunk keys
-// (>= st) take the scores the preparation formed from their unrounded rows (`cs`: this
-// lane's column against chunk keys u = 0..3).
-// kAhead = windows after this one whose copies are in flight (0..2): with two, the planes
-// requested after this window's K are its V, K and V of the next window and K of the one
-// after (32 copies), after its V three planes (24); with one, 24 and 16; with none, 8 and 0.
-template <bool kChunkKeys, int kAhead>
+// V^T P^T for this wave's tile.  `lim` = the last key this lane's column may attend to
+// (start + t).  Chunk keys (>= st) take the scores the preparation formed from their
+// unrounded rows (`cs`: this lane's column against chunk keys u = 0 .. kU-1).  nv = planes
+// of this wave's copies younger than this window's V.
+template <bool kChunkKeys, int kW>
 __device__ __forceinline__ void mt_window(const PrefillArgs& a, const uint8_t* kplane, uint32_t vbase,
-                                          const bf16x8_t (&qop)[3][4], float4 cs, int st, int key0, int k_b,
-                                          int lim, int lane, MtState& t) {
-    // This window's K copies have landed (the counter retires in issue order; requests of
-    // other kinds issued since -- Q operands, stores -- only make the wait longer).
-    __builtin_amdgcn_s_waitcnt(vmcnt_imm(kMtHalf * (kAhead == 2 ? 4 : kAhead == 1 ? 3 : 1)));
+                                          const bf16x8_t (&qop)[3][4], const float (&cs)[4 * kW], int st,
+                                          int key0, int k_b, int lim, int nv, int lane, MtState& t) {
     const int n = lane & 15;
     const int g = lane >> 4;
     f32x4_t sacc[2] = {f32x4_t{0.f, 0.f, 0.f, 0.f}, f32x4_t{0.f, 0.f, 0.f, 0.f}};
@@ -995,7 +1050,12 @@ __device__ __forceinline__ void mt_window(const PrefillArgs& a, const uint8_t* k
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 const int u = key0 + 16 * kt + 4 * g + i - st;
-                if (u >= 0 && u < a.n_new) sacc[kt][i] = u == 0 ? cs.x : u == 1 ? cs.y : u == 2 ? cs.z : cs.w;
+                if (u >= 0 && u < a.n_new) {
+                    float v = cs[0];
+#pragma unroll
+                    for (int q = 1; q < 4 * kW; ++q) v = u == q ? cs[q] : v;
+                    sacc[kt][i] = v;
+                }
             }
     }
     // Mask (keys past the piece or past the column's token), window max per column.
@@ -1027,7 +1087,8 @@ __device__ __forceinline__ void mt_window(const PrefillArgs& a, const uint8_t* k
     for (int kt = 0; kt < 2; ++kt) pf_probs_tile(sacc[kt], m_eff, lsum, ph, kt);
     t.l64 += static_cast<double>(lsum);
 
-    __builtin_amdgcn_s_waitcnt(vmcnt_imm(kMtHalf * (kAhead == 2 ? 3 : kAhead == 1 ? 2 : 0)));
+    mt_wait_planes<kMtCopies / kW>(nv);
+    mt_barrier();
     // V^T P^T: dim tile dt from two transposed reads (rows 4g + a/4 and 16 rows on).
     bf16x8_t pb[3];
 #pragma unroll
@@ -1063,14 +1124,16 @@ __device__ __forceinline__ void mt_window(const PrefillArgs& a, const uint8_t* k
 }
 
 // End of a piece: the column sums over the four rows; a whole segment writes its output
-// rows (tokens < T), a split one its partial at slot wg + segment.
+// rows (tokens < T), a split one its partial at slot wg + segment, columns 16 wv + n, in
+// fp64 (an output that cancels to near zero needs the partials' full precision).
+template <int kW>
 __device__ __forceinline__ void mt_piece_end(const PrefillArgs& a, int b, int kvh, bool whole, int64_t slot,
-                                             int lane, MtState& t) {
+                                             int wv, int lane, MtState& t) {
     const int n = lane & 15;
     const int g = lane >> 4;
     const double l = swap_add_f64<true>(swap_add_f64<false>(t.l64));
     if (whole) {
-        const int tok = n >> 2;
+        const int tok = 4 * wv + (n >> 2);
         if (tok >= a.n_new) return;
         uint16_t* orow = a.out + ((static_cast<int64_t>(b) * a.n_new + tok) * kHq + kvh * kGroup + (n & 3)) * kD;
 #pragma unroll
@@ -1084,14 +1147,15 @@ __device__ __forceinline__ void mt_piece_end(const PrefillArgs& a, int b, int kv
         }
         return;
     }
-    double* po = a.part_o + (slot * kMtCols + n) * kD;
+    const int64_t col = slot * (kMtTile * kW) + kMtTile * wv + n;
+    double* po = a.part_o + col * kD;
 #pragma unroll
     for (int dt = 0; dt < 8; ++dt) {
         double2* d = reinterpret_cast<double2*>(po + 16 * dt + 4 * g);
         d[0] = make_double2(t.o64[dt][0], t.o64[dt][1]);
         d[1] = make_double2(t.o64[dt][2], t.o64[dt][3]);
     }
-    if (g == 0) a.part_ml[slot * kMtCols + n] = make_float2(t.m_run, static_cast<float>(l));
+    if (g == 0) a.part_ml[col] = make_float2(t.m_run, static_cast<float>(l));
 }
 
 // Sequence windows of the plan: o = seq_off[base + lane], o1 = seq_off[base + lane + 1].
@@ -1162,8 +1226,13 @@ __device__ __forceinline__ void mt_advance(const PrefillArgs& a, MtCursor& c, in
     c.k_b = __builtin_amdgcn_readfirstlane(static_cast<int>(min(static_cast<int64_t>(c.nk), x_end - c.x)));
 }
 
-__global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(1))) void mt_stream_kernel(PrefillArgs a) {
-    __shared__ __attribute__((aligned(1024))) uint8_t lds[kMtLdsB];
+template <int kW>
+__global__ __launch_bounds__(kWave * kW) __attribute__((amdgpu_waves_per_eu(1))) void mt_stream_kernel(PrefillArgs a) {
+    constexpr int kA = mt_ahead(kW);
+    constexpr int kS = mt_slots(kW);
+    constexpr int kC = kMtCopies / kW;
+    constexpr int kU = 4 * kW;
+    __shared__ __attribute__((aligned(1024))) uint8_t lds[kS * kMtPlaneB];
     MtWindow w0;
     mt_load_window(a, 0, w0);
     const int64_t wg = blockIdx.x;
@@ -1174,6 +1243,7 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(1))) void
     int64_t x = range_start(per_wg, extra, wg);
     if (x >= total) return;
     const int64_t x_end = min(range_start(per_wg, extra, wg + 1), total);
+    const int wv = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
     const int lane = threadIdx.x & (kWave - 1);
     const int n = lane & 15;
     const int64_t row_bytes = a.kv_pos_stride * 2;
@@ -1210,29 +1280,53 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(1))) void
         return reinterpret_cast<const char*>(base + static_cast<int64_t>(bb) * a.kv_batch_stride +
                                              static_cast<int64_t>(hh) * a.kv_head_stride);
     };
-    auto slot_ptr = [&](int sl) { return lds + sl * kMtPlaneB; };
+    auto slot_ptr = [&](int sl) { return lds + (sl >= kS ? sl - kS : sl) * kMtPlaneB; };
+    auto issue = [&](const uint16_t* base, const MtCursor& q, int sl) {
+        mt_issue_plane<kC>(seg_base(base, q.b, q.kvh), row_bytes, q.kw, q.k_b - 1, slot_ptr(sl), wv, lane);
+    };
     // The producer p is the last window whose K copies were requested; the consumer c's
-    // window has its K plane in slot `slot` and its V plane in the next one.
+    // window has K in slot `slot` and V in the next one.  kq = windows after c's whose K
+    // has been requested (at most kA before the window's own requests).
     MtCursor p = c;
-    int slot = 0;
-    mt_issue_plane(seg_base(a.k, p.b, p.kvh), row_bytes, p.kw, p.k_b - 1, slot_ptr(0), lane);
-    mt_issue_plane(seg_base(a.v, p.b, p.kvh), row_bytes, p.kw, p.k_b - 1, slot_ptr(1), lane);
-    mt_advance(a, p, x_end, lead);
-    if (p.valid) mt_issue_plane(seg_base(a.k, p.b, p.kvh), row_bytes, p.kw, p.k_b - 1, slot_ptr(2), lane);
+    int slot = 0, kq = 0;
+    issue(a.k, p, 0);
+#pragma unroll
+    for (int j = 0; j < kA; ++j) {
+        if (p.valid) {
+            issue(a.v, p, 2 * j + 1);
+            mt_advance(a, p, x_end, lead);
+            if (p.valid) {
+                issue(a.k, p, 2 * j + 2);
+                ++kq;
+            }
+        }
+    }
 
     while (true) {
-        // This piece: Q operands, start, window loop.
+        // This piece: Q operands, chunk-key scores, start, window loop.
         const int st = a.start[c.b];
+        const int64_t seg = static_cast<int64_t>(c.b) * kHkv + c.kvh;
         bf16x8_t qop[3][4];
         {
-            const uint4* src = a.q_op + (static_cast<int64_t>(c.b) * kHkv + c.kvh) * 12 * kWave + lane;
+            const uint4* src = a.q_op + (seg * kW + wv) * 12 * kWave + lane;
 #pragma unroll
             for (int s = 0; s < 3; ++s)
 #pragma unroll
                 for (int kb = 0; kb < 4; ++kb) qop[s][kb] = as_bf16x8(src[(s * 4 + kb) * kWave]);
         }
-        const float4 cs = a.chunk_s[(static_cast<int64_t>(c.b) * kHkv + c.kvh) * kMtCols + n];
-        const int lim = st + min(n >> 2, a.n_new - 1);
+        float cs[kU];
+        {
+            const float4* src = reinterpret_cast<const float4*>(a.chunk_s + (seg * (kMtTile * kW) + kMtTile * wv + n) * kU);
+#pragma unroll
+            for (int q = 0; q < kW; ++q) {
+                const float4 v = src[q];
+                cs[4 * q] = v.x;
+                cs[4 * q + 1] = v.y;
+                cs[4 * q + 2] = v.z;
+                cs[4 * q + 3] = v.w;
+            }
+        }
+        const int lim = st + min(4 * wv + (n >> 2), a.n_new - 1);
         MtState t;
 #pragma unroll
         for (int dt = 0; dt < 8; ++dt)
@@ -1242,48 +1336,45 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(1))) void
         t.m_run = -INFINITY;
 
         for (;;) {
-            // Request V of the producer's window (the consumer's next) and K of the window
-            // after it, then compute this one.
-            int ahead = 0;
-            if (p.valid) {
-                const int sv = slot + 3 >= kMtSlots ? slot + 3 - kMtSlots : slot + 3;
-                mt_issue_plane(seg_base(a.v, p.b, p.kvh), row_bytes, p.kw, p.k_b - 1, slot_ptr(sv), lane);
-                ahead = 1;
+            // Request V of the producer's window (kA after this one) and, once every wave
+            // is done with the previous window, K of the window after it.
+            const bool iv = p.valid;
+            if (iv) issue(a.v, p, slot + 2 * kA + 1);
+            mt_wait_planes<kC>(1 + 2 * kq);
+            mt_barrier();
+            bool ik = false;
+            if (iv) {
                 mt_advance(a, p, x_end, lead);
                 if (p.valid) {
-                    const int sk = slot + 4 >= kMtSlots ? slot + 4 - kMtSlots : slot + 4;
-                    mt_issue_plane(seg_base(a.k, p.b, p.kvh), row_bytes, p.kw, p.k_b - 1, slot_ptr(sk), lane);
-                    ahead = 2;
+                    issue(a.k, p, slot + 2 * kA + 2);
+                    ik = true;
                 }
             }
-            const int slot_v = slot + 1 >= kMtSlots ? 0 : slot + 1;
+            const int nv = 2 * kq + (ik ? 1 : 0);
             const uint8_t* kplane = slot_ptr(slot);
-            const uint32_t vbase = lds_base + slot_v * kMtPlaneB;
-            const bool chunk_keys = c.kw + kMtWin > st;
-#define MT_WINDOW(ck, ah) mt_window<ck, ah>(a, kplane, vbase, qop, cs, st, c.kw, c.k_b, lim, lane, t)
-            if (ahead == 2) {
-                if (chunk_keys) MT_WINDOW(true, 2); else MT_WINDOW(false, 2);
-            } else if (ahead == 1) {
-                if (chunk_keys) MT_WINDOW(true, 1); else MT_WINDOW(false, 1);
-            } else {
-                if (chunk_keys) MT_WINDOW(true, 0); else MT_WINDOW(false, 0);
-            }
-#undef MT_WINDOW
-            slot = slot + 2 >= kMtSlots ? slot + 2 - kMtSlots : slot + 2;
+            const uint32_t vbase = lds_base + (slot + 1 >= kS ? slot + 1 - kS : slot + 1) * kMtPlaneB;
+            if (c.kw + kMtWin > st)
+                mt_window<true, kW>(a, kplane, vbase, qop, cs, st, c.kw, c.k_b, lim, nv, lane, t);
+            else
+                mt_window<false, kW>(a, kplane, vbase, qop, cs, st, c.kw, c.k_b, lim, nv, lane, t);
+            slot = slot + 2 >= kS ? slot + 2 - kS : slot + 2;
+            kq = ik ? kq : kq - 1;
             if (c.kw + kMtWin >= c.k_b) break;
             c.kw += kMtWin;
         }
-        mt_piece_end(a, c.b, c.kvh, c.pk == 0 && c.k_b == c.nk, wg + static_cast<int64_t>(c.b) * kHkv + c.kvh, lane,
-                     t);
+        mt_piece_end<kW>(a, c.b, c.kvh, c.pk == 0 && c.k_b == c.nk, wg + seg, wv, lane, t);
         mt_advance(a, c, x_end, lead);
         if (!c.valid) break;
     }
 }
 
-// Merge the pieces of split segments: one 256-thread workgroup per (KV head, sequence);
-// thread i handles column i/16 (token, head), dims 8(i%16) .. +8.  Weights 2^(m - max) are
-// exact; a piece that saw no key the column may attend to has m = -inf and weight 0.
-__global__ __launch_bounds__(256) void mt_merge_kernel(PrefillArgs a) {
+// Merge the pieces of split segments: one workgroup per (KV head, sequence), 16 threads per
+// column: thread i handles column i/16 (token c/4, head c%4), dims 8(i%16) .. +8.  Weights
+// 2^(m - max) are exact; a piece that saw no key the column may attend to has m = -inf and
+// weight 0.
+template <int kW>
+__global__ __launch_bounds__(256 * kW) void mt_merge_kernel(PrefillArgs a) {
+    constexpr int kCols = kMtTile * kW;
     const int kvh = blockIdx.x;
     const int b = blockIdx.y;
     const int64_t per_wg = a.plan_hdr[1];
@@ -1303,14 +1394,14 @@ __global__ __launch_bounds__(256) void mt_merge_kernel(PrefillArgs a) {
     const int tok = col >> 2;
     if (tok >= a.n_new) return;
     float mx = -INFINITY;
-    for (int p = 0; p < n_pieces; ++p) mx = fmaxf(mx, a.part_ml[(slot0 + p) * kMtCols + col].x);
+    for (int p = 0; p < n_pieces; ++p) mx = fmaxf(mx, a.part_ml[(slot0 + p) * kCols + col].x);
     double l = 0.0, o[8] = {0, 0, 0, 0, 0, 0, 0, 0};
     for (int p = 0; p < n_pieces; ++p) {
-        const float2 ml = a.part_ml[(slot0 + p) * kMtCols + col];
+        const float2 ml = a.part_ml[(slot0 + p) * kCols + col];
         if (ml.x == -INFINITY) continue;
         const int e = static_cast<int>(ml.x - mx);
         l += ldexp(static_cast<double>(ml.y), e);
-        const double* po = a.part_o + ((slot0 + p) * kMtCols + col) * kD + d0;
+        const double* po = a.part_o + ((slot0 + p) * kCols + col) * kD + d0;
 #pragma unroll
         for (int j = 0; j < 8; ++j) o[j] += ldexp(po[j], e);
     }
@@ -1323,22 +1414,28 @@ __global__ __launch_bounds__(256) void mt_merge_kernel(PrefillArgs a) {
     dst[1] = make_uint2(h8[4] | (static_cast<uint32_t>(h8[5]) << 16), h8[6] | (static_cast<uint32_t>(h8[7]) << 16));
 }
 
-hipError_t launch_prefill_multi(const PrefillArgs& a, hipStream_t stream, hipEvent_t* ev) {
+template <int kW>
+hipError_t launch_multi_w(const PrefillArgs& a, hipStream_t stream, hipEvent_t* ev) {
     const bool vec = (reinterpret_cast<uintptr_t>(a.q) % 16) == 0 && (reinterpret_cast<uintptr_t>(a.k_new) % 16) == 0;
     const dim3 grid(kHkv, static_cast<unsigned>(a.batch) + 1);
     if (vec)
-        hipLaunchKernelGGL(mt_prepare_kernel<true>, grid, dim3(4 * kWave), 0, stream, a);
+        hipLaunchKernelGGL((mt_prepare_kernel<true, kW>), grid, dim3(256), 0, stream, a);
     else
-        hipLaunchKernelGGL(mt_prepare_kernel<false>, grid, dim3(4 * kWave), 0, stream, a);
+        hipLaunchKernelGGL((mt_prepare_kernel<false, kW>), grid, dim3(256), 0, stream, a);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     if (ev) (void)hipEventRecord(ev[1], stream);
-    hipLaunchKernelGGL(mt_stream_kernel, dim3(static_cast<unsigned>(a.n_wgs)), dim3(kWave), 0, stream, a);
+    hipLaunchKernelGGL(mt_stream_kernel<kW>, dim3(static_cast<unsigned>(a.n_wgs)), dim3(kWave * kW), 0, stream, a);
     e = hipGetLastError();
     if (ev) (void)hipEventRecord(ev[2], stream);
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL(mt_merge_kernel, dim3(kHkv, static_cast<unsigned>(a.batch)), dim3(256), 0, stream, a);
+    hipLaunchKernelGGL(mt_merge_kernel<kW>, dim3(kHkv, static_cast<unsigned>(a.batch)), dim3(256 * kW), 0, stream, a);
     return hipGetLastError();
+}
+
+hipError_t launch_prefill_multi(const PrefillArgs& a, hipStream_t stream, hipEvent_t* ev) {
+    if (multi_waves(a.n_new) == 1) return launch_multi_w<1>(a, stream, ev);
+    return launch_multi_w<2>(a, stream, ev);
 }
 
 }  // namespace gqa

@@ -55,6 +55,8 @@ MULTI_WORKLOADS = {
     # name: (batch, capacity, min_len, max_len, new tokens): the decode batch's lengths, whose
     # last `new` positions are the new tokens (appended with RoPE, then attended causally)
     "multitoken_b64_ragged_512_8192_t4": (64, 8192, 512, 8192, 4),
+    "multitoken_b64_ragged_512_8192_t8": (64, 8192, 512, 8192, 8),
+    "multitoken_b64_ragged_512_8192_t16": (64, 8192, 512, 8192, 16),
 }
 MFMA_BF16_PEAK_TFLOPS = 2500.0
 TRAFFIC_FILE = ROOT / "profiles" / "decode_stream_b64_ragged_traffic.txt"
@@ -302,13 +304,19 @@ def bench_multitoken(args, torch, gqa, dev, stimulus) -> int:
     print(f"[bench] {args.steps} steps: {ms_per_step * 1e3:.2f} us/step", file=sys.stderr, flush=True)
     roofline = None
     if attn_ms:
+        # Chunks of at most 8 new tokens run the stream-K path (events: preparation with
+        # the append, then the stream kernel); longer ones the prefill attention kernel
+        # (events: append, then attention).
+        stream_k = n_new <= 8 and os.environ.get("GQA_PREFILL_MULTI", "1") != "0"
         achieved = step_bytes / (attn_ms * 1e-3) / 1e9
         roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
-                    "kernel": "mt_stream_kernel", "kernel_us": round(attn_ms * 1e3, 2),
-                    "append_prepare_us": round(append_ms * 1e3, 2), "bytes_per_launch": step_bytes}
+                    "kernel": "mt_stream_kernel" if stream_k else "prefill_attn_kernel",
+                    "kernel_us": round(attn_ms * 1e3, 2),
+                    ("prepare_us" if stream_k else "append_us"): round(append_ms * 1e3, 2),
+                    "bytes_per_launch": step_bytes}
     result = {
-        "metric": "GQA multi-token decode µs/step + achieved HBM GB/s, B=64 ragged ctx 512–8192, 4 new tokens",
+        "metric": f"GQA multi-token decode µs/step + achieved HBM GB/s, B=64 ragged ctx 512–8192, {n_new} new tokens",
         "value": round(step_bytes / (ms_per_step * 1e-3) / 1e9, 1),
         "unit": "GB/s",
         "n_gpus": 1,
