@@ -59,18 +59,33 @@ MULTI_WORKLOADS = {
     "multitoken_b64_ragged_512_8192_t16": (64, 8192, 512, 8192, 16),
 }
 MFMA_BF16_PEAK_TFLOPS = 2500.0
-TRAFFIC_FILE = ROOT / "profiles" / "decode_stream_b64_ragged_traffic.txt"
+TRAFFIC_FILES = {
+    "decode_b64_ragged_512_8192": ROOT / "profiles" / "decode_stream_b64_ragged_traffic.txt",
+    "multitoken_b64_ragged_512_8192_t4": ROOT / "profiles" / "mt_stream_b64_ragged_t4_traffic.txt",
+}
 
 
 def read_traffic(workload: str):
-    """HBM bytes per split-kernel launch measured with rocprofv3 --pmc (FETCH_SIZE +
-    WRITE_SIZE, scaled by the copy-kernel calibration), if committed for this workload."""
-    if workload != "decode_b64_ragged_512_8192" or not TRAFFIC_FILE.exists():
+    """HBM bytes per launch of the workload's dominant kernel measured with rocprofv3 --pmc
+    (FETCH_SIZE + WRITE_SIZE, scaled by the copy-kernel calibration), if committed."""
+    f = TRAFFIC_FILES.get(workload)
+    if f is None or not f.exists():
         return None
-    for line in TRAFFIC_FILE.read_text().splitlines():
+    for line in f.read_text().splitlines():
         if line.startswith("traffic_bytes_per_launch="):
             return float(line.split("=", 1)[1])
     return None
+
+
+def calibrate_copy(torch, dev):
+    """Five plain 1 GiB device copies: the known-size kernel the PMC byte counters are
+    scaled by."""
+    src = torch.empty(1 << 30, dtype=torch.uint8, device=dev)
+    dst = torch.empty_like(src)
+    for _ in range(5):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    del src, dst
 
 
 def cpu_baseline(batch, budget_s: float = 12.0):
@@ -302,6 +317,8 @@ def bench_multitoken(args, torch, gqa, dev, stimulus) -> int:
         gqa.profile_enable(0)
         append_ms, attn_ms = ap_ms / n, at_ms / n
     print(f"[bench] {args.steps} steps: {ms_per_step * 1e3:.2f} us/step", file=sys.stderr, flush=True)
+    if args.calibrate_copy:
+        calibrate_copy(torch, dev)
     roofline = None
     if attn_ms:
         # Chunks of at most 8 new tokens run the stream-K path (events: preparation with
@@ -310,7 +327,8 @@ def bench_multitoken(args, torch, gqa, dev, stimulus) -> int:
         stream_k = n_new <= 8 and os.environ.get("GQA_PREFILL_MULTI", "1") != "0"
         achieved = step_bytes / (attn_ms * 1e-3) / 1e9
         roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                    "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                    "frac": round(achieved / HBM_PEAK_GBS, 4),
+                    "traffic": read_traffic(args.workload) if stream_k else None,
                     "kernel": "mt_stream_kernel" if stream_k else "prefill_attn_kernel",
                     "kernel_us": round(attn_ms * 1e3, 2),
                     ("prepare_us" if stream_k else "append_us"): round(append_ms * 1e3, 2),
@@ -462,12 +480,7 @@ def main() -> int:
           file=sys.stderr, flush=True)
 
     if args.calibrate_copy:
-        src = torch.empty(1 << 30, dtype=torch.uint8, device=dev)
-        dst = torch.empty_like(src)
-        for _ in range(5):
-            dst.copy_(src)
-        torch.cuda.synchronize()
-        del src, dst
+        calibrate_copy(torch, dev)
 
     gbs = step_bytes / (ms_per_step * 1e-3) / 1e9
     roofline = None
