@@ -1393,17 +1393,44 @@ __global__ __launch_bounds__(256 * kW) void mt_merge_kernel(PrefillArgs a) {
     const int d0 = 8 * (threadIdx.x & 15);
     const int tok = col >> 2;
     if (tok >= a.n_new) return;
-    float mx = -INFINITY;
-    for (int p = 0; p < n_pieces; ++p) mx = fmaxf(mx, a.part_ml[(slot0 + p) * kCols + col].x);
+    // Pieces four at a time, every load of a group issued before any is used (one memory
+    // round trip per group); the running max moves by whole powers of two, so rescaling
+    // what is already summed is exact.
+    constexpr int kGroupP = 4;
+    float m = -INFINITY;
     double l = 0.0, o[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-    for (int p = 0; p < n_pieces; ++p) {
-        const float2 ml = a.part_ml[(slot0 + p) * kCols + col];
-        if (ml.x == -INFINITY) continue;
-        const int e = static_cast<int>(ml.x - mx);
-        l += ldexp(static_cast<double>(ml.y), e);
-        const double* po = a.part_o + ((slot0 + p) * kCols + col) * kD + d0;
+    for (int p0 = 0; p0 < n_pieces; p0 += kGroupP) {
+        float2 ml[kGroupP];
+        double v[kGroupP][8];
 #pragma unroll
-        for (int j = 0; j < 8; ++j) o[j] += ldexp(po[j], e);
+        for (int q = 0; q < kGroupP; ++q) {
+            ml[q] = make_float2(-INFINITY, 0.f);
+            if (p0 + q < n_pieces) {
+                const int64_t c = (slot0 + p0 + q) * kCols + col;
+                ml[q] = a.part_ml[c];
+                const double* po = a.part_o + c * kD + d0;
+#pragma unroll
+                for (int j = 0; j < 8; ++j) v[q][j] = po[j];
+            }
+        }
+        float mb = m;
+#pragma unroll
+        for (int q = 0; q < kGroupP; ++q) mb = fmaxf(mb, ml[q].x);
+        if (m != -INFINITY && mb != m) {
+            const int e = static_cast<int>(m - mb);
+            l = ldexp(l, e);
+#pragma unroll
+            for (int j = 0; j < 8; ++j) o[j] = ldexp(o[j], e);
+        }
+        m = mb;
+#pragma unroll
+        for (int q = 0; q < kGroupP; ++q) {
+            if (ml[q].x == -INFINITY) continue;
+            const int e = static_cast<int>(ml[q].x - m);
+            l += ldexp(static_cast<double>(ml[q].y), e);
+#pragma unroll
+            for (int j = 0; j < 8; ++j) o[j] += ldexp(v[q][j], e);
+        }
     }
     uint16_t h8[8];
 #pragma unroll
