@@ -501,7 +501,8 @@ __device__ __forceinline__ void build_q_operands(const DecodeArgs& a, const QRaw
 //
 // The stream-K plan (row B of the prepare grid, one wave): seq_off[b] = stream position
 // of sequence b's first segment (an exclusive scan of 8 * plan_span), seq_off[B] = total
-// positions, and the header {total, positions per stream workgroup, segment lead}.  Every
+// positions, and the header {total, positions per stream workgroup, segment lead, XCD
+// extra: positions moved from each odd range to its even neighbour (range_start)}.  Every
 // stream workgroup finds where its range starts from these with one ballot.
 __device__ __forceinline__ void build_plan(const DecodeArgs& a, int lane) {
     int64_t total, per_wg;
@@ -511,6 +512,7 @@ __device__ __forceinline__ void build_plan(const DecodeArgs& a, int lane) {
         a.plan_hdr[0] = total;
         a.plan_hdr[1] = per_wg;
         a.plan_hdr[2] = lead;
+        a.plan_hdr[3] = range_extra(per_wg, a.skew_pm);
         a.seq_off[a.batch] = total;
     }
     int64_t carry = 0;
@@ -751,9 +753,10 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(1))) void
     const int64_t total = a.plan_hdr[0];
     const int64_t per_wg = a.plan_hdr[1];
     const int lead = static_cast<int>(a.plan_hdr[2]);
-    int64_t x = w * per_wg;
+    const int64_t extra = a.plan_hdr[3];
+    int64_t x = range_start(per_wg, extra, w);
     if (x >= total) return;
-    const int64_t x_end = min(x + per_wg, total);
+    const int64_t x_end = min(range_start(per_wg, extra, w + 1), total);
 
     // Start sequence b = the last b with seq_off[b] <= x (it has keys, since x < total).
     SeqWindow sw;
@@ -1301,9 +1304,10 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(1))) void
     const int64_t total = a.plan_hdr[0];
     const int64_t per_wg = a.plan_hdr[1];
     const int lead = static_cast<int>(a.plan_hdr[2]);
-    int64_t x = w * per_wg;
+    const int64_t extra = a.plan_hdr[3];
+    int64_t x = range_start(per_wg, extra, w);
     if (x >= total) return;
-    const int64_t x_end = min(x + per_wg, total);
+    const int64_t x_end = min(range_start(per_wg, extra, w + 1), total);
 
     // Start sequence: the last b with seq_off[b] <= x (it has keys, since x < total).
     SeqWindow sw;
@@ -1397,8 +1401,9 @@ __global__ __launch_bounds__(kGroup * kWave) void decode_merge_kernel(DecodeArgs
     const int lead = static_cast<int>(a.plan_hdr[2]);
     const int nv = span - lead;
     const int64_t seg_off = off + static_cast<int64_t>(kvh) * span + lead;   // stream position of key 0
-    const int64_t w_first = seg_off / per_wg;
-    const int n_pieces = static_cast<int>((seg_off + nv - 1) / per_wg - w_first) + 1;
+    const int64_t extra = a.plan_hdr[3];
+    const int64_t w_first = range_of(per_wg, extra, seg_off);
+    const int n_pieces = static_cast<int>(range_of(per_wg, extra, seg_off + nv - 1) - w_first) + 1;
     if (n_pieces == 1) return;
     const int64_t slot0 = w_first + static_cast<int64_t>(b) * kHkv + kvh;
 

@@ -35,6 +35,7 @@ struct DecodeArgs {
     int32_t n_blocks;         // paged: blocks in the pool (ids outside [0, n_blocks) poison the row)
     int32_t batch;
     int32_t n_wgs;            // persistent workgroups of the stream kernel
+    int32_t skew_pm;          // stream and paged kernels: XCD weighting of the ranges (per mille)
     int32_t pieces_cap;       // > 0: single-launch path, pieces per segment (grid x)
     int32_t piece_keys;       // single-launch path: keys per piece
     int32_t fused;            // 1: one fused stream launch (plan, Q operands, merge in-kernel)

@@ -71,10 +71,11 @@ __device__ __forceinline__ void locate_first_piece(int64_t off, int64_t next, in
 }
 
 // XCD-weighted ranges.  Workgroups are dealt round-robin over the 8 XCDs (block w runs
-// on XCD w % 8), and on MI355X a streaming wave on an odd XCD reads about 7 % slower than
-// one on an even XCD (the same ranges swapped between neighbours: the slowness stays with
-// the XCD).  Each pair of blocks (2j, 2j+1) covers 2 * per positions, the even block
-// per + extra of them, the odd one per - extra.
+// on XCD w % 8).  In a plain streaming probe on MI355X a wave on an odd XCD read about 7 %
+// slower than one on an even XCD (swapping ranges between neighbours left the slowness
+// with the XCD), though which XCDs lag varies between launches and kernels; the weighting
+// is a per-path measured default.  Each pair of blocks (2j, 2j+1) covers 2 * per
+// positions, the even block per + extra of them, the odd one per - extra.
 __device__ __forceinline__ int64_t range_start(int64_t per, int64_t extra, int64_t w) {
     return (w >> 1) * 2 * per + ((w & 1) ? per + extra : 0);
 }

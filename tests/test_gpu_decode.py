@@ -121,6 +121,19 @@ def test_stream_partition_invariance(dev, wgs, fused, monkeypatch):
     assert_within_ulp(_oracle(b), got, 64, f"{wgs} workgroups, fused={fused}")
 
 
+@pytest.mark.parametrize("skew", ["0", "250"])
+@pytest.mark.parametrize("wgs", ["7", "333", "2048"])
+def test_stream_xcd_skew_bounds(dev, wgs, skew, monkeypatch):
+    """Equal ranges (skew 0) and the largest XCD weighting (odd ranges 3/4 of the range
+    size, even ones 5/4): the same parity on the stream and paged-free path."""
+    b = stimulus.decode_batch(5, 3000, min_len=1, max_len=3000, seed=10)
+    monkeypatch.setenv("GQA_STREAM_WGS", wgs)
+    monkeypatch.setenv("GQA_SINGLE_LAUNCH_MAX_KEYS", "0")
+    monkeypatch.setenv("GQA_XCD_SKEW", skew)
+    got = _run(b, dev)
+    assert_within_ulp(_oracle(b), got, 64, f"{wgs} workgroups, skew={skew}")
+
+
 @pytest.mark.parametrize("wgs", ["16", "200", "1024", "5000"])
 def test_single_launch_pieces(dev, wgs, monkeypatch):
     """Small batches run as one launch whose pieces (256 keys and up, here 256 .. 18432)
