@@ -371,6 +371,8 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-profile", action="store_true",
                     help="skip the per-kernel HIP events inside the timed region")
+    ap.add_argument("--graph", action="store_true",
+                    help="decode workloads: time replays of one captured step (HIP graph)")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="also run plain 1 GiB device copies (PMC byte-counter calibration)")
     args = ap.parse_args()
@@ -430,6 +432,17 @@ def main() -> int:
         call()
     torch.cuda.synchronize()
 
+    # --graph: the timed steps replay one captured step (the library issues kernels only,
+    # so a step captures as it is) instead of issuing its launches from the host.
+    step = call
+    if args.graph:
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            call()
+        step = graph.replay
+        step()
+        torch.cuda.synchronize()
+
     # A step whose K/V fit in the 256 MB Infinity Cache would find them there on every
     # repeat; such workloads write 512 MiB between steps (outside the timed events) and
     # time each step on its own.
@@ -445,7 +458,7 @@ def main() -> int:
         for i in range(args.steps):
             flush.fill_(i & 0xFF)
             evs[i][0].record()
-            call()
+            step()
             evs[i][1].record()
         torch.cuda.synchronize()
         ms_per_step = sum(a.elapsed_time(b) for a, b in evs) / args.steps
@@ -453,7 +466,7 @@ def main() -> int:
         ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         ev0.record()
         for _ in range(args.steps):
-            call()
+            step()
         ev1.record()
         torch.cuda.synchronize()
         ms_per_step = ev0.elapsed_time(ev1) / args.steps
@@ -511,7 +524,7 @@ def main() -> int:
                    "kv_heads": 8, "head_dim": 128, "rope": "q", "accumulate": "fp32 scores, fp64 weighted V",
                    "bytes_per_step": step_bytes,
                    "infinity_cache": "flushed between steps" if flushed else "working set > 1 GiB",
-                   "spinup_s": args.spinup_s},
+                   "spinup_s": args.spinup_s, "graph": bool(args.graph)},
         "roofline": roofline,
         "cpu_baseline": None if args.no_cpu_baseline else cpu_baseline(
             stimulus.DecodeBatch(batch.q.cpu(), batch.k, batch.v, batch.seq_len,

@@ -1,0 +1,74 @@
+"""HIP graph capture of the prepared calls (launch amortisation: a serving loop replays one
+captured step instead of issuing its launches from the host).  The library issues kernels
+only -- no memset, allocation or host synchronisation inside a call -- so a step captures
+as it is.  Each test replays the graph several times, with the program's own eager work
+(new inputs, an eager call of the same step) between replays, and checks every replay
+bit for bit against the eager call on the same inputs."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import attention_accelerator_amd as gqa
+from attention_accelerator_amd import stimulus
+from _util import to_codes
+
+pytestmark = pytest.mark.gpu
+
+
+def _replays(q, graph_call, eager_call, n: int = 4):
+    """Capture graph_call, then per replay: new Q (eager), replay, eager reference, compare."""
+    torch.cuda.synchronize()
+    graph_call()                      # warm-up outside the capture
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        out = graph_call()
+    gen = torch.Generator("cuda").manual_seed(77)
+    for r in range(n):
+        q.copy_(torch.randn(q.shape, generator=gen, device=q.device).to(torch.bfloat16))
+        g.replay()
+        torch.cuda.synchronize()
+        got = to_codes(out)
+        want = to_codes(eager_call())
+        torch.cuda.synchronize()
+        assert np.array_equal(got, want), f"replay {r} differs from the eager call"
+
+
+@pytest.mark.parametrize("path", ["single", "stream", "fused"])
+def test_decode_graph_replays(dev, monkeypatch, path):
+    """The three decode launch shapes: one launch (small batch), three launches (prepare,
+    stream, merge), one fused stream launch with its in-kernel merge counters (which each
+    call leaves at zero for the next)."""
+    if path == "single":
+        b = stimulus.decode_batch(2, 400, min_len=50, max_len=400, seed=21, device=dev)
+    else:
+        monkeypatch.setenv("GQA_SINGLE_LAUNCH_MAX_KEYS", "0")
+        monkeypatch.setenv("GQA_DECODE_FUSED", "1" if path == "fused" else "0")
+        b = stimulus.decode_batch(8, 3000, min_len=100, max_len=3000, seed=22, device=dev)
+    sl = b.seq_len.to(dev).to(torch.int32)
+    qpos = (sl - 1).contiguous()
+    q = torch.randn((b.k.shape[0], 32, 128), device=dev).to(torch.bfloat16)
+    graph_call = gqa.PreparedDecode(q, b.k, b.v, qpos, sl)
+    eager_call = gqa.PreparedDecode(q, b.k, b.v, qpos, sl)
+    _replays(q, graph_call, eager_call)
+
+
+@pytest.mark.parametrize("n_new", [4, 8, 40])
+def test_prefill_graph_replays(dev, n_new):
+    """Multi-token decode (stream-K path, T = 4 and 8) and chunked prefill (attention
+    kernel, T = 40): every replay re-appends the same new rows and attends with new Q."""
+    starts = [300, 77, 1024]
+    cap = max(starts) + n_new + 8
+    g = torch.Generator("cpu").manual_seed(23)
+    batch = len(starts)
+    kn = torch.randn((batch, n_new, 8, 128), generator=g).to(torch.bfloat16).to(dev)
+    vn = torch.randn((batch, n_new, 8, 128), generator=g).to(torch.bfloat16).to(dev)
+    k = torch.randn((batch, 8, cap, 128), generator=g).to(torch.bfloat16).to(dev)
+    v = torch.randn((batch, 8, cap, 128), generator=g).to(torch.bfloat16).to(dev)
+    q = torch.randn((batch, n_new, 32, 128), generator=g).to(torch.bfloat16).to(dev)
+    st = torch.tensor(starts, dtype=torch.int32, device=dev)
+    graph_call = gqa.PreparedPrefill(q, kn, vn, k, v, st)
+    eager_call = gqa.PreparedPrefill(q, kn, vn, k, v, st)
+    _replays(q, graph_call, eager_call)
