@@ -768,9 +768,12 @@ void prefill_multi_layout(PrefillArgs& a, void* base, int32_t n_wgs) {
 __device__ __forceinline__ void mt_build_plan(const PrefillArgs& a, int lane) {
     int64_t sum = 0;
     int max_keys = 0, n_seq = 0;
+    // The first 64 sequences' keys are kept for the scan below (the header stores between
+    // the two passes would otherwise make the compiler load them again).
+    const int k_first = lane < a.batch ? mt_keys(a, lane) : 0;
     for (int base = 0; base < a.batch; base += kWave) {
         const int b = base + lane;
-        const int k = b < a.batch ? mt_keys(a, b) : 0;
+        const int k = base == 0 ? k_first : (b < a.batch ? mt_keys(a, b) : 0);
         sum += wave_sum_i64(k);
         max_keys = max(max_keys, static_cast<int>(wave_max_i64(k)));
         n_seq += static_cast<int>(wave_sum_i64(k > 0 ? 1 : 0));
@@ -788,7 +791,7 @@ __device__ __forceinline__ void mt_build_plan(const PrefillArgs& a, int lane) {
     int64_t carry = 0;
     for (int base = 0; base < a.batch; base += kWave) {
         const int b = base + lane;
-        const int k = b < a.batch ? mt_keys(a, b) : 0;
+        const int k = base == 0 ? k_first : (b < a.batch ? mt_keys(a, b) : 0);
         const int span = k > 0 ? k + lead : 0;
         const int64_t incl = wave_incl_scan_i64(span, lane) + carry;
         if (b < a.batch) a.seq_off[b] = (incl - span) * kHkv;
@@ -843,8 +846,9 @@ __global__ __launch_bounds__(256) void mt_prepare_kernel(PrefillArgs a) {
     }
     const int T = a.n_new;
     const int st = a.start[b];
-    // Loads of the append rows and of Q before any store (a store may alias them as far as
-    // the compiler knows, and a load placed after it would wait for it).
+    // Every load before any store or barrier (a store may alias them as far as the compiler
+    // knows, and a load placed after it or after the barrier would wait for it): the append
+    // rows, Q, and the chunk's K rows at this lane's dims.
     const int g = lane >> 4;
     const int n = lane & 15;
     const int kbp = w & 1;
@@ -869,6 +873,15 @@ __global__ __launch_bounds__(256) void mt_prepare_kernel(PrefillArgs a) {
         const uint16_t* qrow = a.q + ((static_cast<int64_t>(b) * T + tc) * kHq + kvh * kGroup + (n & 3)) * kD;
         load4<kVec>(qrow + d0, qx[tau]);
         load4<kVec>(qrow + d0 + kPairs, qy[tau]);
+    }
+    uint16_t kxh[kU][4], kyh[kU][4];
+#pragma unroll
+    for (int u = 0; u < kU; ++u) {
+        if (u < T) {
+            const uint16_t* krow = a.k_new + ((static_cast<int64_t>(b) * T + u) * kHkv + kvh) * kD;
+            load4<kVec>(krow + d0, kxh[u]);
+            load4<kVec>(krow + d0 + kPairs, kyh[u]);
+        }
     }
     if (!prefill_start_ok(a, st)) {
         for (int i = threadIdx.x; i < T * kGroup * (kD / 4); i += blockDim.x) {
@@ -911,17 +924,14 @@ __global__ __launch_bounds__(256) void mt_prepare_kernel(PrefillArgs a) {
         }
     }
     // This wave's share of the chunk-key scores, summed over the four lanes of each column.
+#pragma unroll
     for (int u = 0; u < kU; ++u) {
         double kxr[4] = {0.0, 0.0, 0.0, 0.0}, kyr[4] = {0.0, 0.0, 0.0, 0.0};
         if (u < T) {
-            const uint16_t* krow = a.k_new + ((static_cast<int64_t>(b) * T + u) * kHkv + kvh) * kD;
-            uint16_t hx[4], hy[4];
-            load4<kVec>(krow + d0, hx);
-            load4<kVec>(krow + d0 + kPairs, hy);
 #pragma unroll
             for (int jj = 0; jj < 4; ++jj) {
-                const double x = bf16_to_f32(hx[jj]);
-                const double y = bf16_to_f32(hy[jj]);
+                const double x = bf16_to_f32(kxh[u][jj]);
+                const double y = bf16_to_f32(kyh[u][jj]);
                 kxr[jj] = x;
                 kyr[jj] = y;
                 if (rope_k) {
