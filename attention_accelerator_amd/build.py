@@ -9,7 +9,7 @@ from pathlib import Path
 PKG = Path(__file__).resolve().parent
 ROOT = PKG.parent
 CSRC = PKG / "csrc"
-SOURCES = ("gqa_abi.hip", "gqa_decode.hip", "gqa_prefill.hip", "gqa_rope.hip")
+SOURCES = ("gqa_abi.hip", "gqa_decode.hip", "gqa_prefill.hip", "gqa_multitoken.hip", "gqa_rope.hip")
 OUT = PKG / "libgqa.so"
 
 HIPCC_FLAGS = [

@@ -1,0 +1,833 @@
+// gqa_multitoken.hip -- multi-token decode for gfx950: chunks of at most 8 new tokens per
+// sequence (draft verification, a few decode steps at once) split stream-K over all CUs
+// with the prefill kernel's arithmetic (gqa_prefill.hip); the golden step per token is
+// pyfiles/gen_gqa_wrapper_vectors.py:121-139 at query position start + t.
+#include "gqa_device.h"
+#include "gqa_internal.h"
+#include "gqa_prefill_common.h"
+#include "gqa_streamk.h"
+
+namespace gqa {
+
+// ---------------------------------------------------------------------------------
+// Multi-token decode: chunks of at most kMultiMaxNew (8) new tokens per sequence --
+// drafted tokens being verified, or decode steps that append their own K/V.  The prefill
+// attention kernel (gqa_prefill.hip) gives each (sequence, KV head, 32 positions) one workgroup over all of that
+// sequence's keys, which for a short chunk leaves most of its MFMA columns empty and a
+// ragged batch waiting for its longest sequence.  Here the query rows of a KV head's group
+// form MFMA B operands of 16 columns -- tile w holds tokens 4w .. 4w+3 of the 4 heads,
+// column 16w + n for token 4w + n/4 and head n%4 -- and the keys are split stream-K as in
+// the decode path: every segment (sequence, KV head) holds start + T keys, a range's part
+// of a segment is a piece, a split segment's pieces leave partials that mt_merge_kernel
+// combines.  The arithmetic is the attention kernel's: three BF16 parts of Q, the chunk's
+// own keys at full precision, P in three parts, fp64 accumulation within a piece,
+// integer-valued running max.
+//
+// A workgroup has one wave per column tile (W = 1 or 2 waves for T <= 4 or 8) and there
+// are 4 * CUs / W of them: one wave per SIMD.  Per 32-key window the workgroup copies
+// the window's K rows and V rows (a plane of 8 KB each) from HBM into LDS once -- each wave
+// issues 8/W of the plane's 1 KB copies -- and every wave forms its tile's scores and
+// V^T P^T from them.  The planes form a ring in the order K0 V0 K1 V1 ...: while window i
+// is computed, K of windows i+1 .. i+A+1 and V of windows i+1 .. i+A are in flight.  A = 1
+// for W = 1 and 3 for W = 2 keeps 12 to 14 planes in flight per CU (2A + 3 slots: 40 or 72 KB
+// per workgroup).  Longer chunks are compute-bound here -- every window costs each wave
+// about 2,000 cycles of MFMA and fp64 work for its 16 columns, and T = 16 on four waves
+// measured slower than the prefill attention kernel -- so they take that kernel.  Each wave waits for its own copies, then a fence-free
+// barrier makes the whole plane visible: once after K lands (which also tells every wave
+// that V of the previous window has been read, so its slot may be refilled) and once after
+// V lands.
+
+constexpr int kMtWin = 32;                    // keys per window
+constexpr int kMtPlaneB = kMtWin * kRowB;     // 8 KB: 32 rows of 256 B
+constexpr int kMtTile = 16;                   // query rows per wave: 4 heads x 4 tokens
+constexpr int kMtCopies = kMtWin / 4;         // 1 KB copies per plane (each writes 4 rows)
+
+__host__ __device__ constexpr int mt_ahead(int w) { return w == 1 ? 1 : 3; }
+__host__ __device__ constexpr int mt_slots(int w) { return 2 * mt_ahead(w) + 3; }
+
+// s_waitcnt immediate for vmcnt(n) alone (gfx9: vmcnt bits 3:0 and 15:14, expcnt and
+// lgkmcnt at their maxima).
+constexpr int vmcnt_imm(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
+static_assert(vmcnt_imm(0) == 0x0F70 && vmcnt_imm(16) == 0x4F70, "vmcnt encoding");
+
+// Wait until at most `planes` planes of this wave's copies (kC instructions each) are in
+// flight: the counter retires in issue order, so everything older has landed.  Requests
+// of other kinds issued since (Q operands, stores) only make the wait longer.
+template <int kC>
+__device__ __forceinline__ void mt_wait_planes(int planes) {
+    switch (planes) {
+#define MT_CASE(k) \
+    case k: __builtin_amdgcn_s_waitcnt(vmcnt_imm(k * kC < 63 ? k * kC : 63)); break;
+        MT_CASE(1) MT_CASE(2) MT_CASE(3) MT_CASE(4) MT_CASE(5) MT_CASE(6) MT_CASE(7) MT_CASE(8) MT_CASE(9)
+        MT_CASE(10) MT_CASE(11)
+#undef MT_CASE
+        default: __builtin_amdgcn_s_waitcnt(vmcnt_imm(0)); break;
+    }
+}
+static_assert(7 * (kMtCopies / 2) <= 63 && 3 * kMtCopies <= 63, "vmcnt range");
+
+// Barrier without the memory fence __syncthreads adds (which would wait for every copy in
+// flight).
+__device__ __forceinline__ void mt_barrier() { asm volatile("s_barrier" ::: "memory"); }
+
+int32_t multi_waves(int32_t n_new) { return n_new <= 4 ? 1 : 2; }
+
+// Keys of sequence b's segments: every key its last new token sees (0 for a start outside
+// [0, capacity - T]).
+__device__ __forceinline__ int mt_keys(const PrefillArgs& a, int b) {
+    const int st = a.start[b];
+    return prefill_start_ok(a, st) ? st + a.n_new : 0;
+}
+
+namespace {
+struct MtLayout {
+    size_t q_op, plan, seq_off, part_o, part_ml, chunk_s, total;
+};
+
+MtLayout mt_layout(int32_t batch, int32_t n_new, int32_t n_wgs) {
+    const size_t w = static_cast<size_t>(multi_waves(n_new));
+    const size_t cols = kMtTile * w;
+    const size_t n_slots = static_cast<size_t>(n_wgs) + static_cast<size_t>(kHkv) * batch;
+    auto al = [](size_t x) { return (x + 255) / 256 * 256; };
+    MtLayout l{};
+    l.q_op = 0;
+    l.plan = l.q_op + al(static_cast<size_t>(batch) * kHkv * w * 12 * kWave * sizeof(uint4));
+    l.seq_off = l.plan + 256;
+    l.part_o = l.seq_off + al((static_cast<size_t>(batch) + 1) * sizeof(int64_t));
+    l.part_ml = l.part_o + al(n_slots * cols * kD * sizeof(double));
+    l.chunk_s = l.part_ml + al(n_slots * cols * sizeof(float2));
+    l.total = l.chunk_s + al(static_cast<size_t>(batch) * kHkv * cols * 4 * w * sizeof(float));
+    return l;
+}
+}  // namespace
+
+size_t prefill_multi_bytes(int32_t batch, int32_t n_new, int32_t n_wgs) {
+    return mt_layout(batch, n_new, n_wgs).total;
+}
+
+void prefill_multi_layout(PrefillArgs& a, void* base, int32_t n_wgs) {
+    const MtLayout l = mt_layout(a.batch, a.n_new, n_wgs);
+    char* p = static_cast<char*>(base);
+    a.q_op = reinterpret_cast<uint4*>(p + l.q_op);
+    a.plan_hdr = reinterpret_cast<int64_t*>(p + l.plan);
+    a.seq_off = reinterpret_cast<int64_t*>(p + l.seq_off);
+    a.part_o = reinterpret_cast<double*>(p + l.part_o);
+    a.part_ml = reinterpret_cast<float2*>(p + l.part_ml);
+    a.chunk_s = reinterpret_cast<float*>(p + l.chunk_s);
+    a.n_wgs = n_wgs;
+}
+
+// The stream-K plan (one wave): seq_off[b] = stream position of sequence b's first segment,
+// seq_off[B] = total, header {total, positions per workgroup, lead, XCD extra}
+// (gqa_streamk.h).
+__device__ __forceinline__ void mt_build_plan(const PrefillArgs& a, int lane) {
+    int64_t sum = 0;
+    int max_keys = 0, n_seq = 0;
+    // The first 64 sequences' keys are kept for the scan below (the header stores between
+    // the two passes would otherwise make the compiler load them again).
+    const int k_first = lane < a.batch ? mt_keys(a, lane) : 0;
+    for (int base = 0; base < a.batch; base += kWave) {
+        const int b = base + lane;
+        const int k = base == 0 ? k_first : (b < a.batch ? mt_keys(a, b) : 0);
+        sum += wave_sum_i64(k);
+        max_keys = max(max_keys, static_cast<int>(wave_max_i64(k)));
+        n_seq += static_cast<int>(wave_sum_i64(k > 0 ? 1 : 0));
+    }
+    int lead;
+    int64_t total, per_wg;
+    plan_lead_totals(sum, max_keys, n_seq, a.n_wgs, lead, total, per_wg);
+    if (lane == 0) {
+        a.plan_hdr[0] = total;
+        a.plan_hdr[1] = per_wg;
+        a.plan_hdr[2] = lead;
+        a.plan_hdr[3] = range_extra(per_wg, a.skew_pm);
+        a.seq_off[a.batch] = total;
+    }
+    int64_t carry = 0;
+    for (int base = 0; base < a.batch; base += kWave) {
+        const int b = base + lane;
+        const int k = base == 0 ? k_first : (b < a.batch ? mt_keys(a, b) : 0);
+        const int span = k > 0 ? k + lead : 0;
+        const int64_t incl = wave_incl_scan_i64(span, lane) + carry;
+        if (b < a.batch) a.seq_off[b] = (incl - span) * kHkv;
+        carry = __shfl(incl, kWave - 1);
+    }
+}
+
+// Four consecutive BF16 values from p: one 8-byte load when the tensor is 16-byte aligned
+// (kVec; p is then a multiple of 4 elements past an aligned row start), else four 2-byte
+// loads.
+template <bool kVec>
+__device__ __forceinline__ void load4(const uint16_t* p, uint16_t (&h)[4]) {
+    if (kVec) {
+        const uint2 v = *reinterpret_cast<const uint2*>(p);
+        h[0] = static_cast<uint16_t>(v.x & 0xFFFFu);
+        h[1] = static_cast<uint16_t>(v.x >> 16);
+        h[2] = static_cast<uint16_t>(v.y & 0xFFFFu);
+        h[3] = static_cast<uint16_t>(v.y >> 16);
+    } else {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) h[i] = p[i];
+    }
+}
+
+// Per (sequence b, KV head kvh), four waves; wave w:
+//  - the KV append of this head's new rows u = w, w + 4, ... (what kv_append_kernel does
+//    for all heads): lane i rotates the pair (i, i + 64) at position start + u in double
+//    and writes it rounded to BF16, and copies the V row;
+//  - a quarter of the Q operands of every column tile: lane (g, n) of tile tau holds
+//    column 16 tau + n (token 4 tau + n/4, Q head 4*kvh + n%4) at dims 32kb + 8g + j; wave
+//    w takes kb = w & 1 and its pair kb + 2, j in [4(w >> 1), +4), rotated at the token's
+//    position and scaled by scale*log2(e) in double, split into three BF16 parts; columns
+//    of tokens t >= T are zero;
+//  - the same dims' share of the scores of the chunk's own keys (key start + u, u < T:
+//    the new K row rotated at its position and not rounded, as the reference rotates K)
+//    against every column, in double.  The four shares are added in a fixed order and
+//    rounded once to f32: the stream kernel takes these scores in place of the ones it
+//    would form from the cache's rounded copy of those rows.
+// Row B of the grid builds the plan.  A sequence whose start is out of range gets NaN
+// rows and no cache write.
+template <bool kVec, int kW>
+__global__ __launch_bounds__(256) void mt_prepare_kernel(PrefillArgs a) {
+    constexpr int kCols = kMtTile * kW;
+    constexpr int kU = 4 * kW;                // chunk keys per column held (>= T)
+    const int kvh = blockIdx.x;
+    const int b = blockIdx.y;
+    const int w = threadIdx.x >> 6;
+    const int lane = threadIdx.x & (kWave - 1);
+    if (b == a.batch) {
+        if (kvh == 0 && w == 0) mt_build_plan(a, lane);
+        return;
+    }
+    const int T = a.n_new;
+    const int st = a.start[b];
+    // Every load before any store or barrier (a store may alias them as far as the compiler
+    // knows, and a load placed after it or after the barrier would wait for it): the append
+    // rows, Q, and the chunk's K rows at this lane's dims.
+    const int g = lane >> 4;
+    const int n = lane & 15;
+    const int kbp = w & 1;
+    const int d0 = 32 * kbp + 8 * g + 4 * (w >> 1);
+    uint16_t akx[kW], aky[kW], avx[kW], avy[kW];
+#pragma unroll
+    for (int r = 0; r < kW; ++r) {
+        const int u = w + 4 * r;
+        akx[r] = aky[r] = avx[r] = avy[r] = 0;
+        if (u < T) {
+            const int64_t row = ((static_cast<int64_t>(b) * T + u) * kHkv + kvh) * kD;
+            akx[r] = a.k_new[row + lane];
+            aky[r] = a.k_new[row + lane + kPairs];
+            avx[r] = a.v_new[row + lane];
+            avy[r] = a.v_new[row + lane + kPairs];
+        }
+    }
+    uint16_t qx[kW][4], qy[kW][4];
+#pragma unroll
+    for (int tau = 0; tau < kW; ++tau) {
+        const int tc = min(4 * tau + (n >> 2), T - 1);
+        const uint16_t* qrow = a.q + ((static_cast<int64_t>(b) * T + tc) * kHq + kvh * kGroup + (n & 3)) * kD;
+        load4<kVec>(qrow + d0, qx[tau]);
+        load4<kVec>(qrow + d0 + kPairs, qy[tau]);
+    }
+    uint16_t kxh[kU][4], kyh[kU][4];
+#pragma unroll
+    for (int u = 0; u < kU; ++u) {
+        if (u < T) {
+            const uint16_t* krow = a.k_new + ((static_cast<int64_t>(b) * T + u) * kHkv + kvh) * kD;
+            load4<kVec>(krow + d0, kxh[u]);
+            load4<kVec>(krow + d0 + kPairs, kyh[u]);
+        }
+    }
+    if (!prefill_start_ok(a, st)) {
+        for (int i = threadIdx.x; i < T * kGroup * (kD / 4); i += blockDim.x) {
+            const int tt = i / (kGroup * (kD / 4));
+            const int r = i % (kGroup * (kD / 4));
+            uint2* o = reinterpret_cast<uint2*>(a.out + ((static_cast<int64_t>(b) * T + tt) * kHq + kvh * kGroup) * kD);
+            o[r] = make_uint2(0x7fc07fc0u, 0x7fc07fc0u);
+        }
+        return;
+    }
+    // sin and cos of (start + u) * inv_freq[i]: wave u % 4, lane i.
+    __shared__ double sn_s[kU][kPairs], cs_s[kU][kPairs];
+    __shared__ double part_s[4][kU][kCols];
+    const bool rope_q = (a.flags & 1u) != 0;
+    const bool rope_k = (a.flags & 2u) != 0;
+    if (rope_q || rope_k)
+        for (int u = w; u < T; u += 4)
+            rope_sincos(static_cast<int64_t>(st) + u, a.rope.inv_freq[lane], sn_s[u][lane], cs_s[u][lane]);
+    __syncthreads();
+
+    double qvx[kW][4], qvy[kW][4];
+#pragma unroll
+    for (int tau = 0; tau < kW; ++tau) {
+        const int t = 4 * tau + (n >> 2);
+        const bool col = t < T;
+        const int tc = col ? t : T - 1;
+#pragma unroll
+        for (int jj = 0; jj < 4; ++jj) {
+            const int d = d0 + jj;
+            const double x = bf16_to_f32(qx[tau][jj]);
+            const double y = bf16_to_f32(qy[tau][jj]);
+            double xr = x, yr = y;
+            if (rope_q) {
+                const double sn = sn_s[tc][d], cs = cs_s[tc][d];
+                xr = x * cs - y * sn;
+                yr = x * sn + y * cs;
+            }
+            qvx[tau][jj] = col ? xr * a.qk_scale_log2 : 0.0;
+            qvy[tau][jj] = col ? yr * a.qk_scale_log2 : 0.0;
+        }
+    }
+    // This wave's share of the chunk-key scores, summed over the four lanes of each column.
+#pragma unroll
+    for (int u = 0; u < kU; ++u) {
+        double kxr[4] = {0.0, 0.0, 0.0, 0.0}, kyr[4] = {0.0, 0.0, 0.0, 0.0};
+        if (u < T) {
+#pragma unroll
+            for (int jj = 0; jj < 4; ++jj) {
+                const double x = bf16_to_f32(kxh[u][jj]);
+                const double y = bf16_to_f32(kyh[u][jj]);
+                kxr[jj] = x;
+                kyr[jj] = y;
+                if (rope_k) {
+                    const double sn = sn_s[u][d0 + jj], cs = cs_s[u][d0 + jj];
+                    kxr[jj] = x * cs - y * sn;
+                    kyr[jj] = x * sn + y * cs;
+                }
+            }
+        }
+#pragma unroll
+        for (int tau = 0; tau < kW; ++tau) {
+            double acc = 0.0;
+#pragma unroll
+            for (int jj = 0; jj < 4; ++jj) {
+                acc = fma(qvx[tau][jj], kxr[jj], acc);
+                acc = fma(qvy[tau][jj], kyr[jj], acc);
+            }
+            acc += __shfl_xor(acc, 16);
+            acc += __shfl_xor(acc, 32);
+            if (g == 0) part_s[w][u][kMtTile * tau + n] = acc;
+        }
+    }
+
+    // Stores: the appended cache rows, this wave's quarter of the Q operands.
+#pragma unroll
+    for (int r = 0; r < kW; ++r) {
+        const int u = w + 4 * r;
+        if (u < T) {
+            const int64_t ce = cache_elem(a, b, kvh, static_cast<int64_t>(st) + u);
+            double xr = bf16_to_f32(akx[r]), yr = bf16_to_f32(aky[r]);
+            if (rope_k) {
+                const double x = xr, y = yr;
+                xr = x * cs_s[u][lane] - y * sn_s[u][lane];
+                yr = x * sn_s[u][lane] + y * cs_s[u][lane];
+            }
+            if (ce >= 0) {
+                a.k[ce + lane] = bf16_of(xr);
+                a.k[ce + lane + kPairs] = bf16_of(yr);
+                a.v[ce + lane] = avx[r];
+                a.v[ce + lane + kPairs] = avy[r];
+            }
+        }
+    }
+#pragma unroll
+    for (int tau = 0; tau < kW; ++tau) {
+        uint4* base = a.q_op + ((static_cast<int64_t>(b) * kHkv + kvh) * kW + tau) * 12 * kWave + lane;
+#pragma unroll
+        for (int s = 0; s < 3; ++s) {
+            uint16_t px[4], py[4];
+#pragma unroll
+            for (int jj = 0; jj < 4; ++jj) {
+                px[jj] = split3(qvx[tau][jj], s);
+                py[jj] = split3(qvy[tau][jj], s);
+            }
+            uint2* dx = reinterpret_cast<uint2*>(base + (s * 4 + kbp) * kWave) + (w >> 1);
+            uint2* dy = reinterpret_cast<uint2*>(base + (s * 4 + kbp + 2) * kWave) + (w >> 1);
+            *dx = make_uint2(px[0] | (static_cast<uint32_t>(px[1]) << 16), px[2] | (static_cast<uint32_t>(px[3]) << 16));
+            *dy = make_uint2(py[0] | (static_cast<uint32_t>(py[1]) << 16), py[2] | (static_cast<uint32_t>(py[3]) << 16));
+        }
+    }
+    __syncthreads();
+    float* cs_out = a.chunk_s + (static_cast<int64_t>(b) * kHkv + kvh) * kCols * kU;
+    for (int i = threadIdx.x; i < kCols * kU; i += blockDim.x) {
+        const int c = i / kU;
+        const int u = i % kU;
+        cs_out[i] = static_cast<float>(((part_s[0][u][c] + part_s[1][u][c]) + part_s[2][u][c]) + part_s[3][u][c]);
+    }
+}
+
+// This wave's share (copies [wv * kC, (wv + 1) * kC)) of one plane: K or V rows of the
+// window of keys [key0, key0 + 32) of a segment (rows past k_last repeat row k_last), into
+// the ring slot at `dst`, nontemporal (each row is read once): lane l of copy ii writes row
+// 4ii + l/16, chunk position l%16, the chunk it fetches swizzled as in the attention
+// kernel.
+template <int kC>
+__device__ __forceinline__ void mt_issue_plane(const char* seg, int64_t row_bytes, int key0, int k_last,
+                                               uint8_t* dst, int wv, int lane) {
+    constexpr int kNt = 2;     // cache policy: nontemporal
+    int64_t off[kC];
+#pragma unroll
+    for (int q = 0; q < kC; ++q) {
+        const int r = 4 * (wv * kC + q) + (lane >> 4);
+        const int c = (lane & 15) ^ pf_swz(r);
+        off[q] = static_cast<int64_t>(min(key0 + r, k_last)) * row_bytes + 16 * c;
+    }
+#pragma unroll
+    for (int q = 0; q < kC; ++q)
+        __builtin_amdgcn_global_load_lds(seg + off[q], (lds_void_t*)(dst + (wv * kC + q) * 1024), 16, 0, kNt);
+}
+
+// Running state of a piece in lane (g, n): O^T[16dt + 4g + i][column n] in fp64, the
+// lane's share of the column's sum, and the column's running max (log2 units, integer-
+// valued; -inf until the piece has seen a key the column may attend to).
+struct MtState {
+    double o64[8][4];
+    double l64;
+    float m_run;
+};
+
+// One 32-key window [key0, key0 + 32) of a piece ending at k_b: scores, online softmax,
+// V^T P^T for this wave's tile.  `lim` = the last key this lane's column may attend to
+// (start + t).  Chunk keys (>= st) take the scores the preparation formed from their
+// unrounded rows (`cs`: this lane's column against chunk keys u = 0 .. kU-1).  nv = planes
+// of this wave's copies younger than this window's V.
+template <bool kChunkKeys, int kW>
+__device__ __forceinline__ void mt_window(const PrefillArgs& a, const uint8_t* kplane, uint32_t vbase,
+                                          const bf16x8_t (&qop)[3][4], const float (&cs)[4 * kW], int st,
+                                          int key0, int k_b, int lim, int nv, int lane, MtState& t) {
+    const int n = lane & 15;
+    const int g = lane >> 4;
+    f32x4_t sacc[2] = {f32x4_t{0.f, 0.f, 0.f, 0.f}, f32x4_t{0.f, 0.f, 0.f, 0.f}};
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb) {
+        bf16x8_t ak[2];
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt) ak[kt] = pf_k_chunk(kplane, 16 * kt + n, 4 * kb + g);
+#pragma unroll
+        for (int s = 0; s < 3; ++s)
+#pragma unroll
+            for (int kt = 0; kt < 2; ++kt)
+                sacc[kt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ak[kt], qop[s][kb], sacc[kt], 0, 0, 0);
+    }
+    if (kChunkKeys) {
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int u = key0 + 16 * kt + 4 * g + i - st;
+                if (u >= 0 && u < a.n_new) {
+                    float v = cs[0];
+#pragma unroll
+                    for (int q = 1; q < 4 * kW; ++q) v = u == q ? cs[q] : v;
+                    sacc[kt][i] = v;
+                }
+            }
+    }
+    // Mask (keys past the piece or past the column's token), window max per column.
+    float bmax = -INFINITY;
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int key = key0 + 16 * kt + 4 * g + i;
+            if (key >= k_b || key > lim) sacc[kt][i] = -INFINITY;
+            bmax = fmaxf(bmax, sacc[kt][i]);
+        }
+    bmax = swap32_max(swap16_max(bmax));
+    const float m_new = bmax > t.m_run ? ceilf(bmax) : t.m_run;
+    if (__ballot(m_new != t.m_run)) {
+        const int shift = (t.m_run == -INFINITY) ? 0 : static_cast<int>(t.m_run - m_new);
+#pragma unroll
+        for (int dt = 0; dt < 8; ++dt)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) t.o64[dt][i] = ldexp(t.o64[dt][i], shift);
+        t.l64 = ldexp(t.l64, shift);
+        t.m_run = m_new;
+    }
+    // A column that has seen no key yet keeps m = -inf and p = 0 (every score -inf).
+    const float m_eff = t.m_run == -INFINITY ? 0.f : t.m_run;
+    uint32_t ph[3][2][4];
+    float lsum = 0.f;
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt) pf_probs_tile(sacc[kt], m_eff, lsum, ph, kt);
+    t.l64 += static_cast<double>(lsum);
+
+    mt_wait_planes<kMtCopies / kW>(nv);
+    mt_barrier();
+    // V^T P^T: dim tile dt from two transposed reads (rows 4g + a/4 and 16 rows on).
+    bf16x8_t pb[3];
+#pragma unroll
+    for (int s = 0; s < 3; ++s) pb[s] = as_bf16x8(make_uint4(ph[s][0][0], ph[s][0][1], ph[s][0][2], ph[s][0][3]));
+#pragma unroll
+    for (int d0 = 0; d0 < 8; d0 += 2) {
+        short4_t r[2][2];
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+            const uint32_t ad = vbase + vt_tr_offset(d0 + e, lane);
+            asm volatile("ds_read_b64_tr_b16 %0, %1" : "=v"(r[e][0]) : "v"(ad));
+            asm volatile("ds_read_b64_tr_b16 %0, %1 offset:4096" : "=v"(r[e][1]) : "v"(ad));
+        }
+        asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(r[0][0]), "+v"(r[0][1]), "+v"(r[1][0]), "+v"(r[1][1]));
+        f32x4_t oacc[2];
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+            union {
+                short4_t h[2];
+                bf16x8_t v;
+            } u;
+            u.h[0] = r[e][0];
+            u.h[1] = r[e][1];
+            oacc[e] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int s = 0; s < 3; ++s) oacc[e] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(u.v, pb[s], oacc[e], 0, 0, 0);
+        }
+#pragma unroll
+        for (int e = 0; e < 2; ++e)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) t.o64[d0 + e][i] += static_cast<double>(oacc[e][i]);
+    }
+}
+
+// End of a piece: the column sums over the four rows; a whole segment writes its output
+// rows (tokens < T), a split one its partial at slot wg + segment, columns 16 wv + n, in
+// fp64 (an output that cancels to near zero needs the partials' full precision).
+template <int kW>
+__device__ __forceinline__ void mt_piece_end(const PrefillArgs& a, int b, int kvh, bool whole, int64_t slot,
+                                             int wv, int lane, MtState& t) {
+    const int n = lane & 15;
+    const int g = lane >> 4;
+    const double l = swap_add_f64<true>(swap_add_f64<false>(t.l64));
+    if (whole) {
+        const int tok = 4 * wv + (n >> 2);
+        if (tok >= a.n_new) return;
+        uint16_t* orow = a.out + ((static_cast<int64_t>(b) * a.n_new + tok) * kHq + kvh * kGroup + (n & 3)) * kD;
+#pragma unroll
+        for (int dt = 0; dt < 8; ++dt) {
+            uint2 pk;
+            pk.x = f32_to_bf16_rne(static_cast<float>(t.o64[dt][0] / l)) |
+                   (static_cast<uint32_t>(f32_to_bf16_rne(static_cast<float>(t.o64[dt][1] / l))) << 16);
+            pk.y = f32_to_bf16_rne(static_cast<float>(t.o64[dt][2] / l)) |
+                   (static_cast<uint32_t>(f32_to_bf16_rne(static_cast<float>(t.o64[dt][3] / l))) << 16);
+            *reinterpret_cast<uint2*>(orow + 16 * dt + 4 * g) = pk;
+        }
+        return;
+    }
+    const int64_t col = slot * (kMtTile * kW) + kMtTile * wv + n;
+    double* po = a.part_o + col * kD;
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt) {
+        double2* d = reinterpret_cast<double2*>(po + 16 * dt + 4 * g);
+        d[0] = make_double2(t.o64[dt][0], t.o64[dt][1]);
+        d[1] = make_double2(t.o64[dt][2], t.o64[dt][3]);
+    }
+    if (g == 0) a.part_ml[col] = make_float2(t.m_run, static_cast<float>(l));
+}
+
+// Sequence windows of the plan: o = seq_off[base + lane], o1 = seq_off[base + lane + 1].
+struct MtWindow {
+    int base;
+    int64_t o, o1;
+};
+
+__device__ __forceinline__ void mt_load_window(const PrefillArgs& a, int base, MtWindow& w) {
+    const int bb = base + static_cast<int>(threadIdx.x & (kWave - 1));
+    w.base = base;
+    w.o = bb < a.batch ? a.seq_off[bb] : INT64_MAX;
+    w.o1 = bb < a.batch ? a.seq_off[bb + 1] : INT64_MAX;
+}
+
+// The segment after (b, kvh) that has keys; false when there is none.
+__device__ __forceinline__ bool mt_next_segment(const PrefillArgs& a, MtWindow& w, int lead, int& b, int& kvh,
+                                                int& nk) {
+    if (kvh + 1 < kHkv) {
+        ++kvh;
+        return true;
+    }
+    kvh = 0;
+    while (true) {
+        const int bb = w.base + static_cast<int>(threadIdx.x & (kWave - 1));
+        const uint64_t m = __ballot(bb < a.batch && bb > b && w.o1 > w.o);
+        if (m) {
+            const int j = __ffsll(static_cast<unsigned long long>(m)) - 1;
+            b = w.base + j;
+            nk = static_cast<int>((__shfl(w.o1, j) - __shfl(w.o, j)) / kHkv) - lead;
+            return true;
+        }
+        if (w.base + kWave >= a.batch) return false;
+        mt_load_window(a, w.base + kWave, w);
+    }
+}
+
+// A position in a workgroup's window stream: piece keys [pk, k_b) of segment (b, kvh)
+// (nk keys), current window at key kw, x = stream position of key pk; `sw` is the plan's
+// sequence window around b.  mt_advance moves to the next window of the piece, else to the
+// first window of the next piece, else marks the cursor invalid.
+struct MtCursor {
+    int b, kvh, nk, pk, k_b, kw;
+    int64_t x;
+    bool valid;
+    MtWindow sw;
+};
+
+__device__ __forceinline__ void mt_advance(const PrefillArgs& a, MtCursor& c, int64_t x_end, int lead) {
+    if (c.kw + kMtWin < c.k_b) {
+        c.kw += kMtWin;
+        return;
+    }
+    const int64_t x_next = c.x + (c.k_b - c.pk);
+    int b = c.b, kvh = c.kvh, nk = c.nk;
+    bool more = x_next + lead < x_end;
+    if (more) more = mt_next_segment(a, c.sw, lead, b, kvh, nk);
+    if (!more) {
+        c.valid = false;
+        return;
+    }
+    c.b = __builtin_amdgcn_readfirstlane(b);
+    c.kvh = __builtin_amdgcn_readfirstlane(kvh);
+    c.nk = __builtin_amdgcn_readfirstlane(nk);
+    c.x = uniform_i64(x_next + lead);
+    c.pk = 0;
+    c.kw = 0;
+    c.k_b = __builtin_amdgcn_readfirstlane(static_cast<int>(min(static_cast<int64_t>(c.nk), x_end - c.x)));
+}
+
+template <int kW>
+__global__ __launch_bounds__(kWave * kW) __attribute__((amdgpu_waves_per_eu(1))) void mt_stream_kernel(PrefillArgs a) {
+    constexpr int kA = mt_ahead(kW);
+    constexpr int kS = mt_slots(kW);
+    constexpr int kC = kMtCopies / kW;
+    constexpr int kU = 4 * kW;
+    __shared__ __attribute__((aligned(1024))) uint8_t lds[kS * kMtPlaneB];
+    MtWindow w0;
+    mt_load_window(a, 0, w0);
+    const int64_t wg = blockIdx.x;
+    const int64_t total = a.plan_hdr[0];
+    const int64_t per_wg = a.plan_hdr[1];
+    const int lead = static_cast<int>(a.plan_hdr[2]);
+    const int64_t extra = a.plan_hdr[3];
+    int64_t x = range_start(per_wg, extra, wg);
+    if (x >= total) return;
+    const int64_t x_end = min(range_start(per_wg, extra, wg + 1), total);
+    const int wv = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
+    const int lane = threadIdx.x & (kWave - 1);
+    const int n = lane & 15;
+    const int64_t row_bytes = a.kv_pos_stride * 2;
+    const uint32_t lds_base = static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_void_t*)(lds)));
+
+    // First piece: the last sequence b with seq_off[b] <= x.
+    MtCursor c;
+    int64_t off = 0, next = 0;
+    c.b = 0;
+    for (int base = 0; base < a.batch; base += kWave) {
+        MtWindow t = w0;
+        if (base > 0) mt_load_window(a, base, t);
+        const uint64_t le = __ballot(t.o <= x);
+        if (le) {
+            const int j = 63 - __clzll(static_cast<long long>(le));
+            c.b = base + j;
+            off = __shfl(t.o, j);
+            next = __shfl(t.o1, j);
+            c.sw = t;
+        }
+    }
+    int kvh, key, nk;
+    locate_first_piece(off, next, lead, x, kvh, key, nk);
+    c.x = uniform_i64(x);
+    c.b = __builtin_amdgcn_readfirstlane(c.b);
+    c.kvh = __builtin_amdgcn_readfirstlane(kvh);
+    c.pk = __builtin_amdgcn_readfirstlane(key);
+    c.kw = c.pk;
+    c.nk = __builtin_amdgcn_readfirstlane(nk);
+    c.k_b = __builtin_amdgcn_readfirstlane(static_cast<int>(min(static_cast<int64_t>(c.nk), c.pk + (x_end - c.x))));
+    c.valid = true;
+
+    auto seg_base = [&](const uint16_t* base, int bb, int hh) {
+        return reinterpret_cast<const char*>(base + static_cast<int64_t>(bb) * a.kv_batch_stride +
+                                             static_cast<int64_t>(hh) * a.kv_head_stride);
+    };
+    auto slot_ptr = [&](int sl) { return lds + (sl >= kS ? sl - kS : sl) * kMtPlaneB; };
+    auto issue = [&](const uint16_t* base, const MtCursor& q, int sl) {
+        mt_issue_plane<kC>(seg_base(base, q.b, q.kvh), row_bytes, q.kw, q.k_b - 1, slot_ptr(sl), wv, lane);
+    };
+    // The producer p is the last window whose K copies were requested; the consumer c's
+    // window has K in slot `slot` and V in the next one.  kq = windows after c's whose K
+    // has been requested (at most kA before the window's own requests).
+    MtCursor p = c;
+    int slot = 0, kq = 0;
+    issue(a.k, p, 0);
+#pragma unroll
+    for (int j = 0; j < kA; ++j) {
+        if (p.valid) {
+            issue(a.v, p, 2 * j + 1);
+            mt_advance(a, p, x_end, lead);
+            if (p.valid) {
+                issue(a.k, p, 2 * j + 2);
+                ++kq;
+            }
+        }
+    }
+
+    while (true) {
+        // This piece: Q operands, chunk-key scores, start, window loop.
+        const int st = a.start[c.b];
+        const int64_t seg = static_cast<int64_t>(c.b) * kHkv + c.kvh;
+        bf16x8_t qop[3][4];
+        {
+            const uint4* src = a.q_op + (seg * kW + wv) * 12 * kWave + lane;
+#pragma unroll
+            for (int s = 0; s < 3; ++s)
+#pragma unroll
+                for (int kb = 0; kb < 4; ++kb) qop[s][kb] = as_bf16x8(src[(s * 4 + kb) * kWave]);
+        }
+        float cs[kU];
+        {
+            const float4* src = reinterpret_cast<const float4*>(a.chunk_s + (seg * (kMtTile * kW) + kMtTile * wv + n) * kU);
+#pragma unroll
+            for (int q = 0; q < kW; ++q) {
+                const float4 v = src[q];
+                cs[4 * q] = v.x;
+                cs[4 * q + 1] = v.y;
+                cs[4 * q + 2] = v.z;
+                cs[4 * q + 3] = v.w;
+            }
+        }
+        const int lim = st + min(4 * wv + (n >> 2), a.n_new - 1);
+        MtState t;
+#pragma unroll
+        for (int dt = 0; dt < 8; ++dt)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) t.o64[dt][i] = 0.0;
+        t.l64 = 0.0;
+        t.m_run = -INFINITY;
+
+        for (;;) {
+            // Request V of the producer's window (kA after this one) and, once every wave
+            // is done with the previous window, K of the window after it.
+            const bool iv = p.valid;
+            if (iv) issue(a.v, p, slot + 2 * kA + 1);
+            mt_wait_planes<kC>(1 + 2 * kq);
+            mt_barrier();
+            bool ik = false;
+            if (iv) {
+                mt_advance(a, p, x_end, lead);
+                if (p.valid) {
+                    issue(a.k, p, slot + 2 * kA + 2);
+                    ik = true;
+                }
+            }
+            const int nv = 2 * kq + (ik ? 1 : 0);
+            const uint8_t* kplane = slot_ptr(slot);
+            const uint32_t vbase = lds_base + (slot + 1 >= kS ? slot + 1 - kS : slot + 1) * kMtPlaneB;
+            if (c.kw + kMtWin > st)
+                mt_window<true, kW>(a, kplane, vbase, qop, cs, st, c.kw, c.k_b, lim, nv, lane, t);
+            else
+                mt_window<false, kW>(a, kplane, vbase, qop, cs, st, c.kw, c.k_b, lim, nv, lane, t);
+            slot = slot + 2 >= kS ? slot + 2 - kS : slot + 2;
+            kq = ik ? kq : kq - 1;
+            if (c.kw + kMtWin >= c.k_b) break;
+            c.kw += kMtWin;
+        }
+        mt_piece_end<kW>(a, c.b, c.kvh, c.pk == 0 && c.k_b == c.nk, wg + seg, wv, lane, t);
+        mt_advance(a, c, x_end, lead);
+        if (!c.valid) break;
+    }
+}
+
+// Merge the pieces of split segments: one workgroup per (KV head, sequence), 16 threads per
+// column: thread i handles column i/16 (token c/4, head c%4), dims 8(i%16) .. +8.  Weights
+// 2^(m - max) are exact; a piece that saw no key the column may attend to has m = -inf and
+// weight 0.
+template <int kW>
+__global__ __launch_bounds__(256 * kW) void mt_merge_kernel(PrefillArgs a) {
+    constexpr int kCols = kMtTile * kW;
+    const int kvh = blockIdx.x;
+    const int b = blockIdx.y;
+    const int64_t per_wg = a.plan_hdr[1];
+    const int lead = static_cast<int>(a.plan_hdr[2]);
+    const int64_t extra = a.plan_hdr[3];
+    const int64_t off = a.seq_off[b];
+    const int span = static_cast<int>((a.seq_off[b + 1] - off) / kHkv);
+    if (span == 0) return;
+    const int nk = span - lead;
+    const int64_t seg_off = off + static_cast<int64_t>(kvh) * span + lead;
+    const int64_t w_first = range_of(per_wg, extra, seg_off);
+    const int n_pieces = static_cast<int>(range_of(per_wg, extra, seg_off + nk - 1) - w_first) + 1;
+    if (n_pieces == 1) return;
+    const int64_t slot0 = w_first + static_cast<int64_t>(b) * kHkv + kvh;
+    const int col = threadIdx.x >> 4;
+    const int d0 = 8 * (threadIdx.x & 15);
+    const int tok = col >> 2;
+    if (tok >= a.n_new) return;
+    // Pieces four at a time, every load of a group issued before any is used (one memory
+    // round trip per group); the running max moves by whole powers of two, so rescaling
+    // what is already summed is exact.
+    constexpr int kGroupP = 4;
+    float m = -INFINITY;
+    double l = 0.0, o[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    for (int p0 = 0; p0 < n_pieces; p0 += kGroupP) {
+        float2 ml[kGroupP];
+        double v[kGroupP][8];
+#pragma unroll
+        for (int q = 0; q < kGroupP; ++q) {
+            ml[q] = make_float2(-INFINITY, 0.f);
+            if (p0 + q < n_pieces) {
+                const int64_t c = (slot0 + p0 + q) * kCols + col;
+                ml[q] = a.part_ml[c];
+                const double* po = a.part_o + c * kD + d0;
+#pragma unroll
+                for (int j = 0; j < 8; ++j) v[q][j] = po[j];
+            }
+        }
+        float mb = m;
+#pragma unroll
+        for (int q = 0; q < kGroupP; ++q) mb = fmaxf(mb, ml[q].x);
+        if (m != -INFINITY && mb != m) {
+            const int e = static_cast<int>(m - mb);
+            l = ldexp(l, e);
+#pragma unroll
+            for (int j = 0; j < 8; ++j) o[j] = ldexp(o[j], e);
+        }
+        m = mb;
+#pragma unroll
+        for (int q = 0; q < kGroupP; ++q) {
+            if (ml[q].x == -INFINITY) continue;
+            const int e = static_cast<int>(ml[q].x - m);
+            l += ldexp(static_cast<double>(ml[q].y), e);
+#pragma unroll
+            for (int j = 0; j < 8; ++j) o[j] += ldexp(v[q][j], e);
+        }
+    }
+    uint16_t h8[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) h8[j] = f32_to_bf16_rne(static_cast<float>(o[j] / l));
+    uint2* dst = reinterpret_cast<uint2*>(a.out + ((static_cast<int64_t>(b) * a.n_new + tok) * kHq + kvh * kGroup +
+                                                   (col & 3)) * kD + d0);   // out is 8-byte aligned
+    dst[0] = make_uint2(h8[0] | (static_cast<uint32_t>(h8[1]) << 16), h8[2] | (static_cast<uint32_t>(h8[3]) << 16));
+    dst[1] = make_uint2(h8[4] | (static_cast<uint32_t>(h8[5]) << 16), h8[6] | (static_cast<uint32_t>(h8[7]) << 16));
+}
+
+template <int kW>
+hipError_t launch_multi_w(const PrefillArgs& a, hipStream_t stream, hipEvent_t* ev) {
+    const bool vec = (reinterpret_cast<uintptr_t>(a.q) % 16) == 0 && (reinterpret_cast<uintptr_t>(a.k_new) % 16) == 0;
+    const dim3 grid(kHkv, static_cast<unsigned>(a.batch) + 1);
+    if (vec)
+        hipLaunchKernelGGL((mt_prepare_kernel<true, kW>), grid, dim3(256), 0, stream, a);
+    else
+        hipLaunchKernelGGL((mt_prepare_kernel<false, kW>), grid, dim3(256), 0, stream, a);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    if (ev) (void)hipEventRecord(ev[1], stream);
+    hipLaunchKernelGGL(mt_stream_kernel<kW>, dim3(static_cast<unsigned>(a.n_wgs)), dim3(kWave * kW), 0, stream, a);
+    e = hipGetLastError();
+    if (ev) (void)hipEventRecord(ev[2], stream);
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(mt_merge_kernel<kW>, dim3(kHkv, static_cast<unsigned>(a.batch)), dim3(256 * kW), 0, stream, a);
+    return hipGetLastError();
+}
+
+hipError_t launch_prefill_multi(const PrefillArgs& a, hipStream_t stream, hipEvent_t* ev) {
+    if (multi_waves(a.n_new) == 1) return launch_multi_w<1>(a, stream, ev);
+    return launch_multi_w<2>(a, stream, ev);
+}
+
+}  // namespace gqa
