@@ -41,6 +41,10 @@ constexpr int kMtWin = 32;                    // keys per window
 constexpr int kMtPlaneB = kMtWin * kRowB;     // 8 KB: 32 rows of 256 B
 constexpr int kMtTile = 16;                   // query rows per wave: 4 heads x 4 tokens
 constexpr int kMtCopies = kMtWin / 4;         // 1 KB copies per plane (each writes 4 rows)
+// Stream positions charged per segment start: a piece here costs more than in decode (the
+// 12 KB of Q operands, the 16 KB fp64 partial), about two windows' streaming time.  64
+// measured best of 32, 48, 64, 96 (B=64 ragged: T=4 216.5 -> 215.4 us, T=8 308.9 -> 303.8).
+constexpr int kMtSegLead = 64;
 
 __host__ __device__ constexpr int mt_ahead(int w) { return w == 1 ? 1 : 3; }
 __host__ __device__ constexpr int mt_slots(int w) { return 2 * mt_ahead(w) + 3; }
@@ -135,7 +139,7 @@ __device__ __forceinline__ void mt_build_plan(const PrefillArgs& a, int lane) {
     }
     int lead;
     int64_t total, per_wg;
-    plan_lead_totals(sum, max_keys, n_seq, a.n_wgs, lead, total, per_wg);
+    plan_lead_totals(sum, max_keys, n_seq, a.n_wgs, lead, total, per_wg, kMtSegLead);
     if (lane == 0) {
         a.plan_hdr[0] = total;
         a.plan_hdr[1] = per_wg;

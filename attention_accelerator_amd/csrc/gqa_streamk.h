@@ -101,10 +101,18 @@ __device__ __forceinline__ int64_t range_size(int64_t total, int n_wgs) {
 
 // The lead and the stream totals from the batch's keys per segment: their sum over the
 // sequences, their maximum and the number of sequences with keys.
+// seg_lead: the lead a path charges per segment start (kSegLead for decode).  A lead above
+// kSegLead is cut to a quarter of the lead-free range size (never below kSegLead), so that
+// a range always reaches past a lead into keys.
 __device__ __forceinline__ void plan_lead_totals(int64_t sum, int max_keys, int n_seq, int n_wgs, int& lead,
-                                                 int64_t& total, int64_t& per_wg) {
+                                                 int64_t& total, int64_t& per_wg, int seg_lead = kSegLead) {
     const int64_t per0 = range_size(sum * kHkv, n_wgs);
-    lead = static_cast<int64_t>(max_keys) < kLeadRanges * per0 ? kSegLead : 0;
+    int want = seg_lead;
+    if (want > kSegLead) {
+        const int64_t quarter = per0 / 4 / kRangeAlign * kRangeAlign;
+        want = static_cast<int>(max(static_cast<int64_t>(kSegLead), min(static_cast<int64_t>(want), quarter)));
+    }
+    lead = static_cast<int64_t>(max_keys) < kLeadRanges * per0 ? want : 0;
     total = (sum + static_cast<int64_t>(n_seq) * lead) * kHkv;
     per_wg = range_size(total, n_wgs);
 }
