@@ -152,11 +152,12 @@ def test_multi_position_major_cache(dev):
     assert np.array_equal(to_codes(kp), to_codes(kd_ref))
 
 
-def test_multi_invalid_device_start_gives_nan_rows(dev):
+@pytest.mark.parametrize("n_new", [3, 7, 10])
+def test_multi_invalid_device_start_gives_nan_rows(dev, n_new):
     """A device start past capacity - T: NaN rows for that sequence, its cache untouched,
-    the other sequences unaffected."""
-    starts = torch.tensor([40, 98, 7], dtype=torch.int32)   # sequence 1: 98 + 10 > 100
-    q, kn, vn, k, v = _chunk([40, 0, 7], 10, 100, 46)
+    the other sequences unaffected (one- and two-wave stream-K kernels, prefill kernel)."""
+    starts = torch.tensor([40, 98, 7], dtype=torch.int32)   # sequence 1: 98 + T > 100
+    q, kn, vn, k, v = _chunk([40, 0, 7], n_new, 100, 46)
     kd, vd = k.to(dev), v.to(dev)
     out = gqa.gqa_prefill(q.to(dev), kn.to(dev), vn.to(dev), kd, vd, starts.to(dev))
     torch.cuda.synchronize()
@@ -219,3 +220,20 @@ def test_multi_xcd_skew_bounds(dev, monkeypatch, skew):
     want = _oracle(q, kn, vn, k, v, starts)
     got, _, _ = _run(q, kn, vn, k, v, starts, dev)
     _check(want, got, f"multi skew={skew}")
+
+
+def test_multi_long_context_sampled_rows(dev):
+    """131,064 cached positions (the longest decode workload's capacity) and 8 new tokens:
+    the first and last token's rows against the oracle (each sees 131,065 .. 131,072 keys)."""
+    st, n_new, cap = 131064, 8, 131072
+    g = torch.Generator("cpu").manual_seed(50)
+    q = torch.randn((1, n_new, 32, 128), generator=g).to(torch.bfloat16)
+    kn = torch.randn((1, n_new, 8, 128), generator=g).to(torch.bfloat16)
+    vn = torch.randn((1, n_new, 8, 128), generator=g).to(torch.bfloat16)
+    k = torch.randn((1, 8, cap, 128), generator=g).to(torch.bfloat16)
+    v = torch.randn((1, 8, cap, 128), generator=g).to(torch.bfloat16)
+    got, _, _ = _run(q, kn, vn, k, v, [st], dev)
+    rows = [0, n_new - 1]
+    want, want64 = orc.prefill(to_codes(q), to_codes(k), to_codes(v), to_codes(kn), to_codes(vn),
+                               np.asarray([st]), rows=rows, want_f64=True)
+    assert_within_ulp_or_floor(want, got[:, rows], want64, 64, what="multi 131072")
