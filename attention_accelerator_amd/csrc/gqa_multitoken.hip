@@ -32,10 +32,13 @@ namespace gqa {
 // for W = 1 and 3 for W = 2 keeps 12 to 14 planes in flight per CU (2A + 3 slots: 40 or 72 KB
 // per workgroup).  Longer chunks are compute-bound here -- every window costs each wave
 // about 2,000 cycles of MFMA and fp64 work for its 16 columns, and T = 16 on four waves
-// measured slower than the prefill attention kernel -- so they take that kernel.  Each wave waits for its own copies, then a fence-free
-// barrier makes the whole plane visible: once after K lands (which also tells every wave
-// that V of the previous window has been read, so its slot may be refilled) and once after
-// V lands.
+// measured slower than the prefill attention kernel -- so they take that kernel.
+//
+// Each wave forms the next window's scores beside the current window's probabilities.
+// It waits for its own copies, then a fence-free barrier makes the whole plane visible:
+// once per window after the next window's K lands (which also tells every wave that V of
+// the previous window has been read, so its slot may be refilled) and once after the
+// current window's V lands.
 
 constexpr int kMtWin = 32;                    // keys per window
 constexpr int kMtPlaneB = kMtWin * kRowB;     // 8 KB: 32 rows of 256 B
@@ -390,18 +393,14 @@ struct MtState {
     float m_run;
 };
 
-// One 32-key window [key0, key0 + 32) of a piece ending at k_b: scores, online softmax,
-// V^T P^T for this wave's tile.  `lim` = the last key this lane's column may attend to
-// (start + t).  Chunk keys (>= st) take the scores the preparation formed from their
-// unrounded rows (`cs`: this lane's column against chunk keys u = 0 .. kU-1).  nv = planes
-// of this wave's copies younger than this window's V.
-template <bool kChunkKeys, int kW>
-__device__ __forceinline__ void mt_window(const PrefillArgs& a, const uint8_t* kplane, uint32_t vbase,
-                                          const bf16x8_t (&qop)[3][4], const float (&cs)[4 * kW], int st,
-                                          int key0, int k_b, int lim, int nv, int lane, MtState& t) {
+// The stages of one 32-key window [key0, key0 + 32) of a piece ending at k_b, for this
+// wave's tile.  mt_qk: the raw scores S^T = K Q^T of both 16-key tiles from the K plane.
+__device__ __forceinline__ void mt_qk(const uint8_t* kplane, const bf16x8_t (&qop)[3][4], int lane,
+                                      f32x4_t (&sacc)[2]) {
     const int n = lane & 15;
     const int g = lane >> 4;
-    f32x4_t sacc[2] = {f32x4_t{0.f, 0.f, 0.f, 0.f}, f32x4_t{0.f, 0.f, 0.f, 0.f}};
+    sacc[0] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    sacc[1] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int kb = 0; kb < 4; ++kb) {
         bf16x8_t ak[2];
@@ -413,21 +412,33 @@ __device__ __forceinline__ void mt_window(const PrefillArgs& a, const uint8_t* k
             for (int kt = 0; kt < 2; ++kt)
                 sacc[kt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ak[kt], qop[s][kb], sacc[kt], 0, 0, 0);
     }
-    if (kChunkKeys) {
+}
+
+// mt_max: chunk keys (>= st) take the scores the preparation formed from their unrounded
+// rows (`cs`: this lane's column against chunk keys u = 0 .. kU-1); keys past the piece or
+// past the column's token (`lim` = start + t) are masked; the window max per column updates
+// the running max (rescaling O and l by an exact power of two).  Returns the max the
+// probabilities are taken against.
+template <int kU>
+__device__ __forceinline__ float mt_max(const PrefillArgs& a, bool chunk_keys, const float (&cs)[kU], int st,
+                                        int key0, int k_b, int lim, int lane, f32x4_t (&sacc)[2], MtState& t) {
+    const int g = lane >> 4;
+    if (chunk_keys) {
 #pragma unroll
         for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 const int u = key0 + 16 * kt + 4 * g + i - st;
                 if (u >= 0 && u < a.n_new) {
-                    float v = cs[0];
+                    // cs[u] by bit masks (a select chain is turned into an indexed load from
+                    // a stack copy; masking keeps a NaN in another entry out of this one).
+                    uint32_t vb = 0u;
 #pragma unroll
-                    for (int q = 1; q < 4 * kW; ++q) v = u == q ? cs[q] : v;
-                    sacc[kt][i] = v;
+                    for (int q = 0; q < kU; ++q) vb |= __float_as_uint(cs[q]) & (u == q ? 0xFFFFFFFFu : 0u);
+                    sacc[kt][i] = __uint_as_float(vb);
                 }
             }
     }
-    // Mask (keys past the piece or past the column's token), window max per column.
     float bmax = -INFINITY;
 #pragma unroll
     for (int kt = 0; kt < 2; ++kt)
@@ -449,16 +460,25 @@ __device__ __forceinline__ void mt_window(const PrefillArgs& a, const uint8_t* k
         t.m_run = m_new;
     }
     // A column that has seen no key yet keeps m = -inf and p = 0 (every score -inf).
-    const float m_eff = t.m_run == -INFINITY ? 0.f : t.m_run;
-    uint32_t ph[3][2][4];
+    return t.m_run == -INFINITY ? 0.f : t.m_run;
+}
+
+// mt_probs: p = 2^(s - m) in three BF16 parts (the P^T B operand), summed into l.
+__device__ __forceinline__ void mt_probs(const f32x4_t (&sacc)[2], float m_eff, uint32_t (&ph)[3][2][4], MtState& t) {
     float lsum = 0.f;
 #pragma unroll
     for (int kt = 0; kt < 2; ++kt) pf_probs_tile(sacc[kt], m_eff, lsum, ph, kt);
     t.l64 += static_cast<double>(lsum);
+}
 
-    mt_wait_planes<kMtCopies / kW>(nv);
+// mt_pv: once this window's V has landed (nv = planes of this wave's copies, kC
+// instructions each, younger than it) and every wave may read it, O^T += V^T P^T: dim
+// tile dt from two transposed reads (rows 4g + a/4 and 16 rows on), fp32 products added
+// into the fp64 O.
+template <int kC>
+__device__ __forceinline__ void mt_pv(uint32_t vbase, const uint32_t (&ph)[3][2][4], int nv, int lane, MtState& t) {
+    mt_wait_planes<kC>(nv);
     mt_barrier();
-    // V^T P^T: dim tile dt from two transposed reads (rows 4g + a/4 and 16 rows on).
     bf16x8_t pb[3];
 #pragma unroll
     for (int s = 0; s < 3; ++s) pb[s] = as_bf16x8(make_uint4(ph[s][0][0], ph[s][0][1], ph[s][0][2], ph[s][0][3]));
@@ -704,12 +724,21 @@ __global__ __launch_bounds__(kWave * kW) __attribute__((amdgpu_waves_per_eu(1)))
         t.l64 = 0.0;
         t.m_run = -INFINITY;
 
+        // Each window's scores are formed one window ahead, their MFMAs beside the current
+        // window's probabilities (the next window's K plane is in LDS: K runs kA + 1 windows
+        // ahead).  B=64 ragged: T=8 302.4 -> 287.9 us per step, T=4 216.2 -> 215.2.  The
+        // piece's first window's scores are formed here (its V(i + kA) not yet requested).
+        f32x4_t s_cur[2];
+        mt_wait_planes<kC>(kq == kA ? 2 * kA : 1 + 2 * kq);
+        mt_barrier();
+        mt_qk(slot_ptr(slot), qop, lane, s_cur);
         for (;;) {
             // Request V of the producer's window (kA after this one) and, once every wave
             // is done with the previous window, K of the window after it.
             const bool iv = p.valid;
             if (iv) issue(a.v, p, slot + 2 * kA + 1);
-            mt_wait_planes<kC>(1 + 2 * kq);
+            const bool has_next = c.kw + kMtWin < c.k_b;
+            if (has_next) mt_wait_planes<kC>(2 * kq - 1);   // K of the next window landed
             mt_barrier();
             bool ik = false;
             if (iv) {
@@ -720,15 +749,21 @@ __global__ __launch_bounds__(kWave * kW) __attribute__((amdgpu_waves_per_eu(1)))
                 }
             }
             const int nv = 2 * kq + (ik ? 1 : 0);
-            const uint8_t* kplane = slot_ptr(slot);
             const uint32_t vbase = lds_base + (slot + 1 >= kS ? slot + 1 - kS : slot + 1) * kMtPlaneB;
-            if (c.kw + kMtWin > st)
-                mt_window<true, kW>(a, kplane, vbase, qop, cs, st, c.kw, c.k_b, lim, nv, lane, t);
-            else
-                mt_window<false, kW>(a, kplane, vbase, qop, cs, st, c.kw, c.k_b, lim, nv, lane, t);
+            const bool chunk_keys = c.kw + kMtWin > st;
+            uint32_t ph[3][2][4];
+            const float m_eff = mt_max(a, chunk_keys, cs, st, c.kw, c.k_b, lim, lane, s_cur, t);
+            // The next window's scores (on a piece's last window the plane read is the next
+            // piece's or stale, and the result is dropped).
+            f32x4_t s_next[2];
+            mt_qk(slot_ptr(slot + 2), qop, lane, s_next);
+            mt_probs(s_cur, m_eff, ph, t);
+            mt_pv<kC>(vbase, ph, nv, lane, t);
+            s_cur[0] = s_next[0];
+            s_cur[1] = s_next[1];
             slot = slot + 2 >= kS ? slot + 2 - kS : slot + 2;
             kq = ik ? kq : kq - 1;
-            if (c.kw + kMtWin >= c.k_b) break;
+            if (!has_next) break;
             c.kw += kMtWin;
         }
         mt_piece_end<kW>(a, c.b, c.kvh, c.pk == 0 && c.k_b == c.nk, wg + seg, wv, lane, t);
