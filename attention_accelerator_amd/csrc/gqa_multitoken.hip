@@ -305,14 +305,18 @@ __global__ __launch_bounds__(256) void mt_prepare_kernel(PrefillArgs a) {
         }
 #pragma unroll
         for (int tau = 0; tau < kW; ++tau) {
+            // Tile tau holds tokens 4 tau .. 4 tau + 3, which the causal mask hides key
+            // start + u from when u > 4 tau + 3: such a score is never read, and is left 0.
+            // The four lanes of a column are summed through lane swaps (VALU, no LDS).
             double acc = 0.0;
+            if (u <= 4 * tau + 3) {
 #pragma unroll
-            for (int jj = 0; jj < 4; ++jj) {
-                acc = fma(qvx[tau][jj], kxr[jj], acc);
-                acc = fma(qvy[tau][jj], kyr[jj], acc);
+                for (int jj = 0; jj < 4; ++jj) {
+                    acc = fma(qvx[tau][jj], kxr[jj], acc);
+                    acc = fma(qvy[tau][jj], kyr[jj], acc);
+                }
+                acc = swap_add_f64<true>(swap_add_f64<false>(acc));
             }
-            acc += __shfl_xor(acc, 16);
-            acc += __shfl_xor(acc, 32);
             if (g == 0) part_s[w][u][kMtTile * tau + n] = acc;
         }
     }
