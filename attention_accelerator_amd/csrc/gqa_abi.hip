@@ -98,10 +98,10 @@ int32_t xcd_skew_pm(int32_t dflt) {
     return dflt;
 }
 
-// Workgroups of the multi-token stream kernel: one wave per SIMD, multi_waves(n_new) waves
-// per workgroup.
+// Workgroups of the multi-token stream kernel: multi_simd_waves(n_new) waves per SIMD,
+// multi_waves(n_new) waves per workgroup.
 int32_t multi_wgs(int32_t n_new) {
-    const int32_t w = stream_wgs() / multi_waves(n_new);
+    const int32_t w = stream_wgs() * multi_simd_waves(n_new) / multi_waves(n_new);
     return w > 0 ? w : 1;
 }
 

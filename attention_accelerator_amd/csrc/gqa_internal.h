@@ -121,9 +121,11 @@ struct PrefillArgs {
 };
 
 // Chunks of at most this many new tokens per sequence take the multi-token path.
-constexpr int32_t kMultiMaxNew = 8;
-// Waves per workgroup (16-column tiles) of the multi-token path for T new tokens: 1 or 2.
+constexpr int32_t kMultiMaxNew = 16;
+// Waves per workgroup (16-column tiles) of the multi-token path for T new tokens: 1, 2 or 4.
 int32_t multi_waves(int32_t n_new);
+// Waves per SIMD of that path's stream kernel: 1 for one tile, 2 for two or four tiles.
+int32_t multi_simd_waves(int32_t n_new);
 
 size_t prefill_split_bytes(int32_t batch, int32_t n_new);
 // Workspace of the multi-token path: Q operands, plan, partials, chunk-key scores.

@@ -10,7 +10,7 @@
 namespace gqa {
 
 // ---------------------------------------------------------------------------------
-// Multi-token decode: chunks of at most kMultiMaxNew (8) new tokens per sequence --
+// Multi-token decode: chunks of at most kMultiMaxNew (16) new tokens per sequence --
 // drafted tokens being verified, or decode steps that append their own K/V.  The prefill
 // attention kernel (gqa_prefill.hip) gives each (sequence, KV head, 32 positions) one workgroup over all of that
 // sequence's keys, which for a short chunk leaves most of its MFMA columns empty and a
@@ -23,16 +23,17 @@ namespace gqa {
 // own keys at full precision, P in three parts, fp64 accumulation within a piece,
 // integer-valued running max.
 //
-// A workgroup has one wave per column tile (W = 1 or 2 waves for T <= 4 or 8) and there
-// are 4 * CUs / W of them: one wave per SIMD.  Per 32-key window the workgroup copies
-// the window's K rows and V rows (a plane of 8 KB each) from HBM into LDS once -- each wave
-// issues 8/W of the plane's 1 KB copies -- and every wave forms its tile's scores and
-// V^T P^T from them.  The planes form a ring in the order K0 V0 K1 V1 ...: while window i
-// is computed, K of windows i+1 .. i+A+1 and V of windows i+1 .. i+A are in flight.  A = 1
-// for W = 1 and 3 for W = 2 keeps 12 to 14 planes in flight per CU (2A + 3 slots: 40 or 72 KB
-// per workgroup).  Longer chunks are compute-bound here -- every window costs each wave
-// about 2,000 cycles of MFMA and fp64 work for its 16 columns, and T = 16 on four waves
-// measured slower than the prefill attention kernel -- so they take that kernel.
+// A workgroup has one wave per column tile (W = 1, 2 or 4 waves for T <= 4, 8 or 16).  With
+// one tile (HBM-bound) there is one wave per SIMD, 4 * CUs workgroups; with two or four
+// tiles every window costs each wave about 2,000 cycles of MFMA and fp64 work, and two waves
+// per SIMD (8 * CUs / W workgroups) let one wave's MFMA run beside the other's VALU work.
+// Per 32-key window the workgroup copies the window's K rows and V rows (a plane of 8 KB
+// each) from HBM into LDS once -- each wave issues 8/W of the plane's 1 KB copies -- and
+// every wave forms its tile's scores and V^T P^T from them.  The planes form a ring in the
+// order K0 V0 K1 V1 ...: while window i is computed, K of windows i+1 .. i+A+1 and V of
+// windows i+1 .. i+A are in flight.  A = 1 for W = 1 and 2 (four workgroups per CU, 40 KB
+// each) and A = 3 for W = 4 (two per CU, 72 KB each) keep 12 to 14 planes in flight per CU
+// (2A + 3 slots per workgroup).
 //
 // Each wave forms the next window's scores beside the current window's probabilities.
 // It waits for its own copies, then a fence-free barrier makes the whole plane visible:
@@ -49,7 +50,7 @@ constexpr int kMtCopies = kMtWin / 4;         // 1 KB copies per plane (each wri
 // measured best of 32, 48, 64, 96 (B=64 ragged: T=4 216.5 -> 215.4 us, T=8 308.9 -> 303.8).
 constexpr int kMtSegLead = 64;
 
-__host__ __device__ constexpr int mt_ahead(int w) { return w == 1 ? 1 : 3; }
+__host__ __device__ constexpr int mt_ahead(int w) { return w == 4 ? 3 : 1; }
 __host__ __device__ constexpr int mt_slots(int w) { return 2 * mt_ahead(w) + 3; }
 
 // s_waitcnt immediate for vmcnt(n) alone (gfx9: vmcnt bits 3:0 and 15:14, expcnt and
@@ -71,13 +72,14 @@ __device__ __forceinline__ void mt_wait_planes(int planes) {
         default: __builtin_amdgcn_s_waitcnt(vmcnt_imm(0)); break;
     }
 }
-static_assert(7 * (kMtCopies / 2) <= 63 && 3 * kMtCopies <= 63, "vmcnt range");
+static_assert(7 * (kMtCopies / 4) <= 63 && 3 * kMtCopies <= 63, "vmcnt range");
 
 // Barrier without the memory fence __syncthreads adds (which would wait for every copy in
 // flight).
 __device__ __forceinline__ void mt_barrier() { asm volatile("s_barrier" ::: "memory"); }
 
-int32_t multi_waves(int32_t n_new) { return n_new <= 4 ? 1 : 2; }
+int32_t multi_waves(int32_t n_new) { return n_new <= 4 ? 1 : n_new <= 8 ? 2 : 4; }
+int32_t multi_simd_waves(int32_t n_new) { return n_new <= 4 ? 1 : 2; }
 
 // Keys of sequence b's segments: every key its last new token sees (0 for a start outside
 // [0, capacity - T]).
@@ -870,7 +872,8 @@ hipError_t launch_multi_w(const PrefillArgs& a, hipStream_t stream, hipEvent_t* 
 
 hipError_t launch_prefill_multi(const PrefillArgs& a, hipStream_t stream, hipEvent_t* ev) {
     if (multi_waves(a.n_new) == 1) return launch_multi_w<1>(a, stream, ev);
-    return launch_multi_w<2>(a, stream, ev);
+    if (multi_waves(a.n_new) == 2) return launch_multi_w<2>(a, stream, ev);
+    return launch_multi_w<4>(a, stream, ev);
 }
 
 }  // namespace gqa

@@ -181,7 +181,7 @@ int gqa_kv_append_paged_bf16(const gqa_params_t* params, const uint16_t* k_new, 
  * Token t attends to keys p <= start[b] + t (gqa_attention_wrapper.v:279 per token), the
  * chunk's own keys carried to ~24 bits (their rotated value is not re-rounded, as in the
  * golden).  Replaces the reference's per-token start loop for a run of tokens.
- * Chunks of at most 8 new tokens (multi-token decode: drafts, a few steps at once) split
+ * Chunks of at most 16 new tokens (multi-token decode: drafts, a few steps at once) split
  * the keys of every (sequence, KV head) over all CUs and merge per-range partials (three
  * launches: preparation, which also appends the chunk's rows, stream, merge); longer chunks
  * run the KV append and one attention kernel over 32-token query blocks.  The environment
@@ -215,9 +215,9 @@ int gqa_rope_rows_bf16(const uint16_t* in, uint16_t* out, int64_t n_rows, int64_
 /* Kernel timing for measurement harnesses.  While enabled, each decode or prefill
  * call brackets its two kernels with HIP events on the call's stream (up to
  * `max_calls` calls are recorded; later ones are not): decode {stream kernel, merge
- * kernel}, prefill {KV append kernel, attention kernel}, prefill of at most 8 new tokens
+ * kernel}, prefill {KV append kernel, attention kernel}, prefill of at most 16 new tokens
  * {preparation kernel (with the append), stream kernel}.  The Q-operand preparation kernel
- * of a decode call runs before the first event, the merge kernel of a prefill of at most 8
+ * of a decode call runs before the first event, the merge kernel of a prefill of at most 16
  * new tokens after the last.  gqa_profile_read waits for the
  * recorded events, returns the summed kernel times and the number of calls recorded,
  * and clears the record.  Not for the hot path: enabling creates the events.  No

@@ -1,7 +1,7 @@
 """Multi-token decode (chunks of 1..16 new tokens per sequence: speculative drafts, a few
-steps of one sequence at once) through gqa_prefill, which sends chunks of up to 8 tokens
+steps of one sequence at once) through gqa_prefill, which sends chunks of up to 16 tokens
 down the stream-K path (key ranges split over all CUs, per-range partials merged; one wave
-per 16 query columns, 1 or 2 waves per workgroup) and longer ones through the prefill
+per 16 query columns, 1, 2 or 4 waves per workgroup) and longer ones through the prefill
 attention kernel.  Every output row is checked against the compiled oracle's
 per-token reference step (the one-token golden of pyfiles/gen_gqa_wrapper_vectors.py:
 121-139 per new token, new K rotated at its position, not re-rounded), within 64 BF16 ULP
@@ -97,9 +97,10 @@ def test_multi_long_sequences(dev):
 @pytest.mark.parametrize("n_new,n_wgs", [(4, "1"), (4, "7"), (4, "64"), (4, "333"), (4, "4096"),
                                          (7, "2"), (7, "130"), (12, "4"), (12, "37"), (16, "1024")])
 def test_multi_partition_counts(dev, monkeypatch, n_new, n_wgs):
-    """The split of the keys over workgroups (GQA_STREAM_WGS waves, 1 or 2 to a workgroup)
+    """The split of the keys over workgroups (from GQA_STREAM_WGS: that many one-wave
+    workgroups for T <= 4, twice as many waves in workgroups of 2 or 4 for longer chunks)
     changes the order of the partial sums only: every split stays within the tolerance of
-    the oracle (T = 12 and 16 run the prefill attention kernel, which ignores the split)."""
+    the oracle."""
     monkeypatch.setenv("GQA_STREAM_WGS", n_wgs)
     starts = [5, 1200, 64, 2999, 0, 17]
     q, kn, vn, k, v = _chunk(starts, n_new, 3016, 42)
