@@ -46,9 +46,11 @@ constexpr int kMtPlaneB = kMtWin * kRowB;     // 8 KB: 32 rows of 256 B
 constexpr int kMtTile = 16;                   // query rows per wave: 4 heads x 4 tokens
 constexpr int kMtCopies = kMtWin / 4;         // 1 KB copies per plane (each writes 4 rows)
 // Stream positions charged per segment start: a piece here costs more than in decode (the
-// 12 KB of Q operands, the 16 KB fp64 partial), about two windows' streaming time.  64
-// measured best of 32, 48, 64, 96 (B=64 ragged: T=4 216.5 -> 215.4 us, T=8 308.9 -> 303.8).
-constexpr int kMtSegLead = 64;
+// Q operands, the fp64 partial of 16W columns), about two windows' streaming time for one
+// tile and more for two or four (their workgroups share a SIMD).  Measured on B=64 ragged:
+// W = 1 best at 64 of 32, 48, 64, 96 (T=4 216.5 -> 215.4 us); W = 2 and 4 best at 128 of 32,
+// 64, 128, 192 (T=8 248.7 -> 246.9 us, T=16 374.6 -> 370.8 us).
+__host__ __device__ constexpr int mt_seg_lead(int w) { return w == 1 ? 64 : 128; }
 
 __host__ __device__ constexpr int mt_ahead(int w) { return w == 4 ? 3 : 1; }
 __host__ __device__ constexpr int mt_slots(int w) { return 2 * mt_ahead(w) + 3; }
@@ -129,6 +131,7 @@ void prefill_multi_layout(PrefillArgs& a, void* base, int32_t n_wgs) {
 // The stream-K plan (one wave): seq_off[b] = stream position of sequence b's first segment,
 // seq_off[B] = total, header {total, positions per workgroup, lead, XCD extra}
 // (gqa_streamk.h).
+template <int kW>
 __device__ __forceinline__ void mt_build_plan(const PrefillArgs& a, int lane) {
     int64_t sum = 0;
     int max_keys = 0, n_seq = 0;
@@ -144,7 +147,7 @@ __device__ __forceinline__ void mt_build_plan(const PrefillArgs& a, int lane) {
     }
     int lead;
     int64_t total, per_wg;
-    plan_lead_totals(sum, max_keys, n_seq, a.n_wgs, lead, total, per_wg, kMtSegLead);
+    plan_lead_totals(sum, max_keys, n_seq, a.n_wgs, lead, total, per_wg, mt_seg_lead(kW));
     if (lane == 0) {
         a.plan_hdr[0] = total;
         a.plan_hdr[1] = per_wg;
@@ -205,7 +208,7 @@ __global__ __launch_bounds__(256) void mt_prepare_kernel(PrefillArgs a) {
     const int w = threadIdx.x >> 6;
     const int lane = threadIdx.x & (kWave - 1);
     if (b == a.batch) {
-        if (kvh == 0 && w == 0) mt_build_plan(a, lane);
+        if (kvh == 0 && w == 0) mt_build_plan<kW>(a, lane);
         return;
     }
     const int T = a.n_new;
