@@ -31,9 +31,9 @@ namespace gqa {
 // each) from HBM into LDS once -- each wave issues 8/W of the plane's 1 KB copies -- and
 // every wave forms its tile's scores and V^T P^T from them.  The planes form a ring in the
 // order K0 V0 K1 V1 ...: while window i is computed, K of windows i+1 .. i+A+1 and V of
-// windows i+1 .. i+A are in flight.  A = 1 for W = 1 and 2 (four workgroups per CU, 40 KB
-// each) and A = 3 for W = 4 (two per CU, 72 KB each) keep 12 to 14 planes in flight per CU
-// (2A + 3 slots per workgroup).
+// windows i+1 .. i+A are in flight.  A = 1 (2A + 3 = 5 slots, 40 KB per workgroup) keeps 12
+// planes in flight per CU with four one- or two-wave workgroups, 6 with two four-wave ones
+// (measured: A = 1, 2, 3 for W = 4 within 1 %, A = 1 fastest).
 //
 // Each wave forms the next window's scores beside the current window's probabilities.
 // It waits for its own copies, then a fence-free barrier makes the whole plane visible:
@@ -52,7 +52,7 @@ constexpr int kMtCopies = kMtWin / 4;         // 1 KB copies per plane (each wri
 // 64, 128, 192 (T=8 248.7 -> 246.9 us, T=16 374.6 -> 370.8 us).
 __host__ __device__ constexpr int mt_seg_lead(int w) { return w == 1 ? 64 : 128; }
 
-__host__ __device__ constexpr int mt_ahead(int w) { return w == 4 ? 3 : 1; }
+__host__ __device__ constexpr int mt_ahead(int) { return 1; }
 __host__ __device__ constexpr int mt_slots(int w) { return 2 * mt_ahead(w) + 3; }
 
 // s_waitcnt immediate for vmcnt(n) alone (gfx9: vmcnt bits 3:0 and 15:14, expcnt and
@@ -74,7 +74,7 @@ __device__ __forceinline__ void mt_wait_planes(int planes) {
         default: __builtin_amdgcn_s_waitcnt(vmcnt_imm(0)); break;
     }
 }
-static_assert(7 * (kMtCopies / 4) <= 63 && 3 * kMtCopies <= 63, "vmcnt range");
+static_assert((2 * mt_ahead(1) + 1) * kMtCopies <= 63, "vmcnt range");
 
 // Barrier without the memory fence __syncthreads adds (which would wait for every copy in
 // flight).
