@@ -51,7 +51,7 @@ class GqaParams(ctypes.Structure):
         ("n_q_heads", ctypes.c_int32),
         ("n_kv_heads", ctypes.c_int32),
         ("head_dim", ctypes.c_int32),
-        ("scale", ctypes.c_float),
+        ("scale", ctypes.c_double),
         ("rope_theta", ctypes.c_double),
         ("flags", ctypes.c_uint32),
     ]

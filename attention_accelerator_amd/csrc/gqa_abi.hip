@@ -108,12 +108,16 @@ int32_t multi_wgs(int32_t n_new) {
 
 bool geometry_ok(const gqa_params_t* p) {
     if (p->n_q_heads != kHq || p->n_kv_heads != kHkv || p->head_dim != kD) return false;
-    if (!(p->scale != 0.f) || !std::isfinite(p->scale)) return false;
+    if (!(p->scale != 0.0) || !std::isfinite(p->scale)) return false;
     if ((p->flags & ~(GQA_ROPE_Q | GQA_ROPE_K)) != 0) return false;
     if ((p->flags & (GQA_ROPE_Q | GQA_ROPE_K)) && !(p->rope_theta > 0.0 && std::isfinite(p->rope_theta)))
         return false;
     return true;
 }
+
+// The score scale folded into Q: scale * log2(e) in double, so that exp(scale * q.k - max)
+// becomes exp2 of the folded score.
+double qk_scale_log2(const gqa_params_t* p) { return p->scale * 1.4426950408889634; }
 
 bool aligned(const void* p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
 
@@ -159,7 +163,7 @@ DecodePlan plan_decode(int32_t batch, int32_t capacity, bool paged) {
     } else {
         plan.fused = !paged && use_fused(batch);
         plan.n_slots = static_cast<int64_t>(plan.n_wgs) + static_cast<int64_t>(kHkv) * batch;
-        plan.q_op_bytes = static_cast<size_t>(batch) * kHkv * 4 * kWave * sizeof(uint4);
+        plan.q_op_bytes = static_cast<size_t>(batch) * kHkv * kGroup * kD * sizeof(double);
         plan.plan_bytes = 256 + align_up((static_cast<size_t>(batch) + 1) * sizeof(int64_t), 256) +
                           align_up(static_cast<size_t>(batch) * sizeof(int32_t), 256);
     }
@@ -177,7 +181,7 @@ using namespace gqa;
 
 extern "C" {
 
-uint32_t gqa_abi_version(void) { return (1u << 16) | 0u; }
+uint32_t gqa_abi_version(void) { return (2u << 16) | 0u; }
 
 const char* gqa_status_string(int status) {
     switch (status) {
@@ -241,7 +245,7 @@ int decode_launch(const gqa_params_t* params, const uint16_t* q, const uint16_t*
     char* ws = static_cast<char*>(workspace);
     a.part_o = reinterpret_cast<double*>(ws);
     a.part_ml = reinterpret_cast<float2*>(ws + plan.part_o_bytes);
-    a.q_op = reinterpret_cast<uint4*>(ws + plan.part_o_bytes + plan.part_ml_bytes);
+    a.q_op = reinterpret_cast<double*>(ws + plan.part_o_bytes + plan.part_ml_bytes);
     char* pl = ws + plan.part_o_bytes + plan.part_ml_bytes + plan.q_op_bytes;
     a.plan_hdr = reinterpret_cast<int64_t*>(pl);
     a.seq_off = reinterpret_cast<int64_t*>(pl + 256);
@@ -260,7 +264,7 @@ int decode_launch(const gqa_params_t* params, const uint16_t* q, const uint16_t*
     a.batch = batch;
     a.n_wgs = plan.n_wgs;
     a.skew_pm = xcd_skew_pm(0);
-    a.qk_scale_log2 = static_cast<double>(params->scale) * 1.4426950408889634;
+    a.qk_scale_log2 = qk_scale_log2(params);
     a.flags = params->flags;
     fill_rope_table(params->rope_theta, &a.rope);
     const hipError_t e = launch_decode(a, batch, static_cast<hipStream_t>(stream), profile_slot());
@@ -433,7 +437,7 @@ int prefill_args(const gqa_params_t* params, const uint16_t* k_new, const uint16
     a.batch = batch;
     a.n_new = n_new;
     a.n_qblk = (n_new + 31) / 32;
-    a.qk_scale_log2 = static_cast<double>(params->scale) * 1.4426950408889634;
+    a.qk_scale_log2 = qk_scale_log2(params);
     a.flags = params->flags;
     fill_rope_table(params->rope_theta, &a.rope);
     return GQA_OK;

@@ -1,12 +1,12 @@
 // gqa_decode.hip -- GQA decode for gfx950: a persistent stream-K split over all keys
-// of the batch, QK^T on MFMA, weighted V on fp64 VALU, exact merge of pieces.
+// of the batch, scores and weighted V on fp64 MFMA, exact merge of pieces.
 //
 // One decode step of the reference core (gqa_controller.v:140-277 loop nest, datapath
 // rope_unit -> bf16_dot_product_mac -> scale_unit -> flash_softmax ->
 // output_accumulator -> gqa_output_collector) is, by default, three launches on one
 // stream: decode_prepare_kernel (the plan of pieces below, and every segment's 4 Q rows
-// rotated, scaled and split into MFMA operands once), decode_stream_kernel (a persistent
-// grid of n_wgs one-wave workgroups) and decode_merge_kernel:
+// rotated and scaled once), decode_stream_kernel (a persistent grid of n_wgs one-wave
+// workgroups) and decode_merge_kernel:
 //
 //  * The keys of every (sequence, kv_head) segment are laid end to end (segment =
 //    b*8 + h, n_valid(b) keys each; in a batch of segments shorter than a few ranges,
@@ -33,30 +33,33 @@
 // a block-table cache).
 //
 // Arithmetic (the golden model is double, pyfiles/gen_gqa_wrapper_vectors.py:121-139):
-//  * Q is rotated in double, scaled by scale*log2(e) in double and split into three
-//    BF16 parts (hi, mid, lo: ~26 significant bits).  K is BF16 already, so the
-//    bf16 x bf16 MFMA products are exact and the scores carry fp32 accumulation
-//    error only.  With RoPE on K (the reference's unrotated cache) the rotated K row
-//    is split the same way.
-//  * The running max m is kept integer-valued (m = ceil(max score)), so every
-//    rescale of the accumulator and every combine weight is an exact power of two.
-//  * p = exp2(s - m) in fp32; the weighted-V accumulation and the combine run in
-//    fp64 (full-rate on CDNA4), so their rounding never reaches the BF16 output.
+// every step is carried in fp64, so the output differs from the golden's double value by
+// double roundings only, far below one BF16 ULP of any output that is not exactly zero.
+//  * Q is rotated at query_position in double and scaled by scale*log2(e) in double.
+//  * Scores: fp64 MFMA (v_mfma_f64_4x4x4_4b_f64) of the K values (BF16, exact in double;
+//    with RoPE on K the row is rotated in double first) and the fp64 Q.
+//  * The running max m is kept integer-valued (m = ceil(max score)), so every rescale of
+//    the accumulator and every combine weight is an exact power of two.
+//  * p = exp2(s - m) in fp64; weighted V by fp64 MFMA; l, the merge and the division in
+//    fp64; the row is rounded double -> f32 -> BF16 as the reference's f32_to_bf16.
 //
 // Masking (gqa_attention_wrapper.v:279): key p counts iff p < seq_len and
 // p <= query_position.  Only keys p < n_valid = min(seq_len, qpos+1) are ever
-// loaded; inside the last chunk the other lanes load nothing, score -inf and get
+// loaded; inside the last chunk the other lanes load a clamped row, score -inf and get
 // p = 0 exactly (flash_softmax.v:319-325).
 //
-// Lane layouts (wave64, l = lane):
-//  * QK, MFMA f32_16x16x32_bf16 with A = K (row = key l%16), B = Q^T (column
-//    n = l%16: n = 4*split + head for n < 12, zero for n >= 12).  Lane group
-//    g = l/16 and element j of MFMA kb cover head dim d = 32*kb + 8*g + j, so a
-//    lane loads 16 contiguous bytes per kb and holds both halves (d, d+64) of its
-//    RoPE pairs (kb and kb+2).  Output lane l holds score(key 4g+i, column n).
-//  * PV: lane (g, n) owns dims [8n, 8n+8) of keys 4g+i of the chunk -- the keys whose
-//    scores row g holds -- so each 16-lane row runs its own online softmax and the
-//    rows merge once per piece.  V load i covers whole rows i, 4+i, 8+i, 12+i.
+// Lane layouts of one 16-key chunk (wave64, l = lane).  v_mfma_f64_4x4x4_4b_f64 runs four
+// 4x4x4 blocks; lane l holds A[m = l%4][k = l/16] and B[k = l/16][n = l%4] of block
+// (l/4)%4 and receives C[m = l/16][n = l%4] of that block.
+//  * QK^T: A = K (block row = key l%16), B = Q^T (column = head l%4); MFMA (kb, e), kb,
+//    e < 4, 8, takes head dim 32kb + 8(l/16) + e in k-slot l/16, so a lane loads 16
+//    contiguous bytes of its key's row per kb and holds both halves (d, d+64) of its RoPE
+//    pairs (kb and kb+2).  C: lane l holds the score of key 4((l/4)%4) + l/16, head l%4.
+//  * PV: A = V^T, B = P: MFMA (q, e) takes keys 4q + k in k-slot k, and block b's rows
+//    m are dims 8(4b + m) + e, so V load q of lane l is 16 contiguous bytes of row
+//    4q + l/16, dims 8(l%16) .. -- four whole rows per load instruction.  B lane l holds
+//    p of head l%4, key 4q + l/16, gathered through 512 bytes of LDS from the score lanes.
+//    C: lane l accumulates O[head l%4][8(4((l/4)%4) + l/16) + e] over all keys.
 #include "gqa_device.h"
 #include "gqa_internal.h"
 #include "gqa_streamk.h"
@@ -102,19 +105,39 @@ __device__ __forceinline__ void stream_totals(const DecodeArgs& a, int lane, int
     plan_lead_totals(sum, max_keys, n_seq, a.n_wgs, lead, total, per_wg);
 }
 
-// K and V rows of one 16-key chunk, in the MFMA (K) and PV (V) lane layouts.
+// Key of lane l's score within a chunk (the QK^T output layout).
+__device__ __forceinline__ int chunk_key_of_lane(int lane) { return 4 * ((lane >> 2) & 3) + (lane >> 4); }
+
+// First of the 8 output dims lane l accumulates (PV output layout), head l%4.
+__device__ __forceinline__ int out_dim_of_lane(int lane) { return 8 * (4 * ((lane >> 2) & 3) + (lane >> 4)); }
+
+// K and V rows of one 16-key chunk: kw[kb] = 8 K values of key l%16, dims 32kb + 8(l/16)..;
+// vw[q] = 8 V values of key 4q + l/16, dims 8(l%16)...
 struct Chunk {
     uint4 kw[4];
     uint4 vw[4];
 };
 
-// Running state of one piece in lane (g, n): fp64 weighted-V accumulator of row g
-// (4 heads x dims [8n, 8n+8)), and row g's integer-valued running max and sum of p
-// for head n%4.
+// Running state of one piece in lane l: O[head l%4][out_dim_of_lane(l) + e] in acc[e], and
+// the head's integer-valued running max and (this lane's share of the) sum of p.  m_run is
+// the same in every lane of a head.
 struct PieceState {
-    double acc[kGroup][8];
+    double acc[8];
+    double l_run;
     float m_run;
-    float l_run;
+};
+
+__device__ __forceinline__ void init_piece(PieceState& st) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) st.acc[i] = 0.0;
+    st.l_run = 0.0;
+    st.m_run = -INFINITY;
+}
+
+// The 32 Q values lane l feeds the QK^T MFMAs: q[kb][e] = Q[head l%4][32kb + 8(l/16) + e],
+// rotated and scaled by scale*log2(e) in double.
+struct QOps {
+    double q[4][8];
 };
 
 // Byte offsets (from the segment's first K / V row) of this lane's rows in the current
@@ -122,8 +145,8 @@ struct PieceState {
 // under a branch makes it wait for every outstanding load at the join, prefetches
 // included); rows past the piece are clamped to its last row and masked afterwards.
 struct ChunkRows {
-    uint32_t k;       // key kc + n, + 16*g bytes into the row
-    uint32_t v[4];    // keys kc + 4*g + i, + 16*n bytes into the row
+    uint32_t k;       // key kc + l%16, + 16*(l/16) bytes into the row
+    uint32_t v[4];    // key kc + 4q + l/16, + 16*(l%16) bytes into the row
 };
 
 __device__ __forceinline__ void load_chunk(const char* kseg, const char* vseg, const ChunkRows& r,
@@ -132,32 +155,58 @@ __device__ __forceinline__ void load_chunk(const char* kseg, const char* vseg, c
 #pragma unroll
     for (int kb = 0; kb < 4; ++kb) c.kw[kb] = load_stream16(kp + 64 * kb);
 #pragma unroll
-    for (int it = 0; it < 4; ++it)
-        c.vw[it] = load_stream16(vseg + min(r.v[it], v_last));
+    for (int q = 0; q < 4; ++q) c.vw[q] = load_stream16(vseg + min(r.v[q], v_last));
 }
 
 __device__ __forceinline__ void advance(ChunkRows& r, uint32_t step) {
     r.k += step;
 #pragma unroll
-    for (int it = 0; it < 4; ++it) r.v[it] += step;
+    for (int q = 0; q < 4; ++q) r.v[q] += step;
+}
+
+__device__ __forceinline__ double mfma_f64(double a, double b, double c) {
+    return __builtin_amdgcn_mfma_f64_4x4x4f64(a, b, c, 0, 0, 0);
+}
+
+// Scores may exceed the running reference m by this much (log2 units) before it is raised:
+// p <= 2^64 and a piece's l <= 2^95 (still an fp32 in the partial record).
+constexpr double kMaxHeadroom = 64.0;
+
+// 2^x for finite x <= kMaxHeadroom + 1, relative error below 1e-14: x = n + f with
+// n = rint(x), |f| <= 1/2, and 2^f = e^t, t = f ln 2, by its Taylor series to degree 11
+// (truncation error < (ln2/2)^12 / 12! < 7e-15).  x below about -1075 gives 0.
+__device__ __forceinline__ double exp2_f64(double x) {
+    const double n = rint(x);
+    const double t = (x - n) * 0.6931471805599453094;
+    double y = 1.0 / 39916800.0;              // 1/11!
+    y = fma(y, t, 1.0 / 3628800.0);           // 1/10!
+    y = fma(y, t, 1.0 / 362880.0);
+    y = fma(y, t, 1.0 / 40320.0);
+    y = fma(y, t, 1.0 / 5040.0);
+    y = fma(y, t, 1.0 / 720.0);
+    y = fma(y, t, 1.0 / 120.0);
+    y = fma(y, t, 1.0 / 24.0);
+    y = fma(y, t, 1.0 / 6.0);
+    y = fma(y, t, 0.5);
+    y = fma(y, t, 1.0);
+    y = fma(y, t, 1.0);
+    return ldexp(y, static_cast<int>(fmax(n, -2000.0)));
 }
 
 // Scores, online softmax and weighted V of one chunk [kc, kc+16) (keys >= k_b masked).
-//
-// Lane (g = l/16, n = l%16): MFMA output rows are keys kc+4g+i (i = 0..3) and
-// columns n, so after summing the split columns every lane holds the scores of
-// keys kc+4g+i for head n%4.  The same row g then weights V rows kc+4g+i (dims
-// [8n, 8n+8)), so each 16-lane row is an independent flash-decoding stream with
-// its own running max and sum per head: no cross-row step until the piece ends,
-// and p moves to the weighted-V lanes by quad_perm DPP, not through LDS.
 template <bool kRopeK>
-__device__ __forceinline__ void compute_chunk(const DecodeArgs& a, int kc, int k_b, int n, int g,
-                                              const Chunk& c, const bf16x8_t (&bq)[4],
-                                              PieceState& st) {
-    f32x4_t d = {0.f, 0.f, 0.f, 0.f};
+__device__ __forceinline__ void compute_chunk(const DecodeArgs& a, int kc, int k_b, const Chunk& c,
+                                              const QOps& qa, PieceState& st) {
+    // p exchange slice of this wave (workgroups of up to four waves).
+    __shared__ double p_lds[4][kWave];
+    double* pl = p_lds[(threadIdx.x >> 6) & 3];
+    const int lane = threadIdx.x & (kWave - 1);
+    // QK^T: four independent accumulation chains (one per kb), summed in a fixed order.
+    double s4[4] = {0.0, 0.0, 0.0, 0.0};
     if (kRopeK) {
-        // Rotate the K row at its position: pairs (kb, kb+2) of this lane.
-        const int kkey = kc + n;
+        // Rotate the K row at its position in double: pairs (kb, kb+2) of this lane.
+        const int kkey = kc + (lane & 15);
+        const int g = lane >> 4;
         double kr[4][8];
 #pragma unroll
         for (int kb = 0; kb < 2; ++kb) {
@@ -173,150 +222,123 @@ __device__ __forceinline__ void compute_chunk(const DecodeArgs& a, int kc, int k
             }
         }
 #pragma unroll
-        for (int part = 0; part < 3; ++part) {
+        for (int e = 0; e < 8; ++e)
 #pragma unroll
-            for (int kb = 0; kb < 4; ++kb) {
-                uint16_t h8[8];
-#pragma unroll
-                for (int j = 0; j < 8; ++j) h8[j] = split3(kr[kb][j], part);
-                d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pack8(h8), bq[kb], d, 0, 0, 0);
-            }
-        }
+            for (int kb = 0; kb < 4; ++kb) s4[kb] = mfma_f64(kr[kb][e], qa.q[kb][e], s4[kb]);
     } else {
+        // Every K value converted first, then the 32 MFMAs back to back: VALU work does not
+        // overlap an fp64 MFMA on gfx950, and interleaving adds wait states between them.
+        double kd[4][8];
 #pragma unroll
-        for (int kb = 0; kb < 4; ++kb)
-            d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(c.kw[kb]), bq[kb], d, 0, 0, 0);
-    }
-    // Sum the hi/mid/lo columns (n, n+4, n+8; 12..15 are zero): the rotations by 4, 8
-    // and 12 within the 16-lane row leave every lane with the total of its n%4 class.
-    float s[4];
+        for (int kb = 0; kb < 4; ++kb) {
+            float kf[8];
+            unpack8(c.kw[kb], kf);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const float x = d[i];
-        s[i] = x + dpp_f<0x124>(x) + dpp_f<0x128>(x) + dpp_f<0x12C>(x);
-        if (kc + 4 * g + i >= k_b) s[i] = -INFINITY;
+            for (int e = 0; e < 8; ++e) kd[kb][e] = static_cast<double>(kf[e]);
+        }
+        __builtin_amdgcn_sched_group_barrier(0x002, 64, 0);
+        __builtin_amdgcn_sched_group_barrier(0x008, 32, 0);
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+#pragma unroll
+            for (int kb = 0; kb < 4; ++kb) s4[kb] = mfma_f64(kd[kb][e], qa.q[kb][e], s4[kb]);
     }
+    const int key = kc + chunk_key_of_lane(lane);
+    double s = (s4[0] + s4[1]) + (s4[2] + s4[3]);
+    if (key >= k_b) s = -INFINITY;
 
-    // Online softmax of this row's 4 keys for head n%4 (m integer-valued, so every
-    // rescale is an exact power of two).
-    const float cm = fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3]));
-    const bool grow = cm > st.m_run;
-    if (__ballot(grow)) {
+    // Online softmax per head with a lazy reference: m (integer-valued, common to the 16
+    // lanes with lane%4 == head) is raised only when a score exceeds m + kMaxHeadroom, so
+    // the rescale below runs about once per piece; p = 2^(s - m) <= 2^kMaxHeadroom then,
+    // far inside the fp64 range.  The new m is the ceiling of the head's chunk max, taken
+    // in fp32 over its 16 lanes (rows through lane swaps, blocks through row rotations).
+    if (__ballot(s > static_cast<double>(st.m_run) + kMaxHeadroom)) {
+        float cm = static_cast<float>(s);
+        cm = fmaxf(cm, dpp_f<0x124>(cm));
+        cm = fmaxf(cm, dpp_f<0x128>(cm));
+        cm = swap32_max(swap16_max(cm));
+        const bool grow = static_cast<double>(cm) > static_cast<double>(st.m_run) + kMaxHeadroom;
         const float m_new = grow ? ceilf(cm) : st.m_run;
-        // 2^(m_run - m_new), exact; 0 when nothing has been accumulated yet.
-        const int shift = (st.m_run == -INFINITY) ? -1100 : static_cast<int>(st.m_run - m_new);
-        st.l_run = ldexpf(st.l_run, max(shift, -200));
+        // 2^(m_run - m_new), exact; nothing has been accumulated while m_run is -inf.
+        const int shift = (st.m_run == -INFINITY) ? 0 : static_cast<int>(st.m_run - m_new);
+        st.l_run = ldexp(st.l_run, shift);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) st.acc[i] = ldexp(st.acc[i], shift);
         st.m_run = m_new;
-        int sh[kGroup];
-        sh[0] = dpp_i<0x00>(shift);
-        sh[1] = dpp_i<0x55>(shift);
-        sh[2] = dpp_i<0xAA>(shift);
-        sh[3] = dpp_i<0xFF>(shift);
-#pragma unroll
-        for (int h = 0; h < kGroup; ++h)
-#pragma unroll
-            for (int j = 0; j < 8; ++j) st.acc[h][j] = ldexp(st.acc[h][j], sh[h]);
     }
-    float p[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        p[i] = (s[i] == -INFINITY) ? 0.f : exp2f(s[i] - st.m_run);
-        st.l_run += p[i];
-    }
+    // p = 0 for a masked key (and for every key while m is -inf, when all of them are).
+    const double p = key < k_b ? exp2_f64(fmax(s - static_cast<double>(st.m_run), -2000.0)) : 0.0;
+    st.l_run += p;
 
-    // Weighted V in fp64.  In a partial chunk the clamped rows carry p = 0; their V is
-    // zeroed too so that no value of another row can reach the sum.
-    const bool partial = kc + kChunk > k_b;
+    // p of (head l%4, key 4q + l/16) for q = 0..3, from the lane holding that score
+    // (lane 16(key%4) + 4(key/4) + head): through LDS, [row l/16][head][q].
+    pl[(lane >> 4) * 16 + (lane & 3) * 4 + ((lane >> 2) & 3)] = p;
+    const double2 pa = *reinterpret_cast<const double2*>(pl + (lane >> 4) * 16 + (lane & 3) * 4);
+    const double2 pb = *reinterpret_cast<const double2*>(pl + (lane >> 4) * 16 + (lane & 3) * 4 + 2);
+    const double pq[4] = {pa.x, pa.y, pb.x, pb.y};
+
+    // Weighted V.  A masked key's V row is a clamped row of the piece, weighted by p = 0.
+    double vd[4][8];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        // p of key kc+4g+i for heads 0..3, from lanes 4*(n/4) + h of this quad.
-        const double pd[kGroup] = {static_cast<double>(dpp_f<0x00>(p[i])),
-                                   static_cast<double>(dpp_f<0x55>(p[i])),
-                                   static_cast<double>(dpp_f<0xAA>(p[i])),
-                                   static_cast<double>(dpp_f<0xFF>(p[i]))};
-        uint4 vw = c.vw[i];
-        if (partial && kc + 4 * g + i >= k_b) vw = make_uint4(0, 0, 0, 0);
+    for (int q = 0; q < 4; ++q) {
         float vf[8];
-        unpack8(vw, vf);
-        double vd[8];
+        unpack8(c.vw[q], vf);
 #pragma unroll
-        for (int j = 0; j < 8; ++j) vd[j] = static_cast<double>(vf[j]);
-#pragma unroll
-        for (int h = 0; h < kGroup; ++h)
-#pragma unroll
-            for (int j = 0; j < 8; ++j) st.acc[h][j] = fma(pd[h], vd[j], st.acc[h][j]);
+        for (int e = 0; e < 8; ++e) vd[q][e] = static_cast<double>(vf[e]);
     }
+    __builtin_amdgcn_sched_group_barrier(0x002, 64, 1);
+    __builtin_amdgcn_sched_group_barrier(0x008, 32, 1);
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) st.acc[e] = mfma_f64(vd[q][e], pq[q], st.acc[e]);
 }
 
 // ---- end of a piece.
 
-// Merge the four 16-lane rows of a piece (each ran its own online softmax): common max per
-// head, exact power-of-two weights, sums in fp64.  Afterwards every row holds the totals:
-// lane (g, n) has O[h][8n .. 8n+8) for the 4 heads in st.acc, and m_tot / l_tot per head.
-__device__ __forceinline__ void merge_rows(PieceState& st, float (&m_tot)[kGroup], double (&l_tot)[kGroup]) {
-    float mh[kGroup];
-    mh[0] = dpp_f<0x00>(st.m_run);
-    mh[1] = dpp_f<0x55>(st.m_run);
-    mh[2] = dpp_f<0xAA>(st.m_run);
-    mh[3] = dpp_f<0xFF>(st.m_run);
-    float lh[kGroup];
-    lh[0] = dpp_f<0x00>(st.l_run);
-    lh[1] = dpp_f<0x55>(st.l_run);
-    lh[2] = dpp_f<0xAA>(st.l_run);
-    lh[3] = dpp_f<0xFF>(st.l_run);
-    // Rows 16 lanes apart combine through lane swaps (no LDS round trips).
-#pragma unroll
-    for (int h = 0; h < kGroup; ++h) {
-        const float mx = swap32_max(swap16_max(mh[h]));
-        m_tot[h] = mx;
-        // a row that saw no key of this piece has m = -inf and contributes nothing
-        const int e = (mh[h] == -INFINITY) ? -1100 : static_cast<int>(mh[h] - mx);
-        l_tot[h] = swap_add_f64<true>(swap_add_f64<false>(ldexp(static_cast<double>(lh[h]), e)));
-#pragma unroll
-        for (int j = 0; j < 8; ++j)
-            st.acc[h][j] = swap_add_f64<true>(swap_add_f64<false>(ldexp(st.acc[h][j], e)));
-    }
+// fp64 sum of x over lanes l, l+4, l+8, l+12 of each 16-lane row (row rotations by 4 and 8).
+__device__ __forceinline__ double row_quad_sum(double x) {
+    const unsigned long long u = static_cast<unsigned long long>(__double_as_longlong(x));
+    const int lo = static_cast<int>(u), hi = static_cast<int>(u >> 32);
+    double y = x + __longlong_as_double(static_cast<long long>(
+                       (static_cast<unsigned long long>(static_cast<uint32_t>(dpp_i<0x124>(hi))) << 32) |
+                       static_cast<uint32_t>(dpp_i<0x124>(lo))));
+    const unsigned long long v = static_cast<unsigned long long>(__double_as_longlong(y));
+    const int lo2 = static_cast<int>(v), hi2 = static_cast<int>(v >> 32);
+    return y + __longlong_as_double(static_cast<long long>(
+                   (static_cast<unsigned long long>(static_cast<uint32_t>(dpp_i<0x128>(hi2))) << 32) |
+                   static_cast<uint32_t>(dpp_i<0x128>(lo2))));
+}
+
+// Totals of a piece: the head's l summed over its 16 lanes (m_run is already common to
+// them; O needs no cross-lane step, each lane owns its 8 dims over all keys).
+__device__ __forceinline__ void finish_piece(PieceState& st, double& l_tot) {
+    l_tot = swap_add_f64<true>(swap_add_f64<false>(row_quad_sum(st.l_run)));
+}
+
+// Element offset, within a [4][128] group of rows, of the 8 dims lane l holds.
+__device__ __forceinline__ int lane_row_offset() {
+    const int lane = threadIdx.x & (kWave - 1);
+    return (lane & 3) * kD + out_dim_of_lane(lane);
 }
 
 // Normalise in fp64 and round double -> f32 -> BF16 (the 4 output rows of the group, in
 // Q-head order, output_accumulator.v:540-686, gqa_output_collector.v:32-61).
-__device__ __forceinline__ void write_rows(const DecodeArgs& a, int b, int kvh, const PieceState& st,
-                                           const double (&l_tot)[kGroup]) {
-    const int lane = threadIdx.x & (kWave - 1);
-    if (lane >= 16) return;
-    const int n = lane;
+__device__ __forceinline__ void write_rows(const DecodeArgs& a, int b, int kvh, const PieceState& st, double l_tot) {
+    uint16_t o8[8];
 #pragma unroll
-    for (int h = 0; h < kGroup; ++h) {
-        uint16_t o8[8];
-#pragma unroll
-        for (int j = 0; j < 8; ++j) o8[j] = f32_to_bf16_rne(static_cast<float>(st.acc[h][j] / l_tot[h]));
-        uint4 pk;
-        pk.x = o8[0] | (static_cast<uint32_t>(o8[1]) << 16);
-        pk.y = o8[2] | (static_cast<uint32_t>(o8[3]) << 16);
-        pk.z = o8[4] | (static_cast<uint32_t>(o8[5]) << 16);
-        pk.w = o8[6] | (static_cast<uint32_t>(o8[7]) << 16);
-        *reinterpret_cast<uint4*>(a.out + (static_cast<int64_t>(b) * kHq + kvh * kGroup + h) * kD + 8 * n) = pk;
-    }
+    for (int e = 0; e < 8; ++e) o8[e] = f64_to_bf16_via_f32(st.acc[e] / l_tot);
+    *reinterpret_cast<bf16x8_t*>(a.out + (static_cast<int64_t>(b) * kHq + kvh * kGroup) * kD + lane_row_offset()) =
+        pack8(o8);
 }
 
 // Unnormalised partial of a piece: O (fp64) and (m, l) per head at `slot`.
-__device__ __forceinline__ void write_partial(const DecodeArgs& a, int64_t slot, const PieceState& st,
-                                              const float (&m_tot)[kGroup], const double (&l_tot)[kGroup]) {
+__device__ __forceinline__ void write_partial(const DecodeArgs& a, int64_t slot, const PieceState& st, double l_tot) {
     const int lane = threadIdx.x & (kWave - 1);
-    const int n = lane & 15;
-    if (lane < 16) {
+    double2* dst = reinterpret_cast<double2*>(a.part_o + slot * kGroup * kD + lane_row_offset());
 #pragma unroll
-        for (int h = 0; h < kGroup; ++h) {
-            double2* dst = reinterpret_cast<double2*>(a.part_o + (slot * kGroup + h) * kD + 8 * n);
-#pragma unroll
-            for (int j = 0; j < 4; ++j) dst[j] = make_double2(st.acc[h][2 * j], st.acc[h][2 * j + 1]);
-        }
-    }
-    if (lane < kGroup) {
-        const float mm = lane == 0 ? m_tot[0] : lane == 1 ? m_tot[1] : lane == 2 ? m_tot[2] : m_tot[3];
-        const double ll = lane == 0 ? l_tot[0] : lane == 1 ? l_tot[1] : lane == 2 ? l_tot[2] : l_tot[3];
-        a.part_ml[slot * kGroup + lane] = make_float2(mm, static_cast<float>(ll));
-    }
+    for (int j = 0; j < 4; ++j) dst[j] = make_double2(st.acc[2 * j], st.acc[2 * j + 1]);
+    if (lane < kGroup) a.part_ml[slot * kGroup + lane] = make_float2(st.m_run, static_cast<float>(l_tot));
 }
 
 // Agent-scope (sc1) 8-byte stores and loads: coherent across the XCDs without a cache
@@ -348,24 +370,14 @@ __device__ __forceinline__ double2 load_agent_d2(const double* p) {
 
 // write_partial with agent-scope stores, for a partial merged inside the same launch.
 __device__ __forceinline__ void publish_partial(const DecodeArgs& a, int64_t slot, const PieceState& st,
-                                                const float (&m_tot)[kGroup], const double (&l_tot)[kGroup]) {
+                                                double l_tot) {
     const int lane = threadIdx.x & (kWave - 1);
-    const int n = lane & 15;
-    if (lane < 16) {
+    unsigned long long* dst = reinterpret_cast<unsigned long long*>(a.part_o + slot * kGroup * kD + lane_row_offset());
 #pragma unroll
-        for (int h = 0; h < kGroup; ++h) {
-            unsigned long long* dst =
-                reinterpret_cast<unsigned long long*>(a.part_o + (slot * kGroup + h) * kD + 8 * n);
-#pragma unroll
-            for (int j = 0; j < 8; ++j) store_agent(dst + j, st.acc[h][j]);
-        }
-    }
-    if (lane < kGroup) {
-        const float mm = lane == 0 ? m_tot[0] : lane == 1 ? m_tot[1] : lane == 2 ? m_tot[2] : m_tot[3];
-        const double ll = lane == 0 ? l_tot[0] : lane == 1 ? l_tot[1] : lane == 2 ? l_tot[2] : l_tot[3];
+    for (int e = 0; e < 8; ++e) store_agent(dst + e, st.acc[e]);
+    if (lane < kGroup)
         store_agent(reinterpret_cast<unsigned long long*>(a.part_ml + slot * kGroup + lane),
-                    make_float2(mm, static_cast<float>(ll)));
-    }
+                    make_float2(st.m_run, static_cast<float>(l_tot)));
 }
 
 // A partial held in LDS until the end of the workgroup's range (fused kernel).
@@ -374,21 +386,11 @@ struct PartialStage {
     float2 ml[kGroup];
 };
 
-__device__ __forceinline__ void stage_partial(PartialStage& s, const PieceState& st, const float (&m_tot)[kGroup],
-                                              const double (&l_tot)[kGroup]) {
+__device__ __forceinline__ void stage_partial(PartialStage& s, const PieceState& st, double l_tot) {
     const int lane = threadIdx.x & (kWave - 1);
-    const int n = lane & 15;
-    if (lane < 16) {
 #pragma unroll
-        for (int h = 0; h < kGroup; ++h)
-#pragma unroll
-            for (int j = 0; j < 8; ++j) s.o[h][8 * n + j] = st.acc[h][j];
-    }
-    if (lane < kGroup) {
-        const float mm = lane == 0 ? m_tot[0] : lane == 1 ? m_tot[1] : lane == 2 ? m_tot[2] : m_tot[3];
-        const double ll = lane == 0 ? l_tot[0] : lane == 1 ? l_tot[1] : lane == 2 ? l_tot[2] : l_tot[3];
-        s.ml[lane] = make_float2(mm, static_cast<float>(ll));
-    }
+    for (int e = 0; e < 8; ++e) (&s.o[0][0])[lane_row_offset() + e] = st.acc[e];
+    if (lane < kGroup) s.ml[lane] = make_float2(st.m_run, static_cast<float>(l_tot));
 }
 
 // publish_partial of a staged partial: lane l writes dims [8(l%16), 8(l%16) + 8) of head l/16.
@@ -408,17 +410,13 @@ __device__ __forceinline__ void publish_staged(const DecodeArgs& a, int64_t slot
 __device__ __forceinline__ void wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0F70); }
 
 // This lane's Q operands for (sequence b, KV head kvh): the group's 4 Q rows rotated at
-// query_position and scaled by scale*log2(e) in double, each value split into three BF16
-// parts, in the MFMA B-operand layout.  Two steps, so that the loads can be issued long
-// before the values are needed: load_q_raw reads the 4 Q rows (lane l: dims l and l + 64
-// of each head) and the query position; build_q_operands rotates and scales them (q),
-// splits each value once into hi/mid/lo codes (lane l splits dims [8(l%16), 8(l%16) + 8)
-// of head l/16) and reads the codes back in the B layout (lane (g, n), MFMA kb: 8 codes
-// of part n/4 of head n%4, dims 32kb + 8g ..; columns 12..15 zero).  sin/cos are kept
-// while the query position stays the same (the 8 KV heads of a sequence).
+// query_position and scaled by scale*log2(e) in double.  Two steps, so that the loads can
+// be issued long before the values are needed: load_q_raw reads the 4 Q rows (lane l:
+// dims l and l + 64 of each head) and the query position; build_q_operands rotates and
+// scales them into LDS and reads back the lane's QOps.  sin/cos are kept while the query
+// position stays the same (the 8 KV heads of a sequence).
 struct QStage {
     double q[kGroup][kD];
-    uint16_t codes[3][kGroup][kD];
 };
 
 struct QRaw {
@@ -442,9 +440,9 @@ __device__ __forceinline__ void load_q_raw(const DecodeArgs& a, int b, int kvh, 
     }
 }
 
+// Rotated and scaled Q of the group into s.q (lane l: dims l and l + 64 of every head).
 template <bool kRopeQ>
-__device__ __forceinline__ void build_q_operands(const DecodeArgs& a, const QRaw& r, QRope& rope, QStage& s,
-                                                 bf16x8_t (&bq)[4]) {
+__device__ __forceinline__ void stage_q(const DecodeArgs& a, const QRaw& r, QRope& rope, QStage& s) {
     const int lane = threadIdx.x & (kWave - 1);
     if (kRopeQ && r.qpos != rope.qpos) {       // (uniform)
         rope_sincos(r.qpos, rope.inv_freq, rope.sn, rope.cs);
@@ -462,42 +460,36 @@ __device__ __forceinline__ void build_q_operands(const DecodeArgs& a, const QRaw
         s.q[h][lane] = xr * a.qk_scale_log2;
         s.q[h][lane + kPairs] = yr * a.qk_scale_log2;
     }
-    __syncthreads();
-    {
-        const int hh = lane >> 4;
-        const int c = lane & 15;
-        uint16_t p0[8], p1[8], p2[8];
+}
+
+// QOps of lane l from a [4][128] block of rotated, scaled Q rows.
+__device__ __forceinline__ void read_q_ops(const double* qs, QOps& qa) {
+    const int lane = threadIdx.x & (kWave - 1);
+    const double* base = qs + (lane & 3) * kD + 8 * (lane >> 4);
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            const double v = s.q[hh][8 * c + j];
-            p0[j] = bf16_of(v);
-            const double r1 = v - f64_of_bf16(p0[j]);
-            p1[j] = bf16_of(r1);
-            p2[j] = bf16_of(r1 - f64_of_bf16(p1[j]));
+    for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+        for (int e = 0; e < 8; e += 2) {
+            const double2 v = *reinterpret_cast<const double2*>(base + 32 * kb + e);
+            qa.q[kb][e] = v.x;
+            qa.q[kb][e + 1] = v.y;
         }
-        *reinterpret_cast<bf16x8_t*>(&s.codes[0][hh][8 * c]) = pack8(p0);
-        *reinterpret_cast<bf16x8_t*>(&s.codes[1][hh][8 * c]) = pack8(p1);
-        *reinterpret_cast<bf16x8_t*>(&s.codes[2][hh][8 * c]) = pack8(p2);
-    }
+}
+
+template <bool kRopeQ>
+__device__ __forceinline__ void build_q_operands(const DecodeArgs& a, const QRaw& r, QRope& rope, QStage& s,
+                                                 QOps& qa) {
+    stage_q<kRopeQ>(a, r, rope, s);
     __syncthreads();
-    const int n = lane & 15;
-    const int g = lane >> 4;
-    const int part = n < 12 ? n >> 2 : 0;
-#pragma unroll
-    for (int kb = 0; kb < 4; ++kb) {
-        const bf16x8_t v = *reinterpret_cast<const bf16x8_t*>(&s.codes[part][n & 3][32 * kb + 8 * g]);
-        bq[kb] = n < 12 ? v : bf16x8_t{};
-    }
+    read_q_ops(&s.q[0][0], qa);
     // (one wave: its LDS accesses run in order, so the next piece's writes need no barrier)
 }
 
-// Q operands of every (sequence, KV head), written once per call by
-// decode_prepare_kernel and read by each piece: the 4 Q rows of the group rotated at
-// query_position and scaled by scale*log2(e) in double, split into hi/mid/lo BF16,
-// in the MFMA B-operand layout (lane l, MFMA kb: column n = l%16 -> split n/4 of
-// head n%4, dims 32kb + 8(l/16) + j).  One wave per (kv_head, sequence).  It also
-// writes the NaN rows of sequences whose lengths break the rules, and (an extra row of
-// the grid) the stream-K plan.
+// Q operands of every (sequence, KV head), written once per call by decode_prepare_kernel
+// and read by each piece: the 4 Q rows of the group rotated at query_position and scaled
+// by scale*log2(e) in double, as [B][8][4][128] doubles.  One wave per (kv_head, sequence).
+// It also writes the NaN rows of sequences whose lengths break the rules, and (an extra
+// row of the grid) the stream-K plan.
 //
 // The stream-K plan (row B of the prepare grid, one wave): seq_off[b] = stream position
 // of sequence b's first segment (an exclusive scan of 8 * plan_span), seq_off[B] = total
@@ -530,7 +522,6 @@ __device__ __forceinline__ void build_plan(const DecodeArgs& a, int lane) {
 
 template <bool kRopeQ>
 __global__ __launch_bounds__(kWave) void decode_prepare_kernel(DecodeArgs a) {
-    __shared__ QStage qs;
     const int kvh = blockIdx.x;
     const int b = blockIdx.y;
     const int lane = threadIdx.x;
@@ -554,11 +545,20 @@ __global__ __launch_bounds__(kWave) void decode_prepare_kernel(DecodeArgs a) {
         }
         return;
     }
-    bf16x8_t bq[4];
-    build_q_operands<kRopeQ>(a, raw, rope, qs, bq);
-    bf16x8_t* dst = reinterpret_cast<bf16x8_t*>(a.q_op) + ((static_cast<int64_t>(b) * kHkv + kvh) * 4) * kWave;
+    if (kRopeQ) rope_sincos(raw.qpos, rope.inv_freq, rope.sn, rope.cs);
+    double* dst = a.q_op + (static_cast<int64_t>(b) * kHkv + kvh) * kGroup * kD;
 #pragma unroll
-    for (int kb = 0; kb < 4; ++kb) dst[kb * kWave + lane] = bq[kb];
+    for (int h = 0; h < kGroup; ++h) {
+        const double x = bf16_to_f32(static_cast<uint16_t>(raw.xy[h] & 0xFFFFu));
+        const double y = bf16_to_f32(static_cast<uint16_t>(raw.xy[h] >> 16));
+        double xr = x, yr = y;
+        if (kRopeQ) {
+            xr = x * rope.cs - y * rope.sn;
+            yr = x * rope.sn + y * rope.cs;
+        }
+        dst[h * kD + lane] = xr * a.qk_scale_log2;
+        dst[h * kD + lane + kPairs] = yr * a.qk_scale_log2;
+    }
 }
 
 // Where the rows of one piece live: segment base pointers and this lane's offsets of
@@ -574,18 +574,16 @@ struct PieceRows {
 __device__ __forceinline__ void piece_rows(const DecodeArgs& a, int b, int kvh, int k_a, int k_b,
                                            PieceRows& r) {
     const int lane = threadIdx.x & (kWave - 1);
-    const int n = lane & 15;
-    const int g = lane >> 4;
     const int64_t head_off = static_cast<int64_t>(b) * a.kv_batch_stride +
                              static_cast<int64_t>(kvh) * a.kv_head_stride;
     r.kseg = reinterpret_cast<const char*>(a.k + head_off);
     r.vseg = reinterpret_cast<const char*>(a.v + head_off);
     const uint32_t row = static_cast<uint32_t>(a.kv_pos_stride) * 2u;   // bytes per position
-    r.rows.k = static_cast<uint32_t>(k_a + n) * row + 16u * g;
+    r.rows.k = static_cast<uint32_t>(k_a + (lane & 15)) * row + 16u * (lane >> 4);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) r.rows.v[i] = static_cast<uint32_t>(k_a + 4 * g + i) * row + 16u * n;
-    r.k_last = static_cast<uint32_t>(k_b - 1) * row + 16u * g;
-    r.v_last = static_cast<uint32_t>(k_b - 1) * row + 16u * n;
+    for (int q = 0; q < 4; ++q) r.rows.v[q] = static_cast<uint32_t>(k_a + 4 * q + (lane >> 4)) * row + 16u * (lane & 15);
+    r.k_last = static_cast<uint32_t>(k_b - 1) * row + 16u * (lane >> 4);
+    r.v_last = static_cast<uint32_t>(k_b - 1) * row + 16u * (lane & 15);
 }
 
 __device__ __forceinline__ void load_next(PieceRows& r, uint32_t step, Chunk& c) {
@@ -603,22 +601,20 @@ __device__ __forceinline__ void load_cur_or_next(bool in_cur, PieceRows& cur, co
 #pragma unroll
     for (int kb = 0; kb < 4; ++kb) c.kw[kb] = load_stream16(kp + 64 * kb);
 #pragma unroll
-    for (int it = 0; it < 4; ++it) {
-        const char* vp = in_cur ? cur.vseg + min(cur.rows.v[it], cur.v_last)
-                                : nxt.vseg + min(nxt.rows.v[it], nxt.v_last);
-        c.vw[it] = load_stream16(vp);
+    for (int q = 0; q < 4; ++q) {
+        const char* vp = in_cur ? cur.vseg + min(cur.rows.v[q], cur.v_last)
+                                : nxt.vseg + min(nxt.rows.v[q], nxt.v_last);
+        c.vw[q] = load_stream16(vp);
     }
     advance(cur.rows, step);
 }
 
-__device__ __forceinline__ void load_q_operands(const DecodeArgs& a, int b, int kvh, bf16x8_t (&bq)[4]) {
-    const uint4* qop = a.q_op + ((static_cast<int64_t>(b) * kHkv + kvh) * 4) * kWave + (threadIdx.x & (kWave - 1));
-#pragma unroll
-    for (int kb = 0; kb < 4; ++kb) bq[kb] = as_bf16x8(qop[kb * kWave]);
+__device__ __forceinline__ void load_q_operands(const DecodeArgs& a, int b, int kvh, QOps& qa) {
+    read_q_ops(a.q_op + (static_cast<int64_t>(b) * kHkv + kvh) * kGroup * kD, qa);
 }
 
 // One piece: keys [k_a, k_b) of segment (b, kvh), whose first chunk is already in c0
-// and whose Q operands are in bq.  While the piece's last chunk is computed, the first
+// and whose Q operands are in qa.  While the piece's last chunk is computed, the first
 // chunk of the next piece (rows `nxt`) is requested into c0, so the wave never waits
 // at a piece boundary.  Writes the output rows itself when the piece is the whole
 // segment; otherwise leaves a partial for the merge kernel.  (Requesting the next piece's
@@ -627,19 +623,11 @@ template <bool kRopeK, bool kFused = false>
 __device__ __forceinline__ bool process_piece(const DecodeArgs& a, int b, int kvh, int nv, int k_a,
                                               int k_b, int64_t wg, PieceRows& cur,
                                               const PieceRows& nxt, Chunk& c0, Chunk& c1,
-                                              const bf16x8_t (&bq)[4], PartialStage* stage = nullptr) {
-    const int lane = threadIdx.x & (kWave - 1);
-    const int n = lane & 15;       // MFMA column / PV dim chunk
-    const int g = lane >> 4;       // MFMA lane group / PV key row
+                                              const QOps& qa, PartialStage* stage = nullptr) {
     const uint32_t step = kChunk * static_cast<uint32_t>(a.kv_pos_stride) * 2u;
 
     PieceState st;
-#pragma unroll
-    for (int h = 0; h < kGroup; ++h)
-#pragma unroll
-        for (int j = 0; j < 8; ++j) st.acc[h][j] = 0.0;
-    st.m_run = -INFINITY;
-    st.l_run = 0.f;
+    init_piece(st);
 
     // Two register sets: chunk j+1 is in flight while chunk j is computed.  Chunk i+1
     // of an odd-length piece does not exist; its slot re-reads the piece's last row (a
@@ -648,15 +636,14 @@ __device__ __forceinline__ bool process_piece(const DecodeArgs& a, int b, int kv
     const int n_chunks = (k_b - k_a + kChunk - 1) / kChunk;
     for (int i = 0;; i += 2) {
         load_cur_or_next(true, cur, nxt, step, c1);
-        compute_chunk<kRopeK>(a, k_a + i * kChunk, k_b, n, g, c0, bq, st);
+        compute_chunk<kRopeK>(a, k_a + i * kChunk, k_b, c0, qa, st);
         load_cur_or_next(i + 2 < n_chunks, cur, nxt, step, c0);
-        if (i + 1 < n_chunks) compute_chunk<kRopeK>(a, k_a + (i + 1) * kChunk, k_b, n, g, c1, bq, st);
+        if (i + 1 < n_chunks) compute_chunk<kRopeK>(a, k_a + (i + 1) * kChunk, k_b, c1, qa, st);
         if (i + 2 >= n_chunks) break;
     }
 
-    float m_tot[kGroup];
-    double l_tot[kGroup];
-    merge_rows(st, m_tot, l_tot);
+    double l_tot;
+    finish_piece(st, l_tot);
     if (k_a == 0 && k_b == nv) {
         write_rows(a, b, kvh, st, l_tot);      // the whole segment
         return false;
@@ -667,15 +654,14 @@ __device__ __forceinline__ bool process_piece(const DecodeArgs& a, int b, int kv
         // retires in order, and these stores complete only once written through to memory),
         // else published at once (nothing follows).
         if (stage)
-            stage_partial(*stage, st, m_tot, l_tot);
+            stage_partial(*stage, st, l_tot);
         else
-            publish_partial(a, wg + static_cast<int64_t>(b) * kHkv + kvh, st, m_tot, l_tot);
+            publish_partial(a, wg + static_cast<int64_t>(b) * kHkv + kvh, st, l_tot);
         return true;
     }
-    write_partial(a, wg + static_cast<int64_t>(b) * kHkv + kvh, st, m_tot, l_tot);
+    write_partial(a, wg + static_cast<int64_t>(b) * kHkv + kvh, st, l_tot);
     return false;
 }
-
 // Per-sequence key offsets for 64 sequences at a time, one per lane: o = seq_off[base +
 // lane], o1 = seq_off[base + lane + 1] (the segments of sequence b hold keys [o, o1)).
 struct SeqWindow {
@@ -790,8 +776,8 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(1))) void
     piece_rows(a, b, kvh, key, k_b, cur);
     Chunk c0, c1;
     load_next(cur, step, c0);
-    bf16x8_t bq[4];
-    load_q_operands(a, b, kvh, bq);
+    QOps qa;
+    load_q_operands(a, b, kvh, qa);
 
     while (true) {
         // The next piece of this range (or, after the last one, a re-read of this piece's
@@ -819,10 +805,10 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(1))) void
         }
         PieceRows nxt;
         piece_rows(a, b2, kvh2, key2, k_b2, nxt);
-        bf16x8_t bq2[4];
-        load_q_operands(a, b2, kvh2, bq2);
+        QOps qa2;
+        load_q_operands(a, b2, kvh2, qa2);
 
-        process_piece<kRopeK>(a, b, kvh, nvb, key, k_b, w, cur, nxt, c0, c1, bq);
+        process_piece<kRopeK>(a, b, kvh, nvb, key, k_b, w, cur, nxt, c0, c1, qa);
         if (!more) break;
 
         x = x_next + lead;
@@ -833,8 +819,7 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(1))) void
         k_b = k_b2;
         cur = nxt;
         advance(cur.rows, step);     // its first chunk is in c0 already
-#pragma unroll
-        for (int kb = 0; kb < 4; ++kb) bq[kb] = bq2[kb];
+        qa = qa2;
     }
 }
 
@@ -1102,8 +1087,8 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(1))) void
     rope.cs = 1.0;
     QRaw raw;
     load_q_raw(a, b, kvh, raw);
-    bf16x8_t bq[4];
-    build_q_operands<kRopeQ>(a, raw, rope, qs, bq);
+    QOps qa;
+    build_q_operands<kRopeQ>(a, raw, rope, qs, qa);
 
     SplitPiece first = {0, 0, 0, -1};
     SplitPiece last = {0, 0, 0, -1};
@@ -1131,7 +1116,7 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(1))) void
         piece_rows(a, b2, kvh2, key2, k_b2, nxt);
         load_q_raw(a, b2, kvh2, raw);              // the next piece's Q rows
 
-        if (process_piece<kRopeK, true>(a, b, kvh, nvb, key, k_b, w, cur, nxt, c0, c1, bq,
+        if (process_piece<kRopeK, true>(a, b, kvh, nvb, key, k_b, w, cur, nxt, c0, c1, qa,
                                         more ? &first_part : nullptr)) {
             // a split piece: the range's first (more pieces follow) or its last
             SplitPiece& sp = more ? first : last;
@@ -1141,7 +1126,7 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(1))) void
             sp.seg_off = x - key;
         }
         if (!more) break;
-        build_q_operands<kRopeQ>(a, raw, rope, qs, bq);   // while the next piece's first chunk is in flight
+        build_q_operands<kRopeQ>(a, raw, rope, qs, qa);   // while the next piece's first chunk is in flight
 
         x = x_next + lead;
         b = b2;
@@ -1184,19 +1169,20 @@ __device__ __forceinline__ int64_t page_elem(const DecodeArgs& a, int id_vgpr, i
     return static_cast<int64_t>(ok ? pid : 0) * a.kv_batch_stride + static_cast<int64_t>(kvh) * a.kv_head_stride;
 }
 
-// K and V rows of one block-chunk: lane rows clamped to the chunk's last valid row.
-__device__ __forceinline__ void load_page_chunk(const DecodeArgs& a, int64_t elem, int rows_valid, int n,
-                                                int g, Chunk& c) {
+// K and V rows of one block-chunk (the Chunk lane layout): lane rows clamped to the chunk's
+// last valid row.
+__device__ __forceinline__ void load_page_chunk(const DecodeArgs& a, int64_t elem, int rows_valid, Chunk& c) {
+    const int lane = threadIdx.x & (kWave - 1);
     const char* kp = reinterpret_cast<const char*>(a.k + elem);
     const char* vp = reinterpret_cast<const char*>(a.v + elem);
     const uint32_t row = static_cast<uint32_t>(a.kv_pos_stride) * 2u;
     const int r_last = rows_valid - 1;
-    const char* krow = kp + static_cast<uint32_t>(min(n, r_last)) * row + 16u * g;
+    const char* krow = kp + static_cast<uint32_t>(min(lane & 15, r_last)) * row + 16u * (lane >> 4);
 #pragma unroll
     for (int kb = 0; kb < 4; ++kb) c.kw[kb] = load_stream16(krow + 64 * kb);
 #pragma unroll
-    for (int it = 0; it < 4; ++it)
-        c.vw[it] = load_stream16(vp + static_cast<uint32_t>(min(4 * g + it, r_last)) * row + 16u * n);
+    for (int q = 0; q < 4; ++q)
+        c.vw[q] = load_stream16(vp + static_cast<uint32_t>(min(4 * q + (lane >> 4), r_last)) * row + 16u * (lane & 15));
 }
 
 // A piece of the paged stream: segment (b, kvh), keys [k_a, k_b) of nvp block-padded keys
@@ -1211,11 +1197,9 @@ struct PagePiece {
 // The first chunk of piece `p` (block k_a/16 of sequence p.b, id `id0`) into c; returns
 // whether the id was valid.
 __device__ __forceinline__ bool load_first_page_chunk(const DecodeArgs& a, const PagePiece& p, int id0, Chunk& c) {
-    const int lane = threadIdx.x & (kWave - 1);
     bool ok;
     const int j0 = p.k_a / kChunk;
-    load_page_chunk(a, page_elem(a, id0, p.kvh, ok), max(1, min(kChunk, p.kend - j0 * kChunk)), lane & 15,
-                    lane >> 4, c);
+    load_page_chunk(a, page_elem(a, id0, p.kvh, ok), max(1, min(kChunk, p.kend - j0 * kChunk)), c);
     return ok;
 }
 
@@ -1224,19 +1208,11 @@ __device__ __forceinline__ bool load_first_page_chunk(const DecodeArgs& a, const
 // piece never waits for its first data -- and sets nx.ok.
 template <bool kRopeK>
 __device__ __forceinline__ void process_page_piece(const DecodeArgs& a, const PagePiece& p, int64_t wg, Chunk& c0,
-                                                   Chunk& c1, const bf16x8_t (&bq)[4], bool has_next, PagePiece& nx,
+                                                   Chunk& c1, const QOps& qa, bool has_next, PagePiece& nx,
                                                    int nx_id0) {
-    const int lane = threadIdx.x & (kWave - 1);
-    const int n = lane & 15;
-    const int g = lane >> 4;
     const int b = p.b, kvh = p.kvh, k_a = p.k_a, kend = p.kend;
     PieceState st;
-#pragma unroll
-    for (int h = 0; h < kGroup; ++h)
-#pragma unroll
-        for (int j = 0; j < 8; ++j) st.acc[h][j] = 0.0;
-    st.m_run = -INFINITY;
-    st.l_run = 0.f;
+    init_piece(st);
     bool all_ok = p.ok;
     if (k_a < kend) {
         const int j0 = k_a / kChunk;
@@ -1254,11 +1230,11 @@ __device__ __forceinline__ void process_page_piece(const DecodeArgs& a, const Pa
             {
                 const int j = min(j0 + i + 1, jn);
                 const int id_after = load_block_id(a, b, min(j + 1, jn));
-                load_page_chunk(a, page_elem(a, id_next, kvh, ok), min(kChunk, kend - j * kChunk), n, g, c1);
+                load_page_chunk(a, page_elem(a, id_next, kvh, ok), min(kChunk, kend - j * kChunk), c1);
                 all_ok = all_ok && ok;
                 id_next = id_after;
             }
-            compute_chunk<kRopeK>(a, k_a + i * kChunk, kend, n, g, c0, bq, st);
+            compute_chunk<kRopeK>(a, k_a + i * kChunk, kend, c0, qa, st);
             {
                 const bool last = i + 2 >= n_chunks;
                 const bool to_next = last && has_next;
@@ -1267,35 +1243,31 @@ __device__ __forceinline__ void process_page_piece(const DecodeArgs& a, const Pa
                 const int nj0 = nx.k_a / kChunk;
                 load_page_chunk(a, page_elem(a, to_next ? nx_id0 : id_next, to_next ? nx.kvh : kvh, ok),
                                 to_next ? max(1, min(kChunk, nx.kend - nj0 * kChunk)) : min(kChunk, kend - j * kChunk),
-                                n, g, c0);
+                                c0);
                 if (to_next)
                     nx.ok = ok;
                 else
                     all_ok = all_ok && ok;
                 id_next = id_after;
             }
-            if (i + 1 < n_chunks) compute_chunk<kRopeK>(a, k_a + (i + 1) * kChunk, kend, n, g, c1, bq, st);
+            if (i + 1 < n_chunks) compute_chunk<kRopeK>(a, k_a + (i + 1) * kChunk, kend, c1, qa, st);
             if (i + 2 >= n_chunks) break;
         }
     } else if (has_next) {
         nx.ok = load_first_page_chunk(a, nx, nx_id0, c0);   // a piece of padding only
     }
-    float m_tot[kGroup];
-    double l_tot[kGroup];
-    merge_rows(st, m_tot, l_tot);
+    double l_tot;
+    finish_piece(st, l_tot);
     if (!all_ok) {
         // an invalid block id: poison the sequence's rows of this segment
-#pragma unroll
-        for (int h = 0; h < kGroup; ++h) {
-            m_tot[h] = 0.f;
-            l_tot[h] = __longlong_as_double(0x7ff8000000000000ll);
-        }
+        st.m_run = 0.f;
+        l_tot = __longlong_as_double(0x7ff8000000000000ll);
     }
     if (k_a == 0 && p.k_b == p.nvp) {
         write_rows(a, b, kvh, st, l_tot);      // the whole segment
         return;
     }
-    write_partial(a, wg + static_cast<int64_t>(b) * kHkv + kvh, st, m_tot, l_tot);
+    write_partial(a, wg + static_cast<int64_t>(b) * kHkv + kvh, st, l_tot);
 }
 
 template <bool kRopeK>
@@ -1347,8 +1319,8 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(1))) void
     }
     Chunk c0, c1;
     if (cur.k_a < cur.kend) cur.ok = load_first_page_chunk(a, cur, load_block_id(a, cur.b, cur.k_a / kChunk), c0);
-    bf16x8_t bq[4];
-    load_q_operands(a, cur.b, cur.kvh, bq);
+    QOps qa;
+    load_q_operands(a, cur.b, cur.kvh, qa);
 
     while (true) {
         // The next piece of this range, and everything it needs before its first chunk
@@ -1359,7 +1331,7 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(1))) void
         bool more = x_next + lead < x_end;
         if (more) more = next_segment(a, sw, b2, kvh2, nv2);
         int nx_id0 = cur.id1;
-        bf16x8_t bq2[4];
+        QOps qa2;
         if (more) {
             nx.b = __builtin_amdgcn_readfirstlane(b2);
             nx.kvh = __builtin_amdgcn_readfirstlane(kvh2);
@@ -1372,14 +1344,13 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(1))) void
             nx_id0 = load_block_id(a, nx.b, 0);
             nx.id1 = load_block_id(a, nx.b, min(1, jn2));
             nx.ok = true;
-            load_q_operands(a, nx.b, nx.kvh, bq2);
+            load_q_operands(a, nx.b, nx.kvh, qa2);
         }
-        process_page_piece<kRopeK>(a, cur, w, c0, c1, bq, more, nx, nx_id0);
+        process_page_piece<kRopeK>(a, cur, w, c0, c1, qa, more, nx, nx_id0);
         if (!more) break;
         x = x_next + lead;
         cur = nx;
-#pragma unroll
-        for (int kb = 0; kb < 4; ++kb) bq[kb] = bq2[kb];
+        qa = qa2;
     }
 }
 
@@ -1481,8 +1452,7 @@ constexpr int kSingleWaves = 4;
 template <bool kRopeQ, bool kRopeK>
 __global__ __launch_bounds__(kSingleWaves * kWave) void decode_single_kernel(DecodeArgs a) {
     __shared__ double q_s[kGroup][kD];
-    __shared__ uint16_t codes_s[3][kGroup][kD];          // hi/mid/lo BF16 parts of q_s
-    __shared__ double o_s[kSingleWaves][kGroup][kD];     // each wave's O (row-merged)
+    __shared__ double o_s[kSingleWaves][kGroup][kD];     // each wave's O (blocks summed)
     __shared__ float m_s[kSingleWaves][kGroup];
     __shared__ double l_s[kSingleWaves][kGroup];
     __shared__ int last_s;
@@ -1492,8 +1462,6 @@ __global__ __launch_bounds__(kSingleWaves * kWave) void decode_single_kernel(Dec
     const int kvh = seg % kHkv;
     const int wave = threadIdx.x / kWave;
     const int lane = threadIdx.x % kWave;
-    const int n = lane & 15;
-    const int g = lane >> 4;
     const int nv = seq_valid_keys(a, b);
     if (nv == 0) {
         if (kvh == 0 && piece == 0) {
@@ -1517,7 +1485,8 @@ __global__ __launch_bounds__(kSingleWaves * kWave) void decode_single_kernel(Dec
     Chunk c0, c1;
     load_next(cur, step, c0);
 
-    // Q operands: wave h rotates and scales Q head 4*kvh + h into q_s.
+    // Q operands: wave h rotates and scales Q head 4*kvh + h into q_s; every wave then
+    // reads its QOps back.
     {
         const int qpos = a.query_pos[b];
         double sn = 0.0, cs = 1.0;
@@ -1534,63 +1503,29 @@ __global__ __launch_bounds__(kSingleWaves * kWave) void decode_single_kernel(Dec
         q_s[wave][lane + kPairs] = yr * a.qk_scale_log2;
     }
     __syncthreads();
-    // Each value split once (two per thread), then read back in the MFMA B-operand layout
-    // (lane (g, n), MFMA kb: 8 codes of part n/4 of head n%4, dims 32kb + 8g ..).
-    {
-        const int hh = threadIdx.x >> 6;
-        const int d = 2 * lane;
-#pragma unroll
-        for (int e = 0; e < 2; ++e) {
-            const double v = q_s[hh][d + e];
-            const uint16_t hi = bf16_of(v);
-            const double r1 = v - f64_of_bf16(hi);
-            const uint16_t mid = bf16_of(r1);
-            codes_s[0][hh][d + e] = hi;
-            codes_s[1][hh][d + e] = mid;
-            codes_s[2][hh][d + e] = bf16_of(r1 - f64_of_bf16(mid));
-        }
-    }
-    __syncthreads();
-    bf16x8_t bq[4];
-    {
-        const int part = n < 12 ? n >> 2 : 0;
-#pragma unroll
-        for (int kb = 0; kb < 4; ++kb) {
-            const bf16x8_t v = *reinterpret_cast<const bf16x8_t*>(&codes_s[part][n & 3][32 * kb + 8 * g]);
-            bq[kb] = n < 12 ? v : bf16x8_t{};
-        }
-    }
+    QOps qa;
+    read_q_ops(&q_s[0][0], qa);
 
     PieceState st;
-#pragma unroll
-    for (int h = 0; h < kGroup; ++h)
-#pragma unroll
-        for (int j = 0; j < 8; ++j) st.acc[h][j] = 0.0;
-    st.m_run = -INFINITY;
-    st.l_run = 0.f;
+    init_piece(st);
     if (busy) {
         const int n_chunks = (k_b - k_a + kChunk - 1) / kChunk;
         for (int i = 0;; i += 2) {
             load_next(cur, step, c1);
-            compute_chunk<kRopeK>(a, k_a + i * kChunk, k_b, n, g, c0, bq, st);
+            compute_chunk<kRopeK>(a, k_a + i * kChunk, k_b, c0, qa, st);
             if (i + 1 >= n_chunks) break;
             load_next(cur, step, c0);
-            compute_chunk<kRopeK>(a, k_a + (i + 1) * kChunk, k_b, n, g, c1, bq, st);
+            compute_chunk<kRopeK>(a, k_a + (i + 1) * kChunk, k_b, c1, qa, st);
             if (i + 2 >= n_chunks) break;
         }
     }
-    float m_tot[kGroup];
-    double l_tot[kGroup];
-    merge_rows(st, m_tot, l_tot);
-    if (lane < 16) {
+    double l_tot;
+    finish_piece(st, l_tot);
 #pragma unroll
-        for (int h = 0; h < kGroup; ++h)
-#pragma unroll
-            for (int j = 0; j < 8; ++j) o_s[wave][h][8 * n + j] = st.acc[h][j];
-    }
+    for (int e = 0; e < 8; ++e) (&o_s[wave][0][0])[lane_row_offset() + e] = st.acc[e];
     if (lane < kGroup) {
-        m_s[wave][lane] = lane == 0 ? m_tot[0] : lane == 1 ? m_tot[1] : lane == 2 ? m_tot[2] : m_tot[3];
-        l_s[wave][lane] = lane == 0 ? l_tot[0] : lane == 1 ? l_tot[1] : lane == 2 ? l_tot[2] : l_tot[3];
+        m_s[wave][lane] = st.m_run;
+        l_s[wave][lane] = l_tot;
     }
     __syncthreads();
 

@@ -19,7 +19,7 @@ struct DecodeArgs {
     const int32_t* seq_len;   // [B]
     const int32_t* query_pos; // [B]
     uint16_t* out;            // [B][32][128]
-    uint4* q_op;              // [B][8][4][64] prepared Q operands (MFMA B layout)
+    double* q_op;             // [B][8][4][128] Q rows rotated at query_pos and scaled by scale*log2(e)
     int64_t* plan_hdr;        // {total keys, keys per stream workgroup}
     int64_t* seq_off;         // [B+1] first global key offset of sequence b's segments
     int32_t* seq_nreal;       // [B] keys of sequence b that count (n_valid; the plan pads to blocks)

@@ -1,4 +1,4 @@
-// gqa_multitoken.hip -- multi-token decode for gfx950: chunks of at most 8 new tokens per
+// gqa_multitoken.hip -- multi-token decode for gfx950: chunks of at most 16 new tokens per
 // sequence (draft verification, a few decode steps at once) split stream-K over all CUs
 // with the prefill kernel's arithmetic (gqa_prefill.hip); the golden step per token is
 // pyfiles/gen_gqa_wrapper_vectors.py:121-139 at query position start + t.

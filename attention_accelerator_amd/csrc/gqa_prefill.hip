@@ -37,7 +37,7 @@
 //    thousands of keys adds no fp32 rounding.
 //  * O / l, rounded double -> f32 -> BF16, written in Q-head order.
 //
-// Chunks of at most 8 new tokens take the multi-token decode path instead
+// Chunks of at most 16 new tokens take the multi-token decode path instead
 // (gqa_multitoken.hip), which shares this file's LDS row layout and probability split
 // (gqa_prefill_common.h).
 #include "gqa_device.h"

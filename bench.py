@@ -521,7 +521,7 @@ def main() -> int:
                 f"synthetic N(0,1) BF16, seed {args.seed}",
         "config": {"workload": args.workload, "batch": bsz, "capacity": cap,
                    "min_len": lo, "max_len": hi, "total_keys": sum(lens), "q_heads": 32,
-                   "kv_heads": 8, "head_dim": 128, "rope": "q", "accumulate": "fp32 scores, fp64 weighted V",
+                   "kv_heads": 8, "head_dim": 128, "rope": "q", "accumulate": "fp64 scores, softmax and weighted V (fp64 MFMA)",
                    "bytes_per_step": step_bytes,
                    "infinity_cache": "flushed between steps" if flushed else "working set > 1 GiB",
                    "spinup_s": args.spinup_s, "graph": bool(args.graph)},

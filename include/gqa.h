@@ -58,7 +58,8 @@ typedef struct gqa_params {
     int32_t n_q_heads;
     int32_t n_kv_heads;
     int32_t head_dim;
-    float scale;          /* score scale, normally 1/sqrt(128); 0 is rejected (wrapper.v:237) */
+    double scale;         /* score scale, normally 1/sqrt(128) (the golden's double,
+                             gen_gqa_wrapper_vectors.py:129); 0 is rejected (wrapper.v:237) */
     double rope_theta;    /* normally 500000; must be > 0 when a RoPE flag is set */
     uint32_t flags;       /* GQA_ROPE_Q | GQA_ROPE_K */
 } gqa_params_t;

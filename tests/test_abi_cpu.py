@@ -33,7 +33,7 @@ def test_exports_match_header():
 def test_status_strings_and_version():
     assert _lib.status_string(0) == "ok"
     assert "invalid" in _lib.status_string(1)
-    assert _lib.lib().gqa_abi_version() >> 16 == 1
+    assert _lib.lib().gqa_abi_version() >> 16 == 2
 
 
 @pytest.mark.parametrize("regs,ok", [
