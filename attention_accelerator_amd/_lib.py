@@ -32,6 +32,7 @@ EXPORTS = (
     "gqa_decode_workspace_bytes",
     "gqa_decode_workspace_init",
     "gqa_decode_bf16",
+    "gqa_decode_bf16_noalloc",
     "gqa_decode_paged_workspace_bytes",
     "gqa_decode_paged_bf16",
     "gqa_kv_append_paged_bf16",
@@ -122,6 +123,9 @@ def lib() -> ctypes.CDLL:
                                   ctypes.POINTER(GqaKvLayout), vp, vp, ctypes.c_int32, vp, vp,
                                   ctypes.c_size_t, vp]
     L.gqa_decode_bf16.restype = ctypes.c_int
+    L.gqa_decode_bf16_noalloc.argtypes = [ctypes.POINTER(GqaParams), vp, vp, vp,
+                                          ctypes.POINTER(GqaKvLayout), vp, vp, ctypes.c_int32, vp, vp]
+    L.gqa_decode_bf16_noalloc.restype = ctypes.c_int
     L.gqa_decode_paged_workspace_bytes.argtypes = [ctypes.POINTER(GqaParams), ctypes.c_int32,
                                                    ctypes.c_int32]
     L.gqa_decode_paged_workspace_bytes.restype = ctypes.c_size_t

@@ -144,11 +144,12 @@ hipEvent_t* profile_slot() {
 
 }  // namespace
 
-DecodePlan plan_decode(int32_t batch, int32_t capacity, bool paged) {
+DecodePlan plan_decode(int32_t batch, int32_t capacity, bool paged, int64_t max_single_segments) {
     DecodePlan plan{};
     plan.n_wgs = stream_wgs();
     const int64_t keys_cap = static_cast<int64_t>(batch) * kHkv * capacity;
-    if (!paged && keys_cap <= single_launch_max_keys()) {
+    const bool single_fits = max_single_segments < 0 || static_cast<int64_t>(batch) * kHkv <= max_single_segments;
+    if (!paged && keys_cap <= single_launch_max_keys() && single_fits) {
         // Single launch: about one 4-wave workgroup per CU (n_wgs / 4), pieces of at least
         // 256 keys (64 per wave: below that the last piece's merge of more partials costs
         // more than the shorter streams save; B=1 L=4096 runs in 18.7 us with 256-key pieces,
@@ -227,13 +228,15 @@ size_t gqa_decode_workspace_bytes(const gqa_params_t* params, int32_t batch, int
 namespace {
 
 // Common tail of the contiguous and paged decode entry points: workspace carve-up and launch.
-int decode_launch(const gqa_params_t* params, const uint16_t* q, const uint16_t* k, const uint16_t* v,
-                  int64_t s0, int64_t s1, int64_t s2, int32_t capacity, const int32_t* block_table,
-                  int32_t max_blocks, int32_t n_blocks, const int32_t* seq_len, const int32_t* query_pos,
-                  int32_t batch, uint16_t* out, void* workspace, size_t workspace_bytes, void* stream) {
-    const DecodePlan plan = plan_decode(batch, capacity, block_table != nullptr);
-    if (!workspace || workspace_bytes < plan.workspace_bytes || !aligned(workspace, 256))
-        return GQA_ERR_WORKSPACE;
+// `counters`: the per-segment piece counters of the one-launch paths, when they live outside
+// the workspace (nullptr: at the end of the workspace, as gqa_decode_workspace_bytes counts).
+int decode_launch(const DecodePlan& plan, const gqa_params_t* params, const uint16_t* q, const uint16_t* k,
+                  const uint16_t* v, int64_t s0, int64_t s1, int64_t s2, int32_t capacity,
+                  const int32_t* block_table, int32_t max_blocks, int32_t n_blocks, const int32_t* seq_len,
+                  const int32_t* query_pos, int32_t batch, uint16_t* out, void* workspace,
+                  size_t workspace_bytes, void* stream, unsigned long long* counters = nullptr) {
+    const size_t need = counters ? plan.workspace_bytes - plan.count_bytes : plan.workspace_bytes;
+    if (!workspace || workspace_bytes < need || !aligned(workspace, 256)) return GQA_ERR_WORKSPACE;
 
     DecodeArgs a{};
     a.q = q;
@@ -250,7 +253,7 @@ int decode_launch(const gqa_params_t* params, const uint16_t* q, const uint16_t*
     a.plan_hdr = reinterpret_cast<int64_t*>(pl);
     a.seq_off = reinterpret_cast<int64_t*>(pl + 256);
     a.seq_nreal = reinterpret_cast<int32_t*>(pl + 256 + align_up((static_cast<size_t>(batch) + 1) * sizeof(int64_t), 256));
-    a.seg_count = reinterpret_cast<unsigned long long*>(pl + plan.plan_bytes);
+    a.seg_count = counters ? counters : reinterpret_cast<unsigned long long*>(pl + plan.plan_bytes);
     a.pieces_cap = plan.pieces_cap;
     a.fused = plan.fused;
     a.piece_keys = plan.piece_keys;
@@ -277,14 +280,10 @@ bool paged_layout_ok(const gqa_paged_kv_t* kv) {
            static_cast<int64_t>(kv->max_blocks) * 16 <= 0x7FFFFFFF;
 }
 
-}  // namespace
-
-extern "C" {
-
-int gqa_decode_bf16(const gqa_params_t* params, const uint16_t* q, const uint16_t* k,
-                    const uint16_t* v, const gqa_kv_layout_t* kv, const int32_t* seq_len,
-                    const int32_t* query_pos, int32_t batch, uint16_t* out, void* workspace,
-                    size_t workspace_bytes, void* stream) {
+// Argument checks of the contiguous-cache decode entry points (nothing is launched on error).
+int decode_args_status(const gqa_params_t* params, const uint16_t* q, const uint16_t* k, const uint16_t* v,
+                       const gqa_kv_layout_t* kv, const int32_t* seq_len, const int32_t* query_pos,
+                       int32_t batch, const uint16_t* out) {
     if (!params || !kv) return GQA_ERR_BAD_POINTER;
     if (!geometry_ok(params)) return GQA_ERR_INVALID_CONFIG;
     if (batch <= 0 || kv->capacity <= 0) return GQA_ERR_INVALID_CONFIG;
@@ -300,8 +299,81 @@ int gqa_decode_bf16(const gqa_params_t* params, const uint16_t* q, const uint16_
     if ((static_cast<uint64_t>(kv->capacity) + 64u) * static_cast<uint64_t>(kv->pos_stride) * 2u >
         0xFFFFFF00ull)
         return GQA_ERR_INVALID_CONFIG;
-    return decode_launch(params, q, k, v, kv->batch_stride, kv->head_stride, kv->pos_stride, kv->capacity,
+    return GQA_OK;
+}
+
+// ---- The decode entry point that allocates nothing (gqa_decode_bf16_noalloc): its
+// workspace is this file-scope device array, one copy per GPU, held until the process ends.
+// The first kNoAllocCountBytes hold the per-segment counters of the one-launch paths
+// (they must read zero between calls; every call leaves them so), the rest the plan's
+// partials, Q operands and plan.  Calls on one GPU share it: calls that overlap race.
+constexpr size_t kNoAllocScratchBytes = size_t{32} << 20;
+constexpr size_t kNoAllocCountBytes = size_t{64} << 10;            // 8192 segments
+static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_dev[kMaxDevices] = {};    // device address of `scratch` on each GPU (set-up done)
+
+// Device address of the current GPU's scratch.  The first call on a GPU looks the address
+// up (hipGetSymbolAddress, with that GPU current) and clears the counter region with a fill
+// kernel on `stream` (no memset, so the call may sit in a captured graph).  nullptr and a
+// status on failure.
+void* noalloc_scratch(hipStream_t stream, int& status) {
+    int dev = -1;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+        (void)hipGetLastError();
+        status = GQA_ERR_HIP;
+        return nullptr;
+    }
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_dev[dev]) {
+        void* ptr = nullptr;
+        if (hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)) != hipSuccess || !ptr) {
+            (void)hipGetLastError();
+            status = GQA_ERR_HIP;
+            return nullptr;
+        }
+        if (launch_zero_words(static_cast<uint32_t*>(ptr), static_cast<int64_t>(kNoAllocCountBytes / 4), stream) !=
+            hipSuccess) {
+            status = GQA_ERR_HIP;
+            return nullptr;
+        }
+        g_scratch_dev[dev] = ptr;
+    }
+    status = GQA_OK;
+    return g_scratch_dev[dev];
+}
+
+}  // namespace
+
+extern "C" {
+
+int gqa_decode_bf16(const gqa_params_t* params, const uint16_t* q, const uint16_t* k,
+                    const uint16_t* v, const gqa_kv_layout_t* kv, const int32_t* seq_len,
+                    const int32_t* query_pos, int32_t batch, uint16_t* out, void* workspace,
+                    size_t workspace_bytes, void* stream) {
+    const int st = decode_args_status(params, q, k, v, kv, seq_len, query_pos, batch, out);
+    if (st != GQA_OK) return st;
+    return decode_launch(plan_decode(batch, kv->capacity), params, q, k, v, kv->batch_stride, kv->head_stride,
+                         kv->pos_stride, kv->capacity,
                          nullptr, 0, 0, seq_len, query_pos, batch, out, workspace, workspace_bytes, stream);
+}
+
+int gqa_decode_bf16_noalloc(const gqa_params_t* params, const uint16_t* q, const uint16_t* k,
+                            const uint16_t* v, const gqa_kv_layout_t* kv, const int32_t* seq_len,
+                            const int32_t* query_pos, int32_t batch, uint16_t* out, void* stream) {
+    int st = decode_args_status(params, q, k, v, kv, seq_len, query_pos, batch, out);
+    if (st != GQA_OK) return st;
+    const DecodePlan plan =
+        plan_decode(batch, kv->capacity, false, static_cast<int64_t>(kNoAllocCountBytes / sizeof(unsigned long long)));
+    if (plan.workspace_bytes - plan.count_bytes > kNoAllocScratchBytes - kNoAllocCountBytes) return GQA_ERR_WORKSPACE;
+    char* base = static_cast<char*>(noalloc_scratch(static_cast<hipStream_t>(stream), st));
+    if (!base) return st;
+    return decode_launch(plan, params, q, k, v, kv->batch_stride, kv->head_stride, kv->pos_stride, kv->capacity,
+                         nullptr, 0, 0, seq_len, query_pos, batch, out, base + kNoAllocCountBytes,
+                         kNoAllocScratchBytes - kNoAllocCountBytes, stream,
+                         reinterpret_cast<unsigned long long*>(base));
 }
 
 size_t gqa_decode_paged_workspace_bytes(const gqa_params_t* params, int32_t batch, int32_t max_blocks) {
@@ -322,7 +394,8 @@ int gqa_decode_paged_bf16(const gqa_params_t* params, const uint16_t* q, const u
         !aligned(seq_len, 4) || !aligned(query_pos, 4) || !aligned(block_table, 4))
         return GQA_ERR_BAD_POINTER;
     if (kv->pos_stride % 8 || kv->head_stride % 8 || kv->block_stride % 8) return GQA_ERR_BAD_POINTER;
-    return decode_launch(params, q, k_pool, v_pool, kv->block_stride, kv->head_stride, kv->pos_stride,
+    return decode_launch(plan_decode(batch, kv->max_blocks * 16, true), params, q, k_pool, v_pool,
+                         kv->block_stride, kv->head_stride, kv->pos_stride,
                          kv->max_blocks * 16, block_table, kv->max_blocks, kv->n_blocks, seq_len, query_pos,
                          batch, out, workspace, workspace_bytes, stream);
 }

@@ -60,7 +60,9 @@ struct DecodePlan {
     size_t workspace_bytes;
 };
 
-DecodePlan plan_decode(int32_t batch, int32_t capacity, bool paged = false);
+// max_single_segments >= 0 caps the segments (batch * 8) a single-launch plan may count in
+// (its per-segment counters); larger batches take the stream path.
+DecodePlan plan_decode(int32_t batch, int32_t capacity, bool paged = false, int64_t max_single_segments = -1);
 // ev (optional): three events recorded before the split kernel, between the two
 // kernels and after the combine kernel.
 hipError_t launch_decode(const DecodeArgs& a, int batch, hipStream_t stream,

@@ -129,6 +129,20 @@ int gqa_decode_bf16(const gqa_params_t* params, const uint16_t* q, const uint16_
                     const int32_t* query_pos, int32_t batch, uint16_t* out, void* workspace,
                     size_t workspace_bytes, void* stream);
 
+/* gqa_decode_bf16 without a workspace argument, allocating nothing.  No counterpart in the
+ * reference: it is for callers that cannot allocate device memory (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc).  Same arguments (less the
+ * workspace), results and rules as gqa_decode_bf16.  The workspace is a 32 MiB device array
+ * inside the library, one copy per GPU, held until the process ends; the first call on a
+ * GPU looks up its address and clears its counters with a fill kernel on `stream`.  A batch
+ * whose decode workspace does not fit (about 440 sequences of any capacity on a 256-CU
+ * GPU; gqa_decode_workspace_bytes gives the size) is rejected with GQA_ERR_WORKSPACE before
+ * any launch.  Every call on a GPU shares that array and leaves it as its plan did: calls
+ * that overlap on one GPU (other streams or threads) race, so callers order them. */
+int gqa_decode_bf16_noalloc(const gqa_params_t* params, const uint16_t* q, const uint16_t* k,
+                            const uint16_t* v, const gqa_kv_layout_t* kv, const int32_t* seq_len,
+                            const int32_t* query_pos, int32_t batch, uint16_t* out, void* stream);
+
 /* Paged cache: a pool of blocks of 16 positions (the core's KV_BLOCK_LEN,
  * gqa_controller.v:20); block j of sequence b is pool block block_table[b*max_blocks + j],
  * and row (block id, KV head h, position-in-block r) starts at element
