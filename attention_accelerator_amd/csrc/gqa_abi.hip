@@ -176,6 +176,36 @@ DecodePlan plan_decode(int32_t batch, int32_t capacity, bool paged, int64_t max_
     return plan;
 }
 
+// Rescore region of a prefill or multi-token workspace: header, flagged rows, per-row piece
+// counters, the chunk's cos/sin table, partial slots.
+size_t rescore_bytes(int32_t batch, int32_t n_new) {
+    const size_t rows = static_cast<size_t>(batch) * n_new * kHq;
+    const size_t toks = static_cast<size_t>(batch) * n_new;
+    return 256 + 2 * align_up(rows * sizeof(uint32_t), 256) + align_up(toks * kPairs * sizeof(double2), 256) +
+           align_up(size_t{kRsSlots} * kGroup * kD * sizeof(double), 256) +
+           align_up(size_t{kRsSlots} * kGroup * sizeof(float2), 256);
+}
+
+void rescore_layout(PrefillArgs& a, void* base) {
+    const size_t rows = static_cast<size_t>(a.batch) * a.n_new * kHq;
+    char* p = static_cast<char*>(base);
+    a.rs_hdr = reinterpret_cast<uint32_t*>(p);
+    p += 256;
+    a.rs_rows = reinterpret_cast<uint32_t*>(p);
+    p += align_up(rows * sizeof(uint32_t), 256);
+    a.rs_done = reinterpret_cast<uint32_t*>(p);
+    p += align_up(rows * sizeof(uint32_t), 256);
+    a.rs_cs = reinterpret_cast<double2*>(p);
+    p += align_up(static_cast<size_t>(a.batch) * a.n_new * kPairs * sizeof(double2), 256);
+    a.rs_part_o = reinterpret_cast<double*>(p);
+    p += align_up(size_t{kRsSlots} * kGroup * kD * sizeof(double), 256);
+    a.rs_part_ml = reinterpret_cast<float2*>(p);
+    // One 4-wave workgroup per CU (the kernel's registers allow one wave per SIMD): the
+    // flagged rows are cut into about as many (row, piece) pairs as run at once.
+    const int32_t wgs = stream_wgs() / 4;
+    a.rs_wgs = wgs < 1 ? 1 : wgs > static_cast<int32_t>(kRsSlots) ? static_cast<int32_t>(kRsSlots) : wgs;
+}
+
 }  // namespace gqa
 
 using namespace gqa;
@@ -524,8 +554,9 @@ size_t gqa_prefill_workspace_bytes(const gqa_params_t* params, int32_t batch, in
     if (!params || !geometry_ok(params) || batch <= 0 || n_new <= 0) return 0;
     // The multi-token path needs no split planes: the chunk's unrounded keys enter through
     // the scores its preparation kernel forms.
-    if (use_multi(n_new)) return prefill_multi_bytes(batch, n_new, multi_wgs(n_new));
-    return align_up(prefill_split_bytes(batch, n_new), 256);
+    if (use_multi(n_new))
+        return align_up(prefill_multi_bytes(batch, n_new, multi_wgs(n_new)), 256) + rescore_bytes(batch, n_new);
+    return align_up(prefill_split_bytes(batch, n_new), 256) + rescore_bytes(batch, n_new);
 }
 
 int gqa_kv_append_bf16(const gqa_params_t* params, const uint16_t* k_new, const uint16_t* v_new,
@@ -573,25 +604,30 @@ int gqa_prefill_bf16(const gqa_params_t* params, const uint16_t* q, const uint16
     a.q = q;
     a.out = out;
     const bool multi = use_multi(n_new);
+    char* ws = static_cast<char*>(workspace);
     if (multi) {
         a.k_split = nullptr;
         prefill_multi_layout(a, workspace, multi_wgs(n_new));
         a.skew_pm = xcd_skew_pm(multi_waves(n_new) <= 2 ? 40 : 0);
+        rescore_layout(a, ws + align_up(prefill_multi_bytes(batch, n_new, multi_wgs(n_new)), 256));
     } else {
         a.k_split = static_cast<uint16_t*>(workspace);
+        rescore_layout(a, ws + align_up(prefill_split_bytes(batch, n_new), 256));
     }
     hipStream_t s = static_cast<hipStream_t>(stream);
     hipEvent_t* ev = profile_slot();
     if (ev) (void)hipEventRecord(ev[0], s);
     if (multi) {
         // The preparation kernel of the multi-token path appends the chunk's rows itself.
-        const hipError_t e = launch_prefill_multi(a, s, ev);
+        hipError_t e = launch_prefill_multi(a, s, ev);
+        if (e == hipSuccess) e = launch_rescore(a, s);
         return e == hipSuccess ? GQA_OK : GQA_ERR_HIP;
     }
     hipError_t e = launch_kv_append(a, s);
     if (ev) (void)hipEventRecord(ev[1], s);
     if (e == hipSuccess) e = launch_prefill_attention(a, s);
     if (ev) (void)hipEventRecord(ev[2], s);
+    if (e == hipSuccess) e = launch_rescore(a, s);
     return e == hipSuccess ? GQA_OK : GQA_ERR_HIP;
 }
 

@@ -194,16 +194,20 @@ __device__ __forceinline__ double exp2_f64(double x) {
 }
 
 // Scores, online softmax and weighted V of one chunk [kc, kc+16) (keys >= k_b masked).
-template <bool kRopeK>
-__device__ __forceinline__ void compute_chunk(const DecodeArgs& a, int kc, int k_b, const Chunk& c,
-                                              const QOps& qa, PieceState& st) {
+// kRope 1: each K row is rotated first, at position rope_pos0 + its key index; kRope 2: the
+// same rotation with the cos/sin of key index u read from cs_tab[u * 64 + i] (pair i; rows
+// 0 .. tab_last, lanes past them read the last).
+template <int kRope>
+__device__ __forceinline__ void compute_chunk(const RopeTable& rope, int rope_pos0, int kc, int k_b, const Chunk& c,
+                                              const QOps& qa, PieceState& st, const double2* cs_tab = nullptr,
+                                              int tab_last = 0) {
     // p exchange slice of this wave (workgroups of up to four waves).
     __shared__ double p_lds[4][kWave];
     double* pl = p_lds[(threadIdx.x >> 6) & 3];
     const int lane = threadIdx.x & (kWave - 1);
     // QK^T: four independent accumulation chains (one per kb), summed in a fixed order.
     double s4[4] = {0.0, 0.0, 0.0, 0.0};
-    if (kRopeK) {
+    if (kRope) {
         // Rotate the K row at its position in double: pairs (kb, kb+2) of this lane.
         const int kkey = kc + (lane & 15);
         const int g = lane >> 4;
@@ -215,8 +219,15 @@ __device__ __forceinline__ void compute_chunk(const DecodeArgs& a, int kc, int k
             unpack8(c.kw[kb + 2], yf);
 #pragma unroll
             for (int j = 0; j < 8; ++j) {
+                const int fi = 32 * kb + 8 * g + j;
                 double xr, yr;
-                rope_pair(xf[j], yf[j], kkey, a.rope.inv_freq[32 * kb + 8 * g + j], xr, yr);
+                if (kRope == 2) {
+                    const double2 t = cs_tab[static_cast<int64_t>(min(kkey, tab_last)) * kPairs + fi];
+                    xr = xf[j] * t.x - yf[j] * t.y;
+                    yr = xf[j] * t.y + yf[j] * t.x;
+                } else {
+                    rope_pair(xf[j], yf[j], rope_pos0 + kkey, rope.inv_freq[fi], xr, yr);
+                }
                 kr[kb][j] = xr;
                 kr[kb + 2][j] = yr;
             }
@@ -636,9 +647,9 @@ __device__ __forceinline__ bool process_piece(const DecodeArgs& a, int b, int kv
     const int n_chunks = (k_b - k_a + kChunk - 1) / kChunk;
     for (int i = 0;; i += 2) {
         load_cur_or_next(true, cur, nxt, step, c1);
-        compute_chunk<kRopeK>(a, k_a + i * kChunk, k_b, c0, qa, st);
+        compute_chunk<kRopeK>(a.rope, 0, k_a + i * kChunk, k_b, c0, qa, st);
         load_cur_or_next(i + 2 < n_chunks, cur, nxt, step, c0);
-        if (i + 1 < n_chunks) compute_chunk<kRopeK>(a, k_a + (i + 1) * kChunk, k_b, c1, qa, st);
+        if (i + 1 < n_chunks) compute_chunk<kRopeK>(a.rope, 0, k_a + (i + 1) * kChunk, k_b, c1, qa, st);
         if (i + 2 >= n_chunks) break;
     }
 
@@ -1234,7 +1245,7 @@ __device__ __forceinline__ void process_page_piece(const DecodeArgs& a, const Pa
                 all_ok = all_ok && ok;
                 id_next = id_after;
             }
-            compute_chunk<kRopeK>(a, k_a + i * kChunk, kend, c0, qa, st);
+            compute_chunk<kRopeK>(a.rope, 0, k_a + i * kChunk, kend, c0, qa, st);
             {
                 const bool last = i + 2 >= n_chunks;
                 const bool to_next = last && has_next;
@@ -1250,7 +1261,7 @@ __device__ __forceinline__ void process_page_piece(const DecodeArgs& a, const Pa
                     all_ok = all_ok && ok;
                 id_next = id_after;
             }
-            if (i + 1 < n_chunks) compute_chunk<kRopeK>(a, k_a + (i + 1) * kChunk, kend, c1, qa, st);
+            if (i + 1 < n_chunks) compute_chunk<kRopeK>(a.rope, 0, k_a + (i + 1) * kChunk, kend, c1, qa, st);
             if (i + 2 >= n_chunks) break;
         }
     } else if (has_next) {
@@ -1512,10 +1523,10 @@ __global__ __launch_bounds__(kSingleWaves * kWave) void decode_single_kernel(Dec
         const int n_chunks = (k_b - k_a + kChunk - 1) / kChunk;
         for (int i = 0;; i += 2) {
             load_next(cur, step, c1);
-            compute_chunk<kRopeK>(a, k_a + i * kChunk, k_b, c0, qa, st);
+            compute_chunk<kRopeK>(a.rope, 0, k_a + i * kChunk, k_b, c0, qa, st);
             if (i + 1 >= n_chunks) break;
             load_next(cur, step, c0);
-            compute_chunk<kRopeK>(a, k_a + (i + 1) * kChunk, k_b, c1, qa, st);
+            compute_chunk<kRopeK>(a.rope, 0, k_a + (i + 1) * kChunk, k_b, c1, qa, st);
             if (i + 2 >= n_chunks) break;
         }
     }
@@ -1627,6 +1638,216 @@ __global__ __launch_bounds__(kSingleWaves * kWave) void decode_single_kernel(Dec
     }
     orow[lane] = f32_to_bf16_rne(static_cast<float>(o0 / l)) |
                  (static_cast<uint32_t>(f32_to_bf16_rne(static_cast<float>(o1 / l))) << 16);
+}
+
+// ---------------------------------------------------------------------------------
+// fp64 rescore of the output rows a prefill or multi-token call flags.  Their MFMA kernels
+// carry scores in fp32 (Q in three BF16 parts against BF16 K); an output element that
+// cancels to near zero can then miss 64 BF16 ULP of the golden's double value, so each
+// kernel flags a row holding an element within kRsFlagRatio of the row's rms from zero,
+// and rescore_kernel recomputes the flagged rows with the decode arithmetic (fp64 scores,
+// exp2 and weighted V): the one-token golden step at position start + t over keys
+// 0 .. start + t, the chunk's own keys rotated in double from the new K rows and not
+// re-rounded, as the golden rotates K (pyfiles/gen_gqa_wrapper_vectors.py:121-139).
+//
+// A persistent grid of 4-wave workgroups (one per CU) takes (row, piece) pairs: the flagged
+// rows are split into as many pieces of their keys as there are workgroups (at most
+// kRsMaxPieces per row), a quarter of a piece per wave.  The four MFMA columns are the four Q heads
+// of the row's KV head (its own head's column is written).  A piece's partial is published
+// with agent-scope stores and the row's last piece merges them, as in decode_single_kernel.
+// A row's result depends on its keys and the piece count only, which follows from the
+// number of flagged rows and the grid, never from the order they were flagged in: results are
+// bit-for-bit repeatable.
+
+// Loads chunk [kc, kc+16) in the Chunk layout: K rows at kseg + key * kstride, V rows at
+// vseg + key * vstride (bytes); keys past k_end read row k_end - 1.
+__device__ __forceinline__ void load_chunk_rows(const char* kseg, int64_t kstride, const char* vseg, int64_t vstride,
+                                                int kc, int k_end, Chunk& c) {
+    const int lane = threadIdx.x & (kWave - 1);
+    const char* kp = kseg + static_cast<int64_t>(min(kc + (lane & 15), k_end - 1)) * kstride + 16 * (lane >> 4);
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb) c.kw[kb] = load_stream16(kp + 64 * kb);
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+        c.vw[q] = load_stream16(vseg + static_cast<int64_t>(min(kc + 4 * q + (lane >> 4), k_end - 1)) * vstride +
+                                16 * (lane & 15));
+}
+
+// Keys [k0, k1) of one source, three chunks in flight (kRope 2: K rotated with cs_tab).
+template <int kRope>
+__device__ __forceinline__ void rescore_range(const char* kseg, int64_t kstride, const char* vseg, int64_t vstride,
+                                              int k0, int k1, const QOps& qa, PieceState& st,
+                                              const double2* cs_tab = nullptr) {
+    if (k0 >= k1) return;
+    const RopeTable* no_rope = nullptr;
+    Chunk c[3];
+#pragma unroll
+    for (int i = 0; i < 3; ++i) load_chunk_rows(kseg, kstride, vseg, vstride, min(k0 + i * kChunk, k1 - 1), k1, c[i]);
+    for (int kc = k0;; kc += 3 * kChunk) {
+#pragma unroll
+        for (int i = 0; i < 3; ++i) {
+            const int kci = kc + i * kChunk;
+            compute_chunk<kRope>(*no_rope, 0, kci, k1, c[i], qa, st, cs_tab, k1 - 1);
+            if (kci + kChunk >= k1) return;
+            load_chunk_rows(kseg, kstride, vseg, vstride, min(kci + 3 * kChunk, k1 - 1), k1, c[i]);
+        }
+    }
+}
+
+__global__ __launch_bounds__(4 * kWave) void rescore_kernel(PrefillArgs a) {
+    __shared__ double q_s[kGroup][kD];
+    __shared__ double o_s[4][kGroup][kD];
+    __shared__ float m_s[4][kGroup];
+    __shared__ double l_s[4][kGroup];
+    const int T = a.n_new;
+    const uint32_t cap = static_cast<uint32_t>(a.batch) * static_cast<uint32_t>(T) * kHq;
+    const uint32_t n_rows = min(a.rs_hdr[0], cap);
+    if (n_rows == 0) return;
+    uint32_t n_pieces = gridDim.x / n_rows;      // gridDim.x <= kRsSlots
+    n_pieces = n_pieces < 1 ? 1 : n_pieces > kRsMaxPieces ? kRsMaxPieces : n_pieces;
+    const int wave = threadIdx.x / kWave;
+    const int lane = threadIdx.x % kWave;
+    const int64_t kstride_c = a.kv_pos_stride * 2;                  // cache row bytes
+    const int64_t kstride_n = static_cast<int64_t>(kHkv) * kD * 2;   // new-row bytes
+    const int64_t n_work = static_cast<int64_t>(n_rows) * n_pieces;
+    for (int64_t wk = blockIdx.x; wk < n_work; wk += gridDim.x) {
+        const uint32_t idx = static_cast<uint32_t>(wk / n_pieces);
+        const int piece = static_cast<int>(wk % n_pieces);
+        const uint32_t row = a.rs_rows[idx];
+        const int h = static_cast<int>(row % kHq);
+        const int64_t bt = row / kHq;
+        const int b = static_cast<int>(bt / T);
+        const int t = static_cast<int>(bt % T);
+        const int kvh = h / kGroup;
+        const int st = a.start[b];
+        const int n_keys = st + t + 1;
+        const int per = (n_keys + static_cast<int>(n_pieces) - 1) / static_cast<int>(n_pieces);
+        const int ka = min(n_keys, piece * per);
+        const int kb = min(n_keys, ka + per);
+        const int quarter = (per + 3) / 4;
+        const int k0 = min(kb, ka + wave * quarter);
+        const int k1 = min(kb, k0 + quarter);
+
+        // Q of head 4kvh + wave at token t, rotated at st + t and scaled, into q_s.
+        {
+            double sn = 0.0, cs = 1.0;
+            if (a.flags & 1u) rope_sincos(st + t, a.rope.inv_freq[lane], sn, cs);
+            const uint16_t* qrow = a.q + (bt * kHq + kvh * kGroup + wave) * kD;
+            const double x = bf16_to_f32(qrow[lane]);
+            const double y = bf16_to_f32(qrow[lane + kPairs]);
+            double xr = x, yr = y;
+            if (a.flags & 1u) {
+                xr = x * cs - y * sn;
+                yr = x * sn + y * cs;
+            }
+            q_s[wave][lane] = xr * a.qk_scale_log2;
+            q_s[wave][lane + kPairs] = yr * a.qk_scale_log2;
+        }
+        __syncthreads();
+        QOps qa;
+        read_q_ops(&q_s[0][0], qa);
+
+        PieceState stt;
+        init_piece(stt);
+        const int64_t head_elem = static_cast<int64_t>(b) * a.kv_batch_stride + static_cast<int64_t>(kvh) * a.kv_head_stride;
+        const char* kc_seg = reinterpret_cast<const char*>(a.k + head_elem);
+        const char* vc_seg = reinterpret_cast<const char*>(a.v + head_elem);
+        if (a.flags & 2u) {
+            // cached keys as stored (post-RoPE); the chunk's keys rotated from the new rows
+            rescore_range<0>(kc_seg, kstride_c, vc_seg, kstride_c, k0, min(k1, st), qa, stt);
+            const char* kn_seg = reinterpret_cast<const char*>(a.k_new + (static_cast<int64_t>(b) * T * kHkv + kvh) * kD);
+            const char* vn_seg = vc_seg + static_cast<int64_t>(st) * kstride_c;
+            rescore_range<2>(kn_seg, kstride_n, vn_seg, kstride_c, max(k0, st) - st, k1 - st, qa, stt,
+                             a.rs_cs + static_cast<int64_t>(b) * T * kPairs);
+        } else {
+            rescore_range<0>(kc_seg, kstride_c, vc_seg, kstride_c, k0, k1, qa, stt);
+        }
+        double l_tot;
+        finish_piece(stt, l_tot);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) (&o_s[wave][0][0])[lane_row_offset() + i] = stt.acc[i];
+        if (lane < kGroup) {
+            m_s[wave][lane] = stt.m_run;
+            l_s[wave][lane] = l_tot;
+        }
+        __syncthreads();
+
+        // Wave 0 combines the row's head over the four quarters: lane owns dims 2*lane, +1.
+        const int c = h % kGroup;
+        if (wave == 0) {
+            float mx = -INFINITY;
+#pragma unroll
+            for (int w = 0; w < 4; ++w) mx = fmaxf(mx, m_s[w][c]);
+            double l = 0.0, o0 = 0.0, o1 = 0.0;
+#pragma unroll
+            for (int w = 0; w < 4; ++w) {
+                const float m = m_s[w][c];
+                if (m == -INFINITY) continue;
+                const int ex = static_cast<int>(m - mx);
+                l += ldexp(l_s[w][c], ex);
+                o0 += ldexp(o_s[w][c][2 * lane], ex);
+                o1 += ldexp(o_s[w][c][2 * lane + 1], ex);
+            }
+            uint32_t* orow = reinterpret_cast<uint32_t*>(a.out + static_cast<int64_t>(row) * kD);
+            if (n_pieces == 1) {
+                orow[lane] = f32_to_bf16_rne(static_cast<float>(o0 / l)) |
+                             (static_cast<uint32_t>(f32_to_bf16_rne(static_cast<float>(o1 / l))) << 16);
+            } else {
+                const int64_t slot = static_cast<int64_t>(idx) * n_pieces + piece;
+                unsigned long long* po = reinterpret_cast<unsigned long long*>(a.rs_part_o + slot * kD) + 2 * lane;
+                store_agent(po, o0);
+                store_agent(po + 1, o1);
+                if (lane == 0)
+                    store_agent(reinterpret_cast<unsigned long long*>(a.rs_part_ml + slot),
+                                make_float2(mx, static_cast<float>(l)));
+                wait_vmem();                              // the stores have completed ...
+                __atomic_signal_fence(__ATOMIC_SEQ_CST);  // ... and stay before the count
+                int last = 0;
+                if (lane == 0) last = atomicAdd(&a.rs_done[row], 1u) == n_pieces - 1;
+                last = __shfl(last, 0);
+                __atomic_signal_fence(__ATOMIC_SEQ_CST);  // the merge's loads stay after it
+                if (last) {
+                    // Lane u reads piece u's (m, l); the O partials are read eight pieces
+                    // at a time, every load of a batch in flight together.
+                    const int64_t slot0 = static_cast<int64_t>(idx) * n_pieces;
+                    const int np = static_cast<int>(n_pieces);
+                    const float2 ml = load_agent_f2(a.rs_part_ml + slot0 + min(lane, np - 1));
+                    float m_all = ml.x;
+#pragma unroll
+                    for (int sh = 1; sh < kWave; sh <<= 1) m_all = fmaxf(m_all, __shfl_xor(m_all, sh));
+                    const int my_ex = ml.x == -INFINITY ? -1100 : static_cast<int>(ml.x - m_all);
+                    double lw = lane < np ? ldexp(static_cast<double>(ml.y), my_ex) : 0.0;
+#pragma unroll
+                    for (int sh = 1; sh < kWave; sh <<= 1) lw += __shfl_xor(lw, sh);
+                    o0 = 0.0;
+                    o1 = 0.0;
+                    for (int u0 = 0; u0 < np; u0 += 8) {
+                        double2 ov[8];
+#pragma unroll
+                        for (int u = 0; u < 8; ++u)
+                            ov[u] = load_agent_d2(a.rs_part_o + (slot0 + min(u0 + u, np - 1)) * kD + 2 * lane);
+#pragma unroll
+                        for (int u = 0; u < 8; ++u) {
+                            const int ex = __shfl(my_ex, u0 + u);
+                            if (u0 + u < np) {
+                                o0 += ldexp(ov[u].x, ex);
+                                o1 += ldexp(ov[u].y, ex);
+                            }
+                        }
+                    }
+                    orow[lane] = f32_to_bf16_rne(static_cast<float>(o0 / lw)) |
+                                 (static_cast<uint32_t>(f32_to_bf16_rne(static_cast<float>(o1 / lw))) << 16);
+                }
+            }
+        }
+        __syncthreads();                // LDS reused by the next work item
+    }
+}
+
+hipError_t launch_rescore(const PrefillArgs& a, hipStream_t stream) {
+    if (!a.rs_hdr) return hipSuccess;
+    hipLaunchKernelGGL(rescore_kernel, dim3(static_cast<unsigned>(a.rs_wgs)), dim3(4 * kWave), 0, stream, a);
+    return hipGetLastError();
 }
 
 __global__ __launch_bounds__(256) void zero_words_kernel(uint32_t* p, int64_t n) {

@@ -120,7 +120,43 @@ struct PrefillArgs {
     float* chunk_s;           // [B][8][16W][4W] scores of the chunk's keys u per column (log2 units)
     int32_t n_wgs;            // persistent workgroups of the multi-token stream kernel
     int32_t skew_pm;          // XCD weighting of the ranges (per mille of a range)
+    // fp64 rescore of the output rows the MFMA kernels flag (an element within
+    // kRsFlagRatio of its row's rms from zero); rs_hdr nullptr: off.
+    uint32_t* rs_hdr;         // [1]: flagged rows
+    uint32_t* rs_rows;        // [B*T*32] flagged rows, (b*T + t)*32 + q_head, in flagging order
+    uint32_t* rs_done;        // [B*T*32] finished pieces per flagged row (indexed by row)
+    double2* rs_cs;           // [B][T][64] cos, sin of (start + t) * inv_freq[i] (RoPE on K)
+    double* rs_part_o;        // [kRsSlots][4][128] unnormalised partial outputs
+    float2* rs_part_ml;       // [kRsSlots][4] (running max, sum)
+    int32_t rs_wgs;           // workgroups of the rescore kernel
 };
+
+// Rescore: an output row is recomputed in fp64 when one of its elements lies closer to zero
+// than kRsFlagRatio times the row's rms.  The largest error measured on the MFMA paths is
+// 8.6e-7 of the row's rms (4.8M outputs of N(0,1) inputs, about 5.6 standard deviations
+// of a Gaussian error), so a 64-BF16-ULP miss, which needs an error of a quarter of the
+// element, cannot occur above ~4e-6 of the rms; 2^-17 = 7.6e-6 leaves a margin of 1.7
+// over the 6.4-sigma error of 10^9 outputs.  Squared: min^2 * 128 < ratio^2 * sum x^2.
+constexpr double kRsFlagRatio2 = 1.0 / 17179869184.0;    // (2^-17)^2
+constexpr int kRsSlots = 1024;                            // partial slots (rows x pieces)
+constexpr int kRsMaxPieces = 32;                          // pieces per row at most
+size_t rescore_bytes(int32_t batch, int32_t n_new);
+void rescore_layout(PrefillArgs& a, void* base);
+hipError_t launch_rescore(const PrefillArgs& a, hipStream_t stream);
+
+// Appends a flagged output row (device side).
+__device__ __forceinline__ void rs_append(const PrefillArgs& a, uint32_t row) {
+    const uint32_t i = atomicAdd(a.rs_hdr, 1u);
+    if (i < static_cast<uint32_t>(a.batch) * static_cast<uint32_t>(a.n_new) * kHq) a.rs_rows[i] = row;
+}
+
+// Clears the flagged-row count (the first kernel of a prefill or multi-token call).
+__device__ __forceinline__ void rs_clear(const PrefillArgs& a, int t) {
+    if (a.rs_hdr && t == 0) a.rs_hdr[0] = 0u;
+}
+
+// The same kernel clears row (b*T + t)*32 + h's piece counter and, with RoPE on K, stores
+// the cos/sin table row of token t.
 
 // Chunks of at most this many new tokens per sequence take the multi-token path.
 constexpr int32_t kMultiMaxNew = 16;

@@ -209,6 +209,7 @@ __global__ __launch_bounds__(256) void mt_prepare_kernel(PrefillArgs a) {
     const int lane = threadIdx.x & (kWave - 1);
     if (b == a.batch) {
         if (kvh == 0 && w == 0) mt_build_plan<kW>(a, lane);
+        if (kvh == 1) rs_clear(a, threadIdx.x);
         return;
     }
     const int T = a.n_new;
@@ -265,8 +266,14 @@ __global__ __launch_bounds__(256) void mt_prepare_kernel(PrefillArgs a) {
     const bool rope_q = (a.flags & 1u) != 0;
     const bool rope_k = (a.flags & 2u) != 0;
     if (rope_q || rope_k)
-        for (int u = w; u < T; u += 4)
+        for (int u = w; u < T; u += 4) {
             rope_sincos(static_cast<int64_t>(st) + u, a.rope.inv_freq[lane], sn_s[u][lane], cs_s[u][lane]);
+            if (rope_k && kvh == 0 && a.rs_hdr)
+                a.rs_cs[(static_cast<int64_t>(b) * T + u) * kPairs + lane] = make_double2(cs_s[u][lane], sn_s[u][lane]);
+        }
+    if (a.rs_hdr)
+        for (int i = threadIdx.x; i < T * kGroup; i += blockDim.x)
+            a.rs_done[(static_cast<int64_t>(b) * T + i / kGroup) * kHq + kvh * kGroup + i % kGroup] = 0u;
     __syncthreads();
 
     double qvx[kW][4], qvy[kW][4];
@@ -532,15 +539,31 @@ __device__ __forceinline__ void mt_piece_end(const PrefillArgs& a, int b, int kv
     const double l = swap_add_f64<true>(swap_add_f64<false>(t.l64));
     if (whole) {
         const int tok = 4 * wv + (n >> 2);
+        // Column n's row (lanes n, n+16, n+32, n+48 hold dims 16dt + 4g ..): its smallest
+        // magnitude against its rms decides whether the row is rescored in fp64.
+        double x[8][4], ss = 0.0, mn = INFINITY;
+#pragma unroll
+        for (int dt = 0; dt < 8; ++dt)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                x[dt][i] = t.o64[dt][i] / l;
+                ss = fma(x[dt][i], x[dt][i], ss);
+                mn = fmin(mn, fabs(x[dt][i]));
+            }
+        ss = swap_add_f64<true>(swap_add_f64<false>(ss));
+        mn = fmin(mn, __shfl_xor(mn, 16));
+        mn = fmin(mn, __shfl_xor(mn, 32));
         if (tok >= a.n_new) return;
+        if (g == 0 && a.rs_hdr && mn * mn * kD < kRsFlagRatio2 * ss)
+            rs_append(a, static_cast<uint32_t>((static_cast<int64_t>(b) * a.n_new + tok) * kHq + kvh * kGroup + (n & 3)));
         uint16_t* orow = a.out + ((static_cast<int64_t>(b) * a.n_new + tok) * kHq + kvh * kGroup + (n & 3)) * kD;
 #pragma unroll
         for (int dt = 0; dt < 8; ++dt) {
             uint2 pk;
-            pk.x = f32_to_bf16_rne(static_cast<float>(t.o64[dt][0] / l)) |
-                   (static_cast<uint32_t>(f32_to_bf16_rne(static_cast<float>(t.o64[dt][1] / l))) << 16);
-            pk.y = f32_to_bf16_rne(static_cast<float>(t.o64[dt][2] / l)) |
-                   (static_cast<uint32_t>(f32_to_bf16_rne(static_cast<float>(t.o64[dt][3] / l))) << 16);
+            pk.x = f32_to_bf16_rne(static_cast<float>(x[dt][0])) |
+                   (static_cast<uint32_t>(f32_to_bf16_rne(static_cast<float>(x[dt][1]))) << 16);
+            pk.y = f32_to_bf16_rne(static_cast<float>(x[dt][2])) |
+                   (static_cast<uint32_t>(f32_to_bf16_rne(static_cast<float>(x[dt][3]))) << 16);
             *reinterpret_cast<uint2*>(orow + 16 * dt + 4 * g) = pk;
         }
         return;
@@ -846,8 +869,22 @@ __global__ __launch_bounds__(256 * kW) void mt_merge_kernel(PrefillArgs a) {
         }
     }
     uint16_t h8[8];
+    double ss = 0.0, mn = INFINITY;
 #pragma unroll
-    for (int j = 0; j < 8; ++j) h8[j] = f32_to_bf16_rne(static_cast<float>(o[j] / l));
+    for (int j = 0; j < 8; ++j) {
+        const double x = o[j] / l;
+        h8[j] = f32_to_bf16_rne(static_cast<float>(x));
+        ss = fma(x, x, ss);
+        mn = fmin(mn, fabs(x));
+    }
+    // The column's row is 16 consecutive lanes.
+#pragma unroll
+    for (int d = 1; d < 16; d <<= 1) {
+        ss += __shfl_xor(ss, d);
+        mn = fmin(mn, __shfl_xor(mn, d));
+    }
+    if ((threadIdx.x & 15) == 0 && a.rs_hdr && mn * mn * kD < kRsFlagRatio2 * ss)
+        rs_append(a, static_cast<uint32_t>((static_cast<int64_t>(b) * a.n_new + tok) * kHq + kvh * kGroup + (col & 3)));
     uint2* dst = reinterpret_cast<uint2*>(a.out + ((static_cast<int64_t>(b) * a.n_new + tok) * kHq + kvh * kGroup +
                                                    (col & 3)) * kD + d0);   // out is 8-byte aligned
     dst[0] = make_uint2(h8[0] | (static_cast<uint32_t>(h8[1]) << 16), h8[2] | (static_cast<uint32_t>(h8[3]) << 16));

@@ -74,6 +74,7 @@ __global__ __launch_bounds__(256) void kv_append_kernel(PrefillArgs a) {
             a.k_split + 2 * static_cast<int64_t>(a.batch) * a.n_new * kHkv * kD);
         zero_row[threadIdx.x] = 0u;
     }
+    if (blockIdx.x == 0) rs_clear(a, threadIdx.x);
     if (bt >= static_cast<int64_t>(a.batch) * a.n_new) return;
     const int t = static_cast<int>(bt % a.n_new);
     const int b = static_cast<int>(bt / a.n_new);
@@ -95,6 +96,10 @@ __global__ __launch_bounds__(256) void kv_append_kernel(PrefillArgs a) {
     }
     double sn = 0.0, cs = 1.0;
     if (rope) rope_sincos(pos, a.rope.inv_freq[lane], sn, cs);
+    if (a.rs_hdr) {
+        if (lane < kHq) a.rs_done[bt * kHq + lane] = 0u;
+        if (rope) a.rs_cs[bt * kPairs + lane] = make_double2(cs, sn);
+    }
 #pragma unroll
     for (int kvh = 0; kvh < kHkv; ++kvh) {
         const int64_t row = bt * kHkv + kvh;
@@ -572,18 +577,37 @@ __global__ __launch_bounds__(kPfThreads) void prefill_attn_kernel(PrefillArgs a)
         __syncthreads();
     }
 
-    if (!q_ok) return;
     double l = tl.l64 + __shfl_xor(tl.l64, 16);
     l += __shfl_xor(l, 32);
-    uint16_t* orow = a.out + ((static_cast<int64_t>(b) * T + tq) * kHq + hq) * kD;
+    // The row of query n (lanes n, n+16, n+32, n+48 hold dims 16dt + 4g ..): its smallest
+    // magnitude against its rms decides whether the row is rescored in fp64.
+    double x[8][4], ss = 0.0, mn = INFINITY;
 #pragma unroll
-    for (int dt = 0; dt < 8; ++dt) {
-        uint2 pk;
-        pk.x = f32_to_bf16_rne(static_cast<float>(tl.o64[dt][0] / l)) |
-               (static_cast<uint32_t>(f32_to_bf16_rne(static_cast<float>(tl.o64[dt][1] / l))) << 16);
-        pk.y = f32_to_bf16_rne(static_cast<float>(tl.o64[dt][2] / l)) |
-               (static_cast<uint32_t>(f32_to_bf16_rne(static_cast<float>(tl.o64[dt][3] / l))) << 16);
-        *reinterpret_cast<uint2*>(orow + 16 * dt + 4 * g) = pk;
+    for (int dt = 0; dt < 8; ++dt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            x[dt][i] = tl.o64[dt][i] / l;
+            ss = fma(x[dt][i], x[dt][i], ss);
+            mn = fmin(mn, fabs(x[dt][i]));
+        }
+    ss += __shfl_xor(ss, 16);
+    ss += __shfl_xor(ss, 32);
+    mn = fmin(mn, __shfl_xor(mn, 16));
+    mn = fmin(mn, __shfl_xor(mn, 32));
+    if (!q_ok) return;
+    if (g == 0 && a.rs_hdr && mn * mn * kD < kRsFlagRatio2 * ss)
+        rs_append(a, static_cast<uint32_t>((static_cast<int64_t>(b) * T + tq) * kHq + hq));
+    {
+        uint16_t* orow = a.out + ((static_cast<int64_t>(b) * T + tq) * kHq + hq) * kD;
+#pragma unroll
+        for (int dt = 0; dt < 8; ++dt) {
+            uint2 pk;
+            pk.x = f32_to_bf16_rne(static_cast<float>(x[dt][0])) |
+                   (static_cast<uint32_t>(f32_to_bf16_rne(static_cast<float>(x[dt][1]))) << 16);
+            pk.y = f32_to_bf16_rne(static_cast<float>(x[dt][2])) |
+                   (static_cast<uint32_t>(f32_to_bf16_rne(static_cast<float>(x[dt][3]))) << 16);
+            *reinterpret_cast<uint2*>(orow + 16 * dt + 4 * g) = pk;
+        }
     }
 }
 

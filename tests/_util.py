@@ -61,31 +61,3 @@ def assert_within_ulp(want, got, max_ulp: int = 64, what: str = "", ref64=None) 
 
 __all__ = ["to_dev", "to_codes", "assert_within_ulp", "ulp_distance"]
 
-
-# Absolute error floor of the MFMA paths: scores accumulate in fp32 (Q in three BF16 parts
-# against BF16 K), about 1e-7 in the log2 domain, which moves an N(0,1)-input output by up
-# to ~1e-8.  An output that cancels to within ~4e-8 of zero can therefore exceed 64 BF16
-# ULP of its own tiny value while being as accurate as its neighbours.
-MFMA_FLOOR_ABS = 2e-8
-
-
-def assert_within_ulp_or_floor(want, got, ref64, max_ulp: int = 64, floor_abs: float = MFMA_FLOOR_ABS,
-                               what: str = "") -> int:
-    """64 BF16 ULP per element (the reference checker's policy), except elements whose
-    absolute error against the double-precision golden is within floor_abs; returns the
-    number of such floor elements."""
-    want = np.asarray(want, dtype=np.uint16).reshape(-1)
-    got = np.asarray(got, dtype=np.uint16).reshape(-1)
-    ref = np.asarray(ref64, dtype=np.float64).reshape(-1)
-    bad = failures(want.reshape(-1, 128), got.reshape(-1, 128), max_ulp).reshape(-1)
-    err = np.abs(bf16_value(got) - ref)
-    floor = bad & (err <= floor_abs)
-    real = bad & ~floor
-    if bad.any():
-        idx = np.nonzero(bad)[0][:8]
-        print(f"{what}: {int(bad.sum())} elements over {max_ulp} ULP, {int(floor.sum())} within the "
-              f"{floor_abs:.0e} floor: " + ", ".join(f"{i}: golden {ref[i]:.3e} got {bf16_value(got[i:i+1])[0]:.3e}"
-                                                      for i in idx))
-    assert not real.any(), (f"{what}: {int(real.sum())} elements exceed {max_ulp} ULP and the "
-                            f"{floor_abs:.0e} absolute floor")
-    return int(floor.sum())

@@ -15,7 +15,7 @@ import torch
 
 import attention_accelerator_amd as gqa
 from oracle import oracle as orc
-from _util import assert_within_ulp_or_floor, to_codes
+from _util import assert_within_ulp, to_codes
 
 pytestmark = pytest.mark.gpu
 
@@ -42,8 +42,9 @@ def _oracle(q, kn, vn, k, v, starts, rope_q=True, rope_k=True):
 
 
 def _check(want, got, what):
-    """64 ULP per element, or the fp32 score floor for an element that cancels to near zero."""
-    return assert_within_ulp_or_floor(want[0], got, want[1], 64, what=what)
+    """64 BF16 ULP per element (an output row that cancels to near zero is rescored in fp64
+    by the library); returns the worst distance."""
+    return assert_within_ulp(want[0], got, 64, what, ref64=want[1])
 
 
 def _run(q, kn, vn, k, v, starts, dev, **kw):
@@ -60,16 +61,15 @@ _STARTS = [0, 1, 15, 16, 33, 700, 2047, 4100]
 
 @pytest.mark.parametrize("n_new", [1, 2, 3, 4, 5, 8, 11, 16])
 def test_multi_all_rows_against_oracle(dev, n_new):
-    """Every output row (up to 8 x 16 x 32 x 128 = 524,288 elements) within 64 ULP, or
-    within the fp32 score floor of the double-precision golden for the rare element that
-    cancels to near zero (the prefill attention kernel misses the same elements by the same
-    amount)."""
+    """Every output row (up to 8 x 16 x 32 x 128 = 524,288 elements) within 64 ULP of the
+    oracle.  At T=16 one element of these inputs cancels to 2.0e-9 (10^7 times smaller than
+    its neighbours): the MFMA kernels' fp32 scores put it at -5.8e-9, so its row is flagged
+    and rescored in fp64."""
     starts = _STARTS
     q, kn, vn, k, v = _chunk(starts, n_new, max(starts) + n_new + 5, 30 + n_new)
     want = _oracle(q, kn, vn, k, v, starts)
     got, kd, vd = _run(q, kn, vn, k, v, starts, dev)
-    n_floor = _check(want, got, f"multi T={n_new}")
-    print(f"T={n_new}: {n_floor} elements at the fp32 score floor")
+    _check(want, got, f"multi T={n_new}")
     kc, vc = to_codes(kd), to_codes(vd)
     for b, s in enumerate(starts):
         assert np.array_equal(vc[b, :, s:s + n_new], to_codes(vn[b]).transpose(1, 0, 2))
@@ -237,4 +237,4 @@ def test_multi_long_context_sampled_rows(dev):
     rows = [0, n_new - 1]
     want, want64 = orc.prefill(to_codes(q), to_codes(k), to_codes(v), to_codes(kn), to_codes(vn),
                                np.asarray([st]), rows=rows, want_f64=True)
-    assert_within_ulp_or_floor(want, got[:, rows], want64, 64, what="multi 131072")
+    assert_within_ulp(want, got[:, rows], 64, "multi 131072", ref64=want64)
