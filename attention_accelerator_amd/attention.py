@@ -75,7 +75,18 @@ def new_workspace(batch: int, capacity: int, device, params: Optional[GqaParams]
     check(lib().gqa_decode_workspace_init(ctypes.byref(p), int(batch), int(capacity), ws.data_ptr(),
                                           nbytes, _stream_handle(torch.device(device))),
           "gqa_decode_workspace_init")
+    ws.gqa_decode_plan = (int(batch), int(capacity))
     return ws
+
+
+def _check_workspace_plan(workspace: torch.Tensor, batch: int, capacity: int) -> None:
+    """A workspace from new_workspace carries the (batch, capacity) it was prepared for;
+    the single-launch path's piece counters sit where that plan puts them, so another
+    plan would find stale data there and leave rows unwritten.  Reject the mismatch."""
+    plan = getattr(workspace, "gqa_decode_plan", None)
+    if plan is not None and plan != (int(batch), int(capacity)):
+        raise ValueError(f"workspace was prepared for (batch, capacity) = {plan}, called with "
+                         f"({batch}, {capacity}); make one with new_workspace({batch}, {capacity}, ...)")
 
 
 def gqa_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
@@ -135,6 +146,7 @@ def gqa_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
     elif workspace.numel() * workspace.element_size() < ws_bytes:
         raise ValueError(f"workspace holds {workspace.numel() * workspace.element_size()} bytes; "
                          f"{ws_bytes} needed")
+    _check_workspace_plan(workspace, batch, capacity)
     if out is None:
         out = torch.empty((batch, q.shape[1], q.shape[2]), dtype=torch.bfloat16, device=device)
     elif out.shape != (batch, q.shape[1], q.shape[2]) or out.dtype != torch.bfloat16 \
@@ -207,6 +219,9 @@ class PreparedDecode:
                                   self.capacity)
         self.workspace = new_workspace(self.batch, self.capacity, q.device, self.params)
         ws_bytes = self.workspace.numel()
+        if out is not None and (out.shape != (self.batch, N_Q_HEADS, HEAD_DIM) or out.dtype != torch.bfloat16
+                                or not out.is_contiguous() or out.device != q.device):
+            raise ValueError("out must be a contiguous bfloat16 [B,32,128] tensor on q's device")
         self.out = out if out is not None else torch.empty(
             (self.batch, N_Q_HEADS, HEAD_DIM), dtype=torch.bfloat16, device=q.device)
         self._keep = (q.contiguous(), k_cache, v_cache, query_position.contiguous(),
@@ -387,6 +402,8 @@ def _paged_layout(k_pool: torch.Tensor, v_pool: torch.Tensor, block_table: torch
         raise ValueError("pool rows must be contiguous in head_dim")
     if block_table.dim() != 2 or block_table.dtype != torch.int32 or not block_table.is_cuda:
         raise ValueError("block_table must be an int32 [B, max_blocks] tensor on the GPU")
+    if k_pool.shape[1] != N_KV_HEADS or k_pool.shape[3] != HEAD_DIM:
+        raise ValueError(f"pools hold {N_KV_HEADS} KV heads of {HEAD_DIM} dimensions per block")
     return GqaPagedKv(k_pool.stride(0), k_pool.stride(1), k_pool.stride(2), BLOCK_SIZE,
                       block_table.shape[1], k_pool.shape[0])
 
@@ -399,7 +416,7 @@ def gqa_decode_paged(q: torch.Tensor, k_pool: torch.Tensor, v_pool: torch.Tensor
     """gqa_attention over a paged cache: q [B, 32, 128]; k_pool, v_pool [n_blocks, 8, 16,
     128]; block_table [B, max_blocks] int32 (block j of sequence b holds positions
     16j .. 16j+15).  Host lengths are checked against capacity = 16 * max_blocks."""
-    if q.dim() != 3 or q.dtype != torch.bfloat16 or not q.is_cuda:
+    if q.dim() != 3 or q.dtype != torch.bfloat16 or not q.is_cuda or q.shape[1:] != (N_Q_HEADS, HEAD_DIM):
         raise ValueError("q must be a bfloat16 [B,32,128] tensor on the GPU")
     layout = _paged_layout(k_pool, v_pool, block_table)
     batch = q.shape[0]
@@ -426,6 +443,8 @@ def gqa_decode_paged(q: torch.Tensor, k_pool: torch.Tensor, v_pool: torch.Tensor
                          f"{ws_bytes} needed")
     if out is None:
         out = torch.empty((batch, N_Q_HEADS, HEAD_DIM), dtype=torch.bfloat16, device=device)
+    elif out.shape != (batch, N_Q_HEADS, HEAD_DIM) or out.dtype != torch.bfloat16 or not out.is_contiguous():
+        raise ValueError("out must be a contiguous bfloat16 [B,32,128] tensor")
     q = q.contiguous()
     bt = block_table.contiguous()
     status = lib().gqa_decode_paged_bf16(

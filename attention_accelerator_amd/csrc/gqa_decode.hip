@@ -947,7 +947,8 @@ __device__ __forceinline__ void store_merged(const DecodeArgs& a, int b, int kvh
 
 __device__ __forceinline__ void finish_split_pieces(const DecodeArgs& a, const SplitPiece& p1, const SplitPiece& p2,
                                                     int64_t per_wg) {
-    wait_vmem();                                   // the partials' stores have completed
+    wait_vmem();                                   // the partials' stores have completed ...
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);       // ... and the compiler keeps them before the count
     const int lane = threadIdx.x & (kWave - 1);
     int d1 = -1, d2 = -1;
     if (lane == 0) {
@@ -956,6 +957,7 @@ __device__ __forceinline__ void finish_split_pieces(const DecodeArgs& a, const S
     }
     d1 = __builtin_amdgcn_readfirstlane(d1);
     d2 = __builtin_amdgcn_readfirstlane(d2);
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);       // the merge's loads are not hoisted above the count
     int64_t w1 = 0, w2 = 0;
     const int n1 = p1.seg_off >= 0 ? count_pieces(p1.seg_off, p1.nv, per_wg, w1) : 0;
     const int n2 = p2.seg_off >= 0 ? count_pieces(p2.seg_off, p2.nv, per_wg, w2) : 0;
@@ -1566,7 +1568,10 @@ __global__ __launch_bounds__(kSingleWaves * kWave) void decode_single_kernel(Dec
     // not coherent with the other XCDs'), and wait until they have completed before the
     // counter is touched: a __threadfence here would write back the whole L2 instead.
     // The counter's atomic returns only after it is performed, and the merge's agent-scope
-    // loads are issued after that.
+    // loads are issued after that.  The hardware order comes from the waits (vmcnt(0)
+    // before the count, the atomic's return value before any merge load); the signal
+    // fences and the barriers keep the compiler from moving a store below the count or a
+    // load above it.
     {
         unsigned long long* po =
             reinterpret_cast<unsigned long long*>(a.part_o + ((slot0 + piece) * kGroup + h) * kD) + 2 * lane;
@@ -1576,6 +1581,7 @@ __global__ __launch_bounds__(kSingleWaves * kWave) void decode_single_kernel(Dec
             store_agent(reinterpret_cast<unsigned long long*>(a.part_ml + (slot0 + piece) * kGroup + h),
                         make_float2(mx, static_cast<float>(l)));
         wait_vmem();
+        __atomic_signal_fence(__ATOMIC_SEQ_CST);
     }
     __syncthreads();
     // Count finished pieces (device-scope atomic); the last piece merges and resets the
@@ -1583,6 +1589,7 @@ __global__ __launch_bounds__(kSingleWaves * kWave) void decode_single_kernel(Dec
     if (threadIdx.x == 0) last_s = atomicAdd(&a.seg_count[seg], 1ull) == static_cast<unsigned long long>(n_pieces - 1);
     __syncthreads();
     if (!last_s) return;
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
     if (threadIdx.x == 0) __hip_atomic_store(&a.seg_count[seg], 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 
     // Merge the segment's pieces, wave h for head h (lane owns dims 2*lane, 2*lane + 1), in

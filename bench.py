@@ -88,36 +88,83 @@ def calibrate_copy(torch, dev):
     del src, dst
 
 
-def cpu_baseline(batch, budget_s: float = 12.0):
+def codes_of(t):
+    """bfloat16 tensor -> uint16 BF16 codes on the host."""
+    import numpy as np
+    import torch
+    return t.detach().contiguous().view(torch.int16).cpu().numpy().view(np.uint16)
+
+
+def parity_summary(want, want64, got) -> dict:
+    """The GPU rows against the oracle's rows for the same inputs: worst BF16 ULP, elements
+    over 64 ULP under the reference checker's policy (pyfiles/check_gqa_output.py:57-64),
+    and the largest |GPU - golden| against the golden's float64 value (before rounding)."""
+    import numpy as np
+
+    from attention_accelerator_amd.check import failures, ulp_distance
+    want = np.asarray(want, dtype=np.uint16).reshape(-1, 128)
+    got = np.asarray(got, dtype=np.uint16).reshape(-1, 128)
+    gv = (got.astype(np.uint32) << 16).view(np.float32).astype(np.float64)
+    wv = (want.astype(np.uint32) << 16).view(np.float32).astype(np.float64)
+    w64 = np.asarray(want64).reshape(-1, 128)
+    return {"max_ulp": int(ulp_distance(want, got).max()),
+            "max_abs_err_vs_f64": float(np.abs(gv - w64).max()),
+            # the golden's own BF16 rows are this far from its float64 values (output rounding)
+            "golden_bf16_max_abs_err_vs_f64": float(np.abs(wv - w64).max()),
+            "fails_64ulp": int(failures(want, got, 64).sum()), "elements": int(want.size)}
+
+
+def python_golden(q, k, v, seq_len: int, qpos: int, nbytes: int, what: str) -> dict:
+    """The reference's own arithmetic, pure Python (oracle/golden_model.golden_attention,
+    a restatement of pyfiles/gen_gqa_wrapper_vectors.py:124-139), timed on one query token
+    (all 32 heads), 1 thread; q [32, 128], k / v [8, >= seq_len, 128] BF16 codes, K taken
+    as post-RoPE (Q rotated)."""
+    from oracle import golden_model as gm
+    qb, kb, vb = q.tolist(), k[:, :seq_len].tolist(), v[:, :seq_len].tolist()
+    t0 = time.perf_counter()
+    gm.golden_attention(qb, kb, vb, seq_len, qpos, rope_q=True, rope_k=False)
+    t = time.perf_counter() - t0
+    return {"value": round(nbytes / t / 1e9, 6), "unit": "GB/s", "cores": 1, "seconds": round(t, 2),
+            "sample": f"{what}: {seq_len} keys, all 32 heads, pure-Python golden loop"}
+
+
+def cpu_baseline(batch, gpu_out, budget_s: float = 12.0):
     """The compiled oracle (C restatement of the golden loop, double, 1 thread) on the
-    first sequences of the same batch until ~budget_s of CPU work."""
+    first sequences of the same batch until ~budget_s of CPU work; the GPU's rows for
+    those sequences against its rows (parity), and the pure-Python golden loop on the
+    batch's shortest sequence beside it."""
     import numpy as np
 
     from attention_accelerator_amd.stimulus import algorithmic_bytes_decode
     from oracle import oracle as orc
 
-    def codes(t):
-        return t.contiguous().view(__import__("torch").int16).cpu().numpy().view(np.uint16)
-
-    done, t_total, lens = 0, 0.0, []
+    done, t_total, lens, wants, wants64 = 0, 0.0, [], [], []
     bsz = batch.q.shape[0]
     while done < bsz and t_total < budget_s:
         n = int(batch.seq_len[done])
-        q = codes(batch.q[done:done + 1])
-        k = codes(batch.k[done:done + 1, :, :n])
-        v = codes(batch.v[done:done + 1, :, :n])
+        q = codes_of(batch.q[done:done + 1])
+        k = codes_of(batch.k[done:done + 1, :, :n])
+        v = codes_of(batch.v[done:done + 1, :, :n])
         t0 = time.perf_counter()
-        orc.decode(q, k, v, batch.seq_len[done:done + 1].numpy(),
-                   batch.query_pos[done:done + 1].numpy())
+        w, w64 = orc.decode(q, k, v, batch.seq_len[done:done + 1].numpy(),
+                            batch.query_pos[done:done + 1].numpy(), want_f64=True)
         t_total += time.perf_counter() - t0
+        wants.append(w)
+        wants64.append(w64)
         lens.append(n)
         done += 1
     gbs = algorithmic_bytes_decode(lens) / t_total / 1e9
+    s = int(np.argmin(batch.seq_len.numpy()))
+    n = int(batch.seq_len[s])
+    py = python_golden(codes_of(batch.q[s]), codes_of(batch.k[s, :, :n]), codes_of(batch.v[s, :, :n]), n,
+                       int(batch.query_pos[s]), algorithmic_bytes_decode([n]), f"sequence {s} (the shortest)")
     return {"value": round(gbs, 4), "unit": "GB/s", "cores": 1, "kind": "port",
             "sample": (f"sequences 0..{done - 1} of the same batch ({done} of {bsz}, "
                        f"{sum(lens)} keys, all 32 heads), compiled oracle in double, "
                        f"{t_total:.2f} s; os.cpu_count()={os.cpu_count()}, "
-                       f"affinity={len(os.sched_getaffinity(0))}")}
+                       f"affinity={len(os.sched_getaffinity(0))}"),
+            "parity": parity_summary(np.concatenate(wants), np.concatenate(wants64), gpu_out[:done]),
+            "python_golden": py}
 
 def prefill_flops(batch: int, n_new: int, start: int) -> int:
     """QK^T and PV multiply-adds of a chunk, 2 flops each: token t sees start+t+1 keys."""
@@ -125,30 +172,40 @@ def prefill_flops(batch: int, n_new: int, start: int) -> int:
     return batch * 32 * keys * 128 * 4
 
 
-def prefill_cpu_baseline(q, kn, vn, k, v, starts, budget_s: float = 12.0):
-    """The compiled oracle (double, 1 thread) on the first rows of sequence 0."""
+def prefill_cpu_baseline(q, kn, vn, k, v, starts, gpu_out, budget_s: float = 12.0):
+    """The compiled oracle (double, 1 thread) on the first rows of sequence 0, the GPU's
+    rows against its rows (parity), and the pure-Python golden loop on token 0 beside it."""
     import numpy as np
 
     from oracle import oracle as orc
 
-    def codes(t):
-        return t.contiguous().view(__import__("torch").int16).cpu().numpy().view(np.uint16)
-
     s0 = int(starts[0])
-    qc, knc, vnc = codes(q[:1]), codes(kn[:1]), codes(vn[:1])
-    kc, vc = codes(k[:1, :, :s0]), codes(v[:1, :, :s0])
-    rows, t_total, step = [], 0.0, 8
+    qc, knc, vnc = codes_of(q[:1]), codes_of(kn[:1]), codes_of(vn[:1])
+    kc, vc = codes_of(k[:1, :, :s0]), codes_of(v[:1, :, :s0])
+    rows, t_total, step, wants, wants64 = [], 0.0, 8, [], []
     while t_total < budget_s and len(rows) < q.shape[1]:
         batch_rows = list(range(len(rows), min(len(rows) + step, q.shape[1])))
         t0 = time.perf_counter()
-        orc.prefill(qc, kc, vc, knc, vnc, np.asarray([s0]), rows=batch_rows)
+        w, w64 = orc.prefill(qc, kc, vc, knc, vnc, np.asarray([s0]), rows=batch_rows, want_f64=True)
         t_total += time.perf_counter() - t0
+        wants.append(w)
+        wants64.append(w64)
         rows += batch_rows
     flops = sum(32 * (s0 + t + 1) * 128 * 4 for t in rows)
+    # token 0 of sequence 0 sees the cache and its own new row (timing only: the new K row
+    # enters unrotated and this output is not compared)
+    k0 = np.concatenate([kc[0], knc[0, :1].reshape(8, 1, 128)], axis=1)
+    v0 = np.concatenate([vc[0], vnc[0, :1].reshape(8, 1, 128)], axis=1)
+    py = python_golden(qc[0, 0], k0, v0, s0 + 1, s0, 32 * (s0 + 1) * 128 * 4, "token 0 of sequence 0")
+    py["unit"] = "FLOP/s"
+    py["value"] = round(32 * (s0 + 1) * 128 * 4 / py["seconds"], 1)
     return {"value": round(flops / t_total / 1e12, 6), "unit": "TFLOP/s", "cores": 1, "kind": "port",
             "sample": (f"tokens 0..{rows[-1]} of sequence 0 ({len(rows)} of {q.shape[1]} tokens, all "
                        f"32 heads, {s0} cached keys), compiled oracle in double, {t_total:.2f} s; "
-                       f"os.cpu_count()={os.cpu_count()}, affinity={len(os.sched_getaffinity(0))}")}
+                       f"os.cpu_count()={os.cpu_count()}, affinity={len(os.sched_getaffinity(0))}"),
+            "parity": parity_summary(np.concatenate(wants, axis=1), np.concatenate(wants64, axis=1),
+                                     gpu_out[:1, :len(rows)]),
+            "python_golden": py}
 
 
 def spin_up(call, torch, seconds: float) -> None:
@@ -210,6 +267,8 @@ def bench_prefill(args, torch, gqa, dev) -> int:
         append_ms, attn_ms = ap_ms / n, at_ms / n
     print(f"[bench] {args.steps} steps: {ms_per_step * 1e3:.2f} us/step", file=sys.stderr, flush=True)
 
+    torch.cuda.synchronize()
+    gpu_out = None if args.no_cpu_baseline else codes_of(out)     # the last step's rows
     tflops = flops / (ms_per_step * 1e-3) / 1e12
     roofline = None
     if attn_ms:
@@ -240,7 +299,7 @@ def bench_prefill(args, torch, gqa, dev) -> int:
                    "flops_per_step": flops, "spinup_s": args.spinup_s},
         "roofline": roofline,
         "cpu_baseline": None if args.no_cpu_baseline else prefill_cpu_baseline(
-            q, kn, vn, k_host, v_host, [start] * bsz),
+            q, kn, vn, k_host, v_host, [start] * bsz, gpu_out),
     }
     print(json.dumps(result), flush=True)
     return 0
@@ -253,29 +312,39 @@ def multitoken_bytes(lengths, n_new: int) -> int:
     return kv + 2 * len(lengths) * n_new * 32 * 128 * 2
 
 
-def multitoken_cpu_baseline(q, kn, vn, k, v, starts, n_new: int, budget_s: float = 12.0):
-    """The compiled oracle (double, 1 thread) on whole sequences (all new tokens) from 0 on."""
+def multitoken_cpu_baseline(q, kn, vn, k, v, starts, n_new: int, gpu_out, budget_s: float = 12.0):
+    """The compiled oracle (double, 1 thread) on whole sequences (all new tokens) from 0 on,
+    the GPU's rows against its rows (parity), and the pure-Python golden loop on the first
+    new token of the shortest sequence beside it."""
     import numpy as np
 
     from oracle import oracle as orc
 
-    def codes(t):
-        return t.contiguous().view(__import__("torch").int16).cpu().numpy().view(np.uint16)
-
-    done, t_total, byts = 0, 0.0, 0
+    done, t_total, byts, wants, wants64 = 0, 0.0, 0, [], []
     while t_total < budget_s and done < q.shape[0]:
         b, s0 = done, int(starts[done])
-        qc, knc, vnc = codes(q[b:b + 1]), codes(kn[b:b + 1]), codes(vn[b:b + 1])
-        kc, vc = codes(k[b:b + 1, :, :s0]), codes(v[b:b + 1, :, :s0])
+        qc, knc, vnc = codes_of(q[b:b + 1]), codes_of(kn[b:b + 1]), codes_of(vn[b:b + 1])
+        kc, vc = codes_of(k[b:b + 1, :, :s0]), codes_of(v[b:b + 1, :, :s0])
         t0 = time.perf_counter()
-        orc.prefill(qc, kc, vc, knc, vnc, np.asarray([s0]), rows=list(range(n_new)))
+        w, w64 = orc.prefill(qc, kc, vc, knc, vnc, np.asarray([s0]), rows=list(range(n_new)), want_f64=True)
         t_total += time.perf_counter() - t0
+        wants.append(w)
+        wants64.append(w64)
         byts += multitoken_bytes([s0 + n_new], n_new)
         done += 1
+    b = int(np.argmin(np.asarray(starts)))
+    s0 = int(starts[b])
+    qc, knc, vnc = codes_of(q[b]), codes_of(kn[b]), codes_of(vn[b])
+    k0 = np.concatenate([codes_of(k[b, :, :s0]), knc[0].reshape(8, 1, 128)], axis=1)   # timing only
+    v0 = np.concatenate([codes_of(v[b, :, :s0]), vnc[0].reshape(8, 1, 128)], axis=1)
+    py = python_golden(qc[0], k0, v0, s0 + 1, s0, multitoken_bytes([s0 + 1], 1),
+                       f"new token 0 of sequence {b} (the shortest)")
     return {"value": round(byts / t_total / 1e9, 4), "unit": "GB/s", "cores": 1, "kind": "port",
             "sample": (f"sequences 0..{done - 1} ({done} of {q.shape[0]}, all {n_new} new tokens, all 32 "
                        f"heads), compiled oracle in double, {t_total:.2f} s; "
-                       f"os.cpu_count()={os.cpu_count()}, affinity={len(os.sched_getaffinity(0))}")}
+                       f"os.cpu_count()={os.cpu_count()}, affinity={len(os.sched_getaffinity(0))}"),
+            "parity": parity_summary(np.concatenate(wants), np.concatenate(wants64), gpu_out[:done]),
+            "python_golden": py}
 
 
 def bench_multitoken(args, torch, gqa, dev, stimulus) -> int:
@@ -317,6 +386,7 @@ def bench_multitoken(args, torch, gqa, dev, stimulus) -> int:
         gqa.profile_enable(0)
         append_ms, attn_ms = ap_ms / n, at_ms / n
     print(f"[bench] {args.steps} steps: {ms_per_step * 1e3:.2f} us/step", file=sys.stderr, flush=True)
+    gpu_out = None if args.no_cpu_baseline else codes_of(out)     # the last step's rows
     if args.calibrate_copy:
         calibrate_copy(torch, dev)
     roofline = None
@@ -352,7 +422,7 @@ def bench_multitoken(args, torch, gqa, dev, stimulus) -> int:
                    "bytes_per_step": step_bytes, "spinup_s": args.spinup_s},
         "roofline": roofline,
         "cpu_baseline": None if args.no_cpu_baseline else multitoken_cpu_baseline(
-            q, kn, vn, k_host, v_host, starts_l, n_new),
+            q, kn, vn, k_host, v_host, starts_l, n_new, gpu_out),
     }
     print(json.dumps(result), flush=True)
     return 0
@@ -494,6 +564,9 @@ def main() -> int:
 
     if args.calibrate_copy:
         calibrate_copy(torch, dev)
+    res = call()
+    torch.cuda.synchronize()
+    gpu_out = None if args.no_cpu_baseline else codes_of(out if res is None else res)
 
     gbs = step_bytes / (ms_per_step * 1e-3) / 1e9
     roofline = None
@@ -528,7 +601,7 @@ def main() -> int:
         "roofline": roofline,
         "cpu_baseline": None if args.no_cpu_baseline else cpu_baseline(
             stimulus.DecodeBatch(batch.q.cpu(), batch.k, batch.v, batch.seq_len,
-                                 batch.query_pos)),
+                                 batch.query_pos), gpu_out),
     }
     print(json.dumps(result), flush=True)
     return 0

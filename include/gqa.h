@@ -102,7 +102,10 @@ size_t gqa_decode_workspace_bytes(const gqa_params_t* params, int32_t batch, int
  * may sit inside a captured graph).  Required once before a workspace's first decode
  * call: small batches finish in one launch and count finished pieces in it (each call
  * leaves the counters at zero again).  A workspace prepared for (batch, capacity) serves
- * later calls with the same batch and capacity.  No reference counterpart. */
+ * later calls with the same batch and capacity only: before a call with another batch or
+ * capacity, call gqa_decode_workspace_init again (the counters sit where that plan puts
+ * them; stale partial data there would leave output rows unwritten).  No reference
+ * counterpart. */
 int gqa_decode_workspace_init(const gqa_params_t* params, int32_t batch, int32_t capacity,
                               void* workspace, size_t workspace_bytes, void* stream);
 

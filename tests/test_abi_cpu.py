@@ -193,3 +193,32 @@ def test_kv_append_rejects_before_launch():
     assert L.gqa_kv_append_bf16(ctypes.byref(p), 256, 256, 256, 256, ctypes.byref(lay), 256, 1, 65, None) == BAD_CFG
     assert L.gqa_kv_append_bf16(ctypes.byref(p), 256, None, 256, 256, ctypes.byref(lay), 256, 1, 1, None) == BAD_PTR
     assert L.gqa_kv_append_bf16(ctypes.byref(p), 256, 256, 264, 256, ctypes.byref(lay), 256, 1, 1, None) == BAD_PTR
+
+
+def test_workspace_plan_tag():
+    """A workspace tagged with its (batch, capacity) plan is rejected for another plan
+    (the single-launch counters sit at a plan-dependent offset); untagged buffers pass."""
+    import torch
+    from attention_accelerator_amd.attention import _check_workspace_plan
+    ws = torch.empty(16, dtype=torch.uint8)
+    _check_workspace_plan(ws, 4, 1000)                 # untagged: the caller's contract
+    ws.gqa_decode_plan = (4, 1000)
+    _check_workspace_plan(ws, 4, 1000)
+    with pytest.raises(ValueError, match="prepared for"):
+        _check_workspace_plan(ws, 4, 2000)
+    with pytest.raises(ValueError, match="prepared for"):
+        _check_workspace_plan(ws, 3, 1000)
+
+
+def test_python_shape_checks_before_any_launch():
+    """Host-side shape checks of the paged entry point reject wrong geometry on the CPU
+    (tensors not on a GPU are rejected before any library call)."""
+    import torch
+    import attention_accelerator_amd as gqa
+    q = torch.zeros((2, 32, 128), dtype=torch.bfloat16)
+    pool = torch.zeros((4, 8, 16, 128), dtype=torch.bfloat16)
+    table = torch.zeros((2, 2), dtype=torch.int32)
+    with pytest.raises(ValueError):
+        gqa.gqa_decode_paged(q, pool, pool, table, [0, 0], [1, 1])
+    with pytest.raises(ValueError):
+        gqa.gqa_decode_paged(q[:, :16], pool, pool, table, [0, 0], [1, 1])

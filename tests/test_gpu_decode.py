@@ -320,3 +320,16 @@ def test_long_context_131072(dev):
         rows = [h for kvh in heads for h in range(4 * kvh, 4 * kvh + 4)]
         assert_within_ulp(want[0, rows], out1[s, rows], 64, f"L=131072 seq {s} heads {heads}",
                           ref64=want64[0, rows])
+
+
+def test_workspace_plan_mismatch_rejected(dev):
+    """A workspace from new_workspace(B, S) serves (B, S) only: another capacity or batch
+    is rejected on the host before any launch."""
+    b = stimulus.decode_batch(2, 1024, seed=21)
+    ws = gqa.new_workspace(2, 2048, dev)
+    with pytest.raises(ValueError, match="prepared for"):
+        gqa.gqa_attention(b.q.to(dev), b.k.to(dev), b.v.to(dev), b.query_pos, b.seq_len, workspace=ws)
+    ws = gqa.new_workspace(2, 1024, dev)
+    got = _codes(gqa.gqa_attention(b.q.to(dev), b.k.to(dev), b.v.to(dev), b.query_pos, b.seq_len,
+                                   workspace=ws))
+    assert_within_ulp(_oracle(b), got, 64, "tagged workspace")
