@@ -182,8 +182,7 @@ size_t rescore_bytes(int32_t batch, int32_t n_new) {
     const size_t rows = static_cast<size_t>(batch) * n_new * kHq;
     const size_t toks = static_cast<size_t>(batch) * n_new;
     return 256 + 2 * align_up(rows * sizeof(uint32_t), 256) + align_up(toks * kPairs * sizeof(double2), 256) +
-           align_up(size_t{kRsSlots} * kGroup * kD * sizeof(double), 256) +
-           align_up(size_t{kRsSlots} * kGroup * sizeof(float2), 256);
+           align_up(size_t{kRsSlots} * kD * sizeof(double), 256) + align_up(size_t{kRsSlots} * sizeof(float2), 256);
 }
 
 void rescore_layout(PrefillArgs& a, void* base) {
@@ -198,11 +197,11 @@ void rescore_layout(PrefillArgs& a, void* base) {
     a.rs_cs = reinterpret_cast<double2*>(p);
     p += align_up(static_cast<size_t>(a.batch) * a.n_new * kPairs * sizeof(double2), 256);
     a.rs_part_o = reinterpret_cast<double*>(p);
-    p += align_up(size_t{kRsSlots} * kGroup * kD * sizeof(double), 256);
+    p += align_up(size_t{kRsSlots} * kD * sizeof(double), 256);
     a.rs_part_ml = reinterpret_cast<float2*>(p);
-    // One 4-wave workgroup per CU (the kernel's registers allow one wave per SIMD): the
-    // flagged rows are cut into about as many (row, piece) pairs as run at once.
-    const int32_t wgs = stream_wgs() / 4;
+    // One-wave workgroups, one per SIMD (the kernel's registers allow one wave per SIMD):
+    // the flagged rows are cut into about as many (row, piece) pairs as run at once.
+    const int32_t wgs = stream_wgs();
     a.rs_wgs = wgs < 1 ? 1 : wgs > static_cast<int32_t>(kRsSlots) ? static_cast<int32_t>(kRsSlots) : wgs;
 }
 

@@ -194,13 +194,10 @@ __device__ __forceinline__ double exp2_f64(double x) {
 }
 
 // Scores, online softmax and weighted V of one chunk [kc, kc+16) (keys >= k_b masked).
-// kRope 1: each K row is rotated first, at position rope_pos0 + its key index; kRope 2: the
-// same rotation with the cos/sin of key index u read from cs_tab[u * 64 + i] (pair i; rows
-// 0 .. tab_last, lanes past them read the last).
+// kRope: each K row is rotated first, at position rope_pos0 + its key index.
 template <int kRope>
 __device__ __forceinline__ void compute_chunk(const RopeTable& rope, int rope_pos0, int kc, int k_b, const Chunk& c,
-                                              const QOps& qa, PieceState& st, const double2* cs_tab = nullptr,
-                                              int tab_last = 0) {
+                                              const QOps& qa, PieceState& st) {
     // p exchange slice of this wave (workgroups of up to four waves).
     __shared__ double p_lds[4][kWave];
     double* pl = p_lds[(threadIdx.x >> 6) & 3];
@@ -221,13 +218,7 @@ __device__ __forceinline__ void compute_chunk(const RopeTable& rope, int rope_po
             for (int j = 0; j < 8; ++j) {
                 const int fi = 32 * kb + 8 * g + j;
                 double xr, yr;
-                if (kRope == 2) {
-                    const double2 t = cs_tab[static_cast<int64_t>(min(kkey, tab_last)) * kPairs + fi];
-                    xr = xf[j] * t.x - yf[j] * t.y;
-                    yr = xf[j] * t.y + yf[j] * t.x;
-                } else {
-                    rope_pair(xf[j], yf[j], rope_pos0 + kkey, rope.inv_freq[fi], xr, yr);
-                }
+                rope_pair(xf[j], yf[j], rope_pos0 + kkey, rope.inv_freq[fi], xr, yr);
                 kr[kb][j] = xr;
                 kr[kb + 2][j] = yr;
             }
@@ -1652,70 +1643,251 @@ __global__ __launch_bounds__(kSingleWaves * kWave) void decode_single_kernel(Dec
 // carry scores in fp32 (Q in three BF16 parts against BF16 K); an output element that
 // cancels to near zero can then miss 64 BF16 ULP of the golden's double value, so each
 // kernel flags a row holding an element within kRsFlagRatio of the row's rms from zero,
-// and rescore_kernel recomputes the flagged rows with the decode arithmetic (fp64 scores,
-// exp2 and weighted V): the one-token golden step at position start + t over keys
-// 0 .. start + t, the chunk's own keys rotated in double from the new K rows and not
-// re-rounded, as the golden rotates K (pyfiles/gen_gqa_wrapper_vectors.py:121-139).
+// and rescore_kernel recomputes the flagged rows in fp64 throughout (scores, exp2 and
+// weighted V): the one-token golden step at position start + t over keys 0 .. start + t,
+// the chunk's own keys rotated in double from the new K rows and not re-rounded, as the
+// golden rotates K (pyfiles/gen_gqa_wrapper_vectors.py:121-139).
 //
-// A persistent grid of 4-wave workgroups (one per CU) takes (row, piece) pairs: the flagged
-// rows are split into as many pieces of their keys as there are workgroups (at most
-// kRsMaxPieces per row), a quarter of a piece per wave.  The four MFMA columns are the four Q heads
-// of the row's KV head (its own head's column is written).  A piece's partial is published
-// with agent-scope stores and the row's last piece merges them, as in decode_single_kernel.
-// A row's result depends on its keys and the piece count only, which follows from the
-// number of flagged rows and the grid, never from the order they were flagged in: results are
-// bit-for-bit repeatable.
+// One row is one Q head, so the work is fp64 VALU, not MFMA (an fp64 MFMA would compute
+// four columns for one): lane l of a wave holds key slot l/8 of an 8-key chunk and the 16
+// dims {8c + i, 64 + 8c + i : i < 8}, c = l % 8 -- 8 rotate_half pairs, so a chunk key's
+// rotation is lane-local.  A key's score is the sum over its eight lanes; each lane
+// accumulates p * V over its own keys for its 16 dims, and the 8 key slots are summed once
+// per piece.
+//
+// A persistent grid of one-wave workgroups takes (row, piece) pairs: every flagged row's
+// chunks are dealt to as many pieces as there are workgroups per row (at most
+// kRsMaxPieces), piece p taking chunks p, p + n_pieces, ..., so that the pieces share the
+// costlier chunk keys evenly.  A piece's partial row is published with agent-scope stores
+// and the row's last piece merges them, as in decode_single_kernel.  A row's result depends
+// on its keys and the piece count only, which follows from the number of flagged rows and
+// the grid, never from the order they were flagged in: results are bit-for-bit repeatable.
 
-// Loads chunk [kc, kc+16) in the Chunk layout: K rows at kseg + key * kstride, V rows at
-// vseg + key * vstride (bytes); keys past k_end read row k_end - 1.
-__device__ __forceinline__ void load_chunk_rows(const char* kseg, int64_t kstride, const char* vseg, int64_t vstride,
-                                                int kc, int k_end, Chunk& c) {
-    const int lane = threadIdx.x & (kWave - 1);
-    const char* kp = kseg + static_cast<int64_t>(min(kc + (lane & 15), k_end - 1)) * kstride + 16 * (lane >> 4);
-#pragma unroll
-    for (int kb = 0; kb < 4; ++kb) c.kw[kb] = load_stream16(kp + 64 * kb);
-#pragma unroll
-    for (int q = 0; q < 4; ++q)
-        c.vw[q] = load_stream16(vseg + static_cast<int64_t>(min(kc + 4 * q + (lane >> 4), k_end - 1)) * vstride +
-                                16 * (lane & 15));
+constexpr int kRsKeys = 8;              // keys per rescore chunk (one per 8 lanes)
+
+// This lane's 16 dims of one K row and one V row (BF16): x dims 8c .. 8c+7, y dims 64 + 8c ..
+struct RsRows {
+    uint4 kx, ky, vx, vy;
+};
+
+__device__ __forceinline__ void rs_load(const char* krow, const char* vrow, RsRows& r) {
+    const int c = threadIdx.x & 7;
+    r.kx = load_stream16(krow + 16 * c);
+    r.ky = load_stream16(krow + 2 * kPairs + 16 * c);
+    r.vx = load_stream16(vrow + 16 * c);
+    r.vy = load_stream16(vrow + 2 * kPairs + 16 * c);
 }
 
-// Keys [k0, k1) of one source, three chunks in flight (kRope 2: K rotated with cs_tab).
-template <int kRope>
-__device__ __forceinline__ void rescore_range(const char* kseg, int64_t kstride, const char* vseg, int64_t vstride,
-                                              int k0, int k1, const QOps& qa, PieceState& st,
-                                              const double2* cs_tab = nullptr) {
-    if (k0 >= k1) return;
-    const RopeTable* no_rope = nullptr;
-    Chunk c[3];
+// (cos, sin) of this lane's 8 frequencies 8c + i from a cos/sin row (64 pairs).
+__device__ __forceinline__ void rs_load_cs(const double2* cs_row, double2 (&cs)[8]) {
+    const double2* p = cs_row + 8 * (threadIdx.x & 7);
 #pragma unroll
-    for (int i = 0; i < 3; ++i) load_chunk_rows(kseg, kstride, vseg, vstride, min(k0 + i * kChunk, k1 - 1), k1, c[i]);
-    for (int kc = k0;; kc += 3 * kChunk) {
+    for (int i = 0; i < 8; ++i) cs[i] = p[i];
+}
+
+// 8 BF16 values -> double (exact).
+__device__ __forceinline__ void rs_widen(const uint4& w, double* d) {
+    const uint32_t u[4] = {w.x, w.y, w.z, w.w};
 #pragma unroll
-        for (int i = 0; i < 3; ++i) {
-            const int kci = kc + i * kChunk;
-            compute_chunk<kRope>(*no_rope, 0, kci, k1, c[i], qa, st, cs_tab, k1 - 1);
-            if (kci + kChunk >= k1) return;
-            load_chunk_rows(kseg, kstride, vseg, vstride, min(kci + 3 * kChunk, k1 - 1), k1, c[i]);
+    for (int j = 0; j < 4; ++j) {
+        d[2 * j] = static_cast<double>(__uint_as_float(u[j] << 16));
+        d[2 * j + 1] = static_cast<double>(__uint_as_float(u[j] & 0xffff0000u));
+    }
+}
+
+// Sum over the eight lanes of a key slot (lanes 8j .. 8j+7), the same bits in all eight:
+// within quads by DPP lane swaps, then across the two quads.
+__device__ __forceinline__ double rs_slot_sum(double x) {
+    int lo = __double2loint(x), hi = __double2hiint(x);
+    x += __hiloint2double(__builtin_amdgcn_mov_dpp(hi, 0xB1, 0xF, 0xF, false),
+                          __builtin_amdgcn_mov_dpp(lo, 0xB1, 0xF, 0xF, false));     // quad_perm 1,0,3,2
+    lo = __double2loint(x);
+    hi = __double2hiint(x);
+    x += __hiloint2double(__builtin_amdgcn_mov_dpp(hi, 0x4E, 0xF, 0xF, false),
+                          __builtin_amdgcn_mov_dpp(lo, 0x4E, 0xF, 0xF, false));     // quad_perm 2,3,0,1
+    return x + __shfl_xor(x, 4);
+}
+
+// Running state of a piece: this lane's O over its keys (its 16 dims), the sum of p over
+// its keys (each key counted in all eight of its lanes) and the wave's running max.
+struct RsState {
+    double o[16];
+    double l;
+    float m;
+};
+
+// Lazy running max (integer-valued, wave-uniform): raised to the ceiling of the largest
+// score when one exceeds it by more than kMaxHeadroom; O and l move by an exact power of 2.
+template <int G>
+__device__ __forceinline__ void rs_raise_max(const double (&s)[G], RsState& st) {
+    bool grow = false;
+#pragma unroll
+    for (int g = 0; g < G; ++g) grow |= s[g] > static_cast<double>(st.m) + kMaxHeadroom;
+    if (__ballot(grow)) {
+        float cm = static_cast<float>(s[0]);
+#pragma unroll
+        for (int g = 1; g < G; ++g) cm = fmaxf(cm, static_cast<float>(s[g]));
+#pragma unroll
+        for (int sh = 8; sh < kWave; sh <<= 1) cm = fmaxf(cm, __shfl_xor(cm, sh));
+        const float m_new = ceilf(cm);
+        const int shift = (st.m == -INFINITY) ? 0 : static_cast<int>(st.m - m_new);
+#pragma unroll
+        for (int i = 0; i < 16; ++i) st.o[i] = ldexp(st.o[i], shift);
+        st.l = ldexp(st.l, shift);
+        st.m = m_new;
+    }
+}
+
+// G chunks at once (their score, exp2 and weighted-V chains interleave): one key per 8
+// lanes in each (valid[g]: inside the row's keys); kRot: K rotated with cs first.  The
+// chunks are accumulated in order g = 0, 1, ...
+template <int G, bool kRot>
+__device__ __forceinline__ void rs_chunks(const RsRows* r, const double (&q)[16], const bool (&valid)[G],
+                                          const double2 (*cs)[8], RsState& st) {
+    double sa[G], sb[G];
+#pragma unroll
+    for (int g = 0; g < G; ++g) sa[g] = sb[g] = 0.0;
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+        double k[16];
+        rs_widen(r[g].kx, k);
+        rs_widen(r[g].ky, k + 8);
+        if (kRot) {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const double x = k[i], y = k[8 + i];
+                k[i] = x * cs[g][i].x - y * cs[g][i].y;
+                k[8 + i] = x * cs[g][i].y + y * cs[g][i].x;
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            sa[g] = fma(q[i], k[i], sa[g]);
+            sb[g] = fma(q[8 + i], k[8 + i], sb[g]);
+        }
+    }
+    double s[G];
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+        s[g] = rs_slot_sum(sa[g] + sb[g]);
+        if (!valid[g]) s[g] = -INFINITY;
+    }
+    rs_raise_max<G>(s, st);
+    double p[G];
+#pragma unroll
+    for (int g = 0; g < G; ++g) p[g] = valid[g] ? exp2_f64(fmax(s[g] - static_cast<double>(st.m), -2000.0)) : 0.0;
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+        st.l += p[g];
+        double v[16];
+        rs_widen(r[g].vx, v);
+        rs_widen(r[g].vy, v + 8);
+#pragma unroll
+        for (int i = 0; i < 16; ++i) st.o[i] = fma(p[g], v[i], st.o[i]);
+    }
+}
+
+// Geometry of one (row, piece) pair.
+struct RsItem {
+    const char* kc_seg;      // cache K rows of (b, kvh)
+    const char* vc_seg;      // cache V rows of (b, kvh)
+    const char* kn_seg;      // new K rows of (b, kvh), token u at u * 8 * 128 elements
+    const double2* cs_seg;   // cos/sin rows of (b, token)
+    int64_t stride_c;        // cache row bytes
+    int st, n_keys;          // first chunk key; keys
+};
+
+// Cached chunks of this piece (ci = c0, c0 + step, ... < c_end): rows as stored, in groups
+// of kRsGroup chunks computed together, two groups in flight.  rs_prefetch requests the
+// first two groups (before the Q operands are formed); rs_cached runs them and the rest.
+constexpr int kRsGroup = 4;
+
+__device__ __forceinline__ void rs_issue_group(const RsItem& it, int ci, int c_end, int step, RsRows (&r)[kRsGroup]) {
+    const int j = threadIdx.x >> 3;
+#pragma unroll
+    for (int g = 0; g < kRsGroup; ++g) {
+        const int cc = min(ci + g * step, max(c_end - 1, 0));
+        const int64_t off = static_cast<int64_t>(min(kRsKeys * cc + j, it.n_keys - 1)) * it.stride_c;
+        rs_load(it.kc_seg + off, it.vc_seg + off, r[g]);
+    }
+}
+
+__device__ __forceinline__ void rs_prefetch(const RsItem& it, int c0, int c_end, int step, RsRows (&r)[2][kRsGroup]) {
+    rs_issue_group(it, c0, c_end, step, r[0]);
+    rs_issue_group(it, c0 + kRsGroup * step, c_end, step, r[1]);
+}
+
+__device__ __forceinline__ void rs_cached(const RsItem& it, int c0, int c_end, int step, const double (&q)[16],
+                                          RsState& st, RsRows (&r)[2][kRsGroup]) {
+    if (c0 >= c_end) return;
+    const int j = threadIdx.x >> 3;
+    const double2 (*no_cs)[8] = nullptr;
+    for (int ci = c0;; ci += 2 * kRsGroup * step) {
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const int cg = ci + h * kRsGroup * step;
+            bool valid[kRsGroup];
+#pragma unroll
+            for (int g = 0; g < kRsGroup; ++g) valid[g] = cg + g * step < c_end && kRsKeys * (cg + g * step) + j < it.n_keys;
+            rs_chunks<kRsGroup, false>(r[h], q, valid, no_cs, st);
+            if (cg + kRsGroup * step >= c_end) return;
+            rs_issue_group(it, cg + 2 * kRsGroup * step, c_end, step, r[h]);
         }
     }
 }
 
-__global__ __launch_bounds__(4 * kWave) void rescore_kernel(PrefillArgs a) {
-    __shared__ double q_s[kGroup][kD];
-    __shared__ double o_s[4][kGroup][kD];
-    __shared__ float m_s[4][kGroup];
-    __shared__ double l_s[4][kGroup];
+// Chunks holding chunk keys (ci = c0, c0 + step, ... < c_end): a key >= start is its new
+// row rotated in double with the cos/sin row of its token; a key < start (a chunk that
+// straddles start) is its cache row, rotated by (1, 0), which leaves it exact.  Two in
+// flight, each with its cos/sin values.
+__device__ __forceinline__ void rs_new(const RsItem& it, int c0, int c_end, int step, const double (&q)[16],
+                                       RsState& st) {
+    if (c0 >= c_end) return;
+    const int j = threadIdx.x >> 3;
+    RsRows r[2];
+    double2 cs[2][8];
+    auto issue = [&](int ci, RsRows& rr, double2 (&cc)[8]) {
+        const int key = min(kRsKeys * ci + j, it.n_keys - 1);
+        const int u = max(key - it.st, 0);
+        const char* krow = key >= it.st ? it.kn_seg + static_cast<int64_t>(u) * (kHkv * kD * 2)
+                                        : it.kc_seg + static_cast<int64_t>(key) * it.stride_c;
+        rs_load(krow, it.vc_seg + static_cast<int64_t>(key) * it.stride_c, rr);
+        rs_load_cs(it.cs_seg + static_cast<int64_t>(u) * kPairs, cc);
+        if (key < it.st) {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) cc[i] = make_double2(1.0, 0.0);
+        }
+    };
+#pragma unroll
+    for (int i = 0; i < 2; ++i) issue(min(c0 + i * step, c_end - 1), r[i], cs[i]);
+    for (int ci = c0;; ci += 2 * step) {
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const int cc = ci + i * step;
+            const bool valid[1] = {kRsKeys * cc + j < it.n_keys};
+            rs_chunks<1, true>(&r[i], q, valid, &cs[i], st);
+            if (cc + step >= c_end) return;
+            issue(min(cc + 2 * step, c_end - 1), r[i], cs[i]);
+        }
+    }
+}
+
+// First index >= lo of the sequence p, p + step, ...
+__device__ __forceinline__ int rs_first(int p, int step, int lo) {
+    return p >= lo ? p : p + (lo - p + step - 1) / step * step;
+}
+
+__global__ __launch_bounds__(kWave) void rescore_kernel(PrefillArgs a) {
+    __shared__ double o_s[kRsKeys][8][16];      // per key slot, per lane group
     const int T = a.n_new;
     const uint32_t cap = static_cast<uint32_t>(a.batch) * static_cast<uint32_t>(T) * kHq;
     const uint32_t n_rows = min(a.rs_hdr[0], cap);
     if (n_rows == 0) return;
     uint32_t n_pieces = gridDim.x / n_rows;      // gridDim.x <= kRsSlots
     n_pieces = n_pieces < 1 ? 1 : n_pieces > kRsMaxPieces ? kRsMaxPieces : n_pieces;
-    const int wave = threadIdx.x / kWave;
-    const int lane = threadIdx.x % kWave;
-    const int64_t kstride_c = a.kv_pos_stride * 2;                  // cache row bytes
-    const int64_t kstride_n = static_cast<int64_t>(kHkv) * kD * 2;   // new-row bytes
+    const int np = static_cast<int>(n_pieces);
+    const int lane = threadIdx.x;
+    const int c = lane & 7;
     const int64_t n_work = static_cast<int64_t>(n_rows) * n_pieces;
     for (int64_t wk = blockIdx.x; wk < n_work; wk += gridDim.x) {
         const uint32_t idx = static_cast<uint32_t>(wk / n_pieces);
@@ -1726,134 +1898,127 @@ __global__ __launch_bounds__(4 * kWave) void rescore_kernel(PrefillArgs a) {
         const int b = static_cast<int>(bt / T);
         const int t = static_cast<int>(bt % T);
         const int kvh = h / kGroup;
-        const int st = a.start[b];
-        const int n_keys = st + t + 1;
-        const int per = (n_keys + static_cast<int>(n_pieces) - 1) / static_cast<int>(n_pieces);
-        const int ka = min(n_keys, piece * per);
-        const int kb = min(n_keys, ka + per);
-        const int quarter = (per + 3) / 4;
-        const int k0 = min(kb, ka + wave * quarter);
-        const int k1 = min(kb, k0 + quarter);
-
-        // Q of head 4kvh + wave at token t, rotated at st + t and scaled, into q_s.
-        {
-            double sn = 0.0, cs = 1.0;
-            if (a.flags & 1u) rope_sincos(st + t, a.rope.inv_freq[lane], sn, cs);
-            const uint16_t* qrow = a.q + (bt * kHq + kvh * kGroup + wave) * kD;
-            const double x = bf16_to_f32(qrow[lane]);
-            const double y = bf16_to_f32(qrow[lane + kPairs]);
-            double xr = x, yr = y;
-            if (a.flags & 1u) {
-                xr = x * cs - y * sn;
-                yr = x * sn + y * cs;
-            }
-            q_s[wave][lane] = xr * a.qk_scale_log2;
-            q_s[wave][lane + kPairs] = yr * a.qk_scale_log2;
-        }
-        __syncthreads();
-        QOps qa;
-        read_q_ops(&q_s[0][0], qa);
-
-        PieceState stt;
-        init_piece(stt);
+        RsItem it;
+        it.st = a.start[b];
+        it.n_keys = it.st + t + 1;
+        it.stride_c = a.kv_pos_stride * 2;
         const int64_t head_elem = static_cast<int64_t>(b) * a.kv_batch_stride + static_cast<int64_t>(kvh) * a.kv_head_stride;
-        const char* kc_seg = reinterpret_cast<const char*>(a.k + head_elem);
-        const char* vc_seg = reinterpret_cast<const char*>(a.v + head_elem);
-        if (a.flags & 2u) {
-            // cached keys as stored (post-RoPE); the chunk's keys rotated from the new rows
-            rescore_range<0>(kc_seg, kstride_c, vc_seg, kstride_c, k0, min(k1, st), qa, stt);
-            const char* kn_seg = reinterpret_cast<const char*>(a.k_new + (static_cast<int64_t>(b) * T * kHkv + kvh) * kD);
-            const char* vn_seg = vc_seg + static_cast<int64_t>(st) * kstride_c;
-            rescore_range<2>(kn_seg, kstride_n, vn_seg, kstride_c, max(k0, st) - st, k1 - st, qa, stt,
-                             a.rs_cs + static_cast<int64_t>(b) * T * kPairs);
-        } else {
-            rescore_range<0>(kc_seg, kstride_c, vc_seg, kstride_c, k0, k1, qa, stt);
-        }
-        double l_tot;
-        finish_piece(stt, l_tot);
-#pragma unroll
-        for (int i = 0; i < 8; ++i) (&o_s[wave][0][0])[lane_row_offset() + i] = stt.acc[i];
-        if (lane < kGroup) {
-            m_s[wave][lane] = stt.m_run;
-            l_s[wave][lane] = l_tot;
-        }
-        __syncthreads();
+        it.kc_seg = reinterpret_cast<const char*>(a.k + head_elem);
+        it.vc_seg = reinterpret_cast<const char*>(a.v + head_elem);
+        it.kn_seg = reinterpret_cast<const char*>(a.k_new + (static_cast<int64_t>(b) * T * kHkv + kvh) * kD);
+        it.cs_seg = a.rs_cs + static_cast<int64_t>(b) * T * kPairs;
+        const int n_chunks = (it.n_keys + kRsKeys - 1) / kRsKeys;
+        // first chunk holding a chunk key (with RoPE on K those are rotated from the new rows)
+        const int c_split = (a.flags & 2u) ? it.st / kRsKeys : n_chunks;
 
-        // Wave 0 combines the row's head over the four quarters: lane owns dims 2*lane, +1.
-        const int c = h % kGroup;
-        if (wave == 0) {
-            float mx = -INFINITY;
+        // Q of head h at token t, rotated at start + t (the cos/sin row of token t) and
+        // scaled by scale * log2(e): this lane's 8 pairs.  Its loads are issued first, then
+        // the first cached chunks', so the Q operands are formed while those are in flight.
+        double q[16];
+        RsRows pre[2][kRsGroup];
+        {
+            const char* qrow = reinterpret_cast<const char*>(a.q + (bt * kHq + h) * kD);
+            const uint4 qx = load_stream16(qrow + 16 * c);
+            const uint4 qy = load_stream16(qrow + 2 * kPairs + 16 * c);
+            double2 cs[8];
+            rs_load_cs(a.rs_cs + bt * kPairs, cs);
+            rs_prefetch(it, piece, c_split, np, pre);
+            rs_widen(qx, q);
+            rs_widen(qy, q + 8);
+            if (a.flags & 1u) {
 #pragma unroll
-            for (int w = 0; w < 4; ++w) mx = fmaxf(mx, m_s[w][c]);
-            double l = 0.0, o0 = 0.0, o1 = 0.0;
-#pragma unroll
-            for (int w = 0; w < 4; ++w) {
-                const float m = m_s[w][c];
-                if (m == -INFINITY) continue;
-                const int ex = static_cast<int>(m - mx);
-                l += ldexp(l_s[w][c], ex);
-                o0 += ldexp(o_s[w][c][2 * lane], ex);
-                o1 += ldexp(o_s[w][c][2 * lane + 1], ex);
-            }
-            uint32_t* orow = reinterpret_cast<uint32_t*>(a.out + static_cast<int64_t>(row) * kD);
-            if (n_pieces == 1) {
-                orow[lane] = f32_to_bf16_rne(static_cast<float>(o0 / l)) |
-                             (static_cast<uint32_t>(f32_to_bf16_rne(static_cast<float>(o1 / l))) << 16);
-            } else {
-                const int64_t slot = static_cast<int64_t>(idx) * n_pieces + piece;
-                unsigned long long* po = reinterpret_cast<unsigned long long*>(a.rs_part_o + slot * kD) + 2 * lane;
-                store_agent(po, o0);
-                store_agent(po + 1, o1);
-                if (lane == 0)
-                    store_agent(reinterpret_cast<unsigned long long*>(a.rs_part_ml + slot),
-                                make_float2(mx, static_cast<float>(l)));
-                wait_vmem();                              // the stores have completed ...
-                __atomic_signal_fence(__ATOMIC_SEQ_CST);  // ... and stay before the count
-                int last = 0;
-                if (lane == 0) last = atomicAdd(&a.rs_done[row], 1u) == n_pieces - 1;
-                last = __shfl(last, 0);
-                __atomic_signal_fence(__ATOMIC_SEQ_CST);  // the merge's loads stay after it
-                if (last) {
-                    // Lane u reads piece u's (m, l); the O partials are read eight pieces
-                    // at a time, every load of a batch in flight together.
-                    const int64_t slot0 = static_cast<int64_t>(idx) * n_pieces;
-                    const int np = static_cast<int>(n_pieces);
-                    const float2 ml = load_agent_f2(a.rs_part_ml + slot0 + min(lane, np - 1));
-                    float m_all = ml.x;
-#pragma unroll
-                    for (int sh = 1; sh < kWave; sh <<= 1) m_all = fmaxf(m_all, __shfl_xor(m_all, sh));
-                    const int my_ex = ml.x == -INFINITY ? -1100 : static_cast<int>(ml.x - m_all);
-                    double lw = lane < np ? ldexp(static_cast<double>(ml.y), my_ex) : 0.0;
-#pragma unroll
-                    for (int sh = 1; sh < kWave; sh <<= 1) lw += __shfl_xor(lw, sh);
-                    o0 = 0.0;
-                    o1 = 0.0;
-                    for (int u0 = 0; u0 < np; u0 += 8) {
-                        double2 ov[8];
-#pragma unroll
-                        for (int u = 0; u < 8; ++u)
-                            ov[u] = load_agent_d2(a.rs_part_o + (slot0 + min(u0 + u, np - 1)) * kD + 2 * lane);
-#pragma unroll
-                        for (int u = 0; u < 8; ++u) {
-                            const int ex = __shfl(my_ex, u0 + u);
-                            if (u0 + u < np) {
-                                o0 += ldexp(ov[u].x, ex);
-                                o1 += ldexp(ov[u].y, ex);
-                            }
-                        }
-                    }
-                    orow[lane] = f32_to_bf16_rne(static_cast<float>(o0 / lw)) |
-                                 (static_cast<uint32_t>(f32_to_bf16_rne(static_cast<float>(o1 / lw))) << 16);
+                for (int i = 0; i < 8; ++i) {
+                    const double x = q[i], y = q[8 + i];
+                    q[i] = x * cs[i].x - y * cs[i].y;
+                    q[8 + i] = x * cs[i].y + y * cs[i].x;
                 }
             }
+#pragma unroll
+            for (int i = 0; i < 16; ++i) q[i] *= a.qk_scale_log2;
         }
-        __syncthreads();                // LDS reused by the next work item
+
+        RsState stt;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) stt.o[i] = 0.0;
+        stt.l = 0.0;
+        stt.m = -INFINITY;
+        rs_cached(it, piece, c_split, np, q, stt, pre);
+        rs_new(it, rs_first(piece, np, c_split), n_chunks, np, q, stt);
+
+        // The piece's O over its 8 key slots (through LDS, summed in slot order) and l.
+#pragma unroll
+        for (int i = 0; i < 16; ++i) o_s[lane >> 3][c][i] = stt.o[i];
+        double l_tot = stt.l;
+#pragma unroll
+        for (int sh = 1; sh < kWave; sh <<= 1) l_tot += __shfl_xor(l_tot, sh);
+        l_tot *= 0.125;                              // each key counted in its eight lanes
+        __syncthreads();
+        // lane i merges dims 2i, 2i + 1 (lane group cd, index ii within its 16)
+        const int d0 = 2 * lane;
+        const int cd = (d0 % kPairs) / 8;
+        const int ii = d0 % 8 + (d0 >= kPairs ? 8 : 0);
+        double o0 = 0.0, o1 = 0.0;
+#pragma unroll
+        for (int jj = 0; jj < kRsKeys; ++jj) {
+            o0 += o_s[jj][cd][ii];
+            o1 += o_s[jj][cd][ii + 1];
+        }
+        uint32_t* orow = reinterpret_cast<uint32_t*>(a.out + static_cast<int64_t>(row) * kD);
+        if (np == 1) {
+            orow[lane] = f32_to_bf16_rne(static_cast<float>(o0 / l_tot)) |
+                         (static_cast<uint32_t>(f32_to_bf16_rne(static_cast<float>(o1 / l_tot))) << 16);
+        } else {
+            const int64_t slot = static_cast<int64_t>(idx) * n_pieces + piece;
+            unsigned long long* po = reinterpret_cast<unsigned long long*>(a.rs_part_o + slot * kD) + 2 * lane;
+            store_agent(po, o0);
+            store_agent(po + 1, o1);
+            if (lane == 0)
+                store_agent(reinterpret_cast<unsigned long long*>(a.rs_part_ml + slot),
+                            make_float2(stt.m, static_cast<float>(l_tot)));
+            wait_vmem();                              // the stores have completed ...
+            __atomic_signal_fence(__ATOMIC_SEQ_CST);  // ... and stay before the count
+            int last = 0;
+            if (lane == 0) last = atomicAdd(&a.rs_done[row], 1u) == n_pieces - 1;
+            last = __shfl(last, 0);
+            __atomic_signal_fence(__ATOMIC_SEQ_CST);  // the merge's loads stay after it
+            if (last) {
+                // Lane u reads piece u's (m, l); lane i merges dims 2i, 2i + 1.  Every load is
+                // issued before any is used (unused entries repeat the last piece), so the
+                // merge waits for memory once.  A piece with no key has m = -inf, weight 0.
+                const int64_t slot0 = static_cast<int64_t>(idx) * n_pieces;
+                const float2 ml = load_agent_f2(a.rs_part_ml + slot0 + min(lane, np - 1));
+                double2 ov[kRsMaxPieces];
+#pragma unroll
+                for (int u = 0; u < kRsMaxPieces; ++u)
+                    ov[u] = load_agent_d2(a.rs_part_o + (slot0 + min(u, np - 1)) * kD + 2 * lane);
+                float m_all = ml.x;
+#pragma unroll
+                for (int sh = 1; sh < kWave; sh <<= 1) m_all = fmaxf(m_all, __shfl_xor(m_all, sh));
+                const int my_ex = ml.x == -INFINITY ? -1100 : static_cast<int>(ml.x - m_all);
+                double lw = lane < np ? ldexp(static_cast<double>(ml.y), my_ex) : 0.0;
+#pragma unroll
+                for (int sh = 1; sh < kWave; sh <<= 1) lw += __shfl_xor(lw, sh);
+                o0 = 0.0;
+                o1 = 0.0;
+#pragma unroll
+                for (int u = 0; u < kRsMaxPieces; ++u) {
+                    const int ex = __shfl(my_ex, u);
+                    if (u < np) {
+                        o0 += ldexp(ov[u].x, ex);
+                        o1 += ldexp(ov[u].y, ex);
+                    }
+                }
+                orow[lane] = f32_to_bf16_rne(static_cast<float>(o0 / lw)) |
+                             (static_cast<uint32_t>(f32_to_bf16_rne(static_cast<float>(o1 / lw))) << 16);
+            }
+        }
+        __syncthreads();                // o_s is rewritten by the next work item
     }
 }
 
 hipError_t launch_rescore(const PrefillArgs& a, hipStream_t stream) {
     if (!a.rs_hdr) return hipSuccess;
-    hipLaunchKernelGGL(rescore_kernel, dim3(static_cast<unsigned>(a.rs_wgs)), dim3(4 * kWave), 0, stream, a);
+    hipLaunchKernelGGL(rescore_kernel, dim3(static_cast<unsigned>(a.rs_wgs)), dim3(kWave), 0, stream, a);
     return hipGetLastError();
 }
 

@@ -125,9 +125,9 @@ struct PrefillArgs {
     uint32_t* rs_hdr;         // [1]: flagged rows
     uint32_t* rs_rows;        // [B*T*32] flagged rows, (b*T + t)*32 + q_head, in flagging order
     uint32_t* rs_done;        // [B*T*32] finished pieces per flagged row (indexed by row)
-    double2* rs_cs;           // [B][T][64] cos, sin of (start + t) * inv_freq[i] (RoPE on K)
-    double* rs_part_o;        // [kRsSlots][4][128] unnormalised partial outputs
-    float2* rs_part_ml;       // [kRsSlots][4] (running max, sum)
+    double2* rs_cs;           // [B][T][64] cos, sin of (start + t) * inv_freq[i] (RoPE on Q or K)
+    double* rs_part_o;        // [kRsSlots][128] unnormalised partial output rows
+    float2* rs_part_ml;       // [kRsSlots] (running max, sum)
     int32_t rs_wgs;           // workgroups of the rescore kernel
 };
 

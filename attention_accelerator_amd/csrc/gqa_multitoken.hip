@@ -268,7 +268,7 @@ __global__ __launch_bounds__(256) void mt_prepare_kernel(PrefillArgs a) {
     if (rope_q || rope_k)
         for (int u = w; u < T; u += 4) {
             rope_sincos(static_cast<int64_t>(st) + u, a.rope.inv_freq[lane], sn_s[u][lane], cs_s[u][lane]);
-            if (rope_k && kvh == 0 && a.rs_hdr)
+            if (kvh == 0 && a.rs_hdr)
                 a.rs_cs[(static_cast<int64_t>(b) * T + u) * kPairs + lane] = make_double2(cs_s[u][lane], sn_s[u][lane]);
         }
     if (a.rs_hdr)

@@ -95,10 +95,11 @@ __global__ __launch_bounds__(256) void kv_append_kernel(PrefillArgs a) {
         ce[kvh] = cache_elem(a, b, kvh, pos);
     }
     double sn = 0.0, cs = 1.0;
-    if (rope) rope_sincos(pos, a.rope.inv_freq[lane], sn, cs);
+    const bool any_rope = (a.flags & 3u) != 0;        // the rescore rotates Q with these too
+    if (any_rope) rope_sincos(pos, a.rope.inv_freq[lane], sn, cs);
     if (a.rs_hdr) {
         if (lane < kHq) a.rs_done[bt * kHq + lane] = 0u;
-        if (rope) a.rs_cs[bt * kPairs + lane] = make_double2(cs, sn);
+        if (any_rope) a.rs_cs[bt * kPairs + lane] = make_double2(cs, sn);
     }
 #pragma unroll
     for (int kvh = 0; kvh < kHkv; ++kvh) {
