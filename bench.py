@@ -114,6 +114,49 @@ def parity_summary(want, want64, got) -> dict:
             "fails_64ulp": int(failures(want, got, 64).sum()), "elements": int(want.size)}
 
 
+def fp32_attention(q_ref, k_ref, v_ref, n_keys: int):
+    """The attention step in float32 (torch on the CPU): q_ref [32, 128] rotated and k_ref,
+    v_ref [8, >= n_keys, 128] as the golden prepares them (double), rounded to float32 first;
+    scores * 1/sqrt(128), softmax and weighted V in float32.  Returns [32, 128] float64."""
+    import math
+
+    import numpy as np
+    import torch
+    q = torch.from_numpy(np.ascontiguousarray(q_ref, dtype=np.float32)).view(8, 4, 128)
+    k = torch.from_numpy(np.ascontiguousarray(k_ref[:, :n_keys], dtype=np.float32))
+    v = torch.from_numpy(np.ascontiguousarray(v_ref[:, :n_keys], dtype=np.float32))
+    s = torch.matmul(q, k.transpose(1, 2).contiguous()) * np.float32(1.0 / math.sqrt(128))
+    p = torch.softmax(s, dim=-1)
+    return torch.matmul(p, v).reshape(32, 128).numpy().astype(np.float64)
+
+
+def fp32_summary(parity: dict, got_rows, want64_rows, ref32_rows) -> dict:
+    """Adds the largest |GPU - fp32 reference| and |golden - fp32 reference| to parity."""
+    import numpy as np
+    got = (np.asarray(got_rows, dtype=np.uint16).reshape(-1, 128).astype(np.uint32) << 16).view(np.float32)
+    r32 = np.asarray(ref32_rows).reshape(-1, 128)
+    parity["max_abs_err_vs_fp32_ref"] = float(np.abs(got.astype(np.float64) - r32).max())
+    parity["golden_f64_max_abs_diff_vs_fp32_ref"] = float(np.abs(np.asarray(want64_rows).reshape(-1, 128) - r32).max())
+    return parity
+
+
+def fp32_chunk_rows(qc, kc, vc, knc, vnc, s0: int, rows):
+    """fp32_attention for tokens `rows` of one chunk: qc [T, 32, 128], knc / vnc [T, 8, 128]
+    BF16 codes of the new rows, kc / vc [8, s0, 128] the cache before the chunk (post-RoPE);
+    token t at position s0 + t sees the cache and new rows 0..t (K rotated at s0 + u in
+    double, unrounded, as the golden). Returns [len(rows), 32, 128]."""
+    import numpy as np
+
+    from oracle import oracle as orc
+    k_all = np.stack([np.concatenate([orc.prepare_rows(kc[h], False), orc.prepare_rows(knc[:, h], True, s0)])
+                      for h in range(8)])
+    v_all = np.stack([np.concatenate([orc.prepare_rows(vc[h], False), orc.prepare_rows(vnc[:, h], False)])
+                      for h in range(8)])
+    def q_at(t):
+        return np.stack([orc.prepare_rows(qc[t, h][None], True, s0 + t)[0] for h in range(32)])
+    return np.stack([fp32_attention(q_at(t), k_all, v_all, s0 + t + 1) for t in rows])
+
+
 def python_golden(q, k, v, seq_len: int, qpos: int, nbytes: int, what: str) -> dict:
     """The reference's own arithmetic, pure Python (oracle/golden_model.golden_attention,
     a restatement of pyfiles/gen_gqa_wrapper_vectors.py:124-139), timed on one query token
@@ -154,6 +197,14 @@ def cpu_baseline(batch, gpu_out, budget_s: float = 12.0):
         lens.append(n)
         done += 1
     gbs = algorithmic_bytes_decode(lens) / t_total / 1e9
+    ref32 = []
+    for b in range(done):
+        n, qp = lens[b], int(batch.query_pos[b])
+        qc, kc, vc = codes_of(batch.q[b]), codes_of(batch.k[b, :, :n]), codes_of(batch.v[b, :, :n])
+        q_ref = np.stack([orc.prepare_rows(qc[h][None], True, qp)[0] for h in range(32)])
+        k_ref = np.stack([orc.prepare_rows(kc[h], False) for h in range(8)])
+        v_ref = np.stack([orc.prepare_rows(vc[h], False) for h in range(8)])
+        ref32.append(fp32_attention(q_ref, k_ref, v_ref, qp + 1))
     s = int(np.argmin(batch.seq_len.numpy()))
     n = int(batch.seq_len[s])
     py = python_golden(codes_of(batch.q[s]), codes_of(batch.k[s, :, :n]), codes_of(batch.v[s, :, :n]), n,
@@ -163,7 +214,8 @@ def cpu_baseline(batch, gpu_out, budget_s: float = 12.0):
                        f"{sum(lens)} keys, all 32 heads), compiled oracle in double, "
                        f"{t_total:.2f} s; os.cpu_count()={os.cpu_count()}, "
                        f"affinity={len(os.sched_getaffinity(0))}"),
-            "parity": parity_summary(np.concatenate(wants), np.concatenate(wants64), gpu_out[:done]),
+            "parity": fp32_summary(parity_summary(np.concatenate(wants), np.concatenate(wants64), gpu_out[:done]),
+                                   gpu_out[:done], np.concatenate(wants64), np.stack(ref32)),
             "python_golden": py}
 
 def prefill_flops(batch: int, n_new: int, start: int) -> int:
@@ -203,8 +255,10 @@ def prefill_cpu_baseline(q, kn, vn, k, v, starts, gpu_out, budget_s: float = 12.
             "sample": (f"tokens 0..{rows[-1]} of sequence 0 ({len(rows)} of {q.shape[1]} tokens, all "
                        f"32 heads, {s0} cached keys), compiled oracle in double, {t_total:.2f} s; "
                        f"os.cpu_count()={os.cpu_count()}, affinity={len(os.sched_getaffinity(0))}"),
-            "parity": parity_summary(np.concatenate(wants, axis=1), np.concatenate(wants64, axis=1),
-                                     gpu_out[:1, :len(rows)]),
+            "parity": fp32_summary(parity_summary(np.concatenate(wants, axis=1), np.concatenate(wants64, axis=1),
+                                                  gpu_out[:1, :len(rows)]),
+                                   gpu_out[:1, :len(rows)], np.concatenate(wants64, axis=1),
+                                   fp32_chunk_rows(qc[0], kc[0], vc[0], knc[0], vnc[0], s0, rows)),
             "python_golden": py}
 
 
@@ -332,6 +386,8 @@ def multitoken_cpu_baseline(q, kn, vn, k, v, starts, n_new: int, gpu_out, budget
         wants64.append(w64)
         byts += multitoken_bytes([s0 + n_new], n_new)
         done += 1
+    ref32 = [fp32_chunk_rows(codes_of(q[b]), codes_of(k[b, :, :int(starts[b])]), codes_of(v[b, :, :int(starts[b])]),
+                             codes_of(kn[b]), codes_of(vn[b]), int(starts[b]), range(n_new)) for b in range(done)]
     b = int(np.argmin(np.asarray(starts)))
     s0 = int(starts[b])
     qc, knc, vnc = codes_of(q[b]), codes_of(kn[b]), codes_of(vn[b])
@@ -343,7 +399,8 @@ def multitoken_cpu_baseline(q, kn, vn, k, v, starts, n_new: int, gpu_out, budget
             "sample": (f"sequences 0..{done - 1} ({done} of {q.shape[0]}, all {n_new} new tokens, all 32 "
                        f"heads), compiled oracle in double, {t_total:.2f} s; "
                        f"os.cpu_count()={os.cpu_count()}, affinity={len(os.sched_getaffinity(0))}"),
-            "parity": parity_summary(np.concatenate(wants), np.concatenate(wants64), gpu_out[:done]),
+            "parity": fp32_summary(parity_summary(np.concatenate(wants), np.concatenate(wants64), gpu_out[:done]),
+                                   gpu_out[:done], np.concatenate(wants64), np.stack(ref32)),
             "python_golden": py}
 
 
