@@ -388,6 +388,19 @@ template <int kC>
 __device__ __forceinline__ void mt_issue_plane(const char* seg, int64_t row_bytes, int key0, int k_last,
                                                uint8_t* dst, int wv, int lane) {
     constexpr int kNt = 2;     // cache policy: nontemporal
+    if (key0 + kMtWin - 1 <= k_last) {
+        // Every row of the window exists: a uniform row base plus the lane's 32-bit offset,
+        // which does not change from window to window (the ABI keeps a (sequence, KV head)'s
+        // rows under 4 GiB).
+        const char* base = seg + static_cast<int64_t>(key0) * row_bytes;
+#pragma unroll
+        for (int q = 0; q < kC; ++q) {
+            const uint32_t r = static_cast<uint32_t>(4 * (wv * kC + q) + (lane >> 4));
+            const uint32_t o = r * static_cast<uint32_t>(row_bytes) + 16u * static_cast<uint32_t>((lane & 15) ^ pf_swz(r));
+            __builtin_amdgcn_global_load_lds(base + o, (lds_void_t*)(dst + (wv * kC + q) * 1024), 16, 0, kNt);
+        }
+        return;
+    }
     int64_t off[kC];
 #pragma unroll
     for (int q = 0; q < kC; ++q) {
@@ -455,15 +468,22 @@ __device__ __forceinline__ float mt_max(const PrefillArgs& a, bool chunk_keys, c
                 }
             }
     }
+    // Masks: only a window holding chunk keys (the causal limit lim >= start) or running past
+    // the piece has any (a uniform test).
+    if (chunk_keys || key0 + kMtWin > k_b) {
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int key = key0 + 16 * kt + 4 * g + i;
+                if (key >= k_b || key > lim) sacc[kt][i] = -INFINITY;
+            }
+    }
     float bmax = -INFINITY;
 #pragma unroll
     for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int key = key0 + 16 * kt + 4 * g + i;
-            if (key >= k_b || key > lim) sacc[kt][i] = -INFINITY;
-            bmax = fmaxf(bmax, sacc[kt][i]);
-        }
+        for (int i = 0; i < 4; ++i) bmax = fmaxf(bmax, sacc[kt][i]);
     bmax = swap32_max(swap16_max(bmax));
     const float m_new = bmax > t.m_run ? ceilf(bmax) : t.m_run;
     if (__ballot(m_new != t.m_run)) {
