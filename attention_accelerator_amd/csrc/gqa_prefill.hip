@@ -177,6 +177,16 @@ __device__ __forceinline__ void pf_issue_k(const PrefillArgs& a, const char* kba
     const int64_t row_bytes = a.kv_pos_stride * 2;
     const int64_t n_rows = static_cast<int64_t>(a.batch) * a.n_new * kHkv;
     const int key0 = blk * kPfBlk;
+    if (!has_new && key0 + kPfBlk <= n_keys) {
+        // the common block: cached keys only, all 64 rows exist (a uniform branch, so no
+        // per-lane address arithmetic beyond the lane's fixed offset)
+        const char* brow = kbase + static_cast<int64_t>(key0) * row_bytes;
+#pragma unroll
+        for (int ii = 0; ii < 2; ++ii)
+            __builtin_amdgcn_global_load_lds(brow + loff[ii],
+                                             (lds_void_t*)(lds + kOffK + buf * kPlaneB + (2 * wave + ii) * 1024), 16, 0, 0);
+        return;
+    }
     const bool full = key0 + kPfBlk <= n_keys;
     const char* brow = kbase + static_cast<int64_t>(key0) * row_bytes;
 #pragma unroll
@@ -206,6 +216,13 @@ __device__ __forceinline__ void pf_issue_v(const PrefillArgs& a, const char* vba
     const int key0 = blk * kPfBlk;
     const bool full = key0 + kPfBlk <= n_keys;
     const char* brow = vbase + static_cast<int64_t>(key0) * row_bytes;
+    if (full) {
+#pragma unroll
+        for (int ii = 0; ii < 2; ++ii)
+            __builtin_amdgcn_global_load_lds(brow + loff[ii],
+                                             (lds_void_t*)(lds + kOffV + buf * kPlaneB + (2 * wave + ii) * 1024), 16, 0, 0);
+        return;
+    }
 #pragma unroll
     for (int ii = 0; ii < 2; ++ii) {
         const int r = pf_copy_row(wave, ii, lane);
