@@ -238,3 +238,27 @@ def test_multi_long_context_sampled_rows(dev):
     want, want64 = orc.prefill(to_codes(q), to_codes(k), to_codes(v), to_codes(kn), to_codes(vn),
                                np.asarray([st]), rows=rows, want_f64=True)
     assert_within_ulp(want, got[:, rows], 64, "multi 131072", ref64=want64)
+
+
+@pytest.mark.parametrize("n_new,rope_q,rope_k", [
+    (4, True, True),      # stream-K path, every row flagged: more rows than rescore workgroups
+    (16, True, False),    # Q rotated with the cos/sin rows, the chunk's keys read as stored
+    (40, True, True),     # prefill attention kernel path
+    (24, False, False),   # no RoPE at all
+])
+def test_every_row_rescored(dev, n_new, rope_q, rope_k):
+    """V dimension 5 is exactly zero in every row, so every output row holds an exact zero
+    and is flagged for the fp64 rescore (min |x| = 0 < 2^-17 rms): the rescore runs with
+    one piece per row (more flagged rows than workgroups) and must reproduce every row of
+    the oracle, the zero dimension exactly."""
+    starts = [37, 300, 1000, 8, 513, 64, 2049, 129][: 8 if n_new <= 16 else 3]
+    cap = max(starts) + n_new
+    q, kn, vn, k, v = _chunk(starts, n_new, cap, 40 + n_new)
+    vn[..., 5] = 0.0
+    for b, s in enumerate(starts):
+        v[b, :, :s, 5] = 0.0
+    want = _oracle(q, kn, vn, k, v, starts, rope_q=rope_q, rope_k=rope_k)
+    got, _, _ = _run(q, kn, vn, k, v, starts, dev, rope_q=rope_q, rope_k=rope_k)
+    assert np.all(got[..., 5] == 0)
+    w = _check(want, got.reshape(-1, 128), f"T={n_new} rope_q={rope_q} rope_k={rope_k}, all rows rescored")
+    print("worst ULP", w)
