@@ -115,7 +115,7 @@ struct PrefillArgs {
     int64_t* plan_hdr;        // {total stream positions, positions per workgroup, segment lead,
                               //  positions moved from odd to even ranges}
     int64_t* seq_off;         // [B+1] stream position of sequence b's first segment
-    double* part_o;           // [n_slots][16W][128] unnormalised partial outputs (column 16w + 4t + h)
+    float* part_o;            // [n_slots][16W][128] unnormalised partial outputs (column 16w + 4t + h)
     float2* part_ml;          // [n_slots][16W] (integer-valued running max in log2 units, sum)
     float* chunk_s;           // [B][8][16W][4W] scores of the chunk's keys u per column (log2 units)
     int32_t n_wgs;            // persistent workgroups of the multi-token stream kernel

@@ -20,8 +20,8 @@ namespace gqa {
 // the decode path: every segment (sequence, KV head) holds start + T keys, a range's part
 // of a segment is a piece, a split segment's pieces leave partials that mt_merge_kernel
 // combines.  The arithmetic is the attention kernel's: three BF16 parts of Q, the chunk's
-// own keys at full precision, P in three parts, fp64 accumulation within a piece,
-// integer-valued running max.
+// own keys at full precision, P in three parts, fp64 accumulation within a piece (fp32
+// partials between pieces), integer-valued running max.
 //
 // A workgroup has one wave per column tile (W = 1, 2 or 4 waves for T <= 4, 8 or 16).  With
 // one tile (HBM-bound) there is one wave per SIMD, 4 * CUs workgroups; with two or four
@@ -46,7 +46,7 @@ constexpr int kMtPlaneB = kMtWin * kRowB;     // 8 KB: 32 rows of 256 B
 constexpr int kMtTile = 16;                   // query rows per wave: 4 heads x 4 tokens
 constexpr int kMtCopies = kMtWin / 4;         // 1 KB copies per plane (each writes 4 rows)
 // Stream positions charged per segment start: a piece here costs more than in decode (the
-// Q operands, the fp64 partial of 16W columns), about two windows' streaming time for one
+// Q operands, the fp32 partial of 16W columns), about two windows' streaming time for one
 // tile and more for two or four (their workgroups share a SIMD).  Measured on B=64 ragged:
 // W = 1 best at 64 of 32, 48, 64, 96 (T=4 216.5 -> 215.4 us); W = 2 and 4 best at 128 of 32,
 // 64, 128, 192 (T=8 248.7 -> 246.9 us, T=16 374.6 -> 370.8 us).
@@ -105,7 +105,7 @@ MtLayout mt_layout(int32_t batch, int32_t n_new, int32_t n_wgs) {
     l.plan = l.q_op + al(static_cast<size_t>(batch) * kHkv * w * 12 * kWave * sizeof(uint4));
     l.seq_off = l.plan + 256;
     l.part_o = l.seq_off + al((static_cast<size_t>(batch) + 1) * sizeof(int64_t));
-    l.part_ml = l.part_o + al(n_slots * cols * kD * sizeof(double));
+    l.part_ml = l.part_o + al(n_slots * cols * kD * sizeof(float));
     l.chunk_s = l.part_ml + al(n_slots * cols * sizeof(float2));
     l.total = l.chunk_s + al(static_cast<size_t>(batch) * kHkv * cols * 4 * w * sizeof(float));
     return l;
@@ -122,7 +122,7 @@ void prefill_multi_layout(PrefillArgs& a, void* base, int32_t n_wgs) {
     a.q_op = reinterpret_cast<uint4*>(p + l.q_op);
     a.plan_hdr = reinterpret_cast<int64_t*>(p + l.plan);
     a.seq_off = reinterpret_cast<int64_t*>(p + l.seq_off);
-    a.part_o = reinterpret_cast<double*>(p + l.part_o);
+    a.part_o = reinterpret_cast<float*>(p + l.part_o);
     a.part_ml = reinterpret_cast<float2*>(p + l.part_ml);
     a.chunk_s = reinterpret_cast<float*>(p + l.chunk_s);
     a.n_wgs = n_wgs;
@@ -550,7 +550,9 @@ __device__ __forceinline__ void mt_pv(uint32_t vbase, const uint32_t (&ph)[3][2]
 
 // End of a piece: the column sums over the four rows; a whole segment writes its output
 // rows (tokens < T), a split one its partial at slot wg + segment, columns 16 wv + n, in
-// fp64 (an output that cancels to near zero needs the partials' full precision).
+// fp32: its rounding (2^-24 of the partial, about 6e-8 of an output row's rms) is far below
+// the kernel's own error, and a row with an element near zero, where it could matter, is
+// flagged by the merge and rescored in fp64.
 template <int kW>
 __device__ __forceinline__ void mt_piece_end(const PrefillArgs& a, int b, int kvh, bool whole, int64_t slot,
                                              int wv, int lane, MtState& t) {
@@ -589,13 +591,12 @@ __device__ __forceinline__ void mt_piece_end(const PrefillArgs& a, int b, int kv
         return;
     }
     const int64_t col = slot * (kMtTile * kW) + kMtTile * wv + n;
-    double* po = a.part_o + col * kD;
+    float* po = a.part_o + col * kD;
 #pragma unroll
-    for (int dt = 0; dt < 8; ++dt) {
-        double2* d = reinterpret_cast<double2*>(po + 16 * dt + 4 * g);
-        d[0] = make_double2(t.o64[dt][0], t.o64[dt][1]);
-        d[1] = make_double2(t.o64[dt][2], t.o64[dt][3]);
-    }
+    for (int dt = 0; dt < 8; ++dt)
+        *reinterpret_cast<float4*>(po + 16 * dt + 4 * g) =
+            make_float4(static_cast<float>(t.o64[dt][0]), static_cast<float>(t.o64[dt][1]),
+                        static_cast<float>(t.o64[dt][2]), static_cast<float>(t.o64[dt][3]));
     if (g == 0) a.part_ml[col] = make_float2(t.m_run, static_cast<float>(l));
 }
 
@@ -864,9 +865,16 @@ __global__ __launch_bounds__(256 * kW) void mt_merge_kernel(PrefillArgs a) {
             if (p0 + q < n_pieces) {
                 const int64_t c = (slot0 + p0 + q) * kCols + col;
                 ml[q] = a.part_ml[c];
-                const double* po = a.part_o + c * kD + d0;
-#pragma unroll
-                for (int j = 0; j < 8; ++j) v[q][j] = po[j];
+                const float4* po = reinterpret_cast<const float4*>(a.part_o + c * kD + d0);
+                const float4 x0 = po[0], x1 = po[1];
+                v[q][0] = x0.x;
+                v[q][1] = x0.y;
+                v[q][2] = x0.z;
+                v[q][3] = x0.w;
+                v[q][4] = x1.x;
+                v[q][5] = x1.y;
+                v[q][6] = x1.z;
+                v[q][7] = x1.w;
             }
         }
         float mb = m;
