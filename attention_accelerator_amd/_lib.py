@@ -138,7 +138,7 @@ def lib() -> ctypes.CDLL:
                                            ctypes.c_int32, vp]
     L.gqa_kv_append_paged_bf16.restype = ctypes.c_int
     L.gqa_prefill_workspace_bytes.argtypes = [ctypes.POINTER(GqaParams), ctypes.c_int32,
-                                              ctypes.c_int32]
+                                              ctypes.c_int32, ctypes.c_int32]
     L.gqa_prefill_workspace_bytes.restype = ctypes.c_size_t
     L.gqa_prefill_bf16.argtypes = [ctypes.POINTER(GqaParams), vp, vp, vp, vp, vp,
                                    ctypes.POINTER(GqaKvLayout), vp, ctypes.c_int32, ctypes.c_int32,

@@ -268,9 +268,12 @@ def _start_tensor(start: Lengths, batch: int, capacity: int, n_new: int, device)
     return host.contiguous().to(device)
 
 
-def prefill_workspace_bytes(batch: int, n_new: int, params: Optional[GqaParams] = None) -> int:
+def prefill_workspace_bytes(batch: int, n_new: int, capacity: int, params: Optional[GqaParams] = None) -> int:
+    """Workspace bytes of a gqa_prefill call: batch sequences, n_new new tokens each, a cache
+    of `capacity` positions per sequence (chunks of more than 16 tokens stage 512 bytes per
+    position of every (sequence, KV head) in it)."""
     p = params or make_params()
-    return int(lib().gqa_prefill_workspace_bytes(ctypes.byref(p), int(batch), int(n_new)))
+    return int(lib().gqa_prefill_workspace_bytes(ctypes.byref(p), int(batch), int(n_new), int(capacity)))
 
 
 def gqa_prefill(q: torch.Tensor, k_new: torch.Tensor, v_new: torch.Tensor, k_cache: torch.Tensor,
@@ -301,7 +304,7 @@ def gqa_prefill(q: torch.Tensor, k_new: torch.Tensor, v_new: torch.Tensor, k_cac
     device = q.device
     st = _start_tensor(start, batch, k_cache.shape[2], n_new, device)
     q, k_new, v_new = q.contiguous(), k_new.contiguous(), v_new.contiguous()
-    ws_bytes = int(lib().gqa_prefill_workspace_bytes(ctypes.byref(p), batch, n_new))
+    ws_bytes = int(lib().gqa_prefill_workspace_bytes(ctypes.byref(p), batch, n_new, layout.capacity))
     if ws_bytes == 0:
         check(_lib.GQA_ERR_INVALID_CONFIG, "gqa_prefill_workspace_bytes")
     if workspace is None:
@@ -341,7 +344,8 @@ class PreparedPrefill:
             raise ValueError("batch / token count mismatch")
         self.layout = _cache_layout(k_cache, v_cache)
         self.params = make_params(rope_q=rope_q, rope_k=rope_k, theta=theta, scale=scale)
-        ws_bytes = int(lib().gqa_prefill_workspace_bytes(ctypes.byref(self.params), self.batch, self.n_new))
+        ws_bytes = int(lib().gqa_prefill_workspace_bytes(ctypes.byref(self.params), self.batch, self.n_new,
+                                                          self.layout.capacity))
         if ws_bytes == 0:
             check(_lib.GQA_ERR_INVALID_CONFIG, "gqa_prefill_workspace_bytes")
         self.workspace = torch.empty(ws_bytes, dtype=torch.uint8, device=q.device)

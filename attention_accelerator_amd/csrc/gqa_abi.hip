@@ -211,7 +211,7 @@ using namespace gqa;
 
 extern "C" {
 
-uint32_t gqa_abi_version(void) { return (2u << 16) | 0u; }
+uint32_t gqa_abi_version(void) { return (3u << 16) | 0u; }
 
 const char* gqa_status_string(int status) {
     switch (status) {
@@ -549,13 +549,13 @@ int prefill_args(const gqa_params_t* params, const uint16_t* k_new, const uint16
 
 extern "C" {
 
-size_t gqa_prefill_workspace_bytes(const gqa_params_t* params, int32_t batch, int32_t n_new) {
-    if (!params || !geometry_ok(params) || batch <= 0 || n_new <= 0) return 0;
-    // The multi-token path needs no split planes: the chunk's unrounded keys enter through
-    // the scores its preparation kernel forms.
+size_t gqa_prefill_workspace_bytes(const gqa_params_t* params, int32_t batch, int32_t n_new, int32_t capacity) {
+    if (!params || !geometry_ok(params) || batch <= 0 || n_new <= 0 || capacity < n_new) return 0;
+    // The multi-token path stages nothing: the chunk's unrounded keys enter through the
+    // scores its preparation kernel forms, and the cache is read as stored.
     if (use_multi(n_new))
         return align_up(prefill_multi_bytes(batch, n_new, multi_wgs(n_new)), 256) + rescore_bytes(batch, n_new);
-    return align_up(prefill_split_bytes(batch, n_new), 256) + rescore_bytes(batch, n_new);
+    return align_up(prefill_stage_bytes(batch, n_new, capacity), 256) + rescore_bytes(batch, n_new);
 }
 
 int gqa_kv_append_bf16(const gqa_params_t* params, const uint16_t* k_new, const uint16_t* v_new,
@@ -564,7 +564,6 @@ int gqa_kv_append_bf16(const gqa_params_t* params, const uint16_t* k_new, const 
     PrefillArgs a;
     const int st = prefill_args(params, k_new, v_new, k_cache, v_cache, kv, start, batch, n_new, a);
     if (st != GQA_OK) return st;
-    a.k_split = nullptr;
     const hipError_t e = launch_kv_append(a, static_cast<hipStream_t>(stream));
     return e == hipSuccess ? GQA_OK : GQA_ERR_HIP;
 }
@@ -581,7 +580,6 @@ int gqa_kv_append_paged_bf16(const gqa_params_t* params, const uint16_t* k_new, 
     PrefillArgs a;
     const int st = prefill_args(params, k_new, v_new, k_pool, v_pool, &lay, start, batch, n_new, a);
     if (st != GQA_OK) return st;
-    a.k_split = nullptr;
     a.block_table = block_table;
     a.max_blocks = kv->max_blocks;
     a.n_blocks = kv->n_blocks;
@@ -598,20 +596,19 @@ int gqa_prefill_bf16(const gqa_params_t* params, const uint16_t* q, const uint16
     if (st != GQA_OK) return st;
     if (!q || !out) return GQA_ERR_BAD_POINTER;
     if (!aligned(q, 2) || !aligned(out, 8)) return GQA_ERR_BAD_POINTER;
-    const size_t need = gqa_prefill_workspace_bytes(params, batch, n_new);
+    const size_t need = gqa_prefill_workspace_bytes(params, batch, n_new, kv->capacity);
     if (!workspace || workspace_bytes < need || !aligned(workspace, 256)) return GQA_ERR_WORKSPACE;
     a.q = q;
     a.out = out;
     const bool multi = use_multi(n_new);
     char* ws = static_cast<char*>(workspace);
     if (multi) {
-        a.k_split = nullptr;
         prefill_multi_layout(a, workspace, multi_wgs(n_new));
         a.skew_pm = xcd_skew_pm(multi_waves(n_new) <= 2 ? 40 : 0);
         rescore_layout(a, ws + align_up(prefill_multi_bytes(batch, n_new, multi_wgs(n_new)), 256));
     } else {
-        a.k_split = static_cast<uint16_t*>(workspace);
-        rescore_layout(a, ws + align_up(prefill_split_bytes(batch, n_new), 256));
+        prefill_stage_layout(a, workspace);
+        rescore_layout(a, ws + align_up(prefill_stage_bytes(batch, n_new, kv->capacity), 256));
     }
     hipStream_t s = static_cast<hipStream_t>(stream);
     hipEvent_t* ev = profile_slot();
@@ -623,6 +620,7 @@ int gqa_prefill_bf16(const gqa_params_t* params, const uint16_t* q, const uint16
         return e == hipSuccess ? GQA_OK : GQA_ERR_HIP;
     }
     hipError_t e = launch_kv_append(a, s);
+    if (e == hipSuccess) e = launch_prefill_stage(a, s);
     if (ev) (void)hipEventRecord(ev[1], s);
     if (e == hipSuccess) e = launch_prefill_attention(a, s);
     if (ev) (void)hipEventRecord(ev[2], s);

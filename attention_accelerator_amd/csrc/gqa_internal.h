@@ -97,8 +97,20 @@ struct PrefillArgs {
     int32_t n_blocks;
     const int32_t* start;     // [B] cached positions before the chunk (device)
     uint16_t* out;            // [B][T][32][128]
-    uint16_t* k_split;        // [2][B][T][8][128] second and third BF16 parts of the rotated new K
-                              // (nullptr: append only, no split planes)
+    float* kx32;              // [B][T][8][128] rotated new K rows in fp32, not rounded to BF16
+                              // (nullptr: append only)
+    // fp16 staging of the attention kernel's K/V (prefill_stage_kernel): per (sequence, KV
+    // head, block of 64 positions) a power-of-two scale puts the block's largest magnitude
+    // in [2^14, 2^15), so every BF16 value of the block converts to fp16 exactly except
+    // ones more than 2^31 below that largest magnitude.
+    uint16_t* stg_k;          // [B][8][stg_pos][128] fp16 K rows (chunk keys: leading part)
+    uint16_t* stg_v;          // [B][8][stg_pos][128] fp16 V rows
+    uint16_t* stg_klo;        // [B][8][stg_cb][64][128] fp16 trailing parts of the chunk keys of
+                              // the blocks that hold them (0 for cached keys)
+    uint32_t* stg_scale;      // [B][8][stg_pos / 64]: K scale exponent (int8), V scale exponent
+                              // (int8) << 8, bit 31 set when the block cannot be staged exactly
+    int32_t stg_pos;          // positions per (sequence, KV head): capacity rounded up to 64
+    int32_t stg_cb;           // chunk blocks per (sequence, KV head): ceil(T / 64) + 1
     int64_t kv_batch_stride;
     int64_t kv_head_stride;
     int64_t kv_pos_stride;
@@ -165,7 +177,11 @@ int32_t multi_waves(int32_t n_new);
 // Waves per SIMD of that path's stream kernel: 1 for one tile, 2 for two or four tiles.
 int32_t multi_simd_waves(int32_t n_new);
 
-size_t prefill_split_bytes(int32_t batch, int32_t n_new);
+// Workspace of the prefill attention path (chunks of more than kMultiMaxNew tokens): the
+// fp32 rotated new K rows, then the fp16 staging planes and block scales.
+size_t prefill_stage_bytes(int32_t batch, int32_t n_new, int32_t capacity);
+void prefill_stage_layout(PrefillArgs& a, void* base);
+hipError_t launch_prefill_stage(const PrefillArgs& a, hipStream_t stream);
 // Workspace of the multi-token path: Q operands, plan, partials, chunk-key scores.
 size_t prefill_multi_bytes(int32_t batch, int32_t n_new, int32_t n_wgs);
 void prefill_multi_layout(PrefillArgs& a, void* base, int32_t n_wgs);

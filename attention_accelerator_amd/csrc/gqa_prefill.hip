@@ -9,37 +9,49 @@
 // chunk's own K/V rows, rotated at their positions in double and not re-rounded, as
 // the golden rotates K (gen_gqa_wrapper_vectors.py:124-126).
 //
+// Three launches, then the fp64 rescore of flagged rows (gqa_decode.hip):
+//
 // kv_append_kernel writes the chunk's K rows (rotated, rounded double -> f32 -> BF16,
-// pyfiles/gqa_reference.py:15-19) and V rows into the cache, and the second and third
-// BF16 parts of each rotated K row into the workspace, so that the cache row plus
-// those two parts carry the rotated value to ~24 bits.
+// pyfiles/gqa_reference.py:15-19) and V rows into the cache, and the rotated K rows in fp32
+// (24 bits, not rounded to BF16) into the workspace.
+//
+// prefill_stage_kernel copies the K/V rows the attention reads -- cache rows before the
+// chunk, the chunk's rows -- into fp16 planes in the workspace, one power-of-two scale per
+// (sequence, KV head, block of 64 positions) putting the block's largest magnitude in
+// [2^14, 2^15).  A BF16 value has an 8-bit significand, so it converts exactly unless it
+// lies more than ~2^31 below that largest magnitude; a chunk key's fp32 value becomes two
+// fp16 parts (leading + trailing, ~22 bits).  A block holding a non-finite value, a scale
+// outside the fp32 range the attention kernel uses, or a row more than 2^12 below the
+// block's largest magnitude is marked, and the attention kernel hands all rows that read
+// it to the fp64 rescore.
 //
 // prefill_attn_kernel: one workgroup of 8 waves per (sequence, KV head, 32 query
-// positions); wave w computes Q head 4*kv_head + (w & 3) for 16 positions.  The K/V
+// positions); wave w computes Q head 4*kv_head + (w & 3) for 16 positions.  The staged
 // rows of each 64-key block are copied once per workgroup into LDS and used by all 4
 // heads of the group and all 32 positions (gqa_kv_broadcast.v:38-59 at block scale).
 // K runs one block ahead of V, so that each wave forms block j's probabilities while its
 // MFMAs form block j+1's scores, then accumulates block j's V^T P^T.
 //
-//  * Scores S^T = K Q^T with v_mfma_f32_16x16x32_bf16: A = 16 keys x 32 dims of K from
+//  * Scores S^T = K Q^T with v_mfma_f32_16x16x32_f16: A = 16 keys x 32 dims of K from
 //    LDS (row = key), B = Q^T (column = query) held in registers.  Q is rotated and
-//    scaled by scale*log2(e) in double and split into three BF16 parts, so the exact
-//    bf16 x bf16 products carry ~24 bits of Q; for blocks with chunk keys the second and
-//    third parts of K add the (k2,q1), (k2,q2), (k3,q1) products.  Lane (g, n) ends with
-//    the scores of keys 4g+i (i = 0..3) of each 16-key tile for query n.
+//    scaled by scale*log2(e) in double, scaled by a power of two per query row, and split
+//    into two fp16 parts (11-bit significands: ~22 bits of Q); the products are exact in
+//    fp32.  Blocks with chunk keys add the trailing part of K against Q's leading part.
+//    Lane (g, n) ends with the scores of keys 4g+i (i = 0..3) of each 16-key tile for
+//    query n, times 2^(q scale + block K scale), which one multiply removes.
 //  * Online softmax per query with an integer-valued running max (every rescale is an
 //    exact power of two), p = exp2(s - m) in fp32, masked keys p = 0 exactly.
 //  * O^T += V^T P^T with the same MFMA: A = 16 dims x 32 keys of V^T from LDS, B = P^T.
 //    The lane already holds P for keys {4g+i} of tiles 2w and 2w+1, which is its B
 //    operand for the 32-key window w if V^T stores each window's keys in that order
-//    (slot 8g+4h+i <-> key 16h+4g+i).  P is split into three BF16 parts (~24 bits).
-//    Each block's fp32 product is added to an fp64 accumulator, so accumulation over
-//    thousands of keys adds no fp32 rounding.
+//    (slot 8g+4h+i <-> key 16h+4g+i).  P, scaled by 2^12, is split into two fp16 parts
+//    (rounded to nearest: ~22 bits).  Each block's fp32 product is scaled by the block's
+//    V scale into an fp64 accumulator, so accumulation over thousands of keys adds no fp32
+//    rounding.
 //  * O / l, rounded double -> f32 -> BF16, written in Q-head order.
 //
 // Chunks of at most 16 new tokens take the multi-token decode path instead
-// (gqa_multitoken.hip), which shares this file's LDS row layout and probability split
-// (gqa_prefill_common.h).
+// (gqa_multitoken.hip), which shares this file's LDS row layout (gqa_prefill_common.h).
 #include "gqa_device.h"
 #include "gqa_internal.h"
 #include "gqa_prefill_common.h"
@@ -52,13 +64,41 @@ constexpr int kPfPos = 32;                 // query positions per workgroup
 constexpr int kPfWaves = 8;                // 4 Q heads x 2 tiles of 16 positions
 constexpr int kPfThreads = kPfWaves * kWave;
 constexpr int kPfBlk = 64;                 // keys per K/V block
+constexpr int kStgThreads = 256;           // staging workgroup: 4 threads per row of a block
+constexpr int kStgMaxWgs = 8192;
+constexpr int kPScaleExp = 12;             // P is formed as 2^12 * 2^(s - m) <= 4096
+
+size_t al256(size_t x) { return (x + 255) / 256 * 256; }
 
 }  // namespace
 
-// The second and third BF16 parts of every rotated new K row, then one zero row (the parts
-// of a cached key, which the attention kernel copies for keys before the chunk).
-size_t prefill_split_bytes(int32_t batch, int32_t n_new) {
-    return (2ull * static_cast<size_t>(batch) * static_cast<size_t>(n_new) * kHkv + 1) * kD * sizeof(uint16_t);
+// ---------------------------------------------------------------------------------
+// Workspace of the prefill attention path: the rotated new K rows in fp32, the fp16 K and
+// V planes, the trailing-part planes of the chunk blocks and the block scale words.
+size_t prefill_stage_bytes(int32_t batch, int32_t n_new, int32_t capacity) {
+    const size_t rows = static_cast<size_t>(batch) * n_new * kHkv;
+    const size_t pos = (static_cast<size_t>(capacity) + kPfBlk - 1) / kPfBlk * kPfBlk;
+    const size_t cb = static_cast<size_t>((n_new + kPfBlk - 1) / kPfBlk + 1);
+    const size_t bh = static_cast<size_t>(batch) * kHkv;
+    return al256(rows * kD * sizeof(float)) + 2 * al256(bh * pos * kD * sizeof(uint16_t)) +
+           al256(bh * cb * kPfBlk * kD * sizeof(uint16_t)) + al256(bh * (pos / kPfBlk) * sizeof(uint32_t));
+}
+
+void prefill_stage_layout(PrefillArgs& a, void* base) {
+    const size_t rows = static_cast<size_t>(a.batch) * a.n_new * kHkv;
+    a.stg_pos = (a.capacity + kPfBlk - 1) / kPfBlk * kPfBlk;
+    a.stg_cb = (a.n_new + kPfBlk - 1) / kPfBlk + 1;
+    const size_t bh = static_cast<size_t>(a.batch) * kHkv;
+    char* p = static_cast<char*>(base);
+    a.kx32 = reinterpret_cast<float*>(p);
+    p += al256(rows * kD * sizeof(float));
+    a.stg_k = reinterpret_cast<uint16_t*>(p);
+    p += al256(bh * a.stg_pos * kD * sizeof(uint16_t));
+    a.stg_v = reinterpret_cast<uint16_t*>(p);
+    p += al256(bh * a.stg_pos * kD * sizeof(uint16_t));
+    a.stg_klo = reinterpret_cast<uint16_t*>(p);
+    p += al256(bh * a.stg_cb * kPfBlk * kD * sizeof(uint16_t));
+    a.stg_scale = reinterpret_cast<uint32_t*>(p);
 }
 
 // ---------------------------------------------------------------------------------
@@ -69,11 +109,6 @@ size_t prefill_split_bytes(int32_t batch, int32_t n_new) {
 __global__ __launch_bounds__(256) void kv_append_kernel(PrefillArgs a) {
     const int64_t bt = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);   // b * T + t
     const int lane = threadIdx.x & (kWave - 1);
-    if (a.k_split && blockIdx.x == 0 && threadIdx.x < kD / 2) {
-        uint32_t* zero_row = reinterpret_cast<uint32_t*>(
-            a.k_split + 2 * static_cast<int64_t>(a.batch) * a.n_new * kHkv * kD);
-        zero_row[threadIdx.x] = 0u;
-    }
     if (blockIdx.x == 0) rs_clear(a, threadIdx.x);
     if (bt >= static_cast<int64_t>(a.batch) * a.n_new) return;
     const int t = static_cast<int>(bt % a.n_new);
@@ -81,7 +116,6 @@ __global__ __launch_bounds__(256) void kv_append_kernel(PrefillArgs a) {
     const int st = a.start[b];
     if (!prefill_start_ok(a, st)) return;
     const int64_t pos = static_cast<int64_t>(st) + t;
-    const int64_t n_rows = static_cast<int64_t>(a.batch) * a.n_new * kHkv;
     const bool rope = (a.flags & 2u) != 0;
     uint16_t kx[kHkv], ky[kHkv], vx[kHkv], vy[kHkv];
     int64_t ce[kHkv];
@@ -111,24 +145,18 @@ __global__ __launch_bounds__(256) void kv_append_kernel(PrefillArgs a) {
             xr = x * cs - y * sn;
             yr = x * sn + y * cs;
         }
-        const uint16_t hx = bf16_of(xr), hy = bf16_of(yr);
         if (ce[kvh] >= 0) {
             uint16_t* kdst = a.k + ce[kvh];
             uint16_t* vdst = a.v + ce[kvh];
-            kdst[lane] = hx;
-            kdst[lane + kPairs] = hy;
+            kdst[lane] = bf16_of(xr);
+            kdst[lane + kPairs] = bf16_of(yr);
             vdst[lane] = vx[kvh];
             vdst[lane + kPairs] = vy[kvh];
         }
-        if (a.k_split) {
-            const double rx = xr - f64_of_bf16(hx), ry = yr - f64_of_bf16(hy);
-            const uint16_t mx = bf16_of(rx), my = bf16_of(ry);
-            uint16_t* mid = a.k_split + row * kD;
-            uint16_t* lo = a.k_split + (n_rows + row) * kD;
-            mid[lane] = mx;
-            mid[lane + kPairs] = my;
-            lo[lane] = bf16_of(rx - f64_of_bf16(mx));
-            lo[lane + kPairs] = bf16_of(ry - f64_of_bf16(my));
+        if (a.kx32) {
+            float* kr = a.kx32 + row * kD;
+            kr[lane] = static_cast<float>(xr);
+            kr[lane + kPairs] = static_cast<float>(yr);
         }
     }
 }
@@ -142,13 +170,204 @@ hipError_t launch_kv_append(const PrefillArgs& a, hipStream_t stream) {
 }
 
 // ---------------------------------------------------------------------------------
+// Staging.
+
+typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
+
+// Two floats -> two fp16 codes in one dword, each rounded to nearest (v_cvt_pk_f16_f32).
+__device__ __forceinline__ uint32_t pk_f16(float lo, float hi) {
+    f16x2_t h;
+    h[0] = static_cast<_Float16>(lo);
+    h[1] = static_cast<_Float16>(hi);
+    return __builtin_bit_cast(uint32_t, h);
+}
+
+__device__ __forceinline__ float f16_lo(uint32_t w) { return static_cast<float>(__builtin_bit_cast(f16x2_t, w)[0]); }
+__device__ __forceinline__ float f16_hi(uint32_t w) { return static_cast<float>(__builtin_bit_cast(f16x2_t, w)[1]); }
+
+// x - (fp16 half of h), exact, in one instruction: v_fma_mix_f32 reads the half as fp16
+// (op_sel_hi) and computes -h * 1 + x with one rounding, and x - h is representable.
+__device__ __forceinline__ float sub_f16_lo(float x, uint32_t h) {
+    float r;
+    asm("v_fma_mix_f32 %0, -%1, 1.0, %2 op_sel_hi:[1,0,0]" : "=v"(r) : "v"(h), "v"(x));
+    return r;
+}
+__device__ __forceinline__ float sub_f16_hi(float x, uint32_t h) {
+    float r;
+    asm("v_fma_mix_f32 %0, -%1, 1.0, %2 op_sel:[1,0,0] op_sel_hi:[1,0,0]" : "=v"(r) : "v"(h), "v"(x));
+    return r;
+}
+
+// Scale exponent putting magnitude bits `mb` (fp32, sign cleared) in [2^14, 2^15): 14 - floor(log2).
+// 0 for zero.  Exponents outside [-100, 100] mark the block (the attention kernel keeps the
+// factor 2^-scale in the fp32 normal range) and are clamped.
+__device__ __forceinline__ int stg_scale_exp(uint32_t mb, bool& bad) {
+    if (mb == 0u) return 0;
+    const int e = static_cast<int>(mb >> 23) - 127;
+    if (e < -100 || e > 100) bad = true;
+    return 14 - (e < -100 ? -100 : e > 100 ? 100 : e);
+}
+
+__device__ __forceinline__ float pow2f(int e) { return __uint_as_float(static_cast<uint32_t>(127 + e) << 23); }
+
+// One workgroup per (sequence, KV head, 64-position block) of the positions the attention
+// reads, [0, start + T); thread (r, qq) holds dims 16qq .. 16qq+15 and 64+16qq .. of row r.
+// Rows past start + T in the last block are written as zeros (the attention kernel copies
+// whole blocks and masks them).
+__global__ __launch_bounds__(kStgThreads) void prefill_stage_kernel(PrefillArgs a) {
+    __shared__ uint32_t red[2][kStgThreads / kWave];
+    const int tid = threadIdx.x;
+    const int wave = tid >> 6;
+    const int lane = tid & (kWave - 1);
+    const int r = tid >> 2;
+    const int qq = tid & 3;
+    const int nblk = a.stg_pos / kPfBlk;
+    const int64_t n_items = static_cast<int64_t>(a.batch) * kHkv * nblk;
+    for (int64_t item = blockIdx.x; item < n_items; item += gridDim.x) {
+        const int blk = static_cast<int>(item % nblk);
+        const int bh = static_cast<int>(item / nblk);
+        const int b = bh / kHkv;
+        const int h = bh % kHkv;
+        const int st = a.start[b];
+        if (!prefill_start_ok(a, st)) continue;
+        const int n_keys = st + a.n_new;
+        if (blk * kPfBlk >= n_keys) continue;
+        const int p = blk * kPfBlk + r;
+        float kf[32], vf[32];     // [j] = dim 16qq + j, [16 + j] = dim 64 + 16qq + j
+        bool bad = false;
+#pragma unroll
+        for (int j = 0; j < 32; ++j) kf[j] = vf[j] = 0.f;
+        if (p < n_keys) {
+            const int64_t ce = cache_elem(a, b, h, p);
+            if (ce < 0) {
+                bad = true;
+            } else {
+                const char* vr = reinterpret_cast<const char*>(a.v + ce);
+                uint4 w[4];
+#pragma unroll
+                for (int c = 0; c < 4; ++c) w[c] = load_stream16(vr + 128 * (c >> 1) + 32 * qq + 16 * (c & 1));
+#pragma unroll
+                for (int c = 0; c < 4; ++c) {
+                    float f[8];
+                    unpack8(w[c], f);
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) vf[8 * c + j] = f[j];
+                }
+                if (p < st) {
+                    const char* kr = reinterpret_cast<const char*>(a.k + ce);
+#pragma unroll
+                    for (int c = 0; c < 4; ++c) w[c] = load_stream16(kr + 128 * (c >> 1) + 32 * qq + 16 * (c & 1));
+#pragma unroll
+                    for (int c = 0; c < 4; ++c) {
+                        float f[8];
+                        unpack8(w[c], f);
+#pragma unroll
+                        for (int j = 0; j < 8; ++j) kf[8 * c + j] = f[j];
+                    }
+                } else {
+                    const float* kx = a.kx32 + ((static_cast<int64_t>(b) * a.n_new + (p - st)) * kHkv + h) * kD;
+#pragma unroll
+                    for (int c = 0; c < 8; ++c) {
+                        const float4 f = *reinterpret_cast<const float4*>(kx + 64 * (c >> 2) + 16 * qq + 4 * (c & 3));
+                        kf[4 * c] = f.x;
+                        kf[4 * c + 1] = f.y;
+                        kf[4 * c + 2] = f.z;
+                        kf[4 * c + 3] = f.w;
+                    }
+                }
+            }
+        }
+        // Largest magnitudes as fp32 bit patterns (NaN and infinity compare above every
+        // finite value): per row over its four threads, then over the block.
+        uint32_t rk = 0u, rv = 0u;
+#pragma unroll
+        for (int j = 0; j < 32; ++j) {
+            rk = max(rk, __float_as_uint(kf[j]) & 0x7fffffffu);
+            rv = max(rv, __float_as_uint(vf[j]) & 0x7fffffffu);
+        }
+        rk = max(rk, static_cast<uint32_t>(__shfl_xor(static_cast<int>(rk), 1)));
+        rk = max(rk, static_cast<uint32_t>(__shfl_xor(static_cast<int>(rk), 2)));
+        rv = max(rv, static_cast<uint32_t>(__shfl_xor(static_cast<int>(rv), 1)));
+        rv = max(rv, static_cast<uint32_t>(__shfl_xor(static_cast<int>(rv), 2)));
+        uint32_t wk = rk, wv = rv;
+#pragma unroll
+        for (int sh = 4; sh < kWave; sh <<= 1) {
+            wk = max(wk, static_cast<uint32_t>(__shfl_xor(static_cast<int>(wk), sh)));
+            wv = max(wv, static_cast<uint32_t>(__shfl_xor(static_cast<int>(wv), sh)));
+        }
+        __syncthreads();                      // red is rewritten for every item
+        if (lane == 0) {
+            red[0][wave] = wk;
+            red[1][wave] = wv;
+        }
+        __syncthreads();
+        uint32_t bk = 0u, bv = 0u;
+#pragma unroll
+        for (int w = 0; w < kStgThreads / kWave; ++w) {
+            bk = max(bk, red[0][w]);
+            bv = max(bv, red[1][w]);
+        }
+        if (bk >= 0x7f800000u || bv >= 0x7f800000u) bad = true;
+        const int sk = stg_scale_exp(bk, bad);
+        const int sv = stg_scale_exp(bv, bad);
+        // A row far below the block's largest magnitude would keep fewer bits of its small
+        // elements than the attention's error bound allows.
+        if (bk >= (13u << 23) && rk != 0u && rk < bk - (12u << 23)) bad = true;
+        if (bv >= (13u << 23) && rv != 0u && rv < bv - (12u << 23)) bad = true;
+        const bool any_bad = __syncthreads_or(bad);
+        const float fk = pow2f(sk), fv = pow2f(sv);
+        const bool chunk_row = p >= st && p < n_keys;
+        uint32_t kh[16], kl[16], vh[16];
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+            const float x0 = kf[2 * j] * fk, x1 = kf[2 * j + 1] * fk;
+            kh[j] = pk_f16(x0, x1);
+            kl[j] = chunk_row ? pk_f16(x0 - f16_lo(kh[j]), x1 - f16_hi(kh[j])) : 0u;
+            vh[j] = pk_f16(vf[2 * j] * fv, vf[2 * j + 1] * fv);
+        }
+        const int64_t row = static_cast<int64_t>(bh) * a.stg_pos + p;
+        char* ko = reinterpret_cast<char*>(a.stg_k + row * kD);
+        char* vo = reinterpret_cast<char*>(a.stg_v + row * kD);
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            const int off = 128 * (c >> 1) + 32 * qq + 16 * (c & 1);
+            *reinterpret_cast<uint4*>(ko + off) = make_uint4(kh[4 * c], kh[4 * c + 1], kh[4 * c + 2], kh[4 * c + 3]);
+            *reinterpret_cast<uint4*>(vo + off) = make_uint4(vh[4 * c], vh[4 * c + 1], vh[4 * c + 2], vh[4 * c + 3]);
+        }
+        if (blk * kPfBlk + kPfBlk - 1 >= st) {
+            const int cb = blk - st / kPfBlk;
+            char* lo = reinterpret_cast<char*>(
+                a.stg_klo + ((static_cast<int64_t>(bh) * a.stg_cb + cb) * kPfBlk + r) * kD);
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+                const int off = 128 * (c >> 1) + 32 * qq + 16 * (c & 1);
+                *reinterpret_cast<uint4*>(lo + off) = make_uint4(kl[4 * c], kl[4 * c + 1], kl[4 * c + 2], kl[4 * c + 3]);
+            }
+        }
+        if (tid == 0)
+            a.stg_scale[static_cast<int64_t>(bh) * nblk + blk] =
+                (static_cast<uint32_t>(sk) & 0xffu) | ((static_cast<uint32_t>(sv) & 0xffu) << 8) |
+                (any_bad ? 0x80000000u : 0u);
+    }
+}
+
+hipError_t launch_prefill_stage(const PrefillArgs& a, hipStream_t stream) {
+    const int64_t n_items = static_cast<int64_t>(a.batch) * kHkv * (a.stg_pos / kPfBlk);
+    if (n_items == 0) return hipSuccess;
+    const int64_t grid = n_items < kStgMaxWgs ? n_items : kStgMaxWgs;
+    hipLaunchKernelGGL(prefill_stage_kernel, dim3(static_cast<unsigned>(grid)), dim3(kStgThreads), 0, stream, a);
+    return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------------
 // Attention.
 
-// LDS: eight 16 KB planes of 64 rows x 256 B -- K of buffers 0 and 1, V of buffers 0 and 1,
-// then the second and third BF16 parts of chunk keys for buffers 0 and 1 (128 KB in all).
-// K runs one block ahead of V: while block j's probabilities are formed and its V^T P^T
-// accumulated, block j+1's scores are formed from the other K buffer.  Rows are copied from
-// HBM straight into LDS (global_load_lds_dwordx4: lane l of an instruction writes bytes
+// LDS: six 16 KB planes of 64 rows x 256 B -- K of buffers 0 and 1, V of buffers 0 and 1,
+// the trailing parts of chunk keys for buffers 0 and 1 (96 KB in all).  K runs one block
+// ahead of V: while block j's probabilities are formed and its V^T P^T accumulated, block
+// j+1's scores are formed from the other K buffer.  Rows are copied from the staging planes
+// straight into LDS (global_load_lds_dwordx4: lane l of an instruction writes bytes
 // [16l, 16l + 16) of a 1 KB stretch = 4 rows), so a row's 16 16-byte chunks are placed by
 // choosing which chunk each lane fetches: chunk c of row r sits at position c ^ pf_swz(r & 15).
 // With that swizzle the K operand reads (16 rows, one chunk) and the V^T transpose reads
@@ -157,126 +376,67 @@ hipError_t launch_kv_append(const PrefillArgs& a, hipStream_t stream) {
 constexpr int kPlaneB = kPfBlk * kRowB;     // 16 KB per plane
 constexpr int kOffK = 0;                    // + buffer * kPlaneB
 constexpr int kOffV = 2 * kPlaneB;
-constexpr int kOffK2 = 4 * kPlaneB;
-constexpr int kOffK3 = 6 * kPlaneB;
-constexpr int kLdsB = 8 * kPlaneB;
-
-typedef __attribute__((address_space(3))) void lds_void_t;
+constexpr int kOffKlo = 4 * kPlaneB;
+// Then a ring of block scale words: words for blocks [0, 512) are copied at the start and
+// words for blocks [256k + 256, 256k + 512) at step 256k, into the half whose blocks are done,
+// so that a word is in LDS 255 steps before it is read.  Copied like the rows (straight into
+// LDS, completed by the step's vmcnt(0) wait), it costs no wait of its own: a plain load's
+// wait would also wait for the K/V copies in flight.
+constexpr int kOffSw = 6 * kPlaneB;
+constexpr int kSwRing = 512;
+constexpr int kLdsB = 6 * kPlaneB + kSwRing * 4;
 
 // Wave w of the workgroup copies rows 8w .. 8w+7 of a plane (two 4-row instructions).
-// Rows past the keys this workgroup needs repeat its last key.
 __device__ __forceinline__ int pf_copy_row(int wave, int ii, int lane) { return 4 * (2 * wave + ii) + (lane >> 4); }
 
-// Request the K rows of block blk into K buffer `buf`, and for a block holding chunk keys the
-// second and third parts of its rows (a cached key's parts come from the zero row).  For a
-// block whose 64 keys all exist the addresses are the block's first row (uniform) plus the
-// lane's 32-bit offset `loff` (pf_copy_offsets).
-__device__ __forceinline__ void pf_issue_k(const PrefillArgs& a, const char* kbase, int b, int kvh, int st,
-                                           int blk, int n_keys, bool has_new, const uint32_t (&loff)[2],
-                                           uint8_t* lds, int buf, int wave, int lane) {
-    const int64_t row_bytes = a.kv_pos_stride * 2;
-    const int64_t n_rows = static_cast<int64_t>(a.batch) * a.n_new * kHkv;
-    const int key0 = blk * kPfBlk;
-    if (!has_new && key0 + kPfBlk <= n_keys) {
-        // the common block: cached keys only, all 64 rows exist (a uniform branch, so no
-        // per-lane address arithmetic beyond the lane's fixed offset)
-        const char* brow = kbase + static_cast<int64_t>(key0) * row_bytes;
-#pragma unroll
-        for (int ii = 0; ii < 2; ++ii)
-            __builtin_amdgcn_global_load_lds(brow + loff[ii],
-                                             (lds_void_t*)(lds + kOffK + buf * kPlaneB + (2 * wave + ii) * 1024), 16, 0, 0);
-        return;
-    }
-    const bool full = key0 + kPfBlk <= n_keys;
-    const char* brow = kbase + static_cast<int64_t>(key0) * row_bytes;
+// The lane's byte offset within a staged 64-row block for its two copy instructions.
+__device__ __forceinline__ void pf_copy_offsets(int wave, int lane, uint32_t (&loff)[2]) {
 #pragma unroll
     for (int ii = 0; ii < 2; ++ii) {
         const int r = pf_copy_row(wave, ii, lane);
-        const int c = (lane & 15) ^ pf_swz(r);
-        const int key = min(key0 + r, n_keys - 1);
-        const int stretch = buf * kPlaneB + (2 * wave + ii) * 1024;
-        const char* src = full ? brow + loff[ii] : kbase + static_cast<int64_t>(key) * row_bytes + 16 * c;
-        __builtin_amdgcn_global_load_lds(src, (lds_void_t*)(lds + kOffK + stretch), 16, 0, 0);
-        if (has_new) {
-            const int u = key - st;          // chunk row of this key (< 0: a cached key)
-            const int64_t prow = u < 0 ? 2 * n_rows : (static_cast<int64_t>(b) * a.n_new + u) * kHkv + kvh;
-            const int64_t lrow = u < 0 ? 2 * n_rows : n_rows + prow;
-            const char* p1 = reinterpret_cast<const char*>(a.k_split + prow * kD) + 16 * c;
-            const char* p2 = reinterpret_cast<const char*>(a.k_split + lrow * kD) + 16 * c;
-            __builtin_amdgcn_global_load_lds(p1, (lds_void_t*)(lds + kOffK2 + stretch), 16, 0, 0);
-            __builtin_amdgcn_global_load_lds(p2, (lds_void_t*)(lds + kOffK3 + stretch), 16, 0, 0);
-        }
+        loff[ii] = static_cast<uint32_t>(r * kRowB + 16 * ((lane & 15) ^ pf_swz(r)));
     }
 }
 
-// Request the V rows of block blk into V buffer `buf` (addresses as in pf_issue_k).
-__device__ __forceinline__ void pf_issue_v(const PrefillArgs& a, const char* vbase, int blk, int n_keys,
-                                           const uint32_t (&loff)[2], uint8_t* lds, int buf, int wave, int lane) {
-    const int64_t row_bytes = a.kv_pos_stride * 2;
-    const int key0 = blk * kPfBlk;
-    const bool full = key0 + kPfBlk <= n_keys;
-    const char* brow = vbase + static_cast<int64_t>(key0) * row_bytes;
-    if (full) {
+// Request one staged 64-row block (16 KB at `src`) into the LDS plane at `dst`.
+__device__ __forceinline__ void pf_issue(const char* src, const uint32_t (&loff)[2], uint8_t* dst, int wave) {
 #pragma unroll
-        for (int ii = 0; ii < 2; ++ii)
-            __builtin_amdgcn_global_load_lds(brow + loff[ii],
-                                             (lds_void_t*)(lds + kOffV + buf * kPlaneB + (2 * wave + ii) * 1024), 16, 0, 0);
-        return;
-    }
-#pragma unroll
-    for (int ii = 0; ii < 2; ++ii) {
-        const int r = pf_copy_row(wave, ii, lane);
-        const int c = (lane & 15) ^ pf_swz(r);
-        const int key = min(key0 + r, n_keys - 1);
-        const int stretch = buf * kPlaneB + (2 * wave + ii) * 1024;
-        const char* src = full ? brow + loff[ii] : vbase + static_cast<int64_t>(key) * row_bytes + 16 * c;
-        __builtin_amdgcn_global_load_lds(src, (lds_void_t*)(lds + kOffV + stretch), 16, 0, 0);
-    }
+    for (int ii = 0; ii < 2; ++ii)
+        __builtin_amdgcn_global_load_lds(src + loff[ii], (lds_void_t*)(dst + (2 * wave + ii) * 1024), 16, 0, 0);
 }
 
-// The lane's byte offset from a block's first row for its two copy instructions (below 2^32:
-// the ABI keeps (capacity + 64) rows of a (sequence, KV head) under 4 GiB).
-__device__ __forceinline__ void pf_copy_offsets(const PrefillArgs& a, int wave, int lane, uint32_t (&loff)[2]) {
-    const uint32_t row_bytes = static_cast<uint32_t>(a.kv_pos_stride * 2);
-#pragma unroll
-    for (int ii = 0; ii < 2; ++ii) {
-        const int r = pf_copy_row(wave, ii, lane);
-        loff[ii] = static_cast<uint32_t>(r) * row_bytes + 16u * static_cast<uint32_t>((lane & 15) ^ pf_swz(r));
-    }
+__device__ __forceinline__ f16x8_t as_f16x8(const uint4& w) { return __builtin_bit_cast(f16x8_t, w); }
+
+// 8 fp16 K values of row `row`, bytes [16 chunk, 16 chunk + 16) of the plane at `plane`.
+__device__ __forceinline__ f16x8_t pf_k16(const uint8_t* plane, int row, int chunk) {
+    return *reinterpret_cast<const f16x8_t*>(plane + row * kRowB + 16 * (chunk ^ pf_swz(row)));
 }
 
 // One 32-dim slice (dims 32q .. 32q+31) of the scores S^T[key][query] of one 16-query tile
-// over the block's 4 key tiles: the 3 BF16 parts of Q against the cache row, and for chunk
-// keys the (k2,q1), (k2,q2), (k3,q1) products.
+// over the block's 4 key tiles: the 2 fp16 parts of Q against the K plane, and for chunk
+// keys the trailing part of K against Q's leading part.
 template <bool kNew>
-__device__ __forceinline__ void pf_qk_slice(const uint8_t* kplane, const bf16x8_t (&qop)[3][4], int q, int n,
+__device__ __forceinline__ void pf_qk_slice(const uint8_t* kplane, const f16x8_t (&qop)[2][4], int q, int n,
                                             int g, f32x4_t (&sacc)[4]) {
-    bf16x8_t ak[4];
+    f16x8_t ak[4];
 #pragma unroll
-    for (int kt = 0; kt < 4; ++kt) ak[kt] = pf_k_chunk(kplane, 16 * kt + n, 4 * q + g);
+    for (int kt = 0; kt < 4; ++kt) ak[kt] = pf_k16(kplane, 16 * kt + n, 4 * q + g);
 #pragma unroll
-    for (int s = 0; s < 3; ++s)
+    for (int s = 0; s < 2; ++s)
 #pragma unroll
         for (int kt = 0; kt < 4; ++kt)
-            sacc[kt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ak[kt], qop[s][q], sacc[kt], 0, 0, 0);
+            sacc[kt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ak[kt], qop[s][q], sacc[kt], 0, 0, 0);
     if (kNew) {
 #pragma unroll
-        for (int kt = 0; kt < 4; ++kt) ak[kt] = pf_k_chunk(kplane + (kOffK2 - kOffK), 16 * kt + n, 4 * q + g);
-#pragma unroll
-        for (int s = 0; s < 2; ++s)
-#pragma unroll
-            for (int kt = 0; kt < 4; ++kt)
-                sacc[kt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ak[kt], qop[s][q], sacc[kt], 0, 0, 0);
-#pragma unroll
-        for (int kt = 0; kt < 4; ++kt) ak[kt] = pf_k_chunk(kplane + (kOffK3 - kOffK), 16 * kt + n, 4 * q + g);
+        for (int kt = 0; kt < 4; ++kt) ak[kt] = pf_k16(kplane + (kOffKlo - kOffK), 16 * kt + n, 4 * q + g);
 #pragma unroll
         for (int kt = 0; kt < 4; ++kt)
-            sacc[kt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ak[kt], qop[0][q], sacc[kt], 0, 0, 0);
+            sacc[kt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ak[kt], qop[0][q], sacc[kt], 0, 0, 0);
     }
 }
 
 // Per-tile softmax state: the running max (integer-valued, log2 units), sum and O (fp64,
-// lane (g, n): O^T[16dt + 4g + i][query n]).
+// lane (g, n): O^T[16dt + 4g + i][query n]), both in units of 2^12 p.
 struct PfTile {
     double o64[8][4];
     double l64;
@@ -285,9 +445,10 @@ struct PfTile {
 
 // Running max after a block: masks keys past each query on diagonal blocks, then returns
 // ceil(block max) where that exceeds the running max m (integer-valued, so every rescale is an
-// exact power of two), else m.  The two cross-row steps are gfx950 lane swaps (rows 16 and 32
-// lanes apart), not LDS permutes.
-__device__ __forceinline__ float pf_next_max(f32x4_t (&sacc)[4], bool diag, int key0, int g, int pos_n, float m) {
+// exact power of two), else m.  `mult` turns the block's raw scores into log2 units.  The two
+// cross-row steps are gfx950 lane swaps (rows 16 and 32 lanes apart), not LDS permutes.
+__device__ __forceinline__ float pf_next_max(f32x4_t (&sacc)[4], bool diag, int key0, int g, int pos_n, float m,
+                                             float mult) {
     if (diag) {
 #pragma unroll
         for (int kt = 0; kt < 4; ++kt)
@@ -303,7 +464,7 @@ __device__ __forceinline__ float pf_next_max(f32x4_t (&sacc)[4], bool diag, int 
     const auto x16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(bmax), __float_as_uint(bmax), false, false);
     bmax = fmaxf(__uint_as_float(x16[0]), __uint_as_float(x16[1]));
     const auto x32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(bmax), __float_as_uint(bmax), false, false);
-    bmax = fmaxf(__uint_as_float(x32[0]), __uint_as_float(x32[1]));
+    bmax = fmaxf(__uint_as_float(x32[0]), __uint_as_float(x32[1])) * mult;
     return bmax > m ? ceilf(bmax) : m;
 }
 
@@ -317,6 +478,28 @@ __device__ __forceinline__ void pf_rescale(PfTile& t, float m_new) {
             for (int i = 0; i < 4; ++i) t.o64[dt][i] = ldexp(t.o64[dt][i], shift);
         t.l64 = ldexp(t.l64, shift);
         t.m_run = m_new;
+    }
+}
+
+// p = 2^12 * 2^(s - m) of key tile kt (0 for masked keys; s = raw score * mult), summed into
+// lsum and split into two fp16 parts rounded to nearest (p = p1 + p2 to 2^-22 relative),
+// packed as the P^T B operand: ph[part][window][dword].
+__device__ __forceinline__ void pf_probs_tile16(const f32x4_t& s, float mult, float off, float& lsum,
+                                                uint32_t (&ph)[2][2][4], int kt) {
+    float p[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        // v_exp_f32: 2^x, 0 for -inf (masked keys); results below 2^-126 flush to 0, far
+        // below anything the BF16 output can see.
+        p[i] = __builtin_amdgcn_exp2f(fmaf(s[i], mult, off));
+        lsum += p[i];
+    }
+    const int w = kt >> 1, d0 = (kt & 1) * 2;
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        const uint32_t h1 = pk_f16(p[2 * j], p[2 * j + 1]);
+        ph[0][w][d0 + j] = h1;
+        ph[1][w][d0 + j] = pk_f16(sub_f16_lo(p[2 * j], h1), sub_f16_hi(p[2 * j + 1], h1));
     }
 }
 
@@ -352,10 +535,10 @@ __device__ __forceinline__ void pf_vt_wait(VtPair& v0, VtPair& v1) {
                    "+v"(v1.r[0][1]), "+v"(v1.r[1][0]), "+v"(v1.r[1][1]));
 }
 
-__device__ __forceinline__ bf16x8_t pf_vt_operand(const VtPair& v, int w) {
+__device__ __forceinline__ f16x8_t pf_vt_operand(const VtPair& v, int w) {
     union {
         short4_t h[2];
-        bf16x8_t v;
+        f16x8_t v;
     } u;
     u.h[0] = v.r[w][0];
     u.h[1] = v.r[w][1];
@@ -367,16 +550,17 @@ __device__ __forceinline__ uint32_t pf_vt_addr(uint32_t lds_base, int dt, int la
     return lds_base + kOffV + vt_tr_offset(dt, lane);
 }
 
-// O^T[dim][query] += the block's V^T P^T: per 16-dim tile, V^T (transpose reads) against the
-// three P parts of both 32-key windows in fp32, then added into the fp64 O; two tiles at a
-// time, the next two tiles' operands requested before the current two's products.
-__device__ __forceinline__ void pf_pv(const uint32_t (&vaddr)[8], uint32_t voff, const uint32_t (&ph)[3][2][4],
-                                      PfTile& t) {
-    bf16x8_t pb[2][3];
+// O^T[dim][query] += cv * the block's V^T P^T: per 16-dim tile, V^T (transpose reads) against
+// the two P parts of both 32-key windows in fp32, then scaled by the block's V scale cv (a
+// power of two) into the fp64 O; two tiles at a time, the next two tiles' operands requested
+// before the current two's products.
+__device__ __forceinline__ void pf_pv(const uint32_t (&vaddr)[8], uint32_t voff, const uint32_t (&ph)[2][2][4],
+                                      double cv, PfTile& t) {
+    f16x8_t pb[2][2];
 #pragma unroll
     for (int w = 0; w < 2; ++w)
 #pragma unroll
-        for (int s = 0; s < 3; ++s) pb[w][s] = as_bf16x8(make_uint4(ph[s][w][0], ph[s][w][1], ph[s][w][2], ph[s][w][3]));
+        for (int s = 0; s < 2; ++s) pb[w][s] = as_f16x8(make_uint4(ph[s][w][0], ph[s][w][1], ph[s][w][2], ph[s][w][3]));
     VtPair cur[2];
     cur[0] = pf_vt_issue(vaddr[0] + voff);
     cur[1] = pf_vt_issue(vaddr[1] + voff);
@@ -395,15 +579,15 @@ __device__ __forceinline__ void pf_pv(const uint32_t (&vaddr)[8], uint32_t voff,
         for (int w = 0; w < 2; ++w)
 #pragma unroll
             for (int e = 0; e < 2; ++e) {
-                const bf16x8_t av = pf_vt_operand(cur[e], w);
+                const f16x8_t av = pf_vt_operand(cur[e], w);
 #pragma unroll
-                for (int s = 0; s < 3; ++s)
-                    oacc[e] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, pb[w][s], oacc[e], 0, 0, 0);
+                for (int s = 0; s < 2; ++s)
+                    oacc[e] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, pb[w][s], oacc[e], 0, 0, 0);
             }
 #pragma unroll
         for (int e = 0; e < 2; ++e)
 #pragma unroll
-            for (int i = 0; i < 4; ++i) t.o64[d0 + e][i] += static_cast<double>(oacc[e][i]);
+            for (int i = 0; i < 4; ++i) t.o64[d0 + e][i] = fma(static_cast<double>(oacc[e][i]), cv, t.o64[d0 + e][i]);
         if (d0 + 2 < 8) {
             cur[0] = nxt[0];
             cur[1] = nxt[1];
@@ -411,20 +595,21 @@ __device__ __forceinline__ void pf_pv(const uint32_t (&vaddr)[8], uint32_t voff,
     }
 }
 
-// Probabilities of the current block (scores `scur`, running max already grown) interleaved
-// with the scores of the next block from K buffer `kplane` (kNext: there is one; kNew: it
-// holds chunk keys).
+// Probabilities of the current block (raw scores `scur` times `mult`, running max already
+// grown) interleaved with the scores of the next block from K buffer `kplane` (kNext: there
+// is one; kNew: it holds chunk keys).
 template <bool kNext, bool kNew>
-__device__ __forceinline__ void pf_probs_and_next(const f32x4_t (&scur)[4], const uint8_t* kplane,
-                                                  const bf16x8_t (&qop)[3][4], int n, int g, PfTile& t,
-                                                  uint32_t (&ph)[3][2][4], f32x4_t (&snext)[4]) {
+__device__ __forceinline__ void pf_probs_and_next(const f32x4_t (&scur)[4], float mult, const uint8_t* kplane,
+                                                  const f16x8_t (&qop)[2][4], int n, int g, PfTile& t,
+                                                  uint32_t (&ph)[2][2][4], f32x4_t (&snext)[4]) {
 #pragma unroll
     for (int kt = 0; kt < 4; ++kt) snext[kt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
     float lsum = 0.f;
+    const float off = static_cast<float>(kPScaleExp) - t.m_run;
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
         if (kNext) pf_qk_slice<kNew>(kplane, qop, q, n, g, snext);
-        pf_probs_tile(scur[q], t.m_run, lsum, ph, q);
+        pf_probs_tile16(scur[q], mult, off, lsum, ph, q);
     }
     t.l64 += static_cast<double>(lsum);
 }
@@ -477,55 +662,109 @@ __global__ __launch_bounds__(kPfThreads) void prefill_attn_kernel(PrefillArgs a)
     const int pos_n = st + tq_c;            // this lane's query position
     const int n_keys = st + min(T, qb * kPfPos + kPfPos);
     const int n_blk = (n_keys + kPfBlk - 1) / kPfBlk;
-    const int64_t head_elem = static_cast<int64_t>(b) * a.kv_batch_stride +
-                              static_cast<int64_t>(kvh) * a.kv_head_stride;
-    const char* kbase = reinterpret_cast<const char*>(a.k + head_elem);
-    const char* vbase = reinterpret_cast<const char*>(a.v + head_elem);
-    auto blk_new = [&](int blk) { return blk * kPfBlk + kPfBlk - 1 >= st; };
+    const int nblk_stg = a.stg_pos / kPfBlk;
+    const char* kseg = reinterpret_cast<const char*>(a.stg_k + static_cast<int64_t>(pair) * a.stg_pos * kD);
+    const char* vseg = reinterpret_cast<const char*>(a.stg_v + static_cast<int64_t>(pair) * a.stg_pos * kD);
+    const char* kloseg = reinterpret_cast<const char*>(a.stg_klo + static_cast<int64_t>(pair) * a.stg_cb * kPfBlk * kD);
+    const uint32_t* sw = a.stg_scale + static_cast<int64_t>(pair) * nblk_stg;
+    const int cb0 = st / kPfBlk;            // first block holding chunk keys
+    auto blk_new = [&](int blk) { return blk >= cb0; };
     auto blk_diag = [&](int blk) { return blk * kPfBlk + kPfBlk - 1 > st + t_wave0; };
+    auto issue_k = [&](int blk, int buf, const uint32_t (&loff)[2]) {
+        pf_issue(kseg + static_cast<int64_t>(blk) * kPlaneB, loff, lds + kOffK + buf * kPlaneB, wave);
+        if (blk_new(blk))
+            pf_issue(kloseg + static_cast<int64_t>(blk - cb0) * kPlaneB, loff, lds + kOffKlo + buf * kPlaneB, wave);
+    };
+    auto issue_v = [&](int blk, int buf, const uint32_t (&loff)[2]) {
+        pf_issue(vseg + static_cast<int64_t>(blk) * kPlaneB, loff, lds + kOffV + buf * kPlaneB, wave);
+    };
 
     // K of blocks 0 and 1 and V of block 0 are requested before the Q operands are formed.
     uint32_t loff[2];
-    pf_copy_offsets(a, wave, lane, loff);
-    pf_issue_k(a, kbase, b, kvh, st, 0, n_keys, blk_new(0), loff, lds, 0, wave, lane);
-    pf_issue_v(a, vbase, 0, n_keys, loff, lds, 0, wave, lane);
-    if (n_blk > 1) pf_issue_k(a, kbase, b, kvh, st, 1, n_keys, blk_new(1), loff, lds, 1, wave, lane);
+    pf_copy_offsets(wave, lane, loff);
+    issue_k(0, 0, loff);
+    issue_v(0, 0, loff);
+    if (n_blk > 1) issue_k(1, 1, loff);
+    // Scale words of blocks 64 wave .. 64 wave + 63 (entries past the last block repeat it).
+    auto issue_sw = [&](int first) {
+        __builtin_amdgcn_global_load_lds(sw + min(first + lane, nblk_stg - 1),
+                                         (lds_void_t*)(lds + kOffSw + 4 * (first & (kSwRing - 1))), 4, 0, 0);
+    };
+    issue_sw(64 * wave);
+    auto sw_at = [&](int blk) {
+        return __builtin_amdgcn_readfirstlane(
+            *reinterpret_cast<const uint32_t*>(lds + kOffSw + 4 * (blk & (kSwRing - 1))));
+    };
 
-    // Q operands: query n = this lane's column, dims 32kb + 8g + j, three BF16 parts.
-    bf16x8_t qop[3][4];
+    // Q operands: query n = this lane's column, dims 32kb + 8g + j, two fp16 parts of Q
+    // scaled by 2^sq, sq putting the row's largest magnitude in [2^14, 2^15).
+    f16x8_t qop[2][4];
+    float cq;                               // 2^-sq
+    bool q_bad = false;
     {
         const uint16_t* qrow = a.q + ((static_cast<int64_t>(b) * T + tq_c) * kHq + hq) * kD;
+        // Every load first (the rotation below branches inside sincos, and each branch would
+        // otherwise wait for all memory in flight, the K/V copies included).
+        uint16_t qx[2][8], qy[2][8];
+        double fr[2][8];
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const int d = 32 * kb + 8 * g + j;
+                qx[kb][j] = qrow[d];
+                qy[kb][j] = qrow[d + kPairs];
+                fr[kb][j] = a.rope.inv_freq[d];
+            }
         double qv[4][8];
+        double mx = 0.0;
 #pragma unroll
         for (int kb = 0; kb < 2; ++kb) {
 #pragma unroll
             for (int j = 0; j < 8; ++j) {
-                const int d = 32 * kb + 8 * g + j;
-                const double x = bf16_to_f32(qrow[d]);
-                const double y = bf16_to_f32(qrow[d + kPairs]);
+                const double x = bf16_to_f32(qx[kb][j]);
+                const double y = bf16_to_f32(qy[kb][j]);
                 double xr = x, yr = y;
-                if (a.flags & 1u) rope_pair(x, y, pos_n, a.rope.inv_freq[d], xr, yr);
+                if (a.flags & 1u) rope_pair(x, y, pos_n, fr[kb][j], xr, yr);
                 qv[kb][j] = xr * a.qk_scale_log2;
                 qv[kb + 2][j] = yr * a.qk_scale_log2;
+                // NaN fails both comparisons
+                if (!(fabs(qv[kb][j]) <= 1e300) || !(fabs(qv[kb + 2][j]) <= 1e300)) q_bad = true;
+                mx = fmax(mx, fmax(fabs(qv[kb][j]), fabs(qv[kb + 2][j])));
             }
         }
+        mx = fmax(mx, __shfl_xor(mx, 16));
+        mx = fmax(mx, __shfl_xor(mx, 32));
+        int e = 0;
+        if (mx > 0.0) {
+            e = ilogb(mx);
+            if (e < -100 || e > 100) q_bad = true;
+            e = e < -100 ? -100 : e > 100 ? 100 : e;
+        }
+        const int sq = mx > 0.0 ? 14 - e : 0;
+        cq = pow2f(-sq);
 #pragma unroll
-        for (int s = 0; s < 3; ++s)
+        for (int kb = 0; kb < 4; ++kb) {
+            uint32_t w0[4], w1[4];
 #pragma unroll
-            for (int kb = 0; kb < 4; ++kb) {
-                uint16_t h8[8];
-#pragma unroll
-                for (int j = 0; j < 8; ++j) h8[j] = split3(qv[kb][j], s);
-                // Pin the operand: without this the compiler re-derives it from the double
-                // rows inside the block loop (~600 extra VALU per block) to save registers.
-                union {
-                    bf16x8_t v;
-                    uint32_t w[4];
-                } u;
-                u.v = pack8(h8);
-                asm volatile("" : "+v"(u.w[0]), "+v"(u.w[1]), "+v"(u.w[2]), "+v"(u.w[3]));
-                qop[s][kb] = u.v;
+            for (int j = 0; j < 4; ++j) {
+                const double x0 = ldexp(qv[kb][2 * j], sq), x1 = ldexp(qv[kb][2 * j + 1], sq);
+                const _Float16 h0 = static_cast<_Float16>(static_cast<float>(x0));
+                const _Float16 h1 = static_cast<_Float16>(static_cast<float>(x1));
+                f16x2_t hh;
+                hh[0] = h0;
+                hh[1] = h1;
+                w0[j] = __builtin_bit_cast(uint32_t, hh);
+                w1[j] = pk_f16(static_cast<float>(x0 - static_cast<double>(h0)),
+                               static_cast<float>(x1 - static_cast<double>(h1)));
             }
+            // Pin the operands: without this the compiler re-derives them from the double
+            // rows inside the block loop to save registers.
+            asm volatile("" : "+v"(w0[0]), "+v"(w0[1]), "+v"(w0[2]), "+v"(w0[3]));
+            asm volatile("" : "+v"(w1[0]), "+v"(w1[1]), "+v"(w1[2]), "+v"(w1[3]));
+            qop[0][kb] = as_f16x8(make_uint4(w0[0], w0[1], w0[2], w0[3]));
+            qop[1][kb] = as_f16x8(make_uint4(w1[0], w1[1], w1[2], w1[3]));
+        }
     }
 
     const uint32_t lds_base = static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_void_t*)(lds)));
@@ -541,6 +780,16 @@ __global__ __launch_bounds__(kPfThreads) void prefill_attn_kernel(PrefillArgs a)
     tl.l64 = 0.0;
     tl.m_run = -INFINITY;
 
+    // Raw scores carry 2^(sq + sk): mult = 2^-sq * 2^-sk(block) turns them into log2 units.
+    // (Kept at least 2^-126: a smaller factor means scores below ~2^-90, all p = 1 either way,
+    // and 0 would turn masked keys' -inf into NaN.)
+    auto blk_mult = [&](uint32_t w) {
+        return fmaxf(cq * pow2f(-static_cast<int>(static_cast<int8_t>(w & 0xffu))), 1.17549435e-38f);
+    };
+    auto blk_cv = [&](uint32_t w) {
+        return static_cast<double>(pow2f(-static_cast<int>(static_cast<int8_t>((w >> 8) & 0xffu))));
+    };
+
     // Block 0's scores.  The barrier after them frees K buffer 0 for block 2.
     __builtin_amdgcn_s_waitcnt(0x0F70);    // vmcnt(0)
     __syncthreads();
@@ -554,41 +803,50 @@ __global__ __launch_bounds__(kPfThreads) void prefill_attn_kernel(PrefillArgs a)
 #pragma unroll
         for (int q = 0; q < 4; ++q) pf_qk_slice<false>(lds + kOffK, qop, q, n, g, scur);
     }
-    pf_rescale(tl, pf_next_max(scur, blk_diag(0), 0, g, pos_n, tl.m_run));
+    uint32_t w_cur = sw_at(0);
+    uint32_t unsafe = w_cur;                // bit 31 of any block read marks all rows
+    float mult_cur = blk_mult(w_cur);
+    pf_rescale(tl, pf_next_max(scur, blk_diag(0), 0, g, pos_n, tl.m_run, mult_cur));
     __syncthreads();
 
     for (int blk = 0; blk < n_blk; ++blk) {
         // Resident: K of block blk+1 (K buffer (blk+1)&1) and V of block blk (V buffer blk&1).
         // Free: K buffer blk&1 (block blk, scored in the previous step) and V buffer
         // (blk+1)&1 (block blk-1).
-        if (blk + 2 < n_blk)
-            pf_issue_k(a, kbase, b, kvh, st, blk + 2, n_keys, blk_new(blk + 2), loff, lds, blk & 1, wave, lane);
-        if (blk + 1 < n_blk) pf_issue_v(a, vbase, blk + 1, n_keys, loff, lds, (blk + 1) & 1, wave, lane);
+        if (blk + 2 < n_blk) issue_k(blk + 2, blk & 1, loff);
+        if (blk + 1 < n_blk) issue_v(blk + 1, (blk + 1) & 1, loff);
+        if ((blk & 255) == 0 && blk > 0 && wave < 4 && blk + 256 < n_blk) issue_sw(blk + 256 + 64 * wave);
+        const uint32_t w_next = blk + 1 < n_blk ? sw_at(blk + 1) : w_cur;
+        unsafe |= w_next;
 
-        uint32_t ph[3][2][4];
+        uint32_t ph[2][2][4];
         f32x4_t snext[4];
         const uint8_t* knext = lds + kOffK + ((blk + 1) & 1) * kPlaneB;
         // The two waves of a SIMD run the same steps; the one in this MFMA + VALU mix gets
-        // issue priority over the other's V^T P^T (5 % faster than equal priorities).
+        // issue priority over the other's V^T P^T.
         __builtin_amdgcn_s_setprio(1);
         if (blk + 1 >= n_blk)
-            pf_probs_and_next<false, false>(scur, knext, qop, n, g, tl, ph, snext);
+            pf_probs_and_next<false, false>(scur, mult_cur, knext, qop, n, g, tl, ph, snext);
         else if (blk_new(blk + 1))
-            pf_probs_and_next<true, true>(scur, knext, qop, n, g, tl, ph, snext);
+            pf_probs_and_next<true, true>(scur, mult_cur, knext, qop, n, g, tl, ph, snext);
         else
-            pf_probs_and_next<true, false>(scur, knext, qop, n, g, tl, ph, snext);
+            pf_probs_and_next<true, false>(scur, mult_cur, knext, qop, n, g, tl, ph, snext);
         __builtin_amdgcn_s_setprio(0);
 
         // The next block's running max is found before this block's V^T P^T (which still
         // accumulates at the current max); O and l move to it afterwards.
+        const float mult_next = blk_mult(w_next);
         float m_next = tl.m_run;
-        if (blk + 1 < n_blk) m_next = pf_next_max(snext, blk_diag(blk + 1), (blk + 1) * kPfBlk, g, pos_n, tl.m_run);
+        if (blk + 1 < n_blk)
+            m_next = pf_next_max(snext, blk_diag(blk + 1), (blk + 1) * kPfBlk, g, pos_n, tl.m_run, mult_next);
 
-        pf_pv(vaddr, (blk & 1) * kPlaneB, ph, tl);
+        pf_pv(vaddr, (blk & 1) * kPlaneB, ph, blk_cv(w_cur), tl);
 
         pf_rescale(tl, m_next);
 #pragma unroll
         for (int kt = 0; kt < 4; ++kt) scur[kt] = snext[kt];
+        w_cur = w_next;
+        mult_cur = mult_next;
         // This wave's copies into LDS are complete; after the barrier every wave's are, and
         // every wave is done with the buffers the next step's copies go to.
         __builtin_amdgcn_s_waitcnt(0x0F70);    // vmcnt(0)
@@ -613,7 +871,12 @@ __global__ __launch_bounds__(kPfThreads) void prefill_attn_kernel(PrefillArgs a)
     mn = fmin(mn, __shfl_xor(mn, 16));
     mn = fmin(mn, __shfl_xor(mn, 32));
     if (!q_ok) return;
-    if (g == 0 && a.rs_hdr && mn * mn * kD < kRsFlagRatio2 * ss)
+    // Rows that read a marked block, a Q row out of range, or a non-finite sum go to the
+    // rescore as well (NaN fails the comparison).
+    const bool q_bad_row = __shfl_xor(static_cast<int>(q_bad), 16) | __shfl_xor(static_cast<int>(q_bad), 32) |
+                           __shfl_xor(static_cast<int>(q_bad), 48) | static_cast<int>(q_bad);
+    const bool flag = mn * mn * kD < kRsFlagRatio2 * ss || (unsafe >> 31) != 0u || q_bad_row || !(ss <= 1e300);
+    if (g == 0 && a.rs_hdr && flag)
         rs_append(a, static_cast<uint32_t>((static_cast<int64_t>(b) * T + tq) * kHq + hq));
     {
         uint16_t* orow = a.out + ((static_cast<int64_t>(b) * T + tq) * kHq + hq) * kD;

@@ -330,7 +330,7 @@ def bench_prefill(args, torch, gqa, dev) -> int:
         roofline = {"bound": "mfma", "achieved": round(achieved, 2), "peak": MFMA_BF16_PEAK_TFLOPS,
                     "unit": "TFLOP/s", "frac": round(achieved / MFMA_BF16_PEAK_TFLOPS, 4),
                     "traffic": None, "kernel": "prefill_attn_kernel",
-                    "kernel_us": round(attn_ms * 1e3, 2), "append_us": round(append_ms * 1e3, 2),
+                    "kernel_us": round(attn_ms * 1e3, 2), "append_stage_us": round(append_ms * 1e3, 2),
                     "flops_per_launch": flops}
     result = {
         "metric": "GQA chunked prefill µs/step + MFMA TFLOP/s, B=4 512 new over 8192 cached",
@@ -344,12 +344,13 @@ def bench_prefill(args, torch, gqa, dev) -> int:
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "bf16",
+        "dtype": "fp16",
         "data": f"synthetic N(0,1) BF16, seed {args.seed}",
         "config": {"workload": args.workload, "batch": bsz, "new_tokens": n_new,
                    "cached": start, "q_heads": 32, "kv_heads": 8, "head_dim": 128,
-                   "rope": "q and new k", "precision": "Q, new K and P in three BF16 parts, "
-                   "fp32 MFMA accumulation per 64-key block, fp64 across blocks",
+                   "rope": "q and new k", "precision": "BF16 K/V staged exactly as fp16 (power-of-two "
+                   "scale per 64-position block); Q, the chunk's K and P in two fp16 parts; fp32 MFMA "
+                   "accumulation per 64-key block, fp64 across blocks; fp64 rescore of flagged rows",
                    "flops_per_step": flops, "spinup_s": args.spinup_s},
         "roofline": roofline,
         "cpu_baseline": None if args.no_cpu_baseline else prefill_cpu_baseline(

@@ -195,18 +195,24 @@ int gqa_kv_append_paged_bf16(const gqa_params_t* params, const uint16_t* k_new, 
  *   start      [batch] int32, device; 0 <= start[b] <= capacity - n_new, else that
  *              sequence's output rows are NaN and its cache is not written
  *   out        [batch][n_new][32][128]
- *   workspace  gqa_prefill_workspace_bytes bytes (any contents)
+ *   workspace  gqa_prefill_workspace_bytes(params, batch, n_new, kv->capacity) bytes (any
+ *              contents)
  * Token t attends to keys p <= start[b] + t (gqa_attention_wrapper.v:279 per token), the
  * chunk's own keys carried to ~24 bits (their rotated value is not re-rounded, as in the
  * golden).  Replaces the reference's per-token start loop for a run of tokens.
  * Chunks of at most 16 new tokens (multi-token decode: drafts, a few steps at once) split
  * the keys of every (sequence, KV head) over all CUs and merge per-range partials (three
  * launches: preparation, which also appends the chunk's rows, stream, merge); longer chunks
- * run the KV append and one attention kernel over 32-token query blocks.  The environment
- * variable GQA_PREFILL_MULTI=0 sends short chunks to that kernel too; the workspace size
+ * run the KV append, a staging kernel that copies the K/V rows the attention reads into
+ * fp16 planes in the workspace (a power-of-two scale per 64-position block, so BF16 values
+ * convert exactly), and one attention kernel over 32-token query blocks.  Every path ends
+ * with an fp64 recomputation of the output rows its kernels flag.  The environment variable
+ * GQA_PREFILL_MULTI=0 sends short chunks to the attention kernel too; the workspace size
  * follows that choice and GQA_STREAM_WGS, so query it under the same environment as the
- * call. */
-size_t gqa_prefill_workspace_bytes(const gqa_params_t* params, int32_t batch, int32_t n_new);
+ * call.  For longer chunks it grows with capacity (the staging planes hold 512 bytes per
+ * position of every (sequence, KV head): 143 MB for batch 4 over 8704 positions). */
+size_t gqa_prefill_workspace_bytes(const gqa_params_t* params, int32_t batch, int32_t n_new,
+                                   int32_t capacity);
 
 int gqa_prefill_bf16(const gqa_params_t* params, const uint16_t* q, const uint16_t* k_new,
                      const uint16_t* v_new, uint16_t* k_cache, uint16_t* v_cache,
@@ -233,8 +239,8 @@ int gqa_rope_rows_bf16(const uint16_t* in, uint16_t* out, int64_t n_rows, int64_
 /* Kernel timing for measurement harnesses.  While enabled, each decode or prefill
  * call brackets its two kernels with HIP events on the call's stream (up to
  * `max_calls` calls are recorded; later ones are not): decode {stream kernel, merge
- * kernel}, prefill {KV append kernel, attention kernel}, prefill of at most 16 new tokens
- * {preparation kernel (with the append), stream kernel}.  The Q-operand preparation kernel
+ * kernel}, prefill {KV append and staging kernels, attention kernel}, prefill of at most 16
+ * new tokens {preparation kernel (with the append), stream kernel}.  The Q-operand preparation kernel
  * of a decode call runs before the first event, the merge kernel of a prefill of at most 16
  * new tokens after the last.  gqa_profile_read waits for the
  * recorded events, returns the summed kernel times and the number of calls recorded,

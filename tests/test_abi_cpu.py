@@ -33,7 +33,7 @@ def test_exports_match_header():
 def test_status_strings_and_version():
     assert _lib.status_string(0) == "ok"
     assert "invalid" in _lib.status_string(1)
-    assert _lib.lib().gqa_abi_version() >> 16 == 2
+    assert _lib.lib().gqa_abi_version() >> 16 == 3
 
 
 @pytest.mark.parametrize("regs,ok", [
@@ -147,10 +147,17 @@ def test_workspace_init_rejects():
 def test_prefill_workspace_bytes():
     L = _lib.lib()
     p = _params(flags=3)
-    n = L.gqa_prefill_workspace_bytes(ctypes.byref(p), 4, 512)
-    assert n >= 2 * 4 * 512 * 8 * 128 * 2 and n % 256 == 0
-    assert L.gqa_prefill_workspace_bytes(ctypes.byref(_params(head_dim=64)), 4, 512) == 0
-    assert L.gqa_prefill_workspace_bytes(ctypes.byref(p), 4, 0) == 0
+    n = L.gqa_prefill_workspace_bytes(ctypes.byref(p), 4, 512, 8704)
+    # at least the fp16 K and V staging planes (8704 positions of 32 (sequence, KV head) pairs)
+    # and the fp32 rotated new K rows
+    assert n >= 2 * 4 * 8 * 8704 * 128 * 2 + 4 * 512 * 8 * 128 * 4 and n % 256 == 0
+    # the staging planes (and one block scale word per pair) follow the capacity, rounded up to
+    # 64 positions
+    grow = L.gqa_prefill_workspace_bytes(ctypes.byref(p), 4, 512, 8705) - n
+    assert 2 * 4 * 8 * 64 * 128 * 2 <= grow <= 2 * 4 * 8 * 64 * 128 * 2 + 256
+    assert L.gqa_prefill_workspace_bytes(ctypes.byref(_params(head_dim=64)), 4, 512, 8704) == 0
+    assert L.gqa_prefill_workspace_bytes(ctypes.byref(p), 4, 0, 8704) == 0
+    assert L.gqa_prefill_workspace_bytes(ctypes.byref(p), 4, 512, 511) == 0
 
 
 def _prefill(p, *, q=256, kn=256, vn=256, k=256, v=256, layout=None, start=256, batch=1,

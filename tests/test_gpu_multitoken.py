@@ -176,7 +176,7 @@ def test_multi_workspace_garbage_and_repeat(dev):
     starts = [128, 0, 777, 5]
     q, kn, vn, k, v = _chunk(starts, 4, 790, 47)
     a, _, _ = _run(q, kn, vn, k, v, starts, dev)
-    ws = torch.empty(gqa.prefill_workspace_bytes(4, 4), dtype=torch.uint8, device=dev)
+    ws = torch.empty(gqa.prefill_workspace_bytes(4, 4, k.shape[2]), dtype=torch.uint8, device=dev)
     ws.fill_(0xFF)
     b, _, _ = _run(q, kn, vn, k, v, starts, dev, workspace=ws)
     assert np.array_equal(a, b)

@@ -129,7 +129,7 @@ def test_prefill_deterministic_and_workspace_reuse(dev):
     starts = [128, 0, 77]
     q, kn, vn, k, v = _chunk(3, 50, 180, starts, 7)
     a, _, _ = _run(q, kn, vn, k, v, starts, dev)
-    ws = torch.empty(gqa.prefill_workspace_bytes(3, 50), dtype=torch.uint8, device=dev)
+    ws = torch.empty(gqa.prefill_workspace_bytes(3, 50, k.shape[2]), dtype=torch.uint8, device=dev)
     ws.fill_(0xFF)
     b, _, _ = _run(q, kn, vn, k, v, starts, dev, workspace=ws)
     assert np.array_equal(a, b)
