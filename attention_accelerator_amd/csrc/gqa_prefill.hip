@@ -436,12 +436,26 @@ __device__ __forceinline__ void pf_qk_slice(const uint8_t* kplane, const f16x8_t
 }
 
 // Per-tile softmax state: the running max (integer-valued, log2 units), sum and O (fp64,
-// lane (g, n): O^T[16dt + 4g + i][query n]), both in units of 2^12 p.
+// lane (g, n): O^T[16dt + 4g + i][query n]), both in units of 2^12 p, and the fp32 sum of
+// V^T P^T over the current group of up to kPfGroup blocks (moved into the fp64 O when the
+// group closes: fp32 sums over 256 keys add no error measurable against per-block sums).
+constexpr int kPfGroup = 4;
 struct PfTile {
     double o64[8][4];
+    f32x4_t acc[8];
     double l64;
     float m_run;
 };
+
+// Closes a group: O += acc * cv (cv = 2^-(V scale of the group's blocks), exact).
+__device__ __forceinline__ void pf_flush(PfTile& t, double cv) {
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) t.o64[dt][i] = fma(static_cast<double>(t.acc[dt][i]), cv, t.o64[dt][i]);
+        t.acc[dt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    }
+}
 
 // Running max after a block: masks keys past each query on diagonal blocks, then returns
 // ceil(block max) where that exceeds the running max m (integer-valued, so every rescale is an
@@ -468,14 +482,18 @@ __device__ __forceinline__ float pf_next_max(f32x4_t (&sacc)[4], bool diag, int 
     return bmax > m ? ceilf(bmax) : m;
 }
 
-// Moves O and l to the running max m_new (exact power-of-two scaling).
+// Moves O, the open group's sum and l to the running max m_new (exact power-of-two scaling;
+// an fp32 group term pushed below 2^-149 is below 2^-149 of the new maximum's weight).
 __device__ __forceinline__ void pf_rescale(PfTile& t, float m_new) {
     if (__ballot(m_new != t.m_run)) {
         const int shift = (t.m_run == -INFINITY) ? 0 : static_cast<int>(t.m_run - m_new);
 #pragma unroll
         for (int dt = 0; dt < 8; ++dt)
 #pragma unroll
-            for (int i = 0; i < 4; ++i) t.o64[dt][i] = ldexp(t.o64[dt][i], shift);
+            for (int i = 0; i < 4; ++i) {
+                t.o64[dt][i] = ldexp(t.o64[dt][i], shift);
+                t.acc[dt][i] = ldexpf(t.acc[dt][i], shift);
+            }
         t.l64 = ldexp(t.l64, shift);
         t.m_run = m_new;
     }
@@ -550,12 +568,11 @@ __device__ __forceinline__ uint32_t pf_vt_addr(uint32_t lds_base, int dt, int la
     return lds_base + kOffV + vt_tr_offset(dt, lane);
 }
 
-// O^T[dim][query] += cv * the block's V^T P^T: per 16-dim tile, V^T (transpose reads) against
-// the two P parts of both 32-key windows in fp32, then scaled by the block's V scale cv (a
-// power of two) into the fp64 O; two tiles at a time, the next two tiles' operands requested
-// before the current two's products.
+// The group's fp32 sum += the block's V^T P^T: per 16-dim tile, V^T (transpose reads) against
+// the two P parts of both 32-key windows; two tiles at a time, the next two tiles' operands
+// requested before the current two's products.
 __device__ __forceinline__ void pf_pv(const uint32_t (&vaddr)[8], uint32_t voff, const uint32_t (&ph)[2][2][4],
-                                      double cv, PfTile& t) {
+                                      PfTile& t) {
     f16x8_t pb[2][2];
 #pragma unroll
     for (int w = 0; w < 2; ++w)
@@ -572,22 +589,14 @@ __device__ __forceinline__ void pf_pv(const uint32_t (&vaddr)[8], uint32_t voff,
             nxt[0] = pf_vt_issue(vaddr[d0 + 2] + voff);
             nxt[1] = pf_vt_issue(vaddr[d0 + 3] + voff);
         }
-        f32x4_t oacc[2];
-#pragma unroll
-        for (int e = 0; e < 2; ++e) oacc[e] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int w = 0; w < 2; ++w)
 #pragma unroll
-            for (int e = 0; e < 2; ++e) {
-                const f16x8_t av = pf_vt_operand(cur[e], w);
+            for (int s = 0; s < 2; ++s)
 #pragma unroll
-                for (int s = 0; s < 2; ++s)
-                    oacc[e] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, pb[w][s], oacc[e], 0, 0, 0);
-            }
-#pragma unroll
-        for (int e = 0; e < 2; ++e)
-#pragma unroll
-            for (int i = 0; i < 4; ++i) t.o64[d0 + e][i] = fma(static_cast<double>(oacc[e][i]), cv, t.o64[d0 + e][i]);
+                for (int e = 0; e < 2; ++e)
+                    t.acc[d0 + e] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pf_vt_operand(cur[e], w), pb[w][s],
+                                                                           t.acc[d0 + e], 0, 0, 0);
         if (d0 + 2 < 8) {
             cur[0] = nxt[0];
             cur[1] = nxt[1];
@@ -599,19 +608,20 @@ __device__ __forceinline__ void pf_pv(const uint32_t (&vaddr)[8], uint32_t voff,
 // grown) interleaved with the scores of the next block from K buffer `kplane` (kNext: there
 // is one; kNew: it holds chunk keys).
 template <bool kNext, bool kNew>
-__device__ __forceinline__ void pf_probs_and_next(const f32x4_t (&scur)[4], float mult, const uint8_t* kplane,
-                                                  const f16x8_t (&qop)[2][4], int n, int g, PfTile& t,
-                                                  uint32_t (&ph)[2][2][4], f32x4_t (&snext)[4]) {
+__device__ __forceinline__ void pf_probs_and_next(const f32x4_t (&scur)[4], float mult, float vshift,
+                                                  const uint8_t* kplane, const f16x8_t (&qop)[2][4], int n, int g,
+                                                  PfTile& t, uint32_t (&ph)[2][2][4], f32x4_t (&snext)[4]) {
 #pragma unroll
     for (int kt = 0; kt < 4; ++kt) snext[kt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
     float lsum = 0.f;
-    const float off = static_cast<float>(kPScaleExp) - t.m_run;
+    // p carries 2^vshift more (the group's V scale over this block's, |vshift| <= 3); l does not
+    const float off = static_cast<float>(kPScaleExp) - t.m_run + vshift;
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
         if (kNext) pf_qk_slice<kNew>(kplane, qop, q, n, g, snext);
         pf_probs_tile16(scur[q], mult, off, lsum, ph, q);
     }
-    t.l64 += static_cast<double>(lsum);
+    t.l64 += ldexp(static_cast<double>(lsum), -static_cast<int>(vshift));
 }
 
 __global__ __launch_bounds__(kPfThreads) void prefill_attn_kernel(PrefillArgs a) {
@@ -774,11 +784,21 @@ __global__ __launch_bounds__(kPfThreads) void prefill_attn_kernel(PrefillArgs a)
 
     PfTile tl;
 #pragma unroll
-    for (int dt = 0; dt < 8; ++dt)
+    for (int dt = 0; dt < 8; ++dt) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) tl.o64[dt][i] = 0.0;
+        tl.acc[dt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    }
     tl.l64 = 0.0;
     tl.m_run = -INFINITY;
+    // The open group: blocks summed into tl.acc so far and their V scale exponent.  A block
+    // whose V scale differs from the group's by more than 3 (its P would leave fp16's range
+    // or its precision) closes the group first.  A block holding chunk keys is summed alone:
+    // its scales depend on rows that later tokens see and this token does not, and within a
+    // group a different scale would change how the other blocks' terms round, so this
+    // token's output would depend on keys its mask hides.  Alone, its sum only scales by a
+    // power of two.
+    int grp_n = 0, grp_sv = 0;
 
     // Raw scores carry 2^(sq + sk): mult = 2^-sq * 2^-sk(block) turns them into log2 units.
     // (Kept at least 2^-126: a smaller factor means scores below ~2^-90, all p = 1 either way,
@@ -786,9 +806,7 @@ __global__ __launch_bounds__(kPfThreads) void prefill_attn_kernel(PrefillArgs a)
     auto blk_mult = [&](uint32_t w) {
         return fmaxf(cq * pow2f(-static_cast<int>(static_cast<int8_t>(w & 0xffu))), 1.17549435e-38f);
     };
-    auto blk_cv = [&](uint32_t w) {
-        return static_cast<double>(pow2f(-static_cast<int>(static_cast<int8_t>((w >> 8) & 0xffu))));
-    };
+    auto blk_sv = [&](uint32_t w) { return static_cast<int>(static_cast<int8_t>((w >> 8) & 0xffu)); };
 
     // Block 0's scores.  The barrier after them frees K buffer 0 for block 2.
     __builtin_amdgcn_s_waitcnt(0x0F70);    // vmcnt(0)
@@ -819,6 +837,16 @@ __global__ __launch_bounds__(kPfThreads) void prefill_attn_kernel(PrefillArgs a)
         const uint32_t w_next = blk + 1 < n_blk ? sw_at(blk + 1) : w_cur;
         unsafe |= w_next;
 
+        const int sv = blk_sv(w_cur);
+        const bool solo = blk_new(blk);
+        if (grp_n == kPfGroup || (grp_n > 0 && (solo || abs(grp_sv - sv) > 3))) {
+            pf_flush(tl, static_cast<double>(pow2f(-grp_sv)));
+            grp_n = 0;
+        }
+        if (grp_n == 0) grp_sv = sv;
+        grp_n = solo ? kPfGroup : grp_n + 1;
+        const float vshift = static_cast<float>(grp_sv - sv);
+
         uint32_t ph[2][2][4];
         f32x4_t snext[4];
         const uint8_t* knext = lds + kOffK + ((blk + 1) & 1) * kPlaneB;
@@ -826,11 +854,11 @@ __global__ __launch_bounds__(kPfThreads) void prefill_attn_kernel(PrefillArgs a)
         // issue priority over the other's V^T P^T.
         __builtin_amdgcn_s_setprio(1);
         if (blk + 1 >= n_blk)
-            pf_probs_and_next<false, false>(scur, mult_cur, knext, qop, n, g, tl, ph, snext);
+            pf_probs_and_next<false, false>(scur, mult_cur, vshift, knext, qop, n, g, tl, ph, snext);
         else if (blk_new(blk + 1))
-            pf_probs_and_next<true, true>(scur, mult_cur, knext, qop, n, g, tl, ph, snext);
+            pf_probs_and_next<true, true>(scur, mult_cur, vshift, knext, qop, n, g, tl, ph, snext);
         else
-            pf_probs_and_next<true, false>(scur, mult_cur, knext, qop, n, g, tl, ph, snext);
+            pf_probs_and_next<true, false>(scur, mult_cur, vshift, knext, qop, n, g, tl, ph, snext);
         __builtin_amdgcn_s_setprio(0);
 
         // The next block's running max is found before this block's V^T P^T (which still
@@ -840,7 +868,7 @@ __global__ __launch_bounds__(kPfThreads) void prefill_attn_kernel(PrefillArgs a)
         if (blk + 1 < n_blk)
             m_next = pf_next_max(snext, blk_diag(blk + 1), (blk + 1) * kPfBlk, g, pos_n, tl.m_run, mult_next);
 
-        pf_pv(vaddr, (blk & 1) * kPlaneB, ph, blk_cv(w_cur), tl);
+        pf_pv(vaddr, (blk & 1) * kPlaneB, ph, tl);
 
         pf_rescale(tl, m_next);
 #pragma unroll
@@ -852,6 +880,7 @@ __global__ __launch_bounds__(kPfThreads) void prefill_attn_kernel(PrefillArgs a)
         __builtin_amdgcn_s_waitcnt(0x0F70);    // vmcnt(0)
         __syncthreads();
     }
+    pf_flush(tl, static_cast<double>(pow2f(-grp_sv)));
 
     double l = tl.l64 + __shfl_xor(tl.l64, 16);
     l += __shfl_xor(l, 32);

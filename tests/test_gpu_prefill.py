@@ -74,6 +74,35 @@ def test_prefill_small_all_rows(dev, batch, n_new, starts, seed):
         assert (kc[b, :, s + n_new:] == to_codes(k[b, :, s + n_new:])).all()
 
 
+@pytest.mark.parametrize("case", ["k_row_2^-10", "k_row_2^-14", "v_row_2^-14", "v_head_2^110",
+                                  "k_head_2^-110", "q_head_2^100"])
+def test_prefill_staging_ranges(dev, case):
+    """The attention kernel reads K/V staged in fp16 with one power-of-two scale per
+    64-position block.  Rows scaled far from the rest of their block, blocks whose scale
+    leaves the fp32 range, and Q rows beyond it are sent to the fp64 rescore (a row 2^-10
+    below its block stays on the fp16 path); every row still meets 64 ULP."""
+    starts = [100, 61]
+    q, kn, vn, k, v = _chunk(2, 40, 150, starts, 21)
+    f = {"k_row_2^-10": 2.0 ** -10, "k_row_2^-14": 2.0 ** -14, "v_row_2^-14": 2.0 ** -14,
+         "v_head_2^110": 2.0 ** 110, "k_head_2^-110": 2.0 ** -110, "q_head_2^100": 2.0 ** 100}[case]
+    if case.startswith("k_row"):
+        k[0, 2, 10:13] = (k[0, 2, 10:13].float() * f).to(torch.bfloat16)      # cached rows of block 0
+        kn[1, 5, 3] = (kn[1, 5, 3].float() * f).to(torch.bfloat16)            # a chunk row
+    elif case.startswith("v_row"):
+        v[1, 6, 30:32] = (v[1, 6, 30:32].float() * f).to(torch.bfloat16)
+    elif case.startswith("v_head"):
+        v[0, 1, :100] = (v[0, 1, :100].float() * f).to(torch.bfloat16)
+        vn[0, :, 1] = (vn[0, :, 1].float() * f).to(torch.bfloat16)
+    elif case.startswith("k_head"):
+        k[1, 4, :61] = (k[1, 4, :61].float() * f).to(torch.bfloat16)
+        kn[1, :, 4] = (kn[1, :, 4].float() * f).to(torch.bfloat16)
+    else:
+        q[0, :, 9] = (q[0, :, 9].float() * f).to(torch.bfloat16)
+    want = _oracle(q, kn, vn, k, v, starts)
+    got, _, _ = _run(q, kn, vn, k, v, starts, dev)
+    assert_within_ulp(want.reshape(-1, 128), got.reshape(-1, 128), 64, f"staging {case}")
+
+
 def test_prefill_no_rope(dev):
     starts = [70, 150]
     q, kn, vn, k, v = _chunk(2, 33, 200, starts, 5)
