@@ -415,12 +415,28 @@ __device__ __forceinline__ void mt_issue_plane(const char* seg, int64_t row_byte
 
 // Running state of a piece in lane (g, n): O^T[16dt + 4g + i][column n] in fp64, the
 // lane's share of the column's sum, and the column's running max (log2 units, integer-
-// valued; -inf until the piece has seen a key the column may attend to).
+// valued; -inf until the piece has seen a key the column may attend to).  V^T P^T of the
+// windows since the last kMtGroup boundary is summed in fp32 (acc) and then moved into the
+// fp64 O: fp32 sums over 128 keys add no error measurable against per-window sums, and
+// the move costs two VALU instructions per element.
+constexpr int kMtGroup = 4;
 struct MtState {
     double o64[8][4];
+    f32x4_t acc[8];
     double l64;
     float m_run;
+    int grp;                  // windows summed into acc
 };
+
+__device__ __forceinline__ void mt_flush(MtState& t) {
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) t.o64[dt][i] += static_cast<double>(t.acc[dt][i]);
+        t.acc[dt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    }
+    t.grp = 0;
+}
 
 // The stages of one 32-key window [key0, key0 + 32) of a piece ending at k_b, for this
 // wave's tile.  mt_qk: the raw scores S^T = K Q^T of both 16-key tiles from the K plane.
@@ -491,7 +507,10 @@ __device__ __forceinline__ float mt_max(const PrefillArgs& a, bool chunk_keys, c
 #pragma unroll
         for (int dt = 0; dt < 8; ++dt)
 #pragma unroll
-            for (int i = 0; i < 4; ++i) t.o64[dt][i] = ldexp(t.o64[dt][i], shift);
+            for (int i = 0; i < 4; ++i) {
+                t.o64[dt][i] = ldexp(t.o64[dt][i], shift);
+                t.acc[dt][i] = ldexpf(t.acc[dt][i], shift);
+            }
         t.l64 = ldexp(t.l64, shift);
         t.m_run = m_new;
     }
@@ -509,8 +528,8 @@ __device__ __forceinline__ void mt_probs(const f32x4_t (&sacc)[2], float m_eff, 
 
 // mt_pv: once this window's V has landed (nv = planes of this wave's copies, kC
 // instructions each, younger than it) and every wave may read it, O^T += V^T P^T: dim
-// tile dt from two transposed reads (rows 4g + a/4 and 16 rows on), fp32 products added
-// into the fp64 O.
+// tile dt from two transposed reads (rows 4g + a/4 and 16 rows on), summed in fp32 into
+// the group's acc, which every kMtGroup windows moves into the fp64 O.
 template <int kC>
 __device__ __forceinline__ void mt_pv(uint32_t vbase, const uint32_t (&ph)[3][2][4], int nv, int lane, MtState& t) {
     mt_wait_planes<kC>(nv);
@@ -528,7 +547,7 @@ __device__ __forceinline__ void mt_pv(uint32_t vbase, const uint32_t (&ph)[3][2]
             asm volatile("ds_read_b64_tr_b16 %0, %1 offset:4096" : "=v"(r[e][1]) : "v"(ad));
         }
         asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(r[0][0]), "+v"(r[0][1]), "+v"(r[1][0]), "+v"(r[1][1]));
-        f32x4_t oacc[2];
+        bf16x8_t av[2];
 #pragma unroll
         for (int e = 0; e < 2; ++e) {
             union {
@@ -537,15 +556,15 @@ __device__ __forceinline__ void mt_pv(uint32_t vbase, const uint32_t (&ph)[3][2]
             } u;
             u.h[0] = r[e][0];
             u.h[1] = r[e][1];
-            oacc[e] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-            for (int s = 0; s < 3; ++s) oacc[e] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(u.v, pb[s], oacc[e], 0, 0, 0);
+            av[e] = u.v;
         }
 #pragma unroll
-        for (int e = 0; e < 2; ++e)
+        for (int s = 0; s < 3; ++s)
 #pragma unroll
-            for (int i = 0; i < 4; ++i) t.o64[d0 + e][i] += static_cast<double>(oacc[e][i]);
+            for (int e = 0; e < 2; ++e)
+                t.acc[d0 + e] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av[e], pb[s], t.acc[d0 + e], 0, 0, 0);
     }
+    if (++t.grp == kMtGroup) mt_flush(t);
 }
 
 // End of a piece: the column sums over the four rows; a whole segment writes its output
@@ -669,7 +688,9 @@ __device__ __forceinline__ void mt_advance(const PrefillArgs& a, MtCursor& c, in
 }
 
 template <int kW>
-__global__ __launch_bounds__(kWave * kW) __attribute__((amdgpu_waves_per_eu(1))) void mt_stream_kernel(PrefillArgs a) {
+// Two- and four-tile workgroups run two waves per SIMD: their registers (VGPRs and AGPRs
+// together) must fit in half the SIMD's file.
+__global__ __launch_bounds__(kWave * kW) __attribute__((amdgpu_waves_per_eu(kW == 1 ? 1 : 2))) void mt_stream_kernel(PrefillArgs a) {
     constexpr int kA = mt_ahead(kW);
     constexpr int kS = mt_slots(kW);
     constexpr int kC = kMtCopies / kW;
@@ -771,11 +792,14 @@ __global__ __launch_bounds__(kWave * kW) __attribute__((amdgpu_waves_per_eu(1)))
         const int lim = st + min(4 * wv + (n >> 2), a.n_new - 1);
         MtState t;
 #pragma unroll
-        for (int dt = 0; dt < 8; ++dt)
+        for (int dt = 0; dt < 8; ++dt) {
 #pragma unroll
             for (int i = 0; i < 4; ++i) t.o64[dt][i] = 0.0;
+            t.acc[dt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+        }
         t.l64 = 0.0;
         t.m_run = -INFINITY;
+        t.grp = 0;
 
         // Each window's scores are formed one window ahead, their MFMAs beside the current
         // window's probabilities (the next window's K plane is in LDS: K runs kA + 1 windows
@@ -819,6 +843,7 @@ __global__ __launch_bounds__(kWave * kW) __attribute__((amdgpu_waves_per_eu(1)))
             if (!has_next) break;
             c.kw += kMtWin;
         }
+        mt_flush(t);
         mt_piece_end<kW>(a, c.b, c.kvh, c.pk == 0 && c.k_b == c.nk, wg + seg, wv, lane, t);
         mt_advance(a, c, x_end, lead);
         if (!c.valid) break;
