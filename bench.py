@@ -62,6 +62,8 @@ MFMA_BF16_PEAK_TFLOPS = 2500.0
 TRAFFIC_FILES = {
     "decode_b64_ragged_512_8192": ROOT / "profiles" / "decode_stream_b64_ragged_traffic.txt",
     "multitoken_b64_ragged_512_8192_t4": ROOT / "profiles" / "mt_stream_b64_ragged_t4_traffic.txt",
+    "multitoken_b64_ragged_512_8192_t8": ROOT / "profiles" / "mt_stream_b64_ragged_t8_traffic.txt",
+    "multitoken_b64_ragged_512_8192_t16": ROOT / "profiles" / "mt_stream_b64_ragged_t16_traffic.txt",
 }
 
 
