@@ -144,11 +144,12 @@ struct PrefillArgs {
 };
 
 // Rescore: an output row is recomputed in fp64 when one of its elements lies closer to zero
-// than kRsFlagRatio times the row's rms.  The largest error measured on the MFMA paths is
-// 8.6e-7 of the row's rms (4.8M outputs of N(0,1) inputs, about 5.6 standard deviations
-// of a Gaussian error), so a 64-BF16-ULP miss, which needs an error of a quarter of the
-// element, cannot occur above ~4e-6 of the rms; 2^-17 = 7.6e-6 leaves a margin of 1.7
-// over the 6.4-sigma error of 10^9 outputs.  Squared: min^2 * 128 < ratio^2 * sum x^2.
+// than kRsFlagRatio times the row's rms.  The largest error measured on the MFMA paths (the
+// excess over the output's own BF16 rounding) is 8.6e-7 of the row's rms with three BF16
+// parts (4.8M outputs of N(0,1) inputs) and 8.9e-7 and 1.18e-6 with the prefill kernel's two
+// fp16 parts (two draws of 2.1M outputs), so a 64-BF16-ULP miss, which needs an error of a
+// quarter of the element, needs an element below ~4.7e-6 of the rms; 2^-17 = 7.6e-6 flags
+// those with a margin of 1.6.  Squared: min^2 * 128 < ratio^2 * sum x^2.
 constexpr double kRsFlagRatio2 = 1.0 / 17179869184.0;    // (2^-17)^2
 constexpr int kRsSlots = 1024;                            // partial slots (rows x pieces)
 constexpr int kRsMaxPieces = 32;                          // pieces per row at most
