@@ -63,17 +63,6 @@ int32_t stream_wgs() {
     return device_stream_wgs();
 }
 
-// Fused stream launch (contiguous cache, past the single-launch size, at most
-// kFusedMaxBatch sequences), chosen with GQA_DECODE_FUSED=1: one launch per call instead
-// of three.  It is not the default: on B=64 ragged 512..8192 its call takes about 6 %
-// longer than the three launches (the in-kernel plan, Q operands and end-of-range merge
-// cost more than the two launches they remove).
-bool use_fused(int32_t batch) {
-    if (batch > kFusedMaxBatch) return false;
-    const char* s = std::getenv("GQA_DECODE_FUSED");
-    return s && s[0] == '1';
-}
-
 // Chunks of at most kMultiMaxNew new tokens take the multi-token path (stream-K over the
 // keys, prefill arithmetic); GQA_PREFILL_MULTI=0 in the environment sends them through the
 // prefill attention kernel instead.
@@ -162,7 +151,6 @@ DecodePlan plan_decode(int32_t batch, int32_t capacity, bool paged, int64_t max_
         plan.pieces_cap = static_cast<int32_t>((capacity + pk - 1) / pk);
         plan.n_slots = static_cast<int64_t>(batch) * kHkv * plan.pieces_cap;
     } else {
-        plan.fused = !paged && use_fused(batch);
         plan.n_slots = static_cast<int64_t>(plan.n_wgs) + static_cast<int64_t>(kHkv) * batch;
         plan.q_op_bytes = static_cast<size_t>(batch) * kHkv * kGroup * kD * sizeof(double);
         plan.plan_bytes = 256 + align_up((static_cast<size_t>(batch) + 1) * sizeof(int64_t), 256) +
@@ -284,7 +272,6 @@ int decode_launch(const DecodePlan& plan, const gqa_params_t* params, const uint
     a.seq_nreal = reinterpret_cast<int32_t*>(pl + 256 + align_up((static_cast<size_t>(batch) + 1) * sizeof(int64_t), 256));
     a.seg_count = counters ? counters : reinterpret_cast<unsigned long long*>(pl + plan.plan_bytes);
     a.pieces_cap = plan.pieces_cap;
-    a.fused = plan.fused;
     a.piece_keys = plan.piece_keys;
     a.block_table = block_table;
     a.max_blocks = max_blocks;

@@ -27,10 +27,8 @@
 //
 // Other launch shapes of the same step: decode_single_kernel (small batches: one launch,
 // one 4-wave workgroup per piece of a segment, the last piece of a segment to finish
-// merges it after an agent-scope counter), decode_fused_kernel (opt-in, batches up to kFusedMaxBatch: the
-// stream kernel planning its own range and forming its own Q operands, split segments
-// merged in-kernel the same way) and decode_paged_stream_kernel (the stream kernel over
-// a block-table cache).
+// merges it after an agent-scope counter) and decode_paged_stream_kernel (the stream
+// kernel over a block-table cache).
 //
 // Arithmetic (the golden model is double, pyfiles/gen_gqa_wrapper_vectors.py:121-139):
 // every step is carried in fp64, so the output differs from the golden's double value by
@@ -67,7 +65,6 @@
 namespace gqa {
 
 constexpr int kChunk = 16;           // keys per MFMA group
-constexpr int kFusedWindows = kFusedMaxBatch / kWave;
 
 __device__ __forceinline__ int seq_valid_keys(const DecodeArgs& a, int b) {
     const int L = a.seq_len[b];
@@ -370,42 +367,6 @@ __device__ __forceinline__ double2 load_agent_d2(const double* p) {
                         __longlong_as_double(__hip_atomic_load(q + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)));
 }
 
-// write_partial with agent-scope stores, for a partial merged inside the same launch.
-__device__ __forceinline__ void publish_partial(const DecodeArgs& a, int64_t slot, const PieceState& st,
-                                                double l_tot) {
-    const int lane = threadIdx.x & (kWave - 1);
-    unsigned long long* dst = reinterpret_cast<unsigned long long*>(a.part_o + slot * kGroup * kD + lane_row_offset());
-#pragma unroll
-    for (int e = 0; e < 8; ++e) store_agent(dst + e, st.acc[e]);
-    if (lane < kGroup)
-        store_agent(reinterpret_cast<unsigned long long*>(a.part_ml + slot * kGroup + lane),
-                    make_float2(st.m_run, static_cast<float>(l_tot)));
-}
-
-// A partial held in LDS until the end of the workgroup's range (fused kernel).
-struct PartialStage {
-    double o[kGroup][kD];
-    float2 ml[kGroup];
-};
-
-__device__ __forceinline__ void stage_partial(PartialStage& s, const PieceState& st, double l_tot) {
-    const int lane = threadIdx.x & (kWave - 1);
-#pragma unroll
-    for (int e = 0; e < 8; ++e) (&s.o[0][0])[lane_row_offset() + e] = st.acc[e];
-    if (lane < kGroup) s.ml[lane] = make_float2(st.m_run, static_cast<float>(l_tot));
-}
-
-// publish_partial of a staged partial: lane l writes dims [8(l%16), 8(l%16) + 8) of head l/16.
-__device__ __forceinline__ void publish_staged(const DecodeArgs& a, int64_t slot, const PartialStage& s) {
-    const int lane = threadIdx.x & (kWave - 1);
-    const int hh = lane >> 4;
-    const int c = lane & 15;
-    unsigned long long* dst = reinterpret_cast<unsigned long long*>(a.part_o + (slot * kGroup + hh) * kD + 8 * c);
-#pragma unroll
-    for (int j = 0; j < 8; ++j) store_agent(dst + j, s.o[hh][8 * c + j]);
-    if (lane < kGroup) store_agent(reinterpret_cast<unsigned long long*>(a.part_ml + slot * kGroup + lane), s.ml[lane]);
-}
-
 // Wait until every memory access this wave has issued has completed (s_waitcnt vmcnt(0)).
 // A workgroup-scope release fence does not wait for global stores on gfx950, so a
 // partial's stores are waited for explicitly before the counter that announces them.
@@ -621,11 +582,11 @@ __device__ __forceinline__ void load_q_operands(const DecodeArgs& a, int b, int 
 // at a piece boundary.  Writes the output rows itself when the piece is the whole
 // segment; otherwise leaves a partial for the merge kernel.  (Requesting the next piece's
 // second chunk too, before this piece's end work, measured 1 % slower on long segments.)
-template <bool kRopeK, bool kFused = false>
-__device__ __forceinline__ bool process_piece(const DecodeArgs& a, int b, int kvh, int nv, int k_a,
+template <bool kRopeK>
+__device__ __forceinline__ void process_piece(const DecodeArgs& a, int b, int kvh, int nv, int k_a,
                                               int k_b, int64_t wg, PieceRows& cur,
                                               const PieceRows& nxt, Chunk& c0, Chunk& c1,
-                                              const QOps& qa, PartialStage* stage = nullptr) {
+                                              const QOps& qa) {
     const uint32_t step = kChunk * static_cast<uint32_t>(a.kv_pos_stride) * 2u;
 
     PieceState st;
@@ -648,21 +609,9 @@ __device__ __forceinline__ bool process_piece(const DecodeArgs& a, int b, int kv
     finish_piece(st, l_tot);
     if (k_a == 0 && k_b == nv) {
         write_rows(a, b, kvh, st, l_tot);      // the whole segment
-        return false;
-    }
-    if (kFused) {
-        // A split piece of the fused kernel: kept in LDS while more pieces follow (agent-scope
-        // stores issued now would hold up every later load of the wave: the memory counter
-        // retires in order, and these stores complete only once written through to memory),
-        // else published at once (nothing follows).
-        if (stage)
-            stage_partial(*stage, st, l_tot);
-        else
-            publish_partial(a, wg + static_cast<int64_t>(b) * kHkv + kvh, st, l_tot);
-        return true;
+        return;
     }
     write_partial(a, wg + static_cast<int64_t>(b) * kHkv + kvh, st, l_tot);
-    return false;
 }
 // Per-sequence key offsets for 64 sequences at a time, one per lane: o = seq_off[base +
 // lane], o1 = seq_off[base + lane + 1] (the segments of sequence b hold keys [o, o1)).
@@ -670,7 +619,6 @@ struct SeqWindow {
     int base;
     int64_t o;
     int64_t o1;
-    int64_t carry;    // scanned windows: keys (per segment) of the sequences before base + 64
     int nreal;        // planned windows: keys that count (less than o1 - o for a paged cache)
     int lead;         // stream positions before each segment's first key (uniform)
 };
@@ -683,33 +631,9 @@ __device__ __forceinline__ void load_seq_window(const DecodeArgs& a, int base, S
     sw.nreal = bb < a.batch ? a.seq_nreal[bb] : 0;
 }
 
-// The same window computed from the lengths (the fused kernel has no plan in memory):
-// an inclusive scan of the window's segment spans on top of `carry`, the span of the
-// sequences before `base`.
-__device__ __forceinline__ void scan_seq_window(const DecodeArgs& a, int base, int64_t carry, SeqWindow& sw) {
-    const int lane = static_cast<int>(threadIdx.x & (kWave - 1));
-    const int bb = base + lane;
-    const int span = bb < a.batch ? plan_span(a, bb, sw.lead) : 0;
-    const int64_t incl = wave_incl_scan_i64(span, lane) + carry;
-    sw.base = base;
-    sw.o = bb < a.batch ? (incl - span) * kHkv : INT64_MAX;
-    sw.o1 = bb < a.batch ? incl * kHkv : INT64_MAX;
-    sw.carry = __shfl(incl, kWave - 1);
-    sw.nreal = bb < a.batch ? plan_keys(a, bb) : 0;
-}
-
-template <bool kScan>
-__device__ __forceinline__ void seq_window(const DecodeArgs& a, int base, int64_t carry, SeqWindow& sw) {
-    if (kScan)
-        scan_seq_window(a, base, carry, sw);
-    else
-        load_seq_window(a, base, sw);
-}
-
 // The segment after (b, kvh) that has keys: the next KV head of b, or KV head 0 of the
 // next sequence with keys.  Returns false when there is none (possible only if the
 // lengths changed while the kernel ran).
-template <bool kScan = false>
 __device__ __forceinline__ bool next_segment(const DecodeArgs& a, SeqWindow& sw, int& b, int& kvh,
                                              int& nv) {
     if (kvh + 1 < kHkv) {
@@ -727,7 +651,7 @@ __device__ __forceinline__ bool next_segment(const DecodeArgs& a, SeqWindow& sw,
             return true;
         }
         if (sw.base + kWave >= a.batch) return false;
-        seq_window<kScan>(a, sw.base + kWave, sw.carry, sw);
+        load_seq_window(a, sw.base + kWave, sw);
     }
 }
 
@@ -823,328 +747,6 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(1))) void
         advance(cur.rows, step);     // its first chunk is in c0 already
         qa = qa2;
     }
-}
-
-
-// ---------------------------------------------------------------------------------
-// Fused decode: the stream kernel with its plan, Q operands and merge done in-kernel, so a
-// call is one launch.  Each workgroup scans the lengths itself (a batch of at most
-// kFusedMaxBatch sequences is a few windows of 64), forms the Q operands of each piece
-// while that piece's first chunk is in flight, and the pieces of a split segment meet
-// through agent-scope partials and a per-segment counter: the last piece to finish
-// merges them in piece order and resets the counter.
-
-// Merge the n_pieces partials of segment (b, kvh) at slots slot0.. in piece order: lane
-// (head l/16, dims [8(l%16), 8(l%16) + 8)), exact power-of-two weights, fp64 sums, the
-// row rounded double -> f32 -> BF16.  A piece that saw no key (m = -inf) weighs 0.
-__device__ __forceinline__ void merge_segment(const DecodeArgs& a, int b, int kvh, int64_t slot0, int n_pieces) {
-    const int lane = threadIdx.x & (kWave - 1);
-    const int hh = lane >> 4;
-    const int c = lane & 15;
-    float m_all = -INFINITY;
-    for (int p0 = 0; p0 < n_pieces; p0 += 16) {
-        const int p = min(p0 + c, n_pieces - 1);
-        m_all = fmaxf(m_all, load_agent_f2(a.part_ml + (slot0 + p) * kGroup + hh).x);
-    }
-    m_all = fmaxf(m_all, __shfl_xor(m_all, 1));
-    m_all = fmaxf(m_all, __shfl_xor(m_all, 2));
-    m_all = fmaxf(m_all, __shfl_xor(m_all, 4));
-    m_all = fmaxf(m_all, __shfl_xor(m_all, 8));
-    double l = 0.0;
-    double o[8];
-#pragma unroll
-    for (int j = 0; j < 8; ++j) o[j] = 0.0;
-    for (int p0 = 0; p0 < n_pieces; p0 += 4) {
-        float2 ml[4];
-        double2 ov[4][4];
-#pragma unroll
-        for (int u = 0; u < 4; ++u) {
-            const int64_t slot = slot0 + min(p0 + u, n_pieces - 1);
-            ml[u] = load_agent_f2(a.part_ml + slot * kGroup + hh);
-#pragma unroll
-            for (int q = 0; q < 4; ++q) ov[u][q] = load_agent_d2(a.part_o + (slot * kGroup + hh) * kD + 8 * c + 2 * q);
-        }
-#pragma unroll
-        for (int u = 0; u < 4; ++u) {
-            if (p0 + u < n_pieces) {     // (uniform) copies of the last piece are skipped
-                const int e = ml[u].x == -INFINITY ? -1100 : static_cast<int>(ml[u].x - m_all);
-                l += ldexp(static_cast<double>(ml[u].y), e);
-#pragma unroll
-                for (int q = 0; q < 4; ++q) {
-                    o[2 * q] += ldexp(ov[u][q].x, e);
-                    o[2 * q + 1] += ldexp(ov[u][q].y, e);
-                }
-            }
-        }
-    }
-    uint16_t o8[8];
-#pragma unroll
-    for (int j = 0; j < 8; ++j) o8[j] = f32_to_bf16_rne(static_cast<float>(o[j] / l));
-    *reinterpret_cast<bf16x8_t*>(a.out + (static_cast<int64_t>(b) * kHq + kvh * kGroup + hh) * kD + 8 * c) =
-        pack8(o8);
-}
-
-// A split segment's piece whose partial is published: count it in (device-scope atomic on
-// the segment's counter; the partial's stores have completed before), and the last of
-// the segment's pieces merges and resets the counter.  A workgroup has at most two split
-// pieces, its first and its last; both are counted at its end, with one wait for the
-// stores and the two atomics in flight together, and when the segments it merges hold
-// at most kMergeBatch pieces in all, every partial is requested at once.
-struct SplitPiece {
-    int b, kvh, nv;
-    int64_t seg_off;        // < 0: none
-};
-
-constexpr int kMergeBatch = 8;
-
-__device__ __forceinline__ int count_pieces(int64_t seg_off, int nv, int64_t per_wg, int64_t& w_first) {
-    w_first = seg_off / per_wg;
-    return static_cast<int>((seg_off + nv - 1) / per_wg - w_first) + 1;
-}
-
-// Lane (head l/16, dims [8(l%16), 8(l%16) + 8)) of the merged row of a segment whose
-// partials, in piece order, are ml[u0 .. u0 + n) / ov[u0 .. u0 + n).
-__device__ __forceinline__ void store_merged(const DecodeArgs& a, int b, int kvh, const float2 (&ml)[kMergeBatch],
-                                             const double2 (&ov)[kMergeBatch][4], int u0, int n) {
-    const int lane = threadIdx.x & (kWave - 1);
-    const int hh = lane >> 4;
-    const int c = lane & 15;
-    float m_all = -INFINITY;
-#pragma unroll
-    for (int u = 0; u < kMergeBatch; ++u)
-        if (u >= u0 && u < u0 + n) m_all = fmaxf(m_all, ml[u].x);
-    double l = 0.0;
-    double o[8];
-#pragma unroll
-    for (int j = 0; j < 8; ++j) o[j] = 0.0;
-#pragma unroll
-    for (int u = 0; u < kMergeBatch; ++u) {
-        if (u >= u0 && u < u0 + n) {         // (uniform)
-            const int e = ml[u].x == -INFINITY ? -1100 : static_cast<int>(ml[u].x - m_all);
-            l += ldexp(static_cast<double>(ml[u].y), e);
-#pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                o[2 * q] += ldexp(ov[u][q].x, e);
-                o[2 * q + 1] += ldexp(ov[u][q].y, e);
-            }
-        }
-    }
-    uint16_t o8[8];
-#pragma unroll
-    for (int j = 0; j < 8; ++j) o8[j] = f32_to_bf16_rne(static_cast<float>(o[j] / l));
-    *reinterpret_cast<bf16x8_t*>(a.out + (static_cast<int64_t>(b) * kHq + kvh * kGroup + hh) * kD + 8 * c) =
-        pack8(o8);
-}
-
-__device__ __forceinline__ void finish_split_pieces(const DecodeArgs& a, const SplitPiece& p1, const SplitPiece& p2,
-                                                    int64_t per_wg) {
-    wait_vmem();                                   // the partials' stores have completed ...
-    __atomic_signal_fence(__ATOMIC_SEQ_CST);       // ... and the compiler keeps them before the count
-    const int lane = threadIdx.x & (kWave - 1);
-    int d1 = -1, d2 = -1;
-    if (lane == 0) {
-        if (p1.seg_off >= 0) d1 = static_cast<int>(atomicAdd(&a.seg_count[p1.b * kHkv + p1.kvh], 1ull));
-        if (p2.seg_off >= 0) d2 = static_cast<int>(atomicAdd(&a.seg_count[p2.b * kHkv + p2.kvh], 1ull));
-    }
-    d1 = __builtin_amdgcn_readfirstlane(d1);
-    d2 = __builtin_amdgcn_readfirstlane(d2);
-    __atomic_signal_fence(__ATOMIC_SEQ_CST);       // the merge's loads are not hoisted above the count
-    int64_t w1 = 0, w2 = 0;
-    const int n1 = p1.seg_off >= 0 ? count_pieces(p1.seg_off, p1.nv, per_wg, w1) : 0;
-    const int n2 = p2.seg_off >= 0 ? count_pieces(p2.seg_off, p2.nv, per_wg, w2) : 0;
-    const bool m1 = p1.seg_off >= 0 && d1 == n1 - 1;
-    const bool m2 = p2.seg_off >= 0 && d2 == n2 - 1;
-    if (!m1 && !m2) return;
-    const int seg1 = p1.b * kHkv + p1.kvh;
-    const int seg2 = p2.b * kHkv + p2.kvh;
-    if (lane == 0) {
-        if (m1) __hip_atomic_store(&a.seg_count[seg1], 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        if (m2) __hip_atomic_store(&a.seg_count[seg2], 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
-    const int k1 = m1 ? n1 : 0;
-    const int k2 = m2 ? n2 : 0;
-    if (k1 + k2 > kMergeBatch) {
-        if (m1) merge_segment(a, p1.b, p1.kvh, w1 + seg1, n1);
-        if (m2) merge_segment(a, p2.b, p2.kvh, w2 + seg2, n2);
-        return;
-    }
-    // One batch: slots of segment 1's pieces, then segment 2's (unused entries repeat a
-    // slot of the batch and are not read back).
-    const int hh = lane >> 4;
-    const int c = lane & 15;
-    float2 ml[kMergeBatch];
-    double2 ov[kMergeBatch][4];
-#pragma unroll
-    for (int u = 0; u < kMergeBatch; ++u) {
-        const int64_t slot = u < k1   ? w1 + seg1 + u
-                             : k2 > 0 ? w2 + seg2 + min(u - k1, k2 - 1)
-                                      : w1 + seg1 + (k1 - 1);
-        ml[u] = load_agent_f2(a.part_ml + slot * kGroup + hh);
-#pragma unroll
-        for (int q = 0; q < 4; ++q) ov[u][q] = load_agent_d2(a.part_o + (slot * kGroup + hh) * kD + 8 * c + 2 * q);
-    }
-    if (m1) store_merged(a, p1.b, p1.kvh, ml, ov, 0, k1);
-    if (m2) store_merged(a, p2.b, p2.kvh, ml, ov, k1, k2);
-}
-
-__device__ __forceinline__ void write_nan_rows(const DecodeArgs& a, int b) {
-    uint4* out = reinterpret_cast<uint4*>(a.out + static_cast<int64_t>(b) * kHq * kD);
-    for (int i = threadIdx.x & (kWave - 1); i < kHq * kD / 8; i += kWave)
-        out[i] = make_uint4(0x7fc07fc0u, 0x7fc07fc0u, 0x7fc07fc0u, 0x7fc07fc0u);
-}
-
-// Rows of sequences whose lengths break the rules: NaN, sequence b by workgroup b mod n_wgs
-// (nvw: per-segment keys of the batch, 64 sequences per window, 0 for such a sequence).
-__device__ __forceinline__ void write_nan_rows_of(const DecodeArgs& a, const int (&nvw)[kFusedWindows], int64_t w) {
-    const int lane = threadIdx.x & (kWave - 1);
-#pragma unroll
-    for (int k = 0; k < kFusedWindows; ++k) {
-        const int bb = kWave * k + lane;
-        uint64_t m = __ballot(bb < a.batch && nvw[k] == 0 && bb % a.n_wgs == w);
-        while (m) {
-            const int j = __ffsll(static_cast<unsigned long long>(m)) - 1;
-            m &= m - 1;
-            write_nan_rows(a, kWave * k + j);
-        }
-    }
-}
-
-template <bool kRopeQ, bool kRopeK>
-__global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(1))) void decode_fused_kernel(DecodeArgs a) {
-    __shared__ QStage qs;
-    __shared__ PartialStage first_part;
-    const int64_t w = blockIdx.x;
-    const int lane = threadIdx.x & (kWave - 1);
-
-    // The plan from the lengths, all requested at once (a batch of at most kFusedMaxBatch
-    // sequences: kFusedWindows windows of 64).
-    int nvw[kFusedWindows];
-#pragma unroll
-    for (int k = 0; k < kFusedWindows; ++k) {
-        const int bb = kWave * k + lane;
-        nvw[k] = bb < a.batch ? plan_keys(a, bb) : 0;
-    }
-    int64_t sum = 0;
-    int max_keys = 0, n_seq = 0;
-#pragma unroll
-    for (int k = 0; k < kFusedWindows; ++k) {
-        sum += wave_sum_i64(nvw[k]);
-        max_keys = max(max_keys, static_cast<int>(wave_max_i64(nvw[k])));
-        n_seq += static_cast<int>(wave_sum_i64(nvw[k] > 0 ? 1 : 0));
-    }
-    int lead;
-    int64_t total, per_wg;
-    plan_lead_totals(uniform_i64(sum), __builtin_amdgcn_readfirstlane(max_keys),
-                     __builtin_amdgcn_readfirstlane(n_seq), a.n_wgs, lead, total, per_wg);
-#pragma unroll
-    for (int k = 0; k < kFusedWindows; ++k) nvw[k] = nvw[k] > 0 ? nvw[k] + lead : 0;   // spans
-    int64_t x = w * per_wg;
-    if (x >= total) {
-        write_nan_rows_of(a, nvw, w);
-        return;
-    }
-    const int64_t x_end = min(x + per_wg, total);
-
-    // Start sequence b = the last b whose first segment starts at or before x.
-    SeqWindow sw;
-    int b = 0;
-    int64_t off = 0, next = 0, carry = 0;
-#pragma unroll
-    for (int k = 0; k < kFusedWindows; ++k) {
-        const int bb = kWave * k + lane;
-        const int64_t incl = wave_incl_scan_i64(nvw[k], lane) + carry;
-        SeqWindow t;
-        t.base = kWave * k;
-        t.o = bb < a.batch ? (incl - nvw[k]) * kHkv : INT64_MAX;
-        t.o1 = bb < a.batch ? incl * kHkv : INT64_MAX;
-        t.carry = __shfl(incl, kWave - 1);
-        carry = t.carry;
-        const uint64_t le = __ballot(t.o <= x);
-        if (le) {
-            const int j = 63 - __clzll(static_cast<long long>(le));
-            b = kWave * k + j;
-            off = __shfl(t.o, j);
-            next = __shfl(t.o1, j);
-            sw = t;
-        }
-    }
-    sw.lead = lead;
-    int kvh, key, nvb;
-    locate_first_piece(off, next, lead, x, kvh, key, nvb);
-    x = uniform_i64(x);
-    b = __builtin_amdgcn_readfirstlane(b);
-    kvh = __builtin_amdgcn_readfirstlane(kvh);
-    key = __builtin_amdgcn_readfirstlane(key);
-    nvb = __builtin_amdgcn_readfirstlane(nvb);
-    int k_b = __builtin_amdgcn_readfirstlane(
-        static_cast<int>(min(static_cast<int64_t>(nvb), key + (x_end - x))));
-
-    const uint32_t step = kChunk * static_cast<uint32_t>(a.kv_pos_stride) * 2u;
-    PieceRows cur;
-    piece_rows(a, b, kvh, key, k_b, cur);
-    Chunk c0, c1;
-    load_next(cur, step, c0);
-    QRope rope;
-    rope.qpos = -1;
-    rope.inv_freq = kRopeQ ? a.rope.inv_freq[lane] : 0.0;
-    rope.sn = 0.0;
-    rope.cs = 1.0;
-    QRaw raw;
-    load_q_raw(a, b, kvh, raw);
-    QOps qa;
-    build_q_operands<kRopeQ>(a, raw, rope, qs, qa);
-
-    SplitPiece first = {0, 0, 0, -1};
-    SplitPiece last = {0, 0, 0, -1};
-    while (true) {
-        const int64_t x_next = x + (k_b - key);      // as in decode_stream_kernel
-        int b2 = b, kvh2 = kvh, nv2 = nvb, key2 = k_b - 1, k_b2 = k_b;
-        bool more = x_next + lead < x_end;
-        if (more) {
-            more = next_segment<true>(a, sw, b2, kvh2, nv2);
-            b2 = __builtin_amdgcn_readfirstlane(b2);
-            kvh2 = __builtin_amdgcn_readfirstlane(kvh2);
-            nv2 = __builtin_amdgcn_readfirstlane(nv2);
-            key2 = 0;
-            k_b2 = __builtin_amdgcn_readfirstlane(
-                static_cast<int>(min(static_cast<int64_t>(nv2), x_end - x_next - lead)));
-        }
-        if (!more) {
-            b2 = b;
-            kvh2 = kvh;
-            nv2 = nvb;
-            key2 = k_b - 1;
-            k_b2 = k_b;
-        }
-        PieceRows nxt;
-        piece_rows(a, b2, kvh2, key2, k_b2, nxt);
-        load_q_raw(a, b2, kvh2, raw);              // the next piece's Q rows
-
-        if (process_piece<kRopeK, true>(a, b, kvh, nvb, key, k_b, w, cur, nxt, c0, c1, qa,
-                                        more ? &first_part : nullptr)) {
-            // a split piece: the range's first (more pieces follow) or its last
-            SplitPiece& sp = more ? first : last;
-            sp.b = b;
-            sp.kvh = kvh;
-            sp.nv = nvb;
-            sp.seg_off = x - key;
-        }
-        if (!more) break;
-        build_q_operands<kRopeQ>(a, raw, rope, qs, qa);   // while the next piece's first chunk is in flight
-
-        x = x_next + lead;
-        b = b2;
-        kvh = kvh2;
-        nvb = nv2;
-        key = key2;
-        k_b = k_b2;
-        cur = nxt;
-        advance(cur.rows, step);     // its first chunk is in c0 already
-    }
-    if (first.seg_off >= 0)
-        publish_staged(a, w + static_cast<int64_t>(first.b) * kHkv + first.kvh, first_part);
-    finish_split_pieces(a, first, last, per_wg);
-    write_nan_rows_of(a, nvw, w);
 }
 
 
@@ -2048,25 +1650,6 @@ hipError_t launch_decode(const DecodeArgs& a, int batch, hipStream_t stream, hip
             hipLaunchKernelGGL((decode_single_kernel<false, true>), grid, dim3(kSingleWaves * kWave), 0, stream, a);
         else
             hipLaunchKernelGGL((decode_single_kernel<false, false>), grid, dim3(kSingleWaves * kWave), 0, stream, a);
-        const hipError_t e = hipGetLastError();
-        if (ev) {
-            (void)hipEventRecord(ev[1], stream);
-            (void)hipEventRecord(ev[2], stream);
-        }
-        return e;
-    }
-    if (a.fused && !a.block_table) {
-        // One launch: plan, Q operands and merge inside the stream kernel.
-        if (ev) (void)hipEventRecord(ev[0], stream);
-        const dim3 grid(a.n_wgs);
-        if (rq && rk)
-            hipLaunchKernelGGL((decode_fused_kernel<true, true>), grid, dim3(kWave), 0, stream, a);
-        else if (rq)
-            hipLaunchKernelGGL((decode_fused_kernel<true, false>), grid, dim3(kWave), 0, stream, a);
-        else if (rk)
-            hipLaunchKernelGGL((decode_fused_kernel<false, true>), grid, dim3(kWave), 0, stream, a);
-        else
-            hipLaunchKernelGGL((decode_fused_kernel<false, false>), grid, dim3(kWave), 0, stream, a);
         const hipError_t e = hipGetLastError();
         if (ev) {
             (void)hipEventRecord(ev[1], stream);

@@ -8,9 +8,6 @@
 
 namespace gqa {
 
-// Largest batch of the fused decode launch (its workgroups hold every length in registers).
-constexpr int32_t kFusedMaxBatch = 256;
-
 // Everything one decode launch needs, passed by value as the kernel argument.
 struct DecodeArgs {
     const uint16_t* q;        // [B][32][128]
@@ -38,7 +35,6 @@ struct DecodeArgs {
     int32_t skew_pm;          // stream and paged kernels: XCD weighting of the ranges (per mille)
     int32_t pieces_cap;       // > 0: single-launch path, pieces per segment (grid x)
     int32_t piece_keys;       // single-launch path: keys per piece
-    int32_t fused;            // 1: one fused stream launch (plan, Q operands, merge in-kernel)
     double qk_scale_log2;     // scale * log2(e), folded into Q
     uint32_t flags;           // bit0 RoPE on Q, bit1 RoPE on K
     RopeTable rope;
@@ -49,7 +45,6 @@ struct DecodeArgs {
 struct DecodePlan {
     int32_t n_wgs;
     int32_t pieces_cap;       // > 0 selects the single-launch path
-    int32_t fused;            // 1 selects the fused stream kernel (contiguous cache)
     int32_t piece_keys;
     int64_t n_slots;          // stream path: n_wgs + 8 * batch; single path: 8 * batch * pieces_cap
     size_t part_o_bytes;      // fp64 partial outputs at offset 0

@@ -120,8 +120,7 @@ int gqa_decode_workspace_init(const gqa_params_t* params, int32_t batch, int32_t
  *              workspace must be ordered (same stream)
  * Batches whose caches hold at most 2^18 keys in all (batch * 8 * capacity) run as one
  * launch whose pieces merge in-kernel; larger ones as a prepare, a stream-K and a merge
- * launch, or, with GQA_DECODE_FUSED=1 in the environment and at most 256 sequences, as one
- * launch that plans, prepares and merges in-kernel.
+ * launch.
  * Key p of sequence b contributes iff p < seq_len[b] and p <= query_pos[b]
  * (gqa_attention_wrapper.v:279); rows outside that range are never read.
  * Lengths are read on the device: an entry violating the rules of

@@ -107,18 +107,15 @@ def test_deterministic(dev):
 
 
 @pytest.mark.parametrize("wgs", ["1", "7", "333", "2048", "6000"])
-@pytest.mark.parametrize("fused", ["0", "1"])
-def test_stream_partition_invariance(dev, wgs, fused, monkeypatch):
+def test_stream_partition_invariance(dev, wgs, monkeypatch):
     """The key space cut into 1 .. 6000 workgroup ranges (pieces start and end at
     arbitrary keys, ranges span several sequences and heads, up to 47 pieces per
-    segment): same parity, with the merge in its own kernel (fused=0) or inside the
-    stream launch (fused=1)."""
+    segment): same parity."""
     b = stimulus.decode_batch(5, 3000, min_len=1, max_len=3000, seed=9)
     monkeypatch.setenv("GQA_STREAM_WGS", wgs)
     monkeypatch.setenv("GQA_SINGLE_LAUNCH_MAX_KEYS", "0")       # the stream-K path
-    monkeypatch.setenv("GQA_DECODE_FUSED", fused)
     got = _run(b, dev)
-    assert_within_ulp(_oracle(b), got, 64, f"{wgs} workgroups, fused={fused}")
+    assert_within_ulp(_oracle(b), got, 64, f"{wgs} workgroups")
 
 
 @pytest.mark.parametrize("skew", ["0", "250"])
@@ -173,14 +170,11 @@ def test_single_launch_workspace_init_and_reuse(dev):
             assert np.array_equal(got, ref)
 
 
-@pytest.mark.parametrize("fused", ["0", "1"])
-def test_workspace_reuse_across_calls(dev, fused, monkeypatch):
+def test_workspace_reuse_across_calls(dev, monkeypatch):
     """A prepared call reuses one workspace: repeated calls give identical bits, and
-    the same workspace then serves other inputs (the fused launch leaves its segment
-    counters at zero for the next call)."""
+    the same workspace then serves other inputs."""
     from attention_accelerator_amd.attention import PreparedDecode
     monkeypatch.setenv("GQA_SINGLE_LAUNCH_MAX_KEYS", "0")
-    monkeypatch.setenv("GQA_DECODE_FUSED", fused)
     b = stimulus.decode_batch(6, 2500, min_len=1, max_len=2500, seed=17)
     ref = _run(b, dev)
     call = PreparedDecode(b.q.to(dev), b.k.to(dev), b.v.to(dev), b.query_pos.to(dev),
@@ -230,11 +224,10 @@ def test_device_resident_lengths(dev):
     assert np.array_equal(_codes(out), ref)
 
 
-@pytest.mark.parametrize("path", ["single", "three", "fused"])
+@pytest.mark.parametrize("path", ["single", "three"])
 def test_invalid_device_lengths_give_nan_rows(dev, path, monkeypatch):
     if path != "single":
         monkeypatch.setenv("GQA_SINGLE_LAUNCH_MAX_KEYS", "0")
-        monkeypatch.setenv("GQA_DECODE_FUSED", "1" if path == "fused" else "0")
     b = stimulus.decode_batch(3, 256, lengths=torch.tensor([100, 50, 200]), seed=15)
     qpos = torch.tensor([99, 50, 199], dtype=torch.int32)      # sequence 1: qpos == seq_len
     out = _codes(gqa.gqa_attention(b.q.to(dev), b.k.to(dev), b.v.to(dev), qpos.to(dev),
@@ -272,8 +265,7 @@ def test_batch64_ragged_512_8192(dev):
 def test_many_sequences(dev, bsz, hi, seed, monkeypatch):
     """Batches spanning many 64-sequence windows of the plan (300 sequences up to 600 keys;
     1000 sequences of 1..48 keys, many segments per workgroup range): every output against
-    the oracle, with and without the fused launch (which takes at most 256 sequences, so
-    B=300 and B=1000 stay on three launches either way).  N(0,1) V: with a few dozen keys
+    the oracle.  N(0,1) V: with a few dozen keys
     the outputs are sums of a few large terms, and 1 in ~10^6 of them cancels to within
     1e-7 of zero, where 64 BF16 ULP is an absolute error of a few 1e-8 -- scores carried
     in fp32 once missed it here (72 ULP); carried in fp64 they meet it."""
@@ -282,24 +274,7 @@ def test_many_sequences(dev, bsz, hi, seed, monkeypatch):
     monkeypatch.setenv("GQA_SINGLE_LAUNCH_MAX_KEYS", "0")
     got = _run(b, dev)
     assert_within_ulp(want, got, 64, f"B={bsz}", ref64=want64)
-    monkeypatch.setenv("GQA_DECODE_FUSED", "1")
     assert np.array_equal(_run(b, dev), got)
-
-
-def test_fused_launch_matches_three_kernels(dev, monkeypatch):
-    """B=64 ragged: the fused launch (plan, Q operands and merge in-kernel) and the
-    prepare/stream/merge kernels cut the keys into the same pieces and compute them
-    alike; only the order of the fp64 sum of l in a merge differs, so outputs agree to
-    1 BF16 ULP, and the fused launch is deterministic."""
-    b = stimulus.decode_batch(64, 8192, min_len=512, max_len=8192, seed=7,
-                              gen_device="cuda", device=dev)
-    monkeypatch.setenv("GQA_DECODE_FUSED", "0")
-    three = _codes(gqa.gqa_attention(b.q, b.k, b.v, b.query_pos, b.seq_len))
-    monkeypatch.setenv("GQA_DECODE_FUSED", "1")
-    fused = _codes(gqa.gqa_attention(b.q, b.k, b.v, b.query_pos, b.seq_len))
-    again = _codes(gqa.gqa_attention(b.q, b.k, b.v, b.query_pos, b.seq_len))
-    assert np.array_equal(fused, again)
-    assert_within_ulp(three, fused, 1, "fused vs three kernels")
 
 
 def test_long_context_131072(dev):

@@ -36,16 +36,15 @@ def _replays(q, graph_call, eager_call, n: int = 4):
         assert np.array_equal(got, want), f"replay {r} differs from the eager call"
 
 
-@pytest.mark.parametrize("path", ["single", "stream", "fused"])
+@pytest.mark.parametrize("path", ["single", "stream"])
 def test_decode_graph_replays(dev, monkeypatch, path):
-    """The three decode launch shapes: one launch (small batch), three launches (prepare,
-    stream, merge), one fused stream launch with its in-kernel merge counters (which each
-    call leaves at zero for the next)."""
+    """The two decode launch shapes: one launch with its in-kernel merge counters, which
+    each call leaves at zero for the next (small batch), and three launches (prepare,
+    stream, merge)."""
     if path == "single":
         b = stimulus.decode_batch(2, 400, min_len=50, max_len=400, seed=21, device=dev)
     else:
         monkeypatch.setenv("GQA_SINGLE_LAUNCH_MAX_KEYS", "0")
-        monkeypatch.setenv("GQA_DECODE_FUSED", "1" if path == "fused" else "0")
         b = stimulus.decode_batch(8, 3000, min_len=100, max_len=3000, seed=22, device=dev)
     sl = b.seq_len.to(dev).to(torch.int32)
     qpos = (sl - 1).contiguous()
