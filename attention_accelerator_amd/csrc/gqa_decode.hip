@@ -1257,15 +1257,20 @@ __global__ __launch_bounds__(kSingleWaves * kWave) void decode_single_kernel(Dec
 // accumulates p * V over its own keys for its 16 dims, and the 8 key slots are summed once
 // per piece.
 //
-// A persistent grid of one-wave workgroups takes (row, piece) pairs: every flagged row's
-// chunks are dealt to as many pieces as there are workgroups per row (at most
-// kRsMaxPieces), piece p taking chunks p, p + n_pieces, ..., so that the pieces share the
-// costlier chunk keys evenly.  A piece's partial row is published with agent-scope stores
-// and the row's last piece merges them, as in decode_single_kernel.  A row's result depends
-// on its keys and the piece count only, which follows from the number of flagged rows and
-// the grid, never from the order they were flagged in: results are bit-for-bit repeatable.
+// A persistent grid of one-wave workgroups takes (row, piece) pairs, piece p of a row taking
+// its chunks p, p + n_pieces, ..., so that the pieces share the costlier chunk keys evenly.
+// With at most 64 flagged rows (one per lane) every workgroup reads all of them and gives
+// each row pieces in proportion to its chunks (at least kRsMinChunks per piece, at most
+// kRsMaxPieces pieces): the longest row, which sets the kernel's time, gets the most.
+// With more rows each gets gridDim / rows pieces.  A piece's partial row is published with
+// agent-scope stores and the row's last piece merges them, as in decode_single_kernel.  A
+// row's result depends on its keys and its piece count only, which follows from the flagged
+// rows' key counts and the grid, never from the order they were flagged in: results are
+// bit-for-bit repeatable.
 
 constexpr int kRsKeys = 8;              // keys per rescore chunk (one per 8 lanes)
+constexpr int kRsMinChunks = 4;         // chunks per piece at least (proportional split)
+constexpr int kRsMergeBatch = 32;       // partials loaded at once by a row's merge
 
 // This lane's 16 dims of one K row and one V row (BF16): x dims 8c .. 8c+7, y dims 64 + 8c ..
 struct RsRows {
@@ -1485,16 +1490,56 @@ __global__ __launch_bounds__(kWave) void rescore_kernel(PrefillArgs a) {
     const uint32_t cap = static_cast<uint32_t>(a.batch) * static_cast<uint32_t>(T) * kHq;
     const uint32_t n_rows = min(a.rs_hdr[0], cap);
     if (n_rows == 0) return;
-    uint32_t n_pieces = gridDim.x / n_rows;      // gridDim.x <= kRsSlots
-    n_pieces = n_pieces < 1 ? 1 : n_pieces > kRsMaxPieces ? kRsMaxPieces : n_pieces;
-    const int np = static_cast<int>(n_pieces);
     const int lane = threadIdx.x;
     const int c = lane & 7;
-    const int64_t n_work = static_cast<int64_t>(n_rows) * n_pieces;
+    // The plan.  Proportional (n_rows <= 64): lane r holds row r, its pieces np_l and its
+    // first item first_l; items first_l .. first_l + np_l - 1 are its pieces, and its partial
+    // slots have the same numbers (the items stay below gridDim.x <= kRsSlots: the piece size
+    // is set for gridDim.x - n_rows pieces, and rounding up adds at most one per row).
+    // Uniform otherwise: n_pieces per row, row idx at items idx * n_pieces ...
+    const bool prop = n_rows <= static_cast<uint32_t>(kWave);
+    uint32_t row_l = 0;
+    int np_l = 0, first_l = 0;
+    int64_t n_work;
+    uint32_t n_pieces = 1;
+    if (prop) {
+        int nc = 0;
+        if (lane < static_cast<int>(n_rows)) {
+            row_l = a.rs_rows[lane];
+            const int64_t bt = row_l / kHq;
+            nc = (a.start[bt / T] + static_cast<int>(bt % T) + kRsKeys) / kRsKeys;   // ceil((start + t + 1) / 8)
+        }
+        const int64_t total = wave_sum_i64(nc);
+        const int64_t budget = max(static_cast<int64_t>(gridDim.x) - static_cast<int64_t>(n_rows), int64_t{1});
+        const int per = static_cast<int>(max((total + budget - 1) / budget, static_cast<int64_t>(kRsMinChunks)));
+        np_l = lane < static_cast<int>(n_rows) ? min(max((nc + per - 1) / per, 1), kRsMaxPieces) : 0;
+        const int incl = static_cast<int>(wave_incl_scan_i64(np_l, lane));
+        first_l = incl - np_l;
+        n_work = __shfl(incl, kWave - 1);
+    } else {
+        n_pieces = gridDim.x / n_rows;      // gridDim.x <= kRsSlots
+        n_pieces = n_pieces < 1 ? 1 : n_pieces > kRsMaxPieces ? kRsMaxPieces : n_pieces;
+        n_work = static_cast<int64_t>(n_rows) * n_pieces;
+    }
     for (int64_t wk = blockIdx.x; wk < n_work; wk += gridDim.x) {
-        const uint32_t idx = static_cast<uint32_t>(wk / n_pieces);
-        const int piece = static_cast<int>(wk % n_pieces);
-        const uint32_t row = a.rs_rows[idx];
+        uint32_t idx, row;
+        int piece, np;
+        int64_t slot0;
+        if (prop) {
+            const uint64_t m = __ballot(lane < static_cast<int>(n_rows) && first_l <= wk);
+            const int r = 63 - __clzll(static_cast<long long>(m));
+            idx = static_cast<uint32_t>(r);
+            row = __shfl(row_l, r);
+            slot0 = __shfl(first_l, r);
+            np = __shfl(np_l, r);
+            piece = static_cast<int>(wk - slot0);
+        } else {
+            idx = static_cast<uint32_t>(wk / n_pieces);
+            piece = static_cast<int>(wk % n_pieces);
+            np = static_cast<int>(n_pieces);
+            slot0 = static_cast<int64_t>(idx) * n_pieces;
+            row = a.rs_rows[idx];
+        }
         const int h = static_cast<int>(row % kHq);
         const int64_t bt = row / kHq;
         const int b = static_cast<int>(bt / T);
@@ -1570,7 +1615,7 @@ __global__ __launch_bounds__(kWave) void rescore_kernel(PrefillArgs a) {
             orow[lane] = f32_to_bf16_rne(static_cast<float>(o0 / l_tot)) |
                          (static_cast<uint32_t>(f32_to_bf16_rne(static_cast<float>(o1 / l_tot))) << 16);
         } else {
-            const int64_t slot = static_cast<int64_t>(idx) * n_pieces + piece;
+            const int64_t slot = slot0 + piece;
             unsigned long long* po = reinterpret_cast<unsigned long long*>(a.rs_part_o + slot * kD) + 2 * lane;
             store_agent(po, o0);
             store_agent(po + 1, o1);
@@ -1580,19 +1625,15 @@ __global__ __launch_bounds__(kWave) void rescore_kernel(PrefillArgs a) {
             wait_vmem();                              // the stores have completed ...
             __atomic_signal_fence(__ATOMIC_SEQ_CST);  // ... and stay before the count
             int last = 0;
-            if (lane == 0) last = atomicAdd(&a.rs_done[row], 1u) == n_pieces - 1;
+            if (lane == 0) last = atomicAdd(&a.rs_done[row], 1u) == static_cast<uint32_t>(np) - 1u;
             last = __shfl(last, 0);
             __atomic_signal_fence(__ATOMIC_SEQ_CST);  // the merge's loads stay after it
             if (last) {
-                // Lane u reads piece u's (m, l); lane i merges dims 2i, 2i + 1.  Every load is
-                // issued before any is used (unused entries repeat the last piece), so the
-                // merge waits for memory once.  A piece with no key has m = -inf, weight 0.
-                const int64_t slot0 = static_cast<int64_t>(idx) * n_pieces;
+                // Lane u reads piece u's (m, l); lane i merges dims 2i, 2i + 1, the pieces in
+                // order, kRsMergeBatch at a time: every load of a batch is issued before any
+                // is used (unused entries repeat the last piece), so a batch waits for memory
+                // once.  A piece with no key has m = -inf, weight 0.
                 const float2 ml = load_agent_f2(a.rs_part_ml + slot0 + min(lane, np - 1));
-                double2 ov[kRsMaxPieces];
-#pragma unroll
-                for (int u = 0; u < kRsMaxPieces; ++u)
-                    ov[u] = load_agent_d2(a.rs_part_o + (slot0 + min(u, np - 1)) * kD + 2 * lane);
                 float m_all = ml.x;
 #pragma unroll
                 for (int sh = 1; sh < kWave; sh <<= 1) m_all = fmaxf(m_all, __shfl_xor(m_all, sh));
@@ -1602,12 +1643,18 @@ __global__ __launch_bounds__(kWave) void rescore_kernel(PrefillArgs a) {
                 for (int sh = 1; sh < kWave; sh <<= 1) lw += __shfl_xor(lw, sh);
                 o0 = 0.0;
                 o1 = 0.0;
+                for (int u0 = 0; u0 < np; u0 += kRsMergeBatch) {
+                    double2 ov[kRsMergeBatch];
 #pragma unroll
-                for (int u = 0; u < kRsMaxPieces; ++u) {
-                    const int ex = __shfl(my_ex, u);
-                    if (u < np) {
-                        o0 += ldexp(ov[u].x, ex);
-                        o1 += ldexp(ov[u].y, ex);
+                    for (int u = 0; u < kRsMergeBatch; ++u)
+                        ov[u] = load_agent_d2(a.rs_part_o + (slot0 + min(u0 + u, np - 1)) * kD + 2 * lane);
+#pragma unroll
+                    for (int u = 0; u < kRsMergeBatch; ++u) {
+                        const int ex = __shfl(my_ex, u0 + u);
+                        if (u0 + u < np) {
+                            o0 += ldexp(ov[u].x, ex);
+                            o1 += ldexp(ov[u].y, ex);
+                        }
                     }
                 }
                 orow[lane] = f32_to_bf16_rne(static_cast<float>(o0 / lw)) |

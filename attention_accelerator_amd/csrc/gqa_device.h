@@ -150,6 +150,7 @@ __device__ __forceinline__ void rope_pair(double x, double y, int64_t position, 
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
+typedef double f64x4_t __attribute__((ext_vector_type(4)));
 
 // BF16 code of a double, rounding through f32 (any nearby BF16 value serves as the
 // leading part of a split; the residual is formed exactly in double).

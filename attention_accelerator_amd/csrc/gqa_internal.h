@@ -147,7 +147,7 @@ struct PrefillArgs {
 // those with a margin of 1.6.  Squared: min^2 * 128 < ratio^2 * sum x^2.
 constexpr double kRsFlagRatio2 = 1.0 / 17179869184.0;    // (2^-17)^2
 constexpr int kRsSlots = 1024;                            // partial slots (rows x pieces)
-constexpr int kRsMaxPieces = 32;                          // pieces per row at most
+constexpr int kRsMaxPieces = 64;                          // pieces per row at most (one per lane)
 size_t rescore_bytes(int32_t batch, int32_t n_new);
 void rescore_layout(PrefillArgs& a, void* base);
 hipError_t launch_rescore(const PrefillArgs& a, hipStream_t stream);

@@ -38,8 +38,9 @@ namespace gqa {
 // Each wave forms the next window's scores beside the current window's probabilities.
 // It waits for its own copies, then a fence-free barrier makes the whole plane visible:
 // once per window after the next window's K lands (which also tells every wave that V of
-// the previous window has been read, so its slot may be refilled) and once after the
-// current window's V lands.
+// the previous window has been read, so its slot may be refilled; and since each wave
+// requested the current window's V before that K, V has landed too).  Only a piece's last
+// window, which waits for no next K, waits and meets again for its V.
 
 constexpr int kMtWin = 32;                    // keys per window
 constexpr int kMtPlaneB = kMtWin * kRowB;     // 8 KB: 32 rows of 256 B
@@ -194,9 +195,9 @@ __device__ __forceinline__ void load4(const uint16_t* p, uint16_t (&h)[4]) {
 //    of tokens t >= T are zero;
 //  - the same dims' share of the scores of the chunk's own keys (key start + u, u < T:
 //    the new K row rotated at its position and not rounded, as the reference rotates K)
-//    against every column, in double.  The four shares are added in a fixed order and
-//    rounded once to f32: the stream kernel takes these scores in place of the ones it
-//    would form from the cache's rounded copy of those rows.
+//    against every column, in double (fp64 MFMAs).  The four shares are added in a fixed
+//    order and rounded once to f32: the stream kernel takes these scores in place of the
+//    ones it would form from the cache's rounded copy of those rows.
 // Row B of the grid builds the plan.  A sequence whose start is out of range gets NaN
 // rows and no cache write.
 template <bool kVec, int kW>
@@ -242,14 +243,12 @@ __global__ __launch_bounds__(256) void mt_prepare_kernel(PrefillArgs a) {
         load4<kVec>(qrow + d0, qx[tau]);
         load4<kVec>(qrow + d0 + kPairs, qy[tau]);
     }
-    uint16_t kxh[kU][4], kyh[kU][4];
-#pragma unroll
-    for (int u = 0; u < kU; ++u) {
-        if (u < T) {
-            const uint16_t* krow = a.k_new + ((static_cast<int64_t>(b) * T + u) * kHkv + kvh) * kD;
-            load4<kVec>(krow + d0, kxh[u]);
-            load4<kVec>(krow + d0 + kPairs, kyh[u]);
-        }
+    // The chunk key u = n of this lane's rows of the fp64 score MFMAs.
+    uint16_t kxh[4] = {0, 0, 0, 0}, kyh[4] = {0, 0, 0, 0};
+    if (n < T) {
+        const uint16_t* krow = a.k_new + ((static_cast<int64_t>(b) * T + n) * kHkv + kvh) * kD;
+        load4<kVec>(krow + d0, kxh);
+        load4<kVec>(krow + d0 + kPairs, kyh);
     }
     if (!prefill_start_ok(a, st)) {
         for (int i = threadIdx.x; i < T * kGroup * (kD / 4); i += blockDim.x) {
@@ -262,7 +261,9 @@ __global__ __launch_bounds__(256) void mt_prepare_kernel(PrefillArgs a) {
     }
     // sin and cos of (start + u) * inv_freq[i]: wave u % 4, lane i.
     __shared__ double sn_s[kU][kPairs], cs_s[kU][kPairs];
-    __shared__ double part_s[4][kU][kCols];
+    // Row u of a wave's share padded by one double, so that the final pass (consecutive
+    // threads, consecutive u) reads distinct banks.
+    __shared__ double part_s[4][kU][kCols + 1];
     const bool rope_q = (a.flags & 1u) != 0;
     const bool rope_k = (a.flags & 2u) != 0;
     if (rope_q || rope_k)
@@ -297,39 +298,37 @@ __global__ __launch_bounds__(256) void mt_prepare_kernel(PrefillArgs a) {
             qvy[tau][jj] = col ? yr * a.qk_scale_log2 : 0.0;
         }
     }
-    // This wave's share of the chunk-key scores, summed over the four lanes of each column.
+    // This wave's share of the chunk-key scores: per tile, S[u][column] over this wave's 32
+    // dims by fp64 MFMAs (v_mfma_f64_16x16x4: A[u][k] in lane 16k + u, B[k][column] in lane
+    // 16k + column, D[k + 4r][column] in lane 16k + column, register r), the k index of step
+    // (half, jj) standing for dim d0(k) + jj + 64 half -- the same dims the lane holds as Q
+    // operands.  Rows u >= T are zero; a row the causal mask hides from a column (u > 4 tau
+    // + 3) is never read.
+    {
+        double kxr[4], kyr[4];
 #pragma unroll
-    for (int u = 0; u < kU; ++u) {
-        double kxr[4] = {0.0, 0.0, 0.0, 0.0}, kyr[4] = {0.0, 0.0, 0.0, 0.0};
-        if (u < T) {
-#pragma unroll
-            for (int jj = 0; jj < 4; ++jj) {
-                const double x = bf16_to_f32(kxh[u][jj]);
-                const double y = bf16_to_f32(kyh[u][jj]);
-                kxr[jj] = x;
-                kyr[jj] = y;
-                if (rope_k) {
-                    const double sn = sn_s[u][d0 + jj], cs = cs_s[u][d0 + jj];
-                    kxr[jj] = x * cs - y * sn;
-                    kyr[jj] = x * sn + y * cs;
-                }
+        for (int jj = 0; jj < 4; ++jj) {
+            const double x = bf16_to_f32(kxh[jj]);
+            const double y = bf16_to_f32(kyh[jj]);
+            kxr[jj] = x;
+            kyr[jj] = y;
+            if (rope_k && n < T) {
+                const double sn = sn_s[n][d0 + jj], cs = cs_s[n][d0 + jj];
+                kxr[jj] = x * cs - y * sn;
+                kyr[jj] = x * sn + y * cs;
             }
         }
 #pragma unroll
         for (int tau = 0; tau < kW; ++tau) {
-            // Tile tau holds tokens 4 tau .. 4 tau + 3, which the causal mask hides key
-            // start + u from when u > 4 tau + 3: such a score is never read, and is left 0.
-            // The four lanes of a column are summed through lane swaps (VALU, no LDS).
-            double acc = 0.0;
-            if (u <= 4 * tau + 3) {
+            f64x4_t acc = {0.0, 0.0, 0.0, 0.0};
 #pragma unroll
-                for (int jj = 0; jj < 4; ++jj) {
-                    acc = fma(qvx[tau][jj], kxr[jj], acc);
-                    acc = fma(qvy[tau][jj], kyr[jj], acc);
-                }
-                acc = swap_add_f64<true>(swap_add_f64<false>(acc));
+            for (int jj = 0; jj < 4; ++jj) {
+                acc = __builtin_amdgcn_mfma_f64_16x16x4f64(kxr[jj], qvx[tau][jj], acc, 0, 0, 0);
+                acc = __builtin_amdgcn_mfma_f64_16x16x4f64(kyr[jj], qvy[tau][jj], acc, 0, 0, 0);
             }
-            if (g == 0) part_s[w][u][kMtTile * tau + n] = acc;
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+                if (g + 4 * r < kU) part_s[w][g + 4 * r][kMtTile * tau + n] = acc[r];
         }
     }
 
@@ -526,14 +525,21 @@ __device__ __forceinline__ void mt_probs(const f32x4_t (&sacc)[2], float m_eff, 
     t.l64 += static_cast<double>(lsum);
 }
 
-// mt_pv: once this window's V has landed (nv = planes of this wave's copies, kC
-// instructions each, younger than it) and every wave may read it, O^T += V^T P^T: dim
+// mt_pv: once this window's V has landed and every wave may read it, O^T += V^T P^T: dim
 // tile dt from two transposed reads (rows 4g + a/4 and 16 rows on), summed in fp32 into
-// the group's acc, which every kMtGroup windows moves into the fp64 O.
+// the group's acc, which every kMtGroup windows moves into the fp64 O.  `sync`: wait for
+// this wave's V copies (nv = planes of its copies, kC instructions each, younger than
+// them) and meet the other waves first.  Not needed when the window's top already waited
+// for the next window's K, which every wave requested after this window's V: the copies
+// complete in issue order, so that wait and the barrier after it covered V as well
+// (B=64 ragged, T=16: stream kernel 283 -> 272 us).
 template <int kC>
-__device__ __forceinline__ void mt_pv(uint32_t vbase, const uint32_t (&ph)[3][2][4], int nv, int lane, MtState& t) {
-    mt_wait_planes<kC>(nv);
-    mt_barrier();
+__device__ __forceinline__ void mt_pv(uint32_t vbase, const uint32_t (&ph)[3][2][4], int nv, int lane, MtState& t,
+                                      bool sync) {
+    if (sync) {
+        mt_wait_planes<kC>(nv);
+        mt_barrier();
+    }
     bf16x8_t pb[3];
 #pragma unroll
     for (int s = 0; s < 3; ++s) pb[s] = as_bf16x8(make_uint4(ph[s][0][0], ph[s][0][1], ph[s][0][2], ph[s][0][3]));
@@ -835,7 +841,7 @@ __global__ __launch_bounds__(kWave * kW) __attribute__((amdgpu_waves_per_eu(kW =
             f32x4_t s_next[2];
             mt_qk(slot_ptr(slot + 2), qop, lane, s_next);
             mt_probs(s_cur, m_eff, ph, t);
-            mt_pv<kC>(vbase, ph, nv, lane, t);
+            mt_pv<kC>(vbase, ph, nv, lane, t, !has_next);
             s_cur[0] = s_next[0];
             s_cur[1] = s_next[1];
             slot = slot + 2 >= kS ? slot + 2 - kS : slot + 2;

@@ -240,6 +240,25 @@ def test_multi_long_context_sampled_rows(dev):
     assert_within_ulp(want, got[:, rows], 64, "multi 131072", ref64=want64)
 
 
+@pytest.mark.parametrize("n_wgs", ["1", "7", "64", "1024"])
+def test_rescore_proportional_pieces(dev, monkeypatch, n_wgs):
+    """At most 64 flagged rows: each row's keys are cut into pieces in proportion to its
+    length (a row of 3001 keys gets about 30 times the pieces of one of 91), for rescore
+    grids of 1 (fewer workgroups than rows), 7, 64 and 1024 workgroups (GQA_STREAM_WGS sets
+    the grid).  V dimension 5 is zero in both sequences, so all 64 rows (2 sequences x 1
+    token x 32 heads) are flagged; every row must match the oracle, dimension 5 exactly."""
+    monkeypatch.setenv("GQA_STREAM_WGS", n_wgs)
+    starts = [90, 3000]
+    q, kn, vn, k, v = _chunk(starts, 1, 3001, 77)
+    vn[..., 5] = 0.0
+    for b, s in enumerate(starts):
+        v[b, :, :s, 5] = 0.0
+    want = _oracle(q, kn, vn, k, v, starts)
+    got, _, _ = _run(q, kn, vn, k, v, starts, dev)
+    assert np.all(got[..., 5] == 0)
+    _check(want, got.reshape(-1, 128), f"64 flagged rows, {n_wgs} rescore workgroups")
+
+
 @pytest.mark.parametrize("n_new,rope_q,rope_k", [
     (4, True, True),      # stream-K path, every row flagged: more rows than rescore workgroups
     (16, True, False),    # Q rotated with the cos/sin rows, the chunk's keys read as stored
