@@ -1405,9 +1405,12 @@ struct RsItem {
 };
 
 // Cached chunks of this piece (ci = c0, c0 + step, ... < c_end): rows as stored, in groups
-// of kRsGroup chunks computed together, two groups in flight.  rs_prefetch requests the
-// first two groups (before the Q operands are formed); rs_cached runs them and the rest.
+// of kRsGroup chunks computed together, kRsInflight groups in flight.  rs_prefetch requests
+// the first groups (before the Q operands are formed); rs_cached runs them and the rest.
 constexpr int kRsGroup = 4;
+// Three or four groups in flight measured no faster (config 5: 52.7 -> 51.4 / 52.2 us;
+// B=64 T=16: 28.4 -> 29.4 / 31.1 us): a piece is bound by its fp64 chains, not by memory.
+constexpr int kRsInflight = 2;
 
 __device__ __forceinline__ void rs_issue_group(const RsItem& it, int ci, int c_end, int step, RsRows (&r)[kRsGroup]) {
     const int j = threadIdx.x >> 3;
@@ -1419,26 +1422,27 @@ __device__ __forceinline__ void rs_issue_group(const RsItem& it, int ci, int c_e
     }
 }
 
-__device__ __forceinline__ void rs_prefetch(const RsItem& it, int c0, int c_end, int step, RsRows (&r)[2][kRsGroup]) {
-    rs_issue_group(it, c0, c_end, step, r[0]);
-    rs_issue_group(it, c0 + kRsGroup * step, c_end, step, r[1]);
+__device__ __forceinline__ void rs_prefetch(const RsItem& it, int c0, int c_end, int step,
+                                            RsRows (&r)[kRsInflight][kRsGroup]) {
+#pragma unroll
+    for (int h = 0; h < kRsInflight; ++h) rs_issue_group(it, c0 + h * kRsGroup * step, c_end, step, r[h]);
 }
 
 __device__ __forceinline__ void rs_cached(const RsItem& it, int c0, int c_end, int step, const double (&q)[16],
-                                          RsState& st, RsRows (&r)[2][kRsGroup]) {
+                                          RsState& st, RsRows (&r)[kRsInflight][kRsGroup]) {
     if (c0 >= c_end) return;
     const int j = threadIdx.x >> 3;
     const double2 (*no_cs)[8] = nullptr;
-    for (int ci = c0;; ci += 2 * kRsGroup * step) {
+    for (int ci = c0;; ci += kRsInflight * kRsGroup * step) {
 #pragma unroll
-        for (int h = 0; h < 2; ++h) {
+        for (int h = 0; h < kRsInflight; ++h) {
             const int cg = ci + h * kRsGroup * step;
             bool valid[kRsGroup];
 #pragma unroll
             for (int g = 0; g < kRsGroup; ++g) valid[g] = cg + g * step < c_end && kRsKeys * (cg + g * step) + j < it.n_keys;
             rs_chunks<kRsGroup, false>(r[h], q, valid, no_cs, st);
             if (cg + kRsGroup * step >= c_end) return;
-            rs_issue_group(it, cg + 2 * kRsGroup * step, c_end, step, r[h]);
+            rs_issue_group(it, cg + kRsInflight * kRsGroup * step, c_end, step, r[h]);
         }
     }
 }
@@ -1562,7 +1566,7 @@ __global__ __launch_bounds__(kWave) void rescore_kernel(PrefillArgs a) {
         // scaled by scale * log2(e): this lane's 8 pairs.  Its loads are issued first, then
         // the first cached chunks', so the Q operands are formed while those are in flight.
         double q[16];
-        RsRows pre[2][kRsGroup];
+        RsRows pre[kRsInflight][kRsGroup];
         {
             const char* qrow = reinterpret_cast<const char*>(a.q + (bt * kHq + h) * kD);
             const uint4 qx = load_stream16(qrow + 16 * c);
