@@ -391,7 +391,7 @@ __device__ __forceinline__ void mt_issue_plane(const char* seg, int64_t row_byte
         // Every row of the window exists: a uniform row base plus the lane's 32-bit offset,
         // which does not change from window to window (the ABI keeps a (sequence, KV head)'s
         // rows under 4 GiB).
-        const char* base = seg + static_cast<int64_t>(key0) * row_bytes;
+        const char* base = seg + static_cast<uint32_t>(key0) * static_cast<uint32_t>(row_bytes);
 #pragma unroll
         for (int q = 0; q < kC; ++q) {
             const uint32_t r = static_cast<uint32_t>(4 * (wv * kC + q) + (lane >> 4));
@@ -822,7 +822,7 @@ __global__ __launch_bounds__(kWave * kW) __attribute__((amdgpu_waves_per_eu(kW =
             if (iv) issue(a.v, p, slot + 2 * kA + 1);
             const bool has_next = c.kw + kMtWin < c.k_b;
             if (has_next) {                                  // K of the next window landed
-                if (kq == kA)                                // the steady state: a fixed count
+                if (__builtin_expect(kq == kA, 1))           // the steady state: a fixed count
                     __builtin_amdgcn_s_waitcnt(vmcnt_imm((2 * kA - 1) * kC));
                 else
                     mt_wait_planes<kC>(2 * kq - 1);
