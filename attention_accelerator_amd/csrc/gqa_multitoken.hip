@@ -61,21 +61,21 @@ __host__ __device__ constexpr int mt_slots(int w) { return 2 * mt_ahead(w) + 3; 
 constexpr int vmcnt_imm(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
 static_assert(vmcnt_imm(0) == 0x0F70 && vmcnt_imm(16) == 0x4F70, "vmcnt encoding");
 
-// Wait until at most `planes` planes of this wave's copies (kC instructions each) are in
-// flight: the counter retires in issue order, so everything older has landed.  Requests
-// of other kinds issued since (Q operands, stores) only make the wait longer.
-template <int kC>
-__device__ __forceinline__ void mt_wait_planes(int planes) {
-    switch (planes) {
-#define MT_CASE(k) \
-    case k: __builtin_amdgcn_s_waitcnt(vmcnt_imm(k * kC < 63 ? k * kC : 63)); break;
-        MT_CASE(1) MT_CASE(2) MT_CASE(3) MT_CASE(4) MT_CASE(5) MT_CASE(6) MT_CASE(7) MT_CASE(8) MT_CASE(9)
-        MT_CASE(10) MT_CASE(11)
-#undef MT_CASE
-        default: __builtin_amdgcn_s_waitcnt(vmcnt_imm(0)); break;
-    }
+// Wait until at most kPlanes planes of this wave's copies (kC instructions each) are in
+// flight -- the count when the producer runs its full kA windows ahead (`steady`) -- and
+// otherwise until none is: the counter retires in issue order, so everything older has
+// landed.  Only a range's last kA windows, where nothing is left to overlap, take the full
+// wait (a switch over the exact count cost ~20 scalar instructions and ~8 branches per
+// window).  Requests of other kinds issued since (Q operands, stores) only make the wait
+// longer.
+template <int kC, int kPlanes>
+__device__ __forceinline__ void mt_wait_planes(bool steady) {
+    static_assert(kPlanes * kC <= 63, "vmcnt range");
+    if (steady)
+        __builtin_amdgcn_s_waitcnt(vmcnt_imm(kPlanes * kC));
+    else
+        __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
 }
-static_assert((2 * mt_ahead(1) + 1) * kMtCopies <= 63, "vmcnt range");
 
 // Barrier without the memory fence __syncthreads adds (which would wait for every copy in
 // flight).
@@ -528,16 +528,16 @@ __device__ __forceinline__ void mt_probs(const f32x4_t (&sacc)[2], float m_eff, 
 // mt_pv: once this window's V has landed and every wave may read it, O^T += V^T P^T: dim
 // tile dt from two transposed reads (rows 4g + a/4 and 16 rows on), summed in fp32 into
 // the group's acc, which every kMtGroup windows moves into the fp64 O.  `sync`: wait for
-// this wave's V copies (nv = planes of its copies, kC instructions each, younger than
-// them) and meet the other waves first.  Not needed when the window's top already waited
+// this wave's V copies (kVPlanes planes of its copies younger than them when `steady`) and
+// meet the other waves first.  Not needed when the window's top already waited
 // for the next window's K, which every wave requested after this window's V: the copies
 // complete in issue order, so that wait and the barrier after it covered V as well
 // (B=64 ragged, T=16: stream kernel 283 -> 272 us).
-template <int kC>
-__device__ __forceinline__ void mt_pv(uint32_t vbase, const uint32_t (&ph)[3][2][4], int nv, int lane, MtState& t,
-                                      bool sync) {
+template <int kC, int kVPlanes>
+__device__ __forceinline__ void mt_pv(uint32_t vbase, const uint32_t (&ph)[3][2][4], bool steady, int lane,
+                                      MtState& t, bool sync) {
     if (sync) {
-        mt_wait_planes<kC>(nv);
+        mt_wait_planes<kC, kVPlanes>(steady);
         mt_barrier();
     }
     bf16x8_t pb[3];
@@ -812,7 +812,7 @@ __global__ __launch_bounds__(kWave * kW) __attribute__((amdgpu_waves_per_eu(kW =
         // ahead).  B=64 ragged: T=8 302.4 -> 287.9 us per step, T=4 216.2 -> 215.2.  The
         // piece's first window's scores are formed here (its V(i + kA) not yet requested).
         f32x4_t s_cur[2];
-        mt_wait_planes<kC>(kq == kA ? 2 * kA : 1 + 2 * kq);
+        mt_wait_planes<kC, 2 * kA>(kq == kA);
         mt_barrier();
         mt_qk(slot_ptr(slot), qop, lane, s_cur);
         for (;;) {
@@ -821,12 +821,7 @@ __global__ __launch_bounds__(kWave * kW) __attribute__((amdgpu_waves_per_eu(kW =
             const bool iv = p.valid;
             if (iv) issue(a.v, p, slot + 2 * kA + 1);
             const bool has_next = c.kw + kMtWin < c.k_b;
-            if (has_next) {                                  // K of the next window landed
-                if (__builtin_expect(kq == kA, 1))           // the steady state: a fixed count
-                    __builtin_amdgcn_s_waitcnt(vmcnt_imm((2 * kA - 1) * kC));
-                else
-                    mt_wait_planes<kC>(2 * kq - 1);
-            }
+            if (has_next) mt_wait_planes<kC, 2 * kA - 1>(kq == kA);   // K of the next window landed
             mt_barrier();
             bool ik = false;
             if (iv) {
@@ -836,7 +831,7 @@ __global__ __launch_bounds__(kWave * kW) __attribute__((amdgpu_waves_per_eu(kW =
                     ik = true;
                 }
             }
-            const int nv = 2 * kq + (ik ? 1 : 0);
+            const bool v_steady = kq == kA && ik;     // 2 kA + 1 planes requested after V
             const uint32_t vbase = lds_base + (slot + 1 >= kS ? slot + 1 - kS : slot + 1) * kMtPlaneB;
             const bool chunk_keys = c.kw + kMtWin > st;
             uint32_t ph[3][2][4];
@@ -846,7 +841,7 @@ __global__ __launch_bounds__(kWave * kW) __attribute__((amdgpu_waves_per_eu(kW =
             f32x4_t s_next[2];
             mt_qk(slot_ptr(slot + 2), qop, lane, s_next);
             mt_probs(s_cur, m_eff, ph, t);
-            mt_pv<kC>(vbase, ph, nv, lane, t, !has_next);
+            mt_pv<kC, 2 * kA + 1>(vbase, ph, v_steady, lane, t, !has_next);
             s_cur[0] = s_next[0];
             s_cur[1] = s_next[1];
             slot = slot + 2 >= kS ? slot + 2 - kS : slot + 2;
