@@ -157,7 +157,7 @@ DecodePlan plan_decode(int32_t batch, int32_t capacity, bool paged, int64_t max_
                           align_up(static_cast<size_t>(batch) * sizeof(int32_t), 256);
     }
     plan.part_o_bytes = align_up(static_cast<size_t>(plan.n_slots) * kGroup * kD * sizeof(double), 256);
-    plan.part_ml_bytes = align_up(static_cast<size_t>(plan.n_slots) * kGroup * sizeof(float2), 256);
+    plan.part_ml_bytes = align_up(static_cast<size_t>(plan.n_slots) * kGroup * sizeof(double2), 256);
     plan.count_bytes = align_up(static_cast<size_t>(batch) * kHkv * sizeof(unsigned long long), 256);
     plan.workspace_bytes =
         plan.part_o_bytes + plan.part_ml_bytes + plan.q_op_bytes + plan.plan_bytes + plan.count_bytes;
@@ -170,7 +170,7 @@ size_t rescore_bytes(int32_t batch, int32_t n_new) {
     const size_t rows = static_cast<size_t>(batch) * n_new * kHq;
     const size_t toks = static_cast<size_t>(batch) * n_new;
     return 256 + 2 * align_up(rows * sizeof(uint32_t), 256) + align_up(toks * kPairs * sizeof(double2), 256) +
-           align_up(size_t{kRsSlots} * kD * sizeof(double), 256) + align_up(size_t{kRsSlots} * sizeof(float2), 256);
+           align_up(size_t{kRsSlots} * kD * sizeof(double), 256) + align_up(size_t{kRsSlots} * sizeof(double2), 256);
 }
 
 void rescore_layout(PrefillArgs& a, void* base) {
@@ -186,7 +186,7 @@ void rescore_layout(PrefillArgs& a, void* base) {
     p += align_up(static_cast<size_t>(a.batch) * a.n_new * kPairs * sizeof(double2), 256);
     a.rs_part_o = reinterpret_cast<double*>(p);
     p += align_up(size_t{kRsSlots} * kD * sizeof(double), 256);
-    a.rs_part_ml = reinterpret_cast<float2*>(p);
+    a.rs_part_ml = reinterpret_cast<double2*>(p);
     // One-wave workgroups, one per SIMD (the kernel's registers allow one wave per SIMD):
     // the flagged rows are cut into about as many (row, piece) pairs as run at once.
     const int32_t wgs = stream_wgs();
@@ -264,7 +264,7 @@ int decode_launch(const DecodePlan& plan, const gqa_params_t* params, const uint
     a.out = out;
     char* ws = static_cast<char*>(workspace);
     a.part_o = reinterpret_cast<double*>(ws);
-    a.part_ml = reinterpret_cast<float2*>(ws + plan.part_o_bytes);
+    a.part_ml = reinterpret_cast<double2*>(ws + plan.part_o_bytes);
     a.q_op = reinterpret_cast<double*>(ws + plan.part_o_bytes + plan.part_ml_bytes);
     char* pl = ws + plan.part_o_bytes + plan.part_ml_bytes + plan.q_op_bytes;
     a.plan_hdr = reinterpret_cast<int64_t*>(pl);

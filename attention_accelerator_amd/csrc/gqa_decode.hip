@@ -116,12 +116,13 @@ struct Chunk {
 };
 
 // Running state of one piece in lane l: O[head l%4][out_dim_of_lane(l) + e] in acc[e], and
-// the head's integer-valued running max and (this lane's share of the) sum of p.  m_run is
-// the same in every lane of a head.
+// the head's integer-valued running max (double, as every step here: scores may lie far
+// beyond 2^24) and (this lane's share of the) sum of p.  m_run is the same in every lane
+// of a head.
 struct PieceState {
     double acc[8];
     double l_run;
-    float m_run;
+    double m_run;
 };
 
 __device__ __forceinline__ void init_piece(PieceState& st) {
@@ -249,24 +250,24 @@ __device__ __forceinline__ void compute_chunk(const RopeTable& rope, int rope_po
     // Online softmax per head with a lazy reference: m (integer-valued, common to the 16
     // lanes with lane%4 == head) is raised only when a score exceeds m + kMaxHeadroom, so
     // the rescale below runs about once per piece; p = 2^(s - m) <= 2^kMaxHeadroom then,
-    // far inside the fp64 range.  The new m is the ceiling of the head's chunk max, taken
-    // in fp32 over its 16 lanes (rows through lane swaps, blocks through row rotations).
-    if (__ballot(s > static_cast<double>(st.m_run) + kMaxHeadroom)) {
-        float cm = static_cast<float>(s);
-        cm = fmaxf(cm, dpp_f<0x124>(cm));
-        cm = fmaxf(cm, dpp_f<0x128>(cm));
-        cm = swap32_max(swap16_max(cm));
-        const bool grow = static_cast<double>(cm) > static_cast<double>(st.m_run) + kMaxHeadroom;
-        const float m_new = grow ? ceilf(cm) : st.m_run;
+    // far inside the fp64 range.  The new m is the ceiling of the head's chunk max over its
+    // 16 lanes (rows through lane swaps, blocks through row rotations).
+    if (__ballot(s > st.m_run + kMaxHeadroom)) {
+        double cm = s;
+        cm = fmax(cm, dpp_d<0x124>(cm));
+        cm = fmax(cm, dpp_d<0x128>(cm));
+        cm = swap_max_f64<true>(swap_max_f64<false>(cm));
+        const bool grow = cm > st.m_run + kMaxHeadroom;
+        const double m_new = grow ? ceil(cm) : st.m_run;
         // 2^(m_run - m_new), exact; nothing has been accumulated while m_run is -inf.
-        const int shift = (st.m_run == -INFINITY) ? 0 : static_cast<int>(st.m_run - m_new);
+        const int shift = (st.m_run == -INFINITY) ? 0 : max_shift_f64(st.m_run, m_new);
         st.l_run = ldexp(st.l_run, shift);
 #pragma unroll
         for (int i = 0; i < 8; ++i) st.acc[i] = ldexp(st.acc[i], shift);
         st.m_run = m_new;
     }
     // p = 0 for a masked key (and for every key while m is -inf, when all of them are).
-    const double p = key < k_b ? exp2_f64(fmax(s - static_cast<double>(st.m_run), -2000.0)) : 0.0;
+    const double p = key < k_b ? exp2_f64(fmax(s - st.m_run, -2000.0)) : 0.0;
     st.l_run += p;
 
     // p of (head l%4, key 4q + l/16) for q = 0..3, from the lane holding that score
@@ -337,7 +338,7 @@ __device__ __forceinline__ void write_partial(const DecodeArgs& a, int64_t slot,
     double2* dst = reinterpret_cast<double2*>(a.part_o + slot * kGroup * kD + lane_row_offset());
 #pragma unroll
     for (int j = 0; j < 4; ++j) dst[j] = make_double2(st.acc[2 * j], st.acc[2 * j + 1]);
-    if (lane < kGroup) a.part_ml[slot * kGroup + lane] = make_float2(st.m_run, static_cast<float>(l_tot));
+    if (lane < kGroup) a.part_ml[slot * kGroup + lane] = make_double2(st.m_run, l_tot);
 }
 
 // Agent-scope (sc1) 8-byte stores and loads: coherent across the XCDs without a cache
@@ -866,7 +867,7 @@ __device__ __forceinline__ void process_page_piece(const DecodeArgs& a, const Pa
     finish_piece(st, l_tot);
     if (!all_ok) {
         // an invalid block id: poison the sequence's rows of this segment
-        st.m_run = 0.f;
+        st.m_run = 0.0;
         l_tot = __longlong_as_double(0x7ff8000000000000ll);
     }
     if (k_a == 0 && p.k_b == p.nvp) {
@@ -987,12 +988,12 @@ __global__ __launch_bounds__(kGroup * kWave) void decode_merge_kernel(DecodeArgs
     // Pieces in passes of 64, one (m, l) per lane; the O rows of a pass are requested
     // together with its (m, l) (indices clamped to the last piece, whose extra copies get
     // weight 0) and weighted by 2^(m - running max) once the pass's max is known.
-    float mx = -INFINITY;
+    double mx = -INFINITY;
     double l = 0.0, o0 = 0.0, o1 = 0.0;
     for (int p0 = 0; p0 < n_pieces; p0 += kWave) {
         const int cnt = min(kWave, n_pieces - p0);
         const int p = p0 + min(lane, cnt - 1);
-        const float2 ml = a.part_ml[(slot0 + p) * kGroup + h];
+        const double2 ml = a.part_ml[(slot0 + p) * kGroup + h];
         for (int q = 0; q < cnt; q += 8) {
             double2 o[8];
 #pragma unroll
@@ -1003,19 +1004,19 @@ __global__ __launch_bounds__(kGroup * kWave) void decode_merge_kernel(DecodeArgs
             }
             if (q == 0) {
                 // New running max over this pass; rescale what earlier passes summed.
-                const float m_pass = wave_max(lane < cnt ? ml.x : -INFINITY);
-                const float m_new = fmaxf(mx, m_pass);
+                const double m_pass = wave_max_f64(lane < cnt ? ml.x : -INFINITY);
+                const double m_new = fmax(mx, m_pass);
                 if (mx != -INFINITY && m_new != mx) {
-                    const int e = static_cast<int>(mx - m_new);
+                    const int e = max_shift_f64(mx, m_new);
                     l = ldexp(l, e);
                     o0 = ldexp(o0, e);
                     o1 = ldexp(o1, e);
                 }
                 mx = m_new;
-                if (lane < cnt && ml.x != -INFINITY) l += ldexp(static_cast<double>(ml.y), static_cast<int>(ml.x - mx));
+                if (lane < cnt && ml.x != -INFINITY) l += ldexp(ml.y, max_shift_f64(ml.x, mx));
             }
             // a piece holding no key (padding of a paged segment) has m = -inf: weight 0
-            const int e_lane = lane < cnt && ml.x != -INFINITY ? static_cast<int>(ml.x - mx) : -1100;
+            const int e_lane = lane < cnt && ml.x != -INFINITY ? max_shift_f64(ml.x, mx) : -1100;
 #pragma unroll
             for (int u = 0; u < 8; ++u) {
                 const int ee = __shfl(e_lane, min(q + u, kWave - 1));
@@ -1059,7 +1060,7 @@ template <bool kRopeQ, bool kRopeK>
 __global__ __launch_bounds__(kSingleWaves * kWave) void decode_single_kernel(DecodeArgs a) {
     __shared__ double q_s[kGroup][kD];
     __shared__ double o_s[kSingleWaves][kGroup][kD];     // each wave's O (blocks summed)
-    __shared__ float m_s[kSingleWaves][kGroup];
+    __shared__ double m_s[kSingleWaves][kGroup];
     __shared__ double l_s[kSingleWaves][kGroup];
     __shared__ int last_s;
     const int piece = blockIdx.x;
@@ -1137,15 +1138,15 @@ __global__ __launch_bounds__(kSingleWaves * kWave) void decode_single_kernel(Dec
 
     // Wave h combines head h over the four quarters: lane owns dims 2*lane, 2*lane + 1.
     const int h = wave;
-    float mx = -INFINITY;
+    double mx = -INFINITY;
 #pragma unroll
-    for (int w = 0; w < kSingleWaves; ++w) mx = fmaxf(mx, m_s[w][h]);
+    for (int w = 0; w < kSingleWaves; ++w) mx = fmax(mx, m_s[w][h]);
     double l = 0.0, o0 = 0.0, o1 = 0.0;
 #pragma unroll
     for (int w = 0; w < kSingleWaves; ++w) {
-        const float m = m_s[w][h];
+        const double m = m_s[w][h];
         if (m == -INFINITY) continue;                    // an idle quarter
-        const int e = static_cast<int>(m - mx);
+        const int e = max_shift_f64(m, mx);
         l += ldexp(l_s[w][h], e);
         o0 += ldexp(o_s[w][h][2 * lane], e);
         o1 += ldexp(o_s[w][h][2 * lane + 1], e);
@@ -1170,9 +1171,11 @@ __global__ __launch_bounds__(kSingleWaves * kWave) void decode_single_kernel(Dec
             reinterpret_cast<unsigned long long*>(a.part_o + ((slot0 + piece) * kGroup + h) * kD) + 2 * lane;
         store_agent(po, o0);
         store_agent(po + 1, o1);
-        if (lane == 0)
-            store_agent(reinterpret_cast<unsigned long long*>(a.part_ml + (slot0 + piece) * kGroup + h),
-                        make_float2(mx, static_cast<float>(l)));
+        if (lane == 0) {
+            unsigned long long* pml = reinterpret_cast<unsigned long long*>(a.part_ml + (slot0 + piece) * kGroup + h);
+            store_agent(pml, mx);
+            store_agent(pml + 1, l);
+        }
         wait_vmem();
         __atomic_signal_fence(__ATOMIC_SEQ_CST);
     }
@@ -1192,45 +1195,47 @@ __global__ __launch_bounds__(kSingleWaves * kWave) void decode_single_kernel(Dec
     o0 = 0.0;
     o1 = 0.0;
     if (n_pieces <= 16) {
+        // lane u < 16 holds piece u's (m, l) (copies of the last piece past n_pieces)
         double2 ov[16];
-        float2 ml[16];
+        const double2 mlu = load_agent_d2(reinterpret_cast<const double*>(
+            a.part_ml + (slot0 + min(lane & 15, n_pieces - 1)) * kGroup + h));
 #pragma unroll
         for (int u = 0; u < 16; ++u) {
             const int p = min(u, n_pieces - 1);
             ov[u] = load_agent_d2(a.part_o + ((slot0 + p) * kGroup + h) * kD + 2 * lane);
-            ml[u] = load_agent_f2(a.part_ml + (slot0 + p) * kGroup + h);
         }
-        float m_all = -INFINITY;
-#pragma unroll
-        for (int u = 0; u < 16; ++u) m_all = fmaxf(m_all, ml[u].x);     // copies of the last piece add nothing
+        const double m_all = wave_max_f64(mlu.x);     // copies of the last piece add nothing
+        const int e_l = (lane & 15) < n_pieces ? max_shift_f64(mlu.x, m_all) : -1100;
 #pragma unroll
         for (int u = 0; u < 16; ++u) {
-            const int e = u < n_pieces ? static_cast<int>(ml[u].x - m_all) : -1100;
-            l += ldexp(static_cast<double>(ml[u].y), e);
+            const int e = __shfl(e_l, u);
+            l += ldexp(__shfl(mlu.y, u), e);
             o0 += ldexp(ov[u].x, e);
             o1 += ldexp(ov[u].y, e);
         }
     } else {
-        float m_all = -INFINITY;
+        double m_all = -INFINITY;
         for (int p0 = 0; p0 < n_pieces; p0 += kWave) {
             const int p = p0 + lane;
-            m_all = fmaxf(m_all, p < n_pieces ? load_agent_f2(a.part_ml + (slot0 + p) * kGroup + h).x : -INFINITY);
+            m_all = fmax(m_all, p < n_pieces ? load_agent_d2(reinterpret_cast<const double*>(
+                                                   a.part_ml + (slot0 + p) * kGroup + h)).x
+                                             : -INFINITY);
         }
-        m_all = wave_max(m_all);
+        m_all = wave_max_f64(m_all);
         for (int p0 = 0; p0 < n_pieces; p0 += 16) {
             double2 ov[16];
-            float2 ml[16];
+            double2 ml[16];
 #pragma unroll
             for (int u = 0; u < 16; ++u) {
                 const int p = min(p0 + u, n_pieces - 1);
                 ov[u] = load_agent_d2(a.part_o + ((slot0 + p) * kGroup + h) * kD + 2 * lane);
-                ml[u] = load_agent_f2(a.part_ml + (slot0 + p) * kGroup + h);
+                ml[u] = load_agent_d2(reinterpret_cast<const double*>(a.part_ml + (slot0 + p) * kGroup + h));
             }
 #pragma unroll
             for (int u = 0; u < 16; ++u) {
                 // copies of the last piece (indices clamped above) get weight 0
-                const int e = p0 + u < n_pieces ? static_cast<int>(ml[u].x - m_all) : -1100;
-                l += ldexp(static_cast<double>(ml[u].y), e);
+                const int e = p0 + u < n_pieces ? max_shift_f64(ml[u].x, m_all) : -1100;
+                l += ldexp(ml[u].y, e);
                 o0 += ldexp(ov[u].x, e);
                 o1 += ldexp(ov[u].y, e);
             }
@@ -1316,11 +1321,14 @@ __device__ __forceinline__ double rs_slot_sum(double x) {
 }
 
 // Running state of a piece: this lane's O over its keys (its 16 dims), the sum of p over
-// its keys (each key counted in all eight of its lanes) and the wave's running max.
+// its keys (each key counted in all eight of its lanes) and the wave's running max, in
+// double: the rows sent here include rows whose scores are far beyond 2^24, where an fp32
+// max could not sit within a few units of the largest score (and p of that key would
+// underflow).
 struct RsState {
     double o[16];
     double l;
-    float m;
+    double m;
 };
 
 // Lazy running max (integer-valued, wave-uniform): raised to the ceiling of the largest
@@ -1329,15 +1337,15 @@ template <int G>
 __device__ __forceinline__ void rs_raise_max(const double (&s)[G], RsState& st) {
     bool grow = false;
 #pragma unroll
-    for (int g = 0; g < G; ++g) grow |= s[g] > static_cast<double>(st.m) + kMaxHeadroom;
+    for (int g = 0; g < G; ++g) grow |= s[g] > st.m + kMaxHeadroom;
     if (__ballot(grow)) {
-        float cm = static_cast<float>(s[0]);
+        double cm = s[0];
 #pragma unroll
-        for (int g = 1; g < G; ++g) cm = fmaxf(cm, static_cast<float>(s[g]));
-#pragma unroll
-        for (int sh = 8; sh < kWave; sh <<= 1) cm = fmaxf(cm, __shfl_xor(cm, sh));
-        const float m_new = ceilf(cm);
-        const int shift = (st.m == -INFINITY) ? 0 : static_cast<int>(st.m - m_new);
+        for (int g = 1; g < G; ++g) cm = fmax(cm, s[g]);
+        cm = fmax(cm, dpp_d<0x128>(cm));                      // key slots 8 lanes apart
+        cm = swap_max_f64<true>(swap_max_f64<false>(cm));
+        const double m_new = ceil(cm);
+        const int shift = (st.m == -INFINITY) ? 0 : max_shift_f64(st.m, m_new);
 #pragma unroll
         for (int i = 0; i < 16; ++i) st.o[i] = ldexp(st.o[i], shift);
         st.l = ldexp(st.l, shift);
@@ -1382,7 +1390,7 @@ __device__ __forceinline__ void rs_chunks(const RsRows* r, const double (&q)[16]
     rs_raise_max<G>(s, st);
     double p[G];
 #pragma unroll
-    for (int g = 0; g < G; ++g) p[g] = valid[g] ? exp2_f64(fmax(s[g] - static_cast<double>(st.m), -2000.0)) : 0.0;
+    for (int g = 0; g < G; ++g) p[g] = valid[g] ? exp2_f64(fmax(s[g] - st.m, -2000.0)) : 0.0;
 #pragma unroll
     for (int g = 0; g < G; ++g) {
         st.l += p[g];
@@ -1623,9 +1631,11 @@ __global__ __launch_bounds__(kWave) void rescore_kernel(PrefillArgs a) {
             unsigned long long* po = reinterpret_cast<unsigned long long*>(a.rs_part_o + slot * kD) + 2 * lane;
             store_agent(po, o0);
             store_agent(po + 1, o1);
-            if (lane == 0)
-                store_agent(reinterpret_cast<unsigned long long*>(a.rs_part_ml + slot),
-                            make_float2(stt.m, static_cast<float>(l_tot)));
+            if (lane == 0) {
+                unsigned long long* pml = reinterpret_cast<unsigned long long*>(a.rs_part_ml + slot);
+                store_agent(pml, stt.m);
+                store_agent(pml + 1, l_tot);
+            }
             wait_vmem();                              // the stores have completed ...
             __atomic_signal_fence(__ATOMIC_SEQ_CST);  // ... and stay before the count
             int last = 0;
@@ -1637,12 +1647,12 @@ __global__ __launch_bounds__(kWave) void rescore_kernel(PrefillArgs a) {
                 // order, kRsMergeBatch at a time: every load of a batch is issued before any
                 // is used (unused entries repeat the last piece), so a batch waits for memory
                 // once.  A piece with no key has m = -inf, weight 0.
-                const float2 ml = load_agent_f2(a.rs_part_ml + slot0 + min(lane, np - 1));
-                float m_all = ml.x;
+                const double2 ml = load_agent_d2(reinterpret_cast<const double*>(a.rs_part_ml + slot0 + min(lane, np - 1)));
+                double m_all = ml.x;
 #pragma unroll
-                for (int sh = 1; sh < kWave; sh <<= 1) m_all = fmaxf(m_all, __shfl_xor(m_all, sh));
-                const int my_ex = ml.x == -INFINITY ? -1100 : static_cast<int>(ml.x - m_all);
-                double lw = lane < np ? ldexp(static_cast<double>(ml.y), my_ex) : 0.0;
+                for (int sh = 1; sh < kWave; sh <<= 1) m_all = fmax(m_all, __shfl_xor(m_all, sh));
+                const int my_ex = ml.x == -INFINITY ? -1100 : max_shift_f64(ml.x, m_all);
+                double lw = lane < np ? ldexp(ml.y, my_ex) : 0.0;
 #pragma unroll
                 for (int sh = 1; sh < kWave; sh <<= 1) lw += __shfl_xor(lw, sh);
                 o0 = 0.0;

@@ -49,6 +49,21 @@ __device__ __forceinline__ uint16_t f64_to_bf16_via_f32(double d) {
     return f32_to_bf16_rne(static_cast<float>(d));
 }
 
+// Exponent of the exact weight 2^(m - m_ref) of a running max m against a reference
+// m_ref >= m (both integer-valued floats, m_ref finite), clamped at -2048: every ldexp of a
+// float or double by less gives 0, and converting a difference beyond the int range is
+// undefined.  m = -inf gives -2048, weight 0.
+__device__ __forceinline__ int max_shift(float m, float m_ref) {
+    return static_cast<int>(fmaxf(m - m_ref, -2048.f));
+}
+
+// The same for running maxima kept in double (the fp64 paths: their scores may lie far
+// beyond 2^24, where an integer-valued fp32 max could not sit within a few units of the
+// largest score, and p of that key would underflow).
+__device__ __forceinline__ int max_shift_f64(double m, double m_ref) {
+    return static_cast<int>(fmax(m - m_ref, -2048.0));
+}
+
 // DPP lane moves (row = 16 lanes).  Control codes: quad_perm [1,0,3,2] = 0xB1,
 // quad_perm [2,3,0,1] = 0x4E, quad_perm [h,h,h,h] = 0x55*h (broadcast lane h of each
 // quad), row_ror:n = 0x120 + n.
@@ -60,6 +75,14 @@ __device__ __forceinline__ float dpp_f(float x) {
 template <int kCtrl>
 __device__ __forceinline__ int dpp_i(int x) {
     return __builtin_amdgcn_update_dpp(0, x, kCtrl, 0xf, 0xf, false);
+}
+
+template <int kCtrl>
+__device__ __forceinline__ double dpp_d(double x) {
+    const unsigned long long u = static_cast<unsigned long long>(__double_as_longlong(x));
+    const unsigned lo = static_cast<unsigned>(dpp_i<kCtrl>(static_cast<int>(u)));
+    const unsigned hi = static_cast<unsigned>(dpp_i<kCtrl>(static_cast<int>(u >> 32)));
+    return __longlong_as_double(static_cast<long long>((static_cast<unsigned long long>(hi) << 32) | lo));
 }
 
 // Sum over the 16 lanes of a DPP row; every lane of the row gets the total.
@@ -120,8 +143,32 @@ __device__ __forceinline__ double swap_add_f64(double x) {
     return a + b;
 }
 
+// The larger of x in lane l and in lane l ^ 16 (k32: l ^ 32), as swap_add_f64.
+template <bool k32>
+__device__ __forceinline__ double swap_max_f64(double x) {
+    const unsigned long long u = static_cast<unsigned long long>(__double_as_longlong(x));
+    const unsigned lo = static_cast<unsigned>(u), hi = static_cast<unsigned>(u >> 32);
+    const auto rl = k32 ? __builtin_amdgcn_permlane32_swap(lo, lo, false, false)
+                        : __builtin_amdgcn_permlane16_swap(lo, lo, false, false);
+    const auto rh = k32 ? __builtin_amdgcn_permlane32_swap(hi, hi, false, false)
+                        : __builtin_amdgcn_permlane16_swap(hi, hi, false, false);
+    const double a = __longlong_as_double(static_cast<long long>((static_cast<unsigned long long>(rh[0]) << 32) | rl[0]));
+    const double b = __longlong_as_double(static_cast<long long>((static_cast<unsigned long long>(rh[1]) << 32) | rl[1]));
+    return fmax(a, b);
+}
+
+// Largest x over the wave (all 64 lanes active): within rows by DPP, across them by swaps.
+__device__ __forceinline__ double wave_max_f64(double x) {
+    x = fmax(x, dpp_d<0xB1>(x));
+    x = fmax(x, dpp_d<0x4E>(x));
+    x = fmax(x, dpp_d<0x124>(x));
+    x = fmax(x, dpp_d<0x128>(x));
+    return swap_max_f64<true>(swap_max_f64<false>(x));
+}
+
 __device__ __forceinline__ float wave_sum(float x) { return cross_row_sum(row16_sum(x)); }
 __device__ __forceinline__ float wave_max(float x) { return cross_row_max(row16_max(x)); }
+
 
 // sin and cos of angle = position * inv_freq, in double.  The angle (up to ~2^31 rad)
 // is first reduced modulo 2*pi with a two-part Cody-Waite constant and fused

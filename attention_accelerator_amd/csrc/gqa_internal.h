@@ -21,7 +21,7 @@ struct DecodeArgs {
     int64_t* seq_off;         // [B+1] first global key offset of sequence b's segments
     int32_t* seq_nreal;       // [B] keys of sequence b that count (n_valid; the plan pads to blocks)
     double* part_o;           // [n_slots][4][128] unnormalised partial outputs
-    float2* part_ml;          // [n_slots][4] (integer-valued running max in log2 units, sum)
+    double2* part_ml;         // [n_slots][4] (integer-valued running max in log2 units, sum)
     unsigned long long* seg_count;  // [B*8] pieces finished per segment, single-launch path (zero between calls)
     const int32_t* block_table;  // paged cache: [B][max_blocks] block ids (nullptr: contiguous cache)
     int64_t kv_batch_stride;  // contiguous: elements per sequence; paged: per block of the pool
@@ -134,7 +134,7 @@ struct PrefillArgs {
     uint32_t* rs_done;        // [B*T*32] finished pieces per flagged row (indexed by row)
     double2* rs_cs;           // [B][T][64] cos, sin of (start + t) * inv_freq[i] (RoPE on Q or K)
     double* rs_part_o;        // [kRsSlots][128] unnormalised partial output rows
-    float2* rs_part_ml;       // [kRsSlots] (running max, sum)
+    double2* rs_part_ml;      // [kRsSlots] (running max, sum)
     int32_t rs_wgs;           // workgroups of the rescore kernel
 };
 
@@ -146,6 +146,21 @@ struct PrefillArgs {
 // quarter of the element, needs an element below ~4.7e-6 of the rms; 2^-17 = 7.6e-6 flags
 // those with a margin of 1.6.  Squared: min^2 * 128 < ratio^2 * sum x^2.
 constexpr double kRsFlagRatio2 = 1.0 / 17179869184.0;    // (2^-17)^2
+// Those errors were measured on rows whose running max m (log2 units) is at most ~6.  The
+// scores are fp32 sums of the products q_i k_i, so their error scales with sum |q_i k_i|,
+// which for the keys that carry a row's softmax is about twice |m| (random rows; a key far
+// above the others dominates the row and its own error cancels in the normalisation).  The
+// threshold therefore grows with |m| past kRsFlagScore: Q scaled by 16 (|m| ~ 85) has errors
+// ~16 times those above, and without this a few of its elements missed 64 ULP unflagged.
+constexpr double kRsFlagScore = 6.0;
+
+// Whether an output row (smallest element magnitude mn, sum of squares ss, running max m in
+// log2 units) goes to the fp64 rescore; NaN in mn or ss never flags here (the callers test
+// finiteness where a non-finite row can occur).
+__host__ __device__ inline bool rs_flag_row(double mn, double ss, float m) {
+    const double mm = static_cast<double>(m) * static_cast<double>(m) * (1.0 / (kRsFlagScore * kRsFlagScore));
+    return mn * mn * kD < kRsFlagRatio2 * (mm > 1.0 ? mm : 1.0) * ss;
+}
 constexpr int kRsSlots = 1024;                            // partial slots (rows x pieces)
 constexpr int kRsMaxPieces = 64;                          // pieces per row at most (one per lane)
 size_t rescore_bytes(int32_t batch, int32_t n_new);

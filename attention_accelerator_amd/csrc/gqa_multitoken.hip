@@ -502,7 +502,7 @@ __device__ __forceinline__ float mt_max(const PrefillArgs& a, bool chunk_keys, c
     bmax = swap32_max(swap16_max(bmax));
     const float m_new = bmax > t.m_run ? ceilf(bmax) : t.m_run;
     if (__ballot(m_new != t.m_run)) {
-        const int shift = (t.m_run == -INFINITY) ? 0 : static_cast<int>(t.m_run - m_new);
+        const int shift = (t.m_run == -INFINITY) ? 0 : max_shift(t.m_run, m_new);
 #pragma unroll
         for (int dt = 0; dt < 8; ++dt)
 #pragma unroll
@@ -601,7 +601,7 @@ __device__ __forceinline__ void mt_piece_end(const PrefillArgs& a, int b, int kv
         mn = fmin(mn, __shfl_xor(mn, 16));
         mn = fmin(mn, __shfl_xor(mn, 32));
         if (tok >= a.n_new) return;
-        if (g == 0 && a.rs_hdr && mn * mn * kD < kRsFlagRatio2 * ss)
+        if (g == 0 && a.rs_hdr && rs_flag_row(mn, ss, t.m_run))
             rs_append(a, static_cast<uint32_t>((static_cast<int64_t>(b) * a.n_new + tok) * kHq + kvh * kGroup + (n & 3)));
         uint16_t* orow = a.out + ((static_cast<int64_t>(b) * a.n_new + tok) * kHq + kvh * kGroup + (n & 3)) * kD;
 #pragma unroll
@@ -912,7 +912,7 @@ __global__ __launch_bounds__(256 * kW) void mt_merge_kernel(PrefillArgs a) {
 #pragma unroll
         for (int q = 0; q < kGroupP; ++q) mb = fmaxf(mb, ml[q].x);
         if (m != -INFINITY && mb != m) {
-            const int e = static_cast<int>(m - mb);
+            const int e = max_shift(m, mb);
             l = ldexp(l, e);
 #pragma unroll
             for (int j = 0; j < 8; ++j) o[j] = ldexp(o[j], e);
@@ -921,7 +921,7 @@ __global__ __launch_bounds__(256 * kW) void mt_merge_kernel(PrefillArgs a) {
 #pragma unroll
         for (int q = 0; q < kGroupP; ++q) {
             if (ml[q].x == -INFINITY) continue;
-            const int e = static_cast<int>(ml[q].x - m);
+            const int e = max_shift(ml[q].x, m);
             l += ldexp(static_cast<double>(ml[q].y), e);
 #pragma unroll
             for (int j = 0; j < 8; ++j) o[j] += ldexp(v[q][j], e);
@@ -942,7 +942,7 @@ __global__ __launch_bounds__(256 * kW) void mt_merge_kernel(PrefillArgs a) {
         ss += __shfl_xor(ss, d);
         mn = fmin(mn, __shfl_xor(mn, d));
     }
-    if ((threadIdx.x & 15) == 0 && a.rs_hdr && mn * mn * kD < kRsFlagRatio2 * ss)
+    if ((threadIdx.x & 15) == 0 && a.rs_hdr && rs_flag_row(mn, ss, m))
         rs_append(a, static_cast<uint32_t>((static_cast<int64_t>(b) * a.n_new + tok) * kHq + kvh * kGroup + (col & 3)));
     uint2* dst = reinterpret_cast<uint2*>(a.out + ((static_cast<int64_t>(b) * a.n_new + tok) * kHq + kvh * kGroup +
                                                    (col & 3)) * kD + d0);   // out is 8-byte aligned

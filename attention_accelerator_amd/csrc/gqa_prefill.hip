@@ -486,7 +486,7 @@ __device__ __forceinline__ float pf_next_max(f32x4_t (&sacc)[4], bool diag, int 
 // an fp32 group term pushed below 2^-149 is below 2^-149 of the new maximum's weight).
 __device__ __forceinline__ void pf_rescale(PfTile& t, float m_new) {
     if (__ballot(m_new != t.m_run)) {
-        const int shift = (t.m_run == -INFINITY) ? 0 : static_cast<int>(t.m_run - m_new);
+        const int shift = (t.m_run == -INFINITY) ? 0 : max_shift(t.m_run, m_new);
 #pragma unroll
         for (int dt = 0; dt < 8; ++dt)
 #pragma unroll
@@ -904,7 +904,7 @@ __global__ __launch_bounds__(kPfThreads) void prefill_attn_kernel(PrefillArgs a)
     // rescore as well (NaN fails the comparison).
     const bool q_bad_row = __shfl_xor(static_cast<int>(q_bad), 16) | __shfl_xor(static_cast<int>(q_bad), 32) |
                            __shfl_xor(static_cast<int>(q_bad), 48) | static_cast<int>(q_bad);
-    const bool flag = mn * mn * kD < kRsFlagRatio2 * ss || (unsafe >> 31) != 0u || q_bad_row || !(ss <= 1e300);
+    const bool flag = rs_flag_row(mn, ss, tl.m_run) || (unsafe >> 31) != 0u || q_bad_row || !(ss <= 1e300);
     if (g == 0 && a.rs_hdr && flag)
         rs_append(a, static_cast<uint32_t>((static_cast<int64_t>(b) * T + tq) * kHq + hq));
     {

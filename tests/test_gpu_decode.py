@@ -238,6 +238,22 @@ def test_invalid_device_lengths_give_nan_rows(dev, path, monkeypatch):
     assert_within_ulp(_oracle(good), out[[0, 2]], 64, "valid rows next to an invalid one")
 
 
+@pytest.mark.parametrize("path", ["single", "three"])
+def test_huge_scores(dev, path, monkeypatch):
+    """Q heads scaled by 2^40 and 2^100 (scores far beyond 2^24 in log2 units, a one-hot
+    softmax in the double golden): the running max and the pieces' (m, l) are doubles, so
+    the largest key keeps p = 1 in every piece and the merge weights stay exact; every row,
+    the scaled heads' and the others', within 64 ULP of the oracle."""
+    if path != "single":
+        monkeypatch.setenv("GQA_SINGLE_LAUNCH_MAX_KEYS", "0")
+    b = stimulus.decode_batch(4, 700, min_len=300, max_len=700, seed=41)
+    q = b.q.clone()
+    q[0, 3] = (q[0, 3].float() * 2.0 ** 100).to(torch.bfloat16)
+    q[2, 17] = (q[2, 17].float() * 2.0 ** 40).to(torch.bfloat16)
+    b = stimulus.DecodeBatch(q, b.k, b.v, b.seq_len, b.query_pos)
+    assert_within_ulp(_oracle(b), _run(b, dev), 64, f"huge scores ({path})")
+
+
 def test_host_validation_rejects(dev):
     b = stimulus.decode_batch(2, 64, lengths=torch.tensor([10, 20]), seed=16)
     q, k, v = b.q.to(dev), b.k.to(dev), b.v.to(dev)

@@ -76,6 +76,19 @@ def test_multi_all_rows_against_oracle(dev, n_new):
         assert (kc[b, :, s + n_new:] == to_codes(k[b, :, s + n_new:])).all()
 
 
+@pytest.mark.parametrize("q_scale,seed", [(16.0, 7), (64.0, 8)])
+def test_multi_peaked_scores(dev, q_scale, seed):
+    """Q scaled up by a power of two (a peaked softmax): the fp32 score sums err in
+    proportion to the scores, and the rows sent to the fp64 rescore follow the row's max;
+    every element within 64 ULP of the oracle (T = 16, four sequences)."""
+    starts = [900, 2100, 3000, 1777]
+    q, kn, vn, k, v = _chunk(starts, 16, 3100, seed)
+    q = (q.float() * q_scale).to(torch.bfloat16)
+    want = _oracle(q, kn, vn, k, v, starts)
+    got, _, _ = _run(q, kn, vn, k, v, starts, dev)
+    _check(want, got, f"T=16, Q x{q_scale:g}")
+
+
 def test_multi_no_rope(dev):
     starts = [3, 260, 1500]
     q, kn, vn, k, v = _chunk(starts, 3, 1510, 40)

@@ -103,6 +103,20 @@ def test_prefill_staging_ranges(dev, case):
     assert_within_ulp(want.reshape(-1, 128), got.reshape(-1, 128), 64, f"staging {case}")
 
 
+@pytest.mark.parametrize("q_scale,seed", [(16.0, 5), (64.0, 6)])
+def test_prefill_peaked_scores(dev, q_scale, seed):
+    """Q scaled up by a power of two (a peaked softmax: running max ~85 or ~340 in log2
+    units against ~6 for N(0,1)).  The kernel's scores are fp32 sums whose error grows with
+    the scores, so the rows it sends to the fp64 rescore must follow the row's max: every
+    element within 64 ULP of the oracle, all 200 tokens of both sequences."""
+    starts = [1500, 2300]
+    q, k_new, v_new, k, v = _chunk(2, 100, 2500, starts, seed)
+    q = (q.float() * q_scale).to(torch.bfloat16)
+    want = _oracle(q, k_new, v_new, k, v, starts, rope_q=False)
+    got, _, _ = _run(q, k_new, v_new, k, v, starts, dev, rope_q=False)
+    assert_within_ulp(want, got, 64, f"prefill, Q x{q_scale:g}")
+
+
 def test_prefill_no_rope(dev):
     starts = [70, 150]
     q, kn, vn, k, v = _chunk(2, 33, 200, starts, 5)
