@@ -155,9 +155,11 @@ constexpr double kRsFlagRatio2 = 1.0 / 17179869184.0;    // (2^-17)^2
 constexpr double kRsFlagScore = 6.0;
 
 // Whether an output row (smallest element magnitude mn, sum of squares ss, running max m in
-// log2 units) goes to the fp64 rescore; NaN in mn or ss never flags here (the callers test
-// finiteness where a non-finite row can occur).
+// log2 units) goes to the fp64 rescore.  A row that is not finite always does: scores past
+// the fp32 range (Q and K both far from 1, e.g. 2^100 and 2^40) make the MFMA paths' row NaN
+// where the double golden is finite.
 __host__ __device__ inline bool rs_flag_row(double mn, double ss, float m) {
+    if (!(ss <= 1e300)) return true;
     const double mm = static_cast<double>(m) * static_cast<double>(m) * (1.0 / (kRsFlagScore * kRsFlagScore));
     return mn * mn * kD < kRsFlagRatio2 * (mm > 1.0 ? mm : 1.0) * ss;
 }

@@ -900,11 +900,11 @@ __global__ __launch_bounds__(kPfThreads) void prefill_attn_kernel(PrefillArgs a)
     mn = fmin(mn, __shfl_xor(mn, 16));
     mn = fmin(mn, __shfl_xor(mn, 32));
     if (!q_ok) return;
-    // Rows that read a marked block, a Q row out of range, or a non-finite sum go to the
-    // rescore as well (NaN fails the comparison).
+    // Rows that read a marked block or whose Q row is out of range go to the rescore as well
+    // (rs_flag_row takes the rows whose sum is not finite).
     const bool q_bad_row = __shfl_xor(static_cast<int>(q_bad), 16) | __shfl_xor(static_cast<int>(q_bad), 32) |
                            __shfl_xor(static_cast<int>(q_bad), 48) | static_cast<int>(q_bad);
-    const bool flag = rs_flag_row(mn, ss, tl.m_run) || (unsafe >> 31) != 0u || q_bad_row || !(ss <= 1e300);
+    const bool flag = rs_flag_row(mn, ss, tl.m_run) || (unsafe >> 31) != 0u || q_bad_row;
     if (g == 0 && a.rs_hdr && flag)
         rs_append(a, static_cast<uint32_t>((static_cast<int64_t>(b) * T + tq) * kHq + hq));
     {

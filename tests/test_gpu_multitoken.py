@@ -89,6 +89,22 @@ def test_multi_peaked_scores(dev, q_scale, seed):
     _check(want, got, f"T=16, Q x{q_scale:g}")
 
 
+@pytest.mark.parametrize("q_exp,k_exp", [(100, 40), (64, 64)])
+def test_multi_scores_past_fp32_range(dev, q_exp, k_exp):
+    """One Q head scaled by 2^q_exp and one KV head's keys (cached and new) by 2^k_exp: their
+    dot products pass the fp32 range, so the MFMA kernels' rows for them are not finite, and
+    those rows go to the fp64 rescore, which matches the double golden; every row within
+    64 ULP of the oracle."""
+    starts = [500, 300]
+    q, kn, vn, k, v = _chunk(starts, 8, 700, 3)
+    q[0, :, 5] = (q[0, :, 5].float() * 2.0 ** q_exp).to(torch.bfloat16)
+    k[0, 1, :500] = (k[0, 1, :500].float() * 2.0 ** k_exp).to(torch.bfloat16)
+    kn[0, :, 1] = (kn[0, :, 1].float() * 2.0 ** k_exp).to(torch.bfloat16)
+    want = _oracle(q, kn, vn, k, v, starts)
+    got, _, _ = _run(q, kn, vn, k, v, starts, dev)
+    _check(want, got, f"T=8, Q x2^{q_exp}, K x2^{k_exp}")
+
+
 def test_multi_no_rope(dev):
     starts = [3, 260, 1500]
     q, kn, vn, k, v = _chunk(starts, 3, 1510, 40)
