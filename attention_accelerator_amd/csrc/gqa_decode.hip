@@ -36,8 +36,9 @@
 //  * Q is rotated at query_position in double and scaled by scale*log2(e) in double.
 //  * Scores: fp64 MFMA (v_mfma_f64_4x4x4_4b_f64) of the K values (BF16, exact in double;
 //    with RoPE on K the row is rotated in double first) and the fp64 Q.
-//  * The running max m is kept integer-valued (m = ceil(max score)), so every rescale of
-//    the accumulator and every combine weight is an exact power of two.
+//  * The running max m is kept integer-valued in double (m = ceil(max score)), so every
+//    rescale of the accumulator and every combine weight is an exact power of two, also
+//    for scores past 2^24, where an fp32 m could not stay within a few units of them.
 //  * p = exp2(s - m) in fp64; weighted V by fp64 MFMA; l, the merge and the division in
 //    fp64; the row is rounded double -> f32 -> BF16 as the reference's f32_to_bf16.
 //
