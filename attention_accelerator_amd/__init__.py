@@ -7,6 +7,7 @@ Public surface:
   kv_append, kv_append_paged   KV append with RoPE on insert (HIP kernel)
   rope_half_split              rotate_half RoPE of BF16 rows (HIP kernel)
   decode_workspace_bytes       workspace size of a decode call
+  prefill_rescored_rows        output rows a prefill call recomputed in fp64 (measurement)
 Tools: check (output checker), mem_runner (.mem stimulus -> GPU -> .mem output),
 memfmt (.mem codec), stimulus (synthetic inputs), build (hipcc in-tree build).
 """
@@ -14,7 +15,8 @@ from .attention import (DEFAULT_SCALE, GROUP_SIZE, HEAD_DIM, N_KV_HEADS, N_Q_HEA
                         ROPE_THETA, PreparedDecode, PreparedPrefill, decode_workspace_bytes, gqa_attention,
                         gqa_decode, gqa_decode_paged, gqa_prefill, kv_append, kv_append_paged,
                         make_params, new_workspace,
-                        prefill_workspace_bytes, profile_enable, profile_read, rope_half_split,
+                        prefill_rescored_rows, prefill_workspace_bytes, profile_enable, profile_read,
+                        rope_half_split,
                         validate_lengths)
 from ._lib import GqaConfigError, GqaError  # noqa: F401
 

@@ -38,6 +38,7 @@ EXPORTS = (
     "gqa_kv_append_paged_bf16",
     "gqa_prefill_workspace_bytes",
     "gqa_prefill_bf16",
+    "gqa_prefill_rescored_rows_offset",
     "gqa_kv_append_bf16",
     "gqa_rope_rows_bf16",
     "gqa_profile_enable",
@@ -144,6 +145,9 @@ def lib() -> ctypes.CDLL:
                                    ctypes.POINTER(GqaKvLayout), vp, ctypes.c_int32, ctypes.c_int32,
                                    vp, vp, ctypes.c_size_t, vp]
     L.gqa_prefill_bf16.restype = ctypes.c_int
+    L.gqa_prefill_rescored_rows_offset.argtypes = [ctypes.POINTER(GqaParams), ctypes.c_int32,
+                                                   ctypes.c_int32, ctypes.c_int32]
+    L.gqa_prefill_rescored_rows_offset.restype = ctypes.c_size_t
     L.gqa_kv_append_bf16.argtypes = [ctypes.POINTER(GqaParams), vp, vp, vp, vp,
                                      ctypes.POINTER(GqaKvLayout), vp, ctypes.c_int32, ctypes.c_int32,
                                      vp]

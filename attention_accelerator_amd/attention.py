@@ -268,12 +268,32 @@ def _start_tensor(start: Lengths, batch: int, capacity: int, n_new: int, device)
     return host.contiguous().to(device)
 
 
+def _capacity_arg(capacity) -> int:
+    if isinstance(capacity, GqaParams):
+        raise TypeError("prefill workspace size: the third argument is the cache capacity (positions "
+                        "per sequence); pass params as a keyword, params=...")
+    return int(capacity)
+
+
 def prefill_workspace_bytes(batch: int, n_new: int, capacity: int, params: Optional[GqaParams] = None) -> int:
     """Workspace bytes of a gqa_prefill call: batch sequences, n_new new tokens each, a cache
     of `capacity` positions per sequence (chunks of more than 16 tokens stage 512 bytes per
     position of every (sequence, KV head) in it)."""
     p = params or make_params()
-    return int(lib().gqa_prefill_workspace_bytes(ctypes.byref(p), int(batch), int(n_new), int(capacity)))
+    return int(lib().gqa_prefill_workspace_bytes(ctypes.byref(p), int(batch), int(n_new), _capacity_arg(capacity)))
+
+
+def prefill_rescored_rows(workspace: torch.Tensor, batch: int, n_new: int, capacity: int,
+                          params: Optional[GqaParams] = None) -> int:
+    """How many output rows the last gqa_prefill call on `workspace` recomputed in fp64 (the
+    rows its MFMA kernels may have computed outside 64 BF16 ULP).  Synchronises the device."""
+    p = params or make_params()
+    off = int(lib().gqa_prefill_rescored_rows_offset(ctypes.byref(p), int(batch), int(n_new),
+                                                     _capacity_arg(capacity)))
+    if off == 0:
+        check(_lib.GQA_ERR_INVALID_CONFIG, "gqa_prefill_rescored_rows_offset")
+    word = workspace.view(torch.uint8)[off:off + 4].cpu().numpy().view("<u4")
+    return int(word[0])
 
 
 def gqa_prefill(q: torch.Tensor, k_new: torch.Tensor, v_new: torch.Tensor, k_cache: torch.Tensor,
@@ -364,6 +384,10 @@ class PreparedPrefill:
         if status:
             check(status, "gqa_prefill_bf16")
         return self.out
+
+    def rescored_rows(self) -> int:
+        """Output rows the last call recomputed in fp64 (synchronises the device)."""
+        return prefill_rescored_rows(self.workspace, self.batch, self.n_new, self.layout.capacity, self.params)
 
 
 def kv_append(k_new: torch.Tensor, v_new: torch.Tensor, k_cache: torch.Tensor,

@@ -165,28 +165,59 @@ DecodePlan plan_decode(int32_t batch, int32_t capacity, bool paged, int64_t max_
 }
 
 // Rescore region of a prefill or multi-token workspace: header, flagged rows, per-row piece
-// counters, the chunk's cos/sin table, partial slots.
-size_t rescore_bytes(int32_t batch, int32_t n_new) {
+// counters, the chunk's cos/sin table, partial slots, the per-row running maxima and the key
+// and V statistics the flag decision reads (ncb chunk blocks of nr rows of prefix maxima).
+namespace {
+struct RsLayout {
+    size_t rows, done, cs, part_o, part_ml, m, kc, dc, kpre, dpre, kblk, dblk, total;
+};
+
+RsLayout rs_layout(int32_t batch, int32_t n_new, int32_t ncb, int32_t nr, int32_t nblk) {
     const size_t rows = static_cast<size_t>(batch) * n_new * kHq;
     const size_t toks = static_cast<size_t>(batch) * n_new;
-    return 256 + 2 * align_up(rows * sizeof(uint32_t), 256) + align_up(toks * kPairs * sizeof(double2), 256) +
-           align_up(size_t{kRsSlots} * kD * sizeof(double), 256) + align_up(size_t{kRsSlots} * sizeof(double2), 256);
+    const size_t bh = static_cast<size_t>(batch) * kHkv;
+    const size_t pre = bh * static_cast<size_t>(ncb) * static_cast<size_t>(nr);
+    RsLayout l{};
+    l.rows = 256;
+    l.done = l.rows + align_up(rows * sizeof(uint32_t), 256);
+    l.cs = l.done + align_up(rows * sizeof(uint32_t), 256);
+    l.part_o = l.cs + align_up(toks * kPairs * sizeof(double2), 256);
+    l.part_ml = l.part_o + align_up(size_t{kRsSlots} * kD * sizeof(double), 256);
+    l.m = l.part_ml + align_up(size_t{kRsSlots} * sizeof(double2), 256);
+    l.kc = l.m + align_up(rows * sizeof(float), 256);
+    l.dc = l.kc + align_up(bh * static_cast<size_t>(ncb) * 8 * sizeof(uint32_t), 256);
+    l.kpre = l.dc + align_up(bh * static_cast<size_t>(ncb) * kD * sizeof(uint32_t), 256);
+    l.dpre = l.kpre + align_up(pre * 8 * sizeof(uint32_t), 256);
+    l.kblk = l.dpre + align_up(pre * kD * sizeof(uint16_t), 256);
+    l.dblk = l.kblk + align_up(bh * static_cast<size_t>(nblk) * 8 * sizeof(uint32_t), 256);
+    l.total = l.dblk + align_up(bh * static_cast<size_t>(nblk) * (kD / 2) * sizeof(uint32_t), 256);
+    return l;
+}
+}  // namespace
+
+size_t rescore_bytes(int32_t batch, int32_t n_new, int32_t ncb, int32_t nr, int32_t nblk) {
+    return rs_layout(batch, n_new, ncb, nr, nblk).total;
 }
 
-void rescore_layout(PrefillArgs& a, void* base) {
-    const size_t rows = static_cast<size_t>(a.batch) * a.n_new * kHq;
+void rescore_layout(PrefillArgs& a, void* base, int32_t ncb, int32_t nr, int32_t nblk) {
+    const RsLayout l = rs_layout(a.batch, a.n_new, ncb, nr, nblk);
     char* p = static_cast<char*>(base);
     a.rs_hdr = reinterpret_cast<uint32_t*>(p);
-    p += 256;
-    a.rs_rows = reinterpret_cast<uint32_t*>(p);
-    p += align_up(rows * sizeof(uint32_t), 256);
-    a.rs_done = reinterpret_cast<uint32_t*>(p);
-    p += align_up(rows * sizeof(uint32_t), 256);
-    a.rs_cs = reinterpret_cast<double2*>(p);
-    p += align_up(static_cast<size_t>(a.batch) * a.n_new * kPairs * sizeof(double2), 256);
-    a.rs_part_o = reinterpret_cast<double*>(p);
-    p += align_up(size_t{kRsSlots} * kD * sizeof(double), 256);
-    a.rs_part_ml = reinterpret_cast<double2*>(p);
+    a.rs_rows = reinterpret_cast<uint32_t*>(p + l.rows);
+    a.rs_done = reinterpret_cast<uint32_t*>(p + l.done);
+    a.rs_cs = reinterpret_cast<double2*>(p + l.cs);
+    a.rs_part_o = reinterpret_cast<double*>(p + l.part_o);
+    a.rs_part_ml = reinterpret_cast<double2*>(p + l.part_ml);
+    a.rs_m = reinterpret_cast<float*>(p + l.m);
+    a.rs_kc = reinterpret_cast<uint32_t*>(p + l.kc);
+    a.rs_dc = reinterpret_cast<uint32_t*>(p + l.dc);
+    a.rs_kpre = reinterpret_cast<uint32_t*>(p + l.kpre);
+    a.rs_dpre = reinterpret_cast<uint16_t*>(p + l.dpre);
+    a.rs_ncb = ncb;
+    a.rs_nr = nr;
+    a.rs_kblk = reinterpret_cast<uint32_t*>(p + l.kblk);
+    a.rs_dblk = reinterpret_cast<uint32_t*>(p + l.dblk);
+    a.rs_nblk = nblk;
     // One-wave workgroups, one per SIMD (the kernel's registers allow one wave per SIMD):
     // the flagged rows are cut into about as many (row, piece) pairs as run at once.
     const int32_t wgs = stream_wgs();
@@ -541,8 +572,18 @@ size_t gqa_prefill_workspace_bytes(const gqa_params_t* params, int32_t batch, in
     // The multi-token path stages nothing: the chunk's unrounded keys enter through the
     // scores its preparation kernel forms, and the cache is read as stored.
     if (use_multi(n_new))
-        return align_up(prefill_multi_bytes(batch, n_new, multi_wgs(n_new)), 256) + rescore_bytes(batch, n_new);
-    return align_up(prefill_stage_bytes(batch, n_new, capacity), 256) + rescore_bytes(batch, n_new);
+        return align_up(prefill_multi_bytes(batch, n_new, multi_wgs(n_new)), 256) +
+               rescore_bytes(batch, n_new, 1, n_new, 0);
+    return align_up(prefill_stage_bytes(batch, n_new, capacity), 256) +
+           rescore_bytes(batch, n_new, prefill_chunk_blocks(n_new), 64, prefill_cache_blocks(capacity));
+}
+
+size_t gqa_prefill_rescored_rows_offset(const gqa_params_t* params, int32_t batch, int32_t n_new,
+                                        int32_t capacity) {
+    if (!gqa_prefill_workspace_bytes(params, batch, n_new, capacity)) return 0;
+    // The rescore region (its first word: the flagged-row count) follows the path's own part.
+    if (use_multi(n_new)) return align_up(prefill_multi_bytes(batch, n_new, multi_wgs(n_new)), 256);
+    return align_up(prefill_stage_bytes(batch, n_new, capacity), 256);
 }
 
 int gqa_kv_append_bf16(const gqa_params_t* params, const uint16_t* k_new, const uint16_t* v_new,
@@ -592,10 +633,11 @@ int gqa_prefill_bf16(const gqa_params_t* params, const uint16_t* q, const uint16
     if (multi) {
         prefill_multi_layout(a, workspace, multi_wgs(n_new));
         a.skew_pm = xcd_skew_pm(multi_waves(n_new) <= 2 ? 40 : 0);
-        rescore_layout(a, ws + align_up(prefill_multi_bytes(batch, n_new, multi_wgs(n_new)), 256));
+        rescore_layout(a, ws + align_up(prefill_multi_bytes(batch, n_new, multi_wgs(n_new)), 256), 1, n_new, 0);
     } else {
         prefill_stage_layout(a, workspace);
-        rescore_layout(a, ws + align_up(prefill_stage_bytes(batch, n_new, kv->capacity), 256));
+        rescore_layout(a, ws + align_up(prefill_stage_bytes(batch, n_new, kv->capacity), 256),
+                       prefill_chunk_blocks(n_new), 64, prefill_cache_blocks(kv->capacity));
     }
     hipStream_t s = static_cast<hipStream_t>(stream);
     hipEvent_t* ev = profile_slot();
@@ -603,6 +645,7 @@ int gqa_prefill_bf16(const gqa_params_t* params, const uint16_t* q, const uint16
     if (multi) {
         // The preparation kernel of the multi-token path appends the chunk's rows itself.
         hipError_t e = launch_prefill_multi(a, s, ev);
+        if (e == hipSuccess) e = launch_rs_flag(a, s);
         if (e == hipSuccess) e = launch_rescore(a, s);
         return e == hipSuccess ? GQA_OK : GQA_ERR_HIP;
     }
@@ -611,6 +654,8 @@ int gqa_prefill_bf16(const gqa_params_t* params, const uint16_t* q, const uint16
     if (ev) (void)hipEventRecord(ev[1], s);
     if (e == hipSuccess) e = launch_prefill_attention(a, s);
     if (ev) (void)hipEventRecord(ev[2], s);
+    if (e == hipSuccess) e = launch_prefill_stat_reduce(a, s);
+    if (e == hipSuccess) e = launch_rs_flag(a, s);
     if (e == hipSuccess) e = launch_rescore(a, s);
     return e == hipSuccess ? GQA_OK : GQA_ERR_HIP;
 }

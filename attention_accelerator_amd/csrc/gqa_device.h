@@ -166,6 +166,21 @@ __device__ __forceinline__ double wave_max_f64(double x) {
     return swap_max_f64<true>(swap_max_f64<false>(x));
 }
 
+// Per-half maxima of two pairs of 16-bit codes (v_pk_max_u16): for BF16 magnitudes (sign
+// cleared) the larger code is the larger magnitude, NaN and infinity above every finite value.
+__device__ __forceinline__ uint32_t pk_max_u16(uint32_t x, uint32_t y) {
+    typedef unsigned short u16x2_t __attribute__((ext_vector_type(2)));
+    return __builtin_bit_cast(uint32_t, __builtin_elementwise_max(__builtin_bit_cast(u16x2_t, x),
+                                                                  __builtin_bit_cast(u16x2_t, y)));
+}
+
+// acc + the squares of the two BF16 values in w (v_dot2_f32_bf16, fp32 accumulation).
+__device__ __forceinline__ float bf16x2_sq_acc(uint32_t w, float acc) {
+    typedef __bf16 b16x2_t __attribute__((ext_vector_type(2)));
+    const b16x2_t v = __builtin_bit_cast(b16x2_t, w);
+    return __builtin_amdgcn_fdot2_f32_bf16(v, v, acc, false);
+}
+
 __device__ __forceinline__ float wave_sum(float x) { return cross_row_sum(row16_sum(x)); }
 __device__ __forceinline__ float wave_max(float x) { return cross_row_max(row16_max(x)); }
 

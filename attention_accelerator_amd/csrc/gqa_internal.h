@@ -127,8 +127,8 @@ struct PrefillArgs {
     float* chunk_s;           // [B][8][16W][4W] scores of the chunk's keys u per column (log2 units)
     int32_t n_wgs;            // persistent workgroups of the multi-token stream kernel
     int32_t skew_pm;          // XCD weighting of the ranges (per mille of a range)
-    // fp64 rescore of the output rows the MFMA kernels flag (an element within
-    // kRsFlagRatio of its row's rms from zero); rs_hdr nullptr: off.
+    // fp64 rescore of the output rows the MFMA kernels may have computed outside 64 BF16 ULP
+    // (rs_flag_kernel decides, rescore_kernel recomputes); rs_hdr nullptr: off.
     uint32_t* rs_hdr;         // [1]: flagged rows
     uint32_t* rs_rows;        // [B*T*32] flagged rows, (b*T + t)*32 + q_head, in flagging order
     uint32_t* rs_done;        // [B*T*32] finished pieces per flagged row (indexed by row)
@@ -136,38 +136,89 @@ struct PrefillArgs {
     double* rs_part_o;        // [kRsSlots][128] unnormalised partial output rows
     double2* rs_part_ml;      // [kRsSlots] (running max, sum)
     int32_t rs_wgs;           // workgroups of the rescore kernel
+    // What the flag decision reads besides the output rows and Q:
+    float* rs_m;              // [B*T*32] the row's running max (log2 units); NaN: always rescore
+    // Over the keys of segment (b, kv head) before chunk block cb (cb = 0: the cached keys,
+    // which every new token sees): the largest squared norm of each pair group (dims 8g ..
+    // 8g+7 and 64+8g .. 64+8g+7, g < 8: the RoPE pairs, so a norm does not change under
+    // rotation), fp32 bits, and the largest |V| of each dim, BF16 bits.  Maxima of
+    // non-negative values: the multi-token stream kernel raises entry 0 by atomicMax on bit
+    // patterns, prefill_stat_reduce_kernel writes every entry (order-independent results).
+    uint32_t* rs_kc;          // [B*8][rs_ncb][8]
+    uint32_t* rs_dc;          // [B*8][rs_ncb][128]
+    // The same maxima over the chunk's keys, running over the key positions: entry (cb, r)
+    // covers every key up to row r of chunk block cb (prefill: the 64-position blocks that
+    // hold chunk keys, r = position % 64, including the cached rows at the start of the
+    // first block; multi-token: one block of T rows, r = token).  Entry (cb, rs_nr - 1) is
+    // block cb's maximum.
+    uint32_t* rs_kpre;        // [B*8][rs_ncb][rs_nr][8]
+    uint16_t* rs_dpre;        // [B*8][rs_ncb][rs_nr][128]
+    int32_t rs_ncb;
+    int32_t rs_nr;
+    // Prefill: the maxima of each 64-position block of cached keys (the staging kernel writes
+    // them, prefill_stat_reduce_kernel folds them into rs_kc / rs_dc); |V| codes packed two
+    // per dword (dims 2c, 2c + 1).
+    uint32_t* rs_kblk;        // [B*8][rs_nblk][8]
+    uint32_t* rs_dblk;        // [B*8][rs_nblk][64]
+    int32_t rs_nblk;
 };
 
-// Rescore: an output row is recomputed in fp64 when one of its elements lies closer to zero
-// than kRsFlagRatio times the row's rms.  The largest error measured on the MFMA paths (the
-// excess over the output's own BF16 rounding) is 8.6e-7 of the row's rms with three BF16
-// parts (4.8M outputs of N(0,1) inputs) and 8.9e-7 and 1.18e-6 with the prefill kernel's two
-// fp16 parts (two draws of 2.1M outputs), so a 64-BF16-ULP miss, which needs an error of a
-// quarter of the element, needs an element below ~4.7e-6 of the rms; 2^-17 = 7.6e-6 flags
-// those with a margin of 1.6.  Squared: min^2 * 128 < ratio^2 * sum x^2.
+// Rescore: an output row of the MFMA paths is recomputed in fp64 when one of its elements may
+// lie within the paths' error of zero, where 64 BF16 ULP of the element is less than that
+// error.  The paths' error in output dim j follows two things:
+//   * the error of each score, a sum of products q_i k_i accumulated in fp32: it grows with
+//     sum |q_i k_i|, which may be far above the score itself when the products cancel.
+//     By Cauchy-Schwarz over the 8 pair groups G, sum |q_i k_i| <= E = scale * log2(e) *
+//     sum_G |q_G| * max_k |k_G| (the max over the keys the row sees).
+//   * the spread of V in dim j: a score error moves weight between keys, which changes
+//     output j in proportion to dim j's V values.
+// So each element is measured in units of its dim's V scale, y_j = x_j / D_j with D_j =
+// max_k |v_kj| over the keys the row sees, and a row is rescored when
+//     min_j |y_j| < 2^-17 * F * rms(y),   F = max(1, |m| / 6, E / 32)
+// (m: the row's running max, log2 units).  For N(0,1) inputs (E ~ 23-27, |m| ~ 5-7, F = 1)
+// the largest error measured on the MFMA paths, beyond the output's own BF16 rounding, is
+// 1.18e-6 of the row's rms (two draws of 2.1M outputs of the prefill kernel; 8.6e-7 with
+// the multi-token kernels' three BF16 parts); a 64-ULP miss needs an error of a quarter of
+// the element, so an element below ~4.7e-6 rms, and 2^-17 = 7.6e-6 flags those with a
+// margin of 1.6 (about 7e-4 of N(0,1) rows).  Rows whose products cancel (dims i and i+64
+// of Q equal and of K opposite, x 2^6: E ~ 1.1e5 with |m| ~ 2) err about 8 times less per
+// unit of E than N(0,1) rows in a CPU emulation of the kernels' fp32 accumulation order,
+// and rows whose first-half products are all positive and cancel against the second half
+// (the largest partial sums the 4 x 32-dim MFMA steps can carry) about 1.9 times less;
+// outlier V channels (x 2^6 .. 2^14) err in proportion to their own D_j.
+// Squared: 128 min y^2 < 2^-34 F^2 sum y^2.
 constexpr double kRsFlagRatio2 = 1.0 / 17179869184.0;    // (2^-17)^2
-// Those errors were measured on rows whose running max m (log2 units) is at most ~6.  The
-// scores are fp32 sums of the products q_i k_i, so their error scales with sum |q_i k_i|,
-// which for the keys that carry a row's softmax is about twice |m| (random rows; a key far
-// above the others dominates the row and its own error cancels in the normalisation).  The
-// threshold therefore grows with |m| past kRsFlagScore: Q scaled by 16 (|m| ~ 85) has errors
-// ~16 times those above, and without this a few of its elements missed 64 ULP unflagged.
 constexpr double kRsFlagScore = 6.0;
+constexpr double kRsFlagE = 32.0;
 
-// Whether an output row (smallest element magnitude mn, sum of squares ss, running max m in
-// log2 units) goes to the fp64 rescore.  A row that is not finite always does: scores past
-// the fp32 range (Q and K both far from 1, e.g. 2^100 and 2^40) make the MFMA paths' row NaN
-// where the double golden is finite.
-__host__ __device__ inline bool rs_flag_row(double mn, double ss, float m) {
-    if (!(ss <= 1e300)) return true;
-    const double mm = static_cast<double>(m) * static_cast<double>(m) * (1.0 / (kRsFlagScore * kRsFlagScore));
-    return mn * mn * kD < kRsFlagRatio2 * (mm > 1.0 ? mm : 1.0) * ss;
+// The decision for one row: mn2 = smallest y_j^2 over the dims with D_j > 0, ss = sum y^2,
+// m = running max, e = E.  Not finite: rescored.
+__host__ __device__ inline bool rs_flag_decide(double mn2, double ss, double m, double e) {
+    if (!(ss <= 1e300) || !(e <= 1e300) || !(m == m)) return true;
+    double f2 = 1.0;
+    const double fm = m * m * (1.0 / (kRsFlagScore * kRsFlagScore));
+    const double fe = e * e * (1.0 / (kRsFlagE * kRsFlagE));
+    f2 = fm > f2 ? fm : f2;
+    f2 = fe > f2 ? fe : f2;
+    return mn2 * kD < kRsFlagRatio2 * f2 * ss;
 }
 constexpr int kRsSlots = 1024;                            // partial slots (rows x pieces)
 constexpr int kRsMaxPieces = 64;                          // pieces per row at most (one per lane)
-size_t rescore_bytes(int32_t batch, int32_t n_new);
-void rescore_layout(PrefillArgs& a, void* base);
+// Rescore region of a workspace; ncb, nr: the chunk-prefix blocks and rows (prefill:
+// ceil(T / 64) + 1 and 64; multi-token: 1 and T); nblk: 64-position blocks of the cache
+// (prefill; 0 for multi-token).
+size_t rescore_bytes(int32_t batch, int32_t n_new, int32_t ncb, int32_t nr, int32_t nblk);
+void rescore_layout(PrefillArgs& a, void* base, int32_t ncb, int32_t nr, int32_t nblk);
+// Prefill: the cached-key maxima from the staging kernel's block maxima.
+hipError_t launch_prefill_stat_reduce(const PrefillArgs& a, hipStream_t stream);
+// The flag decision over every output row (after the MFMA kernels), then the rescore.
+hipError_t launch_rs_flag(const PrefillArgs& a, hipStream_t stream);
 hipError_t launch_rescore(const PrefillArgs& a, hipStream_t stream);
+
+// Chunk blocks of the prefill path's prefix statistics (64-position blocks holding chunk keys).
+__host__ __device__ constexpr int32_t prefill_chunk_blocks(int32_t n_new) { return (n_new + 63) / 64 + 1; }
+// 64-position blocks of a cache of `capacity` positions (the staging planes' blocks).
+__host__ __device__ constexpr int32_t prefill_cache_blocks(int32_t capacity) { return (capacity + 63) / 64; }
 
 // Appends a flagged output row (device side).
 __device__ __forceinline__ void rs_append(const PrefillArgs& a, uint32_t row) {

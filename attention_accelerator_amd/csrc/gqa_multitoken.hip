@@ -264,6 +264,10 @@ __global__ __launch_bounds__(256) void mt_prepare_kernel(PrefillArgs a) {
     // Row u of a wave's share padded by one double, so that the final pass (consecutive
     // threads, consecutive u) reads distinct banks.
     __shared__ double part_s[4][kU][kCols + 1];
+    // The chunk rows' statistics for the rescore flag: squared pair-group norms of the rotated
+    // K rows (fp32 bits) and |V| codes, per token.
+    __shared__ uint32_t kn_s[kU][8];
+    __shared__ uint16_t vd_s[kU][kD];
     const bool rope_q = (a.flags & 1u) != 0;
     const bool rope_k = (a.flags & 2u) != 0;
     if (rope_q || rope_k)
@@ -350,6 +354,16 @@ __global__ __launch_bounds__(256) void mt_prepare_kernel(PrefillArgs a) {
                 a.v[ce + lane] = avx[r];
                 a.v[ce + lane + kPairs] = avy[r];
             }
+            if (a.rs_hdr) {
+                // Lane i holds pair i of the row: its group is i / 8.
+                float sq = static_cast<float>(xr * xr + yr * yr);
+                sq += __shfl_xor(sq, 1);
+                sq += __shfl_xor(sq, 2);
+                sq += __shfl_xor(sq, 4);
+                if ((lane & 7) == 0) kn_s[u][lane >> 3] = __float_as_uint(sq);
+                vd_s[u][lane] = avx[r] & 0x7fffu;
+                vd_s[u][lane + kPairs] = avy[r] & 0x7fffu;
+            }
         }
     }
 #pragma unroll
@@ -370,6 +384,26 @@ __global__ __launch_bounds__(256) void mt_prepare_kernel(PrefillArgs a) {
         }
     }
     __syncthreads();
+    if (a.rs_hdr && threadIdx.x < 8 + kD) {
+        // Running maxima over the chunk's tokens (rescore flag: token t sees chunk keys <= t),
+        // and the cached-key maxima of this segment cleared for the stream kernel.
+        const int64_t bh = static_cast<int64_t>(b) * kHkv + kvh;
+        const int c = threadIdx.x;
+        uint32_t run = 0u;
+        for (int u = 0; u < T; ++u) {
+            if (c < 8) {
+                run = max(run, kn_s[u][c]);
+                a.rs_kpre[(bh * T + u) * 8 + c] = run;
+            } else {
+                run = max(run, static_cast<uint32_t>(vd_s[u][c - 8]));
+                a.rs_dpre[(bh * T + u) * kD + c - 8] = static_cast<uint16_t>(run);
+            }
+        }
+        if (c < 8)
+            a.rs_kc[bh * 8 + c] = 0u;
+        else
+            a.rs_dc[bh * kD + c - 8] = 0u;
+    }
     float* cs_out = a.chunk_s + (static_cast<int64_t>(b) * kHkv + kvh) * kCols * kU;
     for (int i = threadIdx.x; i < kCols * kU; i += blockDim.x) {
         const int c = i / kU;
@@ -437,14 +471,45 @@ __device__ __forceinline__ void mt_flush(MtState& t) {
     t.grp = 0;
 }
 
+// The cached keys' statistics of a piece for the rescore flag (rs_kc / rs_dc), kept per lane
+// until the piece ends and formed without branches (a branch between an MFMA and the read of
+// its result can lose the wait states the read needs).
+//  * One tile (W = 1, one wave per SIMD, registers to spare): from the operands the wave
+//    already holds.  K: lane (g, n) reads key 16 kt + n, dims 32 kb + 8g .. +7 in slice kb,
+//    so slices kb and kb + 2 together hold pair group 4 (kb & 1) + g whole: kmax[kb & 1].
+//    V: the V^T operand of dim tile dt gives lane (g, n) 8 keys of dim 16 dt + n: vmax[dt].
+//  * Two or four tiles (their registers are all in use): each wave reads its 32/W keys of
+//    the window from LDS after the window's V^T P^T.  K: lane l takes key (l >> 3) (+ 8 j)
+//    and the two 16-byte chunks of pair group l & 7: kmax[0].  V: lane l takes dims 2l and
+//    2l + 1 of each of its keys: vmax[0].
+template <int kW>
+struct MtStats {
+    static constexpr int kNk = kW == 1 ? 2 : 1;
+    static constexpr int kNv = kW == 1 ? 8 : 1;
+    uint32_t kmax[kNk];                             // squared group norms, fp32 bits
+    uint32_t vmax[kNv];                             // two |V| codes per dword
+};
+
+template <int kW>
+__device__ __forceinline__ void mt_stats_reset(MtStats<kW>& ms) {
+#pragma unroll
+    for (int i = 0; i < MtStats<kW>::kNk; ++i) ms.kmax[i] = 0u;
+#pragma unroll
+    for (int i = 0; i < MtStats<kW>::kNv; ++i) ms.vmax[i] = 0u;
+}
+
 // The stages of one 32-key window [key0, key0 + 32) of a piece ending at k_b, for this
-// wave's tile.  mt_qk: the raw scores S^T = K Q^T of both 16-key tiles from the K plane.
+// wave's tile.  mt_qk: the raw scores S^T = K Q^T of both 16-key tiles from the K plane; for
+// one tile also the squared key norms of the window's first klim keys (the cached keys of
+// the piece; none when klim <= 0).
+template <int kW>
 __device__ __forceinline__ void mt_qk(const uint8_t* kplane, const bf16x8_t (&qop)[3][4], int lane,
-                                      f32x4_t (&sacc)[2]) {
+                                      f32x4_t (&sacc)[2], int klim, MtStats<kW>& ms) {
     const int n = lane & 15;
     const int g = lane >> 4;
     sacc[0] = f32x4_t{0.f, 0.f, 0.f, 0.f};
     sacc[1] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    float nrm[2][2] = {{0.f, 0.f}, {0.f, 0.f}};
 #pragma unroll
     for (int kb = 0; kb < 4; ++kb) {
         bf16x8_t ak[2];
@@ -455,6 +520,67 @@ __device__ __forceinline__ void mt_qk(const uint8_t* kplane, const bf16x8_t (&qo
 #pragma unroll
             for (int kt = 0; kt < 2; ++kt)
                 sacc[kt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ak[kt], qop[s][kb], sacc[kt], 0, 0, 0);
+        if constexpr (kW == 1) {
+#pragma unroll
+            for (int kt = 0; kt < 2; ++kt) {
+                const uint4 w = __builtin_bit_cast(uint4, ak[kt]);
+                nrm[kt][kb & 1] =
+                    bf16x2_sq_acc(w.w, bf16x2_sq_acc(w.z, bf16x2_sq_acc(w.y, bf16x2_sq_acc(w.x, nrm[kt][kb & 1]))));
+            }
+        }
+    }
+    if constexpr (kW == 1) {
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+            for (int pr = 0; pr < 2; ++pr) {
+                const uint32_t x = 16 * kt + n < klim ? __float_as_uint(nrm[kt][pr]) : 0u;
+                ms.kmax[pr] = max(ms.kmax[pr], x);
+            }
+    }
+}
+
+// The |V| code masks of one tile's V^T operand dwords (element 2j + h of lane (g, n)'s 8 is
+// key 16 (j / 2) + 4g + 2 (j % 2) + h): the first vlim keys of the window count.
+__device__ __forceinline__ void mt_vmask(int vlim, int lane, uint32_t (&vm)[4]) {
+    const int g = lane >> 4;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int k0 = 16 * (j >> 1) + 4 * g + 2 * (j & 1);
+        vm[j] = (k0 < vlim ? 0x7fffu : 0u) | (k0 + 1 < vlim ? 0x7fff0000u : 0u);
+    }
+}
+
+// Two or four tiles: this wave's share of the window's statistics from the K and V planes in
+// LDS (keys (32 / W) wv + ..), the first lim keys of the window counting.
+template <int kW>
+__device__ __forceinline__ void mt_stats_window(const uint8_t* kplane, const uint8_t* vplane, int wv, int lane,
+                                                int lim, MtStats<kW>& ms) {
+    constexpr int kKeys = kMtWin / kW;
+    const int c = lane & 7;
+#pragma unroll
+    for (int j = 0; j < kKeys / 8; ++j) {
+        const int row = kKeys * wv + 8 * j + (lane >> 3);
+        const uint8_t* rp = kplane + row * kRowB;
+        const uint4 lo = *reinterpret_cast<const uint4*>(rp + 16 * (c ^ pf_swz(row)));
+        const uint4 hi = *reinterpret_cast<const uint4*>(rp + 16 * ((c + 8) ^ pf_swz(row)));
+        float sq = bf16x2_sq_acc(lo.x, 0.f);
+        sq = bf16x2_sq_acc(lo.y, sq);
+        sq = bf16x2_sq_acc(lo.z, sq);
+        sq = bf16x2_sq_acc(lo.w, sq);
+        sq = bf16x2_sq_acc(hi.x, sq);
+        sq = bf16x2_sq_acc(hi.y, sq);
+        sq = bf16x2_sq_acc(hi.z, sq);
+        sq = bf16x2_sq_acc(hi.w, sq);
+        ms.kmax[0] = max(ms.kmax[0], row < lim ? __float_as_uint(sq) : 0u);
+    }
+    const int vchunk = lane >> 2;
+    const int vword = 4 * (lane & 3);
+#pragma unroll
+    for (int j = 0; j < kKeys; ++j) {
+        const int row = kKeys * wv + j;
+        const uint32_t x = *reinterpret_cast<const uint32_t*>(vplane + row * kRowB + 16 * (vchunk ^ pf_swz(row)) + vword);
+        ms.vmax[0] = pk_max_u16(ms.vmax[0], x & (row < lim ? 0x7fff7fffu : 0u));
     }
 }
 
@@ -533,9 +659,9 @@ __device__ __forceinline__ void mt_probs(const f32x4_t (&sacc)[2], float m_eff, 
 // for the next window's K, which every wave requested after this window's V: the copies
 // complete in issue order, so that wait and the barrier after it covered V as well
 // (B=64 ragged, T=16: stream kernel 283 -> 272 us).
-template <int kC, int kVPlanes>
+template <int kC, int kVPlanes, int kW>
 __device__ __forceinline__ void mt_pv(uint32_t vbase, const uint32_t (&ph)[3][2][4], bool steady, int lane,
-                                      MtState& t, bool sync) {
+                                      MtState& t, bool sync, const uint32_t (&vm)[4], MtStats<kW>& ms) {
     if (sync) {
         mt_wait_planes<kC, kVPlanes>(steady);
         mt_barrier();
@@ -563,6 +689,12 @@ __device__ __forceinline__ void mt_pv(uint32_t vbase, const uint32_t (&ph)[3][2]
             u.h[0] = r[e][0];
             u.h[1] = r[e][1];
             av[e] = u.v;
+            if constexpr (kW == 1) {
+                // The |V| codes of the window's cached keys (masks from mt_vmask).
+                const uint4 w = __builtin_bit_cast(uint4, u.v);
+                uint32_t& m = ms.vmax[d0 + e];
+                m = pk_max_u16(m, pk_max_u16(pk_max_u16(w.x & vm[0], w.y & vm[1]), pk_max_u16(w.z & vm[2], w.w & vm[3])));
+            }
         }
 #pragma unroll
         for (int s = 0; s < 3; ++s)
@@ -586,23 +718,15 @@ __device__ __forceinline__ void mt_piece_end(const PrefillArgs& a, int b, int kv
     const double l = swap_add_f64<true>(swap_add_f64<false>(t.l64));
     if (whole) {
         const int tok = 4 * wv + (n >> 2);
-        // Column n's row (lanes n, n+16, n+32, n+48 hold dims 16dt + 4g ..): its smallest
-        // magnitude against its rms decides whether the row is rescored in fp64.
-        double x[8][4], ss = 0.0, mn = INFINITY;
+        // Column n's row (lanes n, n+16, n+32, n+48 hold dims 16dt + 4g ..).
+        double x[8][4];
 #pragma unroll
         for (int dt = 0; dt < 8; ++dt)
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                x[dt][i] = t.o64[dt][i] / l;
-                ss = fma(x[dt][i], x[dt][i], ss);
-                mn = fmin(mn, fabs(x[dt][i]));
-            }
-        ss = swap_add_f64<true>(swap_add_f64<false>(ss));
-        mn = fmin(mn, __shfl_xor(mn, 16));
-        mn = fmin(mn, __shfl_xor(mn, 32));
+            for (int i = 0; i < 4; ++i) x[dt][i] = t.o64[dt][i] / l;
         if (tok >= a.n_new) return;
-        if (g == 0 && a.rs_hdr && rs_flag_row(mn, ss, t.m_run))
-            rs_append(a, static_cast<uint32_t>((static_cast<int64_t>(b) * a.n_new + tok) * kHq + kvh * kGroup + (n & 3)));
+        if (g == 0 && a.rs_hdr)
+            a.rs_m[(static_cast<int64_t>(b) * a.n_new + tok) * kHq + kvh * kGroup + (n & 3)] = t.m_run;
         uint16_t* orow = a.out + ((static_cast<int64_t>(b) * a.n_new + tok) * kHq + kvh * kGroup + (n & 3)) * kD;
 #pragma unroll
         for (int dt = 0; dt < 8; ++dt) {
@@ -623,6 +747,41 @@ __device__ __forceinline__ void mt_piece_end(const PrefillArgs& a, int b, int kv
             make_float4(static_cast<float>(t.o64[dt][0]), static_cast<float>(t.o64[dt][1]),
                         static_cast<float>(t.o64[dt][2]), static_cast<float>(t.o64[dt][3]));
     if (g == 0) a.part_ml[col] = make_float2(t.m_run, static_cast<float>(l));
+}
+
+// End of a piece's statistics: each value reduced over the lanes that hold it, then raised
+// into the segment's cached-key maxima (atomicMax: the result does not depend on the order).
+template <int kW>
+__device__ __forceinline__ void mt_stats_end(const PrefillArgs& a, int64_t seg, int lane, MtStats<kW>& ms) {
+    if constexpr (kW == 1) {
+        const int n = lane & 15;
+        const int g = lane >> 4;
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            uint32_t x = ms.kmax[i];
+#pragma unroll
+            for (int sh = 1; sh < 16; sh <<= 1) x = max(x, static_cast<uint32_t>(__shfl_xor(static_cast<int>(x), sh)));
+            if (n == 0 && x) atomicMax(a.rs_kc + seg * 8 + 4 * i + g, x);
+        }
+#pragma unroll
+        for (int dt = 0; dt < 8; ++dt) {
+            uint32_t x = ms.vmax[dt];
+            x = pk_max_u16(x, static_cast<uint32_t>(__shfl_xor(static_cast<int>(x), 16)));
+            x = pk_max_u16(x, static_cast<uint32_t>(__shfl_xor(static_cast<int>(x), 32)));
+            x = max(x & 0xffffu, x >> 16);
+            if (g == 0 && x) atomicMax(a.rs_dc + seg * kD + 16 * dt + n, x);
+        }
+    } else {
+        uint32_t x = ms.kmax[0];
+#pragma unroll
+        for (int sh = 8; sh < kWave; sh <<= 1) x = max(x, static_cast<uint32_t>(__shfl_xor(static_cast<int>(x), sh)));
+        if (lane < 8 && x) atomicMax(a.rs_kc + seg * 8 + lane, x);
+        const uint32_t v = ms.vmax[0];
+        uint32_t* dc = a.rs_dc + seg * kD + 2 * lane;
+        if (v & 0xffffu) atomicMax(dc, v & 0xffffu);
+        if (v >> 16) atomicMax(dc + 1, v >> 16);
+    }
+    mt_stats_reset<kW>(ms);
 }
 
 // Sequence windows of the plan: o = seq_off[base + lane], o1 = seq_off[base + lane + 1].
@@ -771,6 +930,8 @@ __global__ __launch_bounds__(kWave * kW) __attribute__((amdgpu_waves_per_eu(kW =
         }
     }
 
+    MtStats<kW> ms;
+    mt_stats_reset<kW>(ms);
     while (true) {
         // This piece: Q operands, chunk-key scores, start, window loop.
         const int st = a.start[c.b];
@@ -814,7 +975,9 @@ __global__ __launch_bounds__(kWave * kW) __attribute__((amdgpu_waves_per_eu(kW =
         f32x4_t s_cur[2];
         mt_wait_planes<kC, 2 * kA>(kq == kA);
         mt_barrier();
-        mt_qk(slot_ptr(slot), qop, lane, s_cur);
+        // Keys of the piece below the chunk: the ones its statistics cover.
+        const int stat_end = min(c.k_b, st);
+        mt_qk<kW>(slot_ptr(slot), qop, lane, s_cur, stat_end - c.kw, ms);
         for (;;) {
             // Request V of the producer's window (kA after this one) and, once every wave
             // is done with the previous window, K of the window after it.
@@ -839,9 +1002,13 @@ __global__ __launch_bounds__(kWave * kW) __attribute__((amdgpu_waves_per_eu(kW =
             // The next window's scores (on a piece's last window the plane read is the next
             // piece's or stale, and the result is dropped).
             f32x4_t s_next[2];
-            mt_qk(slot_ptr(slot + 2), qop, lane, s_next);
+            mt_qk<kW>(slot_ptr(slot + 2), qop, lane, s_next, stat_end - (c.kw + kMtWin), ms);
             mt_probs(s_cur, m_eff, ph, t);
-            mt_pv<kC, 2 * kA + 1>(vbase, ph, v_steady, lane, t, !has_next);
+            uint32_t vm[4] = {0u, 0u, 0u, 0u};
+            if constexpr (kW == 1) mt_vmask(stat_end - c.kw, lane, vm);
+            mt_pv<kC, 2 * kA + 1, kW>(vbase, ph, v_steady, lane, t, !has_next, vm, ms);
+            if constexpr (kW > 1)
+                mt_stats_window<kW>(slot_ptr(slot), slot_ptr(slot + 1), wv, lane, stat_end - c.kw, ms);
             s_cur[0] = s_next[0];
             s_cur[1] = s_next[1];
             slot = slot + 2 >= kS ? slot + 2 - kS : slot + 2;
@@ -851,6 +1018,7 @@ __global__ __launch_bounds__(kWave * kW) __attribute__((amdgpu_waves_per_eu(kW =
         }
         mt_flush(t);
         mt_piece_end<kW>(a, c.b, c.kvh, c.pk == 0 && c.k_b == c.nk, wg + seg, wv, lane, t);
+        mt_stats_end<kW>(a, seg, lane, ms);
         mt_advance(a, c, x_end, lead);
         if (!c.valid) break;
     }
@@ -928,22 +1096,10 @@ __global__ __launch_bounds__(256 * kW) void mt_merge_kernel(PrefillArgs a) {
         }
     }
     uint16_t h8[8];
-    double ss = 0.0, mn = INFINITY;
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-        const double x = o[j] / l;
-        h8[j] = f32_to_bf16_rne(static_cast<float>(x));
-        ss = fma(x, x, ss);
-        mn = fmin(mn, fabs(x));
-    }
-    // The column's row is 16 consecutive lanes.
-#pragma unroll
-    for (int d = 1; d < 16; d <<= 1) {
-        ss += __shfl_xor(ss, d);
-        mn = fmin(mn, __shfl_xor(mn, d));
-    }
-    if ((threadIdx.x & 15) == 0 && a.rs_hdr && rs_flag_row(mn, ss, m))
-        rs_append(a, static_cast<uint32_t>((static_cast<int64_t>(b) * a.n_new + tok) * kHq + kvh * kGroup + (col & 3)));
+    for (int j = 0; j < 8; ++j) h8[j] = f32_to_bf16_rne(static_cast<float>(o[j] / l));
+    if ((threadIdx.x & 15) == 0 && a.rs_hdr)
+        a.rs_m[(static_cast<int64_t>(b) * a.n_new + tok) * kHq + kvh * kGroup + (col & 3)] = m;
     uint2* dst = reinterpret_cast<uint2*>(a.out + ((static_cast<int64_t>(b) * a.n_new + tok) * kHq + kvh * kGroup +
                                                    (col & 3)) * kD + d0);   // out is 8-byte aligned
     dst[0] = make_uint2(h8[0] | (static_cast<uint32_t>(h8[1]) << 16), h8[2] | (static_cast<uint32_t>(h8[3]) << 16));

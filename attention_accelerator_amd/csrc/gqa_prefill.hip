@@ -78,7 +78,7 @@ size_t al256(size_t x) { return (x + 255) / 256 * 256; }
 size_t prefill_stage_bytes(int32_t batch, int32_t n_new, int32_t capacity) {
     const size_t rows = static_cast<size_t>(batch) * n_new * kHkv;
     const size_t pos = (static_cast<size_t>(capacity) + kPfBlk - 1) / kPfBlk * kPfBlk;
-    const size_t cb = static_cast<size_t>((n_new + kPfBlk - 1) / kPfBlk + 1);
+    const size_t cb = static_cast<size_t>(prefill_chunk_blocks(n_new));
     const size_t bh = static_cast<size_t>(batch) * kHkv;
     return al256(rows * kD * sizeof(float)) + 2 * al256(bh * pos * kD * sizeof(uint16_t)) +
            al256(bh * cb * kPfBlk * kD * sizeof(uint16_t)) + al256(bh * (pos / kPfBlk) * sizeof(uint32_t));
@@ -87,7 +87,7 @@ size_t prefill_stage_bytes(int32_t batch, int32_t n_new, int32_t capacity) {
 void prefill_stage_layout(PrefillArgs& a, void* base) {
     const size_t rows = static_cast<size_t>(a.batch) * a.n_new * kHkv;
     a.stg_pos = (a.capacity + kPfBlk - 1) / kPfBlk * kPfBlk;
-    a.stg_cb = (a.n_new + kPfBlk - 1) / kPfBlk + 1;
+    a.stg_cb = prefill_chunk_blocks(a.n_new);
     const size_t bh = static_cast<size_t>(a.batch) * kHkv;
     char* p = static_cast<char*>(base);
     a.kx32 = reinterpret_cast<float*>(p);
@@ -211,12 +211,105 @@ __device__ __forceinline__ int stg_scale_exp(uint32_t mb, bool& bad) {
 
 __device__ __forceinline__ float pow2f(int e) { return __uint_as_float(static_cast<uint32_t>(127 + e) << 23); }
 
+// Statistics of one staged block for the rescore flag: thread (r, qq) holds pair groups 2qq
+// and 2qq+1 of row r whole (dims 16qq .. 16qq+15 and 64+16qq ..), so its two squared group
+// norms need no other thread, and the |V| codes of its 32 dims.  stg_stats_put writes the
+// block's rows to LDS ([64 rows][64 dwords] of |V| codes, dword c = dims 2c and 2c+1; [64
+// rows][8] norms) before the kernel's own barrier; after it, stg_stats_take reduces
+// columns, one wave per 16 dword columns and 2 norm groups: a block of cached rows stores
+// its maxima (rs_kblk / rs_dblk, folded over the cache by prefill_stat_reduce_kernel), a
+// block holding chunk keys the maxima over its rows up to each row (rs_kpre / rs_dpre).
+struct StgStatLds {
+    uint32_t v[kPfBlk][kD / 2];
+    uint32_t k[kPfBlk][8];
+};
+
+__device__ __forceinline__ void stg_stats_put(int r, int qq, const float (&kf)[32], const float (&vf)[32],
+                                              StgStatLds& sl) {
+    float n0 = 0.f, n1 = 0.f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        n0 = fmaf(kf[j], kf[j], fmaf(kf[16 + j], kf[16 + j], n0));
+        n1 = fmaf(kf[8 + j], kf[8 + j], fmaf(kf[24 + j], kf[24 + j], n1));
+    }
+    uint32_t vc[16];
+#pragma unroll
+    for (int j = 0; j < 16; ++j)
+        vc[j] = ((__float_as_uint(vf[2 * j]) >> 16) & 0x7fffu) | (__float_as_uint(vf[2 * j + 1]) & 0x7fff0000u);
+    uint4* vrow = reinterpret_cast<uint4*>(&sl.v[r][0]);
+    vrow[2 * qq] = make_uint4(vc[0], vc[1], vc[2], vc[3]);
+    vrow[2 * qq + 1] = make_uint4(vc[4], vc[5], vc[6], vc[7]);
+    vrow[8 + 2 * qq] = make_uint4(vc[8], vc[9], vc[10], vc[11]);
+    vrow[8 + 2 * qq + 1] = make_uint4(vc[12], vc[13], vc[14], vc[15]);
+    sl.k[r][2 * qq] = __float_as_uint(n0);
+    sl.k[r][2 * qq + 1] = __float_as_uint(n1);
+}
+
+__device__ __forceinline__ void stg_stats_take(const PrefillArgs& a, int bh, int blk, int st, int wave, int lane,
+                                               const StgStatLds& sl) {
+    // Wave w: |V| dword columns 16w .. 16w+15 (lane: column 16w + (lane & 15), rows
+    // 16 (lane >> 4) .. +15) and norm groups 2w, 2w+1 (lane: group 2w + (lane & 1), rows
+    // 2 (lane >> 1) and +1).
+    const int col = 16 * wave + (lane & 15);
+    const int rg = lane >> 4;
+    const int kg = 2 * wave + (lane & 1);
+    const int kr = 2 * (lane >> 1);
+    if (blk * kPfBlk + kPfBlk - 1 < st) {
+        uint32_t x = 0u;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) x = pk_max_u16(x, sl.v[16 * rg + i][col]);
+        x = pk_max_u16(x, static_cast<uint32_t>(__shfl_xor(static_cast<int>(x), 16)));
+        x = pk_max_u16(x, static_cast<uint32_t>(__shfl_xor(static_cast<int>(x), 32)));
+        const int64_t e = static_cast<int64_t>(bh) * a.rs_nblk + blk;
+        if (rg == 0) a.rs_dblk[e * (kD / 2) + col] = x;
+        uint32_t y = max(sl.k[kr][kg], sl.k[kr + 1][kg]);
+#pragma unroll
+        for (int sh = 2; sh < kWave; sh <<= 1) y = max(y, static_cast<uint32_t>(__shfl_xor(static_cast<int>(y), sh)));
+        if (lane < 2) a.rs_kblk[e * 8 + kg] = y;
+        return;
+    }
+    // Running maxima down the rows: within each lane's 16 (or 2) rows, then the earlier
+    // lanes' totals (row groups 16 and 32 lanes apart; norm rows 2, 4, .. lanes apart).
+    const int cb = blk - st / kPfBlk;
+    const int64_t e0 = (static_cast<int64_t>(bh) * a.rs_ncb + cb) * a.rs_nr;
+    uint32_t run[16];
+    uint32_t x = 0u;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        x = pk_max_u16(x, sl.v[16 * rg + i][col]);
+        run[i] = x;
+    }
+    uint32_t carry = 0u;
+    {
+        const uint32_t t16 = static_cast<uint32_t>(__shfl_up(static_cast<int>(x), 16));
+        const uint32_t t32 = static_cast<uint32_t>(__shfl_up(static_cast<int>(x), 32));
+        const uint32_t t48 = static_cast<uint32_t>(__shfl_up(static_cast<int>(x), 48));
+        if (rg >= 1) carry = pk_max_u16(carry, t16);
+        if (rg >= 2) carry = pk_max_u16(carry, t32);
+        if (rg >= 3) carry = pk_max_u16(carry, t48);
+    }
+#pragma unroll
+    for (int i = 0; i < 16; ++i)
+        *reinterpret_cast<uint32_t*>(a.rs_dpre + (e0 + 16 * rg + i) * kD + 2 * col) = pk_max_u16(run[i], carry);
+    const uint32_t y0 = sl.k[kr][kg];
+    const uint32_t y1 = max(y0, sl.k[kr + 1][kg]);
+    uint32_t yc = 0u;
+#pragma unroll
+    for (int sh = 2; sh < kWave; sh <<= 1) {
+        const uint32_t o = static_cast<uint32_t>(__shfl_up(static_cast<int>(max(y1, yc)), sh));
+        if (lane >= sh) yc = max(yc, o);
+    }
+    a.rs_kpre[(e0 + kr) * 8 + kg] = max(y0, yc);
+    a.rs_kpre[(e0 + kr + 1) * 8 + kg] = max(y1, yc);
+}
+
 // One workgroup per (sequence, KV head, 64-position block) of the positions the attention
 // reads, [0, start + T); thread (r, qq) holds dims 16qq .. 16qq+15 and 64+16qq .. of row r.
 // Rows past start + T in the last block are written as zeros (the attention kernel copies
 // whole blocks and masks them).
 __global__ __launch_bounds__(kStgThreads) void prefill_stage_kernel(PrefillArgs a) {
     __shared__ uint32_t red[2][kStgThreads / kWave];
+    __shared__ StgStatLds stat_s;
     const int tid = threadIdx.x;
     const int wave = tid >> 6;
     const int lane = tid & (kWave - 1);
@@ -296,11 +389,12 @@ __global__ __launch_bounds__(kStgThreads) void prefill_stage_kernel(PrefillArgs 
             wk = max(wk, static_cast<uint32_t>(__shfl_xor(static_cast<int>(wk), sh)));
             wv = max(wv, static_cast<uint32_t>(__shfl_xor(static_cast<int>(wv), sh)));
         }
-        __syncthreads();                      // red is rewritten for every item
+        __syncthreads();                      // red and stat_s are rewritten for every item
         if (lane == 0) {
             red[0][wave] = wk;
             red[1][wave] = wv;
         }
+        if (a.rs_hdr) stg_stats_put(r, qq, kf, vf, stat_s);
         __syncthreads();
         uint32_t bk = 0u, bv = 0u;
 #pragma unroll
@@ -349,7 +443,79 @@ __global__ __launch_bounds__(kStgThreads) void prefill_stage_kernel(PrefillArgs 
             a.stg_scale[static_cast<int64_t>(bh) * nblk + blk] =
                 (static_cast<uint32_t>(sk) & 0xffu) | ((static_cast<uint32_t>(sv) & 0xffu) << 8) |
                 (any_bad ? 0x80000000u : 0u);
+        if (a.rs_hdr) stg_stats_take(a, bh, blk, st, wave, lane, stat_s);
     }
+}
+
+// The maxima over the keys before each chunk block of a (sequence, KV head): the blocks of
+// cached rows only (the block maxima the staging kernel wrote) folded by 16 partial sweeps
+// (thread t: dword column t % 64 of every 16th block; norm group t % 8 of every 64th),
+// meeting in LDS; then, chunk block by chunk block, the previous chunk blocks' maxima (row
+// 63 of their running maxima).
+__global__ __launch_bounds__(1024) void prefill_stat_reduce_kernel(PrefillArgs a) {
+    __shared__ uint32_t vpart[16][kD / 2];
+    __shared__ uint32_t kpart[64][8];
+    const int bh = blockIdx.x;
+    const int tid = threadIdx.x;
+    const int st = a.start[bh / kHkv];
+    const int n_cached = prefill_start_ok(a, st) ? st / kPfBlk : 0;
+    {
+        const int col = tid & 63, sub = tid >> 6;
+        const uint32_t* vb = a.rs_dblk + static_cast<int64_t>(bh) * a.rs_nblk * (kD / 2) + col;
+        uint32_t x = 0u;
+        for (int i0 = sub; i0 < n_cached; i0 += 16 * 8) {
+            uint32_t w[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j)
+                w[j] = i0 + 16 * j < n_cached ? vb[static_cast<int64_t>(i0 + 16 * j) * (kD / 2)] : 0u;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) x = pk_max_u16(x, w[j]);
+        }
+        vpart[sub][col] = x;
+    }
+    if (tid < 512) {
+        const int g = tid & 7, ks = tid >> 3;
+        const uint32_t* kb = a.rs_kblk + static_cast<int64_t>(bh) * a.rs_nblk * 8 + g;
+        uint32_t y = 0u;
+        for (int i0 = ks; i0 < n_cached; i0 += 64 * 4) {
+            uint32_t w[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) w[j] = i0 + 64 * j < n_cached ? kb[static_cast<int64_t>(i0 + 64 * j) * 8] : 0u;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) y = max(y, w[j]);
+        }
+        kpart[ks][g] = y;
+    }
+    __syncthreads();
+    if (tid < kD / 2) {
+        uint32_t v = 0u;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) v = pk_max_u16(v, vpart[i][tid]);
+        // Chunk block cb: the cached maxima and chunk blocks 0 .. cb-1 (their last row).
+        const int64_t pre0 = static_cast<int64_t>(bh) * a.rs_ncb * a.rs_nr;
+        for (int cb = 0; cb < a.rs_ncb; ++cb) {
+            uint32_t* dc = a.rs_dc + (static_cast<int64_t>(bh) * a.rs_ncb + cb) * kD + 2 * tid;
+            dc[0] = v & 0xffffu;
+            dc[1] = v >> 16;
+            v = pk_max_u16(v, *reinterpret_cast<const uint32_t*>(a.rs_dpre + (pre0 + static_cast<int64_t>(cb) * a.rs_nr + a.rs_nr - 1) * kD + 2 * tid));
+        }
+    } else if (tid < kD / 2 + 8) {
+        const int g = tid - kD / 2;
+        uint32_t y = 0u;
+#pragma unroll 8
+        for (int i = 0; i < 64; ++i) y = max(y, kpart[i][g]);
+        const int64_t pre0 = static_cast<int64_t>(bh) * a.rs_ncb * a.rs_nr;
+        for (int cb = 0; cb < a.rs_ncb; ++cb) {
+            a.rs_kc[(static_cast<int64_t>(bh) * a.rs_ncb + cb) * 8 + g] = y;
+            y = max(y, a.rs_kpre[(pre0 + static_cast<int64_t>(cb) * a.rs_nr + a.rs_nr - 1) * 8 + g]);
+        }
+    }
+}
+
+hipError_t launch_prefill_stat_reduce(const PrefillArgs& a, hipStream_t stream) {
+    if (!a.rs_hdr) return hipSuccess;
+    hipLaunchKernelGGL(prefill_stat_reduce_kernel, dim3(static_cast<unsigned>(a.batch * kHkv)), dim3(1024), 0, stream, a);
+    return hipGetLastError();
 }
 
 hipError_t launch_prefill_stage(const PrefillArgs& a, hipStream_t stream) {
@@ -884,29 +1050,20 @@ __global__ __launch_bounds__(kPfThreads) void prefill_attn_kernel(PrefillArgs a)
 
     double l = tl.l64 + __shfl_xor(tl.l64, 16);
     l += __shfl_xor(l, 32);
-    // The row of query n (lanes n, n+16, n+32, n+48 hold dims 16dt + 4g ..): its smallest
-    // magnitude against its rms decides whether the row is rescored in fp64.
-    double x[8][4], ss = 0.0, mn = INFINITY;
+    // The row of query n: lanes n, n+16, n+32, n+48 hold dims 16dt + 4g ..
+    double x[8][4];
 #pragma unroll
     for (int dt = 0; dt < 8; ++dt)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            x[dt][i] = tl.o64[dt][i] / l;
-            ss = fma(x[dt][i], x[dt][i], ss);
-            mn = fmin(mn, fabs(x[dt][i]));
-        }
-    ss += __shfl_xor(ss, 16);
-    ss += __shfl_xor(ss, 32);
-    mn = fmin(mn, __shfl_xor(mn, 16));
-    mn = fmin(mn, __shfl_xor(mn, 32));
-    if (!q_ok) return;
-    // Rows that read a marked block or whose Q row is out of range go to the rescore as well
-    // (rs_flag_row takes the rows whose sum is not finite).
+        for (int i = 0; i < 4; ++i) x[dt][i] = tl.o64[dt][i] / l;
     const bool q_bad_row = __shfl_xor(static_cast<int>(q_bad), 16) | __shfl_xor(static_cast<int>(q_bad), 32) |
                            __shfl_xor(static_cast<int>(q_bad), 48) | static_cast<int>(q_bad);
-    const bool flag = rs_flag_row(mn, ss, tl.m_run) || (unsafe >> 31) != 0u || q_bad_row;
-    if (g == 0 && a.rs_hdr && flag)
-        rs_append(a, static_cast<uint32_t>((static_cast<int64_t>(b) * T + tq) * kHq + hq));
+    if (!q_ok) return;
+    // The flag decision (rs_flag_kernel) reads the row's running max; rows that read a
+    // marked block or whose Q row is out of range always go to the rescore (NaN).
+    if (g == 0 && a.rs_hdr)
+        a.rs_m[(static_cast<int64_t>(b) * T + tq) * kHq + hq] =
+            ((unsafe >> 31) != 0u || q_bad_row) ? __builtin_nanf("") : tl.m_run;
     {
         uint16_t* orow = a.out + ((static_cast<int64_t>(b) * T + tq) * kHq + hq) * kD;
 #pragma unroll

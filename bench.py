@@ -325,6 +325,7 @@ def bench_prefill(args, torch, gqa, dev) -> int:
 
     torch.cuda.synchronize()
     gpu_out = None if args.no_cpu_baseline else codes_of(out)     # the last step's rows
+    rescored = call.rescored_rows()                               # the last step's fp64 rows
     tflops = flops / (ms_per_step * 1e-3) / 1e12
     roofline = None
     if attn_ms:
@@ -353,7 +354,8 @@ def bench_prefill(args, torch, gqa, dev) -> int:
                    "rope": "q and new k", "precision": "BF16 K/V staged exactly as fp16 (power-of-two "
                    "scale per 64-position block); Q, the chunk's K and P in two fp16 parts; fp32 MFMA "
                    "accumulation per 64-key block, fp64 across blocks; fp64 rescore of flagged rows",
-                   "flops_per_step": flops, "spinup_s": args.spinup_s},
+                   "flops_per_step": flops, "spinup_s": args.spinup_s,
+                   "rescored_rows": rescored, "output_rows": bsz * n_new * 32},
         "roofline": roofline,
         "cpu_baseline": None if args.no_cpu_baseline else prefill_cpu_baseline(
             q, kn, vn, k_host, v_host, [start] * bsz, gpu_out),
@@ -447,6 +449,7 @@ def bench_multitoken(args, torch, gqa, dev, stimulus) -> int:
         append_ms, attn_ms = ap_ms / n, at_ms / n
     print(f"[bench] {args.steps} steps: {ms_per_step * 1e3:.2f} us/step", file=sys.stderr, flush=True)
     gpu_out = None if args.no_cpu_baseline else codes_of(out)     # the last step's rows
+    rescored = call.rescored_rows()                               # the last step's fp64 rows
     if args.calibrate_copy:
         calibrate_copy(torch, dev)
     roofline = None
@@ -479,7 +482,8 @@ def bench_multitoken(args, torch, gqa, dev, stimulus) -> int:
         "data": f"synthetic N(0,1) BF16, seed {args.seed}",
         "config": {"workload": args.workload, "batch": bsz, "new_tokens": n_new, "keys": sum(lens),
                    "q_heads": 32, "kv_heads": 8, "head_dim": 128, "rope": "q and new k",
-                   "bytes_per_step": step_bytes, "spinup_s": args.spinup_s},
+                   "bytes_per_step": step_bytes, "spinup_s": args.spinup_s,
+                   "rescored_rows": rescored, "output_rows": bsz * n_new * 32},
         "roofline": roofline,
         "cpu_baseline": None if args.no_cpu_baseline else multitoken_cpu_baseline(
             q, kn, vn, k_host, v_host, starts_l, n_new, gpu_out),

@@ -218,6 +218,13 @@ int gqa_prefill_bf16(const gqa_params_t* params, const uint16_t* q, const uint16
                      const gqa_kv_layout_t* kv, const int32_t* start, int32_t batch, int32_t n_new,
                      uint16_t* out, void* workspace, size_t workspace_bytes, void* stream);
 
+/* No counterpart in the reference (measurement): byte offset, within a prefill workspace of
+ * gqa_prefill_workspace_bytes(params, batch, n_new, capacity) bytes, of the uint32 count of
+ * output rows the last gqa_prefill_bf16 call on it recomputed in fp64 (read it after the
+ * call's stream has finished).  0 for arguments gqa_prefill_workspace_bytes rejects. */
+size_t gqa_prefill_rescored_rows_offset(const gqa_params_t* params, int32_t batch, int32_t n_new,
+                                        int32_t capacity);
+
 /* KV append with RoPE on insert: writes k_new / v_new ([batch][n_new][8][128]) into the
  * cache at positions start[b] + t, K rotated at its position when GQA_ROPE_K and rounded
  * double -> f32 -> BF16 (the rope_unit's role in gqa_attention_wrapper.v:302-308 for a

@@ -170,7 +170,7 @@ def prefill(q: np.ndarray, k_cache: np.ndarray, v_cache: np.ndarray, k_new: np.n
             v_new: np.ndarray, start: IntOrSeq, *, rope_q: bool = True, rope_k_new: bool = True,
             rope_k_cache: bool = False, theta: float = 500000.0, scale: Optional[float] = None,
             sum_mode: int = SUM_SEQUENTIAL, rows: Optional[Sequence[int]] = None,
-            want_f64: bool = False):
+            want_f64: bool = False, threads: int = 1):
     """Golden chunked prefill: the one-token golden applied per new query token.
 
     q [B, T, Hq, d], k_new / v_new [B, T, Hkv, d] BF16 codes; k_cache / v_cache
@@ -178,6 +178,8 @@ def prefill(q: np.ndarray, k_cache: np.ndarray, v_cache: np.ndarray, k_new: np.n
     position start[b]+t and sees keys p <= start[b]+t: cached rows for p < start,
     new row p-start otherwise (rotated at p when rope_k_new, unrounded, as the
     golden rotates K).  rows selects which t to compute (default all).
+    threads > 1 runs the tokens of a sequence on that many threads (the C loop
+    releases the GIL; each token's arithmetic is unchanged, so the result is too).
     Returns out [B, len(rows), Hq, d] BF16 codes (and float64 with want_f64)."""
     bsz, t_new, hq, d = q.shape
     hkv = k_new.shape[2]
@@ -196,7 +198,7 @@ def prefill(q: np.ndarray, k_cache: np.ndarray, v_cache: np.ndarray, k_new: np.n
             v_ref[h, :s0] = prepare_rows(v_cache[b, h, :s0], False)
             k_ref[h, s0:] = prepare_rows(k_new[b, :, h], rope_k_new, s0, theta)
             v_ref[h, s0:] = prepare_rows(v_new[b, :, h], False)
-        for i, t in enumerate(rows):
+        def one(i, t, b=b, s0=s0, k_ref=k_ref, v_ref=v_ref):
             pos = s0 + t
             q_ref = np.stack([prepare_rows(q[b, t, h][None], rope_q, pos, theta)[0]
                               for h in range(hq)])
@@ -205,7 +207,24 @@ def prefill(q: np.ndarray, k_cache: np.ndarray, v_cache: np.ndarray, k_new: np.n
                 out[b, i], out64[b, i] = r
             else:
                 out[b, i] = r
+
+        if threads > 1 and len(rows) > 1:
+            from concurrent.futures import ThreadPoolExecutor
+            with ThreadPoolExecutor(max_workers=threads) as ex:
+                list(ex.map(lambda it: one(*it), enumerate(rows)))
+        else:
+            for i, t in enumerate(rows):
+                one(i, t)
     return (out, out64) if want_f64 else out
+
+
+def host_threads(cap: int = 16) -> int:
+    """Threads for the oracle on this host: the cores this process may run on, at most cap."""
+    try:
+        n = len(os.sched_getaffinity(0))
+    except AttributeError:  # pragma: no cover
+        n = os.cpu_count() or 1
+    return max(1, min(cap, n))
 
 
 if os.environ.get("GQA_ORACLE_AUTOBUILD", "1") == "1" and not _LIB_PATH.exists():

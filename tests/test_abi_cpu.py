@@ -151,10 +151,10 @@ def test_prefill_workspace_bytes():
     # at least the fp16 K and V staging planes (8704 positions of 32 (sequence, KV head) pairs)
     # and the fp32 rotated new K rows
     assert n >= 2 * 4 * 8 * 8704 * 128 * 2 + 4 * 512 * 8 * 128 * 4 and n % 256 == 0
-    # the staging planes (and one block scale word per pair) follow the capacity, rounded up to
-    # 64 positions
+    # the staging planes (and per pair one block scale word and the block's key and V maxima
+    # for the rescore flag, 8 + 64 words) follow the capacity, rounded up to 64 positions
     grow = L.gqa_prefill_workspace_bytes(ctypes.byref(p), 4, 512, 8705) - n
-    assert 2 * 4 * 8 * 64 * 128 * 2 <= grow <= 2 * 4 * 8 * 64 * 128 * 2 + 256
+    assert 2 * 4 * 8 * 64 * 128 * 2 <= grow <= 2 * 4 * 8 * 64 * 128 * 2 + 4 * 8 * (1 + 8 + 64) * 4 + 768
     assert L.gqa_prefill_workspace_bytes(ctypes.byref(_params(head_dim=64)), 4, 512, 8704) == 0
     assert L.gqa_prefill_workspace_bytes(ctypes.byref(p), 4, 0, 8704) == 0
     assert L.gqa_prefill_workspace_bytes(ctypes.byref(p), 4, 512, 511) == 0

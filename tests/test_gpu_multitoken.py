@@ -274,16 +274,23 @@ def test_rescore_proportional_pieces(dev, monkeypatch, n_wgs):
     """At most 64 flagged rows: each row's keys are cut into pieces in proportion to its
     length (a row of 3001 keys gets about 30 times the pieces of one of 91), for rescore
     grids of 1 (fewer workgroups than rows), 7, 64 and 1024 workgroups (GQA_STREAM_WGS sets
-    the grid).  V dimension 5 is zero in both sequences, so all 64 rows (2 sequences x 1
-    token x 32 heads) are flagged; every row must match the oracle, dimension 5 exactly."""
+    the grid).  Q is scaled by 2^100 and K by 2^40, so every dot product passes the fp32 range and all
+    64 rows (2 sequences x 1 token x 32 heads) of the MFMA kernels come out not finite and
+    are rescored; every row must match the oracle, and V dimension 5, zero in every key,
+    exactly."""
     monkeypatch.setenv("GQA_STREAM_WGS", n_wgs)
     starts = [90, 3000]
     q, kn, vn, k, v = _chunk(starts, 1, 3001, 77)
     vn[..., 5] = 0.0
     for b, s in enumerate(starts):
         v[b, :, :s, 5] = 0.0
+    q = (q.float() * 2.0 ** 100).to(torch.bfloat16)
+    kn = (kn.float() * 2.0 ** 40).to(torch.bfloat16)
+    k = (k.float() * 2.0 ** 40).to(torch.bfloat16)
     want = _oracle(q, kn, vn, k, v, starts)
-    got, _, _ = _run(q, kn, vn, k, v, starts, dev)
+    ws = torch.empty(gqa.prefill_workspace_bytes(2, 1, 3001), dtype=torch.uint8, device=dev)
+    got, _, _ = _run(q, kn, vn, k, v, starts, dev, workspace=ws)
+    assert gqa.prefill_rescored_rows(ws, 2, 1, 3001) == 64
     assert np.all(got[..., 5] == 0)
     _check(want, got.reshape(-1, 128), f"64 flagged rows, {n_wgs} rescore workgroups")
 

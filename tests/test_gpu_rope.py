@@ -36,9 +36,10 @@ def test_rope_set_512_rows(dev):
     digest = dict(ln.split()[::-1] for ln in (GOLDEN / "rope" / "rope.sha256").read_text().splitlines())
     assert hashlib.sha256(text.encode()).hexdigest() == digest["golden.mem"]
     assert_within_ulp(want, got, 64, "rope 512")
-    exact = float((want == got).mean())
-    print(f"bit-exact fraction {exact:.6f}")
-    assert exact > 0.999
+    # every one of the 65,536 elements bit for bit: the kernel rotates in double and rounds
+    # double -> f32 -> BF16 as the golden does
+    bad = np.argwhere(want != got)
+    assert bad.size == 0, f"{len(bad)} elements differ from the golden, first at (row, dim) {bad[0].tolist()}"
 
 
 def test_rope_positions_tensor_and_large_positions(dev):
