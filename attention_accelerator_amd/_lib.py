@@ -24,6 +24,8 @@ GQA_ERR_HIP = 4
 
 GQA_ROPE_Q = 1
 GQA_ROPE_K = 2
+GQA_PLAN_STREAM_K = 4
+GQA_PLAN_NO_MULTI_TOKEN = 8
 
 # Every function include/gqa.h declares (checked by the CPU test suite).
 EXPORTS = (
@@ -56,6 +58,7 @@ class GqaParams(ctypes.Structure):
         ("scale", ctypes.c_double),
         ("rope_theta", ctypes.c_double),
         ("flags", ctypes.c_uint32),
+        ("stream_wgs", ctypes.c_int32),
     ]
 
 

@@ -18,7 +18,8 @@ from typing import Optional, Sequence, Union
 import torch
 
 from . import _lib
-from ._lib import GQA_ROPE_K, GQA_ROPE_Q, GqaKvLayout, GqaPagedKv, GqaParams, check, lib
+from ._lib import (GQA_PLAN_NO_MULTI_TOKEN, GQA_PLAN_STREAM_K, GQA_ROPE_K, GQA_ROPE_Q, GqaKvLayout, GqaPagedKv,
+                   GqaParams, check, lib)
 
 N_Q_HEADS = 32
 N_KV_HEADS = 8
@@ -32,10 +33,23 @@ Lengths = Union[int, Sequence[int], torch.Tensor]
 
 def make_params(*, rope_q: bool = True, rope_k: bool = False, theta: float = ROPE_THETA,
                 scale: Optional[float] = None, n_q_heads: int = N_Q_HEADS,
-                n_kv_heads: int = N_KV_HEADS, head_dim: int = HEAD_DIM) -> GqaParams:
-    flags = (GQA_ROPE_Q if rope_q else 0) | (GQA_ROPE_K if rope_k else 0)
+                n_kv_heads: int = N_KV_HEADS, head_dim: int = HEAD_DIM, stream_wgs: int = 0,
+                stream_k: bool = False, multi_token: bool = True) -> GqaParams:
+    """The call parameters.  Plan choices (tests and tuning; the results stay within the same
+    tolerance): stream_wgs > 0 sets the persistent workgroups of the stream-K kernels (0:
+    four per CU), stream_k=True makes every contiguous decode call take the three-launch
+    stream-K plan, multi_token=False sends chunks of at most 16 tokens through the prefill
+    attention kernel.  Workspace sizes follow these fields, so size a workspace with the
+    params of the call that will use it."""
+    flags = ((GQA_ROPE_Q if rope_q else 0) | (GQA_ROPE_K if rope_k else 0)
+             | (GQA_PLAN_STREAM_K if stream_k else 0) | (0 if multi_token else GQA_PLAN_NO_MULTI_TOKEN))
     return GqaParams(n_q_heads, n_kv_heads, head_dim,
-                     DEFAULT_SCALE if scale is None else float(scale), float(theta), flags)
+                     DEFAULT_SCALE if scale is None else float(scale), float(theta), flags, int(stream_wgs))
+
+
+def _plan_key(p: GqaParams, batch: int, capacity: int):
+    return (int(batch), int(capacity), int(p.flags) & (GQA_PLAN_STREAM_K | GQA_PLAN_NO_MULTI_TOKEN),
+            int(p.stream_wgs))
 
 
 def _stream_handle(device: torch.device) -> int:
@@ -75,18 +89,20 @@ def new_workspace(batch: int, capacity: int, device, params: Optional[GqaParams]
     check(lib().gqa_decode_workspace_init(ctypes.byref(p), int(batch), int(capacity), ws.data_ptr(),
                                           nbytes, _stream_handle(torch.device(device))),
           "gqa_decode_workspace_init")
-    ws.gqa_decode_plan = (int(batch), int(capacity))
+    ws.gqa_decode_plan = _plan_key(p, batch, capacity)
     return ws
 
 
-def _check_workspace_plan(workspace: torch.Tensor, batch: int, capacity: int) -> None:
-    """A workspace from new_workspace carries the (batch, capacity) it was prepared for;
-    the single-launch path's piece counters sit where that plan puts them, so another
-    plan would find stale data there and leave rows unwritten.  Reject the mismatch."""
+def _check_workspace_plan(workspace: torch.Tensor, p: GqaParams, batch: int, capacity: int) -> None:
+    """A workspace from new_workspace carries the plan (batch, capacity, plan flags,
+    stream_wgs) it was prepared for; the single-launch path's piece counters sit where that
+    plan puts them, so another plan would find stale data there and leave rows unwritten.
+    Reject the mismatch."""
     plan = getattr(workspace, "gqa_decode_plan", None)
-    if plan is not None and plan != (int(batch), int(capacity)):
-        raise ValueError(f"workspace was prepared for (batch, capacity) = {plan}, called with "
-                         f"({batch}, {capacity}); make one with new_workspace({batch}, {capacity}, ...)")
+    want = _plan_key(p, batch, capacity)
+    if plan is not None and plan != want:
+        raise ValueError(f"workspace was prepared for (batch, capacity, plan flags, stream_wgs) = {plan}, "
+                         f"called with {want}; make one with new_workspace({batch}, {capacity}, ..., params)")
 
 
 def gqa_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
@@ -146,7 +162,7 @@ def gqa_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
     elif workspace.numel() * workspace.element_size() < ws_bytes:
         raise ValueError(f"workspace holds {workspace.numel() * workspace.element_size()} bytes; "
                          f"{ws_bytes} needed")
-    _check_workspace_plan(workspace, batch, capacity)
+    _check_workspace_plan(workspace, p, batch, capacity)
     if out is None:
         out = torch.empty((batch, q.shape[1], q.shape[2]), dtype=torch.bfloat16, device=device)
     elif out.shape != (batch, q.shape[1], q.shape[2]) or out.dtype != torch.bfloat16 \
@@ -205,7 +221,7 @@ class PreparedDecode:
     def __init__(self, q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
                  query_position: torch.Tensor, seq_len: torch.Tensor, *, rope_q: bool = True,
                  rope_k: bool = False, theta: float = ROPE_THETA, scale: Optional[float] = None,
-                 out: Optional[torch.Tensor] = None):
+                 out: Optional[torch.Tensor] = None, params: Optional[GqaParams] = None):
         if q.dim() != 3 or k_cache.dim() != 4:
             raise ValueError("expected q [B,32,128] and k/v [B,8,S,128]")
         if not (query_position.is_cuda and seq_len.is_cuda):
@@ -214,7 +230,7 @@ class PreparedDecode:
             raise ValueError("k_cache and v_cache must share strides with contiguous rows")
         self.batch = q.shape[0]
         self.capacity = k_cache.shape[2]
-        self.params = make_params(rope_q=rope_q, rope_k=rope_k, theta=theta, scale=scale)
+        self.params = params or make_params(rope_q=rope_q, rope_k=rope_k, theta=theta, scale=scale)
         self.layout = GqaKvLayout(k_cache.stride(0), k_cache.stride(1), k_cache.stride(2),
                                   self.capacity)
         self.workspace = new_workspace(self.batch, self.capacity, q.device, self.params)
@@ -354,7 +370,7 @@ class PreparedPrefill:
     def __init__(self, q: torch.Tensor, k_new: torch.Tensor, v_new: torch.Tensor, k_cache: torch.Tensor,
                  v_cache: torch.Tensor, start: torch.Tensor, *, rope_q: bool = True, rope_k: bool = True,
                  theta: float = ROPE_THETA, scale: Optional[float] = None,
-                 out: Optional[torch.Tensor] = None):
+                 out: Optional[torch.Tensor] = None, params: Optional[GqaParams] = None):
         if q.dim() != 4 or k_new.dim() != 4 or v_new.shape != k_new.shape:
             raise ValueError("expected q [B,T,32,128] and k_new/v_new [B,T,8,128]")
         if not (isinstance(start, torch.Tensor) and start.is_cuda and start.dtype == torch.int32):
@@ -363,7 +379,7 @@ class PreparedPrefill:
         if k_new.shape[:2] != (self.batch, self.n_new) or start.numel() != self.batch:
             raise ValueError("batch / token count mismatch")
         self.layout = _cache_layout(k_cache, v_cache)
-        self.params = make_params(rope_q=rope_q, rope_k=rope_k, theta=theta, scale=scale)
+        self.params = params or make_params(rope_q=rope_q, rope_k=rope_k, theta=theta, scale=scale)
         ws_bytes = int(lib().gqa_prefill_workspace_bytes(ctypes.byref(self.params), self.batch, self.n_new,
                                                           self.layout.capacity))
         if ws_bytes == 0:
@@ -440,7 +456,8 @@ def gqa_decode_paged(q: torch.Tensor, k_pool: torch.Tensor, v_pool: torch.Tensor
                      block_table: torch.Tensor, query_position: Lengths, seq_len: Lengths, *,
                      rope_q: bool = True, rope_k: bool = False, theta: float = ROPE_THETA,
                      scale: Optional[float] = None, out: Optional[torch.Tensor] = None,
-                     workspace: Optional[torch.Tensor] = None) -> torch.Tensor:
+                     workspace: Optional[torch.Tensor] = None,
+                     params: Optional[GqaParams] = None) -> torch.Tensor:
     """gqa_attention over a paged cache: q [B, 32, 128]; k_pool, v_pool [n_blocks, 8, 16,
     128]; block_table [B, max_blocks] int32 (block j of sequence b holds positions
     16j .. 16j+15).  Host lengths are checked against capacity = 16 * max_blocks."""
@@ -452,7 +469,7 @@ def gqa_decode_paged(q: torch.Tensor, k_pool: torch.Tensor, v_pool: torch.Tensor
         raise ValueError("block_table has one row per sequence")
     capacity = BLOCK_SIZE * block_table.shape[1]
     device = q.device
-    p = make_params(rope_q=rope_q, rope_k=rope_k, theta=theta, scale=scale)
+    p = params or make_params(rope_q=rope_q, rope_k=rope_k, theta=theta, scale=scale)
     sl_dev, sl_host = _lengths_to_device(seq_len, batch, device, "seq_len")
     qp_dev, qp_host = _lengths_to_device(query_position, batch, device, "query_position")
     if sl_host is not None and qp_host is not None:

@@ -25,22 +25,14 @@ namespace {
 // per CU) of the current device -- 1024 on the 256 CUs of an MI355X.  Measured on
 // MI355X, one wave per SIMD streams faster than two (fewer concurrent DRAM streams; the
 // kernel's ~250 registers leave room for one wave per SIMD anyway).  1024 when no
-// device answers.  GQA_STREAM_WGS overrides it (tuning only).
+// device answers.  gqa_params_t.stream_wgs overrides it (tuning and tests).
 constexpr int32_t kStreamWgsDefault = 1024;
 constexpr int32_t kWavesPerCu = 4;
 
 // Batches whose caches hold at most this many keys in all (B * 8 * capacity; 128 MB of
 // K/V) run as one launch (decode_single_kernel): for them the three dependent launches of
-// the stream path cost more than the HBM traffic.  GQA_SINGLE_LAUNCH_MAX_KEYS overrides
-// it (tuning and tests; 0 disables the single-launch path).
-int64_t single_launch_max_keys() {
-    const char* s = std::getenv("GQA_SINGLE_LAUNCH_MAX_KEYS");
-    if (s) {
-        const long long v = std::atoll(s);
-        if (v >= 0) return v;
-    }
-    return int64_t{1} << 18;
-}
+// the stream path cost more than the HBM traffic.  GQA_PLAN_STREAM_K turns it off.
+constexpr int64_t kSingleLaunchMaxKeys = int64_t{1} << 18;
 
 size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
 
@@ -54,22 +46,13 @@ int32_t device_stream_wgs() {
     return cus * kWavesPerCu;
 }
 
-int32_t stream_wgs() {
-    const char* s = std::getenv("GQA_STREAM_WGS");
-    if (s) {
-        const int v = std::atoi(s);
-        if (v >= 1 && v <= 65536) return v;
-    }
-    return device_stream_wgs();
-}
+int32_t stream_wgs(const gqa_params_t* p) { return p->stream_wgs > 0 ? p->stream_wgs : device_stream_wgs(); }
 
 // Chunks of at most kMultiMaxNew new tokens take the multi-token path (stream-K over the
-// keys, prefill arithmetic); GQA_PREFILL_MULTI=0 in the environment sends them through the
-// prefill attention kernel instead.
-bool use_multi(int32_t n_new) {
-    if (n_new > kMultiMaxNew) return false;
-    const char* s = std::getenv("GQA_PREFILL_MULTI");
-    return !(s && s[0] == '0');
+// keys, prefill arithmetic); GQA_PLAN_NO_MULTI_TOKEN sends them through the prefill
+// attention kernel instead.
+bool use_multi(const gqa_params_t* p, int32_t n_new) {
+    return n_new <= kMultiMaxNew && (p->flags & GQA_PLAN_NO_MULTI_TOKEN) == 0u;
 }
 
 // XCD weighting of the stream-K ranges, per mille of a range moved from each workgroup on
@@ -90,15 +73,16 @@ int32_t xcd_skew_pm(int32_t dflt) {
 
 // Workgroups of the multi-token stream kernel: multi_simd_waves(n_new) waves per SIMD,
 // multi_waves(n_new) waves per workgroup.
-int32_t multi_wgs(int32_t n_new) {
-    const int32_t w = stream_wgs() * multi_simd_waves(n_new) / multi_waves(n_new);
+int32_t multi_wgs(const gqa_params_t* p, int32_t n_new) {
+    const int32_t w = stream_wgs(p) * multi_simd_waves(n_new) / multi_waves(n_new);
     return w > 0 ? w : 1;
 }
 
 bool geometry_ok(const gqa_params_t* p) {
     if (p->n_q_heads != kHq || p->n_kv_heads != kHkv || p->head_dim != kD) return false;
     if (!(p->scale != 0.0) || !std::isfinite(p->scale)) return false;
-    if ((p->flags & ~(GQA_ROPE_Q | GQA_ROPE_K)) != 0) return false;
+    if ((p->flags & ~(GQA_ROPE_Q | GQA_ROPE_K | GQA_PLAN_STREAM_K | GQA_PLAN_NO_MULTI_TOKEN)) != 0) return false;
+    if (p->stream_wgs < 0 || p->stream_wgs > kStreamWgsMax) return false;
     if ((p->flags & (GQA_ROPE_Q | GQA_ROPE_K)) && !(p->rope_theta > 0.0 && std::isfinite(p->rope_theta)))
         return false;
     return true;
@@ -133,12 +117,13 @@ hipEvent_t* profile_slot() {
 
 }  // namespace
 
-DecodePlan plan_decode(int32_t batch, int32_t capacity, bool paged, int64_t max_single_segments) {
+DecodePlan plan_decode(const gqa_params_t* params, int32_t batch, int32_t capacity, bool paged,
+                       int64_t max_single_segments) {
     DecodePlan plan{};
-    plan.n_wgs = stream_wgs();
+    plan.n_wgs = stream_wgs(params);
     const int64_t keys_cap = static_cast<int64_t>(batch) * kHkv * capacity;
     const bool single_fits = max_single_segments < 0 || static_cast<int64_t>(batch) * kHkv <= max_single_segments;
-    if (!paged && keys_cap <= single_launch_max_keys() && single_fits) {
+    if (!paged && (params->flags & GQA_PLAN_STREAM_K) == 0u && keys_cap <= kSingleLaunchMaxKeys && single_fits) {
         // Single launch: about one 4-wave workgroup per CU (n_wgs / 4), pieces of at least
         // 256 keys (64 per wave: below that the last piece's merge of more partials costs
         // more than the shorter streams save; B=1 L=4096 runs in 18.7 us with 256-key pieces,
@@ -199,7 +184,7 @@ size_t rescore_bytes(int32_t batch, int32_t n_new, int32_t ncb, int32_t nr, int3
     return rs_layout(batch, n_new, ncb, nr, nblk).total;
 }
 
-void rescore_layout(PrefillArgs& a, void* base, int32_t ncb, int32_t nr, int32_t nblk) {
+void rescore_layout(PrefillArgs& a, const gqa_params_t* params, void* base, int32_t ncb, int32_t nr, int32_t nblk) {
     const RsLayout l = rs_layout(a.batch, a.n_new, ncb, nr, nblk);
     char* p = static_cast<char*>(base);
     a.rs_hdr = reinterpret_cast<uint32_t*>(p);
@@ -220,7 +205,7 @@ void rescore_layout(PrefillArgs& a, void* base, int32_t ncb, int32_t nr, int32_t
     a.rs_nblk = nblk;
     // One-wave workgroups, one per SIMD (the kernel's registers allow one wave per SIMD):
     // the flagged rows are cut into about as many (row, piece) pairs as run at once.
-    const int32_t wgs = stream_wgs();
+    const int32_t wgs = stream_wgs(params);
     a.rs_wgs = wgs < 1 ? 1 : wgs > static_cast<int32_t>(kRsSlots) ? static_cast<int32_t>(kRsSlots) : wgs;
 }
 
@@ -230,7 +215,7 @@ using namespace gqa;
 
 extern "C" {
 
-uint32_t gqa_abi_version(void) { return (3u << 16) | 0u; }
+uint32_t gqa_abi_version(void) { return (4u << 16) | 0u; }
 
 const char* gqa_status_string(int status) {
     switch (status) {
@@ -268,7 +253,7 @@ int gqa_validate_lengths(const int32_t* seq_len, const int32_t* query_pos, int32
 
 size_t gqa_decode_workspace_bytes(const gqa_params_t* params, int32_t batch, int32_t capacity) {
     if (!params || !geometry_ok(params) || batch <= 0 || capacity <= 0) return 0;
-    return plan_decode(batch, capacity).workspace_bytes;
+    return plan_decode(params, batch, capacity).workspace_bytes;
 }
 
 }  // extern "C"
@@ -402,7 +387,7 @@ int gqa_decode_bf16(const gqa_params_t* params, const uint16_t* q, const uint16_
                     size_t workspace_bytes, void* stream) {
     const int st = decode_args_status(params, q, k, v, kv, seq_len, query_pos, batch, out);
     if (st != GQA_OK) return st;
-    return decode_launch(plan_decode(batch, kv->capacity), params, q, k, v, kv->batch_stride, kv->head_stride,
+    return decode_launch(plan_decode(params, batch, kv->capacity), params, q, k, v, kv->batch_stride, kv->head_stride,
                          kv->pos_stride, kv->capacity,
                          nullptr, 0, 0, seq_len, query_pos, batch, out, workspace, workspace_bytes, stream);
 }
@@ -413,7 +398,7 @@ int gqa_decode_bf16_noalloc(const gqa_params_t* params, const uint16_t* q, const
     int st = decode_args_status(params, q, k, v, kv, seq_len, query_pos, batch, out);
     if (st != GQA_OK) return st;
     const DecodePlan plan =
-        plan_decode(batch, kv->capacity, false, static_cast<int64_t>(kNoAllocCountBytes / sizeof(unsigned long long)));
+        plan_decode(params, batch, kv->capacity, false, static_cast<int64_t>(kNoAllocCountBytes / sizeof(unsigned long long)));
     if (plan.workspace_bytes - plan.count_bytes > kNoAllocScratchBytes - kNoAllocCountBytes) return GQA_ERR_WORKSPACE;
     char* base = static_cast<char*>(noalloc_scratch(static_cast<hipStream_t>(stream), st));
     if (!base) return st;
@@ -427,7 +412,7 @@ size_t gqa_decode_paged_workspace_bytes(const gqa_params_t* params, int32_t batc
     if (!params || !geometry_ok(params) || batch <= 0 || max_blocks <= 0 ||
         static_cast<int64_t>(max_blocks) * 16 > 0x7FFFFFFF)
         return 0;
-    return plan_decode(batch, max_blocks * 16, true).workspace_bytes;
+    return plan_decode(params, batch, max_blocks * 16, true).workspace_bytes;
 }
 
 int gqa_decode_paged_bf16(const gqa_params_t* params, const uint16_t* q, const uint16_t* k_pool,
@@ -441,7 +426,7 @@ int gqa_decode_paged_bf16(const gqa_params_t* params, const uint16_t* q, const u
         !aligned(seq_len, 4) || !aligned(query_pos, 4) || !aligned(block_table, 4))
         return GQA_ERR_BAD_POINTER;
     if (kv->pos_stride % 8 || kv->head_stride % 8 || kv->block_stride % 8) return GQA_ERR_BAD_POINTER;
-    return decode_launch(plan_decode(batch, kv->max_blocks * 16, true), params, q, k_pool, v_pool,
+    return decode_launch(plan_decode(params, batch, kv->max_blocks * 16, true), params, q, k_pool, v_pool,
                          kv->block_stride, kv->head_stride, kv->pos_stride,
                          kv->max_blocks * 16, block_table, kv->max_blocks, kv->n_blocks, seq_len, query_pos,
                          batch, out, workspace, workspace_bytes, stream);
@@ -492,7 +477,7 @@ int gqa_decode_workspace_init(const gqa_params_t* params, int32_t batch, int32_t
                               void* workspace, size_t workspace_bytes, void* stream) {
     if (!params) return GQA_ERR_BAD_POINTER;
     if (!geometry_ok(params) || batch <= 0 || capacity <= 0) return GQA_ERR_INVALID_CONFIG;
-    const DecodePlan plan = plan_decode(batch, capacity);
+    const DecodePlan plan = plan_decode(params, batch, capacity);
     if (!workspace || workspace_bytes < plan.workspace_bytes || !aligned(workspace, 256))
         return GQA_ERR_WORKSPACE;
     const hipError_t e = launch_zero_words(static_cast<uint32_t*>(workspace),
@@ -571,8 +556,8 @@ size_t gqa_prefill_workspace_bytes(const gqa_params_t* params, int32_t batch, in
     if (!params || !geometry_ok(params) || batch <= 0 || n_new <= 0 || capacity < n_new) return 0;
     // The multi-token path stages nothing: the chunk's unrounded keys enter through the
     // scores its preparation kernel forms, and the cache is read as stored.
-    if (use_multi(n_new))
-        return align_up(prefill_multi_bytes(batch, n_new, multi_wgs(n_new)), 256) +
+    if (use_multi(params, n_new))
+        return align_up(prefill_multi_bytes(batch, n_new, multi_wgs(params, n_new)), 256) +
                rescore_bytes(batch, n_new, 1, n_new, 0);
     return align_up(prefill_stage_bytes(batch, n_new, capacity), 256) +
            rescore_bytes(batch, n_new, prefill_chunk_blocks(n_new), 64, prefill_cache_blocks(capacity));
@@ -582,7 +567,7 @@ size_t gqa_prefill_rescored_rows_offset(const gqa_params_t* params, int32_t batc
                                         int32_t capacity) {
     if (!gqa_prefill_workspace_bytes(params, batch, n_new, capacity)) return 0;
     // The rescore region (its first word: the flagged-row count) follows the path's own part.
-    if (use_multi(n_new)) return align_up(prefill_multi_bytes(batch, n_new, multi_wgs(n_new)), 256);
+    if (use_multi(params, n_new)) return align_up(prefill_multi_bytes(batch, n_new, multi_wgs(params, n_new)), 256);
     return align_up(prefill_stage_bytes(batch, n_new, capacity), 256);
 }
 
@@ -628,15 +613,16 @@ int gqa_prefill_bf16(const gqa_params_t* params, const uint16_t* q, const uint16
     if (!workspace || workspace_bytes < need || !aligned(workspace, 256)) return GQA_ERR_WORKSPACE;
     a.q = q;
     a.out = out;
-    const bool multi = use_multi(n_new);
+    const bool multi = use_multi(params, n_new);
     char* ws = static_cast<char*>(workspace);
     if (multi) {
-        prefill_multi_layout(a, workspace, multi_wgs(n_new));
+        prefill_multi_layout(a, workspace, multi_wgs(params, n_new));
         a.skew_pm = xcd_skew_pm(multi_waves(n_new) <= 2 ? 40 : 0);
-        rescore_layout(a, ws + align_up(prefill_multi_bytes(batch, n_new, multi_wgs(n_new)), 256), 1, n_new, 0);
+        rescore_layout(a, params, ws + align_up(prefill_multi_bytes(batch, n_new, multi_wgs(params, n_new)), 256), 1,
+                       n_new, 0);
     } else {
         prefill_stage_layout(a, workspace);
-        rescore_layout(a, ws + align_up(prefill_stage_bytes(batch, n_new, kv->capacity), 256),
+        rescore_layout(a, params, ws + align_up(prefill_stage_bytes(batch, n_new, kv->capacity), 256),
                        prefill_chunk_blocks(n_new), 64, prefill_cache_blocks(kv->capacity));
     }
     hipStream_t s = static_cast<hipStream_t>(stream);

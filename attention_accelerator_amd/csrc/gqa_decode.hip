@@ -328,7 +328,7 @@ __device__ __forceinline__ int lane_row_offset() {
 __device__ __forceinline__ void write_rows(const DecodeArgs& a, int b, int kvh, const PieceState& st, double l_tot) {
     uint16_t o8[8];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) o8[e] = f64_to_bf16_via_f32(st.acc[e] / l_tot);
+    for (int e = 0; e < 8; ++e) o8[e] = f32_to_bf16_out(static_cast<float>(st.acc[e] / l_tot));
     *reinterpret_cast<bf16x8_t*>(a.out + (static_cast<int64_t>(b) * kHq + kvh * kGroup) * kD + lane_row_offset()) =
         pack8(o8);
 }
@@ -1036,8 +1036,8 @@ __global__ __launch_bounds__(kGroup * kWave) void decode_merge_kernel(DecodeArgs
     l += __shfl_xor(l, 32);
     uint32_t* out = reinterpret_cast<uint32_t*>(
         a.out + (static_cast<int64_t>(b) * kHq + kvh * kGroup + h) * kD);
-    const uint32_t lo = f32_to_bf16_rne(static_cast<float>(o0 / l));
-    const uint32_t hi = f32_to_bf16_rne(static_cast<float>(o1 / l));
+    const uint32_t lo = f32_to_bf16_out(static_cast<float>(o0 / l));
+    const uint32_t hi = f32_to_bf16_out(static_cast<float>(o1 / l));
     out[lane] = lo | (hi << 16);
 }
 
@@ -1154,8 +1154,8 @@ __global__ __launch_bounds__(kSingleWaves * kWave) void decode_single_kernel(Dec
     }
     uint32_t* orow = reinterpret_cast<uint32_t*>(a.out + (static_cast<int64_t>(b) * kHq + kvh * kGroup + h) * kD);
     if (n_pieces == 1) {
-        orow[lane] = f32_to_bf16_rne(static_cast<float>(o0 / l)) |
-                     (static_cast<uint32_t>(f32_to_bf16_rne(static_cast<float>(o1 / l))) << 16);
+        orow[lane] = f32_to_bf16_out(static_cast<float>(o0 / l)) |
+                     (static_cast<uint32_t>(f32_to_bf16_out(static_cast<float>(o1 / l))) << 16);
         return;
     }
     const int64_t slot0 = static_cast<int64_t>(seg) * a.pieces_cap;
@@ -1242,8 +1242,8 @@ __global__ __launch_bounds__(kSingleWaves * kWave) void decode_single_kernel(Dec
             }
         }
     }
-    orow[lane] = f32_to_bf16_rne(static_cast<float>(o0 / l)) |
-                 (static_cast<uint32_t>(f32_to_bf16_rne(static_cast<float>(o1 / l))) << 16);
+    orow[lane] = f32_to_bf16_out(static_cast<float>(o0 / l)) |
+                 (static_cast<uint32_t>(f32_to_bf16_out(static_cast<float>(o1 / l))) << 16);
 }
 
 // ---------------------------------------------------------------------------------
@@ -1625,8 +1625,8 @@ __global__ __launch_bounds__(kWave) void rescore_kernel(PrefillArgs a) {
         }
         uint32_t* orow = reinterpret_cast<uint32_t*>(a.out + static_cast<int64_t>(row) * kD);
         if (np == 1) {
-            orow[lane] = f32_to_bf16_rne(static_cast<float>(o0 / l_tot)) |
-                         (static_cast<uint32_t>(f32_to_bf16_rne(static_cast<float>(o1 / l_tot))) << 16);
+            orow[lane] = f32_to_bf16_out(static_cast<float>(o0 / l_tot)) |
+                         (static_cast<uint32_t>(f32_to_bf16_out(static_cast<float>(o1 / l_tot))) << 16);
         } else {
             const int64_t slot = slot0 + piece;
             unsigned long long* po = reinterpret_cast<unsigned long long*>(a.rs_part_o + slot * kD) + 2 * lane;
@@ -1672,8 +1672,8 @@ __global__ __launch_bounds__(kWave) void rescore_kernel(PrefillArgs a) {
                         }
                     }
                 }
-                orow[lane] = f32_to_bf16_rne(static_cast<float>(o0 / lw)) |
-                             (static_cast<uint32_t>(f32_to_bf16_rne(static_cast<float>(o1 / lw))) << 16);
+                orow[lane] = f32_to_bf16_out(static_cast<float>(o0 / lw)) |
+                             (static_cast<uint32_t>(f32_to_bf16_out(static_cast<float>(o1 / lw))) << 16);
             }
         }
         __syncthreads();                // o_s is rewritten by the next work item

@@ -43,6 +43,18 @@ __device__ __forceinline__ uint16_t f32_to_bf16_rne(float f) {
     return static_cast<uint16_t>(u >> 16);
 }
 
+// An attention output element -> BF16 code: f32_to_bf16_rne, except that a NaN becomes
+// 0xffc0.  The golden's f32_to_bf16 keeps a NaN's sign (pyfiles/gqa_reference.py:17-19),
+// and on the x86 hosts the golden runs on, a NaN that an invalid operation creates
+// (inf - inf, 0 * inf: the only way a row of finite or infinite inputs reaches NaN) is
+// the default NaN, whose sign bit is set; every later operation passes it on.  (A NaN
+// input in a key the row reads keeps its own sign in the golden; that is not followed.)
+__device__ __forceinline__ uint16_t f32_to_bf16_out(float f) {
+    const uint32_t u = __float_as_uint(f);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return 0xffc0;
+    return static_cast<uint16_t>((u + 0x7fffu + ((u >> 16) & 1u)) >> 16);
+}
+
 // double -> f32 (RNE) -> BF16 (RNE): the reference's f32_to_bf16 path
 // (pyfiles/gqa_reference.py:15-19).
 __device__ __forceinline__ uint16_t f64_to_bf16_via_f32(double d) {

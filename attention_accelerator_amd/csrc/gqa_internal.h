@@ -4,6 +4,7 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "gqa.h"
 #include "gqa_device.h"
 
 namespace gqa {
@@ -56,8 +57,12 @@ struct DecodePlan {
 };
 
 // max_single_segments >= 0 caps the segments (batch * 8) a single-launch plan may count in
-// (its per-segment counters); larger batches take the stream path.
-DecodePlan plan_decode(int32_t batch, int32_t capacity, bool paged = false, int64_t max_single_segments = -1);
+// (its per-segment counters); larger batches take the stream path.  The plan follows the
+// arguments and the device only (params: stream_wgs and the GQA_PLAN_* flags).
+DecodePlan plan_decode(const gqa_params_t* params, int32_t batch, int32_t capacity, bool paged = false,
+                       int64_t max_single_segments = -1);
+// Largest gqa_params_t.stream_wgs accepted.
+constexpr int32_t kStreamWgsMax = 65536;
 // ev (optional): three events recorded before the split kernel, between the two
 // kernels and after the combine kernel.
 hipError_t launch_decode(const DecodeArgs& a, int batch, hipStream_t stream,
@@ -208,7 +213,7 @@ constexpr int kRsMaxPieces = 64;                          // pieces per row at m
 // ceil(T / 64) + 1 and 64; multi-token: 1 and T); nblk: 64-position blocks of the cache
 // (prefill; 0 for multi-token).
 size_t rescore_bytes(int32_t batch, int32_t n_new, int32_t ncb, int32_t nr, int32_t nblk);
-void rescore_layout(PrefillArgs& a, void* base, int32_t ncb, int32_t nr, int32_t nblk);
+void rescore_layout(PrefillArgs& a, const gqa_params_t* params, void* base, int32_t ncb, int32_t nr, int32_t nblk);
 // Prefill: the cached-key maxima from the staging kernel's block maxima.
 hipError_t launch_prefill_stat_reduce(const PrefillArgs& a, hipStream_t stream);
 // The flag decision over every output row (after the MFMA kernels), then the rescore.

@@ -731,10 +731,10 @@ __device__ __forceinline__ void mt_piece_end(const PrefillArgs& a, int b, int kv
 #pragma unroll
         for (int dt = 0; dt < 8; ++dt) {
             uint2 pk;
-            pk.x = f32_to_bf16_rne(static_cast<float>(x[dt][0])) |
-                   (static_cast<uint32_t>(f32_to_bf16_rne(static_cast<float>(x[dt][1]))) << 16);
-            pk.y = f32_to_bf16_rne(static_cast<float>(x[dt][2])) |
-                   (static_cast<uint32_t>(f32_to_bf16_rne(static_cast<float>(x[dt][3]))) << 16);
+            pk.x = f32_to_bf16_out(static_cast<float>(x[dt][0])) |
+                   (static_cast<uint32_t>(f32_to_bf16_out(static_cast<float>(x[dt][1]))) << 16);
+            pk.y = f32_to_bf16_out(static_cast<float>(x[dt][2])) |
+                   (static_cast<uint32_t>(f32_to_bf16_out(static_cast<float>(x[dt][3]))) << 16);
             *reinterpret_cast<uint2*>(orow + 16 * dt + 4 * g) = pk;
         }
         return;
@@ -1097,7 +1097,7 @@ __global__ __launch_bounds__(256 * kW) void mt_merge_kernel(PrefillArgs a) {
     }
     uint16_t h8[8];
 #pragma unroll
-    for (int j = 0; j < 8; ++j) h8[j] = f32_to_bf16_rne(static_cast<float>(o[j] / l));
+    for (int j = 0; j < 8; ++j) h8[j] = f32_to_bf16_out(static_cast<float>(o[j] / l));
     if ((threadIdx.x & 15) == 0 && a.rs_hdr)
         a.rs_m[(static_cast<int64_t>(b) * a.n_new + tok) * kHq + kvh * kGroup + (col & 3)] = m;
     uint2* dst = reinterpret_cast<uint2*>(a.out + ((static_cast<int64_t>(b) * a.n_new + tok) * kHq + kvh * kGroup +

@@ -1069,10 +1069,10 @@ __global__ __launch_bounds__(kPfThreads) void prefill_attn_kernel(PrefillArgs a)
 #pragma unroll
         for (int dt = 0; dt < 8; ++dt) {
             uint2 pk;
-            pk.x = f32_to_bf16_rne(static_cast<float>(x[dt][0])) |
-                   (static_cast<uint32_t>(f32_to_bf16_rne(static_cast<float>(x[dt][1]))) << 16);
-            pk.y = f32_to_bf16_rne(static_cast<float>(x[dt][2])) |
-                   (static_cast<uint32_t>(f32_to_bf16_rne(static_cast<float>(x[dt][3]))) << 16);
+            pk.x = f32_to_bf16_out(static_cast<float>(x[dt][0])) |
+                   (static_cast<uint32_t>(f32_to_bf16_out(static_cast<float>(x[dt][1]))) << 16);
+            pk.y = f32_to_bf16_out(static_cast<float>(x[dt][2])) |
+                   (static_cast<uint32_t>(f32_to_bf16_out(static_cast<float>(x[dt][3]))) << 16);
             *reinterpret_cast<uint2*>(orow + 16 * dt + 4 * g) = pk;
         }
     }

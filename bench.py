@@ -457,7 +457,7 @@ def bench_multitoken(args, torch, gqa, dev, stimulus) -> int:
         # Chunks of at most 16 new tokens run the stream-K path (events: preparation with
         # the append, then the stream kernel); longer ones the prefill attention kernel
         # (events: append, then attention).
-        stream_k = n_new <= 16 and os.environ.get("GQA_PREFILL_MULTI", "1") != "0"
+        stream_k = n_new <= 16
         achieved = step_bytes / (attn_ms * 1e-3) / 1e9
         roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                     "frac": round(achieved / HBM_PEAK_GBS, 4),

@@ -51,9 +51,19 @@ enum gqa_status {
 #define GQA_ROPE_Q 1u
 #define GQA_ROPE_K 2u
 
+/* Plan flags (no counterpart in the reference; tests and tuning, results stay within the
+ * same tolerance): GQA_PLAN_STREAM_K makes every contiguous decode call take the
+ * three-launch stream-K plan (small batches otherwise run as one launch);
+ * GQA_PLAN_NO_MULTI_TOKEN sends chunks of at most 16 new tokens through the prefill
+ * attention kernel instead of the multi-token stream-K path.  Workspace sizes follow them. */
+#define GQA_PLAN_STREAM_K 4u
+#define GQA_PLAN_NO_MULTI_TOKEN 8u
+
 /* Geometry, scale and RoPE: the register subset that shapes the arithmetic.
  * Only n_q_heads=32, n_kv_heads=8, head_dim=128 are accepted
- * (gqa_attention_wrapper.v:231-233). */
+ * (gqa_attention_wrapper.v:231-233).  Zero-initialise the struct: stream_wgs = 0 is the
+ * default.  Every workspace size depends on these fields, the call's sizes and the current
+ * device's CU count only (never on the environment). */
 typedef struct gqa_params {
     int32_t n_q_heads;
     int32_t n_kv_heads;
@@ -61,7 +71,9 @@ typedef struct gqa_params {
     double scale;         /* score scale, normally 1/sqrt(128) (the golden's double,
                              gen_gqa_wrapper_vectors.py:129); 0 is rejected (wrapper.v:237) */
     double rope_theta;    /* normally 500000; must be > 0 when a RoPE flag is set */
-    uint32_t flags;       /* GQA_ROPE_Q | GQA_ROPE_K */
+    uint32_t flags;       /* GQA_ROPE_Q | GQA_ROPE_K, GQA_PLAN_* */
+    int32_t stream_wgs;   /* persistent workgroups of the stream-K kernels: 0 = four per CU
+                             of the current device (tuning and tests: 1 .. 65536) */
 } gqa_params_t;
 
 /* Where K/V rows live.  Row (sequence b, KV head h, position p) starts at element
@@ -205,10 +217,9 @@ int gqa_kv_append_paged_bf16(const gqa_params_t* params, const uint16_t* k_new, 
  * run the KV append, a staging kernel that copies the K/V rows the attention reads into
  * fp16 planes in the workspace (a power-of-two scale per 64-position block, so BF16 values
  * convert exactly), and one attention kernel over 32-token query blocks.  Every path ends
- * with an fp64 recomputation of the output rows its kernels flag.  The environment variable
- * GQA_PREFILL_MULTI=0 sends short chunks to the attention kernel too; the workspace size
- * follows that choice and GQA_STREAM_WGS, so query it under the same environment as the
- * call.  For longer chunks it grows with capacity (the staging planes hold 512 bytes per
+ * with an fp64 recomputation of the output rows its kernels may have computed outside 64
+ * BF16 ULP.  GQA_PLAN_NO_MULTI_TOKEN sends short chunks to the attention kernel too.  For
+ * longer chunks the workspace grows with capacity (the staging planes hold 512 bytes per
  * position of every (sequence, KV head): 143 MB for batch 4 over 8704 positions). */
 size_t gqa_prefill_workspace_bytes(const gqa_params_t* params, int32_t batch, int32_t n_new,
                                    int32_t capacity);

@@ -33,7 +33,7 @@ def test_exports_match_header():
 def test_status_strings_and_version():
     assert _lib.status_string(0) == "ok"
     assert "invalid" in _lib.status_string(1)
-    assert _lib.lib().gqa_abi_version() >> 16 == 3
+    assert _lib.lib().gqa_abi_version() >> 16 == 4
 
 
 @pytest.mark.parametrize("regs,ok", [
@@ -98,7 +98,9 @@ def _decode(p, *, q=256, k=256, v=256, layout=None, sl=256, qp=256, batch=1, out
     (dict(p=_params(scale=0.0)), BAD_CFG),
     (dict(p=_params(scale=float("nan"))), BAD_CFG),
     (dict(p=_params(rope_theta=0.0)), BAD_CFG),
-    (dict(p=_params(flags=8)), BAD_CFG),
+    (dict(p=_params(flags=16)), BAD_CFG),
+    (dict(p=_params(stream_wgs=-1)), BAD_CFG),
+    (dict(p=_params(stream_wgs=65537)), BAD_CFG),
     (dict(p=_params(), batch=0), BAD_CFG),
     (dict(p=_params(), layout=GqaKvLayout(0, 0, 64, 64)), BAD_CFG),
     (dict(p=_params(), layout=GqaKvLayout(0, 0, 128, 0)), BAD_CFG),
@@ -203,18 +205,69 @@ def test_kv_append_rejects_before_launch():
 
 
 def test_workspace_plan_tag():
-    """A workspace tagged with its (batch, capacity) plan is rejected for another plan
-    (the single-launch counters sit at a plan-dependent offset); untagged buffers pass."""
+    """A workspace tagged with its plan (batch, capacity, plan flags, stream_wgs) is rejected
+    for another plan (the single-launch counters sit at a plan-dependent offset); untagged
+    buffers pass."""
     import torch
-    from attention_accelerator_amd.attention import _check_workspace_plan
+    from attention_accelerator_amd.attention import _check_workspace_plan, _plan_key, make_params
+    p = make_params()
     ws = torch.empty(16, dtype=torch.uint8)
-    _check_workspace_plan(ws, 4, 1000)                 # untagged: the caller's contract
-    ws.gqa_decode_plan = (4, 1000)
-    _check_workspace_plan(ws, 4, 1000)
-    with pytest.raises(ValueError, match="prepared for"):
-        _check_workspace_plan(ws, 4, 2000)
-    with pytest.raises(ValueError, match="prepared for"):
-        _check_workspace_plan(ws, 3, 1000)
+    _check_workspace_plan(ws, p, 4, 1000)                 # untagged: the caller's contract
+    ws.gqa_decode_plan = _plan_key(p, 4, 1000)
+    _check_workspace_plan(ws, p, 4, 1000)
+    _check_workspace_plan(ws, make_params(rope_k=True), 4, 1000)      # RoPE flags do not move it
+    for args in ((p, 4, 2000), (p, 3, 1000), (make_params(stream_k=True), 4, 1000),
+                 (make_params(stream_wgs=96), 4, 1000)):
+        with pytest.raises(ValueError, match="prepared for"):
+            _check_workspace_plan(ws, *args)
+
+
+_SIZES_SCRIPT = r"""
+import ctypes, json
+from attention_accelerator_amd import _lib
+from attention_accelerator_amd.attention import make_params
+L = _lib.lib()
+out = []
+for kw in ({}, {"stream_wgs": 96}, {"stream_k": True}, {"multi_token": False}):
+    p = make_params(rope_k=True, **kw)
+    out.append([L.gqa_decode_workspace_bytes(ctypes.byref(p), b, c) for b, c in ((4, 2048), (64, 8192))]
+               + [L.gqa_decode_paged_workspace_bytes(ctypes.byref(p), 64, 512)]
+               + [L.gqa_prefill_workspace_bytes(ctypes.byref(p), b, t, c)
+                  for b, t, c in ((64, 16, 8208), (64, 8, 8200), (4, 512, 8704))]
+               + [L.gqa_prefill_rescored_rows_offset(ctypes.byref(p), 64, 16, 8208)])
+print(json.dumps(out))
+"""
+
+
+def test_workspace_sizes_ignore_the_environment():
+    """Workspace sizes (and the rescored-row offset) follow the arguments only: the same
+    numbers in processes whose environments set the variables that once chose the plan and
+    the XCD weighting of the ranges (which moves no buffer)."""
+    import json
+    import os
+    import subprocess
+    import sys
+    envs = [{}, {"GQA_STREAM_WGS": "96", "GQA_PREFILL_MULTI": "0", "GQA_SINGLE_LAUNCH_MAX_KEYS": "0",
+                 "GQA_XCD_SKEW": "250"}]
+    runs = []
+    for extra in envs:
+        env = dict(os.environ)
+        for k in ("GQA_STREAM_WGS", "GQA_PREFILL_MULTI", "GQA_SINGLE_LAUNCH_MAX_KEYS", "GQA_XCD_SKEW"):
+            env.pop(k, None)
+        env.update(extra)
+        env["PYTHONPATH"] = str(ROOT) + os.pathsep + env.get("PYTHONPATH", "")
+        r = subprocess.run([sys.executable, "-c", _SIZES_SCRIPT], env=env, cwd=str(ROOT),
+                           capture_output=True, text=True, timeout=120)
+        assert r.returncode == 0, r.stderr
+        runs.append(json.loads(r.stdout.strip().splitlines()[-1]))
+    assert runs[0] == runs[1]
+    sizes = runs[0]
+    assert all(n > 0 for row in sizes for n in row)
+    # the params fields do choose the plan: stream_wgs moves the stream-K buffers, stream_k
+    # the small decode batch's plan, multi_token the short chunks' path
+    assert sizes[1][1] != sizes[0][1] and sizes[1][3] != sizes[0][3]
+    assert sizes[2][0] != sizes[0][0]
+    assert sizes[3][3] != sizes[0][3] and sizes[3][5] == sizes[0][5]
 
 
 def test_python_shape_checks_before_any_launch():

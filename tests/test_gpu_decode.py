@@ -107,14 +107,12 @@ def test_deterministic(dev):
 
 
 @pytest.mark.parametrize("wgs", ["1", "7", "333", "2048", "6000"])
-def test_stream_partition_invariance(dev, wgs, monkeypatch):
+def test_stream_partition_invariance(dev, wgs):
     """The key space cut into 1 .. 6000 workgroup ranges (pieces start and end at
     arbitrary keys, ranges span several sequences and heads, up to 47 pieces per
     segment): same parity."""
     b = stimulus.decode_batch(5, 3000, min_len=1, max_len=3000, seed=9)
-    monkeypatch.setenv("GQA_STREAM_WGS", wgs)
-    monkeypatch.setenv("GQA_SINGLE_LAUNCH_MAX_KEYS", "0")       # the stream-K path
-    got = _run(b, dev)
+    got = _run(b, dev, params=gqa.make_params(stream_k=True, stream_wgs=int(wgs)))
     assert_within_ulp(_oracle(b), got, 64, f"{wgs} workgroups")
 
 
@@ -124,25 +122,21 @@ def test_stream_xcd_skew_bounds(dev, wgs, skew, monkeypatch):
     """Equal ranges (skew 0) and the largest XCD weighting (odd ranges 3/4 of the range
     size, even ones 5/4): the same parity on the stream and paged-free path."""
     b = stimulus.decode_batch(5, 3000, min_len=1, max_len=3000, seed=10)
-    monkeypatch.setenv("GQA_STREAM_WGS", wgs)
-    monkeypatch.setenv("GQA_SINGLE_LAUNCH_MAX_KEYS", "0")
     monkeypatch.setenv("GQA_XCD_SKEW", skew)
-    got = _run(b, dev)
+    got = _run(b, dev, params=gqa.make_params(stream_k=True, stream_wgs=int(wgs)))
     assert_within_ulp(_oracle(b), got, 64, f"{wgs} workgroups, skew={skew}")
 
 
 @pytest.mark.parametrize("wgs", ["16", "200", "1024", "5000"])
-def test_single_launch_pieces(dev, wgs, monkeypatch):
+def test_single_launch_pieces(dev, wgs):
     """Small batches run as one launch whose pieces (256 keys and up, here 256 .. 18432)
     merge in-kernel: parity for every piece size, and the stream-K path agrees to 1 BF16
     ULP (both carry every step in fp64; only the order of the sums differs)."""
     b = stimulus.decode_batch(4, 2300, min_len=1, max_len=2300, seed=19)
-    monkeypatch.setenv("GQA_STREAM_WGS", wgs)
-    single = _run(b, dev)
+    single = _run(b, dev, params=gqa.make_params(stream_wgs=int(wgs)))
     want = _oracle(b)
     assert_within_ulp(want, single, 64, f"single launch, {wgs}")
-    monkeypatch.setenv("GQA_SINGLE_LAUNCH_MAX_KEYS", "0")
-    stream = _run(b, dev)
+    stream = _run(b, dev, params=gqa.make_params(stream_k=True, stream_wgs=int(wgs)))
     assert_within_ulp(stream, single, 1, "single launch vs stream-K")
 
 
@@ -170,15 +164,15 @@ def test_single_launch_workspace_init_and_reuse(dev):
             assert np.array_equal(got, ref)
 
 
-def test_workspace_reuse_across_calls(dev, monkeypatch):
+def test_workspace_reuse_across_calls(dev):
     """A prepared call reuses one workspace: repeated calls give identical bits, and
     the same workspace then serves other inputs."""
     from attention_accelerator_amd.attention import PreparedDecode
-    monkeypatch.setenv("GQA_SINGLE_LAUNCH_MAX_KEYS", "0")
+    sk = gqa.make_params(stream_k=True)
     b = stimulus.decode_batch(6, 2500, min_len=1, max_len=2500, seed=17)
-    ref = _run(b, dev)
+    ref = _run(b, dev, params=sk)
     call = PreparedDecode(b.q.to(dev), b.k.to(dev), b.v.to(dev), b.query_pos.to(dev),
-                          b.seq_len.to(dev))
+                          b.seq_len.to(dev), params=sk)
     for _ in range(3):
         out = call()
         torch.cuda.synchronize()
@@ -186,7 +180,7 @@ def test_workspace_reuse_across_calls(dev, monkeypatch):
     # same workspace, other contents
     b2 = stimulus.decode_batch(6, 2500, min_len=1, max_len=2500, seed=18)
     out2 = gqa.gqa_attention(b2.q.to(dev), b2.k.to(dev), b2.v.to(dev), b2.query_pos, b2.seq_len,
-                             workspace=call.workspace)
+                             workspace=call.workspace, params=sk)
     assert_within_ulp(_oracle(b2), _codes(out2), 64, "reused workspace")
 
 
@@ -225,13 +219,12 @@ def test_device_resident_lengths(dev):
 
 
 @pytest.mark.parametrize("path", ["single", "three"])
-def test_invalid_device_lengths_give_nan_rows(dev, path, monkeypatch):
-    if path != "single":
-        monkeypatch.setenv("GQA_SINGLE_LAUNCH_MAX_KEYS", "0")
+def test_invalid_device_lengths_give_nan_rows(dev, path):
+    p = gqa.make_params(stream_k=path != "single")
     b = stimulus.decode_batch(3, 256, lengths=torch.tensor([100, 50, 200]), seed=15)
     qpos = torch.tensor([99, 50, 199], dtype=torch.int32)      # sequence 1: qpos == seq_len
     out = _codes(gqa.gqa_attention(b.q.to(dev), b.k.to(dev), b.v.to(dev), qpos.to(dev),
-                                   b.seq_len.to(dev)))
+                                   b.seq_len.to(dev), params=p))
     assert (out[1] == 0x7FC0).all()
     good = stimulus.DecodeBatch(b.q[[0, 2]], b.k[[0, 2]], b.v[[0, 2]], b.seq_len[[0, 2]],
                                 qpos[[0, 2]])
@@ -239,19 +232,18 @@ def test_invalid_device_lengths_give_nan_rows(dev, path, monkeypatch):
 
 
 @pytest.mark.parametrize("path", ["single", "three"])
-def test_huge_scores(dev, path, monkeypatch):
+def test_huge_scores(dev, path):
     """Q heads scaled by 2^40 and 2^100 (scores far beyond 2^24 in log2 units, a one-hot
     softmax in the double golden): the running max and the pieces' (m, l) are doubles, so
     the largest key keeps p = 1 in every piece and the merge weights stay exact; every row,
     the scaled heads' and the others', within 64 ULP of the oracle."""
-    if path != "single":
-        monkeypatch.setenv("GQA_SINGLE_LAUNCH_MAX_KEYS", "0")
     b = stimulus.decode_batch(4, 700, min_len=300, max_len=700, seed=41)
     q = b.q.clone()
     q[0, 3] = (q[0, 3].float() * 2.0 ** 100).to(torch.bfloat16)
     q[2, 17] = (q[2, 17].float() * 2.0 ** 40).to(torch.bfloat16)
     b = stimulus.DecodeBatch(q, b.k, b.v, b.seq_len, b.query_pos)
-    assert_within_ulp(_oracle(b), _run(b, dev), 64, f"huge scores ({path})")
+    got = _run(b, dev, params=gqa.make_params(stream_k=path != "single"))
+    assert_within_ulp(_oracle(b), got, 64, f"huge scores ({path})")
 
 
 def test_host_validation_rejects(dev):
@@ -278,7 +270,7 @@ def test_batch64_ragged_512_8192(dev):
 
 
 @pytest.mark.parametrize("bsz,hi,seed", [(300, 600, 31), (1000, 48, 32)])
-def test_many_sequences(dev, bsz, hi, seed, monkeypatch):
+def test_many_sequences(dev, bsz, hi, seed):
     """Batches spanning many 64-sequence windows of the plan (300 sequences up to 600 keys;
     1000 sequences of 1..48 keys, many segments per workgroup range): every output against
     the oracle.  N(0,1) V: with a few dozen keys
@@ -287,10 +279,10 @@ def test_many_sequences(dev, bsz, hi, seed, monkeypatch):
     in fp32 once missed it here (72 ULP); carried in fp64 they meet it."""
     b = stimulus.decode_batch(bsz, hi, min_len=1, max_len=hi, seed=seed)
     want, want64 = _oracle(b, want_f64=True)
-    monkeypatch.setenv("GQA_SINGLE_LAUNCH_MAX_KEYS", "0")
-    got = _run(b, dev)
+    sk = gqa.make_params(stream_k=True)
+    got = _run(b, dev, params=sk)
     assert_within_ulp(want, got, 64, f"B={bsz}", ref64=want64)
-    assert np.array_equal(_run(b, dev), got)
+    assert np.array_equal(_run(b, dev, params=sk), got)
 
 
 def test_long_context_131072(dev):

@@ -74,16 +74,14 @@ def _decode(q, k, v, qpos, seq_len, dev, path):
                                    table.reshape(b, n_blk).to(dev), qpos, seq_len,
                                    rope_q=False, rope_k=False, scale=1.0)
     else:
-        out = gqa.gqa_attention(q.to(dev), k.to(dev), v.to(dev), qpos, seq_len,
-                                rope_q=False, rope_k=False, scale=1.0)
+        p = gqa.make_params(rope_q=False, rope_k=False, scale=1.0, stream_k=path == "stream")
+        out = gqa.gqa_attention(q.to(dev), k.to(dev), v.to(dev), qpos, seq_len, params=p)
     torch.cuda.synchronize()
     return to_codes(out)
 
 
 @pytest.fixture(params=["single", "stream", "paged"])
-def decode_path(request, monkeypatch):
-    if request.param == "stream":
-        monkeypatch.setenv("GQA_SINGLE_LAUNCH_MAX_KEYS", "0")
+def decode_path(request):
     return request.param
 
 

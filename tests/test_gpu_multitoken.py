@@ -125,29 +125,28 @@ def test_multi_long_sequences(dev):
 
 @pytest.mark.parametrize("n_new,n_wgs", [(4, "1"), (4, "7"), (4, "64"), (4, "333"), (4, "4096"),
                                          (7, "2"), (7, "130"), (12, "4"), (12, "37"), (16, "1024")])
-def test_multi_partition_counts(dev, monkeypatch, n_new, n_wgs):
-    """The split of the keys over workgroups (from GQA_STREAM_WGS: that many one-wave
+def test_multi_partition_counts(dev, n_new, n_wgs):
+    """The split of the keys over workgroups (params.stream_wgs: that many one-wave
     workgroups for T <= 4, twice as many waves in workgroups of 2 or 4 for longer chunks)
     changes the order of the partial sums only: every split stays within the tolerance of
     the oracle."""
-    monkeypatch.setenv("GQA_STREAM_WGS", n_wgs)
     starts = [5, 1200, 64, 2999, 0, 17]
     q, kn, vn, k, v = _chunk(starts, n_new, 3016, 42)
     want = _oracle(q, kn, vn, k, v, starts)
-    got, _, _ = _run(q, kn, vn, k, v, starts, dev)
+    got, _, _ = _run(q, kn, vn, k, v, starts, dev, params=gqa.make_params(rope_k=True, stream_wgs=int(n_wgs)))
     _check(want, got, f"multi T={n_new} wgs={n_wgs}")
 
 
 @pytest.mark.parametrize("n_new", [4, 16])
-def test_multi_and_prefill_kernel_agree(dev, monkeypatch, n_new):
+def test_multi_and_prefill_kernel_agree(dev, n_new):
     """The same chunk through the stream-K path and through the prefill attention kernel
-    (GQA_PREFILL_MULTI=0): both within the tolerance of the oracle, caches bit-identical."""
+    (params without the multi-token plan): both within the tolerance of the oracle, caches
+    bit-identical."""
     starts = [77, 1024, 300]
     q, kn, vn, k, v = _chunk(starts, n_new, 1100, 43)
     want = _oracle(q, kn, vn, k, v, starts)
     a, ka, va = _run(q, kn, vn, k, v, starts, dev)
-    monkeypatch.setenv("GQA_PREFILL_MULTI", "0")
-    b, kb, vb = _run(q, kn, vn, k, v, starts, dev)
+    b, kb, vb = _run(q, kn, vn, k, v, starts, dev, params=gqa.make_params(rope_k=True, multi_token=False))
     _check(want, a, "stream-K path")
     _check(want, b, "prefill kernel path")
     assert np.array_equal(to_codes(ka), to_codes(kb)) and np.array_equal(to_codes(va), to_codes(vb))
@@ -244,11 +243,10 @@ def test_multi_xcd_skew_bounds(dev, monkeypatch, skew):
     """Equal ranges (skew 0) and the largest XCD weighting (odd ranges 3/4 of the size, even
     ones 5/4) over a short and a long batch: every row within the tolerance of the oracle."""
     monkeypatch.setenv("GQA_XCD_SKEW", skew)
-    monkeypatch.setenv("GQA_STREAM_WGS", "96")
     starts = [5, 1200, 64, 2999, 0, 17, 640]
     q, kn, vn, k, v = _chunk(starts, 4, 3010, 49)
     want = _oracle(q, kn, vn, k, v, starts)
-    got, _, _ = _run(q, kn, vn, k, v, starts, dev)
+    got, _, _ = _run(q, kn, vn, k, v, starts, dev, params=gqa.make_params(rope_k=True, stream_wgs=96))
     _check(want, got, f"multi skew={skew}")
 
 
@@ -270,15 +268,15 @@ def test_multi_long_context_sampled_rows(dev):
 
 
 @pytest.mark.parametrize("n_wgs", ["1", "7", "64", "1024"])
-def test_rescore_proportional_pieces(dev, monkeypatch, n_wgs):
+def test_rescore_proportional_pieces(dev, n_wgs):
     """At most 64 flagged rows: each row's keys are cut into pieces in proportion to its
     length (a row of 3001 keys gets about 30 times the pieces of one of 91), for rescore
-    grids of 1 (fewer workgroups than rows), 7, 64 and 1024 workgroups (GQA_STREAM_WGS sets
-    the grid).  Q is scaled by 2^100 and K by 2^40, so every dot product passes the fp32 range and all
+    grids of 1 (fewer workgroups than rows), 7, 64 and 1024 workgroups (params.stream_wgs
+    sets the grid).  Q is scaled by 2^100 and K by 2^40, so every dot product passes the fp32 range and all
     64 rows (2 sequences x 1 token x 32 heads) of the MFMA kernels come out not finite and
     are rescored; every row must match the oracle, and V dimension 5, zero in every key,
     exactly."""
-    monkeypatch.setenv("GQA_STREAM_WGS", n_wgs)
+    p = gqa.make_params(rope_k=True, stream_wgs=int(n_wgs))
     starts = [90, 3000]
     q, kn, vn, k, v = _chunk(starts, 1, 3001, 77)
     vn[..., 5] = 0.0
@@ -288,9 +286,9 @@ def test_rescore_proportional_pieces(dev, monkeypatch, n_wgs):
     kn = (kn.float() * 2.0 ** 40).to(torch.bfloat16)
     k = (k.float() * 2.0 ** 40).to(torch.bfloat16)
     want = _oracle(q, kn, vn, k, v, starts)
-    ws = torch.empty(gqa.prefill_workspace_bytes(2, 1, 3001), dtype=torch.uint8, device=dev)
-    got, _, _ = _run(q, kn, vn, k, v, starts, dev, workspace=ws)
-    assert gqa.prefill_rescored_rows(ws, 2, 1, 3001) == 64
+    ws = torch.empty(gqa.prefill_workspace_bytes(2, 1, 3001, params=p), dtype=torch.uint8, device=dev)
+    got, _, _ = _run(q, kn, vn, k, v, starts, dev, workspace=ws, params=p)
+    assert gqa.prefill_rescored_rows(ws, 2, 1, 3001, params=p) == 64
     assert np.all(got[..., 5] == 0)
     _check(want, got.reshape(-1, 128), f"64 flagged rows, {n_wgs} rescore workgroups")
 

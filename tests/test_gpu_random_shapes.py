@@ -41,7 +41,7 @@ def _perturb(rng, t: torch.Tensor, head_axis: int):
     return _bf(t.float() * f), f"x 2^{int(np.log2(f))}"
 
 
-def _decode_case(rng, g, dev, paged: bool, single: bool, monkeypatch):
+def _decode_case(rng, g, dev, paged: bool, single: bool):
     batch = int(rng.integers(1, 25))
     cap = int(rng.integers(1, 1500))
     if paged:
@@ -60,8 +60,6 @@ def _decode_case(rng, g, dev, paged: bool, single: bool, monkeypatch):
         v[b, :, sl[b]:] = float("nan")
     what = f"{'paged' if paged else 'decode'} B={batch} cap={cap} rope_k={rope_k} q {dq}, k {dk}, v {dv}"
     print(what, flush=True)
-    if not single:
-        monkeypatch.setenv("GQA_SINGLE_LAUNCH_MAX_KEYS", "0")
     if paged:
         nb = cap // 16
         table = torch.from_numpy(rng.permutation(batch * nb).astype(np.int32)).reshape(batch, nb)
@@ -75,7 +73,7 @@ def _decode_case(rng, g, dev, paged: bool, single: bool, monkeypatch):
                                    [int(x) for x in sl], rope_k=rope_k)
     else:
         out = gqa.gqa_attention(q.to(dev), k.to(dev), v.to(dev), [int(x) for x in qp], [int(x) for x in sl],
-                                rope_k=rope_k)
+                                params=gqa.make_params(rope_k=rope_k, stream_k=not single))
     torch.cuda.synchronize()
     want = orc.decode(to_codes(q), to_codes(k), to_codes(v), sl, qp, rope_k=rope_k)
     return want, to_codes(out), what
@@ -115,12 +113,12 @@ def _chunk_case(rng, g, dev, kind: str):
 
 
 @pytest.mark.parametrize("seed", range(24))
-def test_random_case(dev, monkeypatch, seed):
+def test_random_case(dev, seed):
     rng = np.random.default_rng(9100 + seed)
     g = torch.Generator("cpu").manual_seed(9100 + seed)
     kind = ["decode", "decode1", "paged", "multi", "multi", "prefill", "chunk0"][seed % 7]
     if kind in ("decode", "decode1", "paged"):
-        want, got, what = _decode_case(rng, g, dev, kind == "paged", kind == "decode1", monkeypatch)
+        want, got, what = _decode_case(rng, g, dev, kind == "paged", kind == "decode1")
     else:
         want, got, what = _chunk_case(rng, g, dev, kind)
     assert_within_ulp(want.reshape(-1, 128), got.reshape(-1, 128), 64, what)
