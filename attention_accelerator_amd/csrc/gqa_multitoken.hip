@@ -480,12 +480,12 @@ __device__ __forceinline__ void mt_flush(MtState& t) {
 //    V: the V^T operand of dim tile dt gives lane (g, n) 8 keys of dim 16 dt + n: vmax[dt].
 //  * Two or four tiles (their registers are all in use): each wave reads its 32/W keys of
 //    the window from LDS after the window's V^T P^T.  K: lane l takes key (l >> 3) (+ 8 j)
-//    and the two 16-byte chunks of pair group l & 7: kmax[0].  V: lane l takes dims 2l and
-//    2l + 1 of each of its keys: vmax[0].
+//    and the two 16-byte chunks of pair group l & 7: kmax[0].  V: lane l takes dims
+//    8 (l & 15) .. +7 of key (l >> 4) (+ 4 j): vmax[0..3].
 template <int kW>
 struct MtStats {
     static constexpr int kNk = kW == 1 ? 2 : 1;
-    static constexpr int kNv = kW == 1 ? 8 : 1;
+    static constexpr int kNv = kW == 1 ? 8 : 4;
     uint32_t kmax[kNk];                             // squared group norms, fp32 bits
     uint32_t vmax[kNv];                             // two |V| codes per dword
 };
@@ -574,13 +574,18 @@ __device__ __forceinline__ void mt_stats_window(const uint8_t* kplane, const uin
         sq = bf16x2_sq_acc(hi.w, sq);
         ms.kmax[0] = max(ms.kmax[0], row < lim ? __float_as_uint(sq) : 0u);
     }
-    const int vchunk = lane >> 2;
-    const int vword = 4 * (lane & 3);
+    // V: lane l takes dims 8 (l & 15) .. +7 of key (l >> 4) (+ 4 j): one 16-byte read per
+    // lane and four keys per instruction; the lanes of a dim are combined once per piece.
+    const int vc = lane & 15;
 #pragma unroll
-    for (int j = 0; j < kKeys; ++j) {
-        const int row = kKeys * wv + j;
-        const uint32_t x = *reinterpret_cast<const uint32_t*>(vplane + row * kRowB + 16 * (vchunk ^ pf_swz(row)) + vword);
-        ms.vmax[0] = pk_max_u16(ms.vmax[0], x & (row < lim ? 0x7fff7fffu : 0u));
+    for (int j = 0; j < kKeys / 4; ++j) {
+        const int row = kKeys * wv + 4 * j + (lane >> 4);
+        const uint4 x = *reinterpret_cast<const uint4*>(vplane + row * kRowB + 16 * (vc ^ pf_swz(row)));
+        const uint32_t m = row < lim ? 0x7fff7fffu : 0u;
+        ms.vmax[0] = pk_max_u16(ms.vmax[0], x.x & m);
+        ms.vmax[1] = pk_max_u16(ms.vmax[1], x.y & m);
+        ms.vmax[2] = pk_max_u16(ms.vmax[2], x.z & m);
+        ms.vmax[3] = pk_max_u16(ms.vmax[3], x.w & m);
     }
 }
 
@@ -776,10 +781,15 @@ __device__ __forceinline__ void mt_stats_end(const PrefillArgs& a, int64_t seg, 
 #pragma unroll
         for (int sh = 8; sh < kWave; sh <<= 1) x = max(x, static_cast<uint32_t>(__shfl_xor(static_cast<int>(x), sh)));
         if (lane < 8 && x) atomicMax(a.rs_kc + seg * 8 + lane, x);
-        const uint32_t v = ms.vmax[0];
-        uint32_t* dc = a.rs_dc + seg * kD + 2 * lane;
-        if (v & 0xffffu) atomicMax(dc, v & 0xffffu);
-        if (v >> 16) atomicMax(dc + 1, v >> 16);
+        uint32_t* dc = a.rs_dc + seg * kD + 8 * (lane & 15);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            uint32_t v = ms.vmax[i];
+            v = pk_max_u16(v, static_cast<uint32_t>(__shfl_xor(static_cast<int>(v), 16)));
+            v = pk_max_u16(v, static_cast<uint32_t>(__shfl_xor(static_cast<int>(v), 32)));
+            if (lane < 16 && (v & 0xffffu)) atomicMax(dc + 2 * i, v & 0xffffu);
+            if (lane < 16 && (v >> 16)) atomicMax(dc + 2 * i + 1, v >> 16);
+        }
     }
     mt_stats_reset<kW>(ms);
 }
