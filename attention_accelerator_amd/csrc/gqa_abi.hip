@@ -635,13 +635,14 @@ int gqa_prefill_bf16(const gqa_params_t* params, const uint16_t* q, const uint16
         if (e == hipSuccess) e = launch_rescore(a, s);
         return e == hipSuccess ? GQA_OK : GQA_ERR_HIP;
     }
+    // The attention kernel decides the rescore flag of each row it writes, from the K/V
+    // statistics the staging and reduce kernels leave.
     hipError_t e = launch_kv_append(a, s);
     if (e == hipSuccess) e = launch_prefill_stage(a, s);
+    if (e == hipSuccess) e = launch_prefill_stat_reduce(a, s);
     if (ev) (void)hipEventRecord(ev[1], s);
     if (e == hipSuccess) e = launch_prefill_attention(a, s);
     if (ev) (void)hipEventRecord(ev[2], s);
-    if (e == hipSuccess) e = launch_prefill_stat_reduce(a, s);
-    if (e == hipSuccess) e = launch_rs_flag(a, s);
     if (e == hipSuccess) e = launch_rescore(a, s);
     return e == hipSuccess ? GQA_OK : GQA_ERR_HIP;
 }

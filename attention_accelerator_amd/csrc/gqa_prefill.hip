@@ -9,7 +9,7 @@
 // chunk's own K/V rows, rotated at their positions in double and not re-rounded, as
 // the golden rotates K (gen_gqa_wrapper_vectors.py:124-126).
 //
-// Three launches, then the fp64 rescore of flagged rows (gqa_decode.hip):
+// Four launches, then the fp64 rescore of flagged rows (gqa_decode.hip):
 //
 // kv_append_kernel writes the chunk's K rows (rotated, rounded double -> f32 -> BF16,
 // pyfiles/gqa_reference.py:15-19) and V rows into the cache, and the rotated K rows in fp32
@@ -23,7 +23,10 @@
 // fp16 parts (leading + trailing, ~22 bits).  A block holding a non-finite value, a scale
 // outside the fp32 range the attention kernel uses, or a row more than 2^12 below the
 // block's largest magnitude is marked, and the attention kernel hands all rows that read
-// it to the fp64 rescore.
+// it to the fp64 rescore.  It also leaves each block's K pair-group norm and |V| maxima.
+//
+// prefill_stat_reduce_kernel folds those block maxima into the maxima over the keys each
+// chunk block's rows see (the rescore flag's statistics).
 //
 // prefill_attn_kernel: one workgroup of 8 waves per (sequence, KV head, 32 query
 // positions); wave w computes Q head 4*kv_head + (w & 3) for 16 positions.  The staged
@@ -48,7 +51,8 @@
 //    (rounded to nearest: ~22 bits).  Each block's fp32 product is scaled by the block's
 //    V scale into an fp64 accumulator, so accumulation over thousands of keys adds no fp32
 //    rounding.
-//  * O / l, rounded double -> f32 -> BF16, written in Q-head order.
+//  * O / l, rounded double -> f32 -> BF16, written in Q-head order; the row's rescore flag
+//    decided from those BF16 values (pf_flag_row).
 //
 // Chunks of at most 16 new tokens take the multi-token decode path instead
 // (gqa_multitoken.hip), which shares this file's LDS row layout (gqa_prefill_common.h).
@@ -790,6 +794,72 @@ __device__ __forceinline__ void pf_probs_and_next(const f32x4_t (&scur)[4], floa
     t.l64 += ldexp(static_cast<double>(lsum), -static_cast<int>(vshift));
 }
 
+// The rescore flag of one output row, in the attention kernel's layout: lane (g, n) holds
+// dims 16 dt + 4 g + i of query n's row (BF16 codes, pk[dt]).  The same decision as
+// rs_flag_kernel (rs_flag_decide over the row's elements in units of each dim's largest |V|
+// and the scores' bound E = scale log2(e) sum_G |q_G| max|k_G|), over the keys the row at
+// position pos sees: the keys before its chunk block (rs_kc, rs_dc at that block, reduced
+// before this kernel runs) and the block's rows up to its own (rs_kpre, rs_dpre).  Q's
+// pair-group norms come from the row as given (rotation leaves them unchanged): this lane
+// reads dims 8g .. 8g+7 and 32 + 8g .. (and their pairs 64 on), pair groups g and 4 + g.
+// Returns the decision for the row in every lane of its column.
+__device__ __forceinline__ bool pf_flag_row(const PrefillArgs& a, int b, int kvh, int st, int pos, int64_t row,
+                                            float m, bool forced, const uint2 (&pk)[8], int lane) {
+    const int g = lane >> 4;
+    const int cb = pos / kPfBlk - st / kPfBlk;
+    const int r = pos % kPfBlk;
+    const int64_t ec = (static_cast<int64_t>(b) * kHkv + kvh) * a.rs_ncb + cb;
+    const int64_t er = ec * a.rs_nr + r;
+    const uint16_t* qrow = a.q + row * kD;
+    const uint4 q0 = *reinterpret_cast<const uint4*>(qrow + 8 * g);
+    const uint4 q1 = *reinterpret_cast<const uint4*>(qrow + 32 + 8 * g);
+    const uint4 q2 = *reinterpret_cast<const uint4*>(qrow + kPairs + 8 * g);
+    const uint4 q3 = *reinterpret_cast<const uint4*>(qrow + kPairs + 32 + 8 * g);
+    const uint32_t k0 = max(a.rs_kc[ec * 8 + g], a.rs_kpre[er * 8 + g]);
+    const uint32_t k1 = max(a.rs_kc[ec * 8 + 4 + g], a.rs_kpre[er * 8 + 4 + g]);
+    float ss = 0.f, mn2 = INFINITY;
+    bool bad = forced;
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt) {
+        const uint4 dc = *reinterpret_cast<const uint4*>(a.rs_dc + ec * kD + 16 * dt + 4 * g);
+        const uint2 dp = *reinterpret_cast<const uint2*>(a.rs_dpre + er * kD + 16 * dt + 4 * g);
+        const uint32_t d[4] = {max(dc.x, dp.x & 0xffffu), max(dc.y, dp.x >> 16), max(dc.z, dp.y & 0xffffu),
+                               max(dc.w, dp.y >> 16)};
+        const uint32_t xs[4] = {pk[dt].x << 16, pk[dt].x & 0xffff0000u, pk[dt].y << 16, pk[dt].y & 0xffff0000u};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const float x = __uint_as_float(xs[i]);
+            const float dv = __uint_as_float(d[i] << 16);
+            const float y = dv > 0.f ? x * __builtin_amdgcn_rcpf(dv) : 0.f;
+            ss = fmaf(y, y, ss);
+            if (dv > 0.f) mn2 = fminf(mn2, y * y);
+            bad |= !__builtin_isfinite(x);
+        }
+    }
+    float qq0 = 0.f, qq1 = 0.f;
+    {
+        const uint32_t w0[8] = {q0.x, q0.y, q0.z, q0.w, q2.x, q2.y, q2.z, q2.w};
+        const uint32_t w1[8] = {q1.x, q1.y, q1.z, q1.w, q3.x, q3.y, q3.z, q3.w};
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            qq0 = bf16x2_sq_acc(w0[i], qq0);
+            qq1 = bf16x2_sq_acc(w1[i], qq1);
+        }
+    }
+    float e = sqrtf(qq0) * sqrtf(__uint_as_float(k0)) + sqrtf(qq1) * sqrtf(__uint_as_float(k1));
+    // the row's four lanes: n, n + 16, n + 32, n + 48
+    ss += __shfl_xor(ss, 16);
+    ss += __shfl_xor(ss, 32);
+    e += __shfl_xor(e, 16);
+    e += __shfl_xor(e, 32);
+    mn2 = fminf(mn2, __shfl_xor(mn2, 16));
+    mn2 = fminf(mn2, __shfl_xor(mn2, 32));
+    bad = (__shfl_xor(static_cast<int>(bad), 16) | __shfl_xor(static_cast<int>(bad), 32) |
+           __shfl_xor(static_cast<int>(bad), 48) | static_cast<int>(bad)) != 0;
+    return bad || rs_flag_decide(static_cast<double>(mn2), static_cast<double>(ss), static_cast<double>(m),
+                                 static_cast<double>(e) * fabs(a.qk_scale_log2));
+}
+
 __global__ __launch_bounds__(kPfThreads) void prefill_attn_kernel(PrefillArgs a) {
     __shared__ __attribute__((aligned(1024))) uint8_t lds[kLdsB];
 
@@ -1058,24 +1128,27 @@ __global__ __launch_bounds__(kPfThreads) void prefill_attn_kernel(PrefillArgs a)
         for (int i = 0; i < 4; ++i) x[dt][i] = tl.o64[dt][i] / l;
     const bool q_bad_row = __shfl_xor(static_cast<int>(q_bad), 16) | __shfl_xor(static_cast<int>(q_bad), 32) |
                            __shfl_xor(static_cast<int>(q_bad), 48) | static_cast<int>(q_bad);
-    if (!q_ok) return;
-    // The flag decision (rs_flag_kernel) reads the row's running max; rows that read a
-    // marked block or whose Q row is out of range always go to the rescore (NaN).
-    if (g == 0 && a.rs_hdr)
-        a.rs_m[(static_cast<int64_t>(b) * T + tq) * kHq + hq] =
-            ((unsafe >> 31) != 0u || q_bad_row) ? __builtin_nanf("") : tl.m_run;
-    {
-        uint16_t* orow = a.out + ((static_cast<int64_t>(b) * T + tq) * kHq + hq) * kD;
+    const int64_t row = (static_cast<int64_t>(b) * T + tq_c) * kHq + hq;
+    uint2 pk[8];
 #pragma unroll
-        for (int dt = 0; dt < 8; ++dt) {
-            uint2 pk;
-            pk.x = f32_to_bf16_out(static_cast<float>(x[dt][0])) |
+    for (int dt = 0; dt < 8; ++dt) {
+        pk[dt].x = f32_to_bf16_out(static_cast<float>(x[dt][0])) |
                    (static_cast<uint32_t>(f32_to_bf16_out(static_cast<float>(x[dt][1]))) << 16);
-            pk.y = f32_to_bf16_out(static_cast<float>(x[dt][2])) |
+        pk[dt].y = f32_to_bf16_out(static_cast<float>(x[dt][2])) |
                    (static_cast<uint32_t>(f32_to_bf16_out(static_cast<float>(x[dt][3]))) << 16);
-            *reinterpret_cast<uint2*>(orow + 16 * dt + 4 * g) = pk;
-        }
     }
+    // The rescore flag, decided here from the rounded row: rows that read a marked block or
+    // whose Q row is out of range always go to the rescore.  Waves past the last query (q_ok
+    // false in every lane) decide nothing.
+    if (a.rs_hdr && __ballot(q_ok)) {
+        const bool forced = (unsafe >> 31) != 0u || q_bad_row;
+        if (pf_flag_row(a, b, kvh, st, st + tq_c, row, tl.m_run, forced, pk, lane) && q_ok && g == 0)
+            rs_append(a, static_cast<uint32_t>(row));
+    }
+    if (!q_ok) return;
+    uint16_t* orow = a.out + row * kD;
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt) *reinterpret_cast<uint2*>(orow + 16 * dt + 4 * g) = pk[dt];
 }
 
 hipError_t launch_prefill_attention(const PrefillArgs& a, hipStream_t stream) {
