@@ -228,25 +228,30 @@ struct StgStatLds {
     uint32_t k[kPfBlk][8];
 };
 
-__device__ __forceinline__ void stg_stats_put(int r, int qq, const float (&kf)[32], const float (&vf)[32],
+// n0, n1: the squared norms of pair groups 2qq and 2qq + 1 of the row's K; vw: its V as
+// BF16 codes (dims 16qq .. +7, 16qq + 8 .., 64 + 16qq .., 64 + 16qq + 8 ..).
+__device__ __forceinline__ void stg_stats_put(int r, int qq, float n0, float n1, const uint4 (&vw)[4],
                                               StgStatLds& sl) {
-    float n0 = 0.f, n1 = 0.f;
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-        n0 = fmaf(kf[j], kf[j], fmaf(kf[16 + j], kf[16 + j], n0));
-        n1 = fmaf(kf[8 + j], kf[8 + j], fmaf(kf[24 + j], kf[24 + j], n1));
-    }
-    uint32_t vc[16];
-#pragma unroll
-    for (int j = 0; j < 16; ++j)
-        vc[j] = ((__float_as_uint(vf[2 * j]) >> 16) & 0x7fffu) | (__float_as_uint(vf[2 * j + 1]) & 0x7fff0000u);
     uint4* vrow = reinterpret_cast<uint4*>(&sl.v[r][0]);
-    vrow[2 * qq] = make_uint4(vc[0], vc[1], vc[2], vc[3]);
-    vrow[2 * qq + 1] = make_uint4(vc[4], vc[5], vc[6], vc[7]);
-    vrow[8 + 2 * qq] = make_uint4(vc[8], vc[9], vc[10], vc[11]);
-    vrow[8 + 2 * qq + 1] = make_uint4(vc[12], vc[13], vc[14], vc[15]);
+    const uint32_t m = 0x7fff7fffu;
+    vrow[2 * qq] = make_uint4(vw[0].x & m, vw[0].y & m, vw[0].z & m, vw[0].w & m);
+    vrow[2 * qq + 1] = make_uint4(vw[1].x & m, vw[1].y & m, vw[1].z & m, vw[1].w & m);
+    vrow[8 + 2 * qq] = make_uint4(vw[2].x & m, vw[2].y & m, vw[2].z & m, vw[2].w & m);
+    vrow[8 + 2 * qq + 1] = make_uint4(vw[3].x & m, vw[3].y & m, vw[3].z & m, vw[3].w & m);
     sl.k[r][2 * qq] = __float_as_uint(n0);
     sl.k[r][2 * qq + 1] = __float_as_uint(n1);
+}
+
+// Largest |x| over 8 BF16 codes, as fp32 bits (NaN and infinity above every finite value).
+__device__ __forceinline__ uint32_t stg_absmax8(const uint4& w) {
+    const uint32_t m = pk_max_u16(pk_max_u16(w.x & 0x7fff7fffu, w.y & 0x7fff7fffu),
+                                  pk_max_u16(w.z & 0x7fff7fffu, w.w & 0x7fff7fffu));
+    return max(m << 16, m & 0x7fff0000u);
+}
+
+// Two BF16 codes (one dword) times f, as two fp16 codes.
+__device__ __forceinline__ uint32_t stg_f16x2(uint32_t w, float f) {
+    return pk_f16(__uint_as_float(w << 16) * f, __uint_as_float(w & 0xffff0000u) * f);
 }
 
 __device__ __forceinline__ void stg_stats_take(const PrefillArgs& a, int bh, int blk, int st, int wave, int lane,
@@ -331,58 +336,54 @@ __global__ __launch_bounds__(kStgThreads) void prefill_stage_kernel(PrefillArgs 
         const int n_keys = st + a.n_new;
         if (blk * kPfBlk >= n_keys) continue;
         const int p = blk * kPfBlk + r;
-        float kf[32], vf[32];     // [j] = dim 16qq + j, [16 + j] = dim 64 + 16qq + j
-        bool bad = false;
+        // This thread's 32 dims of the row (16-byte pieces c: dims 16qq + 8c for c < 2, 64 +
+        // 16qq + 8(c - 2) after): V and cached K kept as BF16 codes; a chunk row's K (fp32,
+        // from the append) is read here for its maxima and norms and again for conversion.
+        uint4 vw[4], kw[4];
 #pragma unroll
-        for (int j = 0; j < 32; ++j) kf[j] = vf[j] = 0.f;
+        for (int c = 0; c < 4; ++c) vw[c] = kw[c] = make_uint4(0u, 0u, 0u, 0u);
+        bool bad = false;
+        const bool chunk_row = p >= st && p < n_keys;
+        const float* kx = a.kx32 + ((static_cast<int64_t>(b) * a.n_new + (p - st)) * kHkv + h) * kD;
+        uint32_t rk = 0u, rv = 0u;
+        float n0 = 0.f, n1 = 0.f;
         if (p < n_keys) {
             const int64_t ce = cache_elem(a, b, h, p);
             if (ce < 0) {
                 bad = true;
             } else {
                 const char* vr = reinterpret_cast<const char*>(a.v + ce);
-                uint4 w[4];
 #pragma unroll
-                for (int c = 0; c < 4; ++c) w[c] = load_stream16(vr + 128 * (c >> 1) + 32 * qq + 16 * (c & 1));
-#pragma unroll
-                for (int c = 0; c < 4; ++c) {
-                    float f[8];
-                    unpack8(w[c], f);
-#pragma unroll
-                    for (int j = 0; j < 8; ++j) vf[8 * c + j] = f[j];
-                }
-                if (p < st) {
+                for (int c = 0; c < 4; ++c) vw[c] = load_stream16(vr + 128 * (c >> 1) + 32 * qq + 16 * (c & 1));
+                if (!chunk_row) {
                     const char* kr = reinterpret_cast<const char*>(a.k + ce);
 #pragma unroll
-                    for (int c = 0; c < 4; ++c) w[c] = load_stream16(kr + 128 * (c >> 1) + 32 * qq + 16 * (c & 1));
+                    for (int c = 0; c < 4; ++c) kw[c] = load_stream16(kr + 128 * (c >> 1) + 32 * qq + 16 * (c & 1));
+                    rk = max(max(stg_absmax8(kw[0]), stg_absmax8(kw[1])), max(stg_absmax8(kw[2]), stg_absmax8(kw[3])));
+                    const uint32_t g0[8] = {kw[0].x, kw[0].y, kw[0].z, kw[0].w, kw[2].x, kw[2].y, kw[2].z, kw[2].w};
+                    const uint32_t g1[8] = {kw[1].x, kw[1].y, kw[1].z, kw[1].w, kw[3].x, kw[3].y, kw[3].z, kw[3].w};
 #pragma unroll
-                    for (int c = 0; c < 4; ++c) {
-                        float f[8];
-                        unpack8(w[c], f);
-#pragma unroll
-                        for (int j = 0; j < 8; ++j) kf[8 * c + j] = f[j];
+                    for (int i = 0; i < 8; ++i) {
+                        n0 = bf16x2_sq_acc(g0[i], n0);
+                        n1 = bf16x2_sq_acc(g1[i], n1);
                     }
                 } else {
-                    const float* kx = a.kx32 + ((static_cast<int64_t>(b) * a.n_new + (p - st)) * kHkv + h) * kD;
 #pragma unroll
                     for (int c = 0; c < 8; ++c) {
+                        // dims 16qq + 4c (c < 4), 64 + 16qq + 4(c - 4): groups 2qq + ((c >> 1) & 1)
                         const float4 f = *reinterpret_cast<const float4*>(kx + 64 * (c >> 2) + 16 * qq + 4 * (c & 3));
-                        kf[4 * c] = f.x;
-                        kf[4 * c + 1] = f.y;
-                        kf[4 * c + 2] = f.z;
-                        kf[4 * c + 3] = f.w;
+                        rk = max(rk, max(max(__float_as_uint(f.x) & 0x7fffffffu, __float_as_uint(f.y) & 0x7fffffffu),
+                                         max(__float_as_uint(f.z) & 0x7fffffffu, __float_as_uint(f.w) & 0x7fffffffu)));
+                        const float sq = fmaf(f.x, f.x, fmaf(f.y, f.y, fmaf(f.z, f.z, f.w * f.w)));
+                        if ((c >> 1) & 1) n1 += sq;
+                        else n0 += sq;
                     }
                 }
+                rv = max(max(stg_absmax8(vw[0]), stg_absmax8(vw[1])), max(stg_absmax8(vw[2]), stg_absmax8(vw[3])));
             }
         }
-        // Largest magnitudes as fp32 bit patterns (NaN and infinity compare above every
-        // finite value): per row over its four threads, then over the block.
-        uint32_t rk = 0u, rv = 0u;
-#pragma unroll
-        for (int j = 0; j < 32; ++j) {
-            rk = max(rk, __float_as_uint(kf[j]) & 0x7fffffffu);
-            rv = max(rv, __float_as_uint(vf[j]) & 0x7fffffffu);
-        }
+        // Largest magnitudes as fp32 bit patterns: per row over its four threads, then over
+        // the block.
         rk = max(rk, static_cast<uint32_t>(__shfl_xor(static_cast<int>(rk), 1)));
         rk = max(rk, static_cast<uint32_t>(__shfl_xor(static_cast<int>(rk), 2)));
         rv = max(rv, static_cast<uint32_t>(__shfl_xor(static_cast<int>(rv), 1)));
@@ -398,7 +399,7 @@ __global__ __launch_bounds__(kStgThreads) void prefill_stage_kernel(PrefillArgs 
             red[0][wave] = wk;
             red[1][wave] = wv;
         }
-        if (a.rs_hdr) stg_stats_put(r, qq, kf, vf, stat_s);
+        if (a.rs_hdr) stg_stats_put(r, qq, n0, n1, vw, stat_s);
         __syncthreads();
         uint32_t bk = 0u, bv = 0u;
 #pragma unroll
@@ -415,33 +416,38 @@ __global__ __launch_bounds__(kStgThreads) void prefill_stage_kernel(PrefillArgs 
         if (bv >= (13u << 23) && rv != 0u && rv < bv - (12u << 23)) bad = true;
         const bool any_bad = __syncthreads_or(bad);
         const float fk = pow2f(sk), fv = pow2f(sv);
-        const bool chunk_row = p >= st && p < n_keys;
-        uint32_t kh[16], kl[16], vh[16];
-#pragma unroll
-        for (int j = 0; j < 16; ++j) {
-            const float x0 = kf[2 * j] * fk, x1 = kf[2 * j + 1] * fk;
-            kh[j] = pk_f16(x0, x1);
-            kl[j] = chunk_row ? pk_f16(x0 - f16_lo(kh[j]), x1 - f16_hi(kh[j])) : 0u;
-            vh[j] = pk_f16(vf[2 * j] * fv, vf[2 * j + 1] * fv);
-        }
         const int64_t row = static_cast<int64_t>(bh) * a.stg_pos + p;
         char* ko = reinterpret_cast<char*>(a.stg_k + row * kD);
         char* vo = reinterpret_cast<char*>(a.stg_v + row * kD);
+        const bool chunk_blk = blk * kPfBlk + kPfBlk - 1 >= st;
+        char* lo = reinterpret_cast<char*>(
+            a.stg_klo + ((static_cast<int64_t>(bh) * a.stg_cb + (blk - st / kPfBlk)) * kPfBlk + r) * kD);
 #pragma unroll
         for (int c = 0; c < 4; ++c) {
             const int off = 128 * (c >> 1) + 32 * qq + 16 * (c & 1);
-            *reinterpret_cast<uint4*>(ko + off) = make_uint4(kh[4 * c], kh[4 * c + 1], kh[4 * c + 2], kh[4 * c + 3]);
-            *reinterpret_cast<uint4*>(vo + off) = make_uint4(vh[4 * c], vh[4 * c + 1], vh[4 * c + 2], vh[4 * c + 3]);
-        }
-        if (blk * kPfBlk + kPfBlk - 1 >= st) {
-            const int cb = blk - st / kPfBlk;
-            char* lo = reinterpret_cast<char*>(
-                a.stg_klo + ((static_cast<int64_t>(bh) * a.stg_cb + cb) * kPfBlk + r) * kD);
+            *reinterpret_cast<uint4*>(vo + off) = make_uint4(stg_f16x2(vw[c].x, fv), stg_f16x2(vw[c].y, fv),
+                                                             stg_f16x2(vw[c].z, fv), stg_f16x2(vw[c].w, fv));
+            uint4 kh, kl = make_uint4(0u, 0u, 0u, 0u);
+            if (!chunk_row) {
+                kh = make_uint4(stg_f16x2(kw[c].x, fk), stg_f16x2(kw[c].y, fk), stg_f16x2(kw[c].z, fk),
+                                stg_f16x2(kw[c].w, fk));
+            } else {
+                // the fp32 row as two fp16 parts (leading, trailing)
+                const float* src = kx + 64 * (c >> 1) + 16 * qq + 8 * (c & 1);
+                const float4 f0 = *reinterpret_cast<const float4*>(src);
+                const float4 f1 = *reinterpret_cast<const float4*>(src + 4);
+                const float x[8] = {f0.x * fk, f0.y * fk, f0.z * fk, f0.w * fk, f1.x * fk, f1.y * fk, f1.z * fk, f1.w * fk};
+                uint32_t hh[4], ll[4];
 #pragma unroll
-            for (int c = 0; c < 4; ++c) {
-                const int off = 128 * (c >> 1) + 32 * qq + 16 * (c & 1);
-                *reinterpret_cast<uint4*>(lo + off) = make_uint4(kl[4 * c], kl[4 * c + 1], kl[4 * c + 2], kl[4 * c + 3]);
+                for (int j = 0; j < 4; ++j) {
+                    hh[j] = pk_f16(x[2 * j], x[2 * j + 1]);
+                    ll[j] = pk_f16(x[2 * j] - f16_lo(hh[j]), x[2 * j + 1] - f16_hi(hh[j]));
+                }
+                kh = make_uint4(hh[0], hh[1], hh[2], hh[3]);
+                kl = make_uint4(ll[0], ll[1], ll[2], ll[3]);
             }
+            *reinterpret_cast<uint4*>(ko + off) = kh;
+            if (chunk_blk) *reinterpret_cast<uint4*>(lo + off) = kl;
         }
         if (tid == 0)
             a.stg_scale[static_cast<int64_t>(bh) * nblk + blk] =
