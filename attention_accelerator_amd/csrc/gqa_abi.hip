@@ -154,7 +154,7 @@ DecodePlan plan_decode(const gqa_params_t* params, int32_t batch, int32_t capaci
 // and V statistics the flag decision reads (ncb chunk blocks of nr rows of prefix maxima).
 namespace {
 struct RsLayout {
-    size_t rows, done, cs, part_o, part_ml, m, kc, dc, kpre, dpre, kblk, dblk, total;
+    size_t flat, rows, gcnt, done, cs, part_o, part_ml, m, kc, dc, kpre, dpre, kblk, dblk, total;
 };
 
 RsLayout rs_layout(int32_t batch, int32_t n_new, int32_t ncb, int32_t nr, int32_t nblk) {
@@ -163,12 +163,14 @@ RsLayout rs_layout(int32_t batch, int32_t n_new, int32_t ncb, int32_t nr, int32_
     const size_t bh = static_cast<size_t>(batch) * kHkv;
     const size_t pre = bh * static_cast<size_t>(ncb) * static_cast<size_t>(nr);
     RsLayout l{};
-    l.rows = 256;
-    l.done = l.rows + align_up(rows * sizeof(uint32_t), 256);
+    l.flat = 256;
+    l.rows = l.flat + align_up(rows * sizeof(uint32_t), 256);
+    l.gcnt = l.rows + align_up(rows * sizeof(uint32_t), 256);
+    l.done = l.gcnt + align_up(bh * sizeof(uint32_t), 256);
     l.cs = l.done + align_up(rows * sizeof(uint32_t), 256);
     l.part_o = l.cs + align_up(toks * kPairs * sizeof(double2), 256);
-    l.part_ml = l.part_o + align_up(size_t{kRsSlots} * kD * sizeof(double), 256);
-    l.m = l.part_ml + align_up(size_t{kRsSlots} * sizeof(double2), 256);
+    l.part_ml = l.part_o + align_up(size_t{kRsSlots} * kGroup * kD * sizeof(double), 256);
+    l.m = l.part_ml + align_up(size_t{kRsSlots} * kGroup * sizeof(double2), 256);
     l.kc = l.m + align_up(rows * sizeof(float), 256);
     l.dc = l.kc + align_up(bh * static_cast<size_t>(ncb) * 8 * sizeof(uint32_t), 256);
     l.kpre = l.dc + align_up(bh * static_cast<size_t>(ncb) * kD * sizeof(uint32_t), 256);
@@ -188,7 +190,9 @@ void rescore_layout(PrefillArgs& a, const gqa_params_t* params, void* base, int3
     const RsLayout l = rs_layout(a.batch, a.n_new, ncb, nr, nblk);
     char* p = static_cast<char*>(base);
     a.rs_hdr = reinterpret_cast<uint32_t*>(p);
+    a.rs_flat = reinterpret_cast<uint32_t*>(p + l.flat);
     a.rs_rows = reinterpret_cast<uint32_t*>(p + l.rows);
+    a.rs_gcnt = reinterpret_cast<uint32_t*>(p + l.gcnt);
     a.rs_done = reinterpret_cast<uint32_t*>(p + l.done);
     a.rs_cs = reinterpret_cast<double2*>(p + l.cs);
     a.rs_part_o = reinterpret_cast<double*>(p + l.part_o);
@@ -204,7 +208,7 @@ void rescore_layout(PrefillArgs& a, const gqa_params_t* params, void* base, int3
     a.rs_dblk = reinterpret_cast<uint32_t*>(p + l.dblk);
     a.rs_nblk = nblk;
     // One-wave workgroups, one per SIMD (the kernel's registers allow one wave per SIMD):
-    // the flagged rows are cut into about as many (row, piece) pairs as run at once.
+    // the flagged rows' tiles are cut into about as many (tile, piece) pairs as run at once.
     const int32_t wgs = stream_wgs(params);
     a.rs_wgs = wgs < 1 ? 1 : wgs > static_cast<int32_t>(kRsSlots) ? static_cast<int32_t>(kRsSlots) : wgs;
 }

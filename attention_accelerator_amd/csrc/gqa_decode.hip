@@ -1249,30 +1249,45 @@ __global__ __launch_bounds__(kSingleWaves * kWave) void decode_single_kernel(Dec
 // ---------------------------------------------------------------------------------
 // fp64 rescore of the output rows a prefill or multi-token call flags.  Their MFMA kernels
 // carry scores in fp32 (Q in split parts against BF16 or staged fp16 K); an output element
-// that cancels to near zero can then miss 64 BF16 ULP of the golden's double value, so
-// rs_flag_kernel flags every row holding an element that may lie within the kernels' error
-// of zero (rs_flag_decide), and rescore_kernel recomputes the flagged rows in fp64 throughout (scores, exp2 and
-// weighted V): the one-token golden step at position start + t over keys 0 .. start + t,
-// the chunk's own keys rotated in double from the new K rows and not re-rounded, as the
-// golden rotates K (pyfiles/gen_gqa_wrapper_vectors.py:121-139).
+// that cancels to near zero can then miss 64 BF16 ULP of the golden's double value, so the
+// flag (rs_flag_decide, in the prefill attention epilogue or rs_flag_kernel) marks every row
+// holding an element that may lie within the kernels' error of zero, and rescore_kernel
+// recomputes the flagged rows in fp64 throughout (scores, exp2 and weighted V): the
+// one-token golden step at position start + t over keys 0 .. start + t, the chunk's own keys
+// rotated in double from the new K rows and not re-rounded, as the golden rotates K
+// (pyfiles/gen_gqa_wrapper_vectors.py:121-139).
 //
-// One row is one Q head, so the work is fp64 VALU, not MFMA (an fp64 MFMA would compute
-// four columns for one): lane l of a wave holds key slot l/8 of an 8-key chunk and the 16
+// The flagged rows of one (sequence, KV head) read the same K/V rows, so they are taken four
+// at a time ("tiles", in flagging order) as the four columns of the decode kernels' fp64 MFMA
+// chunk (v_mfma_f64_4x4x4_4b: 16 keys x 4 columns per chunk, each K/V row read once for the
+// four): column c is row c of the tile, with its own Q (rotated at its own position) and its
+// own last key start + t (later keys score -inf, p = 0 exactly).  The columns do not mix: a
+// row's arithmetic is the same whichever rows share its tile.
+//
+// A persistent grid of one-wave workgroups takes (tile, piece) pairs; piece p of a tile's
+// np pieces takes its 16-key chunks p, p + np, p + 2 np, ... (so every piece of a tile has
+// about the same work whatever its rows' lengths), two chunks ahead in flight.  np follows
+// from the tile count, the partial slots and the capacity only -- the flagged rows' count
+// per (sequence, KV head) and the call's sizes, never the order rows were flagged in -- so
+// the results are bit-for-bit repeatable.  A piece's partial (fp64 O, running max and sum
+// per column) is published with agent-scope stores and the tile's last piece merges them
+// (the pieces' (m, l) one piece per lane, their O eight pieces at a time), as in
+// decode_single_kernel.
+
+// Rows path (the flagged rows spread thin over their (sequence, KV head) pairs): one row per
+// wave, fp64 VALU (an fp64 MFMA would compute four columns for one and costs more than the
+// VALU chain for a single row) -- lane l holds key slot l/8 of an 8-key chunk and the 16
 // dims {8c + i, 64 + 8c + i : i < 8}, c = l % 8 -- 8 rotate_half pairs, so a chunk key's
 // rotation is lane-local.  A key's score is the sum over its eight lanes; each lane
 // accumulates p * V over its own keys for its 16 dims, and the 8 key slots are summed once
-// per piece.
-//
-// A persistent grid of one-wave workgroups takes (row, piece) pairs, piece p of a row taking
-// its chunks p, p + n_pieces, ..., so that the pieces share the costlier chunk keys evenly.
-// With at most 64 flagged rows (one per lane) every workgroup reads all of them and gives
-// each row pieces in proportion to its chunks (at least kRsMinChunks per piece, at most
-// kRsMaxPieces pieces): the longest row, which sets the kernel's time, gets the most.
-// With more rows each gets gridDim / rows pieces.  A piece's partial row is published with
-// agent-scope stores and the row's last piece merges them, as in decode_single_kernel.  A
-// row's result depends on its keys and its piece count only, which follows from the flagged
-// rows' key counts and the grid, never from the order they were flagged in: results are
-// bit-for-bit repeatable.
+// per piece.  A persistent grid of one-wave workgroups takes (row, piece) pairs, piece p of
+// a row taking its chunks p, p + n_pieces, ..., so that the pieces share the costlier chunk
+// keys evenly.  With at most 64 flagged rows (one per lane) every workgroup reads all of them
+// and gives each row pieces in proportion to its chunks (at least kRsMinChunks per piece, at
+// most kRsMaxPieces pieces): the longest row, which sets the kernel's time, gets the most.
+// With more rows each gets gridDim / rows pieces.  A row's result depends on its keys and
+// its piece count only, which follow from the flagged rows' key counts and the grid, never
+// from the order they were flagged in.
 
 constexpr int kRsKeys = 8;              // keys per rescore chunk (one per 8 lanes)
 constexpr int kRsMinChunks = 4;         // chunks per piece at least (proportional split)
@@ -1497,12 +1512,9 @@ __device__ __forceinline__ int rs_first(int p, int step, int lo) {
     return p >= lo ? p : p + (lo - p + step - 1) / step * step;
 }
 
-__global__ __launch_bounds__(kWave) void rescore_kernel(PrefillArgs a) {
+__device__ __forceinline__ void rs_rows_path(const PrefillArgs& a, uint32_t n_rows) {
     __shared__ double o_s[kRsKeys][8][16];      // per key slot, per lane group
     const int T = a.n_new;
-    const uint32_t cap = static_cast<uint32_t>(a.batch) * static_cast<uint32_t>(T) * kHq;
-    const uint32_t n_rows = min(a.rs_hdr[0], cap);
-    if (n_rows == 0) return;
     const int lane = threadIdx.x;
     const int c = lane & 7;
     // The plan.  Proportional (n_rows <= 64): lane r holds row r, its pieces np_l and its
@@ -1518,7 +1530,7 @@ __global__ __launch_bounds__(kWave) void rescore_kernel(PrefillArgs a) {
     if (prop) {
         int nc = 0;
         if (lane < static_cast<int>(n_rows)) {
-            row_l = a.rs_rows[lane];
+            row_l = a.rs_flat[lane];
             const int64_t bt = row_l / kHq;
             nc = (a.start[bt / T] + static_cast<int>(bt % T) + kRsKeys) / kRsKeys;   // ceil((start + t + 1) / 8)
         }
@@ -1551,7 +1563,7 @@ __global__ __launch_bounds__(kWave) void rescore_kernel(PrefillArgs a) {
             piece = static_cast<int>(wk % n_pieces);
             np = static_cast<int>(n_pieces);
             slot0 = static_cast<int64_t>(idx) * n_pieces;
-            row = a.rs_rows[idx];
+            row = a.rs_flat[idx];
         }
         const int h = static_cast<int>(row % kHq);
         const int64_t bt = row / kHq;
@@ -1678,6 +1690,324 @@ __global__ __launch_bounds__(kWave) void rescore_kernel(PrefillArgs a) {
         }
         __syncthreads();                // o_s is rewritten by the next work item
     }
+}
+
+
+// Tiles path (the flagged rows of a pair numerous enough to fill the four columns):
+constexpr int kRsMinPieceKeys = 128;
+
+// Where (tile, piece) pair wk lies: the tile's (sequence * 8 + KV head), its index j among
+// that pair's tiles and the pair's flagged-row count.  Tiles are numbered pair by pair.
+__device__ __forceinline__ void rs_locate(const PrefillArgs& a, int64_t ti, uint32_t per_bh, int& bh, int& j,
+                                          uint32_t& cnt) {
+    const int lane = threadIdx.x & (kWave - 1);
+    const int n_bh = a.batch * kHkv;
+    int64_t before = 0;
+    bh = 0;
+    j = 0;
+    cnt = 0u;
+    for (int base = 0; base < n_bh; base += kWave) {
+        const int x = base + lane;
+        const uint32_t c = x < n_bh ? min(a.rs_gcnt[x], per_bh) : 0u;
+        const int64_t t = (c + 3u) / 4u;
+        const int64_t incl = wave_incl_scan_i64(t, lane) + before;
+        const uint64_t m = __ballot(t > 0 && incl - t <= ti && ti < incl);
+        if (m) {
+            const int l = __ffsll(static_cast<unsigned long long>(m)) - 1;
+            bh = base + l;
+            j = static_cast<int>(ti - __shfl(incl - t, l));
+            cnt = __shfl(c, l);
+            return;
+        }
+        before = __shfl(incl, kWave - 1);
+    }
+}
+
+// This lane's Q operands for its column: Q row `row` (b, t, h), rotated at start + t with the
+// (cos, sin) table and scaled by scale*log2(e) in double -- q[kb][e] = Q[32kb + 8(l/16) + e].
+__device__ __forceinline__ void rs_q_operands(const PrefillArgs& a, uint32_t row, QOps& qa) {
+    const int g = (threadIdx.x & (kWave - 1)) >> 4;
+    const int64_t bt = row / kHq;
+    const uint16_t* qrow = a.q + static_cast<int64_t>(row) * kD;
+    const double2* cs = a.rs_cs + bt * kPairs;
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb) {
+        float xf[8], yf[8];
+        unpack8(*reinterpret_cast<const uint4*>(qrow + 32 * kb + 8 * g), xf);
+        unpack8(*reinterpret_cast<const uint4*>(qrow + kPairs + 32 * kb + 8 * g), yf);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            double x = xf[e], y = yf[e];
+            if (a.flags & 1u) {
+                const double2 c = cs[32 * kb + 8 * g + e];
+                const double xr = x * c.x - y * c.y;
+                y = x * c.y + y * c.x;
+                x = xr;
+            }
+            qa.q[kb][e] = x * a.qk_scale_log2;
+            qa.q[kb + 2][e] = y * a.qk_scale_log2;
+        }
+    }
+}
+
+// One 16-key chunk [kc, kc + 16) of a tile: scores of the 4 columns, each column's keys up
+// to col_lim (and below k_hi) counting, online softmax and weighted V, all in fp64 (the
+// arithmetic of compute_chunk).  With RoPE on K, a key >= st is its new row (loaded by the
+// caller) rotated in double with the (cos, sin) row of its token.
+__device__ __forceinline__ void rs_tile_chunk(const PrefillArgs& a, int b, int st, int kc, int k_hi, int col_lim,
+                                              const Chunk& c, const QOps& qa, PieceState& ps) {
+    __shared__ double p_lds[kWave];
+    const int lane = threadIdx.x & (kWave - 1);
+    double kd[4][8];
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb) {
+        float kf[8];
+        unpack8(c.kw[kb], kf);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) kd[kb][e] = static_cast<double>(kf[e]);
+    }
+    if ((a.flags & 2u) && kc + 15 >= st) {
+        const int key = min(kc + (lane & 15), k_hi - 1);
+        if (key >= st) {
+            const int g = lane >> 4;
+            const double2* cs = a.rs_cs + (static_cast<int64_t>(b) * a.n_new + (key - st)) * kPairs;
+#pragma unroll
+            for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    const double2 r = cs[32 * kb + 8 * g + e];
+                    const double x = kd[kb][e], y = kd[kb + 2][e];
+                    kd[kb][e] = x * r.x - y * r.y;
+                    kd[kb + 2][e] = x * r.y + y * r.x;
+                }
+        }
+    }
+    double s4[4] = {0.0, 0.0, 0.0, 0.0};
+#pragma unroll
+    for (int e = 0; e < 8; ++e)
+#pragma unroll
+        for (int kb = 0; kb < 4; ++kb) s4[kb] = mfma_f64(kd[kb][e], qa.q[kb][e], s4[kb]);
+    const int key = kc + chunk_key_of_lane(lane);
+    double s = (s4[0] + s4[1]) + (s4[2] + s4[3]);
+    if (key >= k_hi || key > col_lim) s = -INFINITY;
+    if (__ballot(s > ps.m_run + kMaxHeadroom)) {
+        double cm = s;
+        cm = fmax(cm, dpp_d<0x124>(cm));
+        cm = fmax(cm, dpp_d<0x128>(cm));
+        cm = swap_max_f64<true>(swap_max_f64<false>(cm));
+        const bool grow = cm > ps.m_run + kMaxHeadroom;
+        const double m_new = grow ? ceil(cm) : ps.m_run;
+        const int shift = (ps.m_run == -INFINITY) ? 0 : max_shift_f64(ps.m_run, m_new);
+        ps.l_run = ldexp(ps.l_run, shift);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) ps.acc[i] = ldexp(ps.acc[i], shift);
+        ps.m_run = m_new;
+    }
+    const double p = s == -INFINITY ? 0.0 : exp2_f64(fmax(s - ps.m_run, -2000.0));
+    ps.l_run += p;
+    p_lds[(lane >> 4) * 16 + (lane & 3) * 4 + ((lane >> 2) & 3)] = p;
+    const double2 pa = *reinterpret_cast<const double2*>(p_lds + (lane >> 4) * 16 + (lane & 3) * 4);
+    const double2 pb = *reinterpret_cast<const double2*>(p_lds + (lane >> 4) * 16 + (lane & 3) * 4 + 2);
+    const double pq[4] = {pa.x, pa.y, pb.x, pb.y};
+    double vd[4][8];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        float vf[8];
+        unpack8(c.vw[q], vf);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) vd[q][e] = static_cast<double>(vf[e]);
+    }
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) ps.acc[e] = mfma_f64(vd[q][e], pq[q], ps.acc[e]);
+}
+
+// One BF16 output row segment: this lane's 8 dims of its column's row, O / l rounded
+// double -> f32 -> BF16.
+__device__ __forceinline__ void rs_write8(const PrefillArgs& a, uint32_t row, int d0, const double (&o)[8], double l) {
+    uint16_t o8[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) o8[e] = f32_to_bf16_out(static_cast<float>(o[e] / l));
+    *reinterpret_cast<bf16x8_t*>(a.out + static_cast<int64_t>(row) * kD + d0) = pack8(o8);
+}
+
+__device__ __forceinline__ void rs_tiles_path(const PrefillArgs& a, int64_t n_tiles) {
+    const int T = a.n_new;
+    const int lane = threadIdx.x;
+    const uint32_t per_bh = 4u * static_cast<uint32_t>(T);
+    int np = n_tiles >= kRsSlots ? 1 : static_cast<int>(kRsSlots / n_tiles);
+    np = min(np, kRsMaxPieces);
+    np = max(1, min(np, a.capacity / kRsMinPieceKeys));
+    const int64_t n_work = n_tiles * np;
+    const int col = lane & 3;
+    const int64_t rb = a.kv_pos_stride * 2;      // cache row bytes
+    for (int64_t wk = blockIdx.x; wk < n_work; wk += gridDim.x) {
+        const int64_t ti = wk / np;
+        const int piece = static_cast<int>(wk % np);
+        int bh, j;
+        uint32_t cnt;
+        rs_locate(a, ti, per_bh, bh, j, cnt);
+        const int b = bh / kHkv;
+        const int kvh = bh % kHkv;
+        const int st = a.start[b];
+        const int nr = min(4, static_cast<int>(cnt) - 4 * j);
+        const uint32_t* rows = a.rs_rows + static_cast<int64_t>(bh) * per_bh + 4 * j;
+        // This lane's column: row `row` (a repeat of the tile's first row past nr, which
+        // counts no key and is not written).
+        const uint32_t row = rows[col < nr ? col : 0];
+        const int col_lim = col < nr ? st + static_cast<int>((row / kHq) % T) : -1;
+        int lim_max = col_lim;
+        lim_max = max(lim_max, __shfl_xor(lim_max, 1));
+        lim_max = max(lim_max, __shfl_xor(lim_max, 2));
+        const int k_hi = lim_max + 1;                     // keys [0, k_hi) of the tile
+        const int k_lo = piece * kChunk;                  // first chunk of this piece
+        const int k_step = np * kChunk;
+
+        QOps qa;
+        rs_q_operands(a, row, qa);
+        PieceState ps;
+        init_piece(ps);
+        if (k_lo < k_hi) {
+            const char* kseg = reinterpret_cast<const char*>(a.k + static_cast<int64_t>(b) * a.kv_batch_stride +
+                                                             static_cast<int64_t>(kvh) * a.kv_head_stride);
+            const char* vseg = reinterpret_cast<const char*>(a.v + static_cast<int64_t>(b) * a.kv_batch_stride +
+                                                             static_cast<int64_t>(kvh) * a.kv_head_stride);
+            const bool rope_k = (a.flags & 2u) != 0;
+            // Rows of chunk [kc, kc + 16): clamped to the piece's last key (masked there).
+            auto load = [&](int kc, Chunk& c) {
+                const int kk = min(kc + (lane & 15), k_hi - 1);
+                const char* kp = rope_k && kk >= st
+                                     ? reinterpret_cast<const char*>(
+                                           a.k_new + ((static_cast<int64_t>(b) * T + (kk - st)) * kHkv + kvh) * kD)
+                                     : kseg + kk * rb;
+                kp += 16 * (lane >> 4);
+#pragma unroll
+                for (int kb = 0; kb < 4; ++kb) c.kw[kb] = load_stream16(kp + 64 * kb);
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const int kv = min(kc + 4 * q + (lane >> 4), k_hi - 1);
+                    c.vw[q] = load_stream16(vseg + kv * rb + 16 * (lane & 15));
+                }
+            };
+            Chunk c0, c1, c2;
+            load(k_lo, c0);
+            load(min(k_lo + k_step, k_hi - 1), c1);
+            for (int kc = k_lo; kc < k_hi; kc += k_step) {
+                load(min(kc + 2 * k_step, k_hi - 1), c2);
+                rs_tile_chunk(a, b, st, kc, k_hi, col_lim, c0, qa, ps);
+                c0 = c1;
+                c1 = c2;
+            }
+        }
+        double l_tot;
+        finish_piece(ps, l_tot);
+        if (np == 1) {
+            if (col < nr) rs_write8(a, row, out_dim_of_lane(lane), ps.acc, l_tot);
+            continue;
+        }
+        // Partial at slot wk: O[column][dim] and (m, l) per column.
+        {
+            unsigned long long* po = reinterpret_cast<unsigned long long*>(a.rs_part_o + wk * kGroup * kD) +
+                                     col * kD + out_dim_of_lane(lane);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) store_agent(po + e, ps.acc[e]);
+            if (lane < kGroup) {
+                unsigned long long* pml = reinterpret_cast<unsigned long long*>(a.rs_part_ml + wk * kGroup + lane);
+                store_agent(pml, ps.m_run);
+                store_agent(pml + 1, l_tot);
+            }
+        }
+        wait_vmem();                              // the stores have completed ...
+        __atomic_signal_fence(__ATOMIC_SEQ_CST);  // ... and stay before the count
+        int last = 0;
+        if (lane == 0) last = atomicAdd(&a.rs_done[ti], 1u) == static_cast<uint32_t>(np) - 1u;
+        last = __shfl(last, 0);
+        __atomic_signal_fence(__ATOMIC_SEQ_CST);  // the merge's loads stay after it
+        if (!last) continue;
+        // Merge: lane u reads piece u's (m, l) of all four columns; lane l then takes column
+        // c = l / 16, dims 8 (l % 16) .. +7, the pieces in order, eight at a time (their loads
+        // issued before any is used).  A piece with no key has m = -inf, weight 0.
+        const int mc = lane >> 4;
+        const int d0 = 8 * (lane & 15);
+        const int64_t slot0 = ti * np;
+        int ex[kGroup];
+        double lw = 0.0;
+        {
+            double2 ml[kGroup];
+#pragma unroll
+            for (int c = 0; c < kGroup; ++c)
+                ml[c] = load_agent_d2(
+                    reinterpret_cast<const double*>(a.rs_part_ml + (slot0 + min(lane, np - 1)) * kGroup + c));
+#pragma unroll
+            for (int c = 0; c < kGroup; ++c) {
+                double m_all = lane < np ? ml[c].x : -INFINITY;
+#pragma unroll
+                for (int sh = 1; sh < kWave; sh <<= 1) m_all = fmax(m_all, __shfl_xor(m_all, sh));
+                ex[c] = ml[c].x == -INFINITY ? -1100 : max_shift_f64(ml[c].x, m_all);
+                double lc = lane < np ? ldexp(ml[c].y, ex[c]) : 0.0;
+#pragma unroll
+                for (int sh = 1; sh < kWave; sh <<= 1) lc += __shfl_xor(lc, sh);
+                if (c == mc) lw = lc;
+            }
+        }
+        double o[8] = {0.0, 0.0, 0.0, 0.0, 0.0, 0.0, 0.0, 0.0};
+        constexpr int kMb = 8;
+        for (int u0 = 0; u0 < np; u0 += kMb) {
+            double2 v[kMb][4];
+#pragma unroll
+            for (int u = 0; u < kMb; ++u) {
+                const double* src = a.rs_part_o + ((slot0 + min(u0 + u, np - 1)) * kGroup + mc) * kD + d0;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) v[u][e] = load_agent_d2(src + 2 * e);
+            }
+#pragma unroll
+            for (int u = 0; u < kMb; ++u) {
+                int e_u = __shfl(ex[0], u0 + u);
+#pragma unroll
+                for (int c = 1; c < kGroup; ++c) {
+                    const int x = __shfl(ex[c], u0 + u);
+                    e_u = c == mc ? x : e_u;
+                }
+                if (u0 + u < np) {
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        o[2 * e] += ldexp(v[u][e].x, e_u);
+                        o[2 * e + 1] += ldexp(v[u][e].y, e_u);
+                    }
+                }
+            }
+        }
+        const uint32_t mrow = rows[mc < nr ? mc : 0];
+        if (mc < nr) rs_write8(a, mrow, d0, o, lw);
+    }
+}
+
+// The two paths share the partial slots and piece counters (a call runs one).  The tiles
+// path when the flagged rows average at least kRsTileFill per (sequence, KV head) pair that
+// has any: a tile of four rows costs about what one row costs on the rows path, a tile of
+// one row about twice as much.
+constexpr int kRsTileFill = 3;
+
+__global__ __launch_bounds__(kWave) void rescore_kernel(PrefillArgs a) {
+    const uint32_t cap = static_cast<uint32_t>(a.batch) * static_cast<uint32_t>(a.n_new) * kHq;
+    const uint32_t n_rows = min(a.rs_hdr[0], cap);
+    if (n_rows == 0) return;
+    const uint32_t n_pairs = a.rs_hdr[1];
+    if (static_cast<uint64_t>(n_rows) < static_cast<uint64_t>(kRsTileFill) * n_pairs) {
+        rs_rows_path(a, n_rows);
+        return;
+    }
+    const int lane = threadIdx.x;
+    const int n_bh = a.batch * kHkv;
+    const uint32_t per_bh = 4u * static_cast<uint32_t>(a.n_new);
+    int64_t n_tiles = 0;
+    for (int base = 0; base < n_bh; base += kWave) {
+        const int x = base + lane;
+        const uint32_t c = x < n_bh ? min(a.rs_gcnt[x], per_bh) : 0u;
+        n_tiles += wave_sum_i64((c + 3u) / 4u);
+    }
+    rs_tiles_path(a, n_tiles);
 }
 
 // The flag decision: one wave per (sequence, new token, KV head), its four output rows side

@@ -133,13 +133,17 @@ struct PrefillArgs {
     int32_t n_wgs;            // persistent workgroups of the multi-token stream kernel
     int32_t skew_pm;          // XCD weighting of the ranges (per mille of a range)
     // fp64 rescore of the output rows the MFMA kernels may have computed outside 64 BF16 ULP
-    // (rs_flag_kernel decides, rescore_kernel recomputes); rs_hdr nullptr: off.
-    uint32_t* rs_hdr;         // [1]: flagged rows
-    uint32_t* rs_rows;        // [B*T*32] flagged rows, (b*T + t)*32 + q_head, in flagging order
-    uint32_t* rs_done;        // [B*T*32] finished pieces per flagged row (indexed by row)
+    // (the attention epilogue or rs_flag_kernel decides, rescore_kernel recomputes); rs_hdr
+    // nullptr: off.
+    uint32_t* rs_hdr;         // [2]: flagged rows, (sequence, KV head) pairs with one
+    uint32_t* rs_flat;        // [B*T*32] flagged rows (b*T + t)*32 + q_head, in flagging order
+    uint32_t* rs_rows;        // [B*8][4T] the same rows by (sequence, KV head)
+    uint32_t* rs_gcnt;        // [B*8] flagged rows per (sequence, KV head)
+    uint32_t* rs_done;        // [B*T*32] finished pieces per flagged row or tile of rows
     double2* rs_cs;           // [B][T][64] cos, sin of (start + t) * inv_freq[i] (RoPE on Q or K)
-    double* rs_part_o;        // [kRsSlots][128] unnormalised partial output rows
-    double2* rs_part_ml;      // [kRsSlots] (running max, sum)
+    double* rs_part_o;        // [kRsSlots][4][128] unnormalised partial outputs (a tile's rows, or
+                              // one row per slot ([kRsSlots][128]) on the rows path)
+    double2* rs_part_ml;      // [kRsSlots][4] (running max, sum)
     int32_t rs_wgs;           // workgroups of the rescore kernel
     // What the flag decision reads besides the output rows and Q:
     float* rs_m;              // [B*T*32] the row's running max (log2 units); NaN: always rescore
@@ -207,8 +211,8 @@ __host__ __device__ inline bool rs_flag_decide(double mn2, double ss, double m, 
     f2 = fe > f2 ? fe : f2;
     return mn2 * kD < kRsFlagRatio2 * f2 * ss;
 }
-constexpr int kRsSlots = 1024;                            // partial slots (rows x pieces)
-constexpr int kRsMaxPieces = 64;                          // pieces per row at most (one per lane)
+constexpr int kRsSlots = 1024;                            // partial slots (tiles x pieces)
+constexpr int kRsMaxPieces = 64;                          // pieces per tile at most
 // Rescore region of a workspace; ncb, nr: the chunk-prefix blocks and rows (prefill:
 // ceil(T / 64) + 1 and 64; multi-token: 1 and T); nblk: 64-position blocks of the cache
 // (prefill; 0 for multi-token).
@@ -228,12 +232,17 @@ __host__ __device__ constexpr int32_t prefill_cache_blocks(int32_t capacity) { r
 // Appends a flagged output row (device side).
 __device__ __forceinline__ void rs_append(const PrefillArgs& a, uint32_t row) {
     const uint32_t i = atomicAdd(a.rs_hdr, 1u);
-    if (i < static_cast<uint32_t>(a.batch) * static_cast<uint32_t>(a.n_new) * kHq) a.rs_rows[i] = row;
+    if (i < static_cast<uint32_t>(a.batch) * static_cast<uint32_t>(a.n_new) * kHq) a.rs_flat[i] = row;
+    const uint32_t per = 4u * static_cast<uint32_t>(a.n_new);            // rows of one (b, kv head)
+    const uint32_t bh = row / (static_cast<uint32_t>(a.n_new) * kHq) * kHkv + (row % kHq) / kGroup;
+    const uint32_t j = atomicAdd(a.rs_gcnt + bh, 1u);
+    if (j < per) a.rs_rows[bh * per + j] = row;
+    if (j == 0u) atomicAdd(a.rs_hdr + 1, 1u);                          // pairs with a flagged row
 }
 
 // Clears the flagged-row count (the first kernel of a prefill or multi-token call).
 __device__ __forceinline__ void rs_clear(const PrefillArgs& a, int t) {
-    if (a.rs_hdr && t == 0) a.rs_hdr[0] = 0u;
+    if (a.rs_hdr && t < 2) a.rs_hdr[t] = 0u;
 }
 
 // The same kernel clears row (b*T + t)*32 + h's piece counter and, with RoPE on K, stores

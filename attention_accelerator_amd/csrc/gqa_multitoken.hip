@@ -250,6 +250,13 @@ __global__ __launch_bounds__(256) void mt_prepare_kernel(PrefillArgs a) {
         load4<kVec>(krow + d0, kxh);
         load4<kVec>(krow + d0 + kPairs, kyh);
     }
+    // The rescore's counters start at zero (also for a sequence whose start is out of range:
+    // the tile counters are indexed by tile, not by row).
+    if (a.rs_hdr) {
+        for (int i = threadIdx.x; i < T * kGroup; i += blockDim.x)
+            a.rs_done[(static_cast<int64_t>(b) * T + i / kGroup) * kHq + kvh * kGroup + i % kGroup] = 0u;
+        if (threadIdx.x == 0) a.rs_gcnt[b * kHkv + kvh] = 0u;
+    }
     if (!prefill_start_ok(a, st)) {
         for (int i = threadIdx.x; i < T * kGroup * (kD / 4); i += blockDim.x) {
             const int tt = i / (kGroup * (kD / 4));
@@ -276,9 +283,6 @@ __global__ __launch_bounds__(256) void mt_prepare_kernel(PrefillArgs a) {
             if (kvh == 0 && a.rs_hdr)
                 a.rs_cs[(static_cast<int64_t>(b) * T + u) * kPairs + lane] = make_double2(cs_s[u][lane], sn_s[u][lane]);
         }
-    if (a.rs_hdr)
-        for (int i = threadIdx.x; i < T * kGroup; i += blockDim.x)
-            a.rs_done[(static_cast<int64_t>(b) * T + i / kGroup) * kHq + kvh * kGroup + i % kGroup] = 0u;
     __syncthreads();
 
     double qvx[kW][4], qvy[kW][4];

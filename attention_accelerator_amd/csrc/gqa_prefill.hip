@@ -117,6 +117,12 @@ __global__ __launch_bounds__(256) void kv_append_kernel(PrefillArgs a) {
     if (bt >= static_cast<int64_t>(a.batch) * a.n_new) return;
     const int t = static_cast<int>(bt % a.n_new);
     const int b = static_cast<int>(bt / a.n_new);
+    // The rescore's counters start at zero (also for a sequence whose start is out of range:
+    // the tile counters are indexed by tile, not by row).
+    if (a.rs_hdr) {
+        if (lane < kHq) a.rs_done[bt * kHq + lane] = 0u;
+        if (t == 0 && lane < kHkv) a.rs_gcnt[b * kHkv + lane] = 0u;
+    }
     const int st = a.start[b];
     if (!prefill_start_ok(a, st)) return;
     const int64_t pos = static_cast<int64_t>(st) + t;
@@ -135,10 +141,7 @@ __global__ __launch_bounds__(256) void kv_append_kernel(PrefillArgs a) {
     double sn = 0.0, cs = 1.0;
     const bool any_rope = (a.flags & 3u) != 0;        // the rescore rotates Q with these too
     if (any_rope) rope_sincos(pos, a.rope.inv_freq[lane], sn, cs);
-    if (a.rs_hdr) {
-        if (lane < kHq) a.rs_done[bt * kHq + lane] = 0u;
-        if (any_rope) a.rs_cs[bt * kPairs + lane] = make_double2(cs, sn);
-    }
+    if (a.rs_hdr && any_rope) a.rs_cs[bt * kPairs + lane] = make_double2(cs, sn);
 #pragma unroll
     for (int kvh = 0; kvh < kHkv; ++kvh) {
         const int64_t row = bt * kHkv + kvh;

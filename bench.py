@@ -280,7 +280,7 @@ def bench_prefill(args, torch, gqa, dev) -> int:
     bsz, n_new, start = PREFILL_WORKLOADS[args.workload]
     cap = start + n_new
     g = torch.Generator("cuda").manual_seed(args.seed)
-    q = torch.randn((bsz, n_new, 32, 128), generator=g, device=dev).to(torch.bfloat16)
+    q = (torch.randn((bsz, n_new, 32, 128), generator=g, device=dev) * args.q_scale).to(torch.bfloat16)
     kn = torch.randn((bsz, n_new, 8, 128), generator=g, device=dev).to(torch.bfloat16)
     vn = torch.randn((bsz, n_new, 8, 128), generator=g, device=dev).to(torch.bfloat16)
     k = torch.full((bsz, 8, cap, 128), float("nan"), dtype=torch.bfloat16, device=dev)
@@ -354,7 +354,7 @@ def bench_prefill(args, torch, gqa, dev) -> int:
                    "rope": "q and new k", "precision": "BF16 K/V staged exactly as fp16 (power-of-two "
                    "scale per 64-position block); Q, the chunk's K and P in two fp16 parts; fp32 MFMA "
                    "accumulation per 64-key block, fp64 across blocks; fp64 rescore of flagged rows",
-                   "flops_per_step": flops, "spinup_s": args.spinup_s,
+                   "flops_per_step": flops, "spinup_s": args.spinup_s, "q_scale": args.q_scale,
                    "rescored_rows": rescored, "output_rows": bsz * n_new * 32},
         "roofline": roofline,
         "cpu_baseline": None if args.no_cpu_baseline else prefill_cpu_baseline(
@@ -415,7 +415,7 @@ def bench_multitoken(args, torch, gqa, dev, stimulus) -> int:
                                   gen_device="cuda")
     lens = [int(x) for x in batch.seq_len]
     g = torch.Generator("cuda").manual_seed(args.seed + 1)
-    q = torch.randn((bsz, n_new, 32, 128), generator=g, device=dev).to(torch.bfloat16)
+    q = (torch.randn((bsz, n_new, 32, 128), generator=g, device=dev) * args.q_scale).to(torch.bfloat16)
     kn = torch.randn((bsz, n_new, 8, 128), generator=g, device=dev).to(torch.bfloat16)
     vn = torch.randn((bsz, n_new, 8, 128), generator=g, device=dev).to(torch.bfloat16)
     starts_l = [x - n_new for x in lens]
@@ -482,7 +482,7 @@ def bench_multitoken(args, torch, gqa, dev, stimulus) -> int:
         "data": f"synthetic N(0,1) BF16, seed {args.seed}",
         "config": {"workload": args.workload, "batch": bsz, "new_tokens": n_new, "keys": sum(lens),
                    "q_heads": 32, "kv_heads": 8, "head_dim": 128, "rope": "q and new k",
-                   "bytes_per_step": step_bytes, "spinup_s": args.spinup_s,
+                   "bytes_per_step": step_bytes, "spinup_s": args.spinup_s, "q_scale": args.q_scale,
                    "rescored_rows": rescored, "output_rows": bsz * n_new * 32},
         "roofline": roofline,
         "cpu_baseline": None if args.no_cpu_baseline else multitoken_cpu_baseline(
@@ -507,6 +507,9 @@ def main() -> int:
                     help="skip the per-kernel HIP events inside the timed region")
     ap.add_argument("--graph", action="store_true",
                     help="decode workloads: time replays of one captured step (HIP graph)")
+    ap.add_argument("--q-scale", type=float, default=1.0,
+                    help="prefill and multi-token workloads: Q drawn as N(0, q_scale^2) (a peaked "
+                         "softmax for q_scale > 1; the headline workloads use 1)")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="also run plain 1 GiB device copies (PMC byte-counter calibration)")
     args = ap.parse_args()

@@ -268,29 +268,35 @@ def test_multi_long_context_sampled_rows(dev):
 
 
 @pytest.mark.parametrize("n_wgs", ["1", "7", "64", "1024"])
-def test_rescore_proportional_pieces(dev, n_wgs):
-    """At most 64 flagged rows: each row's keys are cut into pieces in proportion to its
-    length (a row of 3001 keys gets about 30 times the pieces of one of 91), for rescore
-    grids of 1 (fewer workgroups than rows), 7, 64 and 1024 workgroups (params.stream_wgs
-    sets the grid).  Q is scaled by 2^100 and K by 2^40, so every dot product passes the fp32 range and all
-    64 rows (2 sequences x 1 token x 32 heads) of the MFMA kernels come out not finite and
-    are rescored; every row must match the oracle, and V dimension 5, zero in every key,
-    exactly."""
+@pytest.mark.parametrize("heads", ["all", "one per kv head"])
+def test_rescore_pieces(dev, n_wgs, heads):
+    """Rows forced to the fp64 rescore.  Every head: Q scaled by 2^100 and K by 2^40, so
+    every dot product passes the fp32 range and all 64 rows (2 sequences x 1 token x 32
+    heads, 4 per (sequence, KV head)) of the MFMA kernels come out not finite -- the tiles
+    path, four rows as the columns of one fp64 MFMA chunk.  One head per KV head: those Q
+    rows scaled by 2^100 (scores ~2^100, far past the flag's bound), 16 rows, one per pair --
+    the rows path, each row's keys cut into pieces in proportion to its length (a row of 3001
+    keys gets about 30 times the pieces of one of 91).  Rescore grids of 1 (fewer workgroups
+    than rows), 7, 64 and 1024 workgroups (params.stream_wgs sets the grid).  Every row must
+    match the oracle, and V dimension 5, zero in every key, exactly."""
     p = gqa.make_params(rope_k=True, stream_wgs=int(n_wgs))
     starts = [90, 3000]
     q, kn, vn, k, v = _chunk(starts, 1, 3001, 77)
     vn[..., 5] = 0.0
     for b, s in enumerate(starts):
         v[b, :, :s, 5] = 0.0
-    q = (q.float() * 2.0 ** 100).to(torch.bfloat16)
-    kn = (kn.float() * 2.0 ** 40).to(torch.bfloat16)
-    k = (k.float() * 2.0 ** 40).to(torch.bfloat16)
+    hs = list(range(32)) if heads == "all" else list(range(0, 32, 4))
+    q[:, :, hs] = (q[:, :, hs].float() * 2.0 ** 100).to(torch.bfloat16)
+    if heads == "all":
+        kn = (kn.float() * 2.0 ** 40).to(torch.bfloat16)
+        k = (k.float() * 2.0 ** 40).to(torch.bfloat16)
     want = _oracle(q, kn, vn, k, v, starts)
     ws = torch.empty(gqa.prefill_workspace_bytes(2, 1, 3001, params=p), dtype=torch.uint8, device=dev)
     got, _, _ = _run(q, kn, vn, k, v, starts, dev, workspace=ws, params=p)
-    assert gqa.prefill_rescored_rows(ws, 2, 1, 3001, params=p) == 64
+    n_rs = gqa.prefill_rescored_rows(ws, 2, 1, 3001, params=p)
+    assert n_rs == 64 if heads == "all" else 16 <= n_rs < 32
     assert np.all(got[..., 5] == 0)
-    _check(want, got.reshape(-1, 128), f"64 flagged rows, {n_wgs} rescore workgroups")
+    _check(want, got.reshape(-1, 128), f"{n_rs} flagged rows ({heads}), {n_wgs} rescore workgroups")
 
 
 @pytest.mark.parametrize("n_new,rope_q,rope_k", [
