@@ -130,6 +130,8 @@ struct PrefillArgs {
     float* part_o;            // [n_slots][16W][128] unnormalised partial outputs (column 16w + 4t + h)
     float2* part_ml;          // [n_slots][16W] (integer-valued running max in log2 units, sum)
     float* chunk_s;           // [B][8][16W][4W] scores of the chunk's keys u per column (log2 units)
+    uint32_t* piece_st;       // [n_slots][W][8 + 128] each piece's (and wave's) cached-key maxima for
+                              // the rescore flag (K pair-group norms, |V| codes), reduced by the merge
     int32_t n_wgs;            // persistent workgroups of the multi-token stream kernel
     int32_t skew_pm;          // XCD weighting of the ranges (per mille of a range)
     // fp64 rescore of the output rows the MFMA kernels may have computed outside 64 BF16 ULP
@@ -151,8 +153,8 @@ struct PrefillArgs {
     // which every new token sees): the largest squared norm of each pair group (dims 8g ..
     // 8g+7 and 64+8g .. 64+8g+7, g < 8: the RoPE pairs, so a norm does not change under
     // rotation), fp32 bits, and the largest |V| of each dim, BF16 bits.  Maxima of
-    // non-negative values: the multi-token stream kernel raises entry 0 by atomicMax on bit
-    // patterns, prefill_stat_reduce_kernel writes every entry (order-independent results).
+    // non-negative values compared as bit patterns: the multi-token merge kernel writes entry 0
+    // from its pieces' records, prefill_stat_reduce_kernel every entry (order-independent).
     uint32_t* rs_kc;          // [B*8][rs_ncb][8]
     uint32_t* rs_dc;          // [B*8][rs_ncb][128]
     // The same maxima over the chunk's keys, running over the key positions: entry (cb, r)

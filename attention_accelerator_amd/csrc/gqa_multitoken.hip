@@ -93,7 +93,7 @@ __device__ __forceinline__ int mt_keys(const PrefillArgs& a, int b) {
 
 namespace {
 struct MtLayout {
-    size_t q_op, plan, seq_off, part_o, part_ml, chunk_s, total;
+    size_t q_op, plan, seq_off, part_o, part_ml, chunk_s, piece_st, total;
 };
 
 MtLayout mt_layout(int32_t batch, int32_t n_new, int32_t n_wgs) {
@@ -108,7 +108,8 @@ MtLayout mt_layout(int32_t batch, int32_t n_new, int32_t n_wgs) {
     l.part_o = l.seq_off + al((static_cast<size_t>(batch) + 1) * sizeof(int64_t));
     l.part_ml = l.part_o + al(n_slots * cols * kD * sizeof(float));
     l.chunk_s = l.part_ml + al(n_slots * cols * sizeof(float2));
-    l.total = l.chunk_s + al(static_cast<size_t>(batch) * kHkv * cols * 4 * w * sizeof(float));
+    l.piece_st = l.chunk_s + al(static_cast<size_t>(batch) * kHkv * cols * 4 * w * sizeof(float));
+    l.total = l.piece_st + al(n_slots * w * (8 + kD) * sizeof(uint32_t));
     return l;
 }
 }  // namespace
@@ -126,6 +127,7 @@ void prefill_multi_layout(PrefillArgs& a, void* base, int32_t n_wgs) {
     a.part_o = reinterpret_cast<float*>(p + l.part_o);
     a.part_ml = reinterpret_cast<float2*>(p + l.part_ml);
     a.chunk_s = reinterpret_cast<float*>(p + l.chunk_s);
+    a.piece_st = reinterpret_cast<uint32_t*>(p + l.piece_st);
     a.n_wgs = n_wgs;
 }
 
@@ -403,10 +405,6 @@ __global__ __launch_bounds__(256) void mt_prepare_kernel(PrefillArgs a) {
                 a.rs_dpre[(bh * T + u) * kD + c - 8] = static_cast<uint16_t>(run);
             }
         }
-        if (c < 8)
-            a.rs_kc[bh * 8 + c] = 0u;
-        else
-            a.rs_dc[bh * kD + c - 8] = 0u;
     }
     float* cs_out = a.chunk_s + (static_cast<int64_t>(b) * kHkv + kvh) * kCols * kU;
     for (int i = threadIdx.x; i < kCols * kU; i += blockDim.x) {
@@ -758,10 +756,15 @@ __device__ __forceinline__ void mt_piece_end(const PrefillArgs& a, int b, int kv
     if (g == 0) a.part_ml[col] = make_float2(t.m_run, static_cast<float>(l));
 }
 
-// End of a piece's statistics: each value reduced over the lanes that hold it, then raised
-// into the segment's cached-key maxima (atomicMax: the result does not depend on the order).
+// End of a piece's statistics: each value reduced over the lanes that hold it, then stored
+// into the piece's slot (wg + segment, as its partial), one record per wave; the merge kernel
+// reduces a segment's records into its maxima (rs_kc / rs_dc).  Plain stores, one writer per
+// record (atomic maxima from every piece onto a segment's 136 words instead: B=64 ragged
+// T = 8 and 16 stream kernels 2-3 us slower).
 template <int kW>
-__device__ __forceinline__ void mt_stats_end(const PrefillArgs& a, int64_t seg, int lane, MtStats<kW>& ms) {
+__device__ __forceinline__ void mt_stats_end(const PrefillArgs& a, int64_t slot, int wv, int lane, MtStats<kW>& ms) {
+    uint32_t* kdst = a.piece_st + (slot * kW + wv) * (8 + kD);
+    uint32_t* ddst = kdst + 8;
     if constexpr (kW == 1) {
         const int n = lane & 15;
         const int g = lane >> 4;
@@ -770,7 +773,7 @@ __device__ __forceinline__ void mt_stats_end(const PrefillArgs& a, int64_t seg, 
             uint32_t x = ms.kmax[i];
 #pragma unroll
             for (int sh = 1; sh < 16; sh <<= 1) x = max(x, static_cast<uint32_t>(__shfl_xor(static_cast<int>(x), sh)));
-            if (n == 0 && x) atomicMax(a.rs_kc + seg * 8 + 4 * i + g, x);
+            if (n == 0) kdst[4 * i + g] = x;
         }
 #pragma unroll
         for (int dt = 0; dt < 8; ++dt) {
@@ -778,21 +781,23 @@ __device__ __forceinline__ void mt_stats_end(const PrefillArgs& a, int64_t seg, 
             x = pk_max_u16(x, static_cast<uint32_t>(__shfl_xor(static_cast<int>(x), 16)));
             x = pk_max_u16(x, static_cast<uint32_t>(__shfl_xor(static_cast<int>(x), 32)));
             x = max(x & 0xffffu, x >> 16);
-            if (g == 0 && x) atomicMax(a.rs_dc + seg * kD + 16 * dt + n, x);
+            if (g == 0) ddst[16 * dt + n] = x;
         }
     } else {
         uint32_t x = ms.kmax[0];
 #pragma unroll
         for (int sh = 8; sh < kWave; sh <<= 1) x = max(x, static_cast<uint32_t>(__shfl_xor(static_cast<int>(x), sh)));
-        if (lane < 8 && x) atomicMax(a.rs_kc + seg * 8 + lane, x);
-        uint32_t* dc = a.rs_dc + seg * kD + 8 * (lane & 15);
+        if (lane < 8) kdst[lane] = x;
+        uint32_t* dc = ddst + 8 * (lane & 15);
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             uint32_t v = ms.vmax[i];
             v = pk_max_u16(v, static_cast<uint32_t>(__shfl_xor(static_cast<int>(v), 16)));
             v = pk_max_u16(v, static_cast<uint32_t>(__shfl_xor(static_cast<int>(v), 32)));
-            if (lane < 16 && (v & 0xffffu)) atomicMax(dc + 2 * i, v & 0xffffu);
-            if (lane < 16 && (v >> 16)) atomicMax(dc + 2 * i + 1, v >> 16);
+            if (lane < 16) {
+                dc[2 * i] = v & 0xffffu;
+                dc[2 * i + 1] = v >> 16;
+            }
         }
     }
     mt_stats_reset<kW>(ms);
@@ -1032,7 +1037,7 @@ __global__ __launch_bounds__(kWave * kW) __attribute__((amdgpu_waves_per_eu(kW =
         }
         mt_flush(t);
         mt_piece_end<kW>(a, c.b, c.kvh, c.pk == 0 && c.k_b == c.nk, wg + seg, wv, lane, t);
-        mt_stats_end<kW>(a, seg, lane, ms);
+        mt_stats_end<kW>(a, wg + seg, wv, lane, ms);
         mt_advance(a, c, x_end, lead);
         if (!c.valid) break;
     }
@@ -1057,8 +1062,21 @@ __global__ __launch_bounds__(256 * kW) void mt_merge_kernel(PrefillArgs a) {
     const int64_t seg_off = off + static_cast<int64_t>(kvh) * span + lead;
     const int64_t w_first = range_of(per_wg, extra, seg_off);
     const int n_pieces = static_cast<int>(range_of(per_wg, extra, seg_off + nk - 1) - w_first) + 1;
-    if (n_pieces == 1) return;
     const int64_t slot0 = w_first + static_cast<int64_t>(b) * kHkv + kvh;
+    // The segment's cached-key maxima for the rescore flag: every piece's records (one per
+    // wave), whole segments too.
+    if (a.rs_hdr && threadIdx.x < 8 + kD) {
+        const int64_t seg = static_cast<int64_t>(b) * kHkv + kvh;
+        uint32_t x = 0u;
+        for (int p = 0; p < n_pieces; ++p)
+#pragma unroll
+            for (int w = 0; w < kW; ++w) x = max(x, a.piece_st[((slot0 + p) * kW + w) * (8 + kD) + threadIdx.x]);
+        if (threadIdx.x < 8)
+            a.rs_kc[seg * 8 + threadIdx.x] = x;
+        else
+            a.rs_dc[seg * kD + threadIdx.x - 8] = x;
+    }
+    if (n_pieces == 1) return;
     const int col = threadIdx.x >> 4;
     const int d0 = 8 * (threadIdx.x & 15);
     const int tok = col >> 2;
