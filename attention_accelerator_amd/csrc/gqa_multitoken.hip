@@ -481,9 +481,9 @@ __device__ __forceinline__ void mt_flush(MtState& t) {
 //    so slices kb and kb + 2 together hold pair group 4 (kb & 1) + g whole: kmax[kb & 1].
 //    V: the V^T operand of dim tile dt gives lane (g, n) 8 keys of dim 16 dt + n: vmax[dt].
 //  * Two or four tiles (their registers are all in use): each wave reads its 32/W keys of
-//    the window from LDS after the window's V^T P^T.  K: lane l takes key (l >> 3) (+ 8 j)
-//    and the two 16-byte chunks of pair group l & 7: kmax[0].  V: lane l takes dims
-//    8 (l & 15) .. +7 of key (l >> 4) (+ 4 j): vmax[0..3].
+//    the window from LDS, K beside the window's scores, V after its V^T P^T.  K: lane l
+//    takes key (l >> 3) (+ 8 j) and the two 16-byte chunks of pair group l & 7: kmax[0].
+//    V: lane l takes dims 8 (l & 15) .. +7 of key (l >> 4) (+ 4 j): vmax[0..3].
 template <int kW>
 struct MtStats {
     static constexpr int kNk = kW == 1 ? 2 : 1;
@@ -501,11 +501,12 @@ __device__ __forceinline__ void mt_stats_reset(MtStats<kW>& ms) {
 }
 
 // The stages of one 32-key window [key0, key0 + 32) of a piece ending at k_b, for this
-// wave's tile.  mt_qk: the raw scores S^T = K Q^T of both 16-key tiles from the K plane; for
-// one tile also the squared key norms of the window's first klim keys (the cached keys of
-// the piece; none when klim <= 0).
+// wave's tile.  mt_qk: the raw scores S^T = K Q^T of both 16-key tiles from the K plane, and
+// the squared pair-group norms of the window's first klim keys (the cached keys of the piece;
+// none when klim <= 0): one tile from its operands, two or four from this wave's share of
+// the plane.
 template <int kW>
-__device__ __forceinline__ void mt_qk(const uint8_t* kplane, const bf16x8_t (&qop)[3][4], int lane,
+__device__ __forceinline__ void mt_qk(const uint8_t* kplane, const bf16x8_t (&qop)[3][4], int wv, int lane,
                                       f32x4_t (&sacc)[2], int klim, MtStats<kW>& ms) {
     const int n = lane & 15;
     const int g = lane >> 4;
@@ -539,6 +540,8 @@ __device__ __forceinline__ void mt_qk(const uint8_t* kplane, const bf16x8_t (&qo
                 const uint32_t x = 16 * kt + n < klim ? __float_as_uint(nrm[kt][pr]) : 0u;
                 ms.kmax[pr] = max(ms.kmax[pr], x);
             }
+    } else {
+        mt_stats_k<kW>(kplane, wv, lane, klim, ms);
     }
 }
 
@@ -553,19 +556,20 @@ __device__ __forceinline__ void mt_vmask(int vlim, int lane, uint32_t (&vm)[4]) 
     }
 }
 
-// Two or four tiles: this wave's share of the window's statistics from the K and V planes in
-// LDS (keys (32 / W) wv + ..), the first lim keys of the window counting.
+// Two or four tiles: this wave's share of a window's statistics from its planes in LDS
+// (keys (32 / W) wv + ..), the first lim keys of the window counting.  K is taken from the
+// plane the window's scores are formed from (one window ahead: the ring refills a K slot with
+// a later V before the next barrier, so a K plane is not read once its window is current);
+// V from the current window's plane.
 template <int kW>
-__device__ __forceinline__ void mt_stats_window(const uint8_t* kplane, const uint8_t* vplane, int wv, int lane,
-                                                int lim, MtStats<kW>& ms) {
+__device__ __forceinline__ void mt_stats_k(const uint8_t* kplane, int wv, int lane, int lim, MtStats<kW>& ms) {
     constexpr int kKeys = kMtWin / kW;
     const int c = lane & 7;
 #pragma unroll
     for (int j = 0; j < kKeys / 8; ++j) {
         const int row = kKeys * wv + 8 * j + (lane >> 3);
-        const uint8_t* rp = kplane + row * kRowB;
-        const uint4 lo = *reinterpret_cast<const uint4*>(rp + 16 * (c ^ pf_swz(row)));
-        const uint4 hi = *reinterpret_cast<const uint4*>(rp + 16 * ((c + 8) ^ pf_swz(row)));
+        const uint4 lo = __builtin_bit_cast(uint4, pf_k_chunk(kplane, row, c));
+        const uint4 hi = __builtin_bit_cast(uint4, pf_k_chunk(kplane, row, c + 8));
         float sq = bf16x2_sq_acc(lo.x, 0.f);
         sq = bf16x2_sq_acc(lo.y, sq);
         sq = bf16x2_sq_acc(lo.z, sq);
@@ -576,13 +580,18 @@ __device__ __forceinline__ void mt_stats_window(const uint8_t* kplane, const uin
         sq = bf16x2_sq_acc(hi.w, sq);
         ms.kmax[0] = max(ms.kmax[0], row < lim ? __float_as_uint(sq) : 0u);
     }
-    // V: lane l takes dims 8 (l & 15) .. +7 of key (l >> 4) (+ 4 j): one 16-byte read per
-    // lane and four keys per instruction; the lanes of a dim are combined once per piece.
+}
+
+// V: lane l takes dims 8 (l & 15) .. +7 of key (l >> 4) (+ 4 j): one 16-byte read per lane
+// and four keys per instruction; the lanes of a dim are combined once per piece.
+template <int kW>
+__device__ __forceinline__ void mt_stats_v(const uint8_t* vplane, int wv, int lane, int lim, MtStats<kW>& ms) {
+    constexpr int kKeys = kMtWin / kW;
     const int vc = lane & 15;
 #pragma unroll
     for (int j = 0; j < kKeys / 4; ++j) {
         const int row = kKeys * wv + 4 * j + (lane >> 4);
-        const uint4 x = *reinterpret_cast<const uint4*>(vplane + row * kRowB + 16 * (vc ^ pf_swz(row)));
+        const uint4 x = __builtin_bit_cast(uint4, pf_k_chunk(vplane, row, vc));
         const uint32_t m = row < lim ? 0x7fff7fffu : 0u;
         ms.vmax[0] = pk_max_u16(ms.vmax[0], x.x & m);
         ms.vmax[1] = pk_max_u16(ms.vmax[1], x.y & m);
@@ -658,26 +667,19 @@ __device__ __forceinline__ void mt_probs(const f32x4_t (&sacc)[2], float m_eff, 
     t.l64 += static_cast<double>(lsum);
 }
 
-// mt_pv: once this window's V has landed and every wave may read it, O^T += V^T P^T: dim
-// tile dt from two transposed reads (rows 4g + a/4 and 16 rows on), summed in fp32 into
-// the group's acc, which every kMtGroup windows moves into the fp64 O.  `sync`: wait for
-// this wave's V copies (kVPlanes planes of its copies younger than them when `steady`) and
-// meet the other waves first.  Not needed when the window's top already waited
-// for the next window's K, which every wave requested after this window's V: the copies
-// complete in issue order, so that wait and the barrier after it covered V as well
-// (B=64 ragged, T=16: stream kernel 283 -> 272 us).
-template <int kC, int kVPlanes, int kW>
-__device__ __forceinline__ void mt_pv(uint32_t vbase, const uint32_t (&ph)[3][2][4], bool steady, int lane,
-                                      MtState& t, bool sync, const uint32_t (&vm)[4], MtStats<kW>& ms) {
-    if (sync) {
-        mt_wait_planes<kC, kVPlanes>(steady);
-        mt_barrier();
-    }
+// mt_pv: O^T += V^T P^T of this window (its V in LDS, visible to every wave): dim tile dt
+// from two transposed reads (rows 4g + a/4 and 16 rows on), summed in fp32 into the group's
+// acc, which every kMtGroup windows moves into the fp64 O (the caller's mt_flush).
+template <int kW>
+__device__ __forceinline__ void mt_pv(uint32_t vbase, const uint32_t (&ph)[3][2][4], int lane, MtState& t,
+                                      const uint32_t (&vm)[4], MtStats<kW>& ms) {
     bf16x8_t pb[3];
 #pragma unroll
     for (int s = 0; s < 3; ++s) pb[s] = as_bf16x8(make_uint4(ph[s][0][0], ph[s][0][1], ph[s][0][2], ph[s][0][3]));
 #pragma unroll
     for (int d0 = 0; d0 < 8; d0 += 2) {
+        // Inline reads: the compiler does not see them as LDS accesses, so it adds no wait for
+        // the window copies in flight (the reads' own wait is explicit).
         short4_t r[2][2];
 #pragma unroll
         for (int e = 0; e < 2; ++e) {
@@ -709,7 +711,7 @@ __device__ __forceinline__ void mt_pv(uint32_t vbase, const uint32_t (&ph)[3][2]
             for (int e = 0; e < 2; ++e)
                 t.acc[d0 + e] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av[e], pb[s], t.acc[d0 + e], 0, 0, 0);
     }
-    if (++t.grp == kMtGroup) mt_flush(t);
+    ++t.grp;
 }
 
 // End of a piece: the column sums over the four rows; a whole segment writes its output
@@ -996,7 +998,7 @@ __global__ __launch_bounds__(kWave * kW) __attribute__((amdgpu_waves_per_eu(kW =
         mt_barrier();
         // Keys of the piece below the chunk: the ones its statistics cover.
         const int stat_end = min(c.k_b, st);
-        mt_qk<kW>(slot_ptr(slot), qop, lane, s_cur, stat_end - c.kw, ms);
+        mt_qk<kW>(slot_ptr(slot), qop, wv, lane, s_cur, stat_end - c.kw, ms);
         for (;;) {
             // Request V of the producer's window (kA after this one) and, once every wave
             // is done with the previous window, K of the window after it.
@@ -1014,20 +1016,29 @@ __global__ __launch_bounds__(kWave * kW) __attribute__((amdgpu_waves_per_eu(kW =
                 }
             }
             const bool v_steady = kq == kA && ik;     // 2 kA + 1 planes requested after V
-            const uint32_t vbase = lds_base + (slot + 1 >= kS ? slot + 1 - kS : slot + 1) * kMtPlaneB;
             const bool chunk_keys = c.kw + kMtWin > st;
+            // A piece's last window waited for no next K: wait for its V and meet here.
+            // Otherwise the wait above covered it: every wave requested this window's V
+            // before the next window's K, and the copies complete in issue order (B=64
+            // ragged, T=16: stream kernel 283 -> 272 us).
+            if (!has_next) {
+                mt_wait_planes<kC, 2 * kA + 1>(v_steady);
+                mt_barrier();
+            }
+            if (t.grp == kMtGroup) mt_flush(t);
             uint32_t ph[3][2][4];
             const float m_eff = mt_max(a, chunk_keys, cs, st, c.kw, c.k_b, lim, lane, s_cur, t);
-            // The next window's scores (on a piece's last window the plane read is the next
-            // piece's or stale, and the result is dropped).
+            // One branch-free block: the next window's scores (on a piece's last window the
+            // plane read is the next piece's or stale, and the result is dropped), this
+            // window's probabilities, V^T P^T and statistics.
             f32x4_t s_next[2];
-            mt_qk<kW>(slot_ptr(slot + 2), qop, lane, s_next, stat_end - (c.kw + kMtWin), ms);
+            mt_qk<kW>(slot_ptr(slot + 2), qop, wv, lane, s_next, stat_end - (c.kw + kMtWin), ms);
             mt_probs(s_cur, m_eff, ph, t);
             uint32_t vm[4] = {0u, 0u, 0u, 0u};
             if constexpr (kW == 1) mt_vmask(stat_end - c.kw, lane, vm);
-            mt_pv<kC, 2 * kA + 1, kW>(vbase, ph, v_steady, lane, t, !has_next, vm, ms);
+            mt_pv<kW>(lds_base + (slot + 1 >= kS ? slot + 1 - kS : slot + 1) * kMtPlaneB, ph, lane, t, vm, ms);
             if constexpr (kW > 1)
-                mt_stats_window<kW>(slot_ptr(slot), slot_ptr(slot + 1), wv, lane, stat_end - c.kw, ms);
+                mt_stats_v<kW>(slot_ptr(slot + 1), wv, lane, stat_end - c.kw, ms);
             s_cur[0] = s_next[0];
             s_cur[1] = s_next[1];
             slot = slot + 2 >= kS ? slot + 2 - kS : slot + 2;
