@@ -635,7 +635,6 @@ int gqa_prefill_bf16(const gqa_params_t* params, const uint16_t* q, const uint16
     if (multi) {
         // The preparation kernel of the multi-token path appends the chunk's rows itself.
         hipError_t e = launch_prefill_multi(a, s, ev);
-        if (e == hipSuccess) e = launch_rs_flag(a, s);
         if (e == hipSuccess) e = launch_rescore(a, s);
         return e == hipSuccess ? GQA_OK : GQA_ERR_HIP;
     }

@@ -1250,7 +1250,7 @@ __global__ __launch_bounds__(kSingleWaves * kWave) void decode_single_kernel(Dec
 // fp64 rescore of the output rows a prefill or multi-token call flags.  Their MFMA kernels
 // carry scores in fp32 (Q in split parts against BF16 or staged fp16 K); an output element
 // that cancels to near zero can then miss 64 BF16 ULP of the golden's double value, so the
-// flag (rs_flag_decide, in the prefill attention epilogue or rs_flag_kernel) marks every row
+// flag (rs_flag_decide, in the prefill attention epilogue or the multi-token merge) marks every row
 // holding an element that may lie within the kernels' error of zero, and rescore_kernel
 // recomputes the flagged rows in fp64 throughout (scores, exp2 and weighted V): the
 // one-token golden step at position start + t over keys 0 .. start + t, the chunk's own keys
@@ -2008,98 +2008,6 @@ __global__ __launch_bounds__(kWave) void rescore_kernel(PrefillArgs a) {
         n_tiles += wave_sum_i64((c + 3u) / 4u);
     }
     rs_tiles_path(a, n_tiles);
-}
-
-// The flag decision: one wave per (sequence, new token, KV head), its four output rows side
-// by side -- lane (h, j) = (lane / 16, lane % 16) holds dims 8j .. 8j+7 of Q head 4 kvh + h,
-// which lie in pair group j % 8 -- so each row's sums and minimum are 16-lane reductions.
-// The keys the token sees are the keys before its chunk block (rs_kc, rs_dc at that block)
-// and the block's rows up to its own (rs_kpre / rs_dpre), so no key a token cannot see
-// moves its decision.  Q's pair-group norms are taken from the row as
-// given: rotation does not change them.
-__device__ __forceinline__ void rs_max8_u16(uint32_t (&d)[8], const uint4& a) {
-    const uint32_t w[4] = {a.x, a.y, a.z, a.w};
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        d[2 * i] = max(d[2 * i], w[i] & 0xffffu);
-        d[2 * i + 1] = max(d[2 * i + 1], w[i] >> 16);
-    }
-}
-
-__global__ __launch_bounds__(256) void rs_flag_kernel(PrefillArgs a) {
-    const int64_t item = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);   // (b*T + t)*8 + kvh
-    const int lane = threadIdx.x & (kWave - 1);
-    const int h = lane >> 4;
-    const int j = lane & 15;
-    const int T = a.n_new;
-    if (item >= static_cast<int64_t>(a.batch) * T * kHkv) return;
-    const int kvh = static_cast<int>(item % kHkv);
-    const int64_t bt = item / kHkv;
-    const int t = static_cast<int>(bt % T);
-    const int b = static_cast<int>(bt / T);
-    const int64_t row = bt * kHq + kvh * kGroup + h;
-    const int grp = j & 7;
-    const int64_t bh = static_cast<int64_t>(b) * kHkv + kvh;
-    const uint4 ox = *reinterpret_cast<const uint4*>(a.out + row * kD + 8 * j);
-    const uint4 qx = *reinterpret_cast<const uint4*>(a.q + row * kD + 8 * j);
-    const float mrow = a.rs_m[row];
-    const int st = a.start[b];
-    if (st < 0 || st > a.capacity - T) return;      // NaN rows, nothing to rescore
-    int cb = 0, r = t;
-    if (a.rs_nr == 64) {
-        const int p = st + t;
-        cb = p / 64 - st / 64;
-        r = p % 64;
-    }
-    // The keys before the row's chunk block, then the block's rows up to the row's own.
-    const int64_t er = (bh * a.rs_ncb + cb) * a.rs_nr + r;
-    const int64_t ec = bh * a.rs_ncb + cb;
-    const uint4* dc = reinterpret_cast<const uint4*>(a.rs_dc + ec * kD + 8 * j);
-    const uint4 d0 = dc[0], d1 = dc[1];
-    const uint4 dp = *reinterpret_cast<const uint4*>(a.rs_dpre + er * kD + 8 * j);
-    const uint32_t kq = max(a.rs_kc[ec * 8 + grp], a.rs_kpre[er * 8 + grp]);
-    uint32_t d[8] = {d0.x, d0.y, d0.z, d0.w, d1.x, d1.y, d1.z, d1.w};
-    rs_max8_u16(d, dp);
-    // Elements in units of their dim's V scale (a dim whose V is zero in every key the row
-    // sees is exactly zero and left out); Q's squared norm over these 8 dims.  fp32: y is at
-    // most 1 in magnitude (an output element is a weighted mean of its dim's V), and a
-    // decision about a threshold needs no more.
-    const uint32_t xw[4] = {ox.x, ox.y, ox.z, ox.w};
-    const uint32_t qw[4] = {qx.x, qx.y, qx.z, qx.w};
-    float ss = 0.f, mn2 = INFINITY, qq = 0.f;
-    bool bad = false;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-        const uint32_t xs = i & 1 ? xw[i >> 1] & 0xffff0000u : xw[i >> 1] << 16;
-        const uint32_t qs = i & 1 ? qw[i >> 1] & 0xffff0000u : qw[i >> 1] << 16;
-        const float x = __uint_as_float(xs), q = __uint_as_float(qs);
-        const float dv = __uint_as_float(d[i] << 16);
-        const float y = dv > 0.f ? x * __builtin_amdgcn_rcpf(dv) : 0.f;
-        ss = fmaf(y, y, ss);
-        if (dv > 0.f) mn2 = fminf(mn2, y * y);
-        bad |= !__builtin_isfinite(x);
-        qq = fmaf(q, q, qq);
-    }
-    // |q_G| |k_G|max: lanes j and j + 8 hold the two halves of pair group j % 8.
-    qq += dpp_f<0x128>(qq);                         // row_ror:8
-    float e = j < 8 ? sqrtf(qq) * sqrtf(__uint_as_float(kq)) : 0.f;
-    ss = row16_sum(ss);
-    e = row16_sum(e);
-    mn2 = -row16_max(-mn2);
-    const uint64_t bads = __ballot(bad);
-    const bool row_bad = ((bads >> (16 * h)) & 0xffffull) != 0ull;
-    if (j == 0 && a.rs_hdr &&
-        (row_bad || rs_flag_decide(static_cast<double>(mn2), static_cast<double>(ss), static_cast<double>(mrow),
-                                   static_cast<double>(e) * fabs(a.qk_scale_log2))))
-        rs_append(a, static_cast<uint32_t>(row));
-}
-
-hipError_t launch_rs_flag(const PrefillArgs& a, hipStream_t stream) {
-    if (!a.rs_hdr) return hipSuccess;
-    const int64_t n = static_cast<int64_t>(a.batch) * a.n_new * kHkv;
-    if (n == 0) return hipSuccess;
-    hipLaunchKernelGGL(rs_flag_kernel, dim3(static_cast<unsigned>((n + 3) / 4)), dim3(256), 0, stream, a);
-    return hipGetLastError();
 }
 
 hipError_t launch_rescore(const PrefillArgs& a, hipStream_t stream) {

@@ -135,7 +135,7 @@ struct PrefillArgs {
     int32_t n_wgs;            // persistent workgroups of the multi-token stream kernel
     int32_t skew_pm;          // XCD weighting of the ranges (per mille of a range)
     // fp64 rescore of the output rows the MFMA kernels may have computed outside 64 BF16 ULP
-    // (the attention epilogue or rs_flag_kernel decides, rescore_kernel recomputes); rs_hdr
+    // (the attention epilogue or the multi-token merge decides, rescore_kernel recomputes); rs_hdr
     // nullptr: off.
     uint32_t* rs_hdr;         // [2]: flagged rows, (sequence, KV head) pairs with one
     uint32_t* rs_flat;        // [B*T*32] flagged rows (b*T + t)*32 + q_head, in flagging order
@@ -153,8 +153,8 @@ struct PrefillArgs {
     // which every new token sees): the largest squared norm of each pair group (dims 8g ..
     // 8g+7 and 64+8g .. 64+8g+7, g < 8: the RoPE pairs, so a norm does not change under
     // rotation), fp32 bits, and the largest |V| of each dim, BF16 bits.  Maxima of
-    // non-negative values compared as bit patterns: the multi-token merge kernel writes entry 0
-    // from its pieces' records, prefill_stat_reduce_kernel every entry (order-independent).
+    // non-negative values compared as bit patterns: prefill_stat_reduce_kernel writes every
+    // entry (order-independent); the multi-token merge kernel keeps its segment's in LDS.
     uint32_t* rs_kc;          // [B*8][rs_ncb][8]
     uint32_t* rs_dc;          // [B*8][rs_ncb][128]
     // The same maxima over the chunk's keys, running over the key positions: entry (cb, r)
@@ -222,8 +222,7 @@ size_t rescore_bytes(int32_t batch, int32_t n_new, int32_t ncb, int32_t nr, int3
 void rescore_layout(PrefillArgs& a, const gqa_params_t* params, void* base, int32_t ncb, int32_t nr, int32_t nblk);
 // Prefill: the cached-key maxima from the staging kernel's block maxima.
 hipError_t launch_prefill_stat_reduce(const PrefillArgs& a, hipStream_t stream);
-// The flag decision over every output row (after the MFMA kernels), then the rescore.
-hipError_t launch_rs_flag(const PrefillArgs& a, hipStream_t stream);
+// The fp64 rescore of the flagged rows (after the kernels that decide the flags).
 hipError_t launch_rescore(const PrefillArgs& a, hipStream_t stream);
 
 // Chunk blocks of the prefill path's prefix statistics (64-position blocks holding chunk keys).

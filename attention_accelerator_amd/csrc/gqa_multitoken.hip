@@ -473,9 +473,10 @@ __device__ __forceinline__ void mt_flush(MtState& t) {
     t.grp = 0;
 }
 
-// The cached keys' statistics of a piece for the rescore flag (rs_kc / rs_dc), kept per lane
-// until the piece ends and formed without branches (a branch between an MFMA and the read of
-// its result can lose the wait states the read needs).
+// The cached keys' statistics of a piece for the rescore flag (the largest squared norm of
+// each K pair group and the largest |V| of each dim over the piece's keys below the chunk),
+// kept per lane until the piece ends and formed without branches (a branch between an MFMA
+// and the read of its result can lose the wait states the read needs).
 //  * One tile (W = 1, one wave per SIMD, registers to spare): from the operands the wave
 //    already holds.  K: lane (g, n) reads key 16 kt + n, dims 32 kb + 8g .. +7 in slice kb,
 //    so slices kb and kb + 2 together hold pair group 4 (kb & 1) + g whole: kmax[kb & 1].
@@ -760,7 +761,7 @@ __device__ __forceinline__ void mt_piece_end(const PrefillArgs& a, int b, int kv
 
 // End of a piece's statistics: each value reduced over the lanes that hold it, then stored
 // into the piece's slot (wg + segment, as its partial), one record per wave; the merge kernel
-// reduces a segment's records into its maxima (rs_kc / rs_dc).  Plain stores, one writer per
+// reduces a segment's records into its maxima.  Plain stores, one writer per
 // record (atomic maxima from every piece onto a segment's 136 words instead: B=64 ragged
 // T = 8 and 16 stream kernels 2-3 us slower).
 template <int kW>
@@ -1054,10 +1055,72 @@ __global__ __launch_bounds__(kWave * kW) __attribute__((amdgpu_waves_per_eu(kW =
     }
 }
 
-// Merge the pieces of split segments: one workgroup per (KV head, sequence), 16 threads per
-// column: thread i handles column i/16 (token c/4, head c%4), dims 8(i%16) .. +8.  Weights
-// 2^(m - max) are exact; a piece that saw no key the column may attend to has m = -inf and
-// weight 0.
+// The rescore flag of one output row, where the row is final: lane j of the row's 16 lanes
+// holds dims 8j .. 8j+7 (BF16 codes ow), which lie in pair group j % 8.  The keys token t
+// sees: its segment's cached keys (their maxima seg_st: the 8 pair-group norms, then the
+// |V| code of each dim) and the chunk's rows up to its own (rs_kpre / rs_dpre, the running
+// maxima the preparation left).  The elements in units of their dim's largest |V| (a dim
+// whose V is zero in every key the row sees is exactly zero and left out) and the scores'
+// bound E = scale log2(e) sum_G |q_G| max|k_G| decide (rs_flag_decide); Q's pair-group norms
+// come from the row as given, which rotation leaves unchanged.  fp32: y is at most 1 in
+// magnitude (an output element is a weighted mean of its dim's V), and a decision about a
+// threshold needs no more.
+// What the decision reads from memory, loaded before the merge so that it is in flight
+// beside the partials: this lane's 8 Q values, the chunk rows' |V| maxima at its dims and
+// the pair-group norm maximum of its group.
+struct MtFlagIn {
+    uint4 qx, dp;
+    uint32_t kpre;
+};
+
+__device__ __forceinline__ void mt_flag_load(const PrefillArgs& a, int64_t bh, int t, int64_t row, int j,
+                                             MtFlagIn& in) {
+    const int64_t er = bh * a.n_new + t;
+    in.qx = *reinterpret_cast<const uint4*>(a.q + row * kD + 8 * j);
+    in.dp = *reinterpret_cast<const uint4*>(a.rs_dpre + er * kD + 8 * j);
+    in.kpre = a.rs_kpre[er * 8 + (j & 7)];
+}
+
+__device__ __forceinline__ void mt_flag_row(const PrefillArgs& a, int64_t row, float m, const uint32_t (&ow)[4],
+                                            const MtFlagIn& in, const uint32_t* seg_st, int j) {
+    const uint4 qx = in.qx, dp = in.dp;
+    const uint32_t kq = max(seg_st[j & 7], in.kpre);
+    const uint32_t dw[4] = {dp.x, dp.y, dp.z, dp.w};
+    const uint32_t qw[4] = {qx.x, qx.y, qx.z, qx.w};
+    float ss = 0.f, mn2 = INFINITY, qq = 0.f;
+    bool bad = false;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const uint32_t d = max(seg_st[8 + 8 * j + i], i & 1 ? dw[i >> 1] >> 16 : dw[i >> 1] & 0xffffu);
+        const uint32_t xs = i & 1 ? ow[i >> 1] & 0xffff0000u : ow[i >> 1] << 16;
+        const uint32_t qs = i & 1 ? qw[i >> 1] & 0xffff0000u : qw[i >> 1] << 16;
+        const float x = __uint_as_float(xs), q = __uint_as_float(qs);
+        const float dv = __uint_as_float(d << 16);
+        const float y = dv > 0.f ? x * __builtin_amdgcn_rcpf(dv) : 0.f;
+        ss = fmaf(y, y, ss);
+        if (dv > 0.f) mn2 = fminf(mn2, y * y);
+        bad |= !__builtin_isfinite(x);
+        qq = fmaf(q, q, qq);
+    }
+    // |q_G| |k_G|max: lanes j and j + 8 hold the two halves of pair group j % 8.
+    qq += dpp_f<0x128>(qq);                         // row_ror:8
+    float e = j < 8 ? sqrtf(qq) * sqrtf(__uint_as_float(kq)) : 0.f;
+    ss = row16_sum(ss);
+    e = row16_sum(e);
+    mn2 = -row16_max(-mn2);
+    const uint64_t bads = __ballot(bad);
+    const int h = (threadIdx.x & (kWave - 1)) >> 4;
+    const bool row_bad = ((bads >> (16 * h)) & 0xffffull) != 0ull;
+    if (j == 0 && (row_bad || rs_flag_decide(static_cast<double>(mn2), static_cast<double>(ss), static_cast<double>(m),
+                                             static_cast<double>(e) * fabs(a.qk_scale_log2))))
+        rs_append(a, static_cast<uint32_t>(row));
+}
+
+// One workgroup per (KV head, sequence), 16 threads per column: thread i handles column
+// i/16 (token c/4, head c%4), dims 8(i%16) .. +8.  It reduces the segment's cached-key
+// maxima from every piece's records, merges the partials of a split segment's pieces
+// (weights 2^(m - max) are exact; a piece that saw no key the column may attend to has
+// m = -inf and weight 0) and decides each output row's rescore flag.
 template <int kW>
 __global__ __launch_bounds__(256 * kW) void mt_merge_kernel(PrefillArgs a) {
     constexpr int kCols = kMtTile * kW;
@@ -1068,85 +1131,112 @@ __global__ __launch_bounds__(256 * kW) void mt_merge_kernel(PrefillArgs a) {
     const int64_t extra = a.plan_hdr[3];
     const int64_t off = a.seq_off[b];
     const int span = static_cast<int>((a.seq_off[b + 1] - off) / kHkv);
-    if (span == 0) return;
+    if (span == 0) return;                          // no keys: a start out of range, NaN rows
     const int nk = span - lead;
     const int64_t seg_off = off + static_cast<int64_t>(kvh) * span + lead;
     const int64_t w_first = range_of(per_wg, extra, seg_off);
     const int n_pieces = static_cast<int>(range_of(per_wg, extra, seg_off + nk - 1) - w_first) + 1;
     const int64_t slot0 = w_first + static_cast<int64_t>(b) * kHkv + kvh;
-    // The segment's cached-key maxima for the rescore flag: every piece's records (one per
-    // wave), whole segments too.
-    if (a.rs_hdr && threadIdx.x < 8 + kD) {
-        const int64_t seg = static_cast<int64_t>(b) * kHkv + kvh;
-        uint32_t x = 0u;
-        for (int p = 0; p < n_pieces; ++p)
-#pragma unroll
-            for (int w = 0; w < kW; ++w) x = max(x, a.piece_st[((slot0 + p) * kW + w) * (8 + kD) + threadIdx.x]);
-        if (threadIdx.x < 8)
-            a.rs_kc[seg * 8 + threadIdx.x] = x;
-        else
-            a.rs_dc[seg * kD + threadIdx.x - 8] = x;
-    }
-    if (n_pieces == 1) return;
+    const int64_t bh = static_cast<int64_t>(b) * kHkv + kvh;
     const int col = threadIdx.x >> 4;
-    const int d0 = 8 * (threadIdx.x & 15);
+    const int j = threadIdx.x & 15;
+    const int d0 = 8 * j;
     const int tok = col >> 2;
-    if (tok >= a.n_new) return;
-    // Pieces four at a time, every load of a group issued before any is used (one memory
-    // round trip per group); the running max moves by whole powers of two, so rescaling
-    // what is already summed is exact.
-    constexpr int kGroupP = 4;
-    float m = -INFINITY;
-    double l = 0.0, o[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-    for (int p0 = 0; p0 < n_pieces; p0 += kGroupP) {
-        float2 ml[kGroupP];
-        double v[kGroupP][8];
+    const bool live = tok < a.n_new;
+    const int64_t row = (static_cast<int64_t>(b) * a.n_new + min(tok, a.n_new - 1)) * kHq + kvh * kGroup + (col & 3);
+    // The flag's inputs (and a whole segment's row, which the stream kernel wrote with its
+    // running max) requested first.
+    MtFlagIn fin{};
+    uint32_t ow[4] = {0u, 0u, 0u, 0u};
+    float m = 0.f;
+    if (a.rs_hdr && live) {
+        mt_flag_load(a, bh, tok, row, j, fin);
+        if (n_pieces == 1) {
+            const uint2* src = reinterpret_cast<const uint2*>(a.out + row * kD + d0);   // out is 8-byte aligned
+            const uint2 x0 = src[0], x1 = src[1];
+            ow[0] = x0.x;
+            ow[1] = x0.y;
+            ow[2] = x1.x;
+            ow[3] = x1.y;
+            m = a.rs_m[row];
+        }
+    }
+    __shared__ uint32_t seg_st[8 + kD];
+    if (a.rs_hdr && threadIdx.x < 8 + kD) {
+        // Four pieces' records at a time, all requested before any is used.
+        uint32_t x = 0u;
+        for (int p0 = 0; p0 < n_pieces; p0 += 4) {
+            uint32_t r[4][kW];
 #pragma unroll
-        for (int q = 0; q < kGroupP; ++q) {
-            ml[q] = make_float2(-INFINITY, 0.f);
-            if (p0 + q < n_pieces) {
-                const int64_t c = (slot0 + p0 + q) * kCols + col;
-                ml[q] = a.part_ml[c];
-                const float4* po = reinterpret_cast<const float4*>(a.part_o + c * kD + d0);
-                const float4 x0 = po[0], x1 = po[1];
-                v[q][0] = x0.x;
-                v[q][1] = x0.y;
-                v[q][2] = x0.z;
-                v[q][3] = x0.w;
-                v[q][4] = x1.x;
-                v[q][5] = x1.y;
-                v[q][6] = x1.z;
-                v[q][7] = x1.w;
+            for (int q = 0; q < 4; ++q)
+#pragma unroll
+                for (int w = 0; w < kW; ++w)
+                    r[q][w] = p0 + q < n_pieces ? a.piece_st[((slot0 + p0 + q) * kW + w) * (8 + kD) + threadIdx.x] : 0u;
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+#pragma unroll
+                for (int w = 0; w < kW; ++w) x = max(x, r[q][w]);
+        }
+        seg_st[threadIdx.x] = x;
+    }
+    __syncthreads();
+    if (!live) return;
+    if (n_pieces > 1) {
+        // Pieces four at a time, every load of a group issued before any is used (one memory
+        // round trip per group); the running max moves by whole powers of two, so rescaling
+        // what is already summed is exact.
+        constexpr int kGroupP = 4;
+        m = -INFINITY;
+        double l = 0.0, o[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+        for (int p0 = 0; p0 < n_pieces; p0 += kGroupP) {
+            float2 ml[kGroupP];
+            double v[kGroupP][8];
+#pragma unroll
+            for (int q = 0; q < kGroupP; ++q) {
+                ml[q] = make_float2(-INFINITY, 0.f);
+                if (p0 + q < n_pieces) {
+                    const int64_t c = (slot0 + p0 + q) * kCols + col;
+                    ml[q] = a.part_ml[c];
+                    const float4* po = reinterpret_cast<const float4*>(a.part_o + c * kD + d0);
+                    const float4 x0 = po[0], x1 = po[1];
+                    v[q][0] = x0.x;
+                    v[q][1] = x0.y;
+                    v[q][2] = x0.z;
+                    v[q][3] = x0.w;
+                    v[q][4] = x1.x;
+                    v[q][5] = x1.y;
+                    v[q][6] = x1.z;
+                    v[q][7] = x1.w;
+                }
+            }
+            float mb = m;
+#pragma unroll
+            for (int q = 0; q < kGroupP; ++q) mb = fmaxf(mb, ml[q].x);
+            if (m != -INFINITY && mb != m) {
+                const int e = max_shift(m, mb);
+                l = ldexp(l, e);
+#pragma unroll
+                for (int i = 0; i < 8; ++i) o[i] = ldexp(o[i], e);
+            }
+            m = mb;
+#pragma unroll
+            for (int q = 0; q < kGroupP; ++q) {
+                if (ml[q].x == -INFINITY) continue;
+                const int e = max_shift(ml[q].x, m);
+                l += ldexp(static_cast<double>(ml[q].y), e);
+#pragma unroll
+                for (int i = 0; i < 8; ++i) o[i] += ldexp(v[q][i], e);
             }
         }
-        float mb = m;
 #pragma unroll
-        for (int q = 0; q < kGroupP; ++q) mb = fmaxf(mb, ml[q].x);
-        if (m != -INFINITY && mb != m) {
-            const int e = max_shift(m, mb);
-            l = ldexp(l, e);
-#pragma unroll
-            for (int j = 0; j < 8; ++j) o[j] = ldexp(o[j], e);
-        }
-        m = mb;
-#pragma unroll
-        for (int q = 0; q < kGroupP; ++q) {
-            if (ml[q].x == -INFINITY) continue;
-            const int e = max_shift(ml[q].x, m);
-            l += ldexp(static_cast<double>(ml[q].y), e);
-#pragma unroll
-            for (int j = 0; j < 8; ++j) o[j] += ldexp(v[q][j], e);
-        }
+        for (int i = 0; i < 4; ++i)
+            ow[i] = f32_to_bf16_out(static_cast<float>(o[2 * i] / l)) |
+                    (static_cast<uint32_t>(f32_to_bf16_out(static_cast<float>(o[2 * i + 1] / l))) << 16);
+        uint2* dst = reinterpret_cast<uint2*>(a.out + row * kD + d0);   // out is 8-byte aligned
+        dst[0] = make_uint2(ow[0], ow[1]);
+        dst[1] = make_uint2(ow[2], ow[3]);
     }
-    uint16_t h8[8];
-#pragma unroll
-    for (int j = 0; j < 8; ++j) h8[j] = f32_to_bf16_out(static_cast<float>(o[j] / l));
-    if ((threadIdx.x & 15) == 0 && a.rs_hdr)
-        a.rs_m[(static_cast<int64_t>(b) * a.n_new + tok) * kHq + kvh * kGroup + (col & 3)] = m;
-    uint2* dst = reinterpret_cast<uint2*>(a.out + ((static_cast<int64_t>(b) * a.n_new + tok) * kHq + kvh * kGroup +
-                                                   (col & 3)) * kD + d0);   // out is 8-byte aligned
-    dst[0] = make_uint2(h8[0] | (static_cast<uint32_t>(h8[1]) << 16), h8[2] | (static_cast<uint32_t>(h8[3]) << 16));
-    dst[1] = make_uint2(h8[4] | (static_cast<uint32_t>(h8[5]) << 16), h8[6] | (static_cast<uint32_t>(h8[7]) << 16));
+    if (a.rs_hdr) mt_flag_row(a, row, m, ow, fin, seg_st, j);
 }
 
 template <int kW>

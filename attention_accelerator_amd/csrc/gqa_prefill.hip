@@ -804,8 +804,8 @@ __device__ __forceinline__ void pf_probs_and_next(const f32x4_t (&scur)[4], floa
 }
 
 // The rescore flag of one output row, in the attention kernel's layout: lane (g, n) holds
-// dims 16 dt + 4 g + i of query n's row (BF16 codes, pk[dt]).  The same decision as
-// rs_flag_kernel (rs_flag_decide over the row's elements in units of each dim's largest |V|
+// dims 16 dt + 4 g + i of query n's row (BF16 codes, pk[dt]).  The same decision as the
+// multi-token merge's (rs_flag_decide over the row's elements in units of each dim's largest |V|
 // and the scores' bound E = scale log2(e) sum_G |q_G| max|k_G|), over the keys the row at
 // position pos sees: the keys before its chunk block (rs_kc, rs_dc at that block, reduced
 // before this kernel runs) and the block's rows up to its own (rs_kpre, rs_dpre).  Q's
