@@ -232,16 +232,6 @@ __device__ __forceinline__ uint16_t bf16_of(double d) { return f32_to_bf16_rne(s
 
 __device__ __forceinline__ double f64_of_bf16(uint16_t b) { return static_cast<double>(bf16_to_f32(b)); }
 
-// Split v into hi + mid + lo BF16 codes; returns part `which`.
-__device__ __forceinline__ uint16_t split3(double v, int which) {
-    const uint16_t hi = bf16_of(v);
-    const double r1 = v - f64_of_bf16(hi);
-    const uint16_t mid = bf16_of(r1);
-    if (which == 0) return hi;
-    if (which == 1) return mid;
-    return bf16_of(r1 - f64_of_bf16(mid));
-}
-
 __device__ __forceinline__ bf16x8_t pack8(const uint16_t (&h)[8]) {
     union {
         uint16_t u[8];

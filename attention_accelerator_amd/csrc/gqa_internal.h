@@ -123,7 +123,8 @@ struct PrefillArgs {
     RopeTable rope;
     // Multi-token path (n_new <= kMultiMaxNew): the stream-K split of the decode path, W =
     // multi_waves(n_new) column tiles of 16 (4 heads x 4 tokens) per segment.
-    uint4* q_op;              // [B][8][W][3][4][64] Q operands (3 BF16 parts, MFMA B layout)
+    float4* q_op;             // [B][8][W][8][64] Q rotated and scaled, f32, in the MFMA B layout
+                              // (float4 2kb + h of lane (g, n): dims 32kb + 8g + 4h .. +3)
     int64_t* plan_hdr;        // {total stream positions, positions per workgroup, segment lead,
                               //  positions moved from odd to even ranges}
     int64_t* seq_off;         // [B+1] stream position of sequence b's first segment

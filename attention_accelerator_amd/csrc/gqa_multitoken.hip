@@ -81,6 +81,10 @@ __device__ __forceinline__ void mt_wait_planes(bool steady) {
 // flight).
 __device__ __forceinline__ void mt_barrier() { asm volatile("s_barrier" ::: "memory"); }
 
+// Barrier after this wave's LDS writes have completed, without waiting for its global stores
+// (which nothing after the barrier reads).
+__device__ __forceinline__ void mt_lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
 int32_t multi_waves(int32_t n_new) { return n_new <= 4 ? 1 : n_new <= 8 ? 2 : 4; }
 int32_t multi_simd_waves(int32_t n_new) { return n_new <= 4 ? 1 : 2; }
 
@@ -103,7 +107,7 @@ MtLayout mt_layout(int32_t batch, int32_t n_new, int32_t n_wgs) {
     auto al = [](size_t x) { return (x + 255) / 256 * 256; };
     MtLayout l{};
     l.q_op = 0;
-    l.plan = l.q_op + al(static_cast<size_t>(batch) * kHkv * w * 12 * kWave * sizeof(uint4));
+    l.plan = l.q_op + al(static_cast<size_t>(batch) * kHkv * w * 8 * kWave * sizeof(float4));
     l.seq_off = l.plan + 256;
     l.part_o = l.seq_off + al((static_cast<size_t>(batch) + 1) * sizeof(int64_t));
     l.part_ml = l.part_o + al(n_slots * cols * kD * sizeof(float));
@@ -121,7 +125,7 @@ size_t prefill_multi_bytes(int32_t batch, int32_t n_new, int32_t n_wgs) {
 void prefill_multi_layout(PrefillArgs& a, void* base, int32_t n_wgs) {
     const MtLayout l = mt_layout(a.batch, a.n_new, n_wgs);
     char* p = static_cast<char*>(base);
-    a.q_op = reinterpret_cast<uint4*>(p + l.q_op);
+    a.q_op = reinterpret_cast<float4*>(p + l.q_op);
     a.plan_hdr = reinterpret_cast<int64_t*>(p + l.plan);
     a.seq_off = reinterpret_cast<int64_t*>(p + l.seq_off);
     a.part_o = reinterpret_cast<float*>(p + l.part_o);
@@ -193,8 +197,8 @@ __device__ __forceinline__ void load4(const uint16_t* p, uint16_t (&h)[4]) {
 //  - a quarter of the Q operands of every column tile: lane (g, n) of tile tau holds
 //    column 16 tau + n (token 4 tau + n/4, Q head 4*kvh + n%4) at dims 32kb + 8g + j; wave
 //    w takes kb = w & 1 and its pair kb + 2, j in [4(w >> 1), +4), rotated at the token's
-//    position and scaled by scale*log2(e) in double, split into three BF16 parts; columns
-//    of tokens t >= T are zero;
+//    position and scaled by scale*log2(e) in double, stored rounded to f32 (the stream
+//    kernel splits each into three BF16 parts, exactly); columns of tokens t >= T are zero;
 //  - the same dims' share of the scores of the chunk's own keys (key start + u, u < T:
 //    the new K row rotated at its position and not rounded, as the reference rotates K)
 //    against every column, in double (fp64 MFMAs).  The four shares are added in a fixed
@@ -280,12 +284,16 @@ __global__ __launch_bounds__(256) void mt_prepare_kernel(PrefillArgs a) {
     const bool rope_q = (a.flags & 1u) != 0;
     const bool rope_k = (a.flags & 2u) != 0;
     if (rope_q || rope_k)
-        for (int u = w; u < T; u += 4) {
-            rope_sincos(static_cast<int64_t>(st) + u, a.rope.inv_freq[lane], sn_s[u][lane], cs_s[u][lane]);
-            if (kvh == 0 && a.rs_hdr)
-                a.rs_cs[(static_cast<int64_t>(b) * T + u) * kPairs + lane] = make_double2(cs_s[u][lane], sn_s[u][lane]);
+#pragma unroll
+        for (int r = 0; r < kW; ++r) {       // unrolled: the sincos chains of one lane overlap
+            const int u = w + 4 * r;
+            if (u < T) {
+                rope_sincos(static_cast<int64_t>(st) + u, a.rope.inv_freq[lane], sn_s[u][lane], cs_s[u][lane]);
+                if (kvh == 0 && a.rs_hdr)
+                    a.rs_cs[(static_cast<int64_t>(b) * T + u) * kPairs + lane] = make_double2(cs_s[u][lane], sn_s[u][lane]);
+            }
         }
-    __syncthreads();
+    mt_lds_barrier();
 
     double qvx[kW][4], qvy[kW][4];
 #pragma unroll
@@ -374,35 +382,34 @@ __global__ __launch_bounds__(256) void mt_prepare_kernel(PrefillArgs a) {
     }
 #pragma unroll
     for (int tau = 0; tau < kW; ++tau) {
-        uint4* base = a.q_op + ((static_cast<int64_t>(b) * kHkv + kvh) * kW + tau) * 12 * kWave + lane;
-#pragma unroll
-        for (int s = 0; s < 3; ++s) {
-            uint16_t px[4], py[4];
-#pragma unroll
-            for (int jj = 0; jj < 4; ++jj) {
-                px[jj] = split3(qvx[tau][jj], s);
-                py[jj] = split3(qvy[tau][jj], s);
-            }
-            uint2* dx = reinterpret_cast<uint2*>(base + (s * 4 + kbp) * kWave) + (w >> 1);
-            uint2* dy = reinterpret_cast<uint2*>(base + (s * 4 + kbp + 2) * kWave) + (w >> 1);
-            *dx = make_uint2(px[0] | (static_cast<uint32_t>(px[1]) << 16), px[2] | (static_cast<uint32_t>(px[3]) << 16));
-            *dy = make_uint2(py[0] | (static_cast<uint32_t>(py[1]) << 16), py[2] | (static_cast<uint32_t>(py[3]) << 16));
-        }
+        // float4 f = 2 kb + h of lane (g, n) holds dims 32 kb + 8 g + 4 h .. +3.
+        float4* base = a.q_op + ((static_cast<int64_t>(b) * kHkv + kvh) * kW + tau) * 8 * kWave + lane;
+        base[(2 * kbp + (w >> 1)) * kWave] =
+            make_float4(static_cast<float>(qvx[tau][0]), static_cast<float>(qvx[tau][1]),
+                        static_cast<float>(qvx[tau][2]), static_cast<float>(qvx[tau][3]));
+        base[(2 * (kbp + 2) + (w >> 1)) * kWave] =
+            make_float4(static_cast<float>(qvy[tau][0]), static_cast<float>(qvy[tau][1]),
+                        static_cast<float>(qvy[tau][2]), static_cast<float>(qvy[tau][3]));
     }
-    __syncthreads();
+    mt_lds_barrier();
     if (a.rs_hdr && threadIdx.x < 8 + kD) {
         // Running maxima over the chunk's tokens (rescore flag: token t sees chunk keys <= t),
         // and the cached-key maxima of this segment cleared for the stream kernel.
         const int64_t bh = static_cast<int64_t>(b) * kHkv + kvh;
         const int c = threadIdx.x;
+        // Unrolled over the most tokens a tile set holds, every LDS read issued up front.
+        uint32_t x[kU];
+#pragma unroll
+        for (int u = 0; u < kU; ++u) x[u] = u < T ? (c < 8 ? kn_s[u][c] : static_cast<uint32_t>(vd_s[u][c - 8])) : 0u;
         uint32_t run = 0u;
-        for (int u = 0; u < T; ++u) {
-            if (c < 8) {
-                run = max(run, kn_s[u][c]);
-                a.rs_kpre[(bh * T + u) * 8 + c] = run;
-            } else {
-                run = max(run, static_cast<uint32_t>(vd_s[u][c - 8]));
-                a.rs_dpre[(bh * T + u) * kD + c - 8] = static_cast<uint16_t>(run);
+#pragma unroll
+        for (int u = 0; u < kU; ++u) {
+            run = max(run, x[u]);
+            if (u < T) {
+                if (c < 8)
+                    a.rs_kpre[(bh * T + u) * 8 + c] = run;
+                else
+                    a.rs_dpre[(bh * T + u) * kD + c - 8] = static_cast<uint16_t>(run);
             }
         }
     }
@@ -877,6 +884,22 @@ __device__ __forceinline__ void mt_advance(const PrefillArgs& a, MtCursor& c, in
     c.k_b = __builtin_amdgcn_readfirstlane(static_cast<int>(min(static_cast<int64_t>(c.nk), x_end - c.x)));
 }
 
+// Eight f32 values split into three BF16 parts each, packed as three MFMA operands (two
+// values per dword): hi = x truncated to 8 significant bits, mid = the residual truncated,
+// lo = what remains, which has at most 8 significant bits -- every step exact, so
+// hi + mid + lo = x.
+__device__ __forceinline__ void mt_split3_8(const float (&x)[8], uint4 (&w)[3]) {
+    float r1[8], r2[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        r1[i] = x[i] - __uint_as_float(__float_as_uint(x[i]) & 0xffff0000u);
+        r2[i] = r1[i] - __uint_as_float(__float_as_uint(r1[i]) & 0xffff0000u);
+    }
+    w[0] = make_uint4(pack_hi16(x[0], x[1]), pack_hi16(x[2], x[3]), pack_hi16(x[4], x[5]), pack_hi16(x[6], x[7]));
+    w[1] = make_uint4(pack_hi16(r1[0], r1[1]), pack_hi16(r1[2], r1[3]), pack_hi16(r1[4], r1[5]), pack_hi16(r1[6], r1[7]));
+    w[2] = make_uint4(pack_hi16(r2[0], r2[1]), pack_hi16(r2[2], r2[3]), pack_hi16(r2[4], r2[5]), pack_hi16(r2[6], r2[7]));
+}
+
 template <int kW>
 // Two- and four-tile workgroups run two waves per SIMD: their registers (VGPRs and AGPRs
 // together) must fit in half the SIMD's file.
@@ -960,11 +983,19 @@ __global__ __launch_bounds__(kWave * kW) __attribute__((amdgpu_waves_per_eu(kW =
         const int64_t seg = static_cast<int64_t>(c.b) * kHkv + c.kvh;
         bf16x8_t qop[3][4];
         {
-            const uint4* src = a.q_op + (seg * kW + wv) * 12 * kWave + lane;
+            const float4* src = a.q_op + (seg * kW + wv) * 8 * kWave + lane;
+            float4 qf[8];
 #pragma unroll
-            for (int s = 0; s < 3; ++s)
+            for (int f = 0; f < 8; ++f) qf[f] = src[f * kWave];
 #pragma unroll
-                for (int kb = 0; kb < 4; ++kb) qop[s][kb] = as_bf16x8(src[(s * 4 + kb) * kWave]);
+            for (int kb = 0; kb < 4; ++kb) {
+                const float x[8] = {qf[2 * kb].x, qf[2 * kb].y, qf[2 * kb].z, qf[2 * kb].w,
+                                    qf[2 * kb + 1].x, qf[2 * kb + 1].y, qf[2 * kb + 1].z, qf[2 * kb + 1].w};
+                uint4 w[3];
+                mt_split3_8(x, w);
+#pragma unroll
+                for (int sp = 0; sp < 3; ++sp) qop[sp][kb] = as_bf16x8(w[sp]);
+            }
         }
         float cs[kU];
         {
@@ -1122,7 +1153,7 @@ __device__ __forceinline__ void mt_flag_row(const PrefillArgs& a, int64_t row, f
 // (weights 2^(m - max) are exact; a piece that saw no key the column may attend to has
 // m = -inf and weight 0) and decides each output row's rescore flag.
 template <int kW>
-__global__ __launch_bounds__(256 * kW) void mt_merge_kernel(PrefillArgs a) {
+__global__ __launch_bounds__(256 * kW) __attribute__((amdgpu_waves_per_eu(8))) void mt_merge_kernel(PrefillArgs a) {
     constexpr int kCols = kMtTile * kW;
     const int kvh = blockIdx.x;
     const int b = blockIdx.y;
@@ -1179,18 +1210,20 @@ __global__ __launch_bounds__(256 * kW) void mt_merge_kernel(PrefillArgs a) {
         }
         seg_st[threadIdx.x] = x;
     }
-    __syncthreads();
+    mt_lds_barrier();
     if (!live) return;
     if (n_pieces > 1) {
-        // Pieces four at a time, every load of a group issued before any is used (one memory
-        // round trip per group); the running max moves by whole powers of two, so rescaling
-        // what is already summed is exact.
-        constexpr int kGroupP = 4;
+        // Pieces two at a time, every load of a group issued before any is used (one memory
+        // round trip per group; with 61 registers eight waves fit on a SIMD, so a 16-wave
+        // workgroup per segment at T = 16 no longer leaves half of them waiting for a CU);
+        // the running max moves by whole powers of two, so rescaling what is already summed
+        // is exact.
+        constexpr int kGroupP = 2;
         m = -INFINITY;
         double l = 0.0, o[8] = {0, 0, 0, 0, 0, 0, 0, 0};
         for (int p0 = 0; p0 < n_pieces; p0 += kGroupP) {
             float2 ml[kGroupP];
-            double v[kGroupP][8];
+            float v[kGroupP][8];                        // widened where summed
 #pragma unroll
             for (int q = 0; q < kGroupP; ++q) {
                 ml[q] = make_float2(-INFINITY, 0.f);
@@ -1225,7 +1258,7 @@ __global__ __launch_bounds__(256 * kW) void mt_merge_kernel(PrefillArgs a) {
                 const int e = max_shift(ml[q].x, m);
                 l += ldexp(static_cast<double>(ml[q].y), e);
 #pragma unroll
-                for (int i = 0; i < 8; ++i) o[i] += ldexp(v[q][i], e);
+                for (int i = 0; i < 8; ++i) o[i] += ldexp(static_cast<double>(v[q][i]), e);
             }
         }
 #pragma unroll
