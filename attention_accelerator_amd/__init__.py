@@ -14,9 +14,8 @@ memfmt (.mem codec), stimulus (synthetic inputs), build (hipcc in-tree build).
 from .attention import (DEFAULT_SCALE, GROUP_SIZE, HEAD_DIM, N_KV_HEADS, N_Q_HEADS,  # noqa: F401
                         ROPE_THETA, PreparedDecode, PreparedPrefill, decode_workspace_bytes, gqa_attention,
                         gqa_decode, gqa_decode_paged, gqa_prefill, kv_append, kv_append_paged,
-                        make_params, new_workspace,
-                        prefill_rescored_rows, prefill_workspace_bytes, profile_enable, profile_read,
-                        rope_half_split,
+                        make_params, new_workspace, prefill_rescored_rows, prefill_workspace_bytes,
+                        profile_enable, profile_read, profile_read_stages, rope_half_split,
                         validate_lengths)
 from ._lib import GqaConfigError, GqaError  # noqa: F401
 

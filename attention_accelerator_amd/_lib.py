@@ -45,6 +45,7 @@ EXPORTS = (
     "gqa_rope_rows_bf16",
     "gqa_profile_enable",
     "gqa_profile_read",
+    "gqa_profile_read_stages",
     "gqa_status_string",
     "gqa_abi_version",
 )
@@ -162,6 +163,9 @@ def lib() -> ctypes.CDLL:
     L.gqa_profile_enable.restype = ctypes.c_int
     L.gqa_profile_read.argtypes = [ctypes.POINTER(GqaProfile)]
     L.gqa_profile_read.restype = ctypes.c_int
+    L.gqa_profile_read_stages.argtypes = [ctypes.POINTER(ctypes.c_double), ctypes.c_int32,
+                                          ctypes.POINTER(ctypes.c_int32)]
+    L.gqa_profile_read_stages.restype = ctypes.c_int
     L.gqa_status_string.argtypes = [ctypes.c_int]
     L.gqa_status_string.restype = ctypes.c_char_p
     L.gqa_abi_version.argtypes = []

@@ -544,3 +544,13 @@ def profile_read():
     p = _lib.GqaProfile()
     check(lib().gqa_profile_read(ctypes.byref(p)), "gqa_profile_read")
     return p.kernel_ms[0], p.kernel_ms[1], p.calls
+
+
+def profile_read_stages():
+    """-> ([stage_ms_total] * 4, calls) recorded since the last read: decode {stream, merge,
+    0, 0}, prefill {append + staging + reduce, attention, rescore, 0}, prefill of at most 16
+    new tokens {preparation, stream, merge, rescore}."""
+    ms = (ctypes.c_double * 4)()
+    n = ctypes.c_int32(0)
+    check(lib().gqa_profile_read_stages(ms, 4, ctypes.byref(n)), "gqa_profile_read_stages")
+    return list(ms), n.value

@@ -94,10 +94,10 @@ double qk_scale_log2(const gqa_params_t* p) { return p->scale * 1.44269504088896
 
 bool aligned(const void* p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
 
-// Opt-in kernel timing (gqa_profile_enable / gqa_profile_read).
+// Opt-in kernel timing (gqa_profile_enable / gqa_profile_read / gqa_profile_read_stages).
 struct Profiler {
     std::mutex mu;
-    std::vector<hipEvent_t> events;   // 3 per recorded call
+    std::vector<hipEvent_t> events;   // kProfileEvents per recorded call
     int32_t capacity = 0;
     int32_t used = 0;
 };
@@ -107,12 +107,12 @@ Profiler& profiler() {
     return p;
 }
 
-// Returns the next free event triple, or nullptr when profiling is off or full.
+// Returns the next free set of kProfileEvents events, or nullptr when profiling is off or full.
 hipEvent_t* profile_slot() {
     Profiler& p = profiler();
     std::lock_guard<std::mutex> lock(p.mu);
     if (p.used >= p.capacity) return nullptr;
-    return &p.events[static_cast<size_t>(p.used++) * 3];
+    return &p.events[static_cast<size_t>(p.used++) * kProfileEvents];
 }
 
 }  // namespace
@@ -219,7 +219,7 @@ using namespace gqa;
 
 extern "C" {
 
-uint32_t gqa_abi_version(void) { return (4u << 16) | 0u; }
+uint32_t gqa_abi_version(void) { return (4u << 16) | 1u; }
 
 const char* gqa_status_string(int status) {
     switch (status) {
@@ -445,7 +445,7 @@ int gqa_profile_enable(int32_t max_calls) {
     p.capacity = 0;
     p.used = 0;
     if (max_calls <= 0) return GQA_OK;
-    p.events.resize(static_cast<size_t>(max_calls) * 3);
+    p.events.resize(static_cast<size_t>(max_calls) * kProfileEvents);
     for (auto& e : p.events) {
         if (hipEventCreate(&e) != hipSuccess) {
             e = nullptr;
@@ -456,24 +456,35 @@ int gqa_profile_enable(int32_t max_calls) {
     return GQA_OK;
 }
 
-int gqa_profile_read(gqa_profile_t* out) {
-    if (!out) return GQA_ERR_BAD_POINTER;
+int gqa_profile_read_stages(double* stage_ms, int32_t n_stages, int32_t* calls) {
+    if (!stage_ms || n_stages < 0 || n_stages > kProfileEvents - 1) return GQA_ERR_BAD_POINTER;
     Profiler& p = profiler();
     std::lock_guard<std::mutex> lock(p.mu);
-    double split = 0.0, combine = 0.0;
+    double sum[kProfileEvents - 1] = {};
     for (int32_t i = 0; i < p.used; ++i) {
-        hipEvent_t* ev = &p.events[static_cast<size_t>(i) * 3];
-        float a = 0.f, b = 0.f;
-        if (hipEventSynchronize(ev[2]) != hipSuccess) return GQA_ERR_HIP;
-        if (hipEventElapsedTime(&a, ev[0], ev[1]) != hipSuccess) return GQA_ERR_HIP;
-        if (hipEventElapsedTime(&b, ev[1], ev[2]) != hipSuccess) return GQA_ERR_HIP;
-        split += a;
-        combine += b;
+        hipEvent_t* ev = &p.events[static_cast<size_t>(i) * kProfileEvents];
+        if (hipEventSynchronize(ev[kProfileEvents - 1]) != hipSuccess) return GQA_ERR_HIP;
+        for (int j = 0; j + 1 < kProfileEvents; ++j) {
+            float ms = 0.f;
+            if (hipEventElapsedTime(&ms, ev[j], ev[j + 1]) != hipSuccess) return GQA_ERR_HIP;
+            sum[j] += ms;
+        }
     }
-    out->kernel_ms[0] = split;
-    out->kernel_ms[1] = combine;
-    out->calls = p.used;
+    for (int j = 0; j < n_stages; ++j) stage_ms[j] = sum[j];
+    if (calls) *calls = p.used;
     p.used = 0;
+    return GQA_OK;
+}
+
+int gqa_profile_read(gqa_profile_t* out) {
+    if (!out) return GQA_ERR_BAD_POINTER;
+    double st[2] = {0.0, 0.0};
+    int32_t n = 0;
+    const int rc = gqa_profile_read_stages(st, 2, &n);
+    if (rc != GQA_OK) return rc;
+    out->kernel_ms[0] = st[0];
+    out->kernel_ms[1] = st[1];
+    out->calls = n;
     return GQA_OK;
 }
 
@@ -636,6 +647,7 @@ int gqa_prefill_bf16(const gqa_params_t* params, const uint16_t* q, const uint16
         // The preparation kernel of the multi-token path appends the chunk's rows itself.
         hipError_t e = launch_prefill_multi(a, s, ev);
         if (e == hipSuccess) e = launch_rescore(a, s);
+        if (ev) (void)hipEventRecord(ev[4], s);
         return e == hipSuccess ? GQA_OK : GQA_ERR_HIP;
     }
     // The attention kernel decides the rescore flag of each row it writes, from the K/V
@@ -647,6 +659,10 @@ int gqa_prefill_bf16(const gqa_params_t* params, const uint16_t* q, const uint16
     if (e == hipSuccess) e = launch_prefill_attention(a, s);
     if (ev) (void)hipEventRecord(ev[2], s);
     if (e == hipSuccess) e = launch_rescore(a, s);
+    if (ev) {
+        (void)hipEventRecord(ev[3], s);
+        (void)hipEventRecord(ev[4], s);
+    }
     return e == hipSuccess ? GQA_OK : GQA_ERR_HIP;
 }
 

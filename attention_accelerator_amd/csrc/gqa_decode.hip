@@ -2048,10 +2048,8 @@ hipError_t launch_decode(const DecodeArgs& a, int batch, hipStream_t stream, hip
         else
             hipLaunchKernelGGL((decode_single_kernel<false, false>), grid, dim3(kSingleWaves * kWave), 0, stream, a);
         const hipError_t e = hipGetLastError();
-        if (ev) {
-            (void)hipEventRecord(ev[1], stream);
-            (void)hipEventRecord(ev[2], stream);
-        }
+        if (ev)
+            for (int j = 1; j < kProfileEvents; ++j) (void)hipEventRecord(ev[j], stream);
         return e;
     }
     if (rq)
@@ -2076,7 +2074,8 @@ hipError_t launch_decode(const DecodeArgs& a, int batch, hipStream_t stream, hip
     if (ev) (void)hipEventRecord(ev[1], stream);
     hipLaunchKernelGGL(decode_merge_kernel, dim3(kHkv, batch), dim3(kGroup * kWave), 0, stream, a);
     e = hipGetLastError();
-    if (ev) (void)hipEventRecord(ev[2], stream);
+    if (ev)
+        for (int j = 2; j < kProfileEvents; ++j) (void)hipEventRecord(ev[j], stream);
     return e;
 }
 

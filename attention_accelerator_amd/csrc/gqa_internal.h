@@ -214,6 +214,8 @@ __host__ __device__ inline bool rs_flag_decide(double mn2, double ss, double m, 
     f2 = fe > f2 ? fe : f2;
     return mn2 * kD < kRsFlagRatio2 * f2 * ss;
 }
+// HIP events per call of the opt-in kernel timing: up to four stages between them.
+constexpr int kProfileEvents = 5;
 constexpr int kRsSlots = 1024;                            // partial slots (tiles x pieces)
 constexpr int kRsMaxPieces = 64;                          // pieces per tile at most
 // Rescore region of a workspace; ncb, nr: the chunk-prefix blocks and rows (prefill:

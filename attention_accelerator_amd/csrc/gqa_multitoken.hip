@@ -1288,7 +1288,9 @@ hipError_t launch_multi_w(const PrefillArgs& a, hipStream_t stream, hipEvent_t* 
     if (ev) (void)hipEventRecord(ev[2], stream);
     if (e != hipSuccess) return e;
     hipLaunchKernelGGL(mt_merge_kernel<kW>, dim3(kHkv, static_cast<unsigned>(a.batch)), dim3(256 * kW), 0, stream, a);
-    return hipGetLastError();
+    e = hipGetLastError();
+    if (ev) (void)hipEventRecord(ev[3], stream);
+    return e;
 }
 
 hipError_t launch_prefill_multi(const PrefillArgs& a, hipStream_t stream, hipEvent_t* ev) {

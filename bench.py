@@ -318,9 +318,9 @@ def bench_prefill(args, torch, gqa, dev) -> int:
             flush.fill_(i & 0xFF)
             call()
         torch.cuda.synchronize()
-        ap_ms, at_ms, n = gqa.profile_read()
+        st_ms, n = gqa.profile_read_stages()
         gqa.profile_enable(0)
-        append_ms, attn_ms = ap_ms / n, at_ms / n
+        append_ms, attn_ms, rescore_ms = st_ms[0] / n, st_ms[1] / n, st_ms[2] / n
     print(f"[bench] {args.steps} steps: {ms_per_step * 1e3:.2f} us/step", file=sys.stderr, flush=True)
 
     torch.cuda.synchronize()
@@ -334,7 +334,7 @@ def bench_prefill(args, torch, gqa, dev) -> int:
                     "unit": "TFLOP/s", "frac": round(achieved / MFMA_BF16_PEAK_TFLOPS, 4),
                     "traffic": None, "kernel": "prefill_attn_kernel",
                     "kernel_us": round(attn_ms * 1e3, 2), "append_stage_us": round(append_ms * 1e3, 2),
-                    "flops_per_launch": flops}
+                    "rescore_us": round(rescore_ms * 1e3, 2), "flops_per_launch": flops}
     result = {
         "metric": "GQA chunked prefill µs/step + MFMA TFLOP/s, B=4 512 new over 8192 cached",
         "value": round(tflops, 2),
@@ -444,9 +444,10 @@ def bench_multitoken(args, torch, gqa, dev, stimulus) -> int:
         for _ in range(args.steps):
             call()
         torch.cuda.synchronize()
-        ap_ms, at_ms, n = gqa.profile_read()
+        st_ms, n = gqa.profile_read_stages()
         gqa.profile_enable(0)
-        append_ms, attn_ms = ap_ms / n, at_ms / n
+        append_ms, attn_ms = st_ms[0] / n, st_ms[1] / n
+        merge_ms, rescore_ms = st_ms[2] / n, st_ms[3] / n
     print(f"[bench] {args.steps} steps: {ms_per_step * 1e3:.2f} us/step", file=sys.stderr, flush=True)
     gpu_out = None if args.no_cpu_baseline else codes_of(out)     # the last step's rows
     rescored = call.rescored_rows()                               # the last step's fp64 rows
@@ -454,9 +455,9 @@ def bench_multitoken(args, torch, gqa, dev, stimulus) -> int:
         calibrate_copy(torch, dev)
     roofline = None
     if attn_ms:
-        # Chunks of at most 16 new tokens run the stream-K path (events: preparation with
-        # the append, then the stream kernel); longer ones the prefill attention kernel
-        # (events: append, then attention).
+        # Chunks of at most 16 new tokens run the stream-K path (stages: preparation with
+        # the append, the stream kernel, the merge, the rescore); longer ones the prefill
+        # attention kernel (stages: append + staging + reduce, attention, rescore).
         stream_k = n_new <= 16
         achieved = step_bytes / (attn_ms * 1e-3) / 1e9
         roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
@@ -465,6 +466,8 @@ def bench_multitoken(args, torch, gqa, dev, stimulus) -> int:
                     "kernel": "mt_stream_kernel" if stream_k else "prefill_attn_kernel",
                     "kernel_us": round(attn_ms * 1e3, 2),
                     ("prepare_us" if stream_k else "append_us"): round(append_ms * 1e3, 2),
+                    **({"merge_us": round(merge_ms * 1e3, 2), "rescore_us": round(rescore_ms * 1e3, 2)}
+                       if stream_k else {"rescore_us": round(merge_ms * 1e3, 2)}),
                     "bytes_per_launch": step_bytes}
     result = {
         "metric": f"GQA multi-token decode µs/step + achieved HBM GB/s, B=64 ragged ctx 512–8192, {n_new} new tokens",

@@ -254,15 +254,16 @@ int gqa_rope_rows_bf16(const uint16_t* in, uint16_t* out, int64_t n_rows, int64_
                        const int32_t* positions, int32_t pos0, double theta, void* stream);
 
 /* Kernel timing for measurement harnesses.  While enabled, each decode or prefill
- * call brackets its two kernels with HIP events on the call's stream (up to
- * `max_calls` calls are recorded; later ones are not): decode {stream kernel, merge
- * kernel}, prefill {KV append and staging kernels, attention kernel}, prefill of at most 16
- * new tokens {preparation kernel (with the append), stream kernel}.  The Q-operand preparation kernel
- * of a decode call runs before the first event, the merge kernel of a prefill of at most 16
- * new tokens after the last.  gqa_profile_read waits for the
- * recorded events, returns the summed kernel times and the number of calls recorded,
- * and clears the record.  Not for the hot path: enabling creates the events.  No
- * reference counterpart (the reference's timing is its simulator's cycle count). */
+ * call brackets its kernels with HIP events on the call's stream (up to `max_calls`
+ * calls are recorded; later ones are not), in up to four stages: decode {stream kernel,
+ * merge kernel} (the Q-operand preparation kernel runs before the first event), prefill
+ * {KV append, staging and reduce kernels; attention kernel; fp64 rescore}, prefill of at
+ * most 16 new tokens {preparation kernel (with the append); stream kernel; merge kernel;
+ * fp64 rescore}.  gqa_profile_read waits for the recorded events, returns the summed times
+ * of the first two stages and the number of calls recorded, and clears the record;
+ * gqa_profile_read_stages does the same for up to four stages (a path's missing stages
+ * read 0).  Not for the hot path: enabling creates the events.  No reference counterpart
+ * (the reference's timing is its simulator's cycle count). */
 typedef struct gqa_profile {
     double kernel_ms[2];  /* summed durations of the call's first and second kernel */
     int32_t calls;        /* calls recorded */
@@ -270,6 +271,8 @@ typedef struct gqa_profile {
 
 int gqa_profile_enable(int32_t max_calls); /* max_calls <= 0 disables and frees */
 int gqa_profile_read(gqa_profile_t* out);
+/* stage_ms[i], i < n_stages <= 4: summed time of stage i over the recorded calls (ABI 4.1). */
+int gqa_profile_read_stages(double* stage_ms, int32_t n_stages, int32_t* calls);
 
 /* Human-readable name of a status code. */
 const char* gqa_status_string(int status);

@@ -134,6 +134,18 @@ def test_profile_read_empty():
     assert p.calls == 0
 
 
+def test_profile_read_stages_empty_and_bounds():
+    L = _lib.lib()
+    ms = (ctypes.c_double * 4)(-1.0, -1.0, -1.0, -1.0)
+    n = ctypes.c_int32(-1)
+    assert L.gqa_profile_read_stages(ms, 4, ctypes.byref(n)) == OK
+    assert n.value == 0 and list(ms) == [0.0, 0.0, 0.0, 0.0]
+    assert L.gqa_profile_read_stages(ms, 5, ctypes.byref(n)) == BAD_PTR       # at most four stages
+    assert L.gqa_profile_read_stages(None, 2, ctypes.byref(n)) == BAD_PTR
+    assert L.gqa_profile_read_stages(ms, 2, None) == OK                       # the count is optional
+    assert L.gqa_abi_version() == (4 << 16) | 1
+
+
 def test_workspace_init_rejects():
     L = _lib.lib()
     p = _params()
