@@ -58,10 +58,11 @@ bool use_multi(const gqa_params_t* p, int32_t n_new) {
 // XCD weighting of the stream-K ranges, per mille of a range moved from each workgroup on
 // an odd XCD to its even neighbour; GQA_XCD_SKEW overrides the path's default (0 gives
 // equal ranges).  At most 250: an odd range keeps at least 3/4 of the range size, more
-// than a segment lead.  Measured defaults (B=64 ragged 512-8192): 40 for the one- and
-// two-wave multi-token kernels (T <= 4: 219.7 -> 216.2 us per step; T <= 8, two waves per
-// SIMD: 249.4 -> 245.6 us, best of 0..80), 0 for the four-wave one (T <= 16: 40 made it
-// 375 -> 379 us) and for decode (30 made it 187.6 -> 191 us).
+// than a segment lead.  Measured defaults (B=64 ragged 512-8192): 80 for the one-wave
+// multi-token kernel (T <= 4: 0 / 40 / 80 / 120 / 160 gave 226.0 / 223.6 / 221.8 / 225.0 /
+// 228.1 us per step, two boxes), 40 for the two-wave one (T <= 8, two waves per SIMD: 259.9 /
+// 256.1 / 260.8 us at 0 / 40 / 80), 0 for the four-wave one (T <= 16: 40 made it 375 -> 379
+// us) and for decode (30 made it 187.6 -> 191 us).
 int32_t xcd_skew_pm(int32_t dflt) {
     const char* s = std::getenv("GQA_XCD_SKEW");
     if (s) {
@@ -632,7 +633,7 @@ int gqa_prefill_bf16(const gqa_params_t* params, const uint16_t* q, const uint16
     char* ws = static_cast<char*>(workspace);
     if (multi) {
         prefill_multi_layout(a, workspace, multi_wgs(params, n_new));
-        a.skew_pm = xcd_skew_pm(multi_waves(n_new) <= 2 ? 40 : 0);
+        a.skew_pm = xcd_skew_pm(multi_waves(n_new) == 1 ? 80 : multi_waves(n_new) == 2 ? 40 : 0);
         rescore_layout(a, params, ws + align_up(prefill_multi_bytes(batch, n_new, multi_wgs(params, n_new)), 256), 1,
                        n_new, 0);
     } else {
