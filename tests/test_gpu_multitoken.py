@@ -123,6 +123,20 @@ def test_multi_long_sequences(dev):
     _check(want, got, "multi long")
 
 
+@pytest.mark.parametrize("n_new,bsz", [(4, 150), (9, 70), (16, 130)])
+def test_multi_many_sequences(dev, n_new, bsz):
+    """More than 64 sequences: the plan, each workgroup's search for its first piece and the
+    merge take the batch 64 sequences at a time, so the second and third windows of 64 are
+    used here.  Ragged starts 0..600 (short segments, many pieces per workgroup range):
+    every output row within the tolerance of the oracle."""
+    rng = np.random.default_rng(60 + n_new)
+    starts = [int(x) for x in rng.integers(0, 601, size=bsz)]
+    q, kn, vn, k, v = _chunk(starts, n_new, max(starts) + n_new, 60 + n_new)
+    want = _oracle(q, kn, vn, k, v, starts)
+    got, _, _ = _run(q, kn, vn, k, v, starts, dev)
+    _check(want, got, f"multi T={n_new} B={bsz}")
+
+
 @pytest.mark.parametrize("n_new,n_wgs", [(4, "1"), (4, "7"), (4, "64"), (4, "333"), (4, "4096"),
                                          (7, "2"), (7, "130"), (12, "4"), (12, "37"), (16, "1024")])
 def test_multi_partition_counts(dev, n_new, n_wgs):

@@ -61,6 +61,16 @@ def test_paged_matches_oracle_and_contiguous(dev, bsz, cap, lo, seed):
     assert_within_ulp(contiguous, got, 2, "paged vs contiguous")
 
 
+def test_paged_many_sequences(dev):
+    """200 sequences of 1..400 keys: the plan and each workgroup's search for its first piece
+    span four windows of 64 sequences; every output against the oracle."""
+    b = stimulus.decode_batch(200, 400, min_len=1, max_len=400, seed=51)
+    kp, vp, table = _paginate(b.k, b.v, b.seq_len, 51)
+    got = to_codes(gqa.gqa_decode_paged(b.q.to(dev), kp.to(dev), vp.to(dev), table.to(dev),
+                                        b.query_pos, b.seq_len))
+    assert_within_ulp(_oracle(b), got, 64, "paged B=200")
+
+
 def test_paged_causal_and_partial_blocks(dev):
     """query_position < seq_len - 1: rows past the query are in the pool (NaN here) but
     masked, including inside the query's own block."""

@@ -126,6 +126,18 @@ def test_prefill_no_rope(dev):
     assert np.array_equal(to_codes(kd)[0, 3, 70:103], to_codes(kn[0, :, 3]))
 
 
+def test_prefill_many_sequences(dev):
+    """70 sequences of 20 new tokens after 0..300 cached positions (560 (sequence, KV head)
+    pairs: staging, the block-statistics reduction and the attention grid over more than 64
+    sequences): every output row against the oracle."""
+    g = torch.Generator("cpu").manual_seed(61)
+    starts = [int(x) for x in torch.randint(0, 301, (70,), generator=g)]
+    q, kn, vn, k, v = _chunk(70, 20, max(starts) + 20, starts, 61)
+    want = _oracle(q, kn, vn, k, v, starts)
+    got, _, _ = _run(q, kn, vn, k, v, starts, dev)
+    assert_within_ulp(want.reshape(-1, 128), got.reshape(-1, 128), 64, "prefill B=70 T=20")
+
+
 def test_multi_token_decode_ragged_batch(dev):
     """Multi-token decode (T=4 new tokens per sequence, e.g. speculative drafts) over a
     ragged batch of 8 sequences with 100..3000 cached positions, through gqa_prefill:
