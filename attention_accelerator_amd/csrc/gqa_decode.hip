@@ -2035,6 +2035,13 @@ hipError_t launch_zero_words(uint32_t* p, int64_t n, hipStream_t stream) {
 
 hipError_t launch_decode(const DecodeArgs& a, int batch, hipStream_t stream, hipEvent_t* ev) {
     const bool rq = (a.flags & 1u) != 0, rk = (a.flags & 2u) != 0;
+    // Records the call's events from `from` on: a failed launch leaves none unrecorded, so
+    // that the profiler can still read the call's stage times.
+    auto done = [&](int from, hipError_t err) {
+        if (ev)
+            for (int j = from; j < kProfileEvents; ++j) (void)hipEventRecord(ev[j], stream);
+        return err;
+    };
     if (a.pieces_cap > 0 && !a.block_table) {
         // Single launch (small batches, contiguous cache).
         if (ev) (void)hipEventRecord(ev[0], stream);
@@ -2047,17 +2054,14 @@ hipError_t launch_decode(const DecodeArgs& a, int batch, hipStream_t stream, hip
             hipLaunchKernelGGL((decode_single_kernel<false, true>), grid, dim3(kSingleWaves * kWave), 0, stream, a);
         else
             hipLaunchKernelGGL((decode_single_kernel<false, false>), grid, dim3(kSingleWaves * kWave), 0, stream, a);
-        const hipError_t e = hipGetLastError();
-        if (ev)
-            for (int j = 1; j < kProfileEvents; ++j) (void)hipEventRecord(ev[j], stream);
-        return e;
+        return done(1, hipGetLastError());
     }
     if (rq)
         hipLaunchKernelGGL((decode_prepare_kernel<true>), dim3(kHkv, batch + 1), dim3(kWave), 0, stream, a);
     else
         hipLaunchKernelGGL((decode_prepare_kernel<false>), dim3(kHkv, batch + 1), dim3(kWave), 0, stream, a);
     hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return e;
+    if (e != hipSuccess) return done(0, e);
     if (ev) (void)hipEventRecord(ev[0], stream);
     if (a.block_table) {
         if (rk)
@@ -2070,13 +2074,10 @@ hipError_t launch_decode(const DecodeArgs& a, int batch, hipStream_t stream, hip
         hipLaunchKernelGGL((decode_stream_kernel<false>), dim3(a.n_wgs), dim3(kWave), 0, stream, a);
     }
     e = hipGetLastError();
-    if (e != hipSuccess) return e;
+    if (e != hipSuccess) return done(1, e);
     if (ev) (void)hipEventRecord(ev[1], stream);
     hipLaunchKernelGGL(decode_merge_kernel, dim3(kHkv, batch), dim3(kGroup * kWave), 0, stream, a);
-    e = hipGetLastError();
-    if (ev)
-        for (int j = 2; j < kProfileEvents; ++j) (void)hipEventRecord(ev[j], stream);
-    return e;
+    return done(2, hipGetLastError());
 }
 
 }  // namespace gqa

@@ -1276,17 +1276,24 @@ template <int kW>
 hipError_t launch_multi_w(const PrefillArgs& a, hipStream_t stream, hipEvent_t* ev) {
     const bool vec = (reinterpret_cast<uintptr_t>(a.q) % 16) == 0 && (reinterpret_cast<uintptr_t>(a.k_new) % 16) == 0;
     const dim3 grid(kHkv, static_cast<unsigned>(a.batch) + 1);
+    // A failed launch still records the events this function owns (1 .. kProfileEvents - 2),
+    // so that the profiler can read the call's stage times.
+    auto done = [&](int from, hipError_t err) {
+        if (ev)
+            for (int j = from; j < kProfileEvents - 1; ++j) (void)hipEventRecord(ev[j], stream);
+        return err;
+    };
     if (vec)
         hipLaunchKernelGGL((mt_prepare_kernel<true, kW>), grid, dim3(256), 0, stream, a);
     else
         hipLaunchKernelGGL((mt_prepare_kernel<false, kW>), grid, dim3(256), 0, stream, a);
     hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return e;
+    if (e != hipSuccess) return done(1, e);
     if (ev) (void)hipEventRecord(ev[1], stream);
     hipLaunchKernelGGL(mt_stream_kernel<kW>, dim3(static_cast<unsigned>(a.n_wgs)), dim3(kWave * kW), 0, stream, a);
     e = hipGetLastError();
     if (ev) (void)hipEventRecord(ev[2], stream);
-    if (e != hipSuccess) return e;
+    if (e != hipSuccess) return done(3, e);
     hipLaunchKernelGGL(mt_merge_kernel<kW>, dim3(kHkv, static_cast<unsigned>(a.batch)), dim3(256 * kW), 0, stream, a);
     e = hipGetLastError();
     if (ev) (void)hipEventRecord(ev[3], stream);
