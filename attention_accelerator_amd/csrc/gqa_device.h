@@ -114,6 +114,23 @@ __device__ __forceinline__ float row16_max(float x) {
     return x;
 }
 
+// The same two reductions in double.
+__device__ __forceinline__ double row16_sum_f64(double x) {
+    x += dpp_d<0xB1>(x);
+    x += dpp_d<0x4E>(x);
+    x += dpp_d<0x124>(x);
+    x += dpp_d<0x128>(x);
+    return x;
+}
+
+__device__ __forceinline__ double row16_min_f64(double x) {
+    x = fmin(x, dpp_d<0xB1>(x));
+    x = fmin(x, dpp_d<0x4E>(x));
+    x = fmin(x, dpp_d<0x124>(x));
+    x = fmin(x, dpp_d<0x128>(x));
+    return x;
+}
+
 // Across the four rows of a wave (lanes l, l^16, l^32, l^48).
 __device__ __forceinline__ float cross_row_sum(float x) {
     x += __shfl_xor(x, 16);

@@ -198,13 +198,15 @@ struct PrefillArgs {
 // and rows whose first-half products are all positive and cancel against the second half
 // (the largest partial sums the 4 x 32-dim MFMA steps can carry) about 1.9 times less;
 // outlier V channels (x 2^6 .. 2^14) err in proportion to their own D_j.
-// Squared: 128 min y^2 < 2^-34 F^2 sum y^2.
+// Squared: 128 min y^2 <= 2^-34 F^2 sum y^2, in double.
 constexpr double kRsFlagRatio2 = 1.0 / 17179869184.0;    // (2^-17)^2
 constexpr double kRsFlagScore = 6.0;
 constexpr double kRsFlagE = 32.0;
 
-// The decision for one row: mn2 = smallest y_j^2 over the dims with D_j > 0, ss = sum y^2,
-// m = running max, e = E.  Not finite: rescored.
+// The decision for one row: mn2 = smallest y_j^2 over the dims with D_j > 0, ss = sum y^2
+// (both formed in double: see the callers), m = running max, e = E.  Not finite: rescored.
+// A row whose every element is exactly zero while some D_j > 0 (mn2 = ss = 0) is rescored
+// too; with no D_j > 0 (mn2 = inf) the row is exactly zero and is not.
 __host__ __device__ inline bool rs_flag_decide(double mn2, double ss, double m, double e) {
     if (!(ss <= 1e300) || !(e <= 1e300) || !(m == m)) return true;
     double f2 = 1.0;
@@ -212,7 +214,7 @@ __host__ __device__ inline bool rs_flag_decide(double mn2, double ss, double m, 
     const double fe = e * e * (1.0 / (kRsFlagE * kRsFlagE));
     f2 = fm > f2 ? fm : f2;
     f2 = fe > f2 ? fe : f2;
-    return mn2 * kD < kRsFlagRatio2 * f2 * ss;
+    return mn2 * kD <= kRsFlagRatio2 * f2 * ss;
 }
 // HIP events per call of the opt-in kernel timing: up to four stages between them.
 constexpr int kProfileEvents = 5;

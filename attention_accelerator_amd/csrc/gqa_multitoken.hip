@@ -1093,9 +1093,13 @@ __global__ __launch_bounds__(kWave * kW) __attribute__((amdgpu_waves_per_eu(kW =
 // maxima the preparation left).  The elements in units of their dim's largest |V| (a dim
 // whose V is zero in every key the row sees is exactly zero and left out) and the scores'
 // bound E = scale log2(e) sum_G |q_G| max|k_G| decide (rs_flag_decide); Q's pair-group norms
-// come from the row as given, which rotation leaves unchanged.  fp32: y is at most 1 in
-// magnitude (an output element is a weighted mean of its dim's V), and a decision about a
-// threshold needs no more.
+// come from the row as given, which rotation leaves unchanged.  y and its square are formed
+// in double: y is at most 1 in magnitude (an output element is a weighted mean of its dim's
+// V) but may be far smaller -- keys of huge V that the softmax gives no weight set D_j and not
+// the output -- and in fp32 y^2 underflows to zero in every dim once the row's elements lie
+// ~2^63 below their D_j, which leaves nothing to compare (BF16 ratios lie within 2^+-261 and
+// their squares within double's range).  E stays in fp32: it only overflows to infinity
+// (the row is then rescored) or underflows to zero (F = 1 then, the N(0,1) threshold).
 // What the decision reads from memory, loaded before the merge so that it is in flight
 // beside the partials: this lane's 8 Q values, the chunk rows' |V| maxima at its dims and
 // the pair-group norm maximum of its group.
@@ -1118,7 +1122,8 @@ __device__ __forceinline__ void mt_flag_row(const PrefillArgs& a, int64_t row, f
     const uint32_t kq = max(seg_st[j & 7], in.kpre);
     const uint32_t dw[4] = {dp.x, dp.y, dp.z, dp.w};
     const uint32_t qw[4] = {qx.x, qx.y, qx.z, qx.w};
-    float ss = 0.f, mn2 = INFINITY, qq = 0.f;
+    double ss = 0.0, mn2 = INFINITY;
+    float qq = 0.f;
     bool bad = false;
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
@@ -1127,23 +1132,22 @@ __device__ __forceinline__ void mt_flag_row(const PrefillArgs& a, int64_t row, f
         const uint32_t qs = i & 1 ? qw[i >> 1] & 0xffff0000u : qw[i >> 1] << 16;
         const float x = __uint_as_float(xs), q = __uint_as_float(qs);
         const float dv = __uint_as_float(d << 16);
-        const float y = dv > 0.f ? x * __builtin_amdgcn_rcpf(dv) : 0.f;
-        ss = fmaf(y, y, ss);
-        if (dv > 0.f) mn2 = fminf(mn2, y * y);
+        const double y = dv > 0.f ? static_cast<double>(x) * __builtin_amdgcn_rcp(static_cast<double>(dv)) : 0.0;
+        ss = fma(y, y, ss);
+        if (dv > 0.f) mn2 = fmin(mn2, y * y);
         bad |= !__builtin_isfinite(x);
         qq = fmaf(q, q, qq);
     }
     // |q_G| |k_G|max: lanes j and j + 8 hold the two halves of pair group j % 8.
     qq += dpp_f<0x128>(qq);                         // row_ror:8
     float e = j < 8 ? sqrtf(qq) * sqrtf(__uint_as_float(kq)) : 0.f;
-    ss = row16_sum(ss);
+    ss = row16_sum_f64(ss);
     e = row16_sum(e);
-    mn2 = -row16_max(-mn2);
+    mn2 = row16_min_f64(mn2);
     const uint64_t bads = __ballot(bad);
     const int h = (threadIdx.x & (kWave - 1)) >> 4;
     const bool row_bad = ((bads >> (16 * h)) & 0xffffull) != 0ull;
-    if (j == 0 && (row_bad || rs_flag_decide(static_cast<double>(mn2), static_cast<double>(ss), static_cast<double>(m),
-                                             static_cast<double>(e) * fabs(a.qk_scale_log2))))
+    if (j == 0 && (row_bad || rs_flag_decide(mn2, ss, static_cast<double>(m), static_cast<double>(e) * fabs(a.qk_scale_log2))))
         rs_append(a, static_cast<uint32_t>(row));
 }
 

@@ -811,6 +811,8 @@ __device__ __forceinline__ void pf_probs_and_next(const f32x4_t (&scur)[4], floa
 // before this kernel runs) and the block's rows up to its own (rs_kpre, rs_dpre).  Q's
 // pair-group norms come from the row as given (rotation leaves them unchanged): this lane
 // reads dims 8g .. 8g+7 and 32 + 8g .. (and their pairs 64 on), pair groups g and 4 + g.
+// y and its square in double, as in the multi-token merge (in fp32 y^2 underflows in every
+// dim of a row whose elements lie ~2^63 below their dims' largest |V|).
 // Returns the decision for the row in every lane of its column.
 __device__ __forceinline__ bool pf_flag_row(const PrefillArgs& a, int b, int kvh, int st, int pos, int64_t row,
                                             float m, bool forced, const uint2 (&pk)[8], int lane) {
@@ -826,7 +828,7 @@ __device__ __forceinline__ bool pf_flag_row(const PrefillArgs& a, int b, int kvh
     const uint4 q3 = *reinterpret_cast<const uint4*>(qrow + kPairs + 32 + 8 * g);
     const uint32_t k0 = max(a.rs_kc[ec * 8 + g], a.rs_kpre[er * 8 + g]);
     const uint32_t k1 = max(a.rs_kc[ec * 8 + 4 + g], a.rs_kpre[er * 8 + 4 + g]);
-    float ss = 0.f, mn2 = INFINITY;
+    double ss = 0.0, mn2 = INFINITY;
     bool bad = forced;
 #pragma unroll
     for (int dt = 0; dt < 8; ++dt) {
@@ -839,9 +841,9 @@ __device__ __forceinline__ bool pf_flag_row(const PrefillArgs& a, int b, int kvh
         for (int i = 0; i < 4; ++i) {
             const float x = __uint_as_float(xs[i]);
             const float dv = __uint_as_float(d[i] << 16);
-            const float y = dv > 0.f ? x * __builtin_amdgcn_rcpf(dv) : 0.f;
-            ss = fmaf(y, y, ss);
-            if (dv > 0.f) mn2 = fminf(mn2, y * y);
+            const double y = dv > 0.f ? static_cast<double>(x) * __builtin_amdgcn_rcp(static_cast<double>(dv)) : 0.0;
+            ss = fma(y, y, ss);
+            if (dv > 0.f) mn2 = fmin(mn2, y * y);
             bad |= !__builtin_isfinite(x);
         }
     }
@@ -861,12 +863,11 @@ __device__ __forceinline__ bool pf_flag_row(const PrefillArgs& a, int b, int kvh
     ss += __shfl_xor(ss, 32);
     e += __shfl_xor(e, 16);
     e += __shfl_xor(e, 32);
-    mn2 = fminf(mn2, __shfl_xor(mn2, 16));
-    mn2 = fminf(mn2, __shfl_xor(mn2, 32));
+    mn2 = fmin(mn2, __shfl_xor(mn2, 16));
+    mn2 = fmin(mn2, __shfl_xor(mn2, 32));
     bad = (__shfl_xor(static_cast<int>(bad), 16) | __shfl_xor(static_cast<int>(bad), 32) |
            __shfl_xor(static_cast<int>(bad), 48) | static_cast<int>(bad)) != 0;
-    return bad || rs_flag_decide(static_cast<double>(mn2), static_cast<double>(ss), static_cast<double>(m),
-                                 static_cast<double>(e) * fabs(a.qk_scale_log2));
+    return bad || rs_flag_decide(mn2, ss, static_cast<double>(m), static_cast<double>(e) * fabs(a.qk_scale_log2));
 }
 
 __global__ __launch_bounds__(kPfThreads) void prefill_attn_kernel(PrefillArgs a) {

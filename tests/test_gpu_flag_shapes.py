@@ -161,3 +161,28 @@ def test_decode_cancelling_and_outliers(dev):
     want = orc.decode(to_codes(qd), to_codes(k), to_codes(v), np.asarray(starts),
                       np.asarray(starts) - 1, rope_q=False)
     assert_within_ulp(want, got, 64, "decode, cancelling products + V channels x 2^14")
+
+
+@pytest.mark.parametrize("n_new,huge", [(16, "chunk"), (32, "cached")])
+def test_zero_weight_huge_v(dev, n_new, huge):
+    """V rows the softmax gives no weight set each dim's largest |V| far above the outputs:
+    Q x 2^10 (scores ~3000 in natural-log units, the softmax peaked on a cached key or two)
+    and keys that score ~0 (weight exactly 0) with huge V -- the chunk's own rows, K x 2^-100
+    and V x 2^100 (T=16, the multi-token merge's decision), or cached positions 0..63, K x
+    2^-40 and V x 2^90, one staging block of their own that stays inside the staging range
+    (T=32, the prefill kernel's decision; in the chunk's block, or past 2^100, they would mark
+    their block unstageable and every row would be rescored anyway).  Each element in units
+    of its dim's largest |V| is then ~2^-90 or less, and the flag decision has to form its
+    squares without underflow: in fp32 every square was zero, no row was flagged, and rows
+    whose output cancels between two near-tied keys missed 64 ULP (found by a wider run of
+    the random-shape draw, multi-token seed 66941)."""
+    starts = [int(x) for x in np.random.default_rng(77).integers(135, 1104, size=8)]
+    q, kn, vn, k, v = _inputs(starts, n_new, 77 + n_new, dev)
+    q = (q.float() * 2.0 ** 10).to(torch.bfloat16)
+    if huge == "chunk":
+        kn = (kn.float() * 2.0 ** -100).to(torch.bfloat16)
+        vn = (vn.float() * 2.0 ** 100).to(torch.bfloat16)
+    else:
+        k[:, :, :64] = (k[:, :, :64].float() * 2.0 ** -40).to(torch.bfloat16)
+        v[:, :, :64] = (v[:, :, :64].float() * 2.0 ** 90).to(torch.bfloat16)
+    _run_and_check(q, kn, vn, k, v, starts, f"T={n_new}, zero-weight huge V ({huge} keys)")
