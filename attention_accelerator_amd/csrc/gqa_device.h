@@ -203,6 +203,12 @@ __device__ __forceinline__ uint32_t pk_max_u16(uint32_t x, uint32_t y) {
                                                                   __builtin_bit_cast(u16x2_t, y)));
 }
 
+__device__ __forceinline__ uint32_t pk_min_u16(uint32_t x, uint32_t y) {
+    typedef unsigned short u16x2_t __attribute__((ext_vector_type(2)));
+    return __builtin_bit_cast(uint32_t, __builtin_elementwise_min(__builtin_bit_cast(u16x2_t, x),
+                                                                  __builtin_bit_cast(u16x2_t, y)));
+}
+
 // acc + the squares of the two BF16 values in w (v_dot2_f32_bf16, fp32 accumulation).
 __device__ __forceinline__ float bf16x2_sq_acc(uint32_t w, float acc) {
     typedef __bf16 b16x2_t __attribute__((ext_vector_type(2)));

@@ -624,6 +624,7 @@ struct PfTile {
     f32x4_t acc[8];
     double l64;
     float m_run;
+    float u;           // bound on what fp16's subnormal quantum adds to O (O's units, this lane's keys)
 };
 
 // Closes a group: O += acc * cv (cv = 2^-(V scale of the group's blocks), exact).
@@ -674,6 +675,7 @@ __device__ __forceinline__ void pf_rescale(PfTile& t, float m_new) {
                 t.acc[dt][i] = ldexpf(t.acc[dt][i], shift);
             }
         t.l64 = ldexp(t.l64, shift);
+        t.u = ldexpf(t.u, shift);
         t.m_run = m_new;
     }
 }
@@ -686,8 +688,7 @@ __device__ __forceinline__ void pf_probs_tile16(const f32x4_t& s, float mult, fl
     float p[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-        // v_exp_f32: 2^x, 0 for -inf (masked keys); results below 2^-126 flush to 0, far
-        // below anything the BF16 output can see.
+        // v_exp_f32: 2^x, 0 for -inf (masked keys); results below 2^-126 flush to 0.
         p[i] = __builtin_amdgcn_exp2f(fmaf(s[i], mult, off));
         lsum += p[i];
     }
@@ -812,10 +813,12 @@ __device__ __forceinline__ void pf_probs_and_next(const f32x4_t (&scur)[4], floa
 // pair-group norms come from the row as given (rotation leaves them unchanged): this lane
 // reads dims 8g .. 8g+7 and 32 + 8g .. (and their pairs 64 on), pair groups g and 4 + g.
 // y and its square in double, as in the multi-token merge (in fp32 y^2 underflows in every
-// dim of a row whose elements lie ~2^63 below their dims' largest |V|).
-// Returns the decision for the row in every lane of its column.
+// dim of a row whose elements lie ~2^63 below their dims' largest |V|).  ul bounds the error
+// fp16's subnormal quantum added to every element (the attention loop's u over l): a row
+// with an element below 8 ul, where that error could reach 64 ULP with a margin of 2, is
+// rescored as well.  Returns the decision for the row in every lane of its column.
 __device__ __forceinline__ bool pf_flag_row(const PrefillArgs& a, int b, int kvh, int st, int pos, int64_t row,
-                                            float m, bool forced, const uint2 (&pk)[8], int lane) {
+                                            float m, bool forced, double ul, const uint2 (&pk)[8], int lane) {
     const int g = lane >> 4;
     const int cb = pos / kPfBlk - st / kPfBlk;
     const int r = pos % kPfBlk;
@@ -829,6 +832,7 @@ __device__ __forceinline__ bool pf_flag_row(const PrefillArgs& a, int b, int kvh
     const uint32_t k0 = max(a.rs_kc[ec * 8 + g], a.rs_kpre[er * 8 + g]);
     const uint32_t k1 = max(a.rs_kc[ec * 8 + 4 + g], a.rs_kpre[er * 8 + 4 + g]);
     double ss = 0.0, mn2 = INFINITY;
+    float mnx = INFINITY;
     bool bad = forced;
 #pragma unroll
     for (int dt = 0; dt < 8; ++dt) {
@@ -844,6 +848,7 @@ __device__ __forceinline__ bool pf_flag_row(const PrefillArgs& a, int b, int kvh
             const double y = dv > 0.f ? static_cast<double>(x) * __builtin_amdgcn_rcp(static_cast<double>(dv)) : 0.0;
             ss = fma(y, y, ss);
             if (dv > 0.f) mn2 = fmin(mn2, y * y);
+            mnx = fminf(mnx, fabsf(x));
             bad |= !__builtin_isfinite(x);
         }
     }
@@ -865,6 +870,9 @@ __device__ __forceinline__ bool pf_flag_row(const PrefillArgs& a, int b, int kvh
     e += __shfl_xor(e, 32);
     mn2 = fmin(mn2, __shfl_xor(mn2, 16));
     mn2 = fmin(mn2, __shfl_xor(mn2, 32));
+    mnx = fminf(mnx, __shfl_xor(mnx, 16));
+    mnx = fminf(mnx, __shfl_xor(mnx, 32));
+    bad |= static_cast<double>(mnx) < 8.0 * ul;
     bad = (__shfl_xor(static_cast<int>(bad), 16) | __shfl_xor(static_cast<int>(bad), 32) |
            __shfl_xor(static_cast<int>(bad), 48) | static_cast<int>(bad)) != 0;
     return bad || rs_flag_decide(mn2, ss, static_cast<double>(m), static_cast<double>(e) * fabs(a.qk_scale_log2));
@@ -1037,6 +1045,7 @@ __global__ __launch_bounds__(kPfThreads) void prefill_attn_kernel(PrefillArgs a)
     }
     tl.l64 = 0.0;
     tl.m_run = -INFINITY;
+    tl.u = 0.f;
     // The open group: blocks summed into tl.acc so far and their V scale exponent.  A block
     // whose V scale differs from the group's by more than 3 (its P would leave fp16's range
     // or its precision) closes the group first.  A block holding chunk keys is summed alone:
@@ -1053,6 +1062,12 @@ __global__ __launch_bounds__(kPfThreads) void prefill_attn_kernel(PrefillArgs a)
         return fmaxf(cq * pow2f(-static_cast<int>(static_cast<int8_t>(w & 0xffu))), 1.17549435e-38f);
     };
     auto blk_sv = [&](uint32_t w) { return static_cast<int>(static_cast<int8_t>((w >> 8) & 0xffu)); };
+    // The largest V scale exponent among this workgroup's blocks (the smallest-V block's).
+    int sv_hi = -128;
+    for (int j = lane; j < n_blk; j += kWave) sv_hi = max(sv_hi, blk_sv(sw[j]));
+#pragma unroll
+    for (int sh = 1; sh < kWave; sh <<= 1) sv_hi = max(sv_hi, __shfl_xor(sv_hi, sh));
+    sv_hi = __builtin_amdgcn_readfirstlane(sv_hi);
 
     // Block 0's scores.  The barrier after them frees K buffer 0 for block 2.
     __builtin_amdgcn_s_waitcnt(0x0F70);    // vmcnt(0)
@@ -1106,6 +1121,23 @@ __global__ __launch_bounds__(kPfThreads) void prefill_attn_kernel(PrefillArgs a)
         else
             pf_probs_and_next<true, false>(scur, mult_cur, vshift, knext, qop, n, g, tl, ph, snext);
         __builtin_amdgcn_s_setprio(0);
+        // fp16's subnormal quantum: a p below 2^-2 (in the units the MFMAs see) has a second part
+        // below 2^-14, and the split carries it to within 2^-25 absolutely, not 2^-22 of itself
+        // (a p below 2^-25 is dropped).  Harmless while those keys' V is about as large as the
+        // rest's (what is lost is then below the calibrated rounding), not when keys of tiny
+        // weight carry V far larger than the output.  So on blocks whose V is 2^6 times the
+        // smallest-V block's or more (a uniform test), a lane with a p below 2^-2 among its 16
+        // keys (the fp16 codes of the first parts, below 0x3400; masked keys count,
+        // conservatively) adds their bound 16 * 2^-25 * 2^15 (staged |V| < 2^15) = 2^-6, times
+        // 2^-grp_sv, to u, which the epilogue compares with the row's elements.
+        if (grp_sv < sv_hi - 6) {
+            uint32_t m16 = ph[0][0][0];
+#pragma unroll
+            for (int w = 0; w < 2; ++w)
+#pragma unroll
+                for (int d = 0; d < 4; ++d) m16 = pk_min_u16(m16, ph[0][w][d]);
+            if (min(m16 & 0xffffu, m16 >> 16) < 0x3400u) tl.u += pow2f(-6 - grp_sv);
+        }
 
         // The next block's running max is found before this block's V^T P^T (which still
         // accumulates at the current max); O and l move to it afterwards.
@@ -1130,6 +1162,9 @@ __global__ __launch_bounds__(kPfThreads) void prefill_attn_kernel(PrefillArgs a)
 
     double l = tl.l64 + __shfl_xor(tl.l64, 16);
     l += __shfl_xor(l, 32);
+    float u = tl.u + __shfl_xor(tl.u, 16);
+    u += __shfl_xor(u, 32);
+    const double ul = static_cast<double>(u) / l;     // bound on that error in the row's elements
     // The row of query n: lanes n, n+16, n+32, n+48 hold dims 16dt + 4g ..
     double x[8][4];
 #pragma unroll
@@ -1152,7 +1187,7 @@ __global__ __launch_bounds__(kPfThreads) void prefill_attn_kernel(PrefillArgs a)
     // false in every lane) decide nothing.
     if (a.rs_hdr && __ballot(q_ok)) {
         const bool forced = (unsafe >> 31) != 0u || q_bad_row;
-        if (pf_flag_row(a, b, kvh, st, st + tq_c, row, tl.m_run, forced, pk, lane) && q_ok && g == 0)
+        if (pf_flag_row(a, b, kvh, st, st + tq_c, row, tl.m_run, forced, ul, pk, lane) && q_ok && g == 0)
             rs_append(a, static_cast<uint32_t>(row));
     }
     if (!q_ok) return;
