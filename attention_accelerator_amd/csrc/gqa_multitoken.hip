@@ -1147,7 +1147,14 @@ __device__ __forceinline__ void mt_flag_row(const PrefillArgs& a, int64_t row, f
     const uint64_t bads = __ballot(bad);
     const int h = (threadIdx.x & (kWave - 1)) >> 4;
     const bool row_bad = ((bads >> (16 * h)) & 0xffffull) != 0ull;
-    if (j == 0 && (row_bad || rs_flag_decide(mn2, ss, static_cast<double>(m), static_cast<double>(e) * fabs(a.qk_scale_log2))))
+    // A key whose p falls below fp32's normal range is lost to v_exp_f32's flush or to the
+    // BF16 split, at most ~2^-124 of weight each (p <= 1 against the running max, the ceiling
+    // of the largest score, so l >= 1/2).  Harmless unless its V is near the BF16 maximum,
+    // where it can outweigh the output: every element is within capacity * 2^-123 of its D_j,
+    // and a row with an element below 8 times that (|y_j| < capacity * 2^-120) is rescored too.
+    const double tq = static_cast<double>(a.capacity) * 0x1p-120;
+    if (j == 0 && (row_bad || mn2 < tq * tq ||
+                   rs_flag_decide(mn2, ss, static_cast<double>(m), static_cast<double>(e) * fabs(a.qk_scale_log2))))
         rs_append(a, static_cast<uint32_t>(row));
 }
 

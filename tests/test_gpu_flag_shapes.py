@@ -200,3 +200,17 @@ def test_prefill_tiny_weight_huge_v(dev):
     q = (q.float() * 2.0 ** 4).to(torch.bfloat16)
     vn = (vn.float() * 2.0 ** 40).to(torch.bfloat16)
     _run_and_check(q, kn, vn, k, v, starts, "prefill T=64, Q x 2^4, chunk V x 2^40")
+
+
+def test_multi_tiny_weight_huge_v(dev):
+    """Multi-token, T=16: Q x 2^6 (scores up to ~300 in log2 units) and the chunk's V x 2^120,
+    near the BF16 maximum.  Chunk keys whose p lies below fp32's normal range are lost (to
+    v_exp_f32's flush or the BF16 split), yet times V ~2^121 they add ~0.01 to the outputs.
+    The merge bounds that loss per element (capacity * 2^-123 of D_j) and rescores the rows
+    where it reaches an element (found by a run of the random-shape draw with scales 2^+-2 ..
+    2^+-120: nine multi-token draws off by up to 30,911 ULP)."""
+    starts = [int(x) for x in np.random.default_rng(134).integers(256, 700, size=4)]
+    q, kn, vn, k, v = _inputs(starts, 16, 134, dev)
+    q = (q.float() * 2.0 ** 6).to(torch.bfloat16)
+    vn = (vn.float() * 2.0 ** 120).to(torch.bfloat16)
+    _run_and_check(q, kn, vn, k, v, starts, "multi-token T=16, Q x 2^6, chunk V x 2^120")
