@@ -267,8 +267,11 @@ __device__ __forceinline__ void compute_chunk(const RopeTable& rope, int rope_po
         for (int i = 0; i < 8; ++i) st.acc[i] = ldexp(st.acc[i], shift);
         st.m_run = m_new;
     }
-    // p = 0 for a masked key (and for every key while m is -inf, when all of them are).
-    const double p = key < k_b ? exp2_f64(fmax(s - st.m_run, -2000.0)) : 0.0;
+    // p = 0 for a masked key (and for every key while m is -inf, when all of them are).  The
+    // clamp keeps a NaN (a NaN score, or +inf against a running max raised to +inf): as in
+    // the golden's exp(s - max), it makes the row NaN (fmax would turn it into p = 0).
+    const double xs = s - st.m_run;
+    const double p = key < k_b ? exp2_f64(xs < -2000.0 ? -2000.0 : xs) : 0.0;
     st.l_run += p;
 
     // p of (head l%4, key 4q + l/16) for q = 0..3, from the lane holding that score
@@ -286,6 +289,15 @@ __device__ __forceinline__ void compute_chunk(const RopeTable& rope, int rope_po
         unpack8(c.vw[q], vf);
 #pragma unroll
         for (int e = 0; e < 8; ++e) vd[q][e] = static_cast<double>(vf[e]);
+    }
+    if (kc + kChunk > k_b) {
+        // A chunk with masked keys: their V rows (clamped copies) are left out rather than
+        // weighted by 0, which an infinite V would turn into NaN; the golden never sees them.
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+            if (kc + 4 * q + (lane >> 4) >= k_b)
+#pragma unroll
+                for (int e = 0; e < 8; ++e) vd[q][e] = 0.0;
     }
     __builtin_amdgcn_sched_group_barrier(0x002, 64, 1);
     __builtin_amdgcn_sched_group_barrier(0x008, 32, 1);
@@ -1409,15 +1421,22 @@ __device__ __forceinline__ void rs_chunks(const RsRows* r, const double (&q)[16]
     rs_raise_max<G>(s, st);
     double p[G];
 #pragma unroll
-    for (int g = 0; g < G; ++g) p[g] = valid[g] ? exp2_f64(fmax(s[g] - st.m, -2000.0)) : 0.0;
+    for (int g = 0; g < G; ++g) {
+        // NaN-keeping clamp, as in the decode kernels (a NaN or +inf score makes the row NaN)
+        const double x = s[g] - st.m;
+        p[g] = valid[g] ? exp2_f64(x < -2000.0 ? -2000.0 : x) : 0.0;
+    }
 #pragma unroll
     for (int g = 0; g < G; ++g) {
         st.l += p[g];
         double v[16];
         rs_widen(r[g].vx, v);
         rs_widen(r[g].vy, v + 8);
+        // a key past the row's (a clamped row) stays out: 0 * an infinite V would be NaN
+        if (valid[g]) {
 #pragma unroll
-        for (int i = 0; i < 16; ++i) st.o[i] = fma(p[g], v[i], st.o[i]);
+            for (int i = 0; i < 16; ++i) st.o[i] = fma(p[g], v[i], st.o[i]);
+        }
     }
 }
 
@@ -1806,7 +1825,8 @@ __device__ __forceinline__ void rs_tile_chunk(const PrefillArgs& a, int b, int s
         for (int i = 0; i < 8; ++i) ps.acc[i] = ldexp(ps.acc[i], shift);
         ps.m_run = m_new;
     }
-    const double p = s == -INFINITY ? 0.0 : exp2_f64(fmax(s - ps.m_run, -2000.0));
+    const double xs = s - ps.m_run;      // NaN-keeping clamp, as in the decode kernels
+    const double p = s == -INFINITY ? 0.0 : exp2_f64(xs < -2000.0 ? -2000.0 : xs);
     ps.l_run += p;
     p_lds[(lane >> 4) * 16 + (lane & 3) * 4 + ((lane >> 2) & 3)] = p;
     const double2 pa = *reinterpret_cast<const double2*>(p_lds + (lane >> 4) * 16 + (lane & 3) * 4);

@@ -71,3 +71,44 @@ def test_chunk_rows_of_infinite_q(dev, n_new):
     out = gqa.gqa_prefill(q.to(dev), kn.to(dev), vn.to(dev), k.to(dev), v.to(dev), starts)
     torch.cuda.synchronize()
     assert_within_ulp(want.reshape(-1, 128), to_codes(out).reshape(-1, 128), 64, f"T={n_new}, Q heads x 2^126")
+
+
+@pytest.mark.parametrize("stream_k", [False, True])
+def test_decode_infinite_v_beside_masked_keys(dev, stream_k):
+    """V of the last key a query sees holds +inf in one dim, and the keys after it (inside the
+    sequence, past the query position) are masked.  The golden never reads a masked key, so
+    that dim comes out +inf.  The kernels load a masked key's V as a clamped copy of the last
+    valid row; weighted by p = 0 it gave 0 * inf = NaN until masked rows were left out of the
+    weighted sum.  Both launch shapes, every element against the oracle."""
+    from attention_accelerator_amd import stimulus
+    b = stimulus.decode_batch(3, 64, lengths=torch.tensor([40, 33, 64]), seed=71)
+    qp = torch.tensor([20, 32, 50])
+    for s, p in enumerate(qp.tolist()):
+        b.v[s, s % 8, p, 5] = float("inf")
+    want = orc.decode(to_codes(b.q), to_codes(b.k), to_codes(b.v), b.seq_len.numpy(), qp.numpy())
+    got = to_codes(gqa.gqa_attention(b.q.to(dev), b.k.to(dev), b.v.to(dev), qp, b.seq_len,
+                                     params=gqa.make_params(stream_k=stream_k)))
+    torch.cuda.synchronize()
+    w = np.asarray(want).reshape(-1, 128)
+    assert (w[:, 5] == 0x7F80).sum() == 12          # 3 sequences x 4 heads: +inf in the golden
+    assert_within_ulp(want, got, 64, f"decode, +inf V beside masked keys, stream_k={stream_k}")
+
+
+@pytest.mark.parametrize("stream_k", [False, True])
+def test_decode_nan_score_makes_the_row_nan(dev, stream_k):
+    """A key whose score is NaN (K +inf in a dim where every Q head of the group is 0 after
+    RoPE -- both dims of the pair zeroed -- so 0 * inf):
+    the golden's max() and exp(s - max) make every weight, and so the whole row, NaN.  The fp64
+    kernels clamped exp2's argument with fmax, which turned the NaN into p = 0 and left the row
+    finite, until the clamp kept NaN."""
+    from attention_accelerator_amd import stimulus
+    b = stimulus.decode_batch(2, 300, lengths=torch.tensor([300, 170]), seed=72)
+    b.q[0, 4:8, 9] = 0.0
+    b.q[0, 4:8, 9 + 64] = 0.0
+    b.k[0, 1, 123, 9] = float("inf")
+    want = orc.decode(to_codes(b.q), to_codes(b.k), to_codes(b.v), b.seq_len.numpy(), b.query_pos.numpy())
+    got = to_codes(gqa.gqa_attention(b.q.to(dev), b.k.to(dev), b.v.to(dev), b.query_pos, b.seq_len,
+                                     params=gqa.make_params(stream_k=stream_k)))
+    torch.cuda.synchronize()
+    assert _nan_rows(want) == 4                      # heads 4..7 of sequence 0
+    assert_within_ulp(want, got, 64, f"decode, NaN score, stream_k={stream_k}")
