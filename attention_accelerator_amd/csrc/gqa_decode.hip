@@ -2019,7 +2019,7 @@ __global__ __launch_bounds__(kWave) void rescore_kernel(PrefillArgs a) {
     const uint32_t n_rows = min(a.rs_hdr[0], cap);
     if (n_rows == 0) return;
     const uint32_t n_pairs = a.rs_hdr[1];
-    if (static_cast<uint64_t>(n_rows) < static_cast<uint64_t>(kRsTileFill) * n_pairs) {
+    if (a.rs_hdr[2] != 0u || static_cast<uint64_t>(n_rows) < static_cast<uint64_t>(kRsTileFill) * n_pairs) {
         rs_rows_path(a, n_rows);
         return;
     }

@@ -247,8 +247,11 @@ __device__ __forceinline__ void rs_append(const PrefillArgs& a, uint32_t row) {
 }
 
 // Clears the flagged-row count (the first kernel of a prefill or multi-token call).
+// Header words: flagged rows, (sequence, KV head) pairs with one, and a nonzero word when a
+// flagged row sees a V that is not finite (the rescore then takes its rows path: the tiles
+// path shares V between rows of different causal limits, and 0 * inf would give NaN).
 __device__ __forceinline__ void rs_clear(const PrefillArgs& a, int t) {
-    if (a.rs_hdr && t < 2) a.rs_hdr[t] = 0u;
+    if (a.rs_hdr && t < 3) a.rs_hdr[t] = 0u;
 }
 
 // The same kernel clears row (b*T + t)*32 + h's piece counter and, with RoPE on K, stores

@@ -1124,7 +1124,7 @@ __device__ __forceinline__ void mt_flag_row(const PrefillArgs& a, int64_t row, f
     const uint32_t qw[4] = {qx.x, qx.y, qx.z, qx.w};
     double ss = 0.0, mn2 = INFINITY;
     float qq = 0.f;
-    bool bad = false;
+    bool bad = false, vinf = false;
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
         const uint32_t d = max(seg_st[8 + 8 * j + i], i & 1 ? dw[i >> 1] >> 16 : dw[i >> 1] & 0xffffu);
@@ -1136,6 +1136,7 @@ __device__ __forceinline__ void mt_flag_row(const PrefillArgs& a, int64_t row, f
         ss = fma(y, y, ss);
         if (dv > 0.f) mn2 = fmin(mn2, y * y);
         bad |= !__builtin_isfinite(x);
+        vinf |= !(dv <= 3.4028235e38f);             // an infinite or NaN V among the row's keys
         qq = fmaf(q, q, qq);
     }
     // |q_G| |k_G|max: lanes j and j + 8 hold the two halves of pair group j % 8.
@@ -1147,6 +1148,7 @@ __device__ __forceinline__ void mt_flag_row(const PrefillArgs& a, int64_t row, f
     const uint64_t bads = __ballot(bad);
     const int h = (threadIdx.x & (kWave - 1)) >> 4;
     const bool row_bad = ((bads >> (16 * h)) & 0xffffull) != 0ull;
+    const bool row_vinf = ((__ballot(vinf) >> (16 * h)) & 0xffffull) != 0ull;
     // A key whose p falls below fp32's normal range is lost to v_exp_f32's flush or to the
     // BF16 split, at most ~2^-124 of weight each (p <= 1 against the running max, the ceiling
     // of the largest score, so l >= 1/2).  Harmless unless its V is near the BF16 maximum,
@@ -1154,8 +1156,10 @@ __device__ __forceinline__ void mt_flag_row(const PrefillArgs& a, int64_t row, f
     // and a row with an element below 8 times that (|y_j| < capacity * 2^-120) is rescored too.
     const double tq = static_cast<double>(a.capacity) * 0x1p-120;
     if (j == 0 && (row_bad || mn2 < tq * tq ||
-                   rs_flag_decide(mn2, ss, static_cast<double>(m), static_cast<double>(e) * fabs(a.qk_scale_log2))))
+                   rs_flag_decide(mn2, ss, static_cast<double>(m), static_cast<double>(e) * fabs(a.qk_scale_log2)))) {
         rs_append(a, static_cast<uint32_t>(row));
+        if (row_vinf) atomicOr(a.rs_hdr + 2, 1u);
+    }
 }
 
 // One workgroup per (KV head, sequence), 16 threads per column: thread i handles column

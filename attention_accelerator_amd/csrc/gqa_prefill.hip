@@ -833,7 +833,7 @@ __device__ __forceinline__ bool pf_flag_row(const PrefillArgs& a, int b, int kvh
     const uint32_t k1 = max(a.rs_kc[ec * 8 + 4 + g], a.rs_kpre[er * 8 + 4 + g]);
     double ss = 0.0, mn2 = INFINITY;
     float mnx = INFINITY;
-    bool bad = forced;
+    bool bad = forced, vinf = false;
 #pragma unroll
     for (int dt = 0; dt < 8; ++dt) {
         const uint4 dc = *reinterpret_cast<const uint4*>(a.rs_dc + ec * kD + 16 * dt + 4 * g);
@@ -850,6 +850,7 @@ __device__ __forceinline__ bool pf_flag_row(const PrefillArgs& a, int b, int kvh
             if (dv > 0.f) mn2 = fmin(mn2, y * y);
             mnx = fminf(mnx, fabsf(x));
             bad |= !__builtin_isfinite(x);
+            vinf |= !(dv <= 3.4028235e38f);         // an infinite or NaN V among the row's keys
         }
     }
     float qq0 = 0.f, qq1 = 0.f;
@@ -875,6 +876,9 @@ __device__ __forceinline__ bool pf_flag_row(const PrefillArgs& a, int b, int kvh
     bad |= static_cast<double>(mnx) < 8.0 * ul;
     bad = (__shfl_xor(static_cast<int>(bad), 16) | __shfl_xor(static_cast<int>(bad), 32) |
            __shfl_xor(static_cast<int>(bad), 48) | static_cast<int>(bad)) != 0;
+    vinf = (__shfl_xor(static_cast<int>(vinf), 16) | __shfl_xor(static_cast<int>(vinf), 32) |
+            __shfl_xor(static_cast<int>(vinf), 48) | static_cast<int>(vinf)) != 0;
+    if (vinf && (lane >> 4) == 0) atomicOr(a.rs_hdr + 2, 1u);   // the row is flagged: y = 0 there
     return bad || rs_flag_decide(mn2, ss, static_cast<double>(m), static_cast<double>(e) * fabs(a.qk_scale_log2));
 }
 
